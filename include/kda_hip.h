@@ -1,0 +1,99 @@
+/*
+ * kda_hip.h -- C ABI of the gfx950 KDA (Kimi Delta Attention / gated delta
+ * rule) chunkwise WY recurrence.
+ *
+ * Layouts (all contiguous, row-major):
+ *   q, k, v, g, o, dq, dk, dv, dg, dout   [B, T, H, D]
+ *   beta, dbeta                            [B, T, H]
+ *   s0, s_final, ds_final, ds0             [B, H, D, D] fp32, reference
+ *                                          orientation S[i_v][j_k] (o_t = S_t q_t)
+ * dtype / g_dtype: 0 = fp32, 1 = bf16 (raw bfloat16 bits).  q, k, v, beta, o
+ * and dq, dk, dv, dbeta use `dtype`; g and dg use `g_dtype`.  Arithmetic is
+ * fp32 with an fp32 state; bf16 inputs use bf16 MFMA operands.
+ * chunk must be 64.  D must be 32, 64 or 128 (forward) and 32 or 64 (backward).
+ * stream is a hipStream_t (NULL = default stream).  Every call is stream
+ * ordered and allocates nothing: the caller passes a device workspace of at
+ * least kda_workspace_size() bytes (256-byte aligned).
+ *
+ * Return codes: 0 ok, KDA_E_* < 0 on error; kda_last_error() then describes
+ * the failure (thread-local).  Argument checks happen before any device work.
+ */
+#ifndef KDA_HIP_H
+#define KDA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KDA_OK 0
+#define KDA_E_INVALID (-1)      /* null pointer, negative size, misalignment */
+#define KDA_E_UNSUPPORTED (-2)  /* chunk, D or dtype outside what the kernels support */
+#define KDA_E_WORKSPACE (-3)    /* workspace smaller than kda_workspace_size() */
+#define KDA_E_HIP (-4)          /* a HIP launch or runtime call failed */
+
+#define KDA_DTYPE_F32 0
+#define KDA_DTYPE_BF16 1
+
+#define KDA_PASS_FWD 0
+#define KDA_PASS_BWD 1
+
+/* Workspace regions (see kda_workspace_offsets). */
+enum kda_ws_region {
+    KDA_WS_W = 0, KDA_WS_U, KDA_WS_QP, KDA_WS_QPT, KDA_WS_KB, KDA_WS_KBT, KDA_WS_WT,
+    KDA_WS_AQK, KDA_WS_AQKT, KDA_WS_AKK, KDA_WS_TII, KDA_WS_EG, KDA_WS_H, KDA_WS_DH,
+    KDA_WS_VP, KDA_WS_DVP, KDA_WS_NREGIONS
+};
+
+/* ABI version of this header (bumped on any signature change). */
+int kda_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* kda_last_error(void);
+
+/* Bytes of workspace kda_fwd (pass 0) or kda_bwd (pass 1) needs; 0 on invalid
+ * arguments (see kda_last_error). */
+size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int dtype);
+
+/* Byte offsets of the workspace regions for a pass (-1 = unused), so tests can
+ * inspect intermediates.  offsets must hold KDA_WS_NREGIONS entries. */
+int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int dtype,
+                          int64_t* offsets);
+
+/* Forward: o and (if s_final != NULL) the final state.  s0 == NULL means a zero
+ * initial state.
+ * Replaces GatedDeltaLayer._chunkwise_kda_forward (nope_gdn_mlx.py:2318-2456)
+ * and the forward of _chunkwise_kda_vjp_path (nope_gdn_mlx.py:2829-2865), with
+ * heads kept in place instead of folded; same result as _loop_compiled_kda
+ * (nope_gdn_mlx.py:890-917). */
+int kda_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+            const float* s0, void* o, float* s_final,
+            int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+            void* workspace, size_t ws_bytes, void* stream);
+
+/* Backward (VJP): gradients of <o, dout> + <s_final, ds_final> with respect to
+ * q, k, v, g, beta and s0.  ds_final == NULL means zero; ds0 may be NULL.
+ * Chunk-boundary states are recomputed; nothing is kept from kda_fwd.
+ * Replaces the VJP of _get_chunkwise_kda_recurrence_fn (nope_gdn_mlx.py:2746-2808)
+ * and _chunkwise_kda_backward (nope_gdn_mlx.py:2579-2720). */
+int kda_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+            const float* s0, const void* dout, const float* ds_final,
+            void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
+            int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+            void* workspace, size_t ws_bytes, void* stream);
+
+/* y = M^-1 b for unit-triangular M (only the strict lower, or with upper != 0
+ * the strict upper, part of M is read); M [BH, Cm, Cm], b and y [BH, Cm, N],
+ * fp32, 1 <= Cm <= 64, N >= 1.
+ * Replaces GatedDeltaLayer._metal_solve_triangular (nope_gdn_mlx.py:1160-1196)
+ * and _metal_solve_triangular_upper (nope_gdn_mlx.py:1261-1286). */
+int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, int Cm, int N,
+                              int upper, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_HIP_H */

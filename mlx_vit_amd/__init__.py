@@ -1,0 +1,13 @@
+"""MI355X-native KDA (Kimi Delta Attention / gated delta rule) chunkwise recurrence.
+
+Hand-written gfx950 HIP kernels behind a C ABI (``include/kda_hip.h``,
+``libkda_hip.so``), driven from torch through ctypes.
+"""
+from .kda import (ChunkKDAFunction, chunk_kda, kda_backward, kda_forward, solve_unit_triangular,
+                  workspace_bytes, workspace_offsets)
+from .recurrence import HIP_PATH, KDA_PATHS, KDARecurrence
+
+__all__ = [
+    "ChunkKDAFunction", "chunk_kda", "kda_forward", "kda_backward", "solve_unit_triangular",
+    "workspace_bytes", "workspace_offsets", "KDARecurrence", "HIP_PATH", "KDA_PATHS",
+]

@@ -1,0 +1,344 @@
+// kda_api.hip -- the C ABI declared in include/kda_hip.h: argument checks,
+// workspace layout and the launch sequence of the forward and backward passes.
+// Also the standalone unit-triangular solve and a small state-copy kernel.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/kda_hip.h"
+#include "kda_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return KDA_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+struct Layout {
+    int64_t off[KDA_WS_NREGIONS];
+    size_t total;
+};
+
+int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, bool bwd) {
+    if (B < 0 || T < 0 || H < 0) return fail(KDA_E_INVALID, "negative size: B=%d T=%d H=%d", B, T, H);
+    if (chunk != kda::C) return fail(KDA_E_UNSUPPORTED, "chunk=%d: only chunk=64 is supported", chunk);
+    if (bwd) {
+        if (D != 32 && D != 64)
+            return fail(KDA_E_UNSUPPORTED, "D=%d: the backward supports D in {32, 64}", D);
+    } else if (D != 32 && D != 64 && D != 128) {
+        return fail(KDA_E_UNSUPPORTED, "D=%d: the forward supports D in {32, 64, 128}", D);
+    }
+    if (dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_BF16)
+        return fail(KDA_E_UNSUPPORTED, "dtype=%d: expected 0 (fp32) or 1 (bf16)", dtype);
+    if (g_dtype != KDA_DTYPE_F32 && g_dtype != KDA_DTYPE_BF16)
+        return fail(KDA_E_UNSUPPORTED, "g_dtype=%d: expected 0 (fp32) or 1 (bf16)", g_dtype);
+    const long long nchunks = (long long)B * H * ((T + kda::C - 1) / kda::C);
+    if (nchunks > 0x7fffffffLL) return fail(KDA_E_UNSUPPORTED, "B*H*ceil(T/64)=%lld exceeds 2^31-1", nchunks);
+    return KDA_OK;
+}
+
+void make_layout(int pass, int B, int T, int H, int D, Layout& L) {
+    const size_t nc = (size_t)(T + kda::C - 1) / kda::C;
+    const size_t N = (size_t)B * H * nc;
+    const size_t CD = N * kda::C * D, CC = N * kda::C * kda::C, DD = N * (size_t)D * D;
+    const size_t TI = N * kda::NB * kda::BS * kda::BS, EG = N * D;
+    size_t sz[KDA_WS_NREGIONS] = {0};
+    sz[KDA_WS_W] = CD;
+    sz[KDA_WS_U] = CD;
+    sz[KDA_WS_KBT] = CD;
+    sz[KDA_WS_EG] = EG;
+    if (pass == KDA_PASS_FWD) {
+        sz[KDA_WS_QP] = CD;
+        sz[KDA_WS_AQK] = CC;
+    } else {
+        sz[KDA_WS_WT] = CD;
+        sz[KDA_WS_QPT] = CD;
+        sz[KDA_WS_KB] = CD;
+        sz[KDA_WS_AQKT] = CC;
+        sz[KDA_WS_AKK] = CC;
+        sz[KDA_WS_TII] = TI;
+        sz[KDA_WS_H] = DD;
+        sz[KDA_WS_DH] = DD;
+        sz[KDA_WS_VP] = CD;
+        sz[KDA_WS_DVP] = CD;
+    }
+    size_t cur = 0;
+    for (int r = 0; r < KDA_WS_NREGIONS; ++r) {
+        if (sz[r] == 0) {
+            L.off[r] = -1;
+            continue;
+        }
+        L.off[r] = (int64_t)cur;
+        cur += (sz[r] * sizeof(float) + 255) & ~(size_t)255;
+    }
+    L.total = cur;
+}
+
+float* region(void* ws, const Layout& L, int r) {
+    return L.off[r] < 0 ? nullptr : reinterpret_cast<float*>(static_cast<char*>(ws) + L.off[r]);
+}
+
+int check_io(const void* p, const char* name, int dtype, bool nullable) {
+    if (!p) return nullable ? KDA_OK : fail(KDA_E_INVALID, "%s is NULL", name);
+    const size_t al = (dtype == KDA_DTYPE_F32) ? 16 : 8;
+    if (!aligned(p, al)) return fail(KDA_E_INVALID, "%s is not %zu-byte aligned", name, al);
+    return KDA_OK;
+}
+
+int check_scalar(const void* p, const char* name, int dtype) {
+    if (!p) return fail(KDA_E_INVALID, "%s is NULL", name);
+    if (!aligned(p, dtype == KDA_DTYPE_F32 ? 4 : 2)) return fail(KDA_E_INVALID, "%s is misaligned", name);
+    return KDA_OK;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    return fail(KDA_E_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------------------
+// kernels local to this file
+// ----------------------------------------------------------------------------
+namespace kda {
+
+__global__ __launch_bounds__(256) void kda_state_copy_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                             size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src ? src[i] : 0.f;
+}
+
+hipError_t launch_state_copy(const float* src, float* dst, size_t n, hipStream_t st) {
+    if (n == 0 || !dst) return hipSuccess;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(kda_state_copy_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st,
+                       src, dst, n);
+    return hipGetLastError();
+}
+
+// One workgroup per matrix: diagonal 16x16 inverses by substitution, then
+// block substitution over 16-column tiles of b, fp32-accurate (split bf16) MFMA.
+// The upper case solves the index-reversed (lower) system.
+__global__ __launch_bounds__(256) void kda_solve_kernel(const float* __restrict__ M, const float* __restrict__ b,
+                                                        float* __restrict__ y, int Cm, int N, int upper) {
+    __shared__ float sl[C][C + 4];
+    __shared__ float tii[NB][BS][BS + 4];
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    const size_t mb = (size_t)blockIdx.x * Cm * Cm, bb = (size_t)blockIdx.x * Cm * N;
+    const int nbk = (Cm + BS - 1) / BS;
+    auto src = [&](int i) { return upper ? Cm - 1 - i : i; };
+    for (int idx = tid; idx < C * C; idx += 256) {
+        const int i = idx / C, j = idx - i * C;
+        sl[i][j] = (i < Cm && j < i) ? M[mb + (size_t)src(i) * Cm + src(j)] : 0.f;
+    }
+    __syncthreads();
+    diag_inverse<C + 4>(&sl[0][0], tii, nbk);
+    __syncthreads();
+    const int nct = (N + BS - 1) / BS;
+    for (int ct = w; ct < nct; ct += 4) {
+        const int col = ct * BS + r16;
+        f32x4 X[NB];
+        for (int i = 0; i < nbk; ++i) {
+            f32x4 Y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = BS * i + 4 * g4 + e;
+                Y[e] = (r < Cm && col < N) ? b[bb + (size_t)src(r) * N + col] : 0.f;
+            }
+            for (int j = 0; j < i; ++j) Y = mma4<3>(neg(frag4(&sl[0][0], C + 4, BS * i, BS * j)), acc2frag4(X[j]), Y);
+            X[i] = mma4<3>(frag4(&tii[i][0][0], BS + 4, 0, 0), acc2frag4(Y), zero4());
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = BS * i + 4 * g4 + e;
+                if (r < Cm && col < N) y[bb + (size_t)src(r) * N + col] = X[i][e];
+            }
+        }
+    }
+}
+
+hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper, hipStream_t st) {
+    hipLaunchKernelGGL(kda_solve_kernel, dim3(BH), dim3(256), 0, st, M, b, y, Cm, N, upper);
+    return hipGetLastError();
+}
+
+}  // namespace kda
+
+// ----------------------------------------------------------------------------
+// C ABI
+// ----------------------------------------------------------------------------
+extern "C" {
+
+int kda_abi_version(void) { return 1; }
+
+const char* kda_last_error(void) { return g_err.c_str(); }
+
+size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int dtype) {
+    if (pass != KDA_PASS_FWD && pass != KDA_PASS_BWD) {
+        fail(KDA_E_INVALID, "pass=%d: expected 0 (fwd) or 1 (bwd)", pass);
+        return 0;
+    }
+    if (check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass == KDA_PASS_BWD) != KDA_OK) return 0;
+    Layout L;
+    make_layout(pass, B, T, H, D, L);
+    ok();
+    return L.total;
+}
+
+int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int dtype, int64_t* offsets) {
+    if (!offsets) return fail(KDA_E_INVALID, "offsets is NULL");
+    if (pass != KDA_PASS_FWD && pass != KDA_PASS_BWD) return fail(KDA_E_INVALID, "pass=%d", pass);
+    const int rc = check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass == KDA_PASS_BWD);
+    if (rc) return rc;
+    Layout L;
+    make_layout(pass, B, T, H, D, L);
+    for (int r = 0; r < KDA_WS_NREGIONS; ++r) offsets[r] = L.off[r];
+    return ok();
+}
+
+int kda_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0, void* o,
+            float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
+            size_t ws_bytes, void* stream) {
+    int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, false);
+    if (rc) return rc;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const size_t nstate = (size_t)B * H * D * D;
+    if ((rc = check_io(s0, "s0", KDA_DTYPE_F32, true)) || (rc = check_io(s_final, "s_final", KDA_DTYPE_F32, true)))
+        return rc;
+    if ((size_t)B * T * H == 0) {
+        const hipError_t e = kda::launch_state_copy(s0, s_final, nstate, st);
+        return e == hipSuccess ? ok() : hip_fail(e, "state copy");
+    }
+    if ((rc = check_io(q, "q", dtype, false)) || (rc = check_io(k, "k", dtype, false)) ||
+        (rc = check_io(v, "v", dtype, false)) || (rc = check_io(g, "g", g_dtype, false)) ||
+        (rc = check_io(o, "o", dtype, false)) || (rc = check_scalar(beta, "beta", dtype)))
+        return rc;
+    Layout L;
+    make_layout(KDA_PASS_FWD, B, T, H, D, L);
+    if (!workspace || ws_bytes < L.total)
+        return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
+    if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
+
+    const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
+    kda::PrepArgs pa = {};
+    pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
+    pa.W = region(workspace, L, KDA_WS_W);
+    pa.U = region(workspace, L, KDA_WS_U);
+    pa.Qp = region(workspace, L, KDA_WS_QP);
+    pa.KbT = region(workspace, L, KDA_WS_KBT);
+    pa.Aqk = region(workspace, L, KDA_WS_AQK);
+    pa.eG = region(workspace, L, KDA_WS_EG);
+    pa.T = T; pa.H = H; pa.nc = nc;
+    hipError_t e = kda::launch_prep(pa, D, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16, BH * nc, st);
+    if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
+
+    kda::RecurArgs ra = {};
+    ra.W = pa.W; ra.U = pa.U; ra.Qp = pa.Qp; ra.KbT = pa.KbT; ra.Aqk = pa.Aqk; ra.eG = pa.eG;
+    ra.s0 = s0; ra.s_final = s_final; ra.o = o;
+    ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
+    e = kda::launch_recur(ra, D, dtype == KDA_DTYPE_BF16, 0, st);
+    if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
+    return ok();
+}
+
+int kda_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+            const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
+            int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
+            void* stream) {
+    int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, true);
+    if (rc) return rc;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const size_t nstate = (size_t)B * H * D * D;
+    if ((rc = check_io(s0, "s0", KDA_DTYPE_F32, true)) || (rc = check_io(ds_final, "ds_final", KDA_DTYPE_F32, true)) ||
+        (rc = check_io(ds0, "ds0", KDA_DTYPE_F32, true)))
+        return rc;
+    if ((size_t)B * T * H == 0) {
+        const hipError_t e = kda::launch_state_copy(ds_final, ds0, nstate, st);
+        return e == hipSuccess ? ok() : hip_fail(e, "state copy");
+    }
+    if ((rc = check_io(q, "q", dtype, false)) || (rc = check_io(k, "k", dtype, false)) ||
+        (rc = check_io(v, "v", dtype, false)) || (rc = check_io(g, "g", g_dtype, false)) ||
+        (rc = check_io(dout, "dout", dtype, false)) || (rc = check_io(dq, "dq", dtype, false)) ||
+        (rc = check_io(dk, "dk", dtype, false)) || (rc = check_io(dv, "dv", dtype, false)) ||
+        (rc = check_io(dg, "dg", g_dtype, false)) || (rc = check_scalar(beta, "beta", dtype)) ||
+        (rc = check_scalar(dbeta, "dbeta", dtype)))
+        return rc;
+    Layout L;
+    make_layout(KDA_PASS_BWD, B, T, H, D, L);
+    if (!workspace || ws_bytes < L.total)
+        return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
+    if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
+
+    const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
+    const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
+    float* W = region(workspace, L, KDA_WS_W);
+    float* U = region(workspace, L, KDA_WS_U);
+    float* KbT = region(workspace, L, KDA_WS_KBT);
+    float* eG = region(workspace, L, KDA_WS_EG);
+    float* WT = region(workspace, L, KDA_WS_WT);
+    float* QpT = region(workspace, L, KDA_WS_QPT);
+    float* Kb = region(workspace, L, KDA_WS_KB);
+    float* AqkT = region(workspace, L, KDA_WS_AQKT);
+    float* Akk = region(workspace, L, KDA_WS_AKK);
+    float* Tii = region(workspace, L, KDA_WS_TII);
+    float* hS = region(workspace, L, KDA_WS_H);
+    float* dhS = region(workspace, L, KDA_WS_DH);
+    float* Vp = region(workspace, L, KDA_WS_VP);
+    float* dVp = region(workspace, L, KDA_WS_DVP);
+
+    kda::PrepArgs pa = {};
+    pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
+    pa.W = W; pa.U = U; pa.KbT = KbT; pa.eG = eG; pa.WT = WT; pa.QpT = QpT; pa.Kb = Kb;
+    pa.AqkT = AqkT; pa.Akk = Akk; pa.Tii = Tii;
+    pa.T = T; pa.H = H; pa.nc = nc;
+    hipError_t e = kda::launch_prep(pa, D, in_bf16, g_bf16, BH * nc, st);
+    if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
+
+    kda::RecurArgs ra = {};
+    ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
+    ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
+    e = kda::launch_recur(ra, D, in_bf16, 1, st);
+    if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
+
+    kda::DhArgs da = {};
+    da.AqkT = AqkT; da.Kb = Kb; da.QpT = QpT; da.WT = WT; da.eG = eG; da.dout = dout; da.dsf = ds_final;
+    da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
+    da.T = T; da.H = H; da.nc = nc; da.BH = BH;
+    e = kda::launch_dh(da, D, in_bf16, st);
+    if (e != hipSuccess) return hip_fail(e, "kda_dh_kernel");
+
+    kda::LocalArgs la = {};
+    la.q = q; la.k = k; la.v = v; la.g = g; la.beta = beta; la.dout = dout;
+    la.W = W; la.U = U; la.Akk = Akk; la.Tii = Tii; la.h = hS; la.dh = dhS; la.Vp = Vp; la.dVp = dVp;
+    la.dq = dq; la.dk = dk; la.dv = dv; la.dg = dg; la.dbeta = dbeta;
+    la.T = T; la.H = H; la.nc = nc;
+    e = kda::launch_local(la, D, in_bf16, g_bf16, BH * nc, st);
+    if (e != hipSuccess) return hip_fail(e, "kda_bwd_local_kernel");
+    return ok();
+}
+
+int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,
+                              void* stream) {
+    if (!M || !b || !y) return fail(KDA_E_INVALID, "M, b and y must be non-NULL");
+    if (BH < 0 || N < 1 || Cm < 1) return fail(KDA_E_INVALID, "BH=%d Cm=%d N=%d", BH, Cm, N);
+    if (Cm > kda::C) return fail(KDA_E_UNSUPPORTED, "Cm=%d exceeds 64", Cm);
+    if (BH == 0) return ok();
+    const hipError_t e = kda::launch_solve(M, b, y, BH, Cm, N, upper, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "kda_solve_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,168 @@
+// kda_chunk.h -- workgroup-level phases shared by the per-chunk kernels
+// (forward prep and backward local adjoints).  One workgroup = 256 threads =
+// 4 waves works on one (batch, head, chunk) of C = 64 tokens.
+//
+// Anchored decay products.  For rows t, s of one chunk with gamma the in-chunk
+// cumulative log-decay, the pair weight exp(gamma_t - gamma_s) (s <= t) is split
+// at the anchor r = 16 * (t / 16), the first row of t's 16-row sub-block:
+//     exp(gamma_t - gamma_r) * exp(gamma_r - gamma_s).
+// Off the diagonal sub-block both factors are <= 1.  On the diagonal sub-block
+// the second factor is bounded by the sub-block's decay span, which the span
+// guard limits to SPAN_MAX; a chunk that fails the guard (or has any g > 0)
+// takes the pairwise path instead, which evaluates every exp(gamma_t - gamma_s)
+// directly, as the reference's M kernel does (nope_gdn_mlx.py:1319-1334).
+//
+// LDS holds, per chunk (fp32, rows padded by 4 floats against bank conflicts):
+//   g  : gamma                      (raw g until the cumsum)
+//   kl : k_t e^{gamma_t - gamma_r}  (A operand, left factor)
+//   ql : q_t e^{gamma_t - gamma_r}  (raw q until the transform)
+//   kr : k_s e^{gamma_r' - gamma_s} with r' the anchor of s's own sub-block
+//        (raw k until the transform); the right factor for sub-block row i is
+//        kr * f[i][j], f[i][j] = e^{gamma_16i - gamma_16j}
+//   er : e^{gamma_r} per sub-block and channel
+#pragma once
+#include "kda_device.h"
+
+namespace kda {
+
+template <int D>
+struct ChunkLds {
+    float g[C][D + 4];
+    float kl[C][D + 4];
+    float ql[C][D + 4];
+    float kr[C][D + 4];
+    union {
+        struct {
+            float er[NB][D];
+            float f[6][D];
+        };
+        float tmp[256];  // cumsum partial totals; dead before er / f are written
+    };
+    float beta[C];
+};
+
+// pair index of sub-block pair (i, j), j < i: (1,0)=0 (2,0)=1 (2,1)=2 (3,0)=3 (3,1)=4 (3,2)=5
+__device__ __forceinline__ int pair_idx(int i, int j) { return (i * (i - 1)) / 2 + j; }
+
+// lower sub-block tiles (i, j <= i) enumerated 0..9
+__device__ __forceinline__ void tile_ij(int tix, int& i, int& j) {
+    i = (tix >= 6) ? 3 : (tix >= 3) ? 2 : (tix >= 1) ? 1 : 0;
+    j = tix - (i * (i + 1)) / 2;
+}
+
+template <int PREC> __device__ __forceinline__ float kexp(float x) {
+    if constexpr (PREC == 1) return __expf(x);
+    else return expf(x);
+}
+
+// Load one chunk of q, k, g, beta (rows >= valid are zero: g = 0 no decay,
+// beta = 0 no write -- the reference's padding, nope_gdn_mlx.py:2354-2361).
+// Returns 1 if this thread saw g > 0 (or a NaN), which disables the anchored path.
+template <int D, typename TI, typename TG>
+__device__ int chunk_load(ChunkLds<D>& s, const TI* __restrict__ q, const TI* __restrict__ k,
+                          const TG* __restrict__ g, const TI* __restrict__ beta, size_t base,
+                          size_t rstride, size_t bbase, int H, int valid) {
+    const int tid = threadIdx.x;
+    int flag = 0;
+    constexpr int Q4 = D / 4;
+    for (int idx = tid; idx < C * Q4; idx += 256) {
+        const int t = idx / Q4, d = (idx % Q4) * 4;
+        float4 vq = make_float4(0.f, 0.f, 0.f, 0.f), vk = vq, vg = vq;
+        if (t < valid) {
+            const size_t o = base + (size_t)t * rstride + d;
+            vq = ld4<TI>(q + o);
+            vk = ld4<TI>(k + o);
+            vg = ld4<TG>(g + o);
+        }
+        *reinterpret_cast<float4*>(&s.ql[t][d]) = vq;
+        *reinterpret_cast<float4*>(&s.kr[t][d]) = vk;
+        *reinterpret_cast<float4*>(&s.g[t][d]) = vg;
+        if (!(vg.x <= 0.f && vg.y <= 0.f && vg.z <= 0.f && vg.w <= 0.f)) flag = 1;
+    }
+    if (tid < C) s.beta[tid] = (tid < valid) ? ld1<TI>(beta + bbase + (size_t)tid * H) : 0.f;
+    __syncthreads();
+    return flag;
+}
+
+// In-place inclusive cumsum of s.g over rows, per channel.
+template <int D>
+__device__ void chunk_cumsum(ChunkLds<D>& s) {
+    constexpr int PARTS = 256 / D, RP = C / PARTS;
+    const int tid = threadIdx.x, d = tid % D, p = tid / D;
+    float run = 0.f;
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        run += s.g[p * RP + r][d];
+        s.g[p * RP + r][d] = run;
+    }
+    s.tmp[p * D + d] = run;
+    __syncthreads();
+    float off = 0.f;
+    for (int pp = 0; pp < p; ++pp) off += s.tmp[pp * D + d];
+    if (p > 0) {
+#pragma unroll
+        for (int r = 0; r < RP; ++r) s.g[p * RP + r][d] += off;
+    }
+    __syncthreads();
+}
+
+// Anchor factors er, f and the span guard.  Returns nonzero (uniform over the
+// workgroup) when the chunk must take the pairwise path.
+template <int D, int PREC>
+__device__ int chunk_factors(ChunkLds<D>& s, int flag) {
+    const int tid = threadIdx.x;
+    for (int idx = tid; idx < NB * D; idx += 256) {
+        const int j = idx / D, d = idx % D;
+        const float span = s.g[BS * j][d] - s.g[BS * j + BS - 1][d];
+        if (!(span <= SPAN_MAX)) flag = 1;
+        s.er[j][d] = kexp<PREC>(s.g[BS * j][d]);
+    }
+    for (int idx = tid; idx < 6 * D; idx += 256) {
+        const int p = idx / D, d = idx % D;
+        const int i = (p >= 3) ? 3 : (p >= 1) ? 2 : 1;
+        const int j = p - pair_idx(i, 0);
+        s.f[p][d] = kexp<PREC>(s.g[BS * i][d] - s.g[BS * j][d]);
+    }
+    return __syncthreads_or(flag);
+}
+
+// kl = k e^{g_t - g_r}, ql = q e^{g_t - g_r}; with `anchored`, kr = k e^{g_r - g_t}
+// (otherwise kr keeps raw k).  Raw q, k are read from ql, kr.  The caller
+// syncs afterwards.
+template <int D, int PREC>
+__device__ void chunk_transform(ChunkLds<D>& s, bool anchored) {
+    const int tid = threadIdx.x;
+    for (int idx = tid; idx < C * D; idx += 256) {
+        const int t = idx / D, d = idx % D, r = t & ~(BS - 1);
+        const float x = s.g[t][d] - s.g[r][d];
+        const float el = kexp<PREC>(x);
+        const float kv = s.kr[t][d], qv = s.ql[t][d];
+        s.kl[t][d] = kv * el;
+        s.ql[t][d] = qv * el;
+        if (anchored) s.kr[t][d] = kv * kexp<PREC>(-x);
+    }
+}
+
+// Unit-lower inverses of the four 16x16 diagonal blocks of (I + L), by forward
+// substitution in fp32: wave w inverts block w, lane c (< 16) owns column c.
+// L is read from a row-major LDS matrix (leading dimension ldl); the inverse
+// goes to tii[w][row][col].
+template <int LDL>
+__device__ void diag_inverse(const float* __restrict__ L, float (*tii)[BS][BS + 4], int nblocks) {
+    const int w = threadIdx.x >> 6, c = threadIdx.x & 63;
+    if (w < nblocks && c < BS) {
+        const float* Lb = L + (size_t)(BS * w) * LDL + BS * w;
+        float x[BS];
+#pragma unroll
+        for (int t = 0; t < BS; ++t) {
+            float acc = (t == c) ? 1.f : 0.f;
+#pragma unroll
+            for (int j = 0; j < t; ++j) acc -= Lb[t * LDL + j] * x[j];
+            x[t] = acc;
+        }
+#pragma unroll
+        for (int t = 0; t < BS; ++t) tii[w][t][c] = x[t];
+    }
+}
+
+}  // namespace kda

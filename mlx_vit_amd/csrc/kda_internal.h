@@ -1,0 +1,59 @@
+// kda_internal.h -- kernel argument blocks and launcher declarations shared by
+// the kernel translation units and the C-ABI layer.  Not installed.
+//
+// Workspace tensors are fp32, one slab per chunk (chunk id = (b*H + h)*nc + n):
+//   W, U, Qp, Kb, Vp, dVp      [C][D]  row-major (token, channel)
+//   WT, QpT, KbT               [D][C]  transposed copies for MFMA A operands
+//   Aqk, Akk                   [C][C]  (token t, token s), zero above the diagonal
+//   AqkT                       [C][C]  transpose of Aqk
+//   Tii                        [4][16][16] inverses of the diagonal blocks of I + L
+//   eG                         [D]     e^{gamma of the chunk's last row}
+//   h, dh                      [D][D]  state at chunk start / its adjoint at chunk end,
+//                                      [dk][dv] orientation
+#pragma once
+#include <hip/hip_runtime.h>
+#include <type_traits>
+#include "kda_chunk.h"
+
+namespace kda {
+
+struct PrepArgs {
+    const void *q, *k, *v, *g, *beta;
+    float *W, *U, *Qp, *QpT, *Kb, *KbT, *WT, *Aqk, *AqkT, *Akk, *Tii, *eG;
+    int T, H, nc;
+};
+
+struct RecurArgs {
+    const float *W, *U, *Qp, *KbT, *Aqk, *eG;
+    const float* s0;
+    float* s_final;
+    void* o;
+    float *h, *Vp;
+    int T, H, nc, BH;
+};
+
+struct DhArgs {
+    const float *AqkT, *Kb, *QpT, *WT, *eG;
+    const void* dout;
+    const float* dsf;
+    float* ds0;
+    float *dh, *dVp;
+    int T, H, nc, BH;
+};
+
+struct LocalArgs {
+    const void *q, *k, *v, *g, *beta, *dout;
+    const float *W, *U, *Akk, *Tii, *h, *dh, *Vp, *dVp;
+    void *dq, *dk, *dv, *dg, *dbeta;
+    int T, H, nc;
+};
+
+hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
+hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st);
+hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
+hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
+hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,
+                        hipStream_t st);
+hipError_t launch_state_copy(const float* src, float* dst, size_t n, hipStream_t st);
+
+}  // namespace kda

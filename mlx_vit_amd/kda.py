@@ -1,0 +1,196 @@
+"""The KDA chunkwise recurrence on MI355X: torch tensors in, HIP kernels out.
+
+``chunk_kda(q, k, v, g, beta, initial_state)`` has the contract of the
+reference's per-path KDA methods (nope_gdn_mlx.py:3056-3068, 2829-2865):
+
+* ``q, k, v``: (B, T, H, D); ``g``: (B, T, H, D) per-channel log-decay (<= 0);
+  ``beta``: (B, T, H); ``initial_state``: (B, H, D, D) or None (zeros), in the
+  reference orientation ``S[i_v, j_k]`` so that ``o_t = S_t q_t``.
+* returns ``(o, final_state)``: ``o`` in ``q.dtype``, the state in fp32.
+* ``q`` is not scaled inside the op (the layer scales it beforehand,
+  nope_gdn_mlx.py:796-799).
+
+Differentiable in every input, including the initial state.  Arithmetic is fp32
+with an fp32 state; bf16 inputs feed bf16 MFMA operands.  There is no CPU path:
+tensors must live on a ROCm device and the HIP library must be built.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+CHUNK = 64
+FWD_HEAD_DIMS = (32, 64, 128)
+BWD_HEAD_DIMS = (32, 64)
+
+_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _prepare(q, k, v, g, beta, initial_state):
+    """Validate and normalise inputs (contiguous, consistent dtypes)."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+    if q.dim() != 4:
+        raise ValueError(f"q must be (B, T, H, D); got shape {tuple(q.shape)}")
+    B, T, H, D = q.shape
+    for name, t in (("k", k), ("v", v), ("g", g)):
+        if tuple(t.shape) != (B, T, H, D):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != q shape {(B, T, H, D)}")
+    if tuple(beta.shape) != (B, T, H):
+        raise ValueError(f"beta shape {tuple(beta.shape)} != {(B, T, H)}")
+    if initial_state is not None and tuple(initial_state.shape) != (B, H, D, D):
+        raise ValueError(f"initial_state shape {tuple(initial_state.shape)} != {(B, H, D, D)}")
+    if q.dtype not in _DTYPE_CODE:
+        raise ValueError(f"q dtype {q.dtype} unsupported: use float32 or bfloat16")
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError("chunk_kda runs on a ROCm device; got tensors on " + str(dev))
+    for name, t in (("k", k), ("v", v), ("g", g), ("beta", beta)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q on {dev}")
+    dt = q.dtype
+    k, v, beta = (t if t.dtype == dt else t.to(dt) for t in (k, v, beta))
+    if g.dtype not in _DTYPE_CODE:
+        g = g.to(torch.float32)
+    q, k, v, g, beta = (t.contiguous() for t in (q, k, v, g, beta))
+    if initial_state is not None:
+        if initial_state.device != dev:
+            raise ValueError(f"initial_state is on {initial_state.device}, q on {dev}")
+        initial_state = initial_state.to(torch.float32).contiguous()
+    return q, k, v, g, beta, initial_state
+
+
+def _check_chunk(chunk_size: int) -> None:
+    if chunk_size != CHUNK:
+        raise ValueError(f"chunk_size={chunk_size}: the HIP kernels use chunk_size=64")
+
+
+def workspace_bytes(pass_: int, B: int, T: int, H: int, D: int, dtype: torch.dtype = torch.bfloat16) -> int:
+    lib = _lib.load()
+    n = lib.kda_workspace_size(pass_, B, T, H, D, CHUNK, _DTYPE_CODE.get(dtype, 0))
+    if n == 0 and B * T * H > 0:
+        raise ValueError(_lib.last_error())
+    return int(n)
+
+
+def workspace_offsets(pass_: int, B: int, T: int, H: int, D: int) -> dict:
+    lib = _lib.load()
+    arr = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
+    _lib.check(lib.kda_workspace_offsets(pass_, B, T, H, D, CHUNK, 0, arr), "kda_workspace_offsets")
+    return {name: int(arr[i]) for i, name in enumerate(_lib.WS_REGIONS)}
+
+
+def _workspace(pass_: int, B: int, T: int, H: int, D: int, dev: torch.device, dtype) -> torch.Tensor:
+    n = workspace_bytes(pass_, B, T, H, D, dtype)
+    return torch.empty(max(n, 256), dtype=torch.uint8, device=dev)
+
+
+def kda_forward(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
+                workspace: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Forward only (no autograd graph).  Returns (o, final_state)."""
+    _check_chunk(chunk_size)
+    q, k, v, g, beta, s0 = _prepare(q, k, v, g, beta, initial_state)
+    B, T, H, D = q.shape
+    if D not in FWD_HEAD_DIMS:
+        raise ValueError(f"head_dim={D}: the forward supports {FWD_HEAD_DIMS}")
+    lib = _lib.load()
+    dev = q.device
+    o = torch.empty_like(q)
+    s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_FWD, B, T, H, D, dev, q.dtype)
+    rc = lib.kda_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
+                     B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                     _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "kda_fwd")
+    return o, s_final
+
+
+def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size: int = CHUNK,
+                 workspace: Optional[torch.Tensor] = None):
+    """VJP of ``kda_forward``: returns (dq, dk, dv, dg, dbeta, d_initial_state)."""
+    _check_chunk(chunk_size)
+    q, k, v, g, beta, s0 = _prepare(q, k, v, g, beta, initial_state)
+    B, T, H, D = q.shape
+    if D not in BWD_HEAD_DIMS:
+        raise ValueError(f"head_dim={D}: the backward supports {BWD_HEAD_DIMS}")
+    if tuple(do.shape) != (B, T, H, D):
+        raise ValueError(f"do shape {tuple(do.shape)} != {(B, T, H, D)}")
+    do = do.to(q.dtype).contiguous()
+    if ds_final is not None:
+        if tuple(ds_final.shape) != (B, H, D, D):
+            raise ValueError(f"ds_final shape {tuple(ds_final.shape)} != {(B, H, D, D)}")
+        ds_final = ds_final.to(torch.float32).contiguous()
+    lib = _lib.load()
+    dev = q.device
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
+    ds0 = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_BWD, B, T, H, D, dev, q.dtype)
+    rc = lib.kda_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
+                     _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ds0),
+                     B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                     _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "kda_bwd")
+    return dq, dk, dv, dg, dbeta, ds0
+
+
+class ChunkKDAFunction(torch.autograd.Function):
+    """Autograd wrapper: the forward keeps only its inputs; the backward
+    recomputes chunk-boundary states (the role of mx.custom_function in
+    nope_gdn_mlx.py:2725-2808, without the saved U / S trajectories)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state):
+        o, s_final = kda_forward(q, k, v, g, beta, initial_state)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state)
+        ctx.has_state = initial_state is not None
+        return o, s_final
+
+    @staticmethod
+    def backward(ctx, do, ds_final):
+        q, k, v, g, beta, s0 = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros_like(q)
+        dq, dk, dv, dg, dbeta, ds0 = kda_backward(q, k, v, g, beta, s0, do, ds_final)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+                ds0 if ctx.has_state else None)
+
+
+def chunk_kda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+              initial_state: Optional[torch.Tensor] = None, chunk_size: int = CHUNK
+              ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """KDA chunkwise recurrence, differentiable.  Returns (o, final_state)."""
+    _check_chunk(chunk_size)
+    return ChunkKDAFunction.apply(q, k, v, g, beta, initial_state)
+
+
+def solve_unit_triangular(M: torch.Tensor, b: torch.Tensor, upper: bool = False) -> torch.Tensor:
+    """y = M^-1 b for unit-triangular M (BH, C, C), b (BH, C, N); fp32, C <= 64.
+    The HIP counterpart of GatedDeltaLayer._metal_solve_triangular(_upper)
+    (nope_gdn_mlx.py:1160-1196, 1261-1286)."""
+    if M.dim() != 3 or b.dim() != 3 or M.shape[0] != b.shape[0] or M.shape[1] != M.shape[2] \
+            or b.shape[1] != M.shape[1]:
+        raise ValueError(f"shape mismatch: M {tuple(M.shape)}, b {tuple(b.shape)}")
+    if M.device.type != "cuda" or b.device != M.device:
+        raise ValueError("solve_unit_triangular runs on a ROCm device")
+    M = M.to(torch.float32).contiguous()
+    b = b.to(torch.float32).contiguous()
+    y = torch.empty_like(b)
+    BH, Cm, N = b.shape
+    rc = _lib.load().kda_solve_unit_triangular(_ptr(M), _ptr(b), _ptr(y), BH, Cm, N, int(bool(upper)),
+                                               _stream(M.device))
+    _lib.check(rc, "kda_solve_unit_triangular")
+    return y

@@ -1,0 +1,302 @@
+"""GPU parity tests: the HIP path through the C ABI against the CPU oracle.
+
+Bars: rel-L2 <= 1e-4 with fp32 inputs, <= 1e-2 with bf16 inputs (the oracle
+runs in fp64 on the same bf16-rounded values).  Outputs o, final state and the
+gradients dq, dk, dv, dg, dbeta, dS0 are all checked.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cref
+from oracle import kda_reference as R
+from tests import kda_model as M
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-4, torch.bfloat16: 1e-2}
+DEV = "cuda"
+
+
+def _kda():
+    import mlx_vit_amd
+    return mlx_vit_amd
+
+
+def _inputs(B, T, H, D, dtype, seed=0, with_state=False, g_scale=0.1, grad=False):
+    x = R.make_inputs(B, T, H, D, dtype=dtype, seed=seed, with_state=with_state,
+                      with_grad=grad, g_scale=g_scale)
+    return x
+
+
+def _dev(x, names=("q", "k", "v", "g", "beta")):
+    return [x[n].to(DEV) for n in names]
+
+
+def _fwd_errors(x, dtype):
+    kda = _kda()
+    q, k, v, g, beta = _dev(x)
+    s0 = x["s0"].to(DEV) if x["s0"] is not None else None
+    o, sf = kda.kda_forward(q, k, v, g, beta, s0)
+    torch.cuda.synchronize()
+    ref = cref.forward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"])
+    return {"o": R.rel_l2(o.cpu(), ref["o"]), "s_final": R.rel_l2(sf.cpu(), ref["s_final"])}
+
+
+def _bwd_errors(x, dtype, dsf=None):
+    kda = _kda()
+    q, k, v, g, beta = _dev(x)
+    s0 = x["s0"].to(DEV) if x["s0"] is not None else None
+    do = x["do"].to(DEV)
+    grads = kda.kda_backward(q, k, v, g, beta, s0, do, None if dsf is None else dsf.to(DEV))
+    torch.cuda.synchronize()
+    ref = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"], dsf)
+    names = ("dq", "dk", "dv", "dg", "dbeta", "ds0")
+    return {n: R.rel_l2(gr.cpu(), ref[n]) for n, gr in zip(names, grads)}
+
+
+def _assert_all(errs, tol, case):
+    print(case, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    bad = {k: v for k, v in errs.items() if not (v <= tol)}
+    assert not bad, f"{case}: rel-L2 above {tol}: {bad}"
+
+
+# ---------------------------------------------------------------- stage checks
+
+def _ws_view(ws, off, shape):
+    n = int(np.prod(shape))
+    return ws[off:off + 4 * n].view(torch.float32).reshape(shape)
+
+
+def test_prep_workspace_matches_model():
+    """The forward prep kernel's workspace equals the float64 decomposition model."""
+    kda = _kda()
+    B, T, H, D = 1, 100, 2, 64
+    x = _inputs(B, T, H, D, torch.float32, seed=5, g_scale=0.5)
+    q, k, v, g, beta = _dev(x)
+    ws = torch.zeros(kda.workspace_bytes(0, B, T, H, D, torch.float32), dtype=torch.uint8, device=DEV)
+    kda.kda_forward(q, k, v, g, beta, None, workspace=ws)
+    torch.cuda.synchronize()
+    off = kda.workspace_offsets(0, B, T, H, D)
+    nc = (T + 63) // 64
+    N = B * H * nc
+    f = lambda t: R.fold_heads(t.double())
+    pad = nc * 64 - T
+    z = lambda t: torch.cat([t, torch.zeros((t.shape[0], pad) + t.shape[2:], dtype=t.dtype)], 1)
+    qf, kf, vf, gf, bf = (z(f(x[n])) for n in ("q", "k", "v", "g", "beta"))
+    P = M.prep(qf.reshape(N, 64, D), kf.reshape(N, 64, D), vf.reshape(N, 64, D), gf.reshape(N, 64, D),
+               bf.reshape(N, 64))
+    wsc = ws.cpu()
+    errs = {
+        "W": R.rel_l2(_ws_view(wsc, off["W"], (N, 64, D)), P["W"]),
+        "U": R.rel_l2(_ws_view(wsc, off["U"], (N, 64, D)), P["U"]),
+        "Qp": R.rel_l2(_ws_view(wsc, off["Qp"], (N, 64, D)), P["Qp"]),
+        "KbT": R.rel_l2(_ws_view(wsc, off["KbT"], (N, D, 64)), P["Kb"].transpose(-1, -2)),
+        "Aqk": R.rel_l2(_ws_view(wsc, off["Aqk"], (N, 64, 64)), P["Aqk"]),
+        "eG": R.rel_l2(_ws_view(wsc, off["eG"], (N, D)), P["eG"]),
+    }
+    _assert_all(errs, 1e-4, "prep fp32")
+
+
+def test_bwd_workspace_matches_model():
+    """Backward intermediates (recomputed states, dh, V', dV') equal the model."""
+    kda = _kda()
+    B, T, H, D = 1, 130, 2, 64
+    x = _inputs(B, T, H, D, torch.float32, seed=6, with_state=True, grad=True, g_scale=0.3)
+    q, k, v, g, beta = _dev(x)
+    s0, do = x["s0"].to(DEV), x["do"].to(DEV)
+    ws = torch.zeros(kda.workspace_bytes(1, B, T, H, D, torch.float32), dtype=torch.uint8, device=DEV)
+    kda.kda_backward(q, k, v, g, beta, s0, do, None, workspace=ws)
+    torch.cuda.synchronize()
+    off = kda.workspace_offsets(1, B, T, H, D)
+    nc = (T + 63) // 64
+    N = B * H * nc
+    f = lambda t: R.fold_heads(t.double())
+    _, aux = M.backward(f(x["q"]), f(x["k"]), f(x["v"]), f(x["g"]), f(x["beta"]),
+                        x["s0"].double().reshape(B * H, D, D), f(x["do"]), None, return_aux=True)
+    P = aux["P"]
+    wsc = ws.cpu()
+    errs = {
+        "W": R.rel_l2(_ws_view(wsc, off["W"], (N, 64, D)), P["W"]),
+        "WT": R.rel_l2(_ws_view(wsc, off["WT"], (N, D, 64)), P["W"].transpose(-1, -2)),
+        "QpT": R.rel_l2(_ws_view(wsc, off["QpT"], (N, D, 64)), P["Qp"].transpose(-1, -2)),
+        "Kb": R.rel_l2(_ws_view(wsc, off["Kb"], (N, 64, D)), P["Kb"]),
+        "AqkT": R.rel_l2(_ws_view(wsc, off["AqkT"], (N, 64, 64)), P["Aqk"].transpose(-1, -2)),
+        "Akk": R.rel_l2(_ws_view(wsc, off["Akk"], (N, 64, 64)), P["Akk"]),
+        "h": R.rel_l2(_ws_view(wsc, off["h"], (N, D, D)), aux["h"]),
+        "Vp": R.rel_l2(_ws_view(wsc, off["Vp"], (N, 64, D)), aux["Vp"]),
+        "dh": R.rel_l2(_ws_view(wsc, off["dh"], (N, D, D)), aux["dh"]),
+        "dVp": R.rel_l2(_ws_view(wsc, off["dVp"], (N, 64, D)), aux["dVp"]),
+    }
+    _assert_all(errs, 1e-4, "bwd workspace fp32")
+
+
+# ---------------------------------------------------------------- forward parity
+
+@pytest.mark.parametrize("B,T,H,D,with_state", [
+    (1, 256, 2, 64, False),     # config 0
+    (1, 256, 2, 64, True),
+    (2, 100, 3, 64, True),      # ragged last chunk
+    (1, 1, 1, 64, True),        # single token
+    (1, 63, 2, 32, False),
+    (1, 65, 2, 32, True),
+    (1, 200, 2, 128, True),
+])
+def test_fwd_parity_fp32(B, T, H, D, with_state):
+    x = _inputs(B, T, H, D, torch.float32, seed=1, with_state=with_state)
+    _assert_all(_fwd_errors(x, torch.float32), TOL[torch.float32], f"fwd fp32 {B},{T},{H},{D},{with_state}")
+
+
+@pytest.mark.parametrize("B,T,H,D,with_state", [
+    (2, 300, 4, 64, True),
+    (1, 129, 2, 128, False),
+    (1, 64, 3, 32, True),
+])
+def test_fwd_parity_bf16(B, T, H, D, with_state):
+    x = _inputs(B, T, H, D, torch.bfloat16, seed=2, with_state=with_state)
+    _assert_all(_fwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], f"fwd bf16 {B},{T},{H},{D},{with_state}")
+
+
+def test_fwd_parity_config1_full():
+    """Config 1: B=8, H=12, T=1568, D=64, bf16 -- full size against the fp64 oracle."""
+    x = _inputs(8, 1568, 12, 64, torch.bfloat16, seed=0)
+    _assert_all(_fwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "config1 fwd")
+
+
+def test_fwd_parity_config3_long():
+    """Config 3: B=1, H=16, T=32768, D=128, bf16, nonzero fp32 initial state."""
+    x = _inputs(1, 32768, 16, 128, torch.bfloat16, seed=0, with_state=True)
+    _assert_all(_fwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "config3 fwd")
+
+
+def test_fwd_strong_decay_pairwise_path():
+    """Decays beyond the anchored span guard take the pairwise path; still exact."""
+    x = _inputs(1, 160, 2, 64, torch.float32, seed=3, with_state=True, g_scale=6.0)
+    _assert_all(_fwd_errors(x, torch.float32), TOL[torch.float32], "fwd strong decay")
+
+
+def test_fwd_moderate_decay_anchored_path():
+    """Spans up to the guard stay on the anchored MFMA path."""
+    x = _inputs(1, 160, 2, 64, torch.float32, seed=4, with_state=True, g_scale=2.0)
+    _assert_all(_fwd_errors(x, torch.float32), TOL[torch.float32], "fwd moderate decay")
+
+
+def test_fwd_beta_zero_is_pure_decay():
+    """beta = 0: no writes, the state only decays and o_t = S_t q_t."""
+    kda = _kda()
+    x = _inputs(1, 70, 2, 64, torch.float32, seed=7, with_state=True)
+    x["beta"] = torch.zeros_like(x["beta"])
+    q, k, v, g, beta = _dev(x)
+    o, sf = kda.kda_forward(q, k, v, g, beta, x["s0"].to(DEV))
+    G = torch.cumsum(x["g"].double(), 1)                                  # (B, T, H, D)
+    S = x["s0"].double()[:, None] * torch.exp(G)[:, :, :, None, :]      # (B, T, H, D, D)
+    o_ref = torch.einsum("bthij,bthj->bthi", S, x["q"].double())
+    assert R.rel_l2(o.cpu(), o_ref) <= 1e-5
+    assert R.rel_l2(sf.cpu(), S[:, -1]) <= 1e-5
+
+
+# ---------------------------------------------------------------- backward parity
+
+@pytest.mark.parametrize("B,T,H,D,with_state,with_dsf", [
+    (1, 256, 2, 64, False, False),
+    (1, 256, 2, 64, True, True),
+    (2, 100, 3, 64, True, True),
+    (1, 1, 1, 64, True, True),
+    (1, 65, 2, 32, True, False),
+])
+def test_bwd_parity_fp32(B, T, H, D, with_state, with_dsf):
+    x = _inputs(B, T, H, D, torch.float32, seed=11, with_state=with_state, grad=True)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9)) if with_dsf else None
+    _assert_all(_bwd_errors(x, torch.float32, dsf), TOL[torch.float32],
+                f"bwd fp32 {B},{T},{H},{D},{with_state},{with_dsf}")
+
+
+def test_bwd_strong_decay_pairwise_path():
+    x = _inputs(1, 130, 2, 64, torch.float32, seed=12, with_state=True, grad=True, g_scale=6.0)
+    _assert_all(_bwd_errors(x, torch.float32), TOL[torch.float32], "bwd strong decay")
+
+
+def test_bwd_parity_bf16_small():
+    x = _inputs(2, 300, 4, 64, torch.bfloat16, seed=13, with_state=True, grad=True)
+    _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "bwd bf16 small")
+
+
+def test_bwd_parity_config2_full():
+    """Config 2: fwd + VJP at B=8, H=12, T=1568, D=64 bf16, dO ~ N(0,1) bf16."""
+    x = _inputs(8, 1568, 12, 64, torch.bfloat16, seed=0, grad=True)
+    _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "config2 bwd")
+
+
+# ---------------------------------------------------------------- autograd / API
+
+def test_autograd_function_matches_direct_backward():
+    kda = _kda()
+    B, T, H, D = 1, 90, 2, 64
+    x = _inputs(B, T, H, D, torch.float32, seed=21, with_state=True, grad=True)
+    leaves = [t.to(DEV).requires_grad_(True) for t in (x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"])]
+    o, sf = kda.chunk_kda(*leaves)
+    dsf = torch.randn(B, H, D, D, device=DEV)
+    (o * x["do"].to(DEV)).sum().backward(retain_graph=True)
+    g1 = [t.grad.clone() for t in leaves]
+    for t in leaves:
+        t.grad = None
+    ((o * x["do"].to(DEV)).sum() + (sf * dsf).sum()).backward()
+    direct = kda.kda_backward(*[t.detach() for t in leaves[:5]], leaves[5].detach(), x["do"].to(DEV), dsf)
+    for a, b in zip([t.grad for t in leaves], direct):
+        assert R.rel_l2(a.cpu(), b.cpu()) < 1e-6
+    ref = R.autograd_reference(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"])
+    for a, n in zip(g1, ("dq", "dk", "dv", "dg", "dbeta", "ds0")):
+        assert R.rel_l2(a.cpu(), ref[n]) <= 1e-4, n
+
+
+def test_recurrence_dispatch_matches_op():
+    kda = _kda()
+    x = _inputs(1, 64, 2, 64, torch.bfloat16, seed=22)
+    q, k, v, g, beta = _dev(x)
+    rec = kda.KDARecurrence(num_heads=2, head_dim=64)
+    o1, s1 = rec(q, k, v, g, beta)
+    o2, s2 = kda.kda_forward(q, k, v, g, beta)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    with pytest.raises(ValueError):
+        rec(q, k, v, g, beta, compute_path="metal")
+
+
+def test_empty_sequence():
+    kda = _kda()
+    q = torch.zeros(1, 0, 2, 64, device=DEV)
+    beta = torch.zeros(1, 0, 2, device=DEV)
+    s0 = torch.randn(1, 2, 64, 64, device=DEV)
+    o, sf = kda.kda_forward(q, q, q, q, beta, s0)
+    assert o.shape == (1, 0, 2, 64) and torch.equal(sf, s0)
+
+
+def test_deterministic_repeat():
+    kda = _kda()
+    x = _inputs(2, 200, 3, 64, torch.bfloat16, seed=23, grad=True)
+    q, k, v, g, beta = _dev(x)
+    a = kda.kda_forward(q, k, v, g, beta)
+    b = kda.kda_forward(q, k, v, g, beta)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    ga = kda.kda_backward(q, k, v, g, beta, None, x["do"].to(DEV))
+    gb = kda.kda_backward(q, k, v, g, beta, None, x["do"].to(DEV))
+    for u, w in zip(ga, gb):
+        assert torch.equal(u, w)
+
+
+# ---------------------------------------------------------------- triangular solve KAT
+
+@pytest.mark.parametrize("upper", [False, True])
+def test_solve_triangular_kat(upper):
+    """nope_gdn_mlx.py:4793-4835: numpy seed 0 per C, L = tril(randn*0.1, -1) + I,
+    b = randn(BH, C, C), rel-max error < 1e-4 against numpy.linalg.solve."""
+    kda = _kda()
+    BH = 4
+    for C in [4, 8, 16, 32, 40, 48, 56, 64]:
+        np.random.seed(0)
+        Lm = np.tril(np.random.randn(BH, C, C).astype(np.float32) * 0.1, k=-1) + np.eye(C, dtype=np.float32)
+        b = np.random.randn(BH, C, C).astype(np.float32)
+        Mm = np.ascontiguousarray(np.transpose(Lm, (0, 2, 1))) if upper else Lm
+        y_np = np.stack([np.linalg.solve(Mm[i], b[i]) for i in range(BH)])
+        y = kda.solve_unit_triangular(torch.from_numpy(Mm).to(DEV), torch.from_numpy(b).to(DEV), upper=upper)
+        rel = float(np.max(np.abs(y.cpu().numpy() - y_np))) / (float(np.max(np.abs(y_np))) + 1e-9)
+        assert rel < 1e-4, (C, rel)
