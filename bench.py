@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the KDA chunkwise recurrence on one MI355X.
+
+A step is one forward + backward (VJP) pass of the op over one batch of
+synthetic inputs already resident in HBM: config 2, B=8, H=12, T=1568, D=64,
+chunk 64, bf16 q/k/v/g/beta, dO ~ N(0,1) bf16, zero initial state.  Prints ONE
+JSON line.  ``value`` is tokens/s = B*T*steps / wall time of the timed steps.
+
+Per-kernel durations come from HIP events the library records around each of
+its launches (kda_profile_*) during a second pass of the same steps; the
+dominant kernel's roofline is reported from them.  The ``cpu_baseline`` leg
+times the torch fp32 restatement of the reference's 'compiled' path
+(nope_gdn_mlx.py:890-917, autograd for the VJP) on the host cores over a
+bounded sample, and checks the HIP outputs against the fp64 C oracle.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload cfg2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+METRIC = "KDA fwd+bwd tokens/sec @B8 H12 T1568 d64 bf16; % MFMA peak; rel-L2 err"
+PEAK_HBM = 8.0e12            # B/s, MI355X HBM3E
+PEAK_BF16 = 2.5e15           # FLOP/s, MI355X dense bf16 MFMA
+C = 64
+
+WORKLOADS = {
+    # name: (B, T, H, D, backward, with_state, description)
+    "cfg2": (8, 1568, 12, 64, True, False, "KDA fwd+VJP, B8 H12 T1568 D64 bf16 (config 2)"),
+    "cfg1": (8, 1568, 12, 64, False, False, "KDA fwd, B8 H12 T1568 D64 bf16 (config 1)"),
+    "cfg3": (1, 32768, 16, 128, False, True, "KDA fwd, B1 H16 T32768 D128 bf16, fp32 S0 (config 3)"),
+}
+
+
+def op_counts(B, T, H, D, backward):
+    """Algorithmic FLOPs and HBM bytes of the whole op (bf16 inputs, fp32 states):
+    FLOPs per token-head 10CD + 6D^2 + (2/3)C^2 forward, x3 for fwd+bwd; bytes =
+    inputs once, outputs once, states at fp32, nothing stored between passes."""
+    n = B * T * H
+    f_fwd = 10 * C * D + 6 * D * D + (2.0 / 3.0) * C * C
+    flops = n * f_fwd * (3 if backward else 1)
+    es = 2
+    states = B * H * D * D * 4
+    fwd_bytes = n * (4 * D + 1) * es + n * D * es + states
+    if not backward:
+        return flops, fwd_bytes
+    bwd_bytes = n * (5 * D + 1) * es + n * (4 * D + 1) * es + states
+    return flops, fwd_bytes + bwd_bytes
+
+
+def kernel_counts(B, T, H, D):
+    """Per-launch algorithmic FLOPs and compulsory bytes of each library kernel
+    (ids as in kda_profile_name).  FLOPs: the dense products each kernel owns,
+    full rectangles, per token-head; bytes: each input and output tensor of the
+    kernel touched once (inputs bf16, workspace fp32)."""
+    nc = -(-T // C)
+    N = B * H * nc              # chunks
+    n = N * C                   # padded token-heads
+    es, f4 = 2, 4
+    CD, CC, DD = C * D, C * C, D * D
+    fl = {
+        0: n * (8 * C * D + (2.0 / 3.0) * C * C),       # Akk, Aqk, W, U, solve
+        1: n * (6 * D * D + 2 * C * D),                 # W S, Qp S, Kb^T V', Aqk V'
+        2: n * (8 * C * D + (2.0 / 3.0) * C * C),
+        3: n * (4 * D * D),                             # W S, Kb^T V'
+        4: n * (2 * C * D + 6 * D * D),                 # Aqk^T dO, Kb dS, Qp^T dO, W^T dV'
+        5: n * (6 * D * D + 16 * C * D),                # dQp, dKb, dW, dAqk, solve adjoint, dL, K K^T / Q K^T adjoints
+    }
+    by = {
+        0: N * (4 * CD * es + C * es + 4 * CD * f4 + CC * f4 + D * f4),
+        1: N * (4 * CD * f4 + CC * f4 + D * f4 + CD * es) + B * H * DD * f4,
+        2: N * (4 * CD * es + C * es + 6 * CD * f4 + 2 * CC * f4 + 4 * 256 * f4 + D * f4),
+        3: N * (3 * CD * f4 + D * f4 + DD * f4 + CD * f4),
+        4: N * (CC * f4 + 3 * CD * f4 + D * f4 + CD * es + DD * f4 + CD * f4) + B * H * DD * f4,
+        5: N * (5 * CD * es + C * es + 4 * CD * f4 + CC * f4 + 4 * 256 * f4 + 2 * DD * f4 + 4 * CD * es + C * es),
+    }
+    return fl, by
+
+
+def make_inputs_gpu(B, T, H, D, with_state, seed=0):
+    """Synthetic inputs with the configs' distributions, drawn on the GPU."""
+    import torch
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    shp = (B, T, H, D)
+
+    def l2n(x):
+        return x / torch.clamp(torch.linalg.vector_norm(x, dim=-1, keepdim=True), min=1e-12)
+    q = l2n(torch.randn(shp, generator=gen, device="cuda"))
+    k = l2n(torch.randn(shp, generator=gen, device="cuda"))
+    v = torch.randn(shp, generator=gen, device="cuda")
+    beta = torch.sigmoid(torch.randn((B, T, H), generator=gen, device="cuda"))
+    g = -torch.nn.functional.softplus(torch.randn(shp, generator=gen, device="cuda")) * 0.1
+    s0 = torch.randn((B, H, D, D), generator=gen, device="cuda") * 0.02 if with_state else None
+    do = torch.randn(shp, generator=gen, device="cuda")
+    bf = torch.bfloat16
+    return q.to(bf), k.to(bf), v.to(bf), g.to(bf), beta.to(bf), s0, do.to(bf)
+
+
+def load_traffic(kernel_name):
+    """HBM bytes per dispatch of a kernel from the committed rocprofv3 PMC
+    summary (profiles/traffic.json), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel_name)
+        return None if rec is None else float(rec["bytes_per_dispatch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, seed=0):
+    """Time the torch fp32 restatement of the reference 'compiled' path on the
+    host cores (bounded sample: the same B, H, D over `sample_tokens` steps),
+    and measure rel-L2 of the HIP results against the fp64 C oracle on the
+    same seeded inputs (drawn on the CPU so the oracle can regenerate them)."""
+    import torch
+    from oracle import cref
+    from oracle import kda_reference as R
+    import mlx_vit_amd as kda
+
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    # --- timing sample
+    Ts = min(T, sample_tokens)
+    xs = R.make_inputs(B, Ts, H, D, dtype=torch.float32, seed=seed, with_state=with_state, with_grad=True)
+
+    def run():
+        leaves = [xs[nm].clone().requires_grad_(backward) for nm in ("q", "k", "v", "g", "beta")]
+        o, sf = R.loop_compiled_kda(*leaves, xs["s0"], compute_dtype=torch.float32)
+        if backward:
+            torch.sum(o * xs["do"]).backward()
+    run()                                  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t_med = sorted(times)[1]
+    cpu_tps = B * Ts / t_med
+    # --- parity at the full workload size
+    x = R.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=seed, with_state=with_state, with_grad=backward)
+    dev = lambda t: None if t is None else t.to("cuda")
+    q, k, v, g, beta, s0 = (dev(x[nm]) for nm in ("q", "k", "v", "g", "beta", "s0"))
+    o, sf = kda.kda_forward(q, k, v, g, beta, s0)
+    ref = cref.forward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"])
+    errs = {"o": R.rel_l2(o.cpu(), ref["o"]), "s_final": R.rel_l2(sf.cpu(), ref["s_final"])}
+    if backward:
+        grads = kda.kda_backward(q, k, v, g, beta, s0, dev(x["do"]))
+        rb = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"])
+        for nm, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads):
+            errs[nm] = R.rel_l2(gr.cpu(), rb[nm])
+    baseline = {
+        "value": round(cpu_tps, 2), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"torch fp32 restatement of _loop_compiled_kda (D x D x D step matmul, autograd VJP) "
+                   f"at B={B} H={H} D={D} over T={Ts} tokens, median of 3 after 1 warm-up, "
+                   f"{t_med:.2f} s per {'fwd+bwd' if backward else 'fwd'}"),
+    }
+    return baseline, {n: float(f"{e:.3e}") for n, e in errs.items()}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=392)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the op on a "
+              "single MI355X and reports that GPU's throughput.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import mlx_vit_amd as kda
+    from mlx_vit_amd import _lib
+
+    B, T, H, D, backward, with_state, desc = WORKLOADS[args.workload]
+    torch.cuda.set_device(0)
+    q, k, v, g, beta, s0, do = make_inputs_gpu(B, T, H, D, with_state)
+    wsf = torch.empty(kda.workspace_bytes(0, B, T, H, D), dtype=torch.uint8, device="cuda")
+    wsb = (torch.empty(kda.workspace_bytes(1, B, T, H, D), dtype=torch.uint8, device="cuda")
+           if backward else None)
+
+    def step():
+        o, sf = kda.kda_forward(q, k, v, g, beta, s0, workspace=wsf)
+        if backward:
+            kda.kda_backward(q, k, v, g, beta, s0, do, None, workspace=wsb)
+        return o
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+    tokens_per_s = B * T * args.steps / elapsed
+
+    # second pass with per-kernel events
+    lib = _lib.load()
+    lib.kda_profile_enable(1)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    prof_ms_per_step = (time.perf_counter() - t1) / args.steps * 1e3
+    lib.kda_profile_enable(0)
+    import ctypes
+    fl, by = kernel_counts(B, T, H, D)
+    kernels = []
+    for kid in range(_lib.PROF_NKERNELS):
+        tot, cnt = ctypes.c_double(), ctypes.c_int()
+        _lib.check(lib.kda_profile_read(kid, ctypes.byref(tot), ctypes.byref(cnt)), "kda_profile_read")
+        if cnt.value == 0:
+            continue
+        avg_s = tot.value / cnt.value * 1e-3
+        kernels.append({
+            "name": lib.kda_profile_name(kid).decode(), "launches": cnt.value, "avg_us": round(avg_s * 1e6, 2),
+            "tflops": round(fl[kid] / avg_s / 1e12, 2), "mfma_frac": round(fl[kid] / avg_s / PEAK_BF16, 4),
+            "gbs": round(by[kid] / avg_s / 1e9, 1), "hbm_frac": round(by[kid] / avg_s / PEAK_HBM, 4),
+            "alg_flops": fl[kid], "alg_bytes": by[kid], "_avg_s": avg_s, "_id": kid,
+        })
+    dom = max(kernels, key=lambda r: r["avg_us"] * r["launches"])
+    t_mfma, t_hbm = dom["alg_flops"] / PEAK_BF16, dom["alg_bytes"] / PEAK_HBM
+    if t_mfma >= t_hbm:
+        rl = {"bound": "mfma", "achieved": round(dom["alg_flops"] / dom["_avg_s"] / 1e12, 3),
+              "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s"}
+    else:
+        rl = {"bound": "hbm", "achieved": round(dom["alg_bytes"] / dom["_avg_s"] / 1e9, 2),
+              "peak": PEAK_HBM / 1e9, "unit": "GB/s"}
+    rl["frac"] = round(rl["achieved"] / rl["peak"], 5)
+    rl["traffic"] = load_traffic(dom["name"])
+    rl["kernel"] = dom["name"]
+    rl["avg_us"] = dom["avg_us"]
+    for r in kernels:
+        r.pop("_avg_s")
+        r.pop("_id")
+
+    op_flops, op_bytes = op_counts(B, T, H, D, backward)
+    step_s = ms_per_step * 1e-3
+    out = {
+        "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)-derived inputs of the config's distributions, resident in HBM)",
+        "config": {"workload": desc, "B": B, "T": T, "H": H, "D": D, "chunk": C,
+                   "backward": backward, "initial_state": with_state, "state_dtype": "fp32"},
+        "mfma_frac_op": round(op_flops / step_s / PEAK_BF16, 5),
+        "hbm_frac_op": round(op_bytes / step_s / PEAK_HBM, 5),
+        "roofline": rl,
+        "kernels": kernels,
+        "profiled_ms_per_step": round(prof_ms_per_step, 4),
+    }
+    if not args.no_cpu_baseline:
+        cb, errs = cpu_baseline_leg(B, T, H, D, backward, with_state, None, args.cpu_sample_tokens)
+        out["cpu_baseline"] = cb
+        out["rel_l2"] = errs
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -92,6 +92,18 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
 int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, int Cm, int N,
                               int upper, void* stream);
 
+/* ---- launch timing (instrumentation; no counterpart in the reference) ----
+ * With profiling on, every kernel launch made by kda_fwd / kda_bwd is
+ * bracketed by two HIP events recorded on the launch stream.  Used by the
+ * benchmark to measure per-kernel durations live; the kernels do the same work
+ * either way.  Kernel ids: 0 prep (forward), 1 recurrence (forward), 2 prep
+ * (backward), 3 state recompute, 4 reverse state recurrence, 5 local adjoints.
+ * kda_profile_read must be called after the streams have completed. */
+#define KDA_PROF_NKERNELS 6
+int kda_profile_enable(int on);              /* 1: clear records and start; 0: stop */
+const char* kda_profile_name(int id);
+int kda_profile_read(int id, double* total_ms, int* launches);
+
 #ifdef __cplusplus
 }
 #endif

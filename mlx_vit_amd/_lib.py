@@ -33,7 +33,11 @@ SIGNATURES = {
     "kda_fwd": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_bwd": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_solve_unit_triangular": ([_P] * 3 + [_I] * 4 + [_P], _I),
+    "kda_profile_enable": ([_I], _I),
+    "kda_profile_name": ([_I], ctypes.c_char_p),
+    "kda_profile_read": ([_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)], _I),
 }
+PROF_NKERNELS = 6
 
 _lib = None
 _lock = threading.Lock()

@@ -3,7 +3,9 @@
 // Also the standalone unit-triangular solve and a small state-copy kernel.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/kda_hip.h"
 #include "kda_internal.h"
@@ -108,6 +110,52 @@ int check_scalar(const void* p, const char* name, int dtype) {
 
 int hip_fail(hipError_t e, const char* where) {
     return fail(KDA_E_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+// ---- optional launch timing: an event pair around each launch, on its stream ----
+enum { PROF_PREP_FWD = 0, PROF_RECUR_FWD, PROF_PREP_BWD, PROF_RECUR_H, PROF_DH, PROF_LOCAL };
+const char* const kProfNames[KDA_PROF_NKERNELS] = {"kda_prep_kernel(fwd)", "kda_recur_kernel(fwd)",
+                                                   "kda_prep_kernel(bwd)", "kda_recur_kernel(states)",
+                                                   "kda_dh_kernel", "kda_bwd_local_kernel"};
+struct Profiler {
+    std::mutex mu;
+    bool on = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pool[KDA_PROF_NKERNELS];
+    size_t used[KDA_PROF_NKERNELS] = {};
+};
+Profiler& profiler() {
+    static Profiler p;
+    return p;
+}
+int prof_start(int id, hipStream_t st) {
+    Profiler& P = profiler();
+    std::lock_guard<std::mutex> lk(P.mu);
+    if (!P.on) return -1;
+    if (P.used[id] == P.pool[id].size()) {
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess) return -1;
+        if (hipEventCreate(&b) != hipSuccess) {
+            (void)hipEventDestroy(a);
+            return -1;
+        }
+        P.pool[id].emplace_back(a, b);
+    }
+    const int idx = (int)P.used[id]++;
+    (void)hipEventRecord(P.pool[id][idx].first, st);
+    return idx;
+}
+void prof_stop(int id, int idx, hipStream_t st) {
+    if (idx < 0) return;
+    Profiler& P = profiler();
+    std::lock_guard<std::mutex> lk(P.mu);
+    (void)hipEventRecord(P.pool[id][idx].second, st);
+}
+template <typename F>
+hipError_t timed(int id, hipStream_t st, F&& launch) {
+    const int pi = prof_start(id, st);
+    const hipError_t e = launch();
+    prof_stop(id, pi, st);
+    return e;
 }
 
 }  // namespace
@@ -243,14 +291,16 @@ int kda_fwd(const void* q, const void* k, const void* v, const void* g, const vo
     pa.Aqk = region(workspace, L, KDA_WS_AQK);
     pa.eG = region(workspace, L, KDA_WS_EG);
     pa.T = T; pa.H = H; pa.nc = nc;
-    hipError_t e = kda::launch_prep(pa, D, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16, BH * nc, st);
+    hipError_t e = timed(PROF_PREP_FWD, st, [&] {
+        return kda::launch_prep(pa, D, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16, BH * nc, st);
+    });
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     kda::RecurArgs ra = {};
     ra.W = pa.W; ra.U = pa.U; ra.Qp = pa.Qp; ra.KbT = pa.KbT; ra.Aqk = pa.Aqk; ra.eG = pa.eG;
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-    e = kda::launch_recur(ra, D, dtype == KDA_DTYPE_BF16, 0, st);
+    e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, dtype == KDA_DTYPE_BF16, 0, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
     return ok();
 }
@@ -305,20 +355,20 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
     pa.W = W; pa.U = U; pa.KbT = KbT; pa.eG = eG; pa.WT = WT; pa.QpT = QpT; pa.Kb = Kb;
     pa.AqkT = AqkT; pa.Akk = Akk; pa.Tii = Tii;
     pa.T = T; pa.H = H; pa.nc = nc;
-    hipError_t e = kda::launch_prep(pa, D, in_bf16, g_bf16, BH * nc, st);
+    hipError_t e = timed(PROF_PREP_BWD, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, BH * nc, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     kda::RecurArgs ra = {};
     ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-    e = kda::launch_recur(ra, D, in_bf16, 1, st);
+    e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
 
     kda::DhArgs da = {};
     da.AqkT = AqkT; da.Kb = Kb; da.QpT = QpT; da.WT = WT; da.eG = eG; da.dout = dout; da.dsf = ds_final;
     da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
     da.T = T; da.H = H; da.nc = nc; da.BH = BH;
-    e = kda::launch_dh(da, D, in_bf16, st);
+    e = timed(PROF_DH, st, [&] { return kda::launch_dh(da, D, in_bf16, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_dh_kernel");
 
     kda::LocalArgs la = {};
@@ -326,7 +376,7 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
     la.W = W; la.U = U; la.Akk = Akk; la.Tii = Tii; la.h = hS; la.dh = dhS; la.Vp = Vp; la.dVp = dVp;
     la.dq = dq; la.dk = dk; la.dv = dv; la.dg = dg; la.dbeta = dbeta;
     la.T = T; la.H = H; la.nc = nc;
-    e = kda::launch_local(la, D, in_bf16, g_bf16, BH * nc, st);
+    e = timed(PROF_LOCAL, st, [&] { return kda::launch_local(la, D, in_bf16, g_bf16, BH * nc, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_bwd_local_kernel");
     return ok();
 }
@@ -339,6 +389,37 @@ int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, 
     if (BH == 0) return ok();
     const hipError_t e = kda::launch_solve(M, b, y, BH, Cm, N, upper, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "kda_solve_kernel");
+}
+
+int kda_profile_enable(int on) {
+    Profiler& P = profiler();
+    std::lock_guard<std::mutex> lk(P.mu);
+    if (on)
+        for (int i = 0; i < KDA_PROF_NKERNELS; ++i) P.used[i] = 0;
+    P.on = on != 0;
+    return ok();
+}
+
+const char* kda_profile_name(int id) {
+    return (id >= 0 && id < KDA_PROF_NKERNELS) ? kProfNames[id] : "";
+}
+
+int kda_profile_read(int id, double* total_ms, int* launches) {
+    if (id < 0 || id >= KDA_PROF_NKERNELS || !total_ms || !launches)
+        return fail(KDA_E_INVALID, "kda_profile_read: bad arguments");
+    Profiler& P = profiler();
+    std::lock_guard<std::mutex> lk(P.mu);
+    double tot = 0.0;
+    for (size_t i = 0; i < P.used[id]; ++i) {
+        hipError_t e = hipEventSynchronize(P.pool[id][i].second);
+        float ms = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, P.pool[id][i].first, P.pool[id][i].second);
+        if (e != hipSuccess) return hip_fail(e, "kda_profile_read");
+        tot += ms;
+    }
+    *total_ms = tot;
+    *launches = (int)P.used[id];
+    return ok();
 }
 
 }  // extern "C"

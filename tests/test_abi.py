@@ -1,0 +1,111 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function the
+header declares, and rejects bad arguments before any device work."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from mlx_vit_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kda_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kda_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = _declared_functions()
+    for n in ("kda_fwd", "kda_bwd", "kda_workspace_size", "kda_last_error", "kda_solve_unit_triangular"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} declared in kda_hip.h but not exported"
+    assert set(_declared_functions()) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_abi_version():
+    assert _lib.load().kda_abi_version() == 1
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    fwd = lib.kda_workspace_size(0, 8, 1568, 12, 64, 64, 1)
+    bwd = lib.kda_workspace_size(1, 8, 1568, 12, 64, 64, 1)
+    N = 8 * 12 * 25
+    # forward: W, U, Qp, KbT (C*D) + Aqk (C*C) + eG (D), fp32
+    assert fwd == 4 * (4 * N * 64 * 64 + N * 64 * 64 + N * 64)
+    assert bwd > fwd
+    assert lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) == 0 or lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) >= 0
+
+
+def test_workspace_offsets_disjoint():
+    lib = _lib.load()
+    for pass_ in (0, 1):
+        arr = (ctypes.c_int64 * 16)()
+        assert lib.kda_workspace_offsets(pass_, 2, 300, 3, 64, 64, 1, arr) == 0
+        offs = sorted(o for o in arr if o >= 0)
+        assert offs[0] == 0 and all(b - a >= 256 and b % 256 == 0 for a, b in zip(offs, offs[1:]))
+        total = lib.kda_workspace_size(pass_, 2, 300, 3, 64, 64, 1)
+        assert offs[-1] < total
+
+
+@pytest.mark.parametrize("B,T,H,D,chunk,dtype,gdt,code", [
+    (1, 64, 1, 64, 32, 1, 1, _lib.KDA_E_UNSUPPORTED),    # chunk
+    (1, 64, 1, 48, 64, 1, 1, _lib.KDA_E_UNSUPPORTED),    # head dim
+    (1, 64, 1, 64, 64, 2, 1, _lib.KDA_E_UNSUPPORTED),    # dtype
+    (1, 64, 1, 64, 64, 1, 5, _lib.KDA_E_UNSUPPORTED),    # g dtype
+    (-1, 64, 1, 64, 64, 1, 1, _lib.KDA_E_INVALID),       # negative size
+])
+def test_fwd_argument_errors(B, T, H, D, chunk, dtype, gdt, code):
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    rc = lib.kda_fwd(fake, fake, fake, fake, fake, None, fake, None, B, T, H, D, chunk, dtype, gdt,
+                     fake, 1 << 40, None)
+    assert rc == code
+    assert _lib.last_error()
+
+
+def test_null_and_workspace_errors():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    rc = lib.kda_fwd(None, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 64, 64, 1, 1, fake, 1 << 40, None)
+    assert rc == _lib.KDA_E_INVALID and "q" in _lib.last_error()
+    rc = lib.kda_fwd(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 64, 64, 1, 1, fake, 16, None)
+    assert rc == _lib.KDA_E_WORKSPACE
+    misaligned = ctypes.c_void_p((1 << 20) + 4)
+    rc = lib.kda_fwd(misaligned, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 64, 64, 1, 1, fake,
+                     1 << 40, None)
+    assert rc == _lib.KDA_E_INVALID
+    # the backward supports D in {32, 64}
+    rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 128, 64, 1, 1, fake, 1 << 40, None)
+    assert rc == _lib.KDA_E_UNSUPPORTED and "backward" in _lib.last_error()
+
+
+def test_solve_argument_errors():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    assert lib.kda_solve_unit_triangular(fake, fake, fake, 1, 65, 4, 0, None) == _lib.KDA_E_UNSUPPORTED
+    assert lib.kda_solve_unit_triangular(None, fake, fake, 1, 8, 4, 0, None) == _lib.KDA_E_INVALID
+
+
+def test_error_mapping():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.KDA_E_UNSUPPORTED, "x")
+    with pytest.raises(_lib.KDAError):
+        _lib.check(_lib.KDA_E_HIP, "x")
+    _lib.check(_lib.KDA_OK, "x")
+
+
+def test_profile_names():
+    lib = _lib.load()
+    names = [lib.kda_profile_name(i).decode() for i in range(_lib.PROF_NKERNELS)]
+    assert all(names) and len(set(names)) == len(names)
+    assert lib.kda_profile_name(99).decode() == ""
