@@ -7,7 +7,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/kda_hip.h"
+#include "kda_hip.h"
 #include "kda_internal.h"
 
 namespace {
@@ -54,11 +54,14 @@ int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, b
     return KDA_OK;
 }
 
-void make_layout(int pass, int B, int T, int H, int D, Layout& L) {
+// Region sizes in bytes.  Operand slabs use the input dtype's element size;
+// eG, Akk and Tii are fp32.
+void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
     const size_t nc = (size_t)(T + kda::C - 1) / kda::C;
     const size_t N = (size_t)B * H * nc;
-    const size_t CD = N * kda::C * D, CC = N * kda::C * kda::C, DD = N * (size_t)D * D;
-    const size_t TI = N * kda::NB * kda::BS * kda::BS, EG = N * D;
+    const size_t es = (dtype == KDA_DTYPE_BF16) ? 2 : 4;
+    const size_t CD = N * kda::C * D * es, CC = N * kda::C * kda::C * es, DD = N * (size_t)D * D * es;
+    const size_t TI = N * kda::NB * kda::BS * kda::BS * 4, EG = N * D * 4;
     size_t sz[KDA_WS_NREGIONS] = {0};
     sz[KDA_WS_W] = CD;
     sz[KDA_WS_U] = CD;
@@ -72,7 +75,7 @@ void make_layout(int pass, int B, int T, int H, int D, Layout& L) {
         sz[KDA_WS_QPT] = CD;
         sz[KDA_WS_KB] = CD;
         sz[KDA_WS_AQKT] = CC;
-        sz[KDA_WS_AKK] = CC;
+        sz[KDA_WS_AKK] = N * kda::C * kda::C * 4;
         sz[KDA_WS_TII] = TI;
         sz[KDA_WS_H] = DD;
         sz[KDA_WS_DH] = DD;
@@ -86,19 +89,19 @@ void make_layout(int pass, int B, int T, int H, int D, Layout& L) {
             continue;
         }
         L.off[r] = (int64_t)cur;
-        cur += (sz[r] * sizeof(float) + 255) & ~(size_t)255;
+        cur += (sz[r] + 255) & ~(size_t)255;
     }
     L.total = cur;
 }
 
-float* region(void* ws, const Layout& L, int r) {
-    return L.off[r] < 0 ? nullptr : reinterpret_cast<float*>(static_cast<char*>(ws) + L.off[r]);
+void* region(void* ws, const Layout& L, int r) {
+    return L.off[r] < 0 ? nullptr : static_cast<void*>(static_cast<char*>(ws) + L.off[r]);
 }
+float* fregion(void* ws, const Layout& L, int r) { return static_cast<float*>(region(ws, L, r)); }
 
-int check_io(const void* p, const char* name, int dtype, bool nullable) {
+int check_io(const void* p, const char* name, int /*dtype*/, bool nullable) {
     if (!p) return nullable ? KDA_OK : fail(KDA_E_INVALID, "%s is NULL", name);
-    const size_t al = (dtype == KDA_DTYPE_F32) ? 16 : 8;
-    if (!aligned(p, al)) return fail(KDA_E_INVALID, "%s is not %zu-byte aligned", name, al);
+    if (!aligned(p, 16)) return fail(KDA_E_INVALID, "%s is not 16-byte aligned", name);
     return KDA_OK;
 }
 
@@ -242,7 +245,7 @@ size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int d
     }
     if (check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass == KDA_PASS_BWD) != KDA_OK) return 0;
     Layout L;
-    make_layout(pass, B, T, H, D, L);
+    make_layout(pass, B, T, H, D, dtype, L);
     ok();
     return L.total;
 }
@@ -253,7 +256,7 @@ int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int d
     const int rc = check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass == KDA_PASS_BWD);
     if (rc) return rc;
     Layout L;
-    make_layout(pass, B, T, H, D, L);
+    make_layout(pass, B, T, H, D, dtype, L);
     for (int r = 0; r < KDA_WS_NREGIONS; ++r) offsets[r] = L.off[r];
     return ok();
 }
@@ -276,7 +279,7 @@ int kda_fwd(const void* q, const void* k, const void* v, const void* g, const vo
         (rc = check_io(o, "o", dtype, false)) || (rc = check_scalar(beta, "beta", dtype)))
         return rc;
     Layout L;
-    make_layout(KDA_PASS_FWD, B, T, H, D, L);
+    make_layout(KDA_PASS_FWD, B, T, H, D, dtype, L);
     if (!workspace || ws_bytes < L.total)
         return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
     if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
@@ -289,7 +292,7 @@ int kda_fwd(const void* q, const void* k, const void* v, const void* g, const vo
     pa.Qp = region(workspace, L, KDA_WS_QP);
     pa.KbT = region(workspace, L, KDA_WS_KBT);
     pa.Aqk = region(workspace, L, KDA_WS_AQK);
-    pa.eG = region(workspace, L, KDA_WS_EG);
+    pa.eG = fregion(workspace, L, KDA_WS_EG);
     pa.T = T; pa.H = H; pa.nc = nc;
     hipError_t e = timed(PROF_PREP_FWD, st, [&] {
         return kda::launch_prep(pa, D, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16, BH * nc, st);
@@ -328,27 +331,27 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
         (rc = check_scalar(dbeta, "dbeta", dtype)))
         return rc;
     Layout L;
-    make_layout(KDA_PASS_BWD, B, T, H, D, L);
+    make_layout(KDA_PASS_BWD, B, T, H, D, dtype, L);
     if (!workspace || ws_bytes < L.total)
         return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
     if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
 
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
-    float* W = region(workspace, L, KDA_WS_W);
-    float* U = region(workspace, L, KDA_WS_U);
-    float* KbT = region(workspace, L, KDA_WS_KBT);
-    float* eG = region(workspace, L, KDA_WS_EG);
-    float* WT = region(workspace, L, KDA_WS_WT);
-    float* QpT = region(workspace, L, KDA_WS_QPT);
-    float* Kb = region(workspace, L, KDA_WS_KB);
-    float* AqkT = region(workspace, L, KDA_WS_AQKT);
-    float* Akk = region(workspace, L, KDA_WS_AKK);
-    float* Tii = region(workspace, L, KDA_WS_TII);
-    float* hS = region(workspace, L, KDA_WS_H);
-    float* dhS = region(workspace, L, KDA_WS_DH);
-    float* Vp = region(workspace, L, KDA_WS_VP);
-    float* dVp = region(workspace, L, KDA_WS_DVP);
+    void* W = region(workspace, L, KDA_WS_W);
+    void* U = region(workspace, L, KDA_WS_U);
+    void* KbT = region(workspace, L, KDA_WS_KBT);
+    float* eG = fregion(workspace, L, KDA_WS_EG);
+    void* WT = region(workspace, L, KDA_WS_WT);
+    void* QpT = region(workspace, L, KDA_WS_QPT);
+    void* Kb = region(workspace, L, KDA_WS_KB);
+    void* AqkT = region(workspace, L, KDA_WS_AQKT);
+    float* Akk = fregion(workspace, L, KDA_WS_AKK);
+    float* Tii = fregion(workspace, L, KDA_WS_TII);
+    void* hS = region(workspace, L, KDA_WS_H);
+    void* dhS = region(workspace, L, KDA_WS_DH);
+    void* Vp = region(workspace, L, KDA_WS_VP);
+    void* dVp = region(workspace, L, KDA_WS_DVP);
 
     kda::PrepArgs pa = {};
     pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;

@@ -22,94 +22,6 @@
 namespace kda {
 
 // ----------------------------------------------------------------------------
-// reverse state recurrence
-// ----------------------------------------------------------------------------
-template <int D, typename TI, int PREC>
-__global__ __launch_bounds__(64) void kda_dh_kernel(const DhArgs a) {
-    constexpr int NT = D / BS;
-    const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = bid / NT, ct = bid - bh * NT;
-    const int l = threadIdx.x, r16 = l & 15, g4 = l >> 4;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int col = ct * BS + r16;
-    const TI* dout = static_cast<const TI*>(a.dout);
-
-    f32x4 dS[NT];
-#pragma unroll
-    for (int mt = 0; mt < NT; ++mt) {
-        if (a.dsf) {
-            const float4 x = *reinterpret_cast<const float4*>(a.dsf + ((size_t)bh * D + col) * D + BS * mt + 4 * g4);
-            dS[mt] = f32x4{x.x, x.y, x.z, x.w};
-        } else {
-            dS[mt] = zero4();
-        }
-    }
-
-    for (int n = a.nc - 1; n >= 0; --n) {
-        const size_t ch = (size_t)bh * a.nc + n;
-        const int t0 = n * C, valid = min(C, a.T - t0);
-        const float* AqkT = a.AqkT + ch * C * C;
-        const float* Kb = a.Kb + ch * C * D;
-        const float* QpT = a.QpT + ch * C * D;
-        const float* WT = a.WT + ch * C * D;
-        const float* eG = a.eG + ch * D;
-
-        float* dh = a.dh + ch * D * D;
-#pragma unroll
-        for (int mt = 0; mt < NT; ++mt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dh[(size_t)(BS * mt + 4 * g4 + e) * D + col] = dS[mt][e];
-
-        f32x4 dO[NB];
-#pragma unroll
-        for (int m = 0; m < NB; ++m)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * m + 4 * g4 + e;
-                dO[m][e] = (t < valid) ? ld1<TI>(dout + (((size_t)b * a.T + t0 + t) * a.H + h) * D + col) : 0.f;
-            }
-
-        f32x4 dV[NB];
-#pragma unroll
-        for (int m = 0; m < NB; ++m) {
-            f32x4 acc = zero4();
-#pragma unroll
-            for (int ks = m / 2; ks < C / 32; ++ks)
-                acc = mma8<PREC>(frag8(AqkT, C, BS * m, 32 * ks), acc2frag(dO[2 * ks], dO[2 * ks + 1]), acc);
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks)
-                acc = mma8<PREC>(frag8(Kb, D, BS * m, 32 * ks), acc2frag(dS[2 * ks], dS[2 * ks + 1]), acc);
-            dV[m] = acc;
-        }
-        float* dvp = a.dVp + ch * C * D;
-#pragma unroll
-        for (int m = 0; m < NB; ++m)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dvp[(size_t)(BS * m + 4 * g4 + e) * D + col] = dV[m][e];
-
-#pragma unroll
-        for (int mt = 0; mt < NT; ++mt) {
-            const float4 eg = *reinterpret_cast<const float4*>(eG + BS * mt + 4 * g4);
-            f32x4 acc = dS[mt];
-            acc[0] *= eg.x; acc[1] *= eg.y; acc[2] *= eg.z; acc[3] *= eg.w;
-#pragma unroll
-            for (int ks = 0; ks < C / 32; ++ks) {
-                acc = mma8<PREC>(frag8(QpT, C, BS * mt, 32 * ks), acc2frag(dO[2 * ks], dO[2 * ks + 1]), acc);
-                acc = mma8<PREC>(neg(frag8(WT, C, BS * mt, 32 * ks)), acc2frag(dV[2 * ks], dV[2 * ks + 1]), acc);
-            }
-            dS[mt] = acc;
-        }
-    }
-
-    if (a.ds0) {
-#pragma unroll
-        for (int mt = 0; mt < NT; ++mt)
-            *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + col) * D + BS * mt + 4 * g4) =
-                make_float4(dS[mt][0], dS[mt][1], dS[mt][2], dS[mt][3]);
-    }
-}
-
-// ----------------------------------------------------------------------------
 // local adjoints
 // ----------------------------------------------------------------------------
 
@@ -169,12 +81,12 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     const TI* beta = static_cast<const TI*>(a.beta);
     const TI* dout = static_cast<const TI*>(a.dout);
     const size_t cCD = (size_t)ch * C * D, cCC = (size_t)ch * C * C;
-    const float* hS = a.h + (size_t)ch * D * D;
-    const float* dhS = a.dh + (size_t)ch * D * D;
-    const float* Vp = a.Vp + cCD;
-    const float* dVp = a.dVp + cCD;
-    const float* Wc = a.W + cCD;
-    const float* Uc = a.U + cCD;
+    const TI* hS = static_cast<const TI*>(a.h) + (size_t)ch * D * D;
+    const TI* dhS = static_cast<const TI*>(a.dh) + (size_t)ch * D * D;
+    const TI* Vp = static_cast<const TI*>(a.Vp) + cCD;
+    const TI* dVp = static_cast<const TI*>(a.dVp) + cCD;
+    const TI* Wc = static_cast<const TI*>(a.W) + cCD;
+    const TI* Uc = static_cast<const TI*>(a.U) + cCD;
 
     // ---------------- phase 0: chunk factors, raw per-lane values ----------------
     for (int idx = tid; idx < C * C; idx += 256) sp[idx / C][idx % C] = a.Akk[cCC + idx];
@@ -213,6 +125,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     __syncthreads();
     if (!unsafe) chunk_transform<D, PREC>(s, true);
     __syncthreads();
+    // PHASE 1
 
     f32x4 dqa[NB], dka[NB], dga[NB], dWt[NB];
 #pragma unroll
@@ -246,7 +159,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
         // state-decay term of dG: e^G sum_col dh[d][col] h[d][col]
         float part = 0.f;
         for (int c = g4 * (D / 4); c < (g4 + 1) * (D / 4); ++c)
-            part += dhS[(size_t)d * D + c] * hS[(size_t)d * D + c];
+            part += ld1<TI>(dhS + (size_t)d * D + c) * ld1<TI>(hS + (size_t)d * D + c);
         dgcol = sum4g(dgcol) + kexp<PREC>(s.g[C - 1][d]) * sum4g(part);
     }
     // dAqk = tril(dO V'^T), 10 lower tiles over the 4 waves
@@ -265,6 +178,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     }
     __syncthreads();
 
+    // PHASE 2
     // ---------------- phase 2: transposed WY solve ----------------
     if (own) {
         f32x4 dRk[NB], dRv[NB];
@@ -272,7 +186,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
         for (int i = NB - 1; i >= 0; --i) {
             f32x4 Yk = dWt[i], Yv;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) Yv[e] = dVp[(size_t)(BS * i + 4 * g4 + e) * D + d];
+            for (int e = 0; e < 4; ++e) Yv[e] = ld1<TI>(dVp + (size_t)(BS * i + 4 * g4 + e) * D + d);
 #pragma unroll
             for (int j = i + 1; j < NB; ++j) {
                 // A[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a]
@@ -310,6 +224,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     }
     __syncthreads();
 
+    // PHASE 3
     // ---------------- phase 3: dL = -tril(dR X^T, -1); dbeta; dP ----------------
     for (int tix = w; tix < 10; tix += 4) {
         int i, j;
@@ -332,6 +247,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     }
     __syncthreads();
 
+    // PHASE 4
     // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints ----------------
     if (own) {
         if (!unsafe) {
@@ -406,6 +322,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
             }
         }
 
+        // PHASE 5
         // ---------------- phase 5: dG, reverse cumsum, stores ----------------
         if (g4 == 3) dga[NB - 1][3] += dgcol;        // row C-1
         // suffix sums over rows t = 16 m + 4 g4 + e of this lane's channel
@@ -446,29 +363,17 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
             }
     }
     if (tid < valid) st1<TI>(static_cast<TI*>(a.dbeta) + bbase + (size_t)tid * a.H, sdb[tid]);
+    // PHASE 6
 }
 
 // ----------------------------------------------------------------------------
 // launchers
 // ----------------------------------------------------------------------------
-template <int D, typename TI>
-static hipError_t launch_dh_t(const DhArgs& a, hipStream_t st) {
-    constexpr int PREC = std::is_same<TI, float>::value ? 3 : 1;
-    hipLaunchKernelGGL((kda_dh_kernel<D, TI, PREC>), dim3(a.BH * (D / BS)), dim3(64), 0, st, a);
-    return hipGetLastError();
-}
-
 template <int D, typename TI, typename TG>
 static hipError_t launch_local_t(const LocalArgs& a, int nchunks, hipStream_t st) {
     constexpr int PREC = std::is_same<TI, float>::value ? 3 : 1;
     hipLaunchKernelGGL((kda_bwd_local_kernel<D, TI, TG, PREC>), dim3(nchunks), dim3(256), 0, st, a);
     return hipGetLastError();
-}
-
-hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st) {
-    if (D == 32) return in_bf16 ? launch_dh_t<32, uint16_t>(a, st) : launch_dh_t<32, float>(a, st);
-    if (D == 64) return in_bf16 ? launch_dh_t<64, uint16_t>(a, st) : launch_dh_t<64, float>(a, st);
-    return hipErrorInvalidValue;
 }
 
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st) {

@@ -166,3 +166,147 @@ __device__ void diag_inverse(const float* __restrict__ L, float (*tii)[BS][BS + 
 }
 
 }  // namespace kda
+
+// ============================================================================
+// Typed-storage chunk phases (ST = bf16 for bf16 inputs, fp32 otherwise).
+// q, k, v and the anchored operands are kept in ST; gamma and the small
+// factor tables in fp32.  Rows are padded by 16 bytes.
+// ============================================================================
+namespace kda {
+
+template <int D, typename ST>
+struct ChunkSmem {
+    // fp32 storage at D = 128 drops the row pad to fit in 160 KB
+    static constexpr bool TIGHT = sizeof(ST) == 4 && D >= 128;
+    static constexpr int PS = TIGHT ? 0 : 16 / (int)sizeof(ST);
+    static constexpr int LDK = D + PS;     // ST rows
+    static constexpr int LDG = D + (TIGHT ? 0 : 4);   // fp32 rows
+    ST kl[C][LDK];     // k e^{g_t - g_r}
+    ST ql[C][LDK];     // raw q, then q e^{g_t - g_r}
+    ST kr[C][LDK];     // raw k, then k e^{g_r - g_t} (anchored path)
+    float g[C][LDG];   // raw g, then gamma
+    union {
+        struct {
+            float er[NB][D];    // e^{gamma_16j}
+            float egr[NB][D];   // e^{G - gamma_16j}
+            float f[6][D];      // e^{gamma_16i - gamma_16j}, j < i
+        };
+        float tmp[256];
+    };
+    float beta[C];
+};
+
+// All 16-byte loads of one chunk of q, k, g (and optionally v) are issued
+// before anything is written to LDS.  Rows >= valid are zero.  Returns 1 if
+// this thread saw g > 0 or a NaN.
+template <int D, typename ST, typename TG, bool WITH_V>
+__device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, ST* sv, int ldv, const ST* __restrict__ q,
+                                           const ST* __restrict__ k, const ST* __restrict__ v,
+                                           const TG* __restrict__ g, const ST* __restrict__ beta, size_t base,
+                                           size_t rstride, size_t bbase, int H, int valid) {
+    Tile<ST, C, D> tq, tk, tv;
+    Tile<TG, C, D> tg;
+    tq.load(q + base, rstride, valid);
+    tk.load(k + base, rstride, valid);
+    tg.load(g + base, rstride, valid);
+    if constexpr (WITH_V) tv.load(v + base, rstride, valid);
+    const int tid = threadIdx.x;
+    const float bt = (tid < C && tid < valid) ? ld1<ST>(beta + bbase + (size_t)tid * H) : 0.f;
+    tq.store(&s.ql[0][0], ChunkSmem<D, ST>::LDK);
+    tk.store(&s.kr[0][0], ChunkSmem<D, ST>::LDK);
+    if constexpr (WITH_V) tv.store(sv, ldv);
+    int flag = 0;
+    constexpr int EPV = Tile<TG, C, D>::EPV, VPR = Tile<TG, C, D>::VPR;
+#pragma unroll
+    for (int i = 0; i < Tile<TG, C, D>::PER; ++i) {
+        const int vv = tid + 256 * i;
+        const int row = vv / VPR, c = (vv - row * VPR) * EPV;
+        const Vec16<TG> x{tg.get(i)};
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+            const float gv = x.get(e);
+            s.g[row][c + e] = gv;
+            if (!(gv <= 0.f)) flag = 1;
+        }
+    }
+    if (tid < C) s.beta[tid] = bt;
+    __syncthreads();
+    return flag;
+}
+
+template <int D, typename ST>
+__device__ __forceinline__ void chunk_cumsum2(ChunkSmem<D, ST>& s) {
+    constexpr int PARTS = 256 / D, RP = C / PARTS;
+    const int tid = threadIdx.x, d = tid % D, p = tid / D;
+    float run = 0.f;
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        run += s.g[p * RP + r][d];
+        s.g[p * RP + r][d] = run;
+    }
+    s.tmp[p * D + d] = run;
+    __syncthreads();
+    float off = 0.f;
+    for (int pp = 0; pp < p; ++pp) off += s.tmp[pp * D + d];
+    if (p > 0) {
+#pragma unroll
+        for (int r = 0; r < RP; ++r) s.g[p * RP + r][d] += off;
+    }
+    __syncthreads();
+}
+
+// factor tables + span guard; returns nonzero (uniform) for the pairwise path
+template <int D, typename ST, int PREC>
+__device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag) {
+    const int tid = threadIdx.x;
+    for (int idx = tid; idx < NB * D; idx += 256) {
+        const int j = idx / D, d = idx % D;
+        const float g0 = s.g[BS * j][d];
+        const float span = g0 - s.g[BS * j + BS - 1][d];
+        if (!(span <= SPAN_MAX)) flag = 1;
+        s.er[j][d] = kexp<PREC>(g0);
+        s.egr[j][d] = kexp<PREC>(s.g[C - 1][d] - g0);
+    }
+    for (int idx = tid; idx < 6 * D; idx += 256) {
+        const int p = idx / D, d = idx % D;
+        const int i = (p >= 3) ? 3 : (p >= 1) ? 2 : 1;
+        const int j = p - pair_idx(i, 0);
+        s.f[p][d] = kexp<PREC>(s.g[BS * i][d] - s.g[BS * j][d]);
+    }
+    return __syncthreads_or(flag);
+}
+
+// Register-resident inverses of the four 16x16 diagonal blocks of I + L,
+// L[t][s] = beta_t Akk[t][s]: wave w inverts block w, lane c (< 16) owns
+// column c.  The block's strict lower part is read into registers first.
+template <int LDA>
+__device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, const float* __restrict__ beta,
+                                                 float (*tii)[BS][BS + 4]) {
+    const int w = threadIdx.x >> 6, c = threadIdx.x & 63;
+    if (c < BS) {
+        const float* Ab = akk + (size_t)(BS * w) * LDA + BS * w;
+        float Lr[BS][BS];
+#pragma unroll
+        for (int t = 1; t < BS; ++t) {
+            const float bt = beta[BS * w + t];
+#pragma unroll
+            for (int j4 = 0; j4 < (t + 3) / 4; ++j4) {
+                const float4 x = *reinterpret_cast<const float4*>(Ab + t * LDA + 4 * j4);
+                Lr[t][4 * j4] = bt * x.x; Lr[t][4 * j4 + 1] = bt * x.y;
+                Lr[t][4 * j4 + 2] = bt * x.z; Lr[t][4 * j4 + 3] = bt * x.w;
+            }
+        }
+        float x[BS];
+#pragma unroll
+        for (int t = 0; t < BS; ++t) {
+            float acc = (t == c) ? 1.f : 0.f;
+#pragma unroll
+            for (int j = 0; j < t; ++j) acc -= Lr[t][j] * x[j];
+            x[t] = acc;
+        }
+#pragma unroll
+        for (int t = 0; t < BS; ++t) tii[w][t][c] = x[t];
+    }
+}
+
+}  // namespace kda

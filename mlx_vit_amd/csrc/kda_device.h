@@ -21,6 +21,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 namespace kda {
 
@@ -39,12 +40,8 @@ constexpr float SPAN_MAX = 60.0f;  // largest in-block decay span the anchored M
 // ----------------------------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-__device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-    u += 0x7fffu + ((u >> 16) & 1u);                                           // round to nearest even
-    return (uint16_t)(u >> 16);
-}
+// round to nearest even (v_cvt_pk_bf16_f32; NaN stays NaN)
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 template <typename T> __device__ __forceinline__ float ld1(const T* p);
 template <> __device__ __forceinline__ float ld1<float>(const float* p) { return *p; }
@@ -184,6 +181,225 @@ __device__ __forceinline__ Fr4 neg(Fr4 f) {
 }
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// ----------------------------------------------------------------------------
+// bf16-native operands: raw bf16 bits in memory go straight into the MFMA
+// (no fp32 round trip).  Frag8 carries a hi part and, for PREC == 3, a lo part.
+// ----------------------------------------------------------------------------
+struct Frag8 { bf16x8 h, l; };
+struct Frag4 { short4v h, l; };
+
+template <int PREC>
+__device__ __forceinline__ Frag8 frag_from_f32(const float* v) {
+    Frag8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const __bf16 hi = (__bf16)v[e];
+        f.h[e] = hi;
+        if constexpr (PREC == 3) f.l[e] = (__bf16)(v[e] - (float)hi);
+    }
+    return f;
+}
+
+template <int PREC>
+__device__ __forceinline__ Frag4 frag4_from_f32(const float* v) {
+    Frag4 f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint16_t hi = f2bf(v[e]);
+        f.h[e] = (short)hi;
+        if constexpr (PREC == 3) f.l[e] = (short)f2bf(v[e] - bf2f(hi));
+    }
+    return f;
+}
+
+// A operand (row-major, k contiguous) or B operand stored n-major, k contiguous.
+template <int PREC, typename ST>
+__device__ __forceinline__ Frag8 ldfrag(const ST* M, int ld, int row0, int k0) {
+    const int l = lane_id(), r = l & 15, g = l >> 4;
+    const ST* p = M + (size_t)(row0 + r) * ld + k0 + 4 * g;
+    if constexpr (std::is_same<ST, uint16_t>::value) {
+        const uint2 x = *reinterpret_cast<const uint2*>(p);
+        const uint2 y = *reinterpret_cast<const uint2*>(p + 16);
+        Frag8 f;
+        f.h = __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
+        if constexpr (PREC == 3) f.l = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+        return f;
+    } else {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        const float4 y = *reinterpret_cast<const float4*>(p + 16);
+        const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+        return frag_from_f32<PREC>(v);
+    }
+}
+
+// 16-wide k-step, row-major k contiguous
+template <int PREC, typename ST>
+__device__ __forceinline__ Frag4 ldfrag4(const ST* M, int ld, int row0, int k0) {
+    const int l = lane_id(), r = l & 15, g = l >> 4;
+    const ST* p = M + (size_t)(row0 + r) * ld + k0 + 4 * g;
+    if constexpr (std::is_same<ST, uint16_t>::value) {
+        const uint2 x = *reinterpret_cast<const uint2*>(p);
+        Frag4 f;
+        f.h = __builtin_bit_cast(short4v, x);
+        if constexpr (PREC == 3) f.l = short4v{0, 0, 0, 0};
+        return f;
+    } else {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        const float v[4] = {x.x, x.y, x.z, x.w};
+        return frag4_from_f32<PREC>(v);
+    }
+}
+
+// 16-wide k-step of the transpose: A[row][k] = M[k][row]
+template <int PREC, typename ST>
+__device__ __forceinline__ Frag4 ldfrag4T(const ST* M, int ld, int row0, int k0) {
+    const int l = lane_id(), r = l & 15, g = l >> 4;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = ld1<ST>(M + (size_t)(k0 + 4 * g + e) * ld + row0 + r);
+    return frag4_from_f32<PREC>(v);
+}
+
+// ldfrag with every k-slot multiplied by scale[k - k0]
+template <int PREC, typename ST>
+__device__ __forceinline__ Frag8 ldfrag_scaled(const ST* M, int ld, int row0, int k0, const float* scale) {
+    const int l = lane_id(), r = l & 15, g = l >> 4;
+    const ST* p = M + (size_t)(row0 + r) * ld + k0 + 4 * g;
+    const float4 x = ld4<ST>(p), y = ld4<ST>(p + 16);
+    const float4 sx = *reinterpret_cast<const float4*>(scale + 4 * g);
+    const float4 sy = *reinterpret_cast<const float4*>(scale + 16 + 4 * g);
+    const float v[8] = {x.x * sx.x, x.y * sx.y, x.z * sx.z, x.w * sx.w, y.x * sy.x, y.y * sy.y, y.z * sy.z, y.w * sy.w};
+    return frag_from_f32<PREC>(v);
+}
+
+template <int PREC>
+__device__ __forceinline__ Frag8 accfrag(const f32x4& lo, const f32x4& hi) {
+    const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return frag_from_f32<PREC>(v);
+}
+template <int PREC>
+__device__ __forceinline__ Frag4 accfrag4(const f32x4& a) {
+    const float v[4] = {a[0], a[1], a[2], a[3]};
+    return frag4_from_f32<PREC>(v);
+}
+
+template <int PREC>
+__device__ __forceinline__ f32x4 mma(const Frag8& a, const Frag8& b, f32x4 c) {
+    if constexpr (PREC == 3) {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, c, 0, 0, 0);
+    }
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, c, 0, 0, 0);
+}
+template <int PREC>
+__device__ __forceinline__ f32x4 mma4f(const Frag4& a, const Frag4& b, f32x4 c) {
+    if constexpr (PREC == 3) {
+        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.l, b.h, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.l, c, 0, 0, 0);
+    }
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.h, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 negacc(f32x4 a) { return f32x4{-a[0], -a[1], -a[2], -a[3]}; }
+
+// 16-byte vector of storage elements <-> floats
+template <typename ST> struct Vec16;
+template <> struct Vec16<uint16_t> {
+    static constexpr int N = 8;
+    uint4 u;
+    __device__ __forceinline__ float get(int i) const {
+        const uint32_t w = (i < 2) ? u.x : (i < 4) ? u.y : (i < 6) ? u.z : u.w;
+        return (i & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+    }
+};
+template <> struct Vec16<float> {
+    static constexpr int N = 4;
+    uint4 u;
+    __device__ __forceinline__ float get(int i) const {
+        return __uint_as_float((i == 0) ? u.x : (i == 1) ? u.y : (i == 2) ? u.z : u.w);
+    }
+};
+
+__device__ __forceinline__ uint32_t pack2bf(float a, float b) {
+    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+// 16 bytes of storage elements from floats (8 bf16 or 4 fp32)
+template <typename ST> __device__ __forceinline__ void store_vec(ST* p, const float* v);
+template <> __device__ __forceinline__ void store_vec<uint16_t>(uint16_t* p, const float* v) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack2bf(v[0], v[1]), pack2bf(v[2], v[3]), pack2bf(v[4], v[5]),
+                                              pack2bf(v[6], v[7]));
+}
+template <> __device__ __forceinline__ void store_vec<float>(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// ----------------------------------------------------------------------------
+// cooperative 16-byte tile copies (256 threads)
+// ----------------------------------------------------------------------------
+// The prefetched vectors live in one SSA vector value, never in an array: an
+// array indexed inside a loop is an alloca that the backend would place in LDS
+// or scratch, which forces a wait on every load.
+template <typename ST, int ROWS, int COLS>
+struct Tile {
+    static constexpr int EPV = 16 / (int)sizeof(ST);
+    static constexpr int VPR = COLS / EPV;
+    static constexpr int NV = ROWS * VPR;
+    static constexpr int PER = (NV + 255) / 256;
+    typedef uint32_t vec_t __attribute__((ext_vector_type(4 * PER)));
+    vec_t r;
+
+    __device__ __forceinline__ void put(int i, uint4 x) {
+        r[4 * i] = x.x; r[4 * i + 1] = x.y; r[4 * i + 2] = x.z; r[4 * i + 3] = x.w;
+    }
+    __device__ __forceinline__ uint4 get(int i) const {
+        return make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+    }
+    // all ROWS rows are read
+    __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int v = threadIdx.x + 256 * i;
+            if (NV % 256 == 0 || v < NV) {
+                const int row = v / VPR, c = (v - row * VPR) * EPV;
+                put(i, *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c));
+            }
+        }
+    }
+    // rows at or past valid_rows read as zero
+    __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld, int valid_rows) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int v = threadIdx.x + 256 * i;
+            if (NV % 256 == 0 || v < NV) {
+                const int row = v / VPR, c = (v - row * VPR) * EPV;
+                put(i, (row < valid_rows) ? *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c)
+                                          : make_uint4(0u, 0u, 0u, 0u));
+            }
+        }
+    }
+    __device__ __forceinline__ void store(ST* lds, int lld) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int v = threadIdx.x + 256 * i;
+            if (NV % 256 == 0 || v < NV) {
+                const int row = v / VPR, c = (v - row * VPR) * EPV;
+                *reinterpret_cast<uint4*>(lds + row * lld + c) = get(i);
+            }
+        }
+    }
+};
+
+template <typename ST, int ROWS, int COLS>
+__device__ __forceinline__ void tile_out(const ST* lds, int lld, ST* __restrict__ g, size_t gld, int valid_rows) {
+    constexpr int EPV = 16 / (int)sizeof(ST), VPR = COLS / EPV, NV = ROWS * VPR;
+    for (int v = threadIdx.x; v < NV; v += 256) {
+        const int row = v / VPR, c = (v - row * VPR) * EPV;
+        if (row < valid_rows)
+            *reinterpret_cast<uint4*>(g + (size_t)row * gld + c) = *reinterpret_cast<const uint4*>(lds + row * lld + c);
+    }
+}
 
 // ----------------------------------------------------------------------------
 // XCD-aware block remap: blocks with equal blockIdx % 8 run on one XCD (one

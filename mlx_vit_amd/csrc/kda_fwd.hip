@@ -23,12 +23,38 @@ namespace kda {
 
 // ----------------------------------------------------------------------------
 // prep
+//
+// Phases (barriers between them):
+//   load      all 16-byte loads of q, k, g (and v) issued first, then LDS
+//   cumsum    gamma; factor tables; span guard (uniform anchored / pairwise)
+//   pass A    row-major threads (t, 8 channels): anchored operands kl, ql, kr
+//             in place; Qp (forward) / Kb (backward) as 16-byte stores
+//   pass B    column threads (d, 8 tokens): KbT, QpT as 16-byte stores
+//   products  Akk -> fp32 LDS, Aqk -> LDS staging -> coalesced stores
+//   inverse   diagonal 16x16 blocks of I + L in registers
+//   solve     block forward substitution, every tile of a wave interleaved;
+//             W, U (and WT) staged in LDS, stored coalesced
 // ----------------------------------------------------------------------------
-template <int D, typename TI, typename TG, int PREC>
+template <int D, typename ST>
+struct PrepGeom {
+    using CSm = ChunkSmem<D, ST>;
+    static constexpr int PS = CSm::PS, LDK = CSm::LDK, LDA = C + 4, LDT = C + PS;
+    static constexpr int BASE = (int)sizeof(CSm) + C * LDA * 4 + NB * BS * (BS + 4) * 4;
+    static constexpr bool STAGE_V = BASE + C * LDK * (int)sizeof(ST) <= 160 * 1024;
+    static constexpr bool STG_IN_G = (int)sizeof(float) * C * CSm::LDG >= C * LDT * (int)sizeof(ST);
+};
+
+template <int D, typename ST, typename TG, int PREC>
 __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
-    __shared__ ChunkLds<D> s;
-    __shared__ float sl[C][C + 4];            // L = diag(beta) Akk (strict lower)
-    __shared__ float tii[NB][BS][BS + 4];     // (I + L_ii)^-1
+    using G = PrepGeom<D, ST>;
+    constexpr int LDK = G::LDK, LDA = G::LDA, LDT = G::LDT, NT = D / BS, NCT = 2 * NT;
+    constexpr int TPW = (NCT + 3) / 4;
+    constexpr int EPV = 16 / (int)sizeof(ST);
+    __shared__ ChunkSmem<D, ST> s;
+    __shared__ __align__(16) float sa[C][LDA];            // Akk, fp32, strictly lower, unscaled
+    __shared__ __align__(16) float tii[NB][BS][BS + 4];   // (I + L_ii)^-1
+    __shared__ __align__(16) ST svbuf[G::STAGE_V ? C : 1][G::STAGE_V ? LDK : 8];
+    __shared__ __align__(16) ST stgbuf[G::STG_IN_G ? 1 : C][G::STG_IN_G ? 8 : LDT];
 
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
     const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
@@ -37,256 +63,238 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     const size_t rs = (size_t)a.H * D;
     const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
     const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
-    const TI* q = static_cast<const TI*>(a.q);
-    const TI* k = static_cast<const TI*>(a.k);
-    const TI* v = static_cast<const TI*>(a.v);
+    const ST* q = static_cast<const ST*>(a.q);
+    const ST* k = static_cast<const ST*>(a.k);
+    const ST* v = static_cast<const ST*>(a.v);
     const TG* g = static_cast<const TG*>(a.g);
-    const TI* beta = static_cast<const TI*>(a.beta);
+    const ST* beta = static_cast<const ST*>(a.beta);
     const size_t cCD = (size_t)ch * C * D, cCC = (size_t)ch * C * C;
+    ST* oW = static_cast<ST*>(a.W);
+    ST* oU = static_cast<ST*>(a.U);
+    ST* oQp = static_cast<ST*>(a.Qp);
+    ST* oQpT = static_cast<ST*>(a.QpT);
+    ST* oKb = static_cast<ST*>(a.Kb);
+    ST* oKbT = static_cast<ST*>(a.KbT);
+    ST* oWT = static_cast<ST*>(a.WT);
+    ST* oAqk = static_cast<ST*>(a.Aqk);
+    ST* oAqkT = static_cast<ST*>(a.AqkT);
+    const bool bwd = oAqkT != nullptr;
 
-    int flag = chunk_load<D, TI, TG>(s, q, k, g, beta, base, rs, bbase, a.H, valid);
-    chunk_cumsum<D>(s);
-    const int unsafe = chunk_factors<D, PREC>(s, flag);
+    // PHASE 0 (load)
+    const int flag = chunk_load2<D, ST, TG, G::STAGE_V>(s, &svbuf[0][0], LDK, q, k, v, g, beta, base, rs, bbase,
+                                                        a.H, valid);
+    // PHASE 1
+    chunk_cumsum2<D, ST>(s);
+    const int unsafe = chunk_factors2<D, ST, PREC>(s, flag);
+    if (a.eG && tid < D) a.eG[(size_t)ch * D + tid] = kexp<PREC>(s.g[C - 1][tid]);
+    // PHASE 2
 
     if (unsafe) {
-        // pairwise path (reference M kernel order of operations, any decay)
+        // pairwise path: raw q in ql, raw k in kr, exact exp(gamma_t - gamma_s)
         for (int p = tid; p < C * C; p += 256) {
             const int t = p / C, sx = p - t * C;
             float ak = 0.f, aq = 0.f;
             if (sx <= t) {
                 for (int d = 0; d < D; ++d) {
-                    const float e = kexp<PREC>(s.g[t][d] - s.g[sx][d]);
-                    const float ks = s.kr[sx][d] * e;
-                    ak += s.kr[t][d] * ks;
-                    aq += s.ql[t][d] * ks;
+                    const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(s.g[t][d] - s.g[sx][d]);
+                    ak += ld1<ST>(&s.kr[t][d]) * ks;
+                    aq += ld1<ST>(&s.ql[t][d]) * ks;
                 }
             }
             const float akk = (sx < t) ? ak : 0.f;
-            sl[t][sx] = s.beta[t] * akk;
+            sa[t][sx] = akk;
             if (a.Akk) a.Akk[cCC + (size_t)t * C + sx] = akk;
-            if (a.Aqk) a.Aqk[cCC + (size_t)t * C + sx] = aq;
-            if (a.AqkT) a.AqkT[cCC + (size_t)sx * C + t] = aq;
+            if (oAqk) st1<ST>(oAqk + cCC + (size_t)t * C + sx, aq);
+            if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, aq);
         }
         __syncthreads();
     }
 
-    // elementwise: Qp, Kb, e^G to the workspace; anchored operands in LDS
-    for (int idx = tid; idx < C * D; idx += 256) {
-        const int t = idx / D, d = idx - t * D;
-        const float gt = s.g[t][d], G = s.g[C - 1][d];
-        const float qv = s.ql[t][d], kv = s.kr[t][d];
-        const float qp = qv * kexp<PREC>(gt);
-        const float kb = kv * kexp<PREC>(G - gt);
-        if (a.Qp) a.Qp[cCD + (size_t)t * D + d] = qp;
-        if (a.QpT) a.QpT[cCD + (size_t)d * C + t] = qp;
-        if (a.Kb) a.Kb[cCD + (size_t)t * D + d] = kb;
-        if (a.KbT) a.KbT[cCD + (size_t)d * C + t] = kb;
-        if (t == 0 && a.eG) a.eG[(size_t)ch * D + d] = kexp<PREC>(G);
+    // pass A: row threads (t, EPV channels)
+    {
+        constexpr int VPR = D / EPV, NV = C * VPR;
+        for (int vv = tid; vv < NV; vv += 256) {
+            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, r = t & ~(BS - 1), blk = t / BS;
+            const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
+            const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
+            float okl[EPV], oql[EPV], okr[EPV], oqp[EPV], okb[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const int d = c0 + e;
+                const float gt = s.g[t][d], x = gt - s.g[r][d];
+                const float el = kexp<PREC>(x);
+                const float qf = qv.get(e), kf = kv.get(e);
+                okl[e] = kf * el;
+                oql[e] = qf * el;
+                okr[e] = unsafe ? kf : kf * kexp<PREC>(-x);
+                oqp[e] = oql[e] * s.er[blk][d];
+                okb[e] = bwd ? kf * kexp<PREC>(s.g[C - 1][d] - gt) : 0.f;
+            }
+            store_vec<ST>(&s.kl[t][c0], okl);
+            store_vec<ST>(&s.ql[t][c0], oql);
+            store_vec<ST>(&s.kr[t][c0], okr);
+            if (oQp) store_vec<ST>(oQp + cCD + (size_t)t * D + c0, oqp);
+            if (oKb) store_vec<ST>(oKb + cCD + (size_t)t * D + c0, okb);
+        }
     }
     __syncthreads();
-    chunk_transform<D, PREC>(s, !unsafe);
-    __syncthreads();
+    // PHASE 3
 
+    // pass B: column threads (d, EPV tokens)
+    {
+        constexpr int GPC = C / EPV, NV = D * GPC;
+        for (int vv = tid; vv < NV; vv += 256) {
+            const int d = vv / GPC, tb = (vv - d * GPC) * EPV;
+            float okb[EPV], oqp[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const int t = tb + e, blk = t / BS;
+                const float kr = ld1<ST>(&s.kr[t][d]);
+                okb[e] = unsafe ? kr * kexp<PREC>(s.g[C - 1][d] - s.g[t][d]) : kr * s.egr[blk][d];
+                oqp[e] = ld1<ST>(&s.ql[t][d]) * s.er[blk][d];
+            }
+            if (oKbT) store_vec<ST>(oKbT + cCD + (size_t)d * C + tb, okb);
+            if (oQpT) store_vec<ST>(oQpT + cCD + (size_t)d * C + tb, oqp);
+        }
+    }
+    __syncthreads();
+    // PHASE 4
+
+    ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];   // Aqk / AqkT staging
     if (!unsafe) {
-        // 10 lower sub-block tiles of Akk and Aqk; B operand shared by both
+        // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared
         for (int tix = w; tix < 10; tix += 4) {
             int i, j;
             tile_ij(tix, i, j);
             f32x4 P = zero4(), Q = zero4();
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                Fr8 Ak = frag8(&s.kl[0][0], D + 4, BS * i, 32 * ks);
-                Fr8 Aq = frag8(&s.ql[0][0], D + 4, BS * i, 32 * ks);
-                Fr8 Bk = frag8(&s.kr[0][0], D + 4, BS * j, 32 * ks);
-                if (j < i) {
-                    const float* f = &s.f[pair_idx(i, j)][32 * ks];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) Bk.v[e] *= f[kslot(g4, e)];
-                }
-                P = mma8<PREC>(Ak, Bk, P);
-                Q = mma8<PREC>(Aq, Bk, Q);
+                const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
+                const Frag8 Aq = ldfrag<PREC, ST>(&s.ql[0][0], LDK, BS * i, 32 * ks);
+                const Frag8 Bk = (j < i) ? ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
+                                                                  &s.f[pair_idx(i, j)][32 * ks])
+                                         : ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks);
+                P = mma<PREC>(Ak, Bk, P);
+                Q = mma<PREC>(Aq, Bk, Q);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
-                const float akk = (sx < t) ? P[e] : 0.f;
+                sa[t][sx] = (sx < t) ? P[e] : 0.f;
                 const float aq = (sx <= t) ? Q[e] : 0.f;
-                sl[t][sx] = s.beta[t] * akk;
-                if (a.Akk) a.Akk[cCC + (size_t)t * C + sx] = akk;
-                if (a.Aqk) a.Aqk[cCC + (size_t)t * C + sx] = aq;
-                if (a.AqkT) a.AqkT[cCC + (size_t)sx * C + t] = aq;
+                if (bwd) st1<ST>(stA + sx * LDT + t, aq);
+                else st1<ST>(stA + t * LDT + sx, aq);
             }
         }
-        // strictly upper sub-block tiles are zero in the workspace copies
+        // strictly upper sub-block tiles are zero
         for (int idx = tid; idx < 6 * BS * BS; idx += 256) {
             const int tile = idx / (BS * BS), e = idx - tile * BS * BS;
             const int i = (tile < 3) ? 0 : (tile < 5) ? 1 : 2;
             const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
             const int t = BS * i + e / BS, sx = BS * j + (e % BS);
-            if (a.Akk) a.Akk[cCC + (size_t)t * C + sx] = 0.f;
-            if (a.Aqk) a.Aqk[cCC + (size_t)t * C + sx] = 0.f;
-            if (a.AqkT) a.AqkT[cCC + (size_t)sx * C + t] = 0.f;
+            sa[t][sx] = 0.f;
+            if (bwd) st1<ST>(stA + sx * LDT + t, 0.f);
+            else st1<ST>(stA + t * LDT + sx, 0.f);
         }
     }
     __syncthreads();
-
-    diag_inverse<C + 4>(&sl[0][0], tii, NB);
+    // PHASE 5
+    if (!unsafe) {
+        if (oAqk) tile_out<ST, C, C>(stA, LDT, oAqk + cCC, C, C);
+        if (oAqkT) tile_out<ST, C, C>(stA, LDT, oAqkT + cCC, C, C);
+        if (a.Akk) tile_out<float, C, C>(&sa[0][0], LDA, a.Akk + cCC, C, C);
+    }
+    diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
     __syncthreads();
-    if (a.Tii) {
-        for (int idx = tid; idx < NB * BS * BS; idx += 256) {
-            const int i = idx / (BS * BS), e = idx - i * BS * BS;
-            a.Tii[(size_t)ch * NB * BS * BS + idx] = tii[i][e / BS][e % BS];
-        }
+    // PHASE 6
+    if (a.Tii && tid < NB * BS * BS / 4) {
+        const int i = tid / (BS * BS / 4), e4 = (tid - i * (BS * BS / 4)) * 4;
+        *reinterpret_cast<float4*>(a.Tii + (size_t)ch * NB * BS * BS + i * BS * BS + e4) =
+            *reinterpret_cast<const float4*>(&tii[i][e4 / BS][e4 % BS]);
     }
 
-    // block forward substitution, one 16-column tile of [Kt | beta V] at a time
-    constexpr int NCT = 2 * D / BS;
-    for (int ct = w; ct < NCT; ct += 4) {
-        const bool isK = ct < D / BS;
-        const int d = (isK ? ct : ct - D / BS) * BS + r16;
-        f32x4 X[NB];
+    // block forward substitution; the wave's column tiles of [Kt | beta V] advance together
+    f32x4 X[TPW][NB];
+    bool tok[TPW], isK[TPW];
+    int dcol[TPW];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            f32x4 Y;
+    for (int jj = 0; jj < TPW; ++jj) {
+        const int ct = w + 4 * jj;
+        tok[jj] = ct < NCT;
+        isK[jj] = ct < NT;
+        dcol[jj] = (isK[jj] ? ct : ct - NT) * BS + r16;
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        f32x4 Y[TPW];
+#pragma unroll
+        for (int jj = 0; jj < TPW; ++jj)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int t = BS * i + 4 * g4 + e;
-                float rv;
-                if (isK) rv = s.beta[t] * s.er[i][d] * s.kl[t][d];
-                else rv = (t < valid) ? s.beta[t] * ld1<TI>(v + base + (size_t)t * rs + d) : 0.f;
-                Y[e] = rv;
+                const int t = BS * i + 4 * g4 + e, d = dcol[jj];
+                float rv = 0.f;
+                if (tok[jj]) {
+                    if (isK[jj]) {
+                        rv = s.beta[t] * s.er[i][d] * ld1<ST>(&s.kl[t][d]);
+                    } else if constexpr (G::STAGE_V) {
+                        rv = s.beta[t] * ld1<ST>(&svbuf[t][d]);
+                    } else {
+                        rv = (t < valid) ? s.beta[t] * ld1<ST>(v + base + (size_t)t * rs + d) : 0.f;
+                    }
+                }
+                Y[jj][e] = rv;
             }
+        const float brow = -s.beta[BS * i + r16];
 #pragma unroll
-            for (int j = 0; j < i; ++j) {
-                Fr4 A = neg(frag4(&sl[0][0], C + 4, BS * i, BS * j));
-                Y = mma4<3>(A, acc2frag4(X[j]), Y);
-            }
-            X[i] = mma4<3>(frag4(&tii[i][0][0], BS + 4, 0, 0), acc2frag4(Y), zero4());
+        for (int j = 0; j < i; ++j) {
+            const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
+            const float lv[4] = {brow * x.x, brow * x.y, brow * x.z, brow * x.w};
+            const Frag4 A = frag4_from_f32<3>(lv);
+#pragma unroll
+            for (int jj = 0; jj < TPW; ++jj)
+                if (tok[jj]) Y[jj] = mma4f<3>(A, accfrag4<3>(X[jj][j]), Y[jj]);
         }
+        const Frag4 Tf = ldfrag4<3, float>(&tii[i][0][0], BS + 4, 0, 0);
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const int tb = BS * i + 4 * g4;
-            if (isK) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) a.W[cCD + (size_t)(tb + e) * D + d] = X[i][e];
-                if (a.WT)
-                    *reinterpret_cast<float4*>(&a.WT[cCD + (size_t)d * C + tb]) =
-                        make_float4(X[i][0], X[i][1], X[i][2], X[i][3]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) a.U[cCD + (size_t)(tb + e) * D + d] = X[i][e];
-            }
-        }
+        for (int jj = 0; jj < TPW; ++jj) X[jj][i] = tok[jj] ? mma4f<3>(Tf, accfrag4<3>(Y[jj]), zero4()) : zero4();
     }
-}
-
-// ----------------------------------------------------------------------------
-// recurrence
-// ----------------------------------------------------------------------------
-template <int D, typename TI, int PREC, int MODE>
-__global__ __launch_bounds__(64) void kda_recur_kernel(const RecurArgs a) {
-    constexpr int NT = D / BS;
-    const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = bid / NT, ct = bid - bh * NT;
-    const int l = threadIdx.x, r16 = l & 15, g4 = l >> 4;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int col = ct * BS + r16;
-
-    f32x4 S[NT];
+    __syncthreads();
+    // PHASE 7
+    // staging: W -> kl region, U -> ql region, WT -> kr region (all dead now)
+    ST* stW = &s.kl[0][0];
+    ST* stU = &s.ql[0][0];
+    ST* stWT = &s.kr[0][0];
 #pragma unroll
-    for (int mt = 0; mt < NT; ++mt) {
-        if (a.s0) {
-            const float4 x = *reinterpret_cast<const float4*>(a.s0 + ((size_t)bh * D + col) * D + BS * mt + 4 * g4);
-            S[mt] = f32x4{x.x, x.y, x.z, x.w};
-        } else {
-            S[mt] = zero4();
-        }
-    }
-
-    for (int n = 0; n < a.nc; ++n) {
-        const size_t ch = (size_t)bh * a.nc + n;
-        const float* W = a.W + ch * C * D;
-        const float* U = a.U + ch * C * D;
-        const float* KbT = a.KbT + ch * C * D;
-        const float* eG = a.eG + ch * D;
-
-        f32x4 Vp[NB];
+    for (int jj = 0; jj < TPW; ++jj)
+        if (tok[jj])
 #pragma unroll
-        for (int m = 0; m < NB; ++m) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) Vp[m][e] = U[(size_t)(BS * m + 4 * g4 + e) * D + col];
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks)
-                Vp[m] = mma8<PREC>(neg(frag8(W, D, BS * m, 32 * ks)), acc2frag(S[2 * ks], S[2 * ks + 1]), Vp[m]);
-        }
-
-        if constexpr (MODE == 0) {
-            const float* Qp = a.Qp + ch * C * D;
-            const float* Aqk = a.Aqk + ch * C * C;
-            const int t0 = n * C, valid = min(C, a.T - t0);
-            TI* o = static_cast<TI*>(a.o);
-#pragma unroll
-            for (int m = 0; m < NB; ++m) {
-                f32x4 O = zero4();
-#pragma unroll
-                for (int ks = 0; ks < D / 32; ++ks)
-                    O = mma8<PREC>(frag8(Qp, D, BS * m, 32 * ks), acc2frag(S[2 * ks], S[2 * ks + 1]), O);
-#pragma unroll
-                for (int ks = 0; ks <= m / 2; ++ks)
-                    O = mma8<PREC>(frag8(Aqk, C, BS * m, 32 * ks), acc2frag(Vp[2 * ks], Vp[2 * ks + 1]), O);
+            for (int i = 0; i < NB; ++i)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int t = BS * m + 4 * g4 + e;
-                    if (t < valid) st1<TI>(o + (((size_t)b * a.T + t0 + t) * a.H + h) * D + col, O[e]);
+                    const int t = BS * i + 4 * g4 + e, d = dcol[jj];
+                    if (isK[jj]) {
+                        st1<ST>(stW + t * LDK + d, X[jj][i][e]);
+                        if (oWT) st1<ST>(stWT + d * LDT + t, X[jj][i][e]);
+                    } else {
+                        st1<ST>(stU + t * LDK + d, X[jj][i][e]);
+                    }
                 }
-            }
-        } else {
-            float* hh = a.h + ch * D * D;
-            float* vp = a.Vp + ch * C * D;
-#pragma unroll
-            for (int mt = 0; mt < NT; ++mt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) hh[(size_t)(BS * mt + 4 * g4 + e) * D + col] = S[mt][e];
-#pragma unroll
-            for (int m = 0; m < NB; ++m)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) vp[(size_t)(BS * m + 4 * g4 + e) * D + col] = Vp[m][e];
-        }
-
-#pragma unroll
-        for (int mt = 0; mt < NT; ++mt) {
-            const float4 eg = *reinterpret_cast<const float4*>(eG + BS * mt + 4 * g4);
-            S[mt][0] *= eg.x; S[mt][1] *= eg.y; S[mt][2] *= eg.z; S[mt][3] *= eg.w;
-#pragma unroll
-            for (int ks = 0; ks < C / 32; ++ks)
-                S[mt] = mma8<PREC>(frag8(KbT, C, BS * mt, 32 * ks), acc2frag(Vp[2 * ks], Vp[2 * ks + 1]), S[mt]);
-        }
+    __syncthreads();
+    tile_out<ST, C, D>(stW, LDK, oW + cCD, D, C);
+    tile_out<ST, C, D>(stU, LDK, oU + cCD, D, C);
+    if constexpr (D <= C) {
+        if (oWT) tile_out<ST, D, C>(stWT, LDT, oWT + cCD, C, D);
     }
-
-    if (MODE == 0 && a.s_final) {
-#pragma unroll
-        for (int mt = 0; mt < NT; ++mt)
-            *reinterpret_cast<float4*>(a.s_final + ((size_t)bh * D + col) * D + BS * mt + 4 * g4) =
-                make_float4(S[mt][0], S[mt][1], S[mt][2], S[mt][3]);
-    }
+    // PHASE 8
 }
 
 // ----------------------------------------------------------------------------
 // launchers
 // ----------------------------------------------------------------------------
-template <int D, typename TI, typename TG>
+template <int D, typename ST, typename TG>
 static hipError_t launch_prep_t(const PrepArgs& a, int nchunks, hipStream_t st) {
-    constexpr int PREC = std::is_same<TI, float>::value ? 3 : 1;
-    hipLaunchKernelGGL((kda_prep_kernel<D, TI, TG, PREC>), dim3(nchunks), dim3(256), 0, st, a);
-    return hipGetLastError();
-}
-
-template <int D, typename TI>
-static hipError_t launch_recur_t(const RecurArgs& a, int mode, hipStream_t st) {
-    constexpr int PREC = std::is_same<TI, float>::value ? 3 : 1;
-    const dim3 grid(a.BH * (D / BS));
-    if (mode == 0) hipLaunchKernelGGL((kda_recur_kernel<D, TI, PREC, 0>), grid, dim3(64), 0, st, a);
-    else hipLaunchKernelGGL((kda_recur_kernel<D, TI, PREC, 1>), grid, dim3(64), 0, st, a);
+    constexpr int PREC = std::is_same<ST, float>::value ? 3 : 1;
+    hipLaunchKernelGGL((kda_prep_kernel<D, ST, TG, PREC>), dim3(nchunks), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -302,13 +310,6 @@ hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nc
     KDA_PREP_CASE(64)
     KDA_PREP_CASE(128)
 #undef KDA_PREP_CASE
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st) {
-    if (D == 32) return in_bf16 ? launch_recur_t<32, uint16_t>(a, mode, st) : launch_recur_t<32, float>(a, mode, st);
-    if (D == 64) return in_bf16 ? launch_recur_t<64, uint16_t>(a, mode, st) : launch_recur_t<64, float>(a, mode, st);
-    if (D == 128) return in_bf16 ? launch_recur_t<128, uint16_t>(a, mode, st) : launch_recur_t<128, float>(a, mode, st);
     return hipErrorInvalidValue;
 }
 

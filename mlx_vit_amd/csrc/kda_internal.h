@@ -1,13 +1,16 @@
 // kda_internal.h -- kernel argument blocks and launcher declarations shared by
 // the kernel translation units and the C-ABI layer.  Not installed.
 //
-// Workspace tensors are fp32, one slab per chunk (chunk id = (b*H + h)*nc + n):
+// Workspace tensors, one slab per chunk (chunk id = (b*H + h)*nc + n).  Their
+// element type ST is the input dtype (bf16 for bf16 inputs, fp32 for fp32
+// inputs) except eG, Akk and Tii, which are always fp32:
 //   W, U, Qp, Kb, Vp, dVp      [C][D]  row-major (token, channel)
 //   WT, QpT, KbT               [D][C]  transposed copies for MFMA A operands
-//   Aqk, Akk                   [C][C]  (token t, token s), zero above the diagonal
+//   Aqk                        [C][C]  (token t, token s), zero above the diagonal
 //   AqkT                       [C][C]  transpose of Aqk
-//   Tii                        [4][16][16] inverses of the diagonal blocks of I + L
-//   eG                         [D]     e^{gamma of the chunk's last row}
+//   Akk                        [C][C]  fp32, strictly lower, without the beta row scale
+//   Tii                        [4][16][16] fp32 inverses of the diagonal blocks of I + L
+//   eG                         [D]     fp32, e^{gamma of the chunk's last row}
 //   h, dh                      [D][D]  state at chunk start / its adjoint at chunk end,
 //                                      [dk][dv] orientation
 #pragma once
@@ -19,31 +22,35 @@ namespace kda {
 
 struct PrepArgs {
     const void *q, *k, *v, *g, *beta;
-    float *W, *U, *Qp, *QpT, *Kb, *KbT, *WT, *Aqk, *AqkT, *Akk, *Tii, *eG;
+    void *W, *U, *Qp, *QpT, *Kb, *KbT, *WT, *Aqk, *AqkT;
+    float *Akk, *Tii, *eG;
     int T, H, nc;
 };
 
 struct RecurArgs {
-    const float *W, *U, *Qp, *KbT, *Aqk, *eG;
+    const void *W, *U, *Qp, *KbT, *Aqk;
+    const float* eG;
     const float* s0;
     float* s_final;
     void* o;
-    float *h, *Vp;
+    void *h, *Vp;
     int T, H, nc, BH;
 };
 
 struct DhArgs {
-    const float *AqkT, *Kb, *QpT, *WT, *eG;
+    const void *AqkT, *Kb, *QpT, *WT;
+    const float* eG;
     const void* dout;
     const float* dsf;
     float* ds0;
-    float *dh, *dVp;
+    void *dh, *dVp;
     int T, H, nc, BH;
 };
 
 struct LocalArgs {
     const void *q, *k, *v, *g, *beta, *dout;
-    const float *W, *U, *Akk, *Tii, *h, *dh, *Vp, *dVp;
+    const void *W, *U, *h, *dh, *Vp, *dVp;
+    const float *Akk, *Tii;
     void *dq, *dk, *dv, *dg, *dbeta;
     int T, H, nc;
 };
