@@ -221,6 +221,27 @@ def test_bwd_parity_bf16_small():
     _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "bwd bf16 small")
 
 
+@pytest.mark.parametrize("B,T,H,D,with_state,with_dsf,g_scale", [
+    (2, 100, 3, 64, True, True, 0.1),      # ragged last chunk, state + final-state cotangent
+    (1, 1, 1, 64, True, False, 0.1),       # single token
+    (1, 65, 2, 32, True, True, 0.1),       # D = 32, one-token tail chunk
+    (1, 130, 2, 64, True, False, 6.0),     # strong decay: pairwise path
+])
+def test_bwd_parity_bf16_cases(B, T, H, D, with_state, with_dsf, g_scale):
+    x = _inputs(B, T, H, D, torch.bfloat16, seed=14, with_state=with_state, grad=True, g_scale=g_scale)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9)) if with_dsf else None
+    _assert_all(_bwd_errors(x, torch.bfloat16, dsf), TOL[torch.bfloat16],
+                f"bwd bf16 {B},{T},{H},{D},{with_state},{with_dsf},{g_scale}")
+
+
+def test_bwd_bf16_operands_fp32_gate():
+    """bf16 q/k/v/beta with a float32 g: dg comes back float32."""
+    x = _inputs(1, 200, 2, 64, torch.bfloat16, seed=15, with_state=True, grad=True)
+    x["g"] = x["g"].float() * (1.0 + 1e-3 * torch.rand(x["g"].shape, generator=torch.Generator().manual_seed(3)))
+    errs = _bwd_errors(x, torch.bfloat16)
+    _assert_all(errs, TOL[torch.bfloat16], "bwd bf16 operands, fp32 g")
+
+
 def test_bwd_parity_config2_full():
     """Config 2: fwd + VJP at B=8, H=12, T=1568, D=64 bf16, dO ~ N(0,1) bf16."""
     x = _inputs(8, 1568, 12, 64, torch.bfloat16, seed=0, grad=True)
