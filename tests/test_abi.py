@@ -40,8 +40,12 @@ def test_workspace_sizes():
     fwd = lib.kda_workspace_size(0, 8, 1568, 12, 64, 64, 1)
     bwd = lib.kda_workspace_size(1, 8, 1568, 12, 64, 64, 1)
     N = 8 * 12 * 25
-    # forward: W, U, Qp, KbT (C*D) + Aqk (C*C) + eG (D), fp32
-    assert fwd == 4 * (4 * N * 64 * 64 + N * 64 * 64 + N * 64)
+    # forward: W, U, Qp, KbT (C*D) + Aqk (C*C) in the input dtype, eG (D) in fp32
+    assert fwd == 2 * (4 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
+    assert lib.kda_workspace_size(0, 8, 1568, 12, 64, 64, 0) == 4 * (4 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
+    # backward: W, U, KbT, WT, QpT, Kb, Vp, dVp (C*D), h, dh (D*D), AqkT (C*C) in the input
+    # dtype, Akk (C*C), Tii (4*16*16), eG (D) in fp32; the forward's Qp and Aqk are not kept
+    assert bwd == 2 * (8 * N * 64 * 64 + 2 * N * 64 * 64 + N * 64 * 64) + 4 * (N * 64 * 64 + N * 1024 + N * 64)
     assert bwd > fwd
     assert lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) == 0 or lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) >= 0
 
