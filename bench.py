@@ -53,31 +53,42 @@ def op_counts(B, T, H, D, backward):
     return flops, fwd_bytes + bwd_bytes
 
 
-def kernel_counts(B, T, H, D):
-    """Per-launch algorithmic FLOPs and compulsory bytes of each library kernel
-    (ids as in kda_profile_name).  FLOPs: the dense products each kernel owns,
-    full rectangles, per token-head; bytes: each input and output tensor of the
-    kernel touched once (inputs bf16, workspace fp32)."""
+def kernel_counts(B, T, H, D, es=2):
+    """Per-launch algorithmic FLOPs and compulsory HBM bytes of each library
+    kernel (ids as in kda_profile_name).
+
+    FLOPs: the dense products each kernel owns, full rectangles, 2 per MAC, per
+    padded token-head.  Bytes: every input and output tensor of the kernel
+    touched once -- (B, T, H, *) tensors over the T valid tokens, workspace slabs
+    over every chunk -- with the library's storage types: operands and the
+    W/U/Qp/Kb/V'/dV'/A/h/dh workspace in the input dtype (``es`` bytes), Akk,
+    the diagonal-block inverses, e^G and the states in fp32."""
     nc = -(-T // C)
     N = B * H * nc              # chunks
     n = N * C                   # padded token-heads
-    es, f4 = 2, 4
-    CD, CC, DD = C * D, C * C, D * D
+    nt = B * T * H              # valid token-heads
+    f4 = 4
+    CD, CC, DD, TII = C * D, C * C, D * D, 4 * 16 * 16
+    state = B * H * DD * f4
     fl = {
         0: n * (8 * C * D + (2.0 / 3.0) * C * C),       # Akk, Aqk, W, U, solve
         1: n * (6 * D * D + 2 * C * D),                 # W S, Qp S, Kb^T V', Aqk V'
         2: n * (8 * C * D + (2.0 / 3.0) * C * C),
         3: n * (4 * D * D),                             # W S, Kb^T V'
         4: n * (2 * C * D + 6 * D * D),                 # Aqk^T dO, Kb dS, Qp^T dO, W^T dV'
-        5: n * (6 * D * D + 16 * C * D),                # dQp, dKb, dW, dAqk, solve adjoint, dL, K K^T / Q K^T adjoints
+        # dQp, dKb, dW (6D^2); dAqk 2CD; transposed solve on [dW|dU] 4CD; dL 4CD;
+        # the four decay-masked K K^T / Q K^T adjoint products 8CD
+        5: n * (6 * D * D + 18 * C * D),
     }
+    io_in = nt * (4 * D + 1) * es                       # q, k, v, g, beta
     by = {
-        0: N * (4 * CD * es + C * es + 4 * CD * f4 + CC * f4 + D * f4),
-        1: N * (4 * CD * f4 + CC * f4 + D * f4 + CD * es) + B * H * DD * f4,
-        2: N * (4 * CD * es + C * es + 6 * CD * f4 + 2 * CC * f4 + 4 * 256 * f4 + D * f4),
-        3: N * (3 * CD * f4 + D * f4 + DD * f4 + CD * f4),
-        4: N * (CC * f4 + 3 * CD * f4 + D * f4 + CD * es + DD * f4 + CD * f4) + B * H * DD * f4,
-        5: N * (5 * CD * es + C * es + 4 * CD * f4 + CC * f4 + 4 * 256 * f4 + 2 * DD * f4 + 4 * CD * es + C * es),
+        0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp KbT Aqk eG
+        1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state,                      # -> o, S_final
+        2: io_in + N * (6 * CD * es + CC * es + CC * f4 + TII * f4 + D * f4),              # -> W U KbT WT QpT Kb AqkT Akk Tii eG
+        3: N * (3 * CD * es + D * f4 + DD * es + CD * es),                                  # -> h, V'
+        4: N * (CC * es + 3 * CD * es + D * f4 + DD * es + CD * es) + nt * D * es + state,  # -> dh, dV', dS0
+        5: io_in + nt * D * es + N * (4 * CD * es + 2 * DD * es + CC * f4 + TII * f4)
+           + nt * (4 * D + 1) * es,                                                         # -> dq dk dv dg dbeta
     }
     return fl, by
 
@@ -111,6 +122,86 @@ def load_traffic(kernel_name):
         return None if rec is None else float(rec["bytes_per_dispatch"])
     except (OSError, ValueError, KeyError):
         return None
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic from rocprofv3 PMC counters
+# ---------------------------------------------------------------------------
+PROFILE_ROLES = {
+    # rocprof kernel symbol fragment -> profile names in dispatch order within a step
+    "kda_prep_kernel": ["kda_prep_kernel(fwd)", "kda_prep_kernel(bwd)"],
+    "kda_recur_kernel": ["kda_recur_kernel(fwd)", "kda_recur_kernel(states)"],
+    "kda_dh_kernel": ["kda_dh_kernel"],
+    "kda_bwd_local": ["kda_bwd_local_kernel"],
+}
+CALIB_FRAGMENT = "neg_kernel"
+
+
+def copy_calibration(mb):
+    """One plain streaming kernel of known size for scaling the PMC byte
+    counters: y = -x over ``mb`` MiB of fp32 reads and as many writes."""
+    import torch
+    x = torch.ones((mb << 20) // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    return x.numel() * 4
+
+
+def _pmc_rows(root, counter):
+    """(dispatch id, kernel name, value) per dispatch of ``counter`` from every
+    counter_collection.csv under ``root``."""
+    import csv
+    vals = {}
+    for dirpath, _, files in os.walk(root):
+        for fn in files:
+            if not fn.endswith("counter_collection.csv"):
+                continue
+            with open(os.path.join(dirpath, fn), newline="") as f:
+                for row in csv.DictReader(f):
+                    if row.get("Counter_Name") != counter:
+                        continue
+                    key = (int(row.get("Process_Id", 0) or 0), int(row["Dispatch_Id"]))
+                    name, v = vals.get(key, (row["Kernel_Name"], 0.0))
+                    vals[key] = (name, v + float(row["Counter_Value"]))
+    return [(k[1], n, v) for k, (n, v) in sorted(vals.items())]
+
+
+def pmc_summary(fetch_dir, write_dir, calib_mb):
+    """Per-dispatch HBM bytes of each library kernel: FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch) averaged over dispatches, each scaled by the ratio of
+    the calibration kernel's known bytes to what the same counter read for it."""
+    calib_bytes = (calib_mb << 20) // 4 * 4
+    out = {"calibration": {"kernel": CALIB_FRAGMENT, "bytes_read": calib_bytes, "bytes_written": calib_bytes}}
+    per = {}
+    for counter, root, key in (("FETCH_SIZE", fetch_dir, "fetch"), ("WRITE_SIZE", write_dir, "write")):
+        rows = _pmc_rows(root, counter)
+        cal = [v for _, n, v in rows if CALIB_FRAGMENT in n]
+        if not cal:
+            raise SystemExit(f"no {CALIB_FRAGMENT} dispatch with {counter} under {root}")
+        factor = calib_bytes / (max(cal) * 1024.0)
+        out["calibration"][f"{key}_kib"] = max(cal)
+        out["calibration"][f"{key}_factor"] = round(factor, 5)
+        seen = {}
+        for _, name, v in rows:
+            for frag, roles in PROFILE_ROLES.items():
+                if frag in name:
+                    i = seen.get(frag, 0)
+                    seen[frag] = i + 1
+                    rec = per.setdefault(roles[i % len(roles)], {})
+                    rec.setdefault(key, []).append(v)
+    for name, rec in per.items():
+        r = {"dispatches": len(rec.get("fetch", []))}
+        total = 0.0
+        for key in ("fetch", "write"):
+            kib = sum(rec[key]) / len(rec[key])
+            r[f"{key}_kib"] = round(kib, 1)
+            b = kib * 1024.0 * out["calibration"][f"{key}_factor"]
+            r[f"{key}_bytes"] = round(b)
+            total += b
+        r["bytes_per_dispatch"] = round(total)
+        out[name] = r
+    return out
 
 
 def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, seed=0):
@@ -171,7 +262,14 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
     ap.add_argument("--cpu-sample-tokens", type=int, default=392)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="run one plain fp32 streaming kernel of this many MiB first (PMC byte-counter scale)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE output directories and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calibration_mb or 512), indent=1))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the op on a "
               "single MI355X and reports that GPU's throughput.", file=sys.stderr)
@@ -183,6 +281,8 @@ def main():
 
     B, T, H, D, backward, with_state, desc = WORKLOADS[args.workload]
     torch.cuda.set_device(0)
+    if args.copy_calibration_mb:
+        copy_calibration(args.copy_calibration_mb)
     q, k, v, g, beta, s0, do = make_inputs_gpu(B, T, H, D, with_state)
     wsf = torch.empty(kda.workspace_bytes(0, B, T, H, D), dtype=torch.uint8, device="cuda")
     wsb = (torch.empty(kda.workspace_bytes(1, B, T, H, D), dtype=torch.uint8, device="cuda")

@@ -248,6 +248,41 @@ def test_bwd_parity_config2_full():
     _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "config2 bwd")
 
 
+# ---------------------------------------------------------------- committed golden fixtures
+
+def _golden(name):
+    import os
+    return dict(np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)))
+
+
+def test_golden_config0_forward():
+    """Config 0 (B1 T256 H2 D64 fp32, zero state) against tests/golden/kda_cfg0.npz."""
+    from tests.golden import make_golden as MG
+    f, x = _golden("kda_cfg0.npz"), MG.cfg0_inputs()
+    np.testing.assert_allclose(MG.checksums(x, MG.NAMES), f["checksums"], rtol=MG.CHECKSUM_RTOL)
+    o, sf = _kda().kda_forward(*_dev(x), None)
+    torch.cuda.synchronize()
+    _assert_all({"o": R.rel_l2(o.cpu(), torch.from_numpy(f["o"])),
+                 "s_final": R.rel_l2(sf.cpu(), torch.from_numpy(f["s_final"]))}, 1e-4, "golden cfg0")
+
+
+def test_golden_backward_d32():
+    """B1 T70 H2 D32 fp32 with S0 and dS_final against tests/golden/kda_grads_d32.npz."""
+    from tests.golden import make_golden as MG
+    f, x = _golden("kda_grads_d32.npz"), MG.grads_inputs()
+    np.testing.assert_allclose(MG.checksums(x, MG.NAMES + ("s0", "do", "dsf")), f["checksums"], rtol=MG.CHECKSUM_RTOL)
+    kda = _kda()
+    q, k, v, g, beta = _dev(x)
+    o, sf = kda.kda_forward(q, k, v, g, beta, x["s0"].to(DEV))
+    grads = kda.kda_backward(q, k, v, g, beta, x["s0"].to(DEV), x["do"].to(DEV), x["dsf"].to(DEV))
+    torch.cuda.synchronize()
+    errs = {"o": R.rel_l2(o.cpu(), torch.from_numpy(f["o"])),
+            "s_final": R.rel_l2(sf.cpu(), torch.from_numpy(f["s_final"]))}
+    for n, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads):
+        errs[n] = R.rel_l2(gr.cpu(), torch.from_numpy(f[n]))
+    _assert_all(errs, 1e-4, "golden d32 backward")
+
+
 # ---------------------------------------------------------------- autograd / API
 
 def test_autograd_function_matches_direct_backward():
