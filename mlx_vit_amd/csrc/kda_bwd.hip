@@ -1,13 +1,10 @@
 // kda_bwd.hip -- backward kernels of the KDA chunkwise WY recurrence (gfx950).
 //
 // The backward stores no per-step state.  The forward's chunk-boundary states
-// are recomputed (prep + kda_recur_kernel MODE 1), then:
+// are recomputed (prep + kda_recur_kernel MODE 1), the reverse state carry
+// (kda_dh_kernel, kda_recur.hip) stores dS at each chunk end and dV', then:
 //
-//   kda_dh_kernel     one wave per (batch, head, dv tile), reverse over chunks:
-//                         dV' = Aqk^T dO + Kb dS;  dS <- e^G dS + Qp^T dO - W^T dV'
-//                     storing dS at each chunk end and dV'; the final dS is dS0.
-//                     This is the reverse state carry of nope_gdn_mlx.py:2705-2706.
-//   kda_bwd_local_kernel
+//   kda_bwd_local2_kernel (bf16 operands) / kda_bwd_local_kernel (fp32 operands)
 //                     one workgroup per chunk, fully parallel: every remaining
 //                     adjoint of the chunk -- output / state products, the
 //                     transposed WY solve (nope_gdn_mlx.py:2637-2641, as block

@@ -10,13 +10,7 @@
 //                     Replaces nope_gdn_mlx.py:549-597 (preamble, M / M_oq
 //                     kernels 1301-1469, IA build) and lifts the triangular solve
 //                     (1098-1196) out of the sequential chunk loop.
-//   kda_recur_kernel  one wave per (batch, head, 16-column dv tile), sequential
-//                     over chunks, state tile resident in accumulator VGPRs:
-//                         V' = U - W S;  O = Qp S + Aqk V';  S <- e^G S + Kb^T V'
-//                     (S in [dk, dv] orientation).  Replaces the per-chunk
-//                     solve/finalize launches (nope_gdn_mlx.py:1519-1942,
-//                     2408-2451).  MODE 1 stores chunk-start states and V' for
-//                     the backward instead of the output.
+// The sequential half of the forward, kda_recur_kernel, is in kda_recur.hip.
 #include "kda_internal.h"
 
 namespace kda {
