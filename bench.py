@@ -3,8 +3,11 @@
 
 A step is one forward + backward (VJP) pass of the op over one batch of
 synthetic inputs already resident in HBM: config 2, B=8, H=12, T=1568, D=64,
-chunk 64, bf16 q/k/v/g/beta, dO ~ N(0,1) bf16, zero initial state.  Prints ONE
-JSON line.  ``value`` is tokens/s = B*T*steps / wall time of the timed steps.
+chunk 64, bf16 q/k/v/g/beta, dO ~ N(0,1) bf16, zero initial state -- run as a
+training step does, through the training pair (kda_fwd_train keeps the
+per-chunk factors, kda_bwd_train recomputes the chunk-boundary states from
+them).  Prints ONE JSON line.  ``value`` is tokens/s = B*T*steps / wall time of
+the timed steps.
 
 Per-kernel durations come from HIP events the library records around each of
 its launches (kda_profile_*) during a second pass of the same steps; the
@@ -31,7 +34,8 @@ C = 64
 
 WORKLOADS = {
     # name: (B, T, H, D, backward, with_state, description)
-    "cfg2": (8, 1568, 12, 64, True, False, "KDA fwd+VJP, B8 H12 T1568 D64 bf16 (config 2)"),
+    "cfg2": (8, 1568, 12, 64, True, False,
+             "KDA fwd+VJP (training pair), B8 H12 T1568 D64 bf16 (config 2)"),
     "cfg1": (8, 1568, 12, 64, False, False, "KDA fwd, B8 H12 T1568 D64 bf16 (config 1)"),
     "cfg3": (1, 32768, 16, 128, False, True, "KDA fwd, B1 H16 T32768 D128 bf16, fp32 S0 (config 3)"),
 }
@@ -79,6 +83,7 @@ def kernel_counts(B, T, H, D, es=2):
         # dQp, dKb, dW (6D^2); dAqk 2CD; transposed solve on [dW|dU] 4CD; dL 4CD;
         # the four decay-masked K K^T / Q K^T adjoint products 8CD
         5: n * (6 * D * D + 18 * C * D),
+        6: n * (8 * C * D + (2.0 / 3.0) * C * C),
     }
     io_in = nt * (4 * D + 1) * es                       # q, k, v, g, beta
     by = {
@@ -89,6 +94,7 @@ def kernel_counts(B, T, H, D, es=2):
         4: N * (CC * es + 3 * CD * es + D * f4 + DD * es + CD * es) + nt * D * es + state,  # -> dh, dV', dS0
         5: io_in + nt * D * es + N * (4 * CD * es + 2 * DD * es + CC * f4 + TII * f4)
            + nt * (4 * D + 1) * es,                                                         # -> dq dk dv dg dbeta
+        6: io_in + N * (7 * CD * es + 2 * CC * es + CC * f4 + TII * f4 + D * f4),          # -> both sets
     }
     return fl, by
 
@@ -128,8 +134,9 @@ def load_traffic(kernel_name):
 # HBM traffic from rocprofv3 PMC counters
 # ---------------------------------------------------------------------------
 PROFILE_ROLES = {
-    # rocprof kernel symbol fragment -> profile names in dispatch order within a step
-    "kda_prep_kernel": ["kda_prep_kernel(fwd)", "kda_prep_kernel(bwd)"],
+    # rocprof kernel symbol fragment -> profile names in dispatch order within a
+    # fwd+bwd step (the training pair: one prep launch, in its training mode)
+    "kda_prep_kernel": ["kda_prep_kernel(train)"],
     "kda_recur_kernel": ["kda_recur_kernel(fwd)", "kda_recur_kernel(states)"],
     "kda_dh_kernel": ["kda_dh_kernel"],
     "kda_bwd_local": ["kda_bwd_local_kernel"],
@@ -284,14 +291,15 @@ def main():
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb)
     q, k, v, g, beta, s0, do = make_inputs_gpu(B, T, H, D, with_state)
-    wsf = torch.empty(kda.workspace_bytes(0, B, T, H, D), dtype=torch.uint8, device="cuda")
-    wsb = (torch.empty(kda.workspace_bytes(1, B, T, H, D), dtype=torch.uint8, device="cuda")
-           if backward else None)
+    ws = torch.empty(kda.workspace_bytes(2 if backward else 0, B, T, H, D), dtype=torch.uint8, device="cuda")
 
     def step():
-        o, sf = kda.kda_forward(q, k, v, g, beta, s0, workspace=wsf)
+        # a training step runs the training pair; a forward-only workload the plain forward
         if backward:
-            kda.kda_backward(q, k, v, g, beta, s0, do, None, workspace=wsb)
+            o, sf, _ = kda.kda_forward_train(q, k, v, g, beta, s0, workspace=ws)
+            kda.kda_backward_train(q, k, v, g, beta, s0, do, None, ws)
+        else:
+            o, sf = kda.kda_forward(q, k, v, g, beta, s0, workspace=ws)
         return o
 
     for _ in range(args.warmup):

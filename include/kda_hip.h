@@ -39,6 +39,7 @@ extern "C" {
 
 #define KDA_PASS_FWD 0
 #define KDA_PASS_BWD 1
+#define KDA_PASS_TRAIN 2   /* kda_fwd_train + kda_bwd_train share one workspace */
 
 /* Workspace regions (see kda_workspace_offsets). */
 enum kda_ws_region {
@@ -53,8 +54,9 @@ int kda_abi_version(void);
 /* Message for the last failing call on this thread ("" if none). */
 const char* kda_last_error(void);
 
-/* Bytes of workspace kda_fwd (pass 0) or kda_bwd (pass 1) needs; 0 on invalid
- * arguments (see kda_last_error). */
+/* Bytes of workspace kda_fwd (pass 0), kda_bwd (pass 1) or the training pair
+ * kda_fwd_train / kda_bwd_train (pass 2) needs; 0 on invalid arguments (see
+ * kda_last_error). */
 size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int dtype);
 
 /* Byte offsets of the workspace regions for a pass (-1 = unused), so tests can
@@ -84,6 +86,27 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
             int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
             void* workspace, size_t ws_bytes, void* stream);
 
+/* Training pair.  kda_fwd_train computes what kda_fwd computes and also keeps,
+ * in its (pass 2) workspace, every per-chunk factor the backward needs: W, U,
+ * the decay-scaled Q / K operands and their transposes, A_qk and its transpose,
+ * A_kk, the inverted diagonal blocks of I + L and e^G.  No state is kept: the
+ * chunk-boundary states are still recomputed by kda_bwd_train.
+ * kda_bwd_train is kda_bwd without its prep: it requires the workspace that
+ * kda_fwd_train filled for the same q, k, v, g, beta (and the same B, T, H, D,
+ * dtype), unmodified in between, and returns the same gradients as kda_bwd.
+ * Replace the forward of _get_chunkwise_kda_recurrence_fn, which keeps U_traj
+ * and S_traj for its VJP (nope_gdn_mlx.py:2734-2745), and that VJP
+ * (nope_gdn_mlx.py:2746-2808) consuming them. */
+int kda_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  const float* s0, void* o, float* s_final,
+                  int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+                  void* workspace, size_t ws_bytes, void* stream);
+int kda_bwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  const float* s0, const void* dout, const float* ds_final,
+                  void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
+                  int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+                  void* workspace, size_t ws_bytes, void* stream);
+
 /* y = M^-1 b for unit-triangular M (only the strict lower, or with upper != 0
  * the strict upper, part of M is read); M [BH, Cm, Cm], b and y [BH, Cm, N],
  * fp32, 1 <= Cm <= 64, N >= 1.
@@ -97,9 +120,10 @@ int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, 
  * bracketed by two HIP events recorded on the launch stream.  Used by the
  * benchmark to measure per-kernel durations live; the kernels do the same work
  * either way.  Kernel ids: 0 prep (forward), 1 recurrence (forward), 2 prep
- * (backward), 3 state recompute, 4 reverse state recurrence, 5 local adjoints.
+ * (backward), 3 state recompute, 4 reverse state recurrence, 5 local adjoints,
+ * 6 prep (training forward).
  * kda_profile_read must be called after the streams have completed. */
-#define KDA_PROF_NKERNELS 6
+#define KDA_PROF_NKERNELS 7
 int kda_profile_enable(int on);              /* 1: clear records and start; 0: stop */
 const char* kda_profile_name(int id);
 int kda_profile_read(int id, double* total_ms, int* launches);

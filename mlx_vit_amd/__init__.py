@@ -3,11 +3,12 @@
 Hand-written gfx950 HIP kernels behind a C ABI (``include/kda_hip.h``,
 ``libkda_hip.so``), driven from torch through ctypes.
 """
-from .kda import (ChunkKDAFunction, chunk_kda, kda_backward, kda_forward, solve_unit_triangular,
-                  workspace_bytes, workspace_offsets)
+from .kda import (ChunkKDAFunction, chunk_kda, kda_backward, kda_backward_train, kda_forward,
+                  kda_forward_train, solve_unit_triangular, workspace_bytes, workspace_offsets)
 from .recurrence import HIP_PATH, KDA_PATHS, KDARecurrence
 
 __all__ = [
-    "ChunkKDAFunction", "chunk_kda", "kda_forward", "kda_backward", "solve_unit_triangular",
+    "ChunkKDAFunction", "chunk_kda", "kda_forward", "kda_backward", "kda_forward_train",
+    "kda_backward_train", "solve_unit_triangular",
     "workspace_bytes", "workspace_offsets", "KDARecurrence", "HIP_PATH", "KDA_PATHS",
 ]

@@ -19,6 +19,7 @@ KDA_E_HIP = -4
 
 KDA_PASS_FWD = 0
 KDA_PASS_BWD = 1
+KDA_PASS_TRAIN = 2
 
 WS_REGIONS = ("W", "U", "Qp", "QpT", "Kb", "KbT", "WT", "Aqk", "AqkT", "Akk", "Tii", "eG",
               "h", "dh", "Vp", "dVp")
@@ -32,12 +33,14 @@ SIGNATURES = {
     "kda_workspace_offsets": ([_I] * 7 + [ctypes.POINTER(ctypes.c_int64)], _I),
     "kda_fwd": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_bwd": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
+    "kda_fwd_train": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
+    "kda_bwd_train": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_solve_unit_triangular": ([_P] * 3 + [_I] * 4 + [_P], _I),
     "kda_profile_enable": ([_I], _I),
     "kda_profile_name": ([_I], ctypes.c_char_p),
     "kda_profile_read": ([_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)], _I),
 }
-PROF_NKERNELS = 6
+PROF_NKERNELS = 7
 
 _lib = None
 _lock = threading.Lock()

@@ -67,10 +67,11 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
     sz[KDA_WS_U] = CD;
     sz[KDA_WS_KBT] = CD;
     sz[KDA_WS_EG] = EG;
-    if (pass == KDA_PASS_FWD) {
+    if (pass != KDA_PASS_BWD) {
         sz[KDA_WS_QP] = CD;
         sz[KDA_WS_AQK] = CC;
-    } else {
+    }
+    if (pass != KDA_PASS_FWD) {
         sz[KDA_WS_WT] = CD;
         sz[KDA_WS_QPT] = CD;
         sz[KDA_WS_KB] = CD;
@@ -116,10 +117,11 @@ int hip_fail(hipError_t e, const char* where) {
 }
 
 // ---- optional launch timing: an event pair around each launch, on its stream ----
-enum { PROF_PREP_FWD = 0, PROF_RECUR_FWD, PROF_PREP_BWD, PROF_RECUR_H, PROF_DH, PROF_LOCAL };
+enum { PROF_PREP_FWD = 0, PROF_RECUR_FWD, PROF_PREP_BWD, PROF_RECUR_H, PROF_DH, PROF_LOCAL, PROF_PREP_TRAIN };
 const char* const kProfNames[KDA_PROF_NKERNELS] = {"kda_prep_kernel(fwd)", "kda_recur_kernel(fwd)",
                                                    "kda_prep_kernel(bwd)", "kda_recur_kernel(states)",
-                                                   "kda_dh_kernel", "kda_bwd_local_kernel"};
+                                                   "kda_dh_kernel", "kda_bwd_local_kernel",
+                                                   "kda_prep_kernel(train)"};
 struct Profiler {
     std::mutex mu;
     bool on = false;
@@ -230,41 +232,46 @@ hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm
 }  // namespace kda
 
 // ----------------------------------------------------------------------------
-// C ABI
+// launch sequences
 // ----------------------------------------------------------------------------
-extern "C" {
+namespace {
 
-int kda_abi_version(void) { return 1; }
+bool valid_pass(int pass) { return pass == KDA_PASS_FWD || pass == KDA_PASS_BWD || pass == KDA_PASS_TRAIN; }
 
-const char* kda_last_error(void) { return g_err.c_str(); }
-
-size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int dtype) {
-    if (pass != KDA_PASS_FWD && pass != KDA_PASS_BWD) {
-        fail(KDA_E_INVALID, "pass=%d: expected 0 (fwd) or 1 (bwd)", pass);
-        return 0;
-    }
-    if (check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass == KDA_PASS_BWD) != KDA_OK) return 0;
-    Layout L;
-    make_layout(pass, B, T, H, D, dtype, L);
-    ok();
-    return L.total;
+int check_workspace(void* workspace, size_t ws_bytes, const Layout& L) {
+    if (!workspace || ws_bytes < L.total)
+        return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
+    if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
+    return KDA_OK;
 }
 
-int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int dtype, int64_t* offsets) {
-    if (!offsets) return fail(KDA_E_INVALID, "offsets is NULL");
-    if (pass != KDA_PASS_FWD && pass != KDA_PASS_BWD) return fail(KDA_E_INVALID, "pass=%d", pass);
-    const int rc = check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass == KDA_PASS_BWD);
-    if (rc) return rc;
-    Layout L;
-    make_layout(pass, B, T, H, D, dtype, L);
-    for (int r = 0; r < KDA_WS_NREGIONS; ++r) offsets[r] = L.off[r];
-    return ok();
+// Prep: the forward's outputs (pass 0), the backward's (pass 1) or both (pass 2).
+hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+                            void* ws, const Layout& L, int T, int H, int D, int nchunks, int in_bf16, int g_bf16,
+                            hipStream_t st) {
+    kda::PrepArgs pa = {};
+    pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
+    pa.W = region(ws, L, KDA_WS_W);
+    pa.U = region(ws, L, KDA_WS_U);
+    pa.KbT = region(ws, L, KDA_WS_KBT);
+    pa.eG = fregion(ws, L, KDA_WS_EG);
+    pa.Qp = region(ws, L, KDA_WS_QP);
+    pa.Aqk = region(ws, L, KDA_WS_AQK);
+    pa.WT = region(ws, L, KDA_WS_WT);
+    pa.QpT = region(ws, L, KDA_WS_QPT);
+    pa.Kb = region(ws, L, KDA_WS_KB);
+    pa.AqkT = region(ws, L, KDA_WS_AQKT);
+    pa.Akk = fregion(ws, L, KDA_WS_AKK);
+    pa.Tii = fregion(ws, L, KDA_WS_TII);
+    pa.T = T; pa.H = H; pa.nc = (T + kda::C - 1) / kda::C;
+    const int id = pass == KDA_PASS_FWD ? PROF_PREP_FWD : pass == KDA_PASS_BWD ? PROF_PREP_BWD : PROF_PREP_TRAIN;
+    return timed(id, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, nchunks, st); });
 }
 
-int kda_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0, void* o,
-            float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
+int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+            void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
             size_t ws_bytes, void* stream) {
-    int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, false);
+    int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, pass == KDA_PASS_TRAIN);
     if (rc) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t nstate = (size_t)B * H * D * D;
@@ -279,36 +286,31 @@ int kda_fwd(const void* q, const void* k, const void* v, const void* g, const vo
         (rc = check_io(o, "o", dtype, false)) || (rc = check_scalar(beta, "beta", dtype)))
         return rc;
     Layout L;
-    make_layout(KDA_PASS_FWD, B, T, H, D, dtype, L);
-    if (!workspace || ws_bytes < L.total)
-        return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
-    if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
+    make_layout(pass, B, T, H, D, dtype, L);
+    if ((rc = check_workspace(workspace, ws_bytes, L))) return rc;
 
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
-    kda::PrepArgs pa = {};
-    pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
-    pa.W = region(workspace, L, KDA_WS_W);
-    pa.U = region(workspace, L, KDA_WS_U);
-    pa.Qp = region(workspace, L, KDA_WS_QP);
-    pa.KbT = region(workspace, L, KDA_WS_KBT);
-    pa.Aqk = region(workspace, L, KDA_WS_AQK);
-    pa.eG = fregion(workspace, L, KDA_WS_EG);
-    pa.T = T; pa.H = H; pa.nc = nc;
-    hipError_t e = timed(PROF_PREP_FWD, st, [&] {
-        return kda::launch_prep(pa, D, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16, BH * nc, st);
-    });
+    const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
+    hipError_t e = launch_prep_pass(pass, q, k, v, g, beta, workspace, L, T, H, D, BH * nc, in_bf16, g_bf16, st);
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     kda::RecurArgs ra = {};
-    ra.W = pa.W; ra.U = pa.U; ra.Qp = pa.Qp; ra.KbT = pa.KbT; ra.Aqk = pa.Aqk; ra.eG = pa.eG;
+    ra.W = region(workspace, L, KDA_WS_W);
+    ra.U = region(workspace, L, KDA_WS_U);
+    ra.Qp = region(workspace, L, KDA_WS_QP);
+    ra.KbT = region(workspace, L, KDA_WS_KBT);
+    ra.Aqk = region(workspace, L, KDA_WS_AQK);
+    ra.eG = fregion(workspace, L, KDA_WS_EG);
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-    e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, dtype == KDA_DTYPE_BF16, 0, st); });
+    e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 0, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
     return ok();
 }
 
-int kda_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+// pass 1: prep from the inputs, then the backward; pass 2: the workspace holds
+// what kda_fwd_train wrote for the same inputs, so the prep is skipped.
+int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
             int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
             void* stream) {
@@ -331,35 +333,24 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
         (rc = check_scalar(dbeta, "dbeta", dtype)))
         return rc;
     Layout L;
-    make_layout(KDA_PASS_BWD, B, T, H, D, dtype, L);
-    if (!workspace || ws_bytes < L.total)
-        return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
-    if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
+    make_layout(pass, B, T, H, D, dtype, L);
+    if ((rc = check_workspace(workspace, ws_bytes, L))) return rc;
 
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
+    hipError_t e;
+    if (pass == KDA_PASS_BWD) {
+        e = launch_prep_pass(pass, q, k, v, g, beta, workspace, L, T, H, D, BH * nc, in_bf16, g_bf16, st);
+        if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
+    }
     void* W = region(workspace, L, KDA_WS_W);
     void* U = region(workspace, L, KDA_WS_U);
     void* KbT = region(workspace, L, KDA_WS_KBT);
     float* eG = fregion(workspace, L, KDA_WS_EG);
-    void* WT = region(workspace, L, KDA_WS_WT);
-    void* QpT = region(workspace, L, KDA_WS_QPT);
-    void* Kb = region(workspace, L, KDA_WS_KB);
-    void* AqkT = region(workspace, L, KDA_WS_AQKT);
-    float* Akk = fregion(workspace, L, KDA_WS_AKK);
-    float* Tii = fregion(workspace, L, KDA_WS_TII);
     void* hS = region(workspace, L, KDA_WS_H);
     void* dhS = region(workspace, L, KDA_WS_DH);
     void* Vp = region(workspace, L, KDA_WS_VP);
     void* dVp = region(workspace, L, KDA_WS_DVP);
-
-    kda::PrepArgs pa = {};
-    pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
-    pa.W = W; pa.U = U; pa.KbT = KbT; pa.eG = eG; pa.WT = WT; pa.QpT = QpT; pa.Kb = Kb;
-    pa.AqkT = AqkT; pa.Akk = Akk; pa.Tii = Tii;
-    pa.T = T; pa.H = H; pa.nc = nc;
-    hipError_t e = timed(PROF_PREP_BWD, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, BH * nc, st); });
-    if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     kda::RecurArgs ra = {};
     ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
@@ -368,20 +359,88 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
 
     kda::DhArgs da = {};
-    da.AqkT = AqkT; da.Kb = Kb; da.QpT = QpT; da.WT = WT; da.eG = eG; da.dout = dout; da.dsf = ds_final;
-    da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
+    da.AqkT = region(workspace, L, KDA_WS_AQKT);
+    da.Kb = region(workspace, L, KDA_WS_KB);
+    da.QpT = region(workspace, L, KDA_WS_QPT);
+    da.WT = region(workspace, L, KDA_WS_WT);
+    da.eG = eG; da.dout = dout; da.dsf = ds_final; da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
     da.T = T; da.H = H; da.nc = nc; da.BH = BH;
     e = timed(PROF_DH, st, [&] { return kda::launch_dh(da, D, in_bf16, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_dh_kernel");
 
     kda::LocalArgs la = {};
     la.q = q; la.k = k; la.v = v; la.g = g; la.beta = beta; la.dout = dout;
-    la.W = W; la.U = U; la.Akk = Akk; la.Tii = Tii; la.h = hS; la.dh = dhS; la.Vp = Vp; la.dVp = dVp;
+    la.W = W; la.U = U; la.Akk = fregion(workspace, L, KDA_WS_AKK); la.Tii = fregion(workspace, L, KDA_WS_TII);
+    la.h = hS; la.dh = dhS; la.Vp = Vp; la.dVp = dVp;
     la.dq = dq; la.dk = dk; la.dv = dv; la.dg = dg; la.dbeta = dbeta;
     la.T = T; la.H = H; la.nc = nc;
     e = timed(PROF_LOCAL, st, [&] { return kda::launch_local(la, D, in_bf16, g_bf16, BH * nc, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_bwd_local_kernel");
     return ok();
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------------------
+// C ABI
+// ----------------------------------------------------------------------------
+extern "C" {
+
+int kda_abi_version(void) { return 1; }
+
+const char* kda_last_error(void) { return g_err.c_str(); }
+
+size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int dtype) {
+    if (!valid_pass(pass)) {
+        fail(KDA_E_INVALID, "pass=%d: expected 0 (fwd), 1 (bwd) or 2 (train)", pass);
+        return 0;
+    }
+    if (check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass != KDA_PASS_FWD) != KDA_OK) return 0;
+    Layout L;
+    make_layout(pass, B, T, H, D, dtype, L);
+    ok();
+    return L.total;
+}
+
+int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int dtype, int64_t* offsets) {
+    if (!offsets) return fail(KDA_E_INVALID, "offsets is NULL");
+    if (!valid_pass(pass)) return fail(KDA_E_INVALID, "pass=%d", pass);
+    const int rc = check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, pass != KDA_PASS_FWD);
+    if (rc) return rc;
+    Layout L;
+    make_layout(pass, B, T, H, D, dtype, L);
+    for (int r = 0; r < KDA_WS_NREGIONS; ++r) offsets[r] = L.off[r];
+    return ok();
+}
+
+int kda_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0, void* o,
+            float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
+            size_t ws_bytes, void* stream) {
+    return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
+                   ws_bytes, stream);
+}
+
+int kda_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+                  void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+                  void* workspace, size_t ws_bytes, void* stream) {
+    return run_fwd(KDA_PASS_TRAIN, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
+                   ws_bytes, stream);
+}
+
+int kda_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+            const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
+            int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
+            void* stream) {
+    return run_bwd(KDA_PASS_BWD, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D, chunk,
+                   dtype, g_dtype, workspace, ws_bytes, stream);
+}
+
+int kda_bwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+                  const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta,
+                  float* ds0, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
+                  size_t ws_bytes, void* stream) {
+    return run_bwd(KDA_PASS_TRAIN, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D,
+                   chunk, dtype, g_dtype, workspace, ws_bytes, stream);
 }
 
 int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     __shared__ float sda[C][C + 4];          // dAqk
     __shared__ float sdr[C][2 * D + 4];      // dR = (I + L)^-T [dW | dU]
     __shared__ float tii[NB][BS][BS + 4];
-    __shared__ float sdb[C];                 // dbeta
+    __shared__ float sdb[NB + NT][C];        // dbeta partials: [j] from dL tiles of column block j, [NB + nt] from channel tile nt
 
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
     const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
         const int i = idx / (BS * BS), e = idx - i * BS * BS;
         tii[i][e / BS][e % BS] = a.Tii[(size_t)ch * NB * BS * BS + idx];
     }
-    if (tid < C) sdb[tid] = 0.f;
+    for (int idx = tid; idx < (NB + NT) * C; idx += 256) sdb[idx / C][idx % C] = 0.f;
     int flag = chunk_load<D, TI, TG>(s, q, k, g, beta, base, rs, bbase, a.H, valid);
     chunk_cumsum<D>(s);
     const int unsafe = chunk_factors<D, PREC>(s, flag);
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                 dka[m][e] += bt * egt * dRk[m][e];
                 dga[m][e] += dRk[m][e] * bt * egt * kx[m][e];
                 const float db = sum16(dRv[m][e] * vv + dRk[m][e] * egt * kx[m][e]);
-                if (r16 == 0) atomicAdd(&sdb[t], db);
+                if (r16 == 0) sdb[NB + nt][t] = db;
                 sdr[t][d] = dRk[m][e];
                 sdr[t][D + d] = dRv[m][e];
             }
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
             const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
             const float dL = (sx < t) ? -acc[e] : 0.f;
             const float db = sum16(dL * sp[t][sx]);
-            if (r16 == 0) atomicAdd(&sdb[t], db);
+            if (r16 == 0) sdb[j][t] = db;
             sp[t][sx] = s.beta[t] * dL;
         }
     }
@@ -359,7 +359,12 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                 }
             }
     }
-    if (tid < valid) st1<TI>(static_cast<TI*>(a.dbeta) + bbase + (size_t)tid * a.H, sdb[tid]);
+    if (tid < valid) {
+        float db = 0.f;
+#pragma unroll
+        for (int j = 0; j < NB + NT; ++j) db += sdb[j][tid];
+        st1<TI>(static_cast<TI*>(a.dbeta) + bbase + (size_t)tid * a.H, db);
+    }
     // PHASE 6
 }
 

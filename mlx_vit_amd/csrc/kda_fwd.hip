@@ -38,6 +38,20 @@ struct PrepGeom {
     static constexpr bool STG_IN_G = (int)sizeof(float) * C * CSm::LDG >= C * LDT * (int)sizeof(ST);
 };
 
+// g[c][r] = lds[r][c] for an R x CC tile: each thread gathers one 16-byte
+// output vector (EPV consecutive r of one c) from LDS and stores it.
+template <typename ST, int R, int CC>
+__device__ __forceinline__ void tile_out_T(const ST* lds, int lld, ST* __restrict__ g, size_t gld) {
+    constexpr int EPV = 16 / (int)sizeof(ST), GPC = R / EPV, NV = CC * GPC;
+    for (int vv = threadIdx.x; vv < NV; vv += 256) {
+        const int c = vv / GPC, r0 = (vv - c * GPC) * EPV;
+        float x[EPV];
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) x[e] = ld1<ST>(lds + (r0 + e) * lld + c);
+        store_vec<ST>(g + (size_t)c * gld + r0, x);
+    }
+}
+
 template <int D, typename ST, typename TG, int PREC>
 __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     using G = PrepGeom<D, ST>;
@@ -73,6 +87,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     ST* oAqk = static_cast<ST*>(a.Aqk);
     ST* oAqkT = static_cast<ST*>(a.AqkT);
     const bool bwd = oAqkT != nullptr;
+    const bool stT = bwd && oAqk == nullptr;   // Aqk staged transposed (backward-only outputs)
 
     // PHASE 0 (load)
     const int flag = chunk_load2<D, ST, TG, G::STAGE_V>(s, &svbuf[0][0], LDK, q, k, v, g, beta, base, rs, bbase,
@@ -176,7 +191,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
                 sa[t][sx] = (sx < t) ? P[e] : 0.f;
                 const float aq = (sx <= t) ? Q[e] : 0.f;
-                if (bwd) st1<ST>(stA + sx * LDT + t, aq);
+                if (stT) st1<ST>(stA + sx * LDT + t, aq);
                 else st1<ST>(stA + t * LDT + sx, aq);
             }
         }
@@ -187,7 +202,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
             const int t = BS * i + e / BS, sx = BS * j + (e % BS);
             sa[t][sx] = 0.f;
-            if (bwd) st1<ST>(stA + sx * LDT + t, 0.f);
+            if (stT) st1<ST>(stA + sx * LDT + t, 0.f);
             else st1<ST>(stA + t * LDT + sx, 0.f);
         }
     }
@@ -195,7 +210,10 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     // PHASE 5
     if (!unsafe) {
         if (oAqk) tile_out<ST, C, C>(stA, LDT, oAqk + cCC, C, C);
-        if (oAqkT) tile_out<ST, C, C>(stA, LDT, oAqkT + cCC, C, C);
+        if (oAqkT) {
+            if (stT) tile_out<ST, C, C>(stA, LDT, oAqkT + cCC, C, C);
+            else tile_out_T<ST, C, C>(stA, LDT, oAqkT + cCC, C);
+        }
         if (a.Akk) tile_out<float, C, C>(&sa[0][0], LDA, a.Akk + cCC, C, C);
     }
     diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);

@@ -118,8 +118,38 @@ def kda_forward(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
     return o, s_final
 
 
+def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
+                      workspace: Optional[torch.Tensor] = None
+                      ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Forward that also keeps the per-chunk factors the backward needs.
+    Returns (o, final_state, workspace); pass the workspace, unmodified, to
+    ``kda_backward_train`` with the same inputs."""
+    _check_chunk(chunk_size)
+    q, k, v, g, beta, s0 = _prepare(q, k, v, g, beta, initial_state)
+    B, T, H, D = q.shape
+    if D not in BWD_HEAD_DIMS:
+        raise ValueError(f"head_dim={D}: training supports {BWD_HEAD_DIMS}")
+    lib = _lib.load()
+    dev = q.device
+    o = torch.empty_like(q)
+    s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_TRAIN, B, T, H, D, dev, q.dtype)
+    rc = lib.kda_fwd_train(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
+                           B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                           _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "kda_fwd_train")
+    return o, s_final, ws
+
+
+def kda_backward_train(q, k, v, g, beta, initial_state, do, ds_final, workspace: torch.Tensor,
+                       chunk_size: int = CHUNK):
+    """VJP from the workspace of ``kda_forward_train`` (same inputs): returns
+    (dq, dk, dv, dg, dbeta, d_initial_state)."""
+    return kda_backward(q, k, v, g, beta, initial_state, do, ds_final, chunk_size, workspace, _train=True)
+
+
 def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size: int = CHUNK,
-                 workspace: Optional[torch.Tensor] = None):
+                 workspace: Optional[torch.Tensor] = None, _train: bool = False):
     """VJP of ``kda_forward``: returns (dq, dk, dv, dg, dbeta, d_initial_state)."""
     _check_chunk(chunk_size)
     q, k, v, g, beta, s0 = _prepare(q, k, v, g, beta, initial_state)
@@ -138,24 +168,33 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
     ds0 = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    if _train and workspace is None:
+        raise ValueError("kda_backward_train needs the workspace returned by kda_forward_train")
     ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_BWD, B, T, H, D, dev, q.dtype)
-    rc = lib.kda_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
-                     _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ds0),
-                     B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
-                     _ptr(ws), ws.numel(), _stream(dev))
-    _lib.check(rc, "kda_bwd")
+    fn = lib.kda_bwd_train if _train else lib.kda_bwd
+    rc = fn(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
+            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ds0),
+            B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+            _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "kda_bwd_train" if _train else "kda_bwd")
     return dq, dk, dv, dg, dbeta, ds0
 
 
 class ChunkKDAFunction(torch.autograd.Function):
-    """Autograd wrapper: the forward keeps only its inputs; the backward
-    recomputes chunk-boundary states (the role of mx.custom_function in
-    nope_gdn_mlx.py:2725-2808, without the saved U / S trajectories)."""
+    """Autograd wrapper (the role of mx.custom_function in
+    nope_gdn_mlx.py:2725-2808).  When a gradient is needed the forward keeps its
+    inputs and the per-chunk factors of kda_forward_train -- not the U / S
+    trajectories the reference keeps; the backward recomputes the
+    chunk-boundary states from those factors."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, initial_state):
-        o, s_final = kda_forward(q, k, v, g, beta, initial_state)
+        if any(ctx.needs_input_grad):
+            o, s_final, ws = kda_forward_train(q, k, v, g, beta, initial_state)
+        else:
+            (o, s_final), ws = kda_forward(q, k, v, g, beta, initial_state), None
         ctx.save_for_backward(q, k, v, g, beta, initial_state)
+        ctx.ws = ws
         ctx.has_state = initial_state is not None
         return o, s_final
 
@@ -164,7 +203,11 @@ class ChunkKDAFunction(torch.autograd.Function):
         q, k, v, g, beta, s0 = ctx.saved_tensors
         if do is None:
             do = torch.zeros_like(q)
-        dq, dk, dv, dg, dbeta, ds0 = kda_backward(q, k, v, g, beta, s0, do, ds_final)
+        if ctx.ws is not None:
+            dq, dk, dv, dg, dbeta, ds0 = kda_backward_train(q, k, v, g, beta, s0, do, ds_final, ctx.ws)
+            ctx.ws = None
+        else:
+            dq, dk, dv, dg, dbeta, ds0 = kda_backward(q, k, v, g, beta, s0, do, ds_final)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
                 ds0 if ctx.has_state else None)
 

@@ -47,12 +47,15 @@ def test_workspace_sizes():
     # dtype, Akk (C*C), Tii (4*16*16), eG (D) in fp32; the forward's Qp and Aqk are not kept
     assert bwd == 2 * (8 * N * 64 * 64 + 2 * N * 64 * 64 + N * 64 * 64) + 4 * (N * 64 * 64 + N * 1024 + N * 64)
     assert bwd > fwd
+    # the training pair's workspace holds both passes' regions
+    train = lib.kda_workspace_size(2, 8, 1568, 12, 64, 64, 1)
+    assert train == fwd + bwd - 2 * (3 * N * 64 * 64) - 4 * N * 64
     assert lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) == 0 or lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) >= 0
 
 
 def test_workspace_offsets_disjoint():
     lib = _lib.load()
-    for pass_ in (0, 1):
+    for pass_ in (0, 1, 2):
         arr = (ctypes.c_int64 * 16)()
         assert lib.kda_workspace_offsets(pass_, 2, 300, 3, 64, 64, 1, arr) == 0
         offs = sorted(o for o in arr if o >= 0)
@@ -91,6 +94,23 @@ def test_null_and_workspace_errors():
     # the backward supports D in {32, 64}
     rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 128, 64, 1, 1, fake, 1 << 40, None)
     assert rc == _lib.KDA_E_UNSUPPORTED and "backward" in _lib.last_error()
+
+
+def test_training_pair_argument_errors():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    # training needs a backward-capable head dim, and the pass-2 workspace
+    rc = lib.kda_fwd_train(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 128, 64, 1, 1,
+                           fake, 1 << 40, None)
+    assert rc == _lib.KDA_E_UNSUPPORTED
+    need = lib.kda_workspace_size(2, 1, 64, 1, 64, 64, 1)
+    assert need > lib.kda_workspace_size(0, 1, 64, 1, 64, 64, 1)
+    rc = lib.kda_fwd_train(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 64, 64, 1, 1,
+                           fake, need - 1, None)
+    assert rc == _lib.KDA_E_WORKSPACE
+    rc = lib.kda_bwd_train(*([fake] * 14), 1, 64, 1, 64, 64, 1, 1, fake, need - 1, None)
+    assert rc == _lib.KDA_E_WORKSPACE
+    assert lib.kda_workspace_size(3, 1, 64, 1, 64, 64, 1) == 0
 
 
 def test_solve_argument_errors():

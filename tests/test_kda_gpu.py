@@ -248,6 +248,31 @@ def test_bwd_parity_config2_full():
     _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "config2 bwd")
 
 
+# ---------------------------------------------------------------- training pair
+
+@pytest.mark.parametrize("B,T,H,D,dtype,g_scale", [
+    (2, 100, 3, 64, torch.bfloat16, 0.1),
+    (1, 130, 2, 64, torch.bfloat16, 6.0),     # pairwise path writes both A_qk layouts directly
+    (1, 65, 2, 32, torch.float32, 0.1),
+    (1, 1, 1, 64, torch.float32, 0.1),
+])
+def test_training_pair_equals_standalone_calls(B, T, H, D, dtype, g_scale):
+    """kda_fwd_train / kda_bwd_train reproduce kda_fwd / kda_bwd bit for bit."""
+    kda = _kda()
+    x = _inputs(B, T, H, D, dtype, seed=16, with_state=True, grad=True, g_scale=g_scale)
+    q, k, v, g, beta = _dev(x)
+    s0, do = x["s0"].to(DEV), x["do"].to(DEV)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(4)).to(DEV)
+    o1, sf1 = kda.kda_forward(q, k, v, g, beta, s0)
+    g1 = kda.kda_backward(q, k, v, g, beta, s0, do, dsf)
+    o2, sf2, ws = kda.kda_forward_train(q, k, v, g, beta, s0)
+    g2 = kda.kda_backward_train(q, k, v, g, beta, s0, do, dsf, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(sf1, sf2)
+    for n, a, b in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), g1, g2):
+        assert torch.equal(a, b), n
+
+
 # ---------------------------------------------------------------- committed golden fixtures
 
 def _golden(name):
