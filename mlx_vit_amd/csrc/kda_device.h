@@ -379,10 +379,35 @@ struct Tile {
             }
         }
     }
-    __device__ __forceinline__ void store(ST* lds, int lld) const {
+    __device__ __forceinline__ void store(ST* lds, int lld) const { store_at(threadIdx.x, lds, lld); }
+
+    // the same with an explicit thread index t in [0, 256) (for a 256-thread
+    // subset of a larger workgroup)
+    __device__ __forceinline__ void load_at(int t, const ST* __restrict__ g, size_t gld) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int v = threadIdx.x + 256 * i;
+            const int v = t + 256 * i;
+            if (NV % 256 == 0 || v < NV) {
+                const int row = v / VPR, c = (v - row * VPR) * EPV;
+                put(i, *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c));
+            }
+        }
+    }
+    __device__ __forceinline__ void load_at(int t, const ST* __restrict__ g, size_t gld, int valid_rows) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int v = t + 256 * i;
+            if (NV % 256 == 0 || v < NV) {
+                const int row = v / VPR, c = (v - row * VPR) * EPV;
+                put(i, (row < valid_rows) ? *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c)
+                                          : make_uint4(0u, 0u, 0u, 0u));
+            }
+        }
+    }
+    __device__ __forceinline__ void store_at(int t, ST* lds, int lld) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int v = t + 256 * i;
             if (NV % 256 == 0 || v < NV) {
                 const int row = v / VPR, c = (v - row * VPR) * EPV;
                 *reinterpret_cast<uint4*>(lds + row * lld + c) = get(i);
@@ -390,6 +415,17 @@ struct Tile {
         }
     }
 };
+
+template <typename ST, int ROWS, int COLS>
+__device__ __forceinline__ void tile_out_at(int t, const ST* lds, int lld, ST* __restrict__ g, size_t gld,
+                                            int valid_rows) {
+    constexpr int EPV = 16 / (int)sizeof(ST), VPR = COLS / EPV, NV = ROWS * VPR;
+    for (int v = t; v < NV; v += 256) {
+        const int row = v / VPR, c = (v - row * VPR) * EPV;
+        if (row < valid_rows)
+            *reinterpret_cast<uint4*>(g + (size_t)row * gld + c) = *reinterpret_cast<const uint4*>(lds + row * lld + c);
+    }
+}
 
 template <typename ST, int ROWS, int COLS>
 __device__ __forceinline__ void tile_out(const ST* lds, int lld, ST* __restrict__ g, size_t gld, int valid_rows) {
@@ -411,6 +447,116 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     constexpr int NXCD = 8;
     if (nblocks % NXCD != 0) return bid;
     return (bid % NXCD) * (nblocks / NXCD) + bid / NXCD;
+}
+
+// ----------------------------------------------------------------------------
+// LDS DMA (gfx950 global_load_lds_dwordx4): one wave instruction moves 64 x 16
+// bytes from per-lane global addresses into 1 KB of LDS, lane l landing at
+// base + 16 l, without passing through registers.  Completion is counted by
+// vmcnt; a workgroup fence would wait for all of them, so kernels that keep
+// DMA in flight across barriers use lds_barrier() and dma_wait<N>() instead of
+// __syncthreads().
+// ----------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+// Issued as inline assembly with the LDS base bound to M0.  The compiler's
+// wait-count pass does not see it, so it cannot conservatively drain every DMA
+// in flight before an unrelated LDS access (which it does for the builtin
+// whenever it cannot tell the DMA target and the access apart).  Callers wait
+// for their DMA explicitly with dma_wait<N>() before the barrier that
+// publishes it; compiler-generated vmcnt waits for other memory operations
+// stay correct, only more conservative, because a DMA issued after such an
+// operation completes after it.  The s_nop covers the M0-write -> LDS-DMA
+// hazard that the compiler's hazard recognizer does not see through asm.
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_base);
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m) : "memory");
+}
+
+// the same with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane offset
+__device__ __forceinline__ void dma16_s(const void* gbase, uint32_t off, void* lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_base);
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(gbase), "{m0}"(m) : "memory");
+}
+
+// s_waitcnt immediates (gfx9 layout: vmcnt [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
+template <int N>
+__device__ __forceinline__ void dma_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// This wave's LDS writes complete, then the workgroup barrier.  The empty asm
+// statements keep the compiler from moving memory operations across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Swizzled LDS tiles: rows of RB bytes (a multiple of 16); the 16-byte chunk c
+// of row r is stored at chunk c ^ (r & M), M = min(RB / 16, 8) - 1, so that
+// the 16 rows an MFMA fragment read touches spread over the banks.
+template <int RB>
+struct Swz {
+    static constexpr int NCH = RB / 16, M = (NCH < 8 ? NCH : 8) - 1;
+    // byte offset of byte b of row r
+    __device__ __forceinline__ static int at(int r, int b) { return r * RB + ((((b >> 4) ^ (r & M))) << 4) + (b & 15); }
+};
+
+// Fill an NR x RB-byte swizzled LDS tile from a global tile whose rows are GS
+// bytes apart.  The tile is NR * RB / 1024 wave-instructions; wave `first` of
+// STEP waves issues instructions first, first + STEP, ... (COUNT of them), lane
+// l of instruction i filling LDS bytes [1024 i + 16 l, +16).  Rows at or past
+// valid_rows are not loaded (their lanes are inactive).
+template <int NR, int RB, int STEP>
+struct DmaTile {
+    static constexpr int NI = NR * RB / 1024, COUNT = NI / STEP;
+    static_assert((NR * RB) % 1024 == 0 && NI % STEP == 0, "tile must split into whole 1 KB blocks per wave");
+    // per-lane byte offsets of this wave's instructions (fixed for a kernel)
+    __device__ __forceinline__ static void offsets(uint32_t (&off)[COUNT], size_t GS, int first, int lane) {
+#pragma unroll
+        for (int k = 0; k < COUNT; ++k) {
+            const int i = first + STEP * k;
+            const int p = 1024 * i + 16 * lane, r = p / RB, pc = (p % RB) >> 4;
+            off[k] = (uint32_t)(r * GS) + ((uint32_t)(pc ^ (r & Swz<RB>::M)) << 4);
+        }
+    }
+    // all rows valid: wave-uniform base plus the precomputed offsets
+    __device__ __forceinline__ static void issue_s(const char* g, const uint32_t (&off)[COUNT], char* lds, int first) {
+#pragma unroll
+        for (int k = 0; k < COUNT; ++k) dma16_s(g, off[k], lds + 1024 * (first + STEP * k));
+    }
+    __device__ __forceinline__ static void issue(const char* g, size_t GS, char* lds, int first, int lane,
+                                                 int valid_rows = NR) {
+#pragma unroll
+        for (int k = 0; k < COUNT; ++k) {
+            const int i = first + STEP * k;
+            const int p = 1024 * i + 16 * lane, r = p / RB, pc = (p % RB) >> 4;
+            const int c = pc ^ (r & Swz<RB>::M);
+            if (r < valid_rows) dma16(g + (size_t)r * GS + (c << 4), lds + 1024 * i);
+        }
+    }
+};
+
+// MFMA fragment (16x16x32 bf16, same k-slot order as ldfrag) from a swizzled
+// bf16 tile with RB-byte rows: rows row0 + l%16, k = k0 + 4 (l/16) + {0..3, 16..19}
+template <int RB>
+__device__ __forceinline__ Frag8 ldfrag_sw(const uint16_t* M, int row0, int k0) {
+    const int l = lane_id(), r = row0 + (l & 15), g = l >> 4;
+    const char* base = reinterpret_cast<const char*>(M);
+    const uint2 x = *reinterpret_cast<const uint2*>(base + Swz<RB>::at(r, 2 * (k0 + 4 * g)));
+    const uint2 y = *reinterpret_cast<const uint2*>(base + Swz<RB>::at(r, 2 * (k0 + 4 * g + 16)));
+    Frag8 f;
+    f.h = __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
+    return f;
+}
+// one bf16 element (row r, column c) of a swizzled tile, as float
+template <int RB>
+__device__ __forceinline__ float ld_sw(const uint16_t* M, int r, int c) {
+    return bf2f(*reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(M) + Swz<RB>::at(r, 2 * c)));
 }
 
 }  // namespace kda

@@ -521,21 +521,1118 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// bf16 recurrences, row split and warp-specialised.
+//
+// CS workgroups per (batch, head) each own DC = D / CS state columns (the
+// state update, V' and O are all column-separable).  A workgroup has 8 waves:
+//   compute waves 0-3: wave w owns row block w of the chunk's [C][DC] tiles
+//     (V', O / dV') and state row blocks w, w + 4, ... .  Per chunk the state
+//     and then V' pass between them through LDS as bf16 B operands, transposed
+//     so every fragment is two 8-byte reads;
+//   memory waves 4-7: stream the chunk slabs (registers two chunks ahead,
+//     committed to the other half of a double-buffered LDS set one chunk
+//     ahead) and flush the staged outputs with coalesced 16-byte stores.
+// Both roles meet at two barriers per chunk:
+//   compute: [A] fragments, V' = U - W S, write V'^T [B] S <- diag(e^G) S +
+//            Kb^T V', write S^T for the next chunk, O = Qp S + Aqk V' -> staging
+//   memory:  [A] flush chunk n-1 [B] commit chunk n+1, load chunk n+2
+// ----------------------------------------------------------------------------
+template <int D, int MODE, int CS>
+struct Recur2Layout {
+    static constexpr int DC = D / CS, PS = 8;
+    static constexpr int LDR = D + PS, LDU = DC + PS, LDC = C + PS;
+    static constexpr int W_OFF = 0;
+    static constexpr int U_OFF = W_OFF + C * LDR;
+    static constexpr int QP_OFF = U_OFF + C * LDU;
+    static constexpr int KBT_OFF = QP_OFF + (MODE == 0 ? C * LDR : 0);
+    static constexpr int AQK_OFF = KBT_OFF + D * LDC;
+    static constexpr int SET_ELEMS = AQK_OFF + (MODE == 0 ? C * LDC : 0);
+    static constexpr int EG_BYTE = SET_ELEMS * 2;
+    static constexpr int SET_BYTES = (EG_BYTE + D * 4 + 15) & ~15;
+    static constexpr int XS_OFF = 2 * SET_BYTES;                 // S^T  [DC][LDR]
+    static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;         // V'^T [DC][LDC]
+    static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
+    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : D * LDU + C * LDU;   // O | h, V'
+    static constexpr int STG_BYTES = (STG_ELEMS * 2 + 15) & ~15;
+    static constexpr int NSTG = (MODE == 0) ? 2 : 3;            // staging tiles, by chunk % NSTG
+    static constexpr int BYTES = STG_OFF + NSTG * STG_BYTES;
+    static_assert(BYTES <= 160 * 1024, "recurrence LDS");
+};
+
+// the lane's 4 consecutive rows of an accumulator as 4 bf16 (8 bytes)
+__device__ __forceinline__ uint2 pack4bf(const f32x4& x) {
+    return make_uint2(pack2bf(x[0], x[1]), pack2bf(x[2], x[3]));
+}
+
+// one chunk's slabs for the forward recurrence, in registers of a memory wave
+template <int D, int MODE, int CS>
+struct Recur2Slabs {
+    static constexpr int DC = D / CS;
+    Tile<uint16_t, C, D> W, Qp;
+    Tile<uint16_t, C, DC> U;
+    Tile<uint16_t, D, C> KbT;
+    Tile<uint16_t, C, C> Aqk;
+    Tile<float, 1, D> eG;
+};
+
+template <int D, int MODE, int CS>
+__global__ __launch_bounds__(512) void kda_recur2_kernel(const RecurArgs a) {
+    using ST = uint16_t;
+    using Lay = Recur2Layout<D, MODE, CS>;
+    using Slabs = Recur2Slabs<D, MODE, CS>;
+    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4;
+    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
+    __shared__ __align__(16) unsigned char smem[Lay::BYTES];
+
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lb = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    auto set = [&](int buf) __attribute__((always_inline)) { return reinterpret_cast<ST*>(smem + buf * Lay::SET_BYTES); };
+    auto seg = [&](int buf) __attribute__((always_inline)) { return reinterpret_cast<float*>(smem + buf * Lay::SET_BYTES + Lay::EG_BYTE); };
+    auto stg = [&](int sb) __attribute__((always_inline)) { return reinterpret_cast<ST*>(smem + Lay::STG_OFF + sb * Lay::STG_BYTES); };
+    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
+    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
+
+    if (wv >= 4) {
+        // ---------------- memory waves ----------------
+        const int mt = tid - 256;
+        auto issue = [&](int n, Slabs& p) __attribute__((always_inline)) {
+            const size_t ch = (size_t)bh * a.nc + n;
+            p.W.load_at(mt, static_cast<const ST*>(a.W) + ch * C * D, D);
+            p.U.load_at(mt, static_cast<const ST*>(a.U) + ch * C * D + c0, D);
+            p.KbT.load_at(mt, static_cast<const ST*>(a.KbT) + ch * C * D, C);
+            p.eG.load_at(mt, a.eG + ch * D, D);
+            if constexpr (MODE == 0) {
+                p.Qp.load_at(mt, static_cast<const ST*>(a.Qp) + ch * C * D, D);
+                p.Aqk.load_at(mt, static_cast<const ST*>(a.Aqk) + ch * C * C, C);
+            }
+        };
+        auto commit = [&](int buf, const Slabs& p) __attribute__((always_inline)) {
+            p.W.store_at(mt, set(buf) + Lay::W_OFF, LDR);
+            p.U.store_at(mt, set(buf) + Lay::U_OFF, LDU);
+            p.KbT.store_at(mt, set(buf) + Lay::KBT_OFF, LDC);
+            p.eG.store_at(mt, seg(buf), D);
+            if constexpr (MODE == 0) {
+                p.Qp.store_at(mt, set(buf) + Lay::QP_OFF, LDR);
+                p.Aqk.store_at(mt, set(buf) + Lay::AQK_OFF, LDC);
+            }
+        };
+        auto flush = [&](int n) __attribute__((always_inline)) {
+            const ST* sst = stg(n % Lay::NSTG);
+            if constexpr (MODE == 0) {
+                const int t0 = n * C, valid = min(C, a.T - t0);
+                tile_out_at<ST, C, DC>(mt, sst, LDU,
+                                       static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
+                                       (size_t)a.H * D, valid);
+            } else {
+                const size_t ch = (size_t)bh * a.nc + n;
+                tile_out_at<ST, D, DC>(mt, sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
+                tile_out_at<ST, C, DC>(mt, sst + D * LDU, LDU, static_cast<ST*>(a.Vp) + ch * C * D + c0, D, C);
+            }
+        };
+        // Chunk c's slabs live in register set c % NS from their load (NS
+        // chunks ahead) to their commit into LDS set c & 1 (one chunk ahead);
+        // NS = 2 at D = 128, whose slabs would not fit three times.  The loop is
+        // unrolled NS times so that every step names its register set and the
+        // compiler can wait for exactly the loads that step commits.
+        //   between A(n) and B(n): commit chunk n+1
+        //   between B(n) and A(n+1): flush chunk n-1, load chunk n+1+NS
+        constexpr int NS = (D >= 128) ? 2 : 3;
+        Slabs p0, p1, p2;
+        issue(0, p0);
+        if (a.nc > 1) issue(1, p1);
+        if (NS == 3 && a.nc > 2) issue(2, p2);
+        commit(0, p0);
+        if (a.nc > NS) issue(NS, p0);
+        __syncthreads();                                       // P: chunk 0 committed
+        auto step = [&](int n, Slabs& p) __attribute__((always_inline)) {   // p holds chunk n+1
+            __syncthreads();                                   // A(n)
+            if (n + 1 < a.nc) commit((n + 1) & 1, p);
+            __syncthreads();                                   // B(n): chunk n+1 committed
+            if (n > 0) flush(n - 1);
+            if (n + 1 + NS < a.nc) issue(n + 1 + NS, p);
+        };
+        for (int n = 0; n < a.nc; n += NS) {
+            step(n, p1);
+            if (n + 1 < a.nc) step(n + 1, NS == 3 ? p2 : p0);
+            if (NS == 3 && n + 2 < a.nc) step(n + 2, p0);
+        }
+        __syncthreads();
+        flush(a.nc - 1);
+        return;
+    }
+
+    // ---------------- compute waves ----------------
+    const int w = wv, l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    // state tiles: rows d = 16 mt[i] + 4 g4 + e, local columns 16 j + r16
+    int mt[MT];
+    bool own[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        mt[i] = w + 4 * i;
+        own[i] = mt[i] < NT;
+    }
+    f32x4 S[MT][NTW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            S[i][j] = zero4();
+            if (own[i] && a.s0) {
+                const float4 x = *reinterpret_cast<const float4*>(
+                    a.s0 + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4);
+                S[i][j] = f32x4{x.x, x.y, x.z, x.w};
+            }
+        }
+    // S^T for the B operands (and, for the backward, the chunk-start state)
+    auto put_state = [&](ST* sst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(S[i][j]);
+                    if constexpr (MODE == 1)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
+                }
+    };
+    put_state(stg(0));
+
+    // A operands of one chunk, read from its LDS set ahead of time
+    Frag8 Aw[D / 32], Aq[D / 32], Aa[2], Akb[MT][C / 32];
+    f32x4 Uv[NTW];
+    float4 eg[MT];
+    auto preload = [&](int buf) __attribute__((always_inline)) {
+        const ST* sW = set(buf) + Lay::W_OFF;
+        const ST* sU = set(buf) + Lay::U_OFF;
+        const ST* sKbT = set(buf) + Lay::KBT_OFF;
+        const float* seG = seg(buf);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) Aw[ks] = ldfrag<1, ST>(sW, LDR, BS * w, 32 * ks);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Uv[j][e] = ld1<ST>(sU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) Akb[i][ks] = ldfrag<1, ST>(sKbT, LDC, BS * mt[i], 32 * ks);
+                eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
+            }
+        if constexpr (MODE == 0) {
+            const ST* sQp = set(buf) + Lay::QP_OFF;
+            const ST* sAqk = set(buf) + Lay::AQK_OFF;
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Aq[ks] = ldfrag<1, ST>(sQp, LDR, BS * w, 32 * ks);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (ks <= w / 2) Aa[ks] = ldfrag<1, ST>(sAqk, LDC, BS * w, 32 * ks);
+        }
+    };
+    __syncthreads();                                           // P
+    preload(0);
+
+    for (int n = 0; n < a.nc; ++n) {
+        const int buf = n & 1;
+        ST* sst = stg(n % Lay::NSTG);
+        __syncthreads();                                       // A(n)
+
+        Frag8 Bs[NTW][D / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, BS * j, 32 * ks);
+        // V' = U - W S, row block w
+        f32x4 Vp[NTW];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            f32x4 P = zero4();
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) P = mma<1>(Aw[ks], Bs[j][ks], P);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Vp[j][e] = Uv[j][e] - P[e];
+            *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * w + 4 * g4) = pack4bf(Vp[j]);
+            if constexpr (MODE == 1)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, Vp[j][e]);
+        }
+        __syncthreads();                                       // B(n)
+
+        Frag8 Bv[NTW][C / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) Bv[j][ks] = ldfrag<1, ST>(xv, LDC, BS * j, 32 * ks);
+        // S <- diag(e^G) S + Kb^T V'  (first: the next chunk waits for it)
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    S[i][j] = f32x4{S[i][j][0] * eg[i].x, S[i][j][1] * eg[i].y, S[i][j][2] * eg[i].z,
+                                    S[i][j][3] * eg[i].w};
+#pragma unroll
+                    for (int ks = 0; ks < C / 32; ++ks) S[i][j] = mma<1>(Akb[i][ks], Bv[j][ks], S[i][j]);
+                }
+            }
+        if (n + 1 < a.nc) put_state(stg((n + 1) % Lay::NSTG));
+        if constexpr (MODE == 0) {
+            // O = Qp S + Aqk V', row block w (the chunk-start state is in Bs)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                f32x4 O = zero4();
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) O = mma<1>(Aq[ks], Bs[j][ks], O);
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    if (ks <= w / 2) O = mma<1>(Aa[ks], Bv[j][ks], O);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) st1<ST>(sst + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, O[e]);
+            }
+        }
+        if (n + 1 < a.nc) preload(buf ^ 1);
+    }
+    __syncthreads();
+
+    if (MODE == 0 && a.s_final) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j)
+                    *reinterpret_cast<float4*>(a.s_final + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4) =
+                        make_float4(S[i][j][0], S[i][j][1], S[i][j][2], S[i][j][3]);
+    }
+}
+
+template <int D, int CS>
+struct Dh2Layout {
+    static constexpr int DC = D / CS, PS = 8;
+    static constexpr int LDR = D + PS, LDU = DC + PS, LDC = C + PS;
+    static constexpr int AQKT_OFF = 0;
+    static constexpr int KB_OFF = AQKT_OFF + C * LDC;
+    static constexpr int QPT_OFF = KB_OFF + C * LDR;
+    static constexpr int WT_OFF = QPT_OFF + D * LDC;
+    static constexpr int DOT_OFF = WT_OFF + D * LDC;              // dO^T of the owned columns [DC][LDC]
+    static constexpr int SET_ELEMS = DOT_OFF + DC * LDC;
+    static constexpr int EG_BYTE = SET_ELEMS * 2;
+    static constexpr int SET_BYTES = (EG_BYTE + D * 4 + 15) & ~15;
+    static constexpr int XS_OFF = 2 * SET_BYTES;                 // dS^T  [DC][LDR]
+    static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;         // -dV'^T [DC][LDC]
+    static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
+    static constexpr int STG_ELEMS = D * LDU + C * LDU;          // dh, dV'
+    static constexpr int STG_BYTES = (STG_ELEMS * 2 + 15) & ~15;
+    static constexpr int NSTG = 3;                              // staging tiles, by step % 3
+    static constexpr int BYTES = STG_OFF + NSTG * STG_BYTES;
+    static_assert(BYTES <= 160 * 1024, "reverse recurrence LDS");
+};
+
+template <int D, int CS>
+struct Dh2Slabs {
+    static constexpr int DC = D / CS;
+    Tile<uint16_t, C, C> AqkT;
+    Tile<uint16_t, C, D> Kb;
+    Tile<uint16_t, D, C> QpT, WT;
+    Tile<uint16_t, C, DC> dO;
+    Tile<float, 1, D> eG;
+};
+
+// Reverse state recurrence, same roles and barriers as kda_recur2_kernel:
+//   compute: [A] dV' = Aqk^T dO + Kb dS (row block w), write -dV'^T [B]
+//            dS <- diag(e^G) dS + Qp^T dO - W^T dV', write dS^T (and dS, the
+//            chunk-end adjoint, to staging) for the next chunk
+//   memory:  [A] flush [B] commit / load (dO lands transposed: dO^T[col][t])
+template <int D, int CS>
+__global__ __launch_bounds__(512) void kda_dh2_kernel(const DhArgs a) {
+    using ST = uint16_t;
+    using Lay = Dh2Layout<D, CS>;
+    using Slabs = Dh2Slabs<D, CS>;
+    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4;
+    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
+    __shared__ __align__(16) unsigned char smem[Lay::BYTES];
+
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lb = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    auto set = [&](int buf) __attribute__((always_inline)) { return reinterpret_cast<ST*>(smem + buf * Lay::SET_BYTES); };
+    auto seg = [&](int buf) __attribute__((always_inline)) { return reinterpret_cast<float*>(smem + buf * Lay::SET_BYTES + Lay::EG_BYTE); };
+    auto stg = [&](int sb) __attribute__((always_inline)) { return reinterpret_cast<ST*>(smem + Lay::STG_OFF + sb * Lay::STG_BYTES); };
+    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
+    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
+
+    if (wv >= 4) {
+        // ---------------- memory waves ----------------
+        const int mt = tid - 256;
+        auto issue = [&](int n, Slabs& p) __attribute__((always_inline)) {
+            const size_t ch = (size_t)bh * a.nc + n;
+            const int t0 = n * C, valid = min(C, a.T - t0);
+            p.AqkT.load_at(mt, static_cast<const ST*>(a.AqkT) + ch * C * C, C);
+            p.Kb.load_at(mt, static_cast<const ST*>(a.Kb) + ch * C * D, D);
+            p.QpT.load_at(mt, static_cast<const ST*>(a.QpT) + ch * C * D, C);
+            p.WT.load_at(mt, static_cast<const ST*>(a.WT) + ch * C * D, C);
+            p.eG.load_at(mt, a.eG + ch * D, D);
+            p.dO.load_at(mt, static_cast<const ST*>(a.dout) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
+                         (size_t)a.H * D, valid);
+        };
+        auto commit = [&](int buf, const Slabs& p) __attribute__((always_inline)) {
+            p.AqkT.store_at(mt, set(buf) + Lay::AQKT_OFF, LDC);
+            p.Kb.store_at(mt, set(buf) + Lay::KB_OFF, LDR);
+            p.QpT.store_at(mt, set(buf) + Lay::QPT_OFF, LDC);
+            p.WT.store_at(mt, set(buf) + Lay::WT_OFF, LDC);
+            p.eG.store_at(mt, seg(buf), D);
+            ST* dot = set(buf) + Lay::DOT_OFF;
+            constexpr int EPV = 8, VPR = DC / EPV, NV = C * VPR;
+#pragma unroll
+            for (int i = 0; i < Tile<ST, C, DC>::PER; ++i) {
+                const int v = mt + 256 * i;
+                if (NV % 256 == 0 || v < NV) {
+                    const int t = v / VPR, c = (v - t * VPR) * EPV;
+                    const uint4 x = p.dO.get(i);
+                    const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dot[(c + 2 * e) * LDC + t] = (ST)(u[e] & 0xffffu);
+                        dot[(c + 2 * e + 1) * LDC + t] = (ST)(u[e] >> 16);
+                    }
+                }
+            }
+        };
+        auto flush = [&](int it, int n) __attribute__((always_inline)) {
+            const ST* sst = stg(it % Lay::NSTG);
+            const size_t ch = (size_t)bh * a.nc + n;
+            tile_out_at<ST, D, DC>(mt, sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
+            tile_out_at<ST, C, DC>(mt, sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
+        };
+        // Loop step k handles chunk nc-1-k; step k's slabs live in register set
+        // k % 3 from their load (three steps ahead) to their commit into LDS set
+        // k & 1 (one step ahead).  Unrolled three times, as in kda_recur2_kernel.
+        Slabs p0, p1, p2;
+        const int nc = a.nc;
+        issue(nc - 1, p0);
+        if (nc > 1) issue(nc - 2, p1);
+        if (nc > 2) issue(nc - 3, p2);
+        commit(0, p0);
+        if (nc > 3) issue(nc - 4, p0);
+        __syncthreads();                                       // P: step 0 committed
+        auto step = [&](int it, Slabs& p) __attribute__((always_inline)) {   // p holds step it+1
+            const int n = nc - 1 - it;
+            __syncthreads();                                   // A(it)
+            if (it + 1 < nc) commit((it + 1) & 1, p);
+            __syncthreads();                                   // B(it): step it+1 committed
+            if (it > 0) flush(it - 1, n + 1);
+            if (it + 4 < nc) issue(nc - 1 - (it + 4), p);
+        };
+        for (int it = 0; it < nc; it += 3) {
+            step(it, p1);
+            if (it + 1 < nc) step(it + 1, p2);
+            if (it + 2 < nc) step(it + 2, p0);
+        }
+        __syncthreads();
+        flush(nc - 1, 0);
+        return;
+    }
+
+    // ---------------- compute waves ----------------
+    const int w = wv, l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    int mt[MT];
+    bool own[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        mt[i] = w + 4 * i;
+        own[i] = mt[i] < NT;
+    }
+    f32x4 dS[MT][NTW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            dS[i][j] = zero4();
+            if (own[i] && a.dsf) {
+                const float4 x = *reinterpret_cast<const float4*>(
+                    a.dsf + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4);
+                dS[i][j] = f32x4{x.x, x.y, x.z, x.w};
+            }
+        }
+    // dS^T for the B operands, dS (the chunk-end adjoint) to staging
+    auto put_state = [&](ST* sst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(dS[i][j]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, dS[i][j][e]);
+                }
+    };
+    put_state(stg(0));
+
+    Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
+    float4 eg[MT];
+    auto preload = [&](int buf) __attribute__((always_inline)) {
+        const ST* sAqkT = set(buf) + Lay::AQKT_OFF;
+        const ST* sKb = set(buf) + Lay::KB_OFF;
+        const ST* sQpT = set(buf) + Lay::QPT_OFF;
+        const ST* sWT = set(buf) + Lay::WT_OFF;
+        const ST* sdOT = set(buf) + Lay::DOT_OFF;
+        const float* seG = seg(buf);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            if (ks >= w / 2) Aat[ks] = ldfrag<1, ST>(sAqkT, LDC, BS * w, 32 * ks);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) Akb[ks] = ldfrag<1, ST>(sKb, LDR, BS * w, 32 * ks);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) Bo[j][ks] = ldfrag<1, ST>(sdOT, LDC, BS * j, 32 * ks);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) {
+                    Aqt[i][ks] = ldfrag<1, ST>(sQpT, LDC, BS * mt[i], 32 * ks);
+                    Awt[i][ks] = ldfrag<1, ST>(sWT, LDC, BS * mt[i], 32 * ks);
+                }
+                eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
+            }
+    };
+    __syncthreads();                                           // P
+    preload(0);
+
+    for (int it = 0; it < a.nc; ++it) {
+        const int n = a.nc - 1 - it;
+        const int buf = it & 1;
+        ST* sst = stg(it % Lay::NSTG);
+        __syncthreads();                                       // A(it)
+
+        Frag8 Bs[NTW][D / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, BS * j, 32 * ks);
+        // dV' = Aqk^T dO + Kb dS, row block w
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            f32x4 dV = zero4();
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (ks >= w / 2) dV = mma<1>(Aat[ks], Bo[j][ks], dV);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) dV = mma<1>(Akb[ks], Bs[j][ks], dV);
+            *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * w + 4 * g4) = pack4bf(negacc(dV));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, dV[e]);
+        }
+        __syncthreads();                                       // B(it)
+
+        Frag8 Bvn[NTW][C / 32];    // -dV'
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) Bvn[j][ks] = ldfrag<1, ST>(xv, LDC, BS * j, 32 * ks);
+        // dS <- diag(e^G) dS + Qp^T dO - W^T dV'
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    dS[i][j] = f32x4{dS[i][j][0] * eg[i].x, dS[i][j][1] * eg[i].y, dS[i][j][2] * eg[i].z,
+                                     dS[i][j][3] * eg[i].w};
+#pragma unroll
+                    for (int ks = 0; ks < C / 32; ++ks) {
+                        dS[i][j] = mma<1>(Awt[i][ks], Bvn[j][ks], dS[i][j]);
+                        dS[i][j] = mma<1>(Aqt[i][ks], Bo[j][ks], dS[i][j]);
+                    }
+                }
+            }
+        if (n > 0) {
+            put_state(stg((it + 1) % Lay::NSTG));
+            preload(buf ^ 1);
+        }
+    }
+    __syncthreads();
+
+    if (a.ds0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j)
+                    *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4) =
+                        make_float4(dS[i][j][0], dS[i][j][1], dS[i][j][2], dS[i][j][3]);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// bf16 recurrences, row split, LDS-DMA fed (kda_recur3_kernel / kda_dh3_kernel).
+//
+// CS workgroups per (batch, head) own DC = D / CS state columns each.  Wave w
+// owns row block w of the chunk's [C][DC] tiles and state row blocks w, w + 4.
+// The chunk slabs reach LDS by DMA (no registers, no commit step) into NS
+// swizzled LDS sets, NS chunks ahead; each chunk's A operands are read into
+// registers one chunk ahead, so after a barrier only the exchanged state / V'
+// fragments are read.  Per chunk n:
+//   A(n)  flush chunk n-1's staged outputs; DMA chunk n+NS into set n % NS;
+//         V' = U - W S (row block w); write V'^T; wait for chunk n+1's DMA
+//   B(n)  S <- diag(e^G) S + Kb^T V' (own state rows); write S^T for chunk n+1;
+//         O = Qp S + Aqk V' -> staging; read chunk n+1's A operands
+// Barriers are lds_barrier(): DMA stays in flight across them, and each wave
+// waits with an explicit vmcnt for exactly the DMA it needs.
+// ----------------------------------------------------------------------------
+template <int D, int MODE, int CS>
+struct Recur3Layout {
+    static constexpr int DC = D / CS, NS = (D >= 128) ? 2 : 3;
+    static constexpr int RB_W = 2 * D, RB_U = 2 * DC, RB_C = 2 * C;          // swizzled row bytes
+    static constexpr int W_OFF = 0;                                           // [C][D]
+    static constexpr int U_OFF = W_OFF + C * RB_W;                            // [C][DC]
+    static constexpr int QP_OFF = U_OFF + C * RB_U;                           // [C][D]   (MODE 0)
+    static constexpr int KBT_OFF = QP_OFF + (MODE == 0 ? C * RB_W : 0);        // [D][C]
+    static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                        // [C][C]   (MODE 0)
+    static constexpr int EG_OFF = AQK_OFF + (MODE == 0 ? C * RB_C : 0);        // [D] fp32
+    static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
+    static constexpr int PS = 8, LDR = D + PS, LDU = DC + PS, LDC = C + PS;
+    // exchange and staging live in a __shared__ array of their own
+    static constexpr int XS_OFF = 0;                                          // S^T  [DC][LDR] bf16
+    static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;                      // V'^T [DC][LDC] bf16
+    static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
+    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : D * LDU + C * LDU;   // O | h, V'
+    static constexpr int STG_BYTES = (STG_ELEMS * 2 + 15) & ~15;
+    static constexpr int NSTG = (MODE == 0) ? 2 : 3;
+    static constexpr int XBYTES = STG_OFF + NSTG * STG_BYTES;
+    static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "recurrence LDS");
+    // DMA wave-instructions per wave per chunk
+    static constexpr int L = DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_U, 4>::COUNT + DmaTile<D, RB_C, 4>::COUNT +
+                             (MODE == 0 ? DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_C, 4>::COUNT : 0) + 1;
+};
+
+// vmcnt wait: all but the last `k` chunks' DMA (L instructions each) complete
+template <int L>
+__device__ __forceinline__ void dma_wait_chunks(int k) {
+    if (k >= 2) dma_wait<2 * L>();
+    else if (k == 1) dma_wait<L>();
+    else dma_wait<0>();
+}
+
+template <int D, int MODE, int CS>
+__global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
+    using ST = uint16_t;
+    using Lay = Recur3Layout<D, MODE, CS>;
+    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4, NS = Lay::NS;
+    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
+    constexpr int RB_W = Lay::RB_W, RB_U = Lay::RB_U, RB_C = Lay::RB_C;
+    __shared__ __align__(1024) char set0[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set1[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set2[NS == 3 ? Lay::SET_BYTES : 16];
+    __shared__ __align__(16) char smem[Lay::XBYTES];
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    const int lb = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int nc = a.nc;
+    const char* gW = static_cast<const char*>(a.W);
+    const char* gU = static_cast<const char*>(a.U);
+    const char* gQp = static_cast<const char*>(a.Qp);
+    const char* gKbT = static_cast<const char*>(a.KbT);
+    const char* gAqk = static_cast<const char*>(a.Aqk);
+    const char* gEg = reinterpret_cast<const char*>(a.eG);
+
+    auto stg = [&](int c) __attribute__((always_inline)) {
+        return reinterpret_cast<ST*>(smem + Lay::STG_OFF + (c % Lay::NSTG) * Lay::STG_BYTES);
+    };
+    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
+    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
+
+    // chunk c's slabs -> LDS set sb = set (c % NS) (Lay::L instructions per wave)
+    using TW = DmaTile<C, RB_W, 4>;
+    using TU = DmaTile<C, RB_U, 4>;
+    using TK = DmaTile<D, RB_C, 4>;
+    using TA = DmaTile<C, RB_C, 4>;
+    uint32_t oW[TW::COUNT], oU[TU::COUNT], oK[TK::COUNT], oA[TA::COUNT];
+    TW::offsets(oW, RB_W, w, l);
+    TU::offsets(oU, (size_t)D * 2, w, l);
+    TK::offsets(oK, RB_C, w, l);
+    TA::offsets(oA, RB_C, w, l);
+    const uint32_t oE = (uint32_t)((D / 4) * 4 * w + 16 * (l < D / 16 ? l : 0));
+    auto dma_chunk = [&](int c, char* sb) __attribute__((always_inline)) {
+        const size_t ch = (size_t)bh * nc + c;
+        TW::issue_s(gW + ch * C * D * 2, oW, sb + Lay::W_OFF, w);
+        TU::issue_s(gU + (ch * C * D + c0) * 2, oU, sb + Lay::U_OFF, w);
+        TK::issue_s(gKbT + ch * C * D * 2, oK, sb + Lay::KBT_OFF, w);
+        if constexpr (MODE == 0) {
+            TW::issue_s(gQp + ch * C * D * 2, oW, sb + Lay::QP_OFF, w);
+            TA::issue_s(gAqk + ch * C * C * 2, oA, sb + Lay::AQK_OFF, w);
+        }
+        // e^G: D floats, D / 16 lanes of 16 bytes per wave
+        if (l < D / 16) dma16_s(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + D * w);
+    };
+    auto flush = [&](int n) __attribute__((always_inline)) {
+        const ST* sst = stg(n);
+        if constexpr (MODE == 0) {
+            const int t0 = n * C, valid = min(C, a.T - t0);
+            tile_out<ST, C, DC>(sst, LDU, static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
+                                (size_t)a.H * D, valid);
+        } else {
+            const size_t ch = (size_t)bh * nc + n;
+            tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
+            tile_out<ST, C, DC>(sst + D * LDU, LDU, static_cast<ST*>(a.Vp) + ch * C * D + c0, D, C);
+        }
+    };
+
+    int mt[MT];
+    bool own[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        mt[i] = w + 4 * i;
+        own[i] = mt[i] < NT;
+    }
+    f32x4 S[MT][NTW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            S[i][j] = zero4();
+            if (own[i] && a.s0) {
+                const float4 x = *reinterpret_cast<const float4*>(
+                    a.s0 + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4);
+                S[i][j] = f32x4{x.x, x.y, x.z, x.w};
+            }
+        }
+    // S^T for the B operands (and, for the backward, the chunk-start state)
+    auto put_state = [&](ST* sst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(S[i][j]);
+                    if constexpr (MODE == 1)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
+                }
+    };
+
+    // one chunk's A operands, read ahead from its LDS set
+    Frag8 Aw[D / 32], Aq[D / 32], Aa[2], Akb[MT][C / 32];
+    f32x4 Uv[NTW];
+    float4 eg[MT];
+    auto preload = [&](const char* sb) __attribute__((always_inline)) {
+        const ST* sW = reinterpret_cast<const ST*>(sb + Lay::W_OFF);
+        const ST* sU = reinterpret_cast<const ST*>(sb + Lay::U_OFF);
+        const ST* sKbT = reinterpret_cast<const ST*>(sb + Lay::KBT_OFF);
+        const float* seG = reinterpret_cast<const float*>(sb + Lay::EG_OFF);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) Aw[ks] = ldfrag_sw<RB_W>(sW, BS * w, 32 * ks);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Uv[j][e] = ld_sw<RB_U>(sU, BS * w + 4 * g4 + e, BS * j + r16);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) Akb[i][ks] = ldfrag_sw<RB_C>(sKbT, BS * mt[i], 32 * ks);
+                eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
+            }
+        if constexpr (MODE == 0) {
+            const ST* sQp = reinterpret_cast<const ST*>(sb + Lay::QP_OFF);
+            const ST* sAqk = reinterpret_cast<const ST*>(sb + Lay::AQK_OFF);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Aq[ks] = ldfrag_sw<RB_W>(sQp, BS * w, 32 * ks);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (ks <= w / 2) Aa[ks] = ldfrag_sw<RB_C>(sAqk, BS * w, 32 * ks);
+        }
+    };
+
+    // prologue: chunks 0 .. NS-1 in flight, chunk 0 landed and read
+    put_state(stg(0));
+    dma_chunk(0, set0);
+    if (nc > 1) dma_chunk(1, set1);
+    if (NS == 3 && nc > 2) dma_chunk(2, set2);
+    dma_wait_chunks<Lay::L>(min(NS, nc) - 1);
+    lds_barrier();
+    preload(set0);
+
+    // chunk n: DMA chunk n+NS into sdma (set n % NS), read chunk n+1's A
+    // operands from snext (set (n+1) % NS)
+    auto step = [&](int n, char* sdma, const char* snext) __attribute__((always_inline)) {
+        ST* sst = stg(n);
+        lds_barrier();                                          // A(n)
+        if (n > 0) flush(n - 1);
+        if (n + NS < nc) dma_chunk(n + NS, sdma);
+
+        Frag8 Bs[NTW][D / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, BS * j, 32 * ks);
+        // V' = U - W S, row block w
+        f32x4 Vp[NTW];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            f32x4 P = zero4();
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) P = mma<1>(Aw[ks], Bs[j][ks], P);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Vp[j][e] = Uv[j][e] - P[e];
+            *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * w + 4 * g4) = pack4bf(Vp[j]);
+            if constexpr (MODE == 1)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, Vp[j][e]);
+        }
+        // chunk n+1's DMA (this wave's share) complete; later chunks may stay in flight
+        dma_wait_chunks<Lay::L>(min(nc - 1, n + NS) - (n + 1));
+        lds_barrier();                                          // B(n)
+
+        Frag8 Bv[NTW][C / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) Bv[j][ks] = ldfrag<1, ST>(xv, LDC, BS * j, 32 * ks);
+        // S <- diag(e^G) S + Kb^T V'
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    S[i][j] = f32x4{S[i][j][0] * eg[i].x, S[i][j][1] * eg[i].y, S[i][j][2] * eg[i].z,
+                                    S[i][j][3] * eg[i].w};
+#pragma unroll
+                    for (int ks = 0; ks < C / 32; ++ks) S[i][j] = mma<1>(Akb[i][ks], Bv[j][ks], S[i][j]);
+                }
+            }
+        if (n + 1 < nc) put_state(stg(n + 1));
+        if constexpr (MODE == 0) {
+            // O = Qp S + Aqk V', row block w (the chunk-start state is in Bs)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                f32x4 O = zero4();
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) O = mma<1>(Aq[ks], Bs[j][ks], O);
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    if (ks <= w / 2) O = mma<1>(Aa[ks], Bv[j][ks], O);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) st1<ST>(sst + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, O[e]);
+            }
+        }
+        if (n + 1 < nc) preload(snext);
+    };
+    // unrolled NS times so that every set is named statically
+    for (int n = 0; n < nc; n += NS) {
+        step(n, set0, set1);
+        if (n + 1 < nc) step(n + 1, set1, NS == 3 ? set2 : set0);
+        if (NS == 3 && n + 2 < nc) step(n + 2, set2, set0);
+    }
+    lds_barrier();
+    flush(nc - 1);
+
+    if (MODE == 0 && a.s_final) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j)
+                    *reinterpret_cast<float4*>(a.s_final + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4) =
+                        make_float4(S[i][j][0], S[i][j][1], S[i][j][2], S[i][j][3]);
+    }
+}
+
+template <int D, int CS>
+struct Dh3Layout {
+    static constexpr int DC = D / CS, NS = 3;
+    static constexpr int RB_D = 2 * D, RB_C = 2 * C, RB_U = 2 * DC;
+    static constexpr int AQKT_OFF = 0;                                        // [C][C]
+    static constexpr int KB_OFF = AQKT_OFF + C * RB_C;                        // [C][D]
+    static constexpr int QPT_OFF = KB_OFF + C * RB_D;                         // [D][C]
+    static constexpr int WT_OFF = QPT_OFF + D * RB_C;                         // [D][C]
+    static constexpr int DO_OFF = WT_OFF + D * RB_C;                          // [C][DC] (t, own columns)
+    static constexpr int EG_OFF = DO_OFF + C * RB_U;                          // [D] fp32
+    static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
+    static constexpr int PS = 8, LDR = D + PS, LDU = DC + PS, LDC = C + PS;
+    static constexpr int XS_OFF = 0;                                          // dS^T   [DC][LDR]
+    static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;                      // -dV'^T [DC][LDC]
+    static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
+    static constexpr int STG_ELEMS = D * LDU + C * LDU;                       // dh, dV'
+    static constexpr int STG_BYTES = (STG_ELEMS * 2 + 15) & ~15;
+    static constexpr int NSTG = 3;
+    static constexpr int XBYTES = STG_OFF + NSTG * STG_BYTES;
+    static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "reverse recurrence LDS");
+    static constexpr int L = DmaTile<C, RB_C, 4>::COUNT + DmaTile<C, RB_D, 4>::COUNT + 2 * DmaTile<D, RB_C, 4>::COUNT +
+                             DmaTile<C, RB_U, 4>::COUNT + 1;
+};
+
+// Reverse state recurrence, same pipeline as kda_recur3_kernel, loop step k on
+// chunk nc-1-k:
+//   A(k)  flush step k-1; DMA step k+NS; dV' = Aqk^T dO + Kb dS (row block w);
+//         write -dV'^T and dV'; wait for step k+1's DMA
+//   B(k)  dS <- diag(e^G) dS + Qp^T dO - W^T dV'; write dS^T and dS (the next
+//         chunk's chunk-end adjoint); read step k+1's A operands
+template <int D, int CS>
+__global__ __launch_bounds__(256) void kda_dh3_kernel(const DhArgs a) {
+    using ST = uint16_t;
+    using Lay = Dh3Layout<D, CS>;
+    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4, NS = Lay::NS;
+    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
+    constexpr int RB_D = Lay::RB_D, RB_C = Lay::RB_C, RB_U = Lay::RB_U;
+    __shared__ __align__(1024) char set0[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set1[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set2[Lay::SET_BYTES];
+    __shared__ __align__(16) char smem[Lay::XBYTES];
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    const int lb = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int nc = a.nc;
+    const char* gAqkT = static_cast<const char*>(a.AqkT);
+    const char* gKb = static_cast<const char*>(a.Kb);
+    const char* gQpT = static_cast<const char*>(a.QpT);
+    const char* gWT = static_cast<const char*>(a.WT);
+    const char* gdO = static_cast<const char*>(a.dout);
+    const char* gEg = reinterpret_cast<const char*>(a.eG);
+
+    auto stg = [&](int k) __attribute__((always_inline)) {
+        return reinterpret_cast<ST*>(smem + Lay::STG_OFF + (k % Lay::NSTG) * Lay::STG_BYTES);
+    };
+    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
+    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
+
+    // step k's slabs (chunk nc-1-k) -> LDS set sb = set (k % NS)
+    using TA = DmaTile<C, RB_C, 4>;
+    using TB = DmaTile<C, RB_D, 4>;
+    using TQ = DmaTile<D, RB_C, 4>;
+    using TO = DmaTile<C, RB_U, 4>;
+    uint32_t oA[TA::COUNT], oB[TB::COUNT], oQ[TQ::COUNT], oO[TO::COUNT];
+    TA::offsets(oA, RB_C, w, l);
+    TB::offsets(oB, RB_D, w, l);
+    TQ::offsets(oQ, RB_C, w, l);
+    TO::offsets(oO, (size_t)a.H * D * 2, w, l);
+    const uint32_t oE = (uint32_t)((D / 4) * 4 * w + 16 * (l < D / 16 ? l : 0));
+    auto dma_step = [&](int k, char* sb) __attribute__((always_inline)) {
+        const int n = nc - 1 - k;
+        const size_t ch = (size_t)bh * nc + n;
+        const int t0 = n * C, valid = min(C, a.T - t0);
+        TA::issue_s(gAqkT + ch * C * C * 2, oA, sb + Lay::AQKT_OFF, w);
+        TB::issue_s(gKb + ch * C * D * 2, oB, sb + Lay::KB_OFF, w);
+        TQ::issue_s(gQpT + ch * C * D * 2, oQ, sb + Lay::QPT_OFF, w);
+        TQ::issue_s(gWT + ch * C * D * 2, oQ, sb + Lay::WT_OFF, w);
+        const char* gdo = gdO + ((((size_t)b * a.T + t0) * a.H + h) * D + c0) * 2;
+        if (valid == C) TO::issue_s(gdo, oO, sb + Lay::DO_OFF, w);
+        else TO::issue(gdo, (size_t)a.H * D * 2, sb + Lay::DO_OFF, w, l, valid);
+        if (l < D / 16) dma16_s(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + D * w);
+    };
+    auto flush = [&](int k) __attribute__((always_inline)) {
+        const ST* sst = stg(k);
+        const size_t ch = (size_t)bh * nc + (nc - 1 - k);
+        tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
+        tile_out<ST, C, DC>(sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
+    };
+
+    int mt[MT];
+    bool own[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        mt[i] = w + 4 * i;
+        own[i] = mt[i] < NT;
+    }
+    f32x4 dS[MT][NTW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            dS[i][j] = zero4();
+            if (own[i] && a.dsf) {
+                const float4 x = *reinterpret_cast<const float4*>(
+                    a.dsf + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4);
+                dS[i][j] = f32x4{x.x, x.y, x.z, x.w};
+            }
+        }
+    auto put_state = [&](ST* sst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(dS[i][j]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, dS[i][j][e]);
+                }
+    };
+
+    Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
+    float4 eg[MT];
+    auto preload = [&](const char* sb) __attribute__((always_inline)) {
+        const ST* sAqkT = reinterpret_cast<const ST*>(sb + Lay::AQKT_OFF);
+        const ST* sKb = reinterpret_cast<const ST*>(sb + Lay::KB_OFF);
+        const ST* sQpT = reinterpret_cast<const ST*>(sb + Lay::QPT_OFF);
+        const ST* sWT = reinterpret_cast<const ST*>(sb + Lay::WT_OFF);
+        const ST* sdO = reinterpret_cast<const ST*>(sb + Lay::DO_OFF);
+        const float* seG = reinterpret_cast<const float*>(sb + Lay::EG_OFF);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            if (ks >= w / 2) Aat[ks] = ldfrag_sw<RB_C>(sAqkT, BS * w, 32 * ks);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) Akb[ks] = ldfrag_sw<RB_D>(sKb, BS * w, 32 * ks);
+        // dO as B operand (k = t, n = column): gathered from its row-major tile
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) {
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = ld_sw<RB_U>(sdO, 32 * ks + 4 * g4 + e, BS * j + r16);
+                    v[4 + e] = ld_sw<RB_U>(sdO, 32 * ks + 16 + 4 * g4 + e, BS * j + r16);
+                }
+                Bo[j][ks] = frag_from_f32<1>(v);
+            }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) {
+                    Aqt[i][ks] = ldfrag_sw<RB_C>(sQpT, BS * mt[i], 32 * ks);
+                    Awt[i][ks] = ldfrag_sw<RB_C>(sWT, BS * mt[i], 32 * ks);
+                }
+                eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
+            }
+    };
+
+    // prologue: steps 0 .. NS-1 in flight; the last chunk's rows past T are
+    // not loaded, so they are zeroed in LDS
+    put_state(stg(0));
+    dma_step(0, set0);
+    if (nc > 1) dma_step(1, set1);
+    if (nc > 2) dma_step(2, set2);
+    {
+        const int valid = a.T - (nc - 1) * C;
+        if (valid < C) {
+            char* dO0 = set0 + Lay::DO_OFF;
+            for (int idx = tid; idx < C * RB_U / 16; idx += 256)
+                if (idx / (RB_U / 16) >= valid) *reinterpret_cast<uint4*>(dO0 + 16 * idx) = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    dma_wait_chunks<Lay::L>(min(NS, nc) - 1);
+    lds_barrier();
+    preload(set0);
+
+    auto step = [&](int k, char* sdma, const char* snext) __attribute__((always_inline)) {
+        ST* sst = stg(k);
+        lds_barrier();                                          // A(k)
+        if (k > 0) flush(k - 1);
+        if (k + NS < nc) dma_step(k + NS, sdma);
+
+        Frag8 Bs[NTW][D / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, BS * j, 32 * ks);
+        // dV' = Aqk^T dO + Kb dS, row block w
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            f32x4 dV = zero4();
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (ks >= w / 2) dV = mma<1>(Aat[ks], Bo[j][ks], dV);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) dV = mma<1>(Akb[ks], Bs[j][ks], dV);
+            *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * w + 4 * g4) = pack4bf(negacc(dV));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, dV[e]);
+        }
+        dma_wait_chunks<Lay::L>(min(nc - 1, k + NS) - (k + 1));
+        lds_barrier();                                          // B(k)
+
+        Frag8 Bvn[NTW][C / 32];    // -dV'
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) Bvn[j][ks] = ldfrag<1, ST>(xv, LDC, BS * j, 32 * ks);
+        // dS <- diag(e^G) dS + Qp^T dO - W^T dV'
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    dS[i][j] = f32x4{dS[i][j][0] * eg[i].x, dS[i][j][1] * eg[i].y, dS[i][j][2] * eg[i].z,
+                                     dS[i][j][3] * eg[i].w};
+#pragma unroll
+                    for (int ks = 0; ks < C / 32; ++ks) {
+                        dS[i][j] = mma<1>(Awt[i][ks], Bvn[j][ks], dS[i][j]);
+                        dS[i][j] = mma<1>(Aqt[i][ks], Bo[j][ks], dS[i][j]);
+                    }
+                }
+            }
+        if (k + 1 < nc) {
+            put_state(stg(k + 1));
+            preload(snext);
+        }
+    };
+    for (int k = 0; k < nc; k += 3) {
+        step(k, set0, set1);
+        if (k + 1 < nc) step(k + 1, set1, set2);
+        if (k + 2 < nc) step(k + 2, set2, set0);
+    }
+    lds_barrier();
+    flush(nc - 1);
+
+    if (a.ds0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j)
+                    *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4) =
+                        make_float4(dS[i][j][0], dS[i][j][1], dS[i][j][2], dS[i][j][3]);
+    }
+}
+
+// ----------------------------------------------------------------------------
 // launchers
 // ----------------------------------------------------------------------------
 // D = 128 splits the state's dv columns over two workgroups per (batch, head)
+// bf16: row-split kernels with CS2 workgroups per (batch, head); fp32: one
+// workgroup per (batch, head), D = 128 split over two.
+template <int D> struct RowSplit { static constexpr int CS = (D >= 128) ? 4 : 2; };
+
 template <int D, typename ST, int MODE>
 static hipError_t launch_recur_t(const RecurArgs& a, hipStream_t st) {
-    constexpr int PREC = std::is_same<ST, float>::value ? 3 : 1;
-    constexpr int CS = (D >= 128) ? 2 : 1;
-    hipLaunchKernelGGL((kda_recur_kernel<D, ST, PREC, MODE, CS>), dim3(a.BH * CS), dim3(256), 0, st, a);
+    if constexpr (std::is_same<ST, uint16_t>::value && D >= 64) {
+        constexpr int CS2 = RowSplit<D>::CS;
+        hipLaunchKernelGGL((kda_recur3_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(256), 0, st, a);
+    } else if constexpr (std::is_same<ST, uint16_t>::value) {
+        constexpr int CS2 = RowSplit<D>::CS;
+        hipLaunchKernelGGL((kda_recur2_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
+    } else {
+        constexpr int CS = (D >= 128) ? 2 : 1;
+        hipLaunchKernelGGL((kda_recur_kernel<D, ST, 3, MODE, CS>), dim3(a.BH * CS), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
 template <int D, typename ST>
 static hipError_t launch_dh_t(const DhArgs& a, hipStream_t st) {
-    constexpr int PREC = std::is_same<ST, float>::value ? 3 : 1;
-    hipLaunchKernelGGL((kda_dh_kernel<D, ST, PREC>), dim3(a.BH), dim3(256), 0, st, a);
+    if constexpr (std::is_same<ST, uint16_t>::value && D >= 64) {
+        constexpr int CS2 = RowSplit<D>::CS;
+        hipLaunchKernelGGL((kda_dh3_kernel<D, CS2>), dim3(a.BH * CS2), dim3(256), 0, st, a);
+    } else if constexpr (std::is_same<ST, uint16_t>::value) {
+        constexpr int CS2 = RowSplit<D>::CS;
+        hipLaunchKernelGGL((kda_dh2_kernel<D, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((kda_dh_kernel<D, ST, 3>), dim3(a.BH), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
