@@ -828,6 +828,483 @@ __global__ __launch_bounds__(256) void kda_bwd_local2_kernel(const LocalArgs a) 
 }
 
 // ----------------------------------------------------------------------------
+// local adjoints, bf16 operands, 8 waves (two per SIMD, so each hides the
+// other's latencies).  Wave w owns channel tile ct = w % 4 and row half
+// rh = w / 4 (row blocks 2 rh, 2 rh + 1) of every per-(t, d) adjoint.
+//   phase 1  dQp, dKb, dW of the own rows; dA tiles over all waves
+//   phase 2  the transposed solve splits by right-hand side: the rh = 0 waves
+//            run the dW chain, the rh = 1 waves the dV' chain, each for its
+//            channel tile, through LDS (dR)
+//   phase 3  dL tiles over all waves; dbeta row sums
+//   phase 4  decay-masked adjoints: every wave computes exactly the
+//            contributions to its own rows (row blocks i of dK_l / dQ_l, and
+//            row blocks j of dK_r)
+//   phase 5  in-chunk reverse cumsum of dgamma: the two row halves meet
+//            through one LDS total per channel
+// LDS regions and their reuse are those of kda_bwd_local2_kernel.
+// ----------------------------------------------------------------------------
+template <int D, typename ST, typename TG, int PREC>
+__global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) {
+    using L = LocalSmem<D, ST>;
+    constexpr int NTH = 512, NT = D / BS, LDK = L::LDK, LDT = L::LDT, LDA = L::LDA, LDR = L::LDR;
+    __shared__ L sm;
+    __shared__ float xg[D];     // dgamma(C-1) partial of the rh = 0 waves
+    __shared__ float xt[D];     // dgamma column totals of the rh = 1 waves
+    auto& s = sm.s;
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
+              g4 = l >> 4;
+    const int ct = w & 3, rh = w >> 2;
+    const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int t0 = n * C, valid = min(C, a.T - t0);
+    const size_t rs = (size_t)a.H * D;
+    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
+    const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
+    const size_t cCD = (size_t)ch * C * D, cCC = (size_t)ch * C * C, cDD = (size_t)ch * D * D;
+
+    // ---------------- phase 0: one batch of loads ----------------
+    int flag = 0;
+    {
+        Tile<ST, C, D, NTH> tq, tk, tv, tdo, tW, tU, tVp, tdVp;
+        Tile<TG, C, D, NTH> tg;
+        Tile<ST, D, D, NTH> th, tdh;
+        Tile<float, C, C, NTH> takk;
+        Tile<float, NB * BS, BS, NTH> ttii;
+        tq.load(static_cast<const ST*>(a.q) + base, rs, valid);
+        tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
+        tv.load(static_cast<const ST*>(a.v) + base, rs, valid);
+        tdo.load(static_cast<const ST*>(a.dout) + base, rs, valid);
+        tg.load(static_cast<const TG*>(a.g) + base, rs, valid);
+        tW.load(static_cast<const ST*>(a.W) + cCD, D);
+        tU.load(static_cast<const ST*>(a.U) + cCD, D);
+        tVp.load(static_cast<const ST*>(a.Vp) + cCD, D);
+        tdVp.load(static_cast<const ST*>(a.dVp) + cCD, D);
+        th.load(static_cast<const ST*>(a.h) + cDD, D);
+        tdh.load(static_cast<const ST*>(a.dh) + cDD, D);
+        takk.load(a.Akk + cCC, C);
+        ttii.load(a.Tii + (size_t)ch * NB * BS * BS, BS);
+        const float bt = (tid < valid) ? ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)tid * a.H) : 0.f;
+        tq.store(&s.ql[0][0], LDK);
+        tk.store(&s.kr[0][0], LDK);
+        tv.store(&sm.rb.p2.v[0][0], LDK);
+        tdo.store(&sm.ra.p1.dO[0][0], LDK);
+        tW.store(&sm.W[0][0], LDK);
+        tU.store(&sm.U[0][0], LDK);
+        tVp.store(&sm.ra.p1.Vp[0][0], LDK);
+        tdVp.store(&sm.rb.p2.dVp[0][0], LDK);
+        th.store(&sm.ra.p1.h[0][0], LDK);
+        tdh.store(&sm.ra.p1.dh[0][0], LDK);
+        takk.store(&sm.akk[0][0], LDA);
+        ttii.store(&sm.tii[0][0][0], BS + 4);
+        using TGT = Tile<TG, C, D, NTH>;
+#pragma unroll
+        for (int i = 0; i < TGT::PER; ++i) {
+            const int vv = tid + NTH * i;
+            if (TGT::NV % NTH == 0 || vv < TGT::NV) {
+                const int row = vv / TGT::VPR, c = (vv - row * TGT::VPR) * TGT::EPV;
+                const Vec16<TG> x{tg.get(i)};
+#pragma unroll
+                for (int e = 0; e < TGT::EPV; ++e) {
+                    const float gv = x.get(e);
+                    s.g[row][c + e] = gv;
+                    if (!(gv <= 0.f)) flag = 1;
+                }
+            }
+        }
+        if (tid < C) {
+            s.beta[tid] = bt;
+            sm.dbeta[tid] = 0.f;
+        }
+    }
+    __syncthreads();
+    chunk_cumsum2<D, ST, NTH>(s);
+    const int unsafe = chunk_factors2<D, ST, PREC, NTH>(s, flag);
+
+    // per-lane values of the owned (t, d): rows t = 16 m + 4 g4 + e, m = 2 rh + mm, channel d
+    const bool own = ct < NT;
+    const int d = own ? ct * BS + r16 : 0;
+    constexpr int MB = NB / 2;
+    float kx[MB][4], qx[MB][4], el[MB][4], er[MB][4], eb[MB][4], erb[MB];
+    {
+        const float G = s.g[C - 1][d];
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm) {
+            const int m = 2 * rh + mm;
+            const float gr = s.g[BS * m][d];
+            erb[mm] = s.er[m][d];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * m + 4 * g4 + e;
+                const float gt = s.g[t][d];
+                kx[mm][e] = ld1<ST>(&s.kr[t][d]);
+                qx[mm][e] = ld1<ST>(&s.ql[t][d]);
+                el[mm][e] = kexp<PREC>(gt - gr);
+                er[mm][e] = unsafe ? 0.f : kexp<PREC>(gr - gt);
+                eb[mm][e] = kexp<PREC>(G - gt);
+            }
+        }
+    }
+    __syncthreads();
+    if (!unsafe) {
+        constexpr int EPV = 16 / (int)sizeof(ST), VPR = D / EPV;
+        for (int vv = tid; vv < C * VPR; vv += NTH) {
+            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, r = t & ~(BS - 1);
+            const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
+            const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
+            float okl[EPV], oql[EPV], okr[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const float x = s.g[t][c0 + e] - s.g[r][c0 + e];
+                const float e1 = kexp<PREC>(x), e2 = kexp<PREC>(-x);
+                okl[e] = kv.get(e) * e1;
+                oql[e] = qv.get(e) * e1;
+                okr[e] = kv.get(e) * e2;
+            }
+            store_vec<ST>(&s.kl[t][c0], okl);
+            store_vec<ST>(&s.ql[t][c0], oql);
+            store_vec<ST>(&s.kr[t][c0], okr);
+        }
+    }
+    __syncthreads();
+
+    f32x4 dqa[MB], dka[MB], dga[MB], dWt[MB];
+    float dgcol = 0.f, part = 0.f;
+
+    // ---------------- phase 1: products over dv ----------------
+    {
+        const ST* sdO = &sm.ra.p1.dO[0][0];
+        const ST* sVp = &sm.ra.p1.Vp[0][0];
+        const ST* sdVp = &sm.rb.p2.dVp[0][0];
+        const ST* sh = &sm.ra.p1.h[0][0];
+        const ST* sdh = &sm.ra.p1.dh[0][0];
+        if (own) {
+            Frag8 Ao[MB][D / 32], Av[MB][D / 32], Ad[MB][D / 32], Bh[D / 32], Bdh[D / 32];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                Bh[ks] = ldfrag<PREC, ST>(sh, LDK, BS * ct, 32 * ks);
+                Bdh[ks] = ldfrag<PREC, ST>(sdh, LDK, BS * ct, 32 * ks);
+#pragma unroll
+                for (int mm = 0; mm < MB; ++mm) {
+                    const int m = 2 * rh + mm;
+                    Ao[mm][ks] = ldfrag<PREC, ST>(sdO, LDK, BS * m, 32 * ks);
+                    Av[mm][ks] = ldfrag<PREC, ST>(sVp, LDK, BS * m, 32 * ks);
+                    Ad[mm][ks] = ldfrag<PREC, ST>(sdVp, LDK, BS * m, 32 * ks);
+                }
+            }
+            // state-decay term of dG (rh = 1 waves): e^G sum_col dh[d][col] h[d][col]
+            if (rh == 1) {
+#pragma unroll
+                for (int c = 0; c < D / 4; ++c) {
+                    const int cc = g4 * (D / 4) + c;
+                    part += ld1<ST>(sdh + d * LDK + cc) * ld1<ST>(sh + d * LDK + cc);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mm = 0; mm < MB; ++mm) {
+                f32x4 dQp = zero4(), dKb = zero4(), dW = zero4();
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) {
+                    dQp = mma<PREC>(Ao[mm][ks], Bh[ks], dQp);
+                    dKb = mma<PREC>(Av[mm][ks], Bdh[ks], dKb);
+                    dW = mma<PREC>(Ad[mm][ks], Bh[ks], dW);
+                }
+                dWt[mm] = negacc(dW);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float egt = erb[mm] * el[mm][e];                // e^{gamma_t}
+                    const float kbv = kx[mm][e] * eb[mm][e];              // Kb
+                    dqa[mm][e] = dQp[e] * egt;
+                    dka[mm][e] = dKb[e] * eb[mm][e];
+                    dga[mm][e] = dQp[e] * qx[mm][e] * egt - dKb[e] * kbv;
+                    dgcol += dKb[e] * kbv;
+                }
+            }
+            dgcol = sum4g(dgcol);
+            part = sum4g(part);
+            if (rh == 0 && g4 == 0) xg[d] = dgcol;
+        }
+        // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves
+        for (int tix = w; tix < 10; tix += 8) {
+            int i, j;
+            tile_ij(tix, i, j);
+            Frag8 A[D / 32], B[D / 32];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                A[ks] = ldfrag<PREC, ST>(sdO, LDK, BS * i, 32 * ks);
+                B[ks] = ldfrag<PREC, ST>(sVp, LDK, BS * j, 32 * ks);
+            }
+            f32x4 acc = zero4();
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) acc = mma<PREC>(A[ks], B[ks], acc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
+                st1<ST>(&sm.dA[t][sx], (sx <= t) ? acc[e] : 0.f);
+            }
+        }
+    }
+    __syncthreads();   // phase-1 operands (region A) are dead from here
+
+    // ---------------- phase 2: transposed WY solve, by right-hand side ----------------
+    // dW of the own rows -> dR[:, d]
+    if (own) {
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sm.ra.dR[BS * (2 * rh + mm) + 4 * g4 + e][d] = dWt[mm][e];
+    }
+    __syncthreads();
+    if (own) {
+        // rh = 0: Y = dW (from dR[:, d]), result in place; rh = 1: Y = dV', result in dR[:, D + d]
+        const int col = rh ? D + d : d;
+        const ST* sdVp = &sm.rb.p2.dVp[0][0];
+        f32x4 dRx[NB];
+#pragma unroll
+        for (int i = NB - 1; i >= 0; --i) {
+            f32x4 Y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * i + 4 * g4 + e;
+                Y[e] = rh ? ld1<ST>(sdVp + t * LDK + d) : sm.ra.dR[t][d];
+            }
+#pragma unroll
+            for (int j = i + 1; j < NB; ++j) {
+                // A[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a]
+                float av[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int rb = BS * j + 4 * g4 + e;
+                    av[e] = -s.beta[rb] * sm.akk[rb][BS * i + r16];
+                }
+                Y = mma4f<3>(frag4_from_f32<3>(av), accfrag4<3>(dRx[j]), Y);
+            }
+            float tv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tv[e] = sm.tii[i][4 * g4 + e][r16];     // A[a][b] = T_ii[b][a]
+            dRx[i] = mma4f<3>(frag4_from_f32<3>(tv), accfrag4<3>(Y), zero4());
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sm.ra.dR[BS * i + 4 * g4 + e][col] = dRx[i][e];
+        }
+    }
+    __syncthreads();
+    // contributions of dR to the own rows; dv = beta dR_v
+    f32x4 dvo[MB];
+    if (own) {
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * (2 * rh + mm) + 4 * g4 + e;
+                const float bt = s.beta[t], egt = erb[mm] * el[mm][e];
+                const float rk = sm.ra.dR[t][d];
+                dka[mm][e] += bt * egt * rk;
+                dga[mm][e] += rk * bt * egt * kx[mm][e];
+                dvo[mm][e] = bt * sm.ra.dR[t][D + d];
+            }
+    }
+    // dbeta, part 1: sum_d dV~[t][d] v[t][d] + dK~[t][d] e^{gamma_t} k[t][d]; 8 threads per row
+    {
+        const int t = tid >> 3, qd = tid & 7;
+        float acc = 0.f;
+        for (int dd = qd * (D / 8); dd < (qd + 1) * (D / 8); ++dd) {
+            const float egk = unsafe ? ld1<ST>(&s.kr[t][dd]) * kexp<PREC>(s.g[t][dd])
+                                     : ld1<ST>(&s.kl[t][dd]) * s.er[t / BS][dd];
+            acc += sm.ra.dR[t][D + dd] * ld1<ST>(&sm.rb.p2.v[t][dd]) + sm.ra.dR[t][dd] * egk;
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        if (qd == 0) sm.dbeta[t] = acc;
+    }
+    __syncthreads();   // v and dV' (region B) are dead from here
+
+    // ---------------- phase 3: dL = -tril(dR X^T, -1) ----------------
+    for (int tix = w; tix < 10; tix += 8) {
+        int i, j;
+        tile_ij(tix, i, j);
+        Frag8 A[2 * D / 32], B[2 * D / 32];
+#pragma unroll
+        for (int ks = 0; ks < 2 * D / 32; ++ks) {
+            A[ks] = ldfrag<3, float>(&sm.ra.dR[0][0], LDR, BS * i, 32 * ks);
+            B[ks] = (32 * ks < D) ? ldfrag<3, ST>(&sm.W[0][0], LDK, BS * j, 32 * ks)
+                                  : ldfrag<3, ST>(&sm.U[0][0], LDK, BS * j, 32 * ks - D);
+        }
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 2 * D / 32; ++ks) acc = mma<3>(A[ks], B[ks], acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
+            sm.rb.dL[t][sx] = (sx < t) ? -acc[e] : 0.f;
+        }
+    }
+    __syncthreads();
+    // dbeta, part 2: sum_s dL[t][s] Akk[t][s]
+    {
+        const int t = tid >> 3, qd = tid & 7;
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < C / 8; ++c) {
+            const int sx = qd * (C / 8) + c;
+            acc += sm.rb.dL[t][sx] * sm.akk[t][sx];
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        if (qd == 0) sm.dbeta[t] += acc;
+    }
+
+    // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints, own rows ----------------
+    if (own) {
+        if (!unsafe) {
+#pragma unroll
+            for (int mm = 0; mm < MB; ++mm) {
+                const int i = 2 * rh + mm;
+                // rows of block i: dK_l = sum_{j <= i} dP[i][j] (K_r[j] f_ij), dQ_l likewise with dA
+                const float bi = s.beta[BS * i + r16];
+                f32x4 dKl = zero4(), dQl = zero4();
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    if (j > i) continue;
+                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
+                    float bv[4], pv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) bv[e] = ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]) * fs;
+                    const float4 x = *reinterpret_cast<const float4*>(&sm.rb.dL[BS * i + r16][BS * j + 4 * g4]);
+                    pv[0] = bi * x.x; pv[1] = bi * x.y; pv[2] = bi * x.z; pv[3] = bi * x.w;
+                    const Frag4 B = frag4_from_f32<PREC>(bv);
+                    dKl = mma4f<PREC>(frag4_from_f32<PREC>(pv), B, dKl);
+                    dQl = mma4f<PREC>(ldfrag4<PREC, ST>(&sm.dA[0][0], LDT, BS * i, BS * j), B, dQl);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dka[mm][e] += dKl[e] * el[mm][e];
+                    dqa[mm][e] += dQl[e] * el[mm][e];
+                    dga[mm][e] += (dKl[e] * kx[mm][e] + dQl[e] * qx[mm][e]) * el[mm][e];
+                }
+            }
+#pragma unroll
+            for (int mm = 0; mm < MB; ++mm) {
+                const int j = 2 * rh + mm;
+                // rows of block j: dK_r = sum_{i >= j} dP[i][j]^T K_l[i] + dA[i][j]^T Q_l[i], times f_ij e^{gamma_r - gamma}
+                f32x4 dKr = zero4();
+#pragma unroll
+                for (int i = 0; i < NB; ++i) {
+                    if (i < j) continue;
+                    float bkv[4], bqv[4], pv[4], av[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = BS * i + 4 * g4 + e;
+                        bkv[e] = ld1<ST>(&s.kl[t][d]);
+                        bqv[e] = ld1<ST>(&s.ql[t][d]);
+                        pv[e] = s.beta[t] * sm.rb.dL[t][BS * j + r16];      // dP^T
+                        av[e] = ld1<ST>(&sm.dA[t][BS * j + r16]);           // dA^T
+                    }
+                    f32x4 P = mma4f<PREC>(frag4_from_f32<PREC>(pv), frag4_from_f32<PREC>(bkv), zero4());
+                    P = mma4f<PREC>(frag4_from_f32<PREC>(av), frag4_from_f32<PREC>(bqv), P);
+                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dKr[e] += P[e] * fs;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float c = dKr[e] * er[mm][e];
+                    dka[mm][e] += c;
+                    dga[mm][e] -= c * kx[mm][e];
+                }
+            }
+        } else {
+            // pairwise path: raw k in kr, raw q in ql, gamma in g
+#pragma unroll
+            for (int mm = 0; mm < MB; ++mm)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = BS * (2 * rh + mm) + 4 * g4 + e;
+                    const float gt = s.g[t][d], bt = s.beta[t];
+                    float ak = 0.f, aq = 0.f, ag = 0.f;
+                    for (int sx = 0; sx < C; ++sx) {
+                        const float gs = s.g[sx][d];
+                        if (sx <= t) {
+                            const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - gs);
+                            const float pp = bt * sm.rb.dL[t][sx], pa = ld1<ST>(&sm.dA[t][sx]);
+                            ak += pp * ks;
+                            aq += pa * ks;
+                            ag += (pp * kx[mm][e] + pa * qx[mm][e]) * ks;
+                        }
+                        if (sx >= t) {
+                            const float ex = kexp<PREC>(gs - gt);
+                            const float pp = s.beta[sx] * sm.rb.dL[sx][t], pa = ld1<ST>(&sm.dA[sx][t]);
+                            const float c = (pp * ld1<ST>(&s.kr[sx][d]) + pa * ld1<ST>(&s.ql[sx][d])) * ex;
+                            ak += c;
+                            ag -= c * kx[mm][e];
+                        }
+                    }
+                    dka[mm][e] += ak;
+                    dqa[mm][e] += aq;
+                    dga[mm][e] += ag;
+                }
+        }
+    }
+
+    // ---------------- phase 5: dG, reverse cumsum over the two row halves ----------------
+    float lsum[MB][4];
+    if (own) {
+        if (rh == 1 && g4 == 3)      // row C-1
+            dga[MB - 1][3] += dgcol + xg[d] + kexp<PREC>(s.g[C - 1][d]) * part;
+        float tot[MB];
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm) {
+            float run = 0.f;
+#pragma unroll
+            for (int e = 3; e >= 0; --e) { run += dga[mm][e]; lsum[mm][e] = run; }
+            tot[mm] = run;
+        }
+        float after_m = 0.f;
+#pragma unroll
+        for (int mm = MB - 1; mm >= 0; --mm) {
+            const float t0v = __shfl(tot[mm], r16, 64);
+            const float t1v = __shfl(tot[mm], r16 + 16, 64);
+            const float t2v = __shfl(tot[mm], r16 + 32, 64);
+            const float t3v = __shfl(tot[mm], r16 + 48, 64);
+            const float later = (g4 < 1 ? t1v : 0.f) + (g4 < 2 ? t2v : 0.f) + (g4 < 3 ? t3v : 0.f);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) lsum[mm][e] += later + after_m;
+            after_m += t0v + t1v + t2v + t3v;
+        }
+        if (rh == 1 && g4 == 0) xt[d] = after_m;     // total over rows 32..63
+    }
+    __syncthreads();   // xt; region A (dR) and B (dL) dead
+    if (own) {
+        const float add = rh == 0 ? xt[d] : 0.f;
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * (2 * rh + mm) + 4 * g4 + e;
+                st1<ST>(&sm.ra.out[0][t][d], dqa[mm][e]);
+                st1<ST>(&sm.ra.out[1][t][d], dka[mm][e]);
+                st1<ST>(&sm.ra.out[2][t][d], dvo[mm][e]);
+                st1<ST>(&sm.ra.out[3][t][d], lsum[mm][e] + add);
+            }
+    }
+    __syncthreads();
+    tile_out<ST, C, D, NTH>(&sm.ra.out[0][0][0], LDK, static_cast<ST*>(a.dq) + base, rs, valid);
+    tile_out<ST, C, D, NTH>(&sm.ra.out[1][0][0], LDK, static_cast<ST*>(a.dk) + base, rs, valid);
+    tile_out<ST, C, D, NTH>(&sm.ra.out[2][0][0], LDK, static_cast<ST*>(a.dv) + base, rs, valid);
+    if constexpr (std::is_same<TG, ST>::value) {
+        tile_out<ST, C, D, NTH>(&sm.ra.out[3][0][0], LDK, static_cast<ST*>(a.dg) + base, rs, valid);
+    } else {
+        for (int idx = tid; idx < C * D; idx += NTH) {
+            const int t = idx / D, dd = idx - t * D;
+            if (t < valid) st1<TG>(static_cast<TG*>(a.dg) + base + (size_t)t * rs + dd, ld1<ST>(&sm.ra.out[3][t][dd]));
+        }
+    }
+    if (tid < valid) st1<ST>(static_cast<ST*>(a.dbeta) + bbase + (size_t)tid * a.H, sm.dbeta[tid]);
+}
+
+// ----------------------------------------------------------------------------
 // launchers
 // ----------------------------------------------------------------------------
 template <int D, typename TI, typename TG>
@@ -835,7 +1312,7 @@ static hipError_t launch_local_t(const LocalArgs& a, int nchunks, hipStream_t st
     if constexpr (std::is_same<TI, float>::value)
         hipLaunchKernelGGL((kda_bwd_local_kernel<D, TI, TG, 3>), dim3(nchunks), dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((kda_bwd_local2_kernel<D, TI, TG, 1>), dim3(nchunks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((kda_bwd_local3_kernel<D, TI, TG, 1>), dim3(nchunks), dim3(512), 0, st, a);
     return hipGetLastError();
 }
 

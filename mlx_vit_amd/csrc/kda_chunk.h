@@ -191,7 +191,7 @@ struct ChunkSmem {
             float egr[NB][D];   // e^{G - gamma_16j}
             float f[6][D];      // e^{gamma_16i - gamma_16j}, j < i
         };
-        float tmp[256];
+        float tmp[512];
     };
     float beta[C];
 };
@@ -234,9 +234,10 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, ST* sv, int ldv,
     return flag;
 }
 
-template <int D, typename ST>
+template <int D, typename ST, int NTH = 256>
 __device__ __forceinline__ void chunk_cumsum2(ChunkSmem<D, ST>& s) {
-    constexpr int PARTS = 256 / D, RP = C / PARTS;
+    constexpr int PARTS = NTH / D, RP = C / PARTS;
+    static_assert(PARTS * D <= 512, "cumsum partials fit tmp");
     const int tid = threadIdx.x, d = tid % D, p = tid / D;
     float run = 0.f;
 #pragma unroll
@@ -256,10 +257,10 @@ __device__ __forceinline__ void chunk_cumsum2(ChunkSmem<D, ST>& s) {
 }
 
 // factor tables + span guard; returns nonzero (uniform) for the pairwise path
-template <int D, typename ST, int PREC>
+template <int D, typename ST, int PREC, int NTH = 256>
 __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag) {
     const int tid = threadIdx.x;
-    for (int idx = tid; idx < NB * D; idx += 256) {
+    for (int idx = tid; idx < NB * D; idx += NTH) {
         const int j = idx / D, d = idx % D;
         const float g0 = s.g[BS * j][d];
         const float span = g0 - s.g[BS * j + BS - 1][d];
@@ -267,7 +268,7 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag) {
         s.er[j][d] = kexp<PREC>(g0);
         s.egr[j][d] = kexp<PREC>(s.g[C - 1][d] - g0);
     }
-    for (int idx = tid; idx < 6 * D; idx += 256) {
+    for (int idx = tid; idx < 6 * D; idx += NTH) {
         const int p = idx / D, d = idx % D;
         const int i = (p >= 3) ? 3 : (p >= 1) ? 2 : 1;
         const int j = p - pair_idx(i, 0);

@@ -341,12 +341,12 @@ template <> __device__ __forceinline__ void store_vec<float>(float* p, const flo
 // The prefetched vectors live in one SSA vector value, never in an array: an
 // array indexed inside a loop is an alloca that the backend would place in LDS
 // or scratch, which forces a wait on every load.
-template <typename ST, int ROWS, int COLS>
+template <typename ST, int ROWS, int COLS, int NTH = 256>
 struct Tile {
     static constexpr int EPV = 16 / (int)sizeof(ST);
     static constexpr int VPR = COLS / EPV;
     static constexpr int NV = ROWS * VPR;
-    static constexpr int PER = (NV + 255) / 256;
+    static constexpr int PER = (NV + NTH - 1) / NTH;
     typedef uint32_t vec_t __attribute__((ext_vector_type(4 * PER)));
     vec_t r;
 
@@ -360,8 +360,8 @@ struct Tile {
     __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int v = threadIdx.x + 256 * i;
-            if (NV % 256 == 0 || v < NV) {
+            const int v = threadIdx.x + NTH * i;
+            if (NV % NTH == 0 || v < NV) {
                 const int row = v / VPR, c = (v - row * VPR) * EPV;
                 put(i, *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c));
             }
@@ -371,8 +371,8 @@ struct Tile {
     __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld, int valid_rows) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int v = threadIdx.x + 256 * i;
-            if (NV % 256 == 0 || v < NV) {
+            const int v = threadIdx.x + NTH * i;
+            if (NV % NTH == 0 || v < NV) {
                 const int row = v / VPR, c = (v - row * VPR) * EPV;
                 put(i, (row < valid_rows) ? *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c)
                                           : make_uint4(0u, 0u, 0u, 0u));
@@ -386,8 +386,8 @@ struct Tile {
     __device__ __forceinline__ void load_at(int t, const ST* __restrict__ g, size_t gld) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int v = t + 256 * i;
-            if (NV % 256 == 0 || v < NV) {
+            const int v = t + NTH * i;
+            if (NV % NTH == 0 || v < NV) {
                 const int row = v / VPR, c = (v - row * VPR) * EPV;
                 put(i, *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c));
             }
@@ -396,8 +396,8 @@ struct Tile {
     __device__ __forceinline__ void load_at(int t, const ST* __restrict__ g, size_t gld, int valid_rows) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int v = t + 256 * i;
-            if (NV % 256 == 0 || v < NV) {
+            const int v = t + NTH * i;
+            if (NV % NTH == 0 || v < NV) {
                 const int row = v / VPR, c = (v - row * VPR) * EPV;
                 put(i, (row < valid_rows) ? *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c)
                                           : make_uint4(0u, 0u, 0u, 0u));
@@ -407,8 +407,8 @@ struct Tile {
     __device__ __forceinline__ void store_at(int t, ST* lds, int lld) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int v = t + 256 * i;
-            if (NV % 256 == 0 || v < NV) {
+            const int v = t + NTH * i;
+            if (NV % NTH == 0 || v < NV) {
                 const int row = v / VPR, c = (v - row * VPR) * EPV;
                 *reinterpret_cast<uint4*>(lds + row * lld + c) = get(i);
             }
@@ -427,10 +427,10 @@ __device__ __forceinline__ void tile_out_at(int t, const ST* lds, int lld, ST* _
     }
 }
 
-template <typename ST, int ROWS, int COLS>
+template <typename ST, int ROWS, int COLS, int NTH = 256>
 __device__ __forceinline__ void tile_out(const ST* lds, int lld, ST* __restrict__ g, size_t gld, int valid_rows) {
     constexpr int EPV = 16 / (int)sizeof(ST), VPR = COLS / EPV, NV = ROWS * VPR;
-    for (int v = threadIdx.x; v < NV; v += 256) {
+    for (int v = threadIdx.x; v < NV; v += NTH) {
         const int row = v / VPR, c = (v - row * VPR) * EPV;
         if (row < valid_rows)
             *reinterpret_cast<uint4*>(g + (size_t)row * gld + c) = *reinterpret_cast<const uint4*>(lds + row * lld + c);
