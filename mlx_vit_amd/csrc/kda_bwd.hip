@@ -1057,35 +1057,46 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     }
     __syncthreads();
     if (own) {
-        // rh = 0: Y = dW (from dR[:, d]), result in place; rh = 1: Y = dV', result in dR[:, D + d]
+        // rh = 0: Y = dW (from dR[:, d]), result in place; rh = 1: Y = dV', result in dR[:, D + d].
+        // Right-looking block back substitution: as soon as dR_j is known, every
+        // earlier block is updated, Y_i += A_ij dR_j with
+        // A_ij[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a].
         const int col = rh ? D + d : d;
         const ST* sdVp = &sm.rb.p2.dVp[0][0];
-        f32x4 dRx[NB];
+        f32x4 Y[NB];
+        Frag4 At[NB], Aij[6];
 #pragma unroll
-        for (int i = NB - 1; i >= 0; --i) {
-            f32x4 Y;
+        for (int i = 0; i < NB; ++i) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * i + 4 * g4 + e;
-                Y[e] = rh ? ld1<ST>(sdVp + t * LDK + d) : sm.ra.dR[t][d];
+                Y[i][e] = rh ? ld1<ST>(sdVp + t * LDK + d) : sm.ra.dR[t][d];
             }
+            float tv[4];
 #pragma unroll
-            for (int j = i + 1; j < NB; ++j) {
-                // A[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a]
+            for (int e = 0; e < 4; ++e) tv[e] = sm.tii[i][4 * g4 + e][r16];     // A[a][b] = T_ii[b][a]
+            At[i] = frag4_from_f32<3>(tv);
+        }
+#pragma unroll
+        for (int j = 1; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < j; ++i) {
                 float av[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int rb = BS * j + 4 * g4 + e;
                     av[e] = -s.beta[rb] * sm.akk[rb][BS * i + r16];
                 }
-                Y = mma4f<3>(frag4_from_f32<3>(av), accfrag4<3>(dRx[j]), Y);
+                Aij[pair_idx(j, i)] = frag4_from_f32<3>(av);
             }
-            float tv[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) tv[e] = sm.tii[i][4 * g4 + e][r16];     // A[a][b] = T_ii[b][a]
-            dRx[i] = mma4f<3>(frag4_from_f32<3>(tv), accfrag4<3>(Y), zero4());
+        for (int j = NB - 1; j >= 0; --j) {
+            const f32x4 dRj = mma4f<3>(At[j], accfrag4<3>(Y[j]), zero4());
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sm.ra.dR[BS * i + 4 * g4 + e][col] = dRx[i][e];
+            for (int e = 0; e < 4; ++e) sm.ra.dR[BS * j + 4 * g4 + e][col] = dRj[e];
+            const Frag4 Bj = accfrag4<3>(dRj);
+#pragma unroll
+            for (int i = 0; i < j; ++i) Y[i] = mma4f<3>(Aij[pair_idx(j, i)], Bj, Y[i]);
         }
     }
     __syncthreads();
@@ -1127,13 +1138,14 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         Frag8 A[2 * D / 32], B[2 * D / 32];
 #pragma unroll
         for (int ks = 0; ks < 2 * D / 32; ++ks) {
-            A[ks] = ldfrag<3, float>(&sm.ra.dR[0][0], LDR, BS * i, 32 * ks);
-            B[ks] = (32 * ks < D) ? ldfrag<3, ST>(&sm.W[0][0], LDK, BS * j, 32 * ks)
-                                  : ldfrag<3, ST>(&sm.U[0][0], LDK, BS * j, 32 * ks - D);
+            A[ks] = ldfrag<2, float>(&sm.ra.dR[0][0], LDR, BS * i, 32 * ks);
+            B[ks] = (32 * ks < D) ? ldfrag<1, ST>(&sm.W[0][0], LDK, BS * j, 32 * ks)
+                                  : ldfrag<1, ST>(&sm.U[0][0], LDK, BS * j, 32 * ks - D);
         }
+        // W and U are bf16 here: splitting only dR keeps the fp32 accuracy of the product
         f32x4 acc = zero4();
 #pragma unroll
-        for (int ks = 0; ks < 2 * D / 32; ++ks) acc = mma<3>(A[ks], B[ks], acc);
+        for (int ks = 0; ks < 2 * D / 32; ++ks) acc = mma<2>(A[ks], B[ks], acc);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
@@ -1159,24 +1171,35 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints, own rows ----------------
     if (own) {
         if (!unsafe) {
+            // The decay factor f_ij = e^{gamma_16i - gamma_16j} is per channel, so it
+            // scales the accumulated product instead of the B operand.
+            auto colfrag = [&](const ST* M, int ld, int row0) __attribute__((always_inline)) {
+                // B[k][n] = M[row0 + k][d] for the lane's k = 4 g4 + 0..3, raw bf16
+                Frag4 f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) f.h[e] = (short)M[(row0 + 4 * g4 + e) * ld + d];
+                return f;
+            };
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm) {
                 const int i = 2 * rh + mm;
-                // rows of block i: dK_l = sum_{j <= i} dP[i][j] (K_r[j] f_ij), dQ_l likewise with dA
+                // rows of block i: dK_l = sum_{j <= i} f_ij dP[i][j] K_r[j], dQ_l likewise with dA
                 const float bi = s.beta[BS * i + r16];
                 f32x4 dKl = zero4(), dQl = zero4();
 #pragma unroll
                 for (int j = 0; j < NB; ++j) {
                     if (j > i) continue;
-                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
-                    float bv[4], pv[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) bv[e] = ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]) * fs;
+                    const Frag4 B = colfrag(&s.kr[0][0], LDK, BS * j);
                     const float4 x = *reinterpret_cast<const float4*>(&sm.rb.dL[BS * i + r16][BS * j + 4 * g4]);
-                    pv[0] = bi * x.x; pv[1] = bi * x.y; pv[2] = bi * x.z; pv[3] = bi * x.w;
-                    const Frag4 B = frag4_from_f32<PREC>(bv);
-                    dKl = mma4f<PREC>(frag4_from_f32<PREC>(pv), B, dKl);
-                    dQl = mma4f<PREC>(ldfrag4<PREC, ST>(&sm.dA[0][0], LDT, BS * i, BS * j), B, dQl);
+                    const float pv[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
+                    const f32x4 Pk = mma4f<1>(frag4_from_f32<1>(pv), B, zero4());
+                    const f32x4 Pq = mma4f<1>(ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * i, BS * j), B, zero4());
+                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dKl[e] += Pk[e] * fs;
+                        dQl[e] += Pq[e] * fs;
+                    }
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -1188,22 +1211,21 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm) {
                 const int j = 2 * rh + mm;
-                // rows of block j: dK_r = sum_{i >= j} dP[i][j]^T K_l[i] + dA[i][j]^T Q_l[i], times f_ij e^{gamma_r - gamma}
+                // rows of block j: dK_r = sum_{i >= j} f_ij (dP[i][j]^T K_l[i] + dA[i][j]^T Q_l[i]),
+                // then times e^{gamma_r - gamma}
                 f32x4 dKr = zero4();
 #pragma unroll
                 for (int i = 0; i < NB; ++i) {
                     if (i < j) continue;
-                    float bkv[4], bqv[4], pv[4], av[4];
+                    float pv[4], av[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int t = BS * i + 4 * g4 + e;
-                        bkv[e] = ld1<ST>(&s.kl[t][d]);
-                        bqv[e] = ld1<ST>(&s.ql[t][d]);
                         pv[e] = s.beta[t] * sm.rb.dL[t][BS * j + r16];      // dP^T
                         av[e] = ld1<ST>(&sm.dA[t][BS * j + r16]);           // dA^T
                     }
-                    f32x4 P = mma4f<PREC>(frag4_from_f32<PREC>(pv), frag4_from_f32<PREC>(bkv), zero4());
-                    P = mma4f<PREC>(frag4_from_f32<PREC>(av), frag4_from_f32<PREC>(bqv), P);
+                    f32x4 P = mma4f<1>(frag4_from_f32<1>(pv), colfrag(&s.kl[0][0], LDK, BS * i), zero4());
+                    P = mma4f<1>(frag4_from_f32<1>(av), colfrag(&s.ql[0][0], LDK, BS * i), P);
                     const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) dKr[e] += P[e] * fs;

@@ -17,7 +17,8 @@
 // Precision.  PREC == 1 rounds both operands to bf16 (one MFMA).  PREC == 3
 // splits each fp32 operand into hi + lo bf16 parts and issues hi*hi + hi*lo +
 // lo*hi, which carries ~16 mantissa bits (relative error ~1e-5); it is used for
-// fp32 inputs and for the small triangular-solve products.
+// fp32 inputs and for the small triangular-solve products.  PREC == 2 splits
+// only A (hi*hi + lo*hi), for products whose B operand is exact in bf16.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -184,7 +185,7 @@ __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 // ----------------------------------------------------------------------------
 // bf16-native operands: raw bf16 bits in memory go straight into the MFMA
-// (no fp32 round trip).  Frag8 carries a hi part and, for PREC == 3, a lo part.
+// (no fp32 round trip).  Frag8 carries a hi part and, for PREC >= 2, a lo part.
 // ----------------------------------------------------------------------------
 struct Frag8 { bf16x8 h, l; };
 struct Frag4 { short4v h, l; };
@@ -196,7 +197,7 @@ __device__ __forceinline__ Frag8 frag_from_f32(const float* v) {
     for (int e = 0; e < 8; ++e) {
         const __bf16 hi = (__bf16)v[e];
         f.h[e] = hi;
-        if constexpr (PREC == 3) f.l[e] = (__bf16)(v[e] - (float)hi);
+        if constexpr (PREC >= 2) f.l[e] = (__bf16)(v[e] - (float)hi);
     }
     return f;
 }
@@ -208,7 +209,7 @@ __device__ __forceinline__ Frag4 frag4_from_f32(const float* v) {
     for (int e = 0; e < 4; ++e) {
         const uint16_t hi = f2bf(v[e]);
         f.h[e] = (short)hi;
-        if constexpr (PREC == 3) f.l[e] = (short)f2bf(v[e] - bf2f(hi));
+        if constexpr (PREC >= 2) f.l[e] = (short)f2bf(v[e] - bf2f(hi));
     }
     return f;
 }
@@ -223,7 +224,7 @@ __device__ __forceinline__ Frag8 ldfrag(const ST* M, int ld, int row0, int k0) {
         const uint2 y = *reinterpret_cast<const uint2*>(p + 16);
         Frag8 f;
         f.h = __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
-        if constexpr (PREC == 3) f.l = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+        if constexpr (PREC >= 2) f.l = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
         return f;
     } else {
         const float4 x = *reinterpret_cast<const float4*>(p);
@@ -242,7 +243,7 @@ __device__ __forceinline__ Frag4 ldfrag4(const ST* M, int ld, int row0, int k0) 
         const uint2 x = *reinterpret_cast<const uint2*>(p);
         Frag4 f;
         f.h = __builtin_bit_cast(short4v, x);
-        if constexpr (PREC == 3) f.l = short4v{0, 0, 0, 0};
+        if constexpr (PREC >= 2) f.l = short4v{0, 0, 0, 0};
         return f;
     } else {
         const float4 x = *reinterpret_cast<const float4*>(p);
@@ -286,18 +287,16 @@ __device__ __forceinline__ Frag4 accfrag4(const f32x4& a) {
 
 template <int PREC>
 __device__ __forceinline__ f32x4 mma(const Frag8& a, const Frag8& b, f32x4 c) {
-    if constexpr (PREC == 3) {
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, c, 0, 0, 0);
-    }
+    // PREC 3: both operands split into bf16 hi + lo; PREC 2: only A split (B is
+    // exact in bf16, its lo part is zero); PREC 1: bf16 operands
+    if constexpr (PREC >= 2) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, c, 0, 0, 0);
+    if constexpr (PREC == 3) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, c, 0, 0, 0);
 }
 template <int PREC>
 __device__ __forceinline__ f32x4 mma4f(const Frag4& a, const Frag4& b, f32x4 c) {
-    if constexpr (PREC == 3) {
-        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.l, b.h, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.l, c, 0, 0, 0);
-    }
+    if constexpr (PREC >= 2) c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.l, b.h, c, 0, 0, 0);
+    if constexpr (PREC == 3) c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.l, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.h, c, 0, 0, 0);
 }
 
