@@ -57,7 +57,7 @@ def op_counts(B, T, H, D, backward):
     return flops, fwd_bytes + bwd_bytes
 
 
-def kernel_counts(B, T, H, D, es=2):
+def kernel_counts(B, T, H, D, es=2, keep_states=False):
     """Per-launch algorithmic FLOPs and compulsory HBM bytes of each library
     kernel (ids as in kda_profile_name).
 
@@ -66,7 +66,10 @@ def kernel_counts(B, T, H, D, es=2):
     touched once -- (B, T, H, *) tensors over the T valid tokens, workspace slabs
     over every chunk -- with the library's storage types: operands and the
     W/U/Qp/Kb/V'/dV'/A/h/dh workspace in the input dtype (``es`` bytes), Akk,
-    the diagonal-block inverses, e^G and the states in fp32."""
+    the diagonal-block inverses, e^G and the states in fp32.  With bf16 inputs
+    (``es`` = 2) the local-adjoint kernel recomputes Akk, the inverses and V', so
+    no kernel writes or reads them.  ``keep_states``: the forward recurrence
+    also writes the chunk-start states h (the training forward at D = 64)."""
     nc = -(-T // C)
     N = B * H * nc              # chunks
     n = N * C                   # padded token-heads
@@ -74,6 +77,7 @@ def kernel_counts(B, T, H, D, es=2):
     f4 = 4
     CD, CC, DD, TII = C * D, C * C, D * D, 4 * 16 * 16
     state = B * H * DD * f4
+    x = 0 if es == 2 else 1     # Akk, inverses and V' exist in the workspace (fp32 only)
     fl = {
         0: n * (8 * C * D + (2.0 / 3.0) * C * C),       # Akk, Aqk, W, U, solve
         1: n * (6 * D * D + 2 * C * D),                 # W S, Qp S, Kb^T V', Aqk V'
@@ -82,19 +86,21 @@ def kernel_counts(B, T, H, D, es=2):
         4: n * (2 * C * D + 6 * D * D),                 # Aqk^T dO, Kb dS, Qp^T dO, W^T dV'
         # dQp, dKb, dW (6D^2); dAqk 2CD; transposed solve on [dW|dU] 4CD; dL 4CD;
         # the four decay-masked K K^T / Q K^T adjoint products 8CD
-        5: n * (6 * D * D + 18 * C * D),
+        # bf16 also recomputes V' = U - W h (2D^2) and the lower half of Akk (CD)
+        5: n * (6 * D * D + 18 * C * D) + (1 - x) * n * (2 * D * D + C * D),
         6: n * (8 * C * D + (2.0 / 3.0) * C * C),
     }
     io_in = nt * (4 * D + 1) * es                       # q, k, v, g, beta
     by = {
         0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp KbT Aqk eG
-        1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state,                      # -> o, S_final
-        2: io_in + N * (6 * CD * es + CC * es + CC * f4 + TII * f4 + D * f4),              # -> W U KbT WT QpT Kb AqkT Akk Tii eG
-        3: N * (3 * CD * es + D * f4 + DD * es + CD * es),                                  # -> h, V'
+        1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state
+           + (N * DD * es if keep_states else 0),                                          # -> o, S_final [h]
+        2: io_in + N * (6 * CD * es + CC * es + x * (CC + TII) * f4 + D * f4),             # -> W U KbT WT QpT Kb AqkT [Akk Tii] eG
+        3: N * (3 * CD * es + D * f4 + DD * es + x * CD * es),                              # -> h [V']
         4: N * (CC * es + 3 * CD * es + D * f4 + DD * es + CD * es) + nt * D * es + state,  # -> dh, dV', dS0
-        5: io_in + nt * D * es + N * (4 * CD * es + 2 * DD * es + CC * f4 + TII * f4)
+        5: io_in + nt * D * es + N * ((3 + x) * CD * es + 2 * DD * es + x * (CC + TII) * f4)
            + nt * (4 * D + 1) * es,                                                         # -> dq dk dv dg dbeta
-        6: io_in + N * (7 * CD * es + 2 * CC * es + CC * f4 + TII * f4 + D * f4),          # -> both sets
+        6: io_in + N * (7 * CD * es + 2 * CC * es + x * (CC + TII) * f4 + D * f4),         # -> both sets
     }
     return fl, by
 
@@ -135,10 +141,11 @@ def load_traffic(kernel_name):
 # ---------------------------------------------------------------------------
 PROFILE_ROLES = {
     # rocprof kernel symbol fragment -> profile names in dispatch order within a
-    # fwd+bwd step (the training pair: one prep launch, in its training mode)
+    # fwd+bwd step (the training pair at D = 64: one prep launch in its training
+    # mode, one forward recurrence that also keeps the chunk-start states)
     "kda_prep_kernel": ["kda_prep_kernel(train)"],
-    "kda_recur_kernel": ["kda_recur_kernel(fwd)", "kda_recur_kernel(states)"],
-    "kda_dh_kernel": ["kda_dh_kernel"],
+    "kda_recur": ["kda_recur_kernel(fwd)"],
+    "kda_dh": ["kda_dh_kernel"],
     "kda_bwd_local": ["kda_bwd_local_kernel"],
 }
 CALIB_FRAGMENT = "neg_kernel"
@@ -324,7 +331,7 @@ def main():
     prof_ms_per_step = (time.perf_counter() - t1) / args.steps * 1e3
     lib.kda_profile_enable(0)
     import ctypes
-    fl, by = kernel_counts(B, T, H, D)
+    fl, by = kernel_counts(B, T, H, D, keep_states=backward and D == 64)
     kernels = []
     for kid in range(_lib.PROF_NKERNELS):
         tot, cnt = ctypes.c_double(), ctypes.c_int()

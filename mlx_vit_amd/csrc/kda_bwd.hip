@@ -841,6 +841,8 @@ __global__ __launch_bounds__(256) void kda_bwd_local2_kernel(const LocalArgs a) 
 //            row blocks j of dK_r)
 //   phase 5  in-chunk reverse cumsum of dgamma: the two row halves meet
 //            through one LDS total per channel
+// A_kk, its diagonal-block inverses and V' = U - W h are recomputed here from
+// what is already in LDS instead of being read from the workspace.
 // LDS regions and their reuse are those of kda_bwd_local2_kernel.
 // ----------------------------------------------------------------------------
 template <int D, typename ST, typename TG, int PREC>
@@ -861,42 +863,33 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     const size_t rs = (size_t)a.H * D;
     const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
     const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
-    const size_t cCD = (size_t)ch * C * D, cCC = (size_t)ch * C * C, cDD = (size_t)ch * D * D;
+    const size_t cCD = (size_t)ch * C * D, cDD = (size_t)ch * D * D;
 
-    // ---------------- phase 0: one batch of loads ----------------
+    // ---------------- phase 0: loads ----------------
+    // All loads are issued here, in the order they are needed; only q, k, g and
+    // beta are waited for before the in-chunk cumsum.  W, U, h and the phase-1
+    // operands stay in registers (4 per thread per tile) until the cumsum and the
+    // anchored transform are done, so their latency hides behind those phases.
     int flag = 0;
+    Tile<ST, C, D, NTH> tW, tU, tdo, tv, tdVp;
+    Tile<ST, D, D, NTH> th, tdh;
+    float braw;
     {
-        Tile<ST, C, D, NTH> tq, tk, tv, tdo, tW, tU, tVp, tdVp;
+        Tile<ST, C, D, NTH> tq, tk;
         Tile<TG, C, D, NTH> tg;
-        Tile<ST, D, D, NTH> th, tdh;
-        Tile<float, C, C, NTH> takk;
-        Tile<float, NB * BS, BS, NTH> ttii;
         tq.load(static_cast<const ST*>(a.q) + base, rs, valid);
         tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
-        tv.load(static_cast<const ST*>(a.v) + base, rs, valid);
-        tdo.load(static_cast<const ST*>(a.dout) + base, rs, valid);
         tg.load(static_cast<const TG*>(a.g) + base, rs, valid);
+        braw = ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)min(tid, valid - 1) * a.H);
         tW.load(static_cast<const ST*>(a.W) + cCD, D);
         tU.load(static_cast<const ST*>(a.U) + cCD, D);
-        tVp.load(static_cast<const ST*>(a.Vp) + cCD, D);
-        tdVp.load(static_cast<const ST*>(a.dVp) + cCD, D);
         th.load(static_cast<const ST*>(a.h) + cDD, D);
+        tdo.load(static_cast<const ST*>(a.dout) + base, rs, valid);
+        tv.load(static_cast<const ST*>(a.v) + base, rs, valid);
+        tdVp.load(static_cast<const ST*>(a.dVp) + cCD, D);
         tdh.load(static_cast<const ST*>(a.dh) + cDD, D);
-        takk.load(a.Akk + cCC, C);
-        ttii.load(a.Tii + (size_t)ch * NB * BS * BS, BS);
-        const float bt = (tid < valid) ? ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)tid * a.H) : 0.f;
         tq.store(&s.ql[0][0], LDK);
         tk.store(&s.kr[0][0], LDK);
-        tv.store(&sm.rb.p2.v[0][0], LDK);
-        tdo.store(&sm.ra.p1.dO[0][0], LDK);
-        tW.store(&sm.W[0][0], LDK);
-        tU.store(&sm.U[0][0], LDK);
-        tVp.store(&sm.ra.p1.Vp[0][0], LDK);
-        tdVp.store(&sm.rb.p2.dVp[0][0], LDK);
-        th.store(&sm.ra.p1.h[0][0], LDK);
-        tdh.store(&sm.ra.p1.dh[0][0], LDK);
-        takk.store(&sm.akk[0][0], LDA);
-        ttii.store(&sm.tii[0][0][0], BS + 4);
         using TGT = Tile<TG, C, D, NTH>;
 #pragma unroll
         for (int i = 0; i < TGT::PER; ++i) {
@@ -912,14 +905,15 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                 }
             }
         }
-        if (tid < C) {
-            s.beta[tid] = bt;
-            sm.dbeta[tid] = 0.f;
-        }
+        if (tid < C) sm.dbeta[tid] = 0.f;
     }
     __syncthreads();
     chunk_cumsum2<D, ST, NTH>(s);
     const int unsafe = chunk_factors2<D, ST, PREC, NTH>(s, flag);
+    if (tid < C) s.beta[tid] = (tid < valid) ? braw : 0.f;
+    tW.store(&sm.W[0][0], LDK);
+    tU.store(&sm.U[0][0], LDK);
+    th.store(&sm.ra.p1.h[0][0], LDK);
 
     // per-lane values of the owned (t, d): rows t = 16 m + 4 g4 + e, m = 2 rh + mm, channel d
     const bool own = ct < NT;
@@ -966,6 +960,95 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             store_vec<ST>(&s.kr[t][c0], okr);
         }
     }
+    tdo.store(&sm.ra.p1.dO[0][0], LDK);
+    tv.store(&sm.rb.p2.v[0][0], LDK);
+    tdVp.store(&sm.rb.p2.dVp[0][0], LDK);
+    tdh.store(&sm.ra.p1.dh[0][0], LDK);
+    __syncthreads();
+
+    // ---------------- recomputed intermediates ----------------
+    // A_kk = strict-lower(K K^T . decay), formed as the prep kernel forms it, its
+    // diagonal-block inverses, and V' = U - W h (h is the chunk-start state in the
+    // bf16 the state recurrence used, so V' equals what it computed).  Waves 0-3
+    // each form one diagonal tile of A_kk and invert it at once (their own LDS
+    // writes, no barrier); waves 4-7 form the off-diagonal tiles; V' is split
+    // over all eight waves.
+    auto akk_tile = [&](int i, int j) __attribute__((always_inline)) {
+        f32x4 P = zero4();
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
+            const Frag8 Bk = (j < i) ? ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
+                                                              &s.f[pair_idx(i, j)][32 * ks])
+                                     : ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks);
+            P = mma<PREC>(Ak, Bk, P);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
+            sm.akk[t][sx] = (sx < t) ? P[e] : 0.f;
+        }
+    };
+    auto vp_tile = [&](int tix) __attribute__((always_inline)) {
+        const ST* sh = &sm.ra.p1.h[0][0];
+        const int m = tix / NT, c = tix - m * NT;
+        f32x4 P = zero4();
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const Frag8 A = ldfrag<PREC, ST>(&sm.W[0][0], LDK, BS * m, 32 * ks);
+            uint16_t hv[8];   // B[k][n] = h[k][n], k in the fragment's slot order
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hv[e] = sh[(32 * ks + 4 * g4 + e) * LDK + BS * c + r16];
+                hv[4 + e] = sh[(32 * ks + 16 + 4 * g4 + e) * LDK + BS * c + r16];
+            }
+            Frag8 B;
+            B.h = __builtin_bit_cast(bf16x8, make_uint4(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16),
+                                                        hv[4] | ((uint32_t)hv[5] << 16), hv[6] | ((uint32_t)hv[7] << 16)));
+            P = mma<PREC>(A, B, P);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = BS * m + 4 * g4 + e, cc = BS * c + r16;
+            st1<ST>(&sm.ra.p1.Vp[t][cc], ld1<ST>(&sm.U[t][cc]) - P[e]);
+        }
+    };
+    if (!unsafe) {
+        if (w < NB) {
+            akk_tile(w, w);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back its own tile
+            diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii);
+        } else {
+            constexpr int OFF[6] = {1, 3, 4, 6, 7, 8};   // tile_ij indices of the blocks below the diagonal
+            for (int o = w - NB; o < 6; o += 8 - NB) {
+                int i, j;
+                tile_ij(OFF[o], i, j);
+                akk_tile(i, j);
+            }
+        }
+        for (int idx = tid; idx < 6 * BS * BS; idx += NTH) {
+            const int tile = idx / (BS * BS), e = idx - tile * BS * BS;
+            const int i = (tile < 3) ? 0 : (tile < 5) ? 1 : 2;
+            const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
+            sm.akk[BS * i + e / BS][BS * j + (e % BS)] = 0.f;
+        }
+    } else {
+        // pairwise path: raw k in kr, exact exp(gamma_t - gamma_s)
+        for (int p = tid; p < C * C; p += NTH) {
+            const int t = p / C, sx = p - t * C;
+            float ak = 0.f;
+            if (sx < t)
+                for (int dd = 0; dd < D; ++dd)
+                    ak += ld1<ST>(&s.kr[t][dd]) * (ld1<ST>(&s.kr[sx][dd]) * kexp<PREC>(s.g[t][dd] - s.g[sx][dd]));
+            sm.akk[t][sx] = ak;
+        }
+        __syncthreads();
+        if (w < NB) diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii);
+    }
+    // V' tiles: one each for waves 0-3, the rest over waves 4-7
+    if (w < NB) vp_tile(w);
+    else
+        for (int tix = w; tix < NB * NT; tix += 8 - NB) vp_tile(tix);
     __syncthreads();
 
     f32x4 dqa[MB], dka[MB], dga[MB], dWt[MB];

@@ -211,7 +211,8 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, ST* sv, int ldv,
     tg.load(g + base, rstride, valid);
     if constexpr (WITH_V) tv.load(v + base, rstride, valid);
     const int tid = threadIdx.x;
-    const float bt = (tid < C && tid < valid) ? ld1<ST>(beta + bbase + (size_t)tid * H) : 0.f;
+    const float braw = ld1<ST>(beta + bbase + (size_t)min(tid, valid - 1) * H);
+    const float bt = (tid < valid) ? braw : 0.f;
     tq.store(&s.ql[0][0], ChunkSmem<D, ST>::LDK);
     tk.store(&s.kr[0][0], ChunkSmem<D, ST>::LDK);
     if constexpr (WITH_V) tv.store(sv, ldv);
@@ -279,31 +280,36 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag) {
 
 // Register-resident inverses of the four 16x16 diagonal blocks of I + L,
 // L[t][s] = beta_t Akk[t][s]: wave w inverts block w, lane c (< 16) owns
-// column c.  The block's strict lower part is read into registers first.
+// column c.  All 36 row reads of the block's strict lower part are issued
+// before the substitution starts (one LDS round trip instead of one per row);
+// beta_t scales the row sum: x_t = [t == c] - beta_t sum_{s<t} Akk[t][s] x_s.
 template <int LDA>
 __device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, const float* __restrict__ beta,
                                                  float (*tii)[BS][BS + 4]) {
     const int w = threadIdx.x >> 6, c = threadIdx.x & 63;
     if (c < BS) {
         const float* Ab = akk + (size_t)(BS * w) * LDA + BS * w;
-        float Lr[BS][BS];
+        float4 R[BS][BS / 4];
+        float bt[BS];
 #pragma unroll
         for (int t = 1; t < BS; ++t) {
-            const float bt = beta[BS * w + t];
+            bt[t] = beta[BS * w + t];
 #pragma unroll
-            for (int j4 = 0; j4 < (t + 3) / 4; ++j4) {
-                const float4 x = *reinterpret_cast<const float4*>(Ab + t * LDA + 4 * j4);
-                Lr[t][4 * j4] = bt * x.x; Lr[t][4 * j4 + 1] = bt * x.y;
-                Lr[t][4 * j4 + 2] = bt * x.z; Lr[t][4 * j4 + 3] = bt * x.w;
-            }
+            for (int j4 = 0; j4 < (t + 3) / 4; ++j4) R[t][j4] = *reinterpret_cast<const float4*>(Ab + t * LDA + 4 * j4);
         }
+        __builtin_amdgcn_sched_barrier(0);
         float x[BS];
+        x[0] = (c == 0) ? 1.f : 0.f;
 #pragma unroll
-        for (int t = 0; t < BS; ++t) {
-            float acc = (t == c) ? 1.f : 0.f;
+        for (int t = 1; t < BS; ++t) {
+            float acc = 0.f;
 #pragma unroll
-            for (int j = 0; j < t; ++j) acc -= Lr[t][j] * x[j];
-            x[t] = acc;
+            for (int j = 0; j < t; ++j) {
+                const float4 r = R[t][j / 4];
+                const float a = (j % 4 == 0) ? r.x : (j % 4 == 1) ? r.y : (j % 4 == 2) ? r.z : r.w;
+                acc += a * x[j];
+            }
+            x[t] = ((t == c) ? 1.f : 0.f) - bt[t] * acc;
         }
 #pragma unroll
         for (int t = 0; t < BS; ++t) tii[w][t][c] = x[t];

@@ -348,12 +348,17 @@ struct Tile {
     static constexpr int PER = (NV + NTH - 1) / NTH;
     typedef uint32_t vec_t __attribute__((ext_vector_type(4 * PER)));
     vec_t r;
+    // bit i: element i lies in a valid row.  Rows past valid_rows are loaded
+    // from the last valid row (so the load needs no branch, and the compiler no
+    // wait inside one) and read back as zero.
+    uint32_t ok = ~0u;
 
     __device__ __forceinline__ void put(int i, uint4 x) {
         r[4 * i] = x.x; r[4 * i + 1] = x.y; r[4 * i + 2] = x.z; r[4 * i + 3] = x.w;
     }
     __device__ __forceinline__ uint4 get(int i) const {
-        return make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+        const bool v = (ok >> i) & 1u;
+        return make_uint4(v ? r[4 * i] : 0u, v ? r[4 * i + 1] : 0u, v ? r[4 * i + 2] : 0u, v ? r[4 * i + 3] : 0u);
     }
     // all ROWS rows are read
     __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld) {
@@ -366,17 +371,9 @@ struct Tile {
             }
         }
     }
-    // rows at or past valid_rows read as zero
+    // rows at or past valid_rows (>= 1) read as zero
     __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld, int valid_rows) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int v = threadIdx.x + NTH * i;
-            if (NV % NTH == 0 || v < NV) {
-                const int row = v / VPR, c = (v - row * VPR) * EPV;
-                put(i, (row < valid_rows) ? *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c)
-                                          : make_uint4(0u, 0u, 0u, 0u));
-            }
-        }
+        load_at(threadIdx.x, g, gld, valid_rows);
     }
     __device__ __forceinline__ void store(ST* lds, int lld) const { store_at(threadIdx.x, lds, lld); }
 
@@ -393,13 +390,15 @@ struct Tile {
         }
     }
     __device__ __forceinline__ void load_at(int t, const ST* __restrict__ g, size_t gld, int valid_rows) {
+        ok = 0u;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int v = t + NTH * i;
             if (NV % NTH == 0 || v < NV) {
                 const int row = v / VPR, c = (v - row * VPR) * EPV;
-                put(i, (row < valid_rows) ? *reinterpret_cast<const uint4*>(g + (size_t)row * gld + c)
-                                          : make_uint4(0u, 0u, 0u, 0u));
+                const int rr = min(row, valid_rows - 1);
+                put(i, *reinterpret_cast<const uint4*>(g + (size_t)rr * gld + c));
+                ok |= (uint32_t)(row < valid_rows) << i;
             }
         }
     }

@@ -14,7 +14,8 @@
 //     MODE 0 writes O and the final state -- the chunk loop of
 //     nope_gdn_mlx.py:2408-2451 (fused solve/finalize 1519-1942) with the
 //     triangular solve hoisted into the prep kernel.
-//     MODE 1 writes the chunk-start states h and V' for the backward instead.
+//     MODE 1 writes the chunk-start states h for the backward instead (the
+//     fp32 kernel also writes V', which only the fp32 local-adjoint kernel reads).
 //   kda_dh_kernel  (reverse order)
 //       dV' = Aqk^T dO + Kb dS;  dS <- diag(e^G) dS + Qp^T dO - W^T dV'
 //     writing dS at each chunk end and dV'; the final dS is dS0 -- the state
@@ -552,7 +553,7 @@ struct Recur2Layout {
     static constexpr int XS_OFF = 2 * SET_BYTES;                 // S^T  [DC][LDR]
     static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;         // V'^T [DC][LDC]
     static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
-    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : D * LDU + C * LDU;   // O | h, V'
+    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : D * LDU;   // O | h
     static constexpr int STG_BYTES = (STG_ELEMS * 2 + 15) & ~15;
     static constexpr int NSTG = (MODE == 0) ? 2 : 3;            // staging tiles, by chunk % NSTG
     static constexpr int BYTES = STG_OFF + NSTG * STG_BYTES;
@@ -629,7 +630,6 @@ __global__ __launch_bounds__(512) void kda_recur2_kernel(const RecurArgs a) {
             } else {
                 const size_t ch = (size_t)bh * a.nc + n;
                 tile_out_at<ST, D, DC>(mt, sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
-                tile_out_at<ST, C, DC>(mt, sst + D * LDU, LDU, static_cast<ST*>(a.Vp) + ch * C * D + c0, D, C);
             }
         };
         // Chunk c's slabs live in register set c % NS from their load (NS
@@ -757,9 +757,6 @@ __global__ __launch_bounds__(512) void kda_recur2_kernel(const RecurArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) Vp[j][e] = Uv[j][e] - P[e];
             *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * w + 4 * g4) = pack4bf(Vp[j]);
-            if constexpr (MODE == 1)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, Vp[j][e]);
         }
         __syncthreads();                                       // B(n)
 
@@ -1086,6 +1083,9 @@ __global__ __launch_bounds__(512) void kda_dh2_kernel(const DhArgs a) {
 //         O = Qp S + Aqk V' -> staging; read chunk n+1's A operands
 // Barriers are lds_barrier(): DMA stays in flight across them, and each wave
 // waits with an explicit vmcnt for exactly the DMA it needs.
+// MODE 0 writes O and the final state, MODE 1 the chunk-start states h, MODE 2
+// both: the training forward keeps h for the backward, as the reference's
+// forward keeps S_traj for its VJP (nope_gdn_mlx.py:2734-2745).
 // ----------------------------------------------------------------------------
 template <int D, int MODE, int CS>
 struct Recur3Layout {
@@ -1093,24 +1093,27 @@ struct Recur3Layout {
     static constexpr int RB_W = 2 * D, RB_U = 2 * DC, RB_C = 2 * C;          // swizzled row bytes
     static constexpr int W_OFF = 0;                                           // [C][D]
     static constexpr int U_OFF = W_OFF + C * RB_W;                            // [C][DC]
-    static constexpr int QP_OFF = U_OFF + C * RB_U;                           // [C][D]   (MODE 0)
-    static constexpr int KBT_OFF = QP_OFF + (MODE == 0 ? C * RB_W : 0);        // [D][C]
-    static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                        // [C][C]   (MODE 0)
-    static constexpr int EG_OFF = AQK_OFF + (MODE == 0 ? C * RB_C : 0);        // [D] fp32
+    static constexpr bool FWD = MODE != 1;                                    // computes O
+    static constexpr int QP_OFF = U_OFF + C * RB_U;                           // [C][D]   (FWD)
+    static constexpr int KBT_OFF = QP_OFF + (FWD ? C * RB_W : 0);        // [D][C]
+    static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                        // [C][C]   (FWD)
+    static constexpr int EG_OFF = AQK_OFF + (FWD ? C * RB_C : 0);        // [D] fp32
     static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
     static constexpr int PS = 8, LDR = D + PS, LDU = DC + PS, LDC = C + PS;
     // exchange and staging live in a __shared__ array of their own
     static constexpr int XS_OFF = 0;                                          // S^T  [DC][LDR] bf16
     static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;                      // V'^T [DC][LDC] bf16
     static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
-    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : D * LDU + C * LDU;   // O | h, V'
+    static constexpr int H_OFF = (MODE == 2) ? C * LDU : 0;                    // h after O (MODE 2)
+    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : (MODE == 1) ? D * LDU : C * LDU + D * LDU;
     static constexpr int STG_BYTES = (STG_ELEMS * 2 + 15) & ~15;
+    // h for chunk n+1 is staged while chunk n-1 is flushed: three tiles
     static constexpr int NSTG = (MODE == 0) ? 2 : 3;
     static constexpr int XBYTES = STG_OFF + NSTG * STG_BYTES;
     static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "recurrence LDS");
     // DMA wave-instructions per wave per chunk
     static constexpr int L = DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_U, 4>::COUNT + DmaTile<D, RB_C, 4>::COUNT +
-                             (MODE == 0 ? DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_C, 4>::COUNT : 0) + 1;
+                             (FWD ? DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_C, 4>::COUNT : 0) + 1;
 };
 
 // vmcnt wait: all but the last `k` chunks' DMA (L instructions each) complete
@@ -1167,7 +1170,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
         TW::issue_s(gW + ch * C * D * 2, oW, sb + Lay::W_OFF, w);
         TU::issue_s(gU + (ch * C * D + c0) * 2, oU, sb + Lay::U_OFF, w);
         TK::issue_s(gKbT + ch * C * D * 2, oK, sb + Lay::KBT_OFF, w);
-        if constexpr (MODE == 0) {
+        if constexpr (Lay::FWD) {
             TW::issue_s(gQp + ch * C * D * 2, oW, sb + Lay::QP_OFF, w);
             TA::issue_s(gAqk + ch * C * C * 2, oA, sb + Lay::AQK_OFF, w);
         }
@@ -1176,14 +1179,14 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
     };
     auto flush = [&](int n) __attribute__((always_inline)) {
         const ST* sst = stg(n);
-        if constexpr (MODE == 0) {
+        if constexpr (Lay::FWD) {
             const int t0 = n * C, valid = min(C, a.T - t0);
             tile_out<ST, C, DC>(sst, LDU, static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
                                 (size_t)a.H * D, valid);
-        } else {
+        }
+        if constexpr (MODE >= 1) {
             const size_t ch = (size_t)bh * nc + n;
-            tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
-            tile_out<ST, C, DC>(sst + D * LDU, LDU, static_cast<ST*>(a.Vp) + ch * C * D + c0, D, C);
+            tile_out<ST, D, DC>(sst + Lay::H_OFF, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
         }
     };
 
@@ -1214,10 +1217,10 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
 #pragma unroll
                 for (int j = 0; j < NTW; ++j) {
                     *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(S[i][j]);
-                    if constexpr (MODE == 1)
+                    if constexpr (MODE >= 1)
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
+                            st1<ST>(sst + Lay::H_OFF + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
                 }
     };
 
@@ -1243,7 +1246,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
                 for (int ks = 0; ks < C / 32; ++ks) Akb[i][ks] = ldfrag_sw<RB_C>(sKbT, BS * mt[i], 32 * ks);
                 eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
             }
-        if constexpr (MODE == 0) {
+        if constexpr (Lay::FWD) {
             const ST* sQp = reinterpret_cast<const ST*>(sb + Lay::QP_OFF);
             const ST* sAqk = reinterpret_cast<const ST*>(sb + Lay::AQK_OFF);
 #pragma unroll
@@ -1286,9 +1289,6 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) Vp[j][e] = Uv[j][e] - P[e];
             *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * w + 4 * g4) = pack4bf(Vp[j]);
-            if constexpr (MODE == 1)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, Vp[j][e]);
         }
         // chunk n+1's DMA (this wave's share) complete; later chunks may stay in flight
         dma_wait_chunks<Lay::L>(min(nc - 1, n + NS) - (n + 1));
@@ -1312,7 +1312,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
                 }
             }
         if (n + 1 < nc) put_state(stg(n + 1));
-        if constexpr (MODE == 0) {
+        if constexpr (Lay::FWD) {
             // O = Qp S + Aqk V', row block w (the chunk-start state is in Bs)
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
@@ -1337,7 +1337,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
     lds_barrier();
     flush(nc - 1);
 
-    if (MODE == 0 && a.s_final) {
+    if (Lay::FWD && a.s_final) {
 #pragma unroll
         for (int i = 0; i < MT; ++i)
             if (own[i])
@@ -1636,7 +1636,15 @@ static hipError_t launch_dh_t(const DhArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+bool recur_keeps_states(int D, int in_bf16) { return in_bf16 && D == 64; }
+
 hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st) {
+    if (mode == 2) {
+        if (!recur_keeps_states(D, in_bf16)) return hipErrorInvalidValue;
+        constexpr int CS2 = RowSplit<64>::CS;
+        hipLaunchKernelGGL((kda_recur3_kernel<64, 2, CS2>), dim3(a.BH * CS2), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
 #define KDA_RECUR_CASE(DD)                                                                        \
     if (D == DD) {                                                                                \
         if (mode == 0) return in_bf16 ? launch_recur_t<DD, uint16_t, 0>(a, st)                    \
