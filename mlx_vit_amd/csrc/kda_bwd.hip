@@ -856,6 +856,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
               g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 8);
     const int ct = w & 3, rh = w >> 2;
     const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
     const int b = bh / a.H, h = bh - b * a.H;

@@ -286,7 +286,7 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag) {
 template <int LDA>
 __device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, const float* __restrict__ beta,
                                                  float (*tii)[BS][BS + 4]) {
-    const int w = threadIdx.x >> 6, c = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), c = threadIdx.x & 63;
     if (c < BS) {
         const float* Ab = akk + (size_t)(BS * w) * LDA + BS * w;
         float4 R[BS][BS / 4];

@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     __shared__ __align__(16) ST svbuf[G::STAGE_V ? C : 1][G::STAGE_V ? LDK : 8];
     __shared__ __align__(16) ST stgbuf[G::STG_IN_G ? 1 : C][G::STG_IN_G ? 8 : LDT];
 
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 4);
     const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
     const int b = bh / a.H, h = bh - b * a.H;
     const int t0 = n * C, valid = min(C, a.T - t0);

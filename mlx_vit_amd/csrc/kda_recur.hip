@@ -1137,6 +1137,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
     __shared__ __align__(16) char smem[Lay::XBYTES];
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 4);
     const int lb = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
     const int b = bh / a.H, h = bh - b * a.H;
@@ -1391,6 +1392,7 @@ __global__ __launch_bounds__(256) void kda_dh3_kernel(const DhArgs a) {
     __shared__ __align__(16) char smem[Lay::XBYTES];
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 4);
     const int lb = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
     const int b = bh / a.H, h = bh - b * a.H;
