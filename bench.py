@@ -57,7 +57,7 @@ def op_counts(B, T, H, D, backward):
     return flops, fwd_bytes + bwd_bytes
 
 
-def kernel_counts(B, T, H, D, es=2, keep_states=False):
+def kernel_counts(B, T, H, D, es=2):
     """Per-launch algorithmic FLOPs and compulsory HBM bytes of each library
     kernel (ids as in kda_profile_name).
 
@@ -68,8 +68,7 @@ def kernel_counts(B, T, H, D, es=2, keep_states=False):
     W/U/Qp/Kb/V'/dV'/A/h/dh workspace in the input dtype (``es`` bytes), Akk,
     the diagonal-block inverses, e^G and the states in fp32.  With bf16 inputs
     (``es`` = 2) the local-adjoint kernel recomputes Akk, the inverses and V', so
-    no kernel writes or reads them.  ``keep_states``: the forward recurrence
-    also writes the chunk-start states h (the training forward at D = 64)."""
+    no kernel writes or reads them."""
     nc = -(-T // C)
     N = B * H * nc              # chunks
     n = N * C                   # padded token-heads
@@ -93,8 +92,7 @@ def kernel_counts(B, T, H, D, es=2, keep_states=False):
     io_in = nt * (4 * D + 1) * es                       # q, k, v, g, beta
     by = {
         0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp KbT Aqk eG
-        1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state
-           + (N * DD * es if keep_states else 0),                                          # -> o, S_final [h]
+        1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state,                      # -> o, S_final
         2: io_in + N * (6 * CD * es + CC * es + x * (CC + TII) * f4 + D * f4),             # -> W U KbT WT QpT Kb AqkT [Akk Tii] eG
         3: N * (3 * CD * es + D * f4 + DD * es + x * CD * es),                              # -> h [V']
         4: N * (CC * es + 3 * CD * es + D * f4 + DD * es + CD * es) + nt * D * es + state,  # -> dh, dV', dS0
@@ -141,10 +139,9 @@ def load_traffic(kernel_name):
 # ---------------------------------------------------------------------------
 PROFILE_ROLES = {
     # rocprof kernel symbol fragment -> profile names in dispatch order within a
-    # fwd+bwd step (the training pair at D = 64: one prep launch in its training
-    # mode, one forward recurrence that also keeps the chunk-start states)
+    # fwd+bwd step (the training pair: one prep launch, in its training mode)
     "kda_prep_kernel": ["kda_prep_kernel(train)"],
-    "kda_recur": ["kda_recur_kernel(fwd)"],
+    "kda_recur": ["kda_recur_kernel(fwd)", "kda_recur_kernel(states)"],
     "kda_dh": ["kda_dh_kernel"],
     "kda_bwd_local": ["kda_bwd_local_kernel"],
 }
@@ -331,7 +328,7 @@ def main():
     prof_ms_per_step = (time.perf_counter() - t1) / args.steps * 1e3
     lib.kda_profile_enable(0)
     import ctypes
-    fl, by = kernel_counts(B, T, H, D, keep_states=backward and D == 64)
+    fl, by = kernel_counts(B, T, H, D)
     kernels = []
     for kid in range(_lib.PROF_NKERNELS):
         tot, cnt = ctypes.c_double(), ctypes.c_int()

@@ -87,11 +87,11 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
             void* workspace, size_t ws_bytes, void* stream);
 
 /* Training pair.  kda_fwd_train computes what kda_fwd computes and also keeps,
- * in its (pass 2) workspace, every per-chunk factor the backward needs (W, U,
+ * in its (pass 2) workspace, every per-chunk factor the backward needs: W, U,
  * the decay-scaled Q / K operands and their transposes, A_qk and its transpose,
- * e^G; with fp32 inputs also A_kk and the inverted diagonal blocks of I + L)
- * and the chunk-start states h in the input dtype.
- * kda_bwd_train is kda_bwd without its prep and state recompute: it requires the workspace that
+ * e^G (with fp32 inputs also A_kk and the inverted diagonal blocks of I + L).
+ * No state is kept: kda_bwd_train recomputes the chunk-boundary states.
+ * kda_bwd_train is kda_bwd without its prep: it requires the workspace that
  * kda_fwd_train filled for the same q, k, v, g, beta (and the same B, T, H, D,
  * dtype), unmodified in between, and returns the same gradients as kda_bwd.
  * Replace the forward of _get_chunkwise_kda_recurrence_fn, which keeps U_traj

@@ -306,27 +306,14 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     ra.eG = fregion(workspace, L, KDA_WS_EG);
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-    if (pass == KDA_PASS_TRAIN) {
-        // keep the chunk-start states for kda_bwd_train: written by the forward
-        // recurrence itself where it can, else by the state recompute
-        ra.h = region(workspace, L, KDA_WS_H);
-        ra.Vp = region(workspace, L, KDA_WS_VP);
-        if (kda::recur_keeps_states(D, in_bf16)) {
-            e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 2, st); });
-            if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
-            return ok();
-        }
-        e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
-        if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
-    }
     e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 0, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
     return ok();
 }
 
-// pass 1: prep and state recompute from the inputs, then the backward; pass 2:
-// the workspace holds what kda_fwd_train wrote for the same inputs (the
-// per-chunk factors and the chunk-start states), so both are skipped.
+// pass 1: prep from the inputs, then the backward; pass 2: the workspace holds
+// the per-chunk factors kda_fwd_train wrote for the same inputs, so the prep is
+// skipped.  Either way the chunk-boundary states are recomputed.
 int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
             int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
@@ -369,13 +356,12 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
     void* Vp = region(workspace, L, KDA_WS_VP);
     void* dVp = region(workspace, L, KDA_WS_DVP);
 
-    if (pass == KDA_PASS_BWD) {
-        kda::RecurArgs ra = {};
-        ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
-        ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-        e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
-        if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
-    }
+    // chunk-boundary states, recomputed from the per-chunk factors
+    kda::RecurArgs ra = {};
+    ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
+    ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
+    e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
+    if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
 
     kda::DhArgs da = {};
     da.AqkT = region(workspace, L, KDA_WS_AQKT);

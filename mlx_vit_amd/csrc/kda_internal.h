@@ -56,10 +56,8 @@ struct LocalArgs {
 };
 
 hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
-// mode 0: O and the final state; 1: the chunk-start states h; 2: both (only
-// where recur_keeps_states holds)
+// mode 0: O and the final state; 1: the chunk-start states h
 hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st);
-bool recur_keeps_states(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
 hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,

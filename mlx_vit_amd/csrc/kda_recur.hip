@@ -1083,9 +1083,7 @@ __global__ __launch_bounds__(512) void kda_dh2_kernel(const DhArgs a) {
 //         O = Qp S + Aqk V' -> staging; read chunk n+1's A operands
 // Barriers are lds_barrier(): DMA stays in flight across them, and each wave
 // waits with an explicit vmcnt for exactly the DMA it needs.
-// MODE 0 writes O and the final state, MODE 1 the chunk-start states h, MODE 2
-// both: the training forward keeps h for the backward, as the reference's
-// forward keeps S_traj for its VJP (nope_gdn_mlx.py:2734-2745).
+// MODE 0 writes O and the final state, MODE 1 the chunk-start states h.
 // ----------------------------------------------------------------------------
 template <int D, int MODE, int CS>
 struct Recur3Layout {
@@ -1093,19 +1091,21 @@ struct Recur3Layout {
     static constexpr int RB_W = 2 * D, RB_U = 2 * DC, RB_C = 2 * C;          // swizzled row bytes
     static constexpr int W_OFF = 0;                                           // [C][D]
     static constexpr int U_OFF = W_OFF + C * RB_W;                            // [C][DC]
-    static constexpr bool FWD = MODE != 1;                                    // computes O
-    static constexpr int QP_OFF = U_OFF + C * RB_U;                           // [C][D]   (FWD)
-    static constexpr int KBT_OFF = QP_OFF + (FWD ? C * RB_W : 0);        // [D][C]
-    static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                        // [C][C]   (FWD)
-    static constexpr int EG_OFF = AQK_OFF + (FWD ? C * RB_C : 0);        // [D] fp32
+    static constexpr int QP_OFF = U_OFF + C * RB_U;                           // [C][D]   (MODE 0)
+    static constexpr int KBT_OFF = QP_OFF + (MODE == 0 ? C * RB_W : 0);        // [D][C]
+    static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                        // [C][C]   (MODE 0)
+    static constexpr int EG_OFF = AQK_OFF + (MODE == 0 ? C * RB_C : 0);        // [D] fp32
     static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
-    static constexpr int PS = 8, LDR = D + PS, LDU = DC + PS, LDC = C + PS;
+    // Staging rows (LDU) keep a 16-byte pad for 16-byte row access.  The
+    // exchange tiles (LDR, LDC) are only touched 8 bytes at a time: a 4-element
+    // pad (rows of 34 dwords, 2 mod 32) puts the 16 rows of a fragment read or
+    // a C-layout write in 16 distinct bank pairs.
+    static constexpr int PS = 8, PX = 4, LDR = D + PX, LDU = DC + PS, LDC = C + PX;
     // exchange and staging live in a __shared__ array of their own
     static constexpr int XS_OFF = 0;                                          // S^T  [DC][LDR] bf16
     static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;                      // V'^T [DC][LDC] bf16
     static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
-    static constexpr int H_OFF = (MODE == 2) ? C * LDU : 0;                    // h after O (MODE 2)
-    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : (MODE == 1) ? D * LDU : C * LDU + D * LDU;
+    static constexpr int STG_ELEMS = (MODE == 0) ? C * LDU : D * LDU;   // O | h
     static constexpr int STG_BYTES = (STG_ELEMS * 2 + 15) & ~15;
     // h for chunk n+1 is staged while chunk n-1 is flushed: three tiles
     static constexpr int NSTG = (MODE == 0) ? 2 : 3;
@@ -1113,7 +1113,7 @@ struct Recur3Layout {
     static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "recurrence LDS");
     // DMA wave-instructions per wave per chunk
     static constexpr int L = DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_U, 4>::COUNT + DmaTile<D, RB_C, 4>::COUNT +
-                             (FWD ? DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_C, 4>::COUNT : 0) + 1;
+                             (MODE == 0 ? DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_C, 4>::COUNT : 0) + 1;
 };
 
 // vmcnt wait: all but the last `k` chunks' DMA (L instructions each) complete
@@ -1171,7 +1171,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
         TW::issue_s(gW + ch * C * D * 2, oW, sb + Lay::W_OFF, w);
         TU::issue_s(gU + (ch * C * D + c0) * 2, oU, sb + Lay::U_OFF, w);
         TK::issue_s(gKbT + ch * C * D * 2, oK, sb + Lay::KBT_OFF, w);
-        if constexpr (Lay::FWD) {
+        if constexpr (MODE == 0) {
             TW::issue_s(gQp + ch * C * D * 2, oW, sb + Lay::QP_OFF, w);
             TA::issue_s(gAqk + ch * C * C * 2, oA, sb + Lay::AQK_OFF, w);
         }
@@ -1180,14 +1180,13 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
     };
     auto flush = [&](int n) __attribute__((always_inline)) {
         const ST* sst = stg(n);
-        if constexpr (Lay::FWD) {
+        if constexpr (MODE == 0) {
             const int t0 = n * C, valid = min(C, a.T - t0);
             tile_out<ST, C, DC>(sst, LDU, static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
                                 (size_t)a.H * D, valid);
-        }
-        if constexpr (MODE >= 1) {
+        } else {
             const size_t ch = (size_t)bh * nc + n;
-            tile_out<ST, D, DC>(sst + Lay::H_OFF, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
+            tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
         }
     };
 
@@ -1218,10 +1217,10 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
 #pragma unroll
                 for (int j = 0; j < NTW; ++j) {
                     *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(S[i][j]);
-                    if constexpr (MODE >= 1)
+                    if constexpr (MODE == 1)
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            st1<ST>(sst + Lay::H_OFF + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
+                            st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
                 }
     };
 
@@ -1247,7 +1246,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
                 for (int ks = 0; ks < C / 32; ++ks) Akb[i][ks] = ldfrag_sw<RB_C>(sKbT, BS * mt[i], 32 * ks);
                 eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
             }
-        if constexpr (Lay::FWD) {
+        if constexpr (MODE == 0) {
             const ST* sQp = reinterpret_cast<const ST*>(sb + Lay::QP_OFF);
             const ST* sAqk = reinterpret_cast<const ST*>(sb + Lay::AQK_OFF);
 #pragma unroll
@@ -1313,7 +1312,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
                 }
             }
         if (n + 1 < nc) put_state(stg(n + 1));
-        if constexpr (Lay::FWD) {
+        if constexpr (MODE == 0) {
             // O = Qp S + Aqk V', row block w (the chunk-start state is in Bs)
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
@@ -1338,7 +1337,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
     lds_barrier();
     flush(nc - 1);
 
-    if (Lay::FWD && a.s_final) {
+    if (MODE == 0 && a.s_final) {
 #pragma unroll
         for (int i = 0; i < MT; ++i)
             if (own[i])
@@ -1360,7 +1359,11 @@ struct Dh3Layout {
     static constexpr int DO_OFF = WT_OFF + D * RB_C;                          // [C][DC] (t, own columns)
     static constexpr int EG_OFF = DO_OFF + C * RB_U;                          // [D] fp32
     static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
-    static constexpr int PS = 8, LDR = D + PS, LDU = DC + PS, LDC = C + PS;
+    // Staging rows (LDU) keep a 16-byte pad for 16-byte row access.  The
+    // exchange tiles (LDR, LDC) are only touched 8 bytes at a time: a 4-element
+    // pad (rows of 34 dwords, 2 mod 32) puts the 16 rows of a fragment read or
+    // a C-layout write in 16 distinct bank pairs.
+    static constexpr int PS = 8, PX = 4, LDR = D + PX, LDU = DC + PS, LDC = C + PX;
     static constexpr int XS_OFF = 0;                                          // dS^T   [DC][LDR]
     static constexpr int XV_OFF = XS_OFF + DC * LDR * 2;                      // -dV'^T [DC][LDC]
     static constexpr int STG_OFF = XV_OFF + DC * LDC * 2;
@@ -1638,15 +1641,7 @@ static hipError_t launch_dh_t(const DhArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-bool recur_keeps_states(int D, int in_bf16) { return in_bf16 && D == 64; }
-
 hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st) {
-    if (mode == 2) {
-        if (!recur_keeps_states(D, in_bf16)) return hipErrorInvalidValue;
-        constexpr int CS2 = RowSplit<64>::CS;
-        hipLaunchKernelGGL((kda_recur3_kernel<64, 2, CS2>), dim3(a.BH * CS2), dim3(256), 0, st, a);
-        return hipGetLastError();
-    }
 #define KDA_RECUR_CASE(DD)                                                                        \
     if (D == DD) {                                                                                \
         if (mode == 0) return in_bf16 ? launch_recur_t<DD, uint16_t, 0>(a, st)                    \

@@ -121,9 +121,9 @@ def kda_forward(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
 def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
                       workspace: Optional[torch.Tensor] = None
                       ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Forward that also keeps the per-chunk factors and the chunk-start states
-    the backward needs.  Returns (o, final_state, workspace); pass the
-    workspace, unmodified, to ``kda_backward_train`` with the same inputs."""
+    """Forward that also keeps the per-chunk factors the backward needs.
+    Returns (o, final_state, workspace); pass the workspace, unmodified, to
+    ``kda_backward_train`` with the same inputs."""
     _check_chunk(chunk_size)
     q, k, v, g, beta, s0 = _prepare(q, k, v, g, beta, initial_state)
     B, T, H, D = q.shape
@@ -183,9 +183,9 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
 class ChunkKDAFunction(torch.autograd.Function):
     """Autograd wrapper (the role of mx.custom_function in
     nope_gdn_mlx.py:2725-2808).  When a gradient is needed the forward keeps its
-    inputs and the workspace of kda_forward_train: the per-chunk factors and the
-    chunk-start states (the reference keeps the U / S trajectories); the
-    backward starts from them."""
+    inputs and the per-chunk factors of kda_forward_train -- not the U / S
+    trajectories the reference keeps; the backward recomputes the
+    chunk-boundary states from those factors."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, initial_state):
