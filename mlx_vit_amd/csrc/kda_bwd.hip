@@ -867,8 +867,8 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     const size_t cCD = (size_t)ch * C * D, cDD = (size_t)ch * D * D;
 
     // ---------------- phase 0: loads ----------------
-    // All loads are issued here, in the order they are needed; only q, k, g and
-    // beta are waited for before the in-chunk cumsum.  W, U, h and the phase-1
+    // All loads are issued here, in the order they are needed (q, k, g, beta of
+    // all waves first); only q, k, g and beta are waited for before the cumsum.  W, U, h and the phase-1
     // operands stay in registers (4 per thread per tile) until the cumsum and the
     // anchored transform are done, so their latency hides behind those phases.
     int flag = 0;
@@ -882,6 +882,9 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
         tg.load(static_cast<const TG*>(a.g) + base, rs, valid);
         braw = ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)min(tid, valid - 1) * a.H);
+        // Every wave's q, k, g, beta requests enter the CU's memory pipeline before
+        // any wave's later tiles, so no wave waits behind another's 80 KB.
+        __builtin_amdgcn_s_barrier();
         tW.load(static_cast<const ST*>(a.W) + cCD, D);
         tU.load(static_cast<const ST*>(a.U) + cCD, D);
         th.load(static_cast<const ST*>(a.h) + cDD, D);
@@ -920,9 +923,10 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     const bool own = ct < NT;
     const int d = own ? ct * BS + r16 : 0;
     constexpr int MB = NB / 2;
-    float kx[MB][4], qx[MB][4], el[MB][4], er[MB][4], eb[MB][4], erb[MB];
+    float kx[MB][4], qx[MB][4], el[MB][4], er[MB][4], eb[MB][4], erb[MB], eGd;
     {
         const float G = s.g[C - 1][d];
+        eGd = kexp<PREC>(G);
 #pragma unroll
         for (int mm = 0; mm < MB; ++mm) {
             const int m = 2 * rh + mm;
@@ -1358,7 +1362,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     float lsum[MB][4];
     if (own) {
         if (rh == 1 && g4 == 3)      // row C-1
-            dga[MB - 1][3] += dgcol + xg[d] + kexp<PREC>(s.g[C - 1][d]) * part;
+            dga[MB - 1][3] += dgcol + xg[d] + eGd * part;
         float tot[MB];
 #pragma unroll
         for (int mm = 0; mm < MB; ++mm) {

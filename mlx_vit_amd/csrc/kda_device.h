@@ -293,11 +293,28 @@ __device__ __forceinline__ f32x4 mma(const Frag8& a, const Frag8& b, f32x4 c) {
     if constexpr (PREC == 3) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, c, 0, 0, 0);
 }
+// [x | y]: two 4-element fragments as the two k-halves of one 8-element fragment
+__device__ __forceinline__ bf16x8 cat4(short4v x, short4v y) {
+    const uint2 u = __builtin_bit_cast(uint2, x), v = __builtin_bit_cast(uint2, y);
+    return __builtin_bit_cast(bf16x8, make_uint4(u.x, u.y, v.x, v.y));
+}
+// 16x16x16 product.  For PREC >= 2 the two terms a_hi b_hi + a_lo b_hi go into
+// one K = 32 instruction, A = [a_hi | a_lo], B = [b_hi | b_hi] (lane (r, g)
+// holds k = 4g..4g+3 of each half, the same k in A and B), which issues at the
+// rate of one K = 16 instruction; PREC 3 adds a_hi b_lo as a second K = 32
+// instruction with a zero half, so that dependent products never mix the two
+// MFMA shapes on one accumulator.
 template <int PREC>
 __device__ __forceinline__ f32x4 mma4f(const Frag4& a, const Frag4& b, f32x4 c) {
-    if constexpr (PREC >= 2) c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.l, b.h, c, 0, 0, 0);
-    if constexpr (PREC == 3) c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.l, c, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.h, c, 0, 0, 0);
+    if constexpr (PREC == 1) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.h, c, 0, 0, 0);
+    } else {
+        if constexpr (PREC == 3) {
+            const short4v z = short4v{0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat4(a.h, z), cat4(b.l, z), c, 0, 0, 0);
+        }
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat4(a.h, a.l), cat4(b.h, b.h), c, 0, 0, 0);
+    }
 }
 
 __device__ __forceinline__ f32x4 negacc(f32x4 a) { return f32x4{-a[0], -a[1], -a[2], -a[3]}; }
