@@ -1056,7 +1056,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         for (int tix = w; tix < NB * NT; tix += 8 - NB) vp_tile(tix);
     __syncthreads();
 
-    f32x4 dqa[MB], dka[MB], dga[MB], dWt[MB];
+    f32x4 dqa[MB], dka[MB], dga[MB], dWt[NB];
     float dgcol = 0.f, part = 0.f;
 
     // ---------------- phase 1: products over dv ----------------
@@ -1067,7 +1067,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         const ST* sh = &sm.ra.p1.h[0][0];
         const ST* sdh = &sm.ra.p1.dh[0][0];
         if (own) {
-            Frag8 Ao[MB][D / 32], Av[MB][D / 32], Ad[MB][D / 32], Bh[D / 32], Bdh[D / 32];
+            Frag8 Ao[MB][D / 32], Av[MB][D / 32], Bh[D / 32], Bdh[D / 32];
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
                 Bh[ks] = ldfrag<PREC, ST>(sh, LDK, BS * ct, 32 * ks);
@@ -1077,7 +1077,18 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     const int m = 2 * rh + mm;
                     Ao[mm][ks] = ldfrag<PREC, ST>(sdO, LDK, BS * m, 32 * ks);
                     Av[mm][ks] = ldfrag<PREC, ST>(sVp, LDK, BS * m, 32 * ks);
-                    Ad[mm][ks] = ldfrag<PREC, ST>(sdVp, LDK, BS * m, 32 * ks);
+                }
+            }
+            // dW = -dV' h^T, all row blocks of the channel tile, for the rh = 0
+            // waves, which run the dW chain of the solve from registers
+            if (rh == 0) {
+#pragma unroll
+                for (int m = 0; m < NB; ++m) {
+                    f32x4 dW = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < D / 32; ++ks)
+                        dW = mma<PREC>(ldfrag<PREC, ST>(sdVp, LDK, BS * m, 32 * ks), Bh[ks], dW);
+                    dWt[m] = negacc(dW);
                 }
             }
             // state-decay term of dG (rh = 1 waves): e^G sum_col dh[d][col] h[d][col]
@@ -1091,14 +1102,12 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm) {
-                f32x4 dQp = zero4(), dKb = zero4(), dW = zero4();
+                f32x4 dQp = zero4(), dKb = zero4();
 #pragma unroll
                 for (int ks = 0; ks < D / 32; ++ks) {
                     dQp = mma<PREC>(Ao[mm][ks], Bh[ks], dQp);
                     dKb = mma<PREC>(Av[mm][ks], Bdh[ks], dKb);
-                    dW = mma<PREC>(Ad[mm][ks], Bh[ks], dW);
                 }
-                dWt[mm] = negacc(dW);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float egt = erb[mm] * el[mm][e];                // e^{gamma_t}
@@ -1113,8 +1122,9 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             part = sum4g(part);
             if (rh == 0 && g4 == 0) xg[d] = dgcol;
         }
-        // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves
-        for (int tix = w; tix < 10; tix += 8) {
+        // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves, the rh = 1 waves
+        // first (the rh = 0 waves carry the extra dW blocks)
+        for (int tix = (w + 4) & 7; tix < 10; tix += 8) {
             int i, j;
             tile_ij(tix, i, j);
             Frag8 A[D / 32], B[D / 32];
@@ -1133,32 +1143,26 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             }
         }
     }
-    __syncthreads();   // phase-1 operands (region A) are dead from here
 
     // ---------------- phase 2: transposed WY solve, by right-hand side ----------------
-    // dW of the own rows -> dR[:, d]
+    // Each wave goes on from its own phase 1 (the operands are in registers or
+    // unchanged LDS); dR reaches region A only after the barrier that ends phase 1.
+    f32x4 X[NB];
     if (own) {
-#pragma unroll
-        for (int mm = 0; mm < MB; ++mm)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sm.ra.dR[BS * (2 * rh + mm) + 4 * g4 + e][d] = dWt[mm][e];
-    }
-    __syncthreads();
-    if (own) {
-        // rh = 0: Y = dW (from dR[:, d]), result in place; rh = 1: Y = dV', result in dR[:, D + d].
+        // rh = 0: Y = dW (registers), result dR[:, d]; rh = 1: Y = dV', result dR[:, D + d].
         // Right-looking block back substitution: as soon as dR_j is known, every
         // earlier block is updated, Y_i += A_ij dR_j with
         // A_ij[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a].
-        const int col = rh ? D + d : d;
         const ST* sdVp = &sm.rb.p2.dVp[0][0];
         f32x4 Y[NB];
         Frag4 At[NB], Aij[6];
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
+            if (rh) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * i + 4 * g4 + e;
-                Y[i][e] = rh ? ld1<ST>(sdVp + t * LDK + d) : sm.ra.dR[t][d];
+                for (int e = 0; e < 4; ++e) Y[i][e] = ld1<ST>(sdVp + (BS * i + 4 * g4 + e) * LDK + d);
+            } else {
+                Y[i] = dWt[i];
             }
             float tv[4];
 #pragma unroll
@@ -1179,13 +1183,19 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             }
 #pragma unroll
         for (int j = NB - 1; j >= 0; --j) {
-            const f32x4 dRj = mma4f<3>(At[j], accfrag4<3>(Y[j]), zero4());
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sm.ra.dR[BS * j + 4 * g4 + e][col] = dRj[e];
-            const Frag4 Bj = accfrag4<3>(dRj);
+            X[j] = mma4f<3>(At[j], accfrag4<3>(Y[j]), zero4());
+            const Frag4 Bj = accfrag4<3>(X[j]);
 #pragma unroll
             for (int i = 0; i < j; ++i) Y[i] = mma4f<3>(Aij[pair_idx(j, i)], Bj, Y[i]);
         }
+    }
+    __syncthreads();   // phase-1 operands (region A) are dead from here
+    if (own) {
+        const int col = rh ? D + d : d;
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sm.ra.dR[BS * j + 4 * g4 + e][col] = X[j][e];
     }
     __syncthreads();
     // contributions of dR to the own rows; dv = beta dR_v
@@ -1217,7 +1227,16 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         acc += __shfl_xor(acc, 4, 64);
         if (qd == 0) sm.dbeta[t] = acc;
     }
-    __syncthreads();   // v and dV' (region B) are dead from here
+    // dL goes to the g region, dead on the anchored path, when it fits (D >= 64):
+    // then phase 3 need not wait for the v reads above.  Otherwise it reuses
+    // region B once v and dV' are dead.
+    constexpr int LDG = ChunkSmem<D, ST>::LDG;
+    constexpr bool DL_IN_G = LDG >= LDA;
+    const bool dl_g = DL_IN_G && !unsafe;
+    float* sdL = dl_g ? &s.g[0][0] : &sm.rb.dL[0][0];
+    constexpr int LDL = DL_IN_G ? LDG : LDA;
+    static_assert(!DL_IN_G || LDG == LDA, "one dL stride");
+    if (!dl_g) __syncthreads();   // v and dV' (region B) are dead from here
 
     // ---------------- phase 3: dL = -tril(dR X^T, -1) ----------------
     for (int tix = w; tix < 10; tix += 8) {
@@ -1237,7 +1256,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
-            sm.rb.dL[t][sx] = (sx < t) ? -acc[e] : 0.f;
+            sdL[t * LDL + sx] = (sx < t) ? -acc[e] : 0.f;
         }
     }
     __syncthreads();
@@ -1248,7 +1267,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
 #pragma unroll
         for (int c = 0; c < C / 8; ++c) {
             const int sx = qd * (C / 8) + c;
-            acc += sm.rb.dL[t][sx] * sm.akk[t][sx];
+            acc += sdL[t * LDL + sx] * sm.akk[t][sx];
         }
         acc += __shfl_xor(acc, 1, 64);
         acc += __shfl_xor(acc, 2, 64);
@@ -1278,7 +1297,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                 for (int j = 0; j < NB; ++j) {
                     if (j > i) continue;
                     const Frag4 B = colfrag(&s.kr[0][0], LDK, BS * j);
-                    const float4 x = *reinterpret_cast<const float4*>(&sm.rb.dL[BS * i + r16][BS * j + 4 * g4]);
+                    const float4 x = *reinterpret_cast<const float4*>(sdL + (BS * i + r16) * LDL + BS * j + 4 * g4);
                     const float pv[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
                     const f32x4 Pk = mma4f<1>(frag4_from_f32<1>(pv), B, zero4());
                     const f32x4 Pq = mma4f<1>(ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * i, BS * j), B, zero4());
@@ -1309,7 +1328,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int t = BS * i + 4 * g4 + e;
-                        pv[e] = s.beta[t] * sm.rb.dL[t][BS * j + r16];      // dP^T
+                        pv[e] = s.beta[t] * sdL[t * LDL + BS * j + r16];   // dP^T
                         av[e] = ld1<ST>(&sm.dA[t][BS * j + r16]);           // dA^T
                     }
                     f32x4 P = mma4f<1>(frag4_from_f32<1>(pv), colfrag(&s.kl[0][0], LDK, BS * i), zero4());
@@ -1338,14 +1357,14 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                         const float gs = s.g[sx][d];
                         if (sx <= t) {
                             const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - gs);
-                            const float pp = bt * sm.rb.dL[t][sx], pa = ld1<ST>(&sm.dA[t][sx]);
+                            const float pp = bt * sdL[t * LDL + sx], pa = ld1<ST>(&sm.dA[t][sx]);
                             ak += pp * ks;
                             aq += pa * ks;
                             ag += (pp * kx[mm][e] + pa * qx[mm][e]) * ks;
                         }
                         if (sx >= t) {
                             const float ex = kexp<PREC>(gs - gt);
-                            const float pp = s.beta[sx] * sm.rb.dL[sx][t], pa = ld1<ST>(&sm.dA[sx][t]);
+                            const float pp = s.beta[sx] * sdL[sx * LDL + t], pa = ld1<ST>(&sm.dA[sx][t]);
                             const float c = (pp * ld1<ST>(&s.kr[sx][d]) + pa * ld1<ST>(&s.ql[sx][d])) * ex;
                             ak += c;
                             ag -= c * kx[mm][e];
