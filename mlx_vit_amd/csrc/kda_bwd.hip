@@ -971,6 +971,15 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     tdh.store(&sm.ra.p1.dh[0][0], LDK);
     __syncthreads();
 
+    // Split A fragments of the phase-2 solve, written once by the waves that form
+    // A_kk and the inverses (anchored path), read by every solving wave with one
+    // 16-byte read per lane: fc[64 i + lane] = T_ii^T, fc[64 (4 + p) + lane] =
+    // A_ij = -L_ji^T for pair p = (j, i), j > i.  They live in the g region, dead
+    // on this path from here until dL takes it in phase 3 (D >= 64: at D = 32
+    // the region is too small and the solve reads A_kk and the inverses).
+    constexpr bool FC = 10 * 64 * sizeof(Frag4) <= sizeof(s.g);
+    Frag4* fc = reinterpret_cast<Frag4*>(&s.g[0][0]);
+
     // ---------------- recomputed intermediates ----------------
     // A_kk = strict-lower(K K^T . decay), formed as the prep kernel forms it, its
     // diagonal-block inverses, and V' = U - W h (h is the chunk-start state in the
@@ -992,6 +1001,14 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         for (int e = 0; e < 4; ++e) {
             const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
             sm.akk[t][sx] = (sx < t) ? P[e] : 0.f;
+        }
+        if (FC && j < i) {
+            // this lane's P[e] = A_kk[16i + 4 g4 + e][16j + r16] is exactly what the
+            // same lane of A_ji = -L_ij^T holds: A[r16][4 g4 + e]
+            float lv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) lv[e] = -s.beta[BS * i + 4 * g4 + e] * P[e];
+            fc[64 * (4 + pair_idx(i, j)) + l] = frag4_from_f32<3>(lv);
         }
     };
     auto vp_tile = [&](int tix) __attribute__((always_inline)) {
@@ -1022,7 +1039,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         if (w < NB) {
             akk_tile(w, w);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back its own tile
-            diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii);
+            diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii, FC ? fc : nullptr);
         } else {
             constexpr int OFF[6] = {1, 3, 4, 6, 7, 8};   // tile_ij indices of the blocks below the diagonal
             for (int o = w - NB; o < 6; o += 8 - NB) {
@@ -1059,6 +1076,45 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     f32x4 dqa[MB], dka[MB], dga[MB], dWt[NB];
     float dgcol = 0.f, part = 0.f;
 
+    // Operands of the phase-2 solve, read now so that their LDS latency hides
+    // behind phase 1: T_ii^T and A_ij = -L_ji^T blocks, and (rh = 1) Y = dV'.
+    f32x4 Y[NB];
+    Frag4 At[NB], Aij[6];
+    if (own) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            if (rh) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) Y[i][e] = ld1<ST>(&sm.rb.p2.dVp[BS * i + 4 * g4 + e][d]);
+            }
+        if (FC && !unsafe) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) At[i] = fc[64 * i + l];
+#pragma unroll
+            for (int p = 0; p < 6; ++p) Aij[p] = fc[64 * (4 + p) + l];
+        } else {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                float tv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tv[e] = sm.tii[i][4 * g4 + e][r16];     // A[a][b] = T_ii[b][a]
+                At[i] = frag4_from_f32<3>(tv);
+            }
+#pragma unroll
+            for (int j = 1; j < NB; ++j)
+#pragma unroll
+                for (int i = 0; i < j; ++i) {
+                    float av[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int rb = BS * j + 4 * g4 + e;
+                        av[e] = -s.beta[rb] * sm.akk[rb][BS * i + r16];
+                    }
+                    Aij[pair_idx(j, i)] = frag4_from_f32<3>(av);
+                }
+        }
+    }
+
     // ---------------- phase 1: products over dv ----------------
     {
         const ST* sdO = &sm.ra.p1.dO[0][0];
@@ -1091,12 +1147,16 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     dWt[m] = negacc(dW);
                 }
             }
-            // state-decay term of dG (rh = 1 waves): e^G sum_col dh[d][col] h[d][col]
+            // state-decay term of dG (rh = 1 waves): e^G sum_col dh[d][col] h[d][col],
+            // lane (g4, d) over columns 16 g4 .. 16 g4 + 15 in 16-byte reads
             if (rh == 1) {
 #pragma unroll
-                for (int c = 0; c < D / 4; ++c) {
-                    const int cc = g4 * (D / 4) + c;
-                    part += ld1<ST>(sdh + d * LDK + cc) * ld1<ST>(sh + d * LDK + cc);
+                for (int c8 = 0; c8 < D / 4; c8 += 8) {
+                    const int cc = g4 * (D / 4) + c8;
+                    const Vec16<ST> x{*reinterpret_cast<const uint4*>(sdh + d * LDK + cc)};
+                    const Vec16<ST> y{*reinterpret_cast<const uint4*>(sh + d * LDK + cc)};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) part += x.get(e) * y.get(e);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -1122,9 +1182,10 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             part = sum4g(part);
             if (rh == 0 && g4 == 0) xg[d] = dgcol;
         }
-        // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves, the rh = 1 waves
-        // first (the rh = 0 waves carry the extra dW blocks)
-        for (int tix = (w + 4) & 7; tix < 10; tix += 8) {
+        // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves, one each for the
+        // rh = 1 waves (they also form the state-decay term), the rest for the
+        // rh = 0 waves (whose solve starts from registers)
+        for (int tix = (w < 4) ? w + 4 : w - 4; tix < 10; tix += (w < 4) ? 4 : 10) {
             int i, j;
             tile_ij(tix, i, j);
             Frag8 A[D / 32], B[D / 32];
@@ -1153,34 +1214,10 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         // Right-looking block back substitution: as soon as dR_j is known, every
         // earlier block is updated, Y_i += A_ij dR_j with
         // A_ij[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a].
-        const ST* sdVp = &sm.rb.p2.dVp[0][0];
-        f32x4 Y[NB];
-        Frag4 At[NB], Aij[6];
+        if (!rh) {
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            if (rh) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) Y[i][e] = ld1<ST>(sdVp + (BS * i + 4 * g4 + e) * LDK + d);
-            } else {
-                Y[i] = dWt[i];
-            }
-            float tv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) tv[e] = sm.tii[i][4 * g4 + e][r16];     // A[a][b] = T_ii[b][a]
-            At[i] = frag4_from_f32<3>(tv);
+            for (int i = 0; i < NB; ++i) Y[i] = dWt[i];
         }
-#pragma unroll
-        for (int j = 1; j < NB; ++j)
-#pragma unroll
-            for (int i = 0; i < j; ++i) {
-                float av[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int rb = BS * j + 4 * g4 + e;
-                    av[e] = -s.beta[rb] * sm.akk[rb][BS * i + r16];
-                }
-                Aij[pair_idx(j, i)] = frag4_from_f32<3>(av);
-            }
 #pragma unroll
         for (int j = NB - 1; j >= 0; --j) {
             X[j] = mma4f<3>(At[j], accfrag4<3>(Y[j]), zero4());

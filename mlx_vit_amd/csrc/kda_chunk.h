@@ -283,9 +283,12 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag) {
 // column c.  All 36 row reads of the block's strict lower part are issued
 // before the substitution starts (one LDS round trip instead of one per row);
 // beta_t scales the row sum: x_t = [t == c] - beta_t sum_{s<t} Akk[t][s] x_s.
+// With fc != nullptr the block's transpose is also written as split (PREC 3)
+// MFMA A fragments, fc[64 w + lane] = fragment of lane (g, r) holding
+// T_ww[4g + e][r], so that other waves load it with one 16-byte read per lane.
 template <int LDA>
 __device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, const float* __restrict__ beta,
-                                                 float (*tii)[BS][BS + 4]) {
+                                                 float (*tii)[BS][BS + 4], Frag4* fc = nullptr) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), c = threadIdx.x & 63;
     if (c < BS) {
         const float* Ab = akk + (size_t)(BS * w) * LDA + BS * w;
@@ -313,6 +316,10 @@ __device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, 
         }
 #pragma unroll
         for (int t = 0; t < BS; ++t) tii[w][t][c] = x[t];
+        if (fc) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) fc[64 * w + 16 * g + c] = frag4_from_f32<3>(&x[4 * g]);
+        }
     }
 }
 
