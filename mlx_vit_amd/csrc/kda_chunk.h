@@ -196,26 +196,29 @@ struct ChunkSmem {
     float beta[C];
 };
 
-// All 16-byte loads of one chunk of q, k, g (and optionally v) are issued
-// before anything is written to LDS.  Rows >= valid are zero.  Returns 1 if
-// this thread saw g > 0 or a NaN.
+// All 16-byte loads of one chunk of q, k, g, beta (and optionally v) are issued
+// before anything is written to LDS; every wave's q, k, g, beta requests enter
+// the memory pipeline before any v request.  v stays in tv for the caller to
+// store once its latency is hidden.  Rows >= valid are zero.  Returns 1 if this
+// thread saw g > 0 or a NaN.
 template <int D, typename ST, typename TG, bool WITH_V>
-__device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, ST* sv, int ldv, const ST* __restrict__ q,
+__device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& tv, const ST* __restrict__ q,
                                            const ST* __restrict__ k, const ST* __restrict__ v,
                                            const TG* __restrict__ g, const ST* __restrict__ beta, size_t base,
                                            size_t rstride, size_t bbase, int H, int valid) {
-    Tile<ST, C, D> tq, tk, tv;
+    Tile<ST, C, D> tq, tk;
     Tile<TG, C, D> tg;
     tq.load(q + base, rstride, valid);
     tk.load(k + base, rstride, valid);
     tg.load(g + base, rstride, valid);
-    if constexpr (WITH_V) tv.load(v + base, rstride, valid);
     const int tid = threadIdx.x;
     const float braw = ld1<ST>(beta + bbase + (size_t)min(tid, valid - 1) * H);
-    const float bt = (tid < valid) ? braw : 0.f;
+    if constexpr (WITH_V) {
+        __builtin_amdgcn_s_barrier();
+        tv.load(v + base, rstride, valid);
+    }
     tq.store(&s.ql[0][0], ChunkSmem<D, ST>::LDK);
     tk.store(&s.kr[0][0], ChunkSmem<D, ST>::LDK);
-    if constexpr (WITH_V) tv.store(sv, ldv);
     int flag = 0;
     constexpr int EPV = Tile<TG, C, D>::EPV, VPR = Tile<TG, C, D>::VPR;
 #pragma unroll
@@ -230,7 +233,7 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, ST* sv, int ldv,
             if (!(gv <= 0.f)) flag = 1;
         }
     }
-    if (tid < C) s.beta[tid] = bt;
+    if (tid < C) s.beta[tid] = (tid < valid) ? braw : 0.f;
     __syncthreads();
     return flag;
 }

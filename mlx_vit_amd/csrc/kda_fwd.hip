@@ -90,9 +90,9 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     const bool bwd = oAqkT != nullptr;
     const bool stT = bwd && oAqk == nullptr;   // Aqk staged transposed (backward-only outputs)
 
-    // PHASE 0 (load)
-    const int flag = chunk_load2<D, ST, TG, G::STAGE_V>(s, &svbuf[0][0], LDK, q, k, v, g, beta, base, rs, bbase,
-                                                        a.H, valid);
+    // PHASE 0 (load); v stays in registers until the column pass is done
+    Tile<ST, C, D> tv;
+    const int flag = chunk_load2<D, ST, TG, G::STAGE_V>(s, tv, q, k, v, g, beta, base, rs, bbase, a.H, valid);
     // PHASE 1
     chunk_cumsum2<D, ST>(s);
     const int unsafe = chunk_factors2<D, ST, PREC>(s, flag);
@@ -167,6 +167,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             if (oQpT) store_vec<ST>(oQpT + cCD + (size_t)d * C + tb, oqp);
         }
     }
+    if constexpr (G::STAGE_V) tv.store(&svbuf[0][0], LDK);   // first read by the forward substitution
     __syncthreads();
     // PHASE 4
 
