@@ -1348,6 +1348,282 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
     }
 }
 
+// ----------------------------------------------------------------------------
+// kda_recur4_kernel: kda_recur3_kernel with the per-chunk work split between
+// two wave roles, so that one wave per SIMD runs the state chain while the
+// other does the work off it.  512 threads; role 0 = waves 0-3 (chain), role 1
+// = waves 4-7.  Wave wr = w % 4 of a role owns row block wr of the chunk tiles.
+//   chain waves: V' = U - W S (row block wr), write V'^T; after B: state update
+//                of state rows wr, wr + 4, write S^T (MODE 1: and h); read the
+//                next chunk's W, U, Kb^T, e^G operands
+//   role-1 waves: flush the previous chunk's outputs; MODE 0: O = Qp S + Aqk V'
+//                (row block wr) after B, read the next chunk's Qp, Aqk operands
+//   DMA: chunk n+NS is brought after barrier B(n), once chunk n's operands (the
+//        chain waves read its Kb^T and e^G between A(n) and B(n)) have left its
+//        LDS set: MODE 0 the chain waves bring W, U, Kb^T, e^G after their state
+//        update and the role-1 waves Qp, Aqk; MODE 1 the role-1 waves bring all.
+// The barriers, LDS sets and staging are those of kda_recur3_kernel.
+// ----------------------------------------------------------------------------
+template <int D, int MODE, int CS>
+__global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
+    using ST = uint16_t;
+    using Lay = Recur3Layout<D, MODE, CS>;
+    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4, NS = Lay::NS;
+    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
+    constexpr int RB_W = Lay::RB_W, RB_U = Lay::RB_U, RB_C = Lay::RB_C;
+    __shared__ __align__(1024) char set0[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set1[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set2[NS == 3 ? Lay::SET_BYTES : 16];
+    __shared__ __align__(16) char smem[Lay::XBYTES];
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 8);
+    const int role = w >> 2, wr = w & 3;
+    const int lb = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int nc = a.nc;
+    const char* gW = static_cast<const char*>(a.W);
+    const char* gU = static_cast<const char*>(a.U);
+    const char* gQp = static_cast<const char*>(a.Qp);
+    const char* gKbT = static_cast<const char*>(a.KbT);
+    const char* gAqk = static_cast<const char*>(a.Aqk);
+    const char* gEg = reinterpret_cast<const char*>(a.eG);
+
+    auto stg = [&](int c) __attribute__((always_inline)) {
+        return reinterpret_cast<ST*>(smem + Lay::STG_OFF + (c % Lay::NSTG) * Lay::STG_BYTES);
+    };
+    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
+    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
+
+    using TW = DmaTile<C, RB_W, 4>;
+    using TU = DmaTile<C, RB_U, 4>;
+    using TK = DmaTile<D, RB_C, 4>;
+    using TA = DmaTile<C, RB_C, 4>;
+    // which role brings the state-chain slabs (W, U, Kb^T, e^G) and how many DMA
+    // instructions per chunk this wave issues
+    constexpr int CHAIN_ROLE = (MODE == 0) ? 0 : 1;
+    constexpr int L_CHAIN = TW::COUNT + TU::COUNT + TK::COUNT + 1;
+    constexpr int L_OUT = (MODE == 0) ? TW::COUNT + TA::COUNT : 0;
+    constexpr int L0 = (CHAIN_ROLE == 0) ? L_CHAIN : 0;
+    constexpr int L1 = ((CHAIN_ROLE == 1) ? L_CHAIN : 0) + L_OUT;
+    const bool chain_dma = role == CHAIN_ROLE;
+    uint32_t oW[TW::COUNT], oU[TU::COUNT], oK[TK::COUNT], oA[TA::COUNT];
+    TW::offsets(oW, RB_W, wr, l);
+    TU::offsets(oU, (size_t)D * 2, wr, l);
+    TK::offsets(oK, RB_C, wr, l);
+    TA::offsets(oA, RB_C, wr, l);
+    const uint32_t oE = (uint32_t)((D / 4) * 4 * wr + 16 * (l < D / 16 ? l : 0));
+    auto dma_chunk = [&](int c, char* sb) __attribute__((always_inline)) {
+        const size_t ch = (size_t)bh * nc + c;
+        if (chain_dma) {
+            TW::issue_s(gW + ch * C * D * 2, oW, sb + Lay::W_OFF, wr);
+            TU::issue_s(gU + (ch * C * D + c0) * 2, oU, sb + Lay::U_OFF, wr);
+            TK::issue_s(gKbT + ch * C * D * 2, oK, sb + Lay::KBT_OFF, wr);
+            if (l < D / 16) dma16_s(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + D * wr);
+        }
+        if constexpr (MODE == 0) {
+            if (role == 1) {
+                TW::issue_s(gQp + ch * C * D * 2, oW, sb + Lay::QP_OFF, wr);
+                TA::issue_s(gAqk + ch * C * C * 2, oA, sb + Lay::AQK_OFF, wr);
+            }
+        }
+    };
+    // this wave's DMA of all but the last k chunks in flight complete
+    auto dma_wait_own = [&](int k) __attribute__((always_inline)) {
+        if (role == 0) {
+            if constexpr (L0 > 0) dma_wait_chunks<L0>(k);
+        } else {
+            if constexpr (L1 > 0) dma_wait_chunks<L1>(k);
+        }
+    };
+    auto flush = [&](int n) __attribute__((always_inline)) {   // role-1 waves
+        const ST* sst = stg(n);
+        const int t1 = tid - 256;
+        if constexpr (MODE == 0) {
+            const int t0 = n * C, valid = min(C, a.T - t0);
+            tile_out_at<ST, C, DC>(t1, sst, LDU,
+                                   static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
+                                   (size_t)a.H * D, valid);
+        } else {
+            const size_t ch = (size_t)bh * nc + n;
+            tile_out_at<ST, D, DC>(t1, sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
+        }
+    };
+
+    int mt[MT];
+    bool own[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        mt[i] = wr + 4 * i;
+        own[i] = role == 0 && mt[i] < NT;
+    }
+    f32x4 S[MT][NTW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            S[i][j] = zero4();
+            if (own[i] && a.s0) {
+                const float4 x = *reinterpret_cast<const float4*>(
+                    a.s0 + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4);
+                S[i][j] = f32x4{x.x, x.y, x.z, x.w};
+            }
+        }
+    // S^T for the B operands (and, for the backward, the chunk-start state)
+    auto put_state = [&](ST* sst) __attribute__((always_inline)) {   // chain waves
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(S[i][j]);
+                    if constexpr (MODE == 1)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
+                }
+    };
+
+    // one chunk's A operands, read ahead from its LDS set (each role its own)
+    Frag8 Aw[D / 32], Aq[D / 32], Aa[2], Akb[MT][C / 32];
+    f32x4 Uv[NTW];
+    float4 eg[MT];
+    // chain waves: the state-update operands (Kb^T rows, e^G) of a chunk, read
+    // after its V' is out (they are needed only after barrier B)
+    auto preload_kb = [&](const char* sb) __attribute__((always_inline)) {
+        const ST* sKbT = reinterpret_cast<const ST*>(sb + Lay::KBT_OFF);
+        const float* seG = reinterpret_cast<const float*>(sb + Lay::EG_OFF);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) Akb[i][ks] = ldfrag_sw<RB_C>(sKbT, BS * mt[i], 32 * ks);
+                eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
+            }
+    };
+    auto preload = [&](const char* sb) __attribute__((always_inline)) {
+        if (role == 0) {
+            const ST* sW = reinterpret_cast<const ST*>(sb + Lay::W_OFF);
+            const ST* sU = reinterpret_cast<const ST*>(sb + Lay::U_OFF);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Aw[ks] = ldfrag_sw<RB_W>(sW, BS * wr, 32 * ks);
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) Uv[j][e] = ld_sw<RB_U>(sU, BS * wr + 4 * g4 + e, BS * j + r16);
+        } else if constexpr (MODE == 0) {
+            const ST* sQp = reinterpret_cast<const ST*>(sb + Lay::QP_OFF);
+            const ST* sAqk = reinterpret_cast<const ST*>(sb + Lay::AQK_OFF);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Aq[ks] = ldfrag_sw<RB_W>(sQp, BS * wr, 32 * ks);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (ks <= wr / 2) Aa[ks] = ldfrag_sw<RB_C>(sAqk, BS * wr, 32 * ks);
+        }
+    };
+
+    // prologue: chunks 0 .. NS-1 in flight, chunk 0 landed and read
+    if (role == 0) put_state(stg(0));
+    dma_chunk(0, set0);
+    if (nc > 1) dma_chunk(1, set1);
+    if (NS == 3 && nc > 2) dma_chunk(2, set2);
+    dma_wait_own(min(NS, nc) - 1);
+    lds_barrier();
+    preload(set0);
+
+    auto step = [&](int n, char* sdma, const char* snext, const char* scur) __attribute__((always_inline)) {
+        ST* sst = stg(n);
+        lds_barrier();                                          // A(n): S^T of chunk n in xs
+        Frag8 Bs[NTW][D / 32];
+        if (role == 0 || MODE == 0) {
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, BS * j, 32 * ks);
+        }
+        if (role == 0) {
+            // V' = U - W S, row block wr
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                f32x4 P = zero4();
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) P = mma<1>(Aw[ks], Bs[j][ks], P);
+                f32x4 Vp;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) Vp[e] = Uv[j][e] - P[e];
+                *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * wr + 4 * g4) = pack4bf(Vp);
+            }
+            preload_kb(scur);
+        } else {
+            if (n > 0) flush(n - 1);
+        }
+        // chunk n+1's slabs landed; chunks up to n+NS-1 (issued after earlier B
+        // barriers) may stay in flight
+        dma_wait_own(min(nc - 1, n + NS - 1) - (n + 1));
+        lds_barrier();                                          // B(n): V'^T in xv, chunk n+1 visible
+        // set n % NS is free now (chunk n's operands are all in registers); the
+        // chain waves bring their share after the state update
+        if (role == 1 && n + NS < nc) dma_chunk(n + NS, sdma);
+
+        Frag8 Bv[NTW][C / 32];
+        if (role == 0 || MODE == 0) {
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) Bv[j][ks] = ldfrag<1, ST>(xv, LDC, BS * j, 32 * ks);
+        }
+        if (role == 0) {
+            // S <- diag(e^G) S + Kb^T V'
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+                if (own[i]) {
+#pragma unroll
+                    for (int j = 0; j < NTW; ++j) {
+                        S[i][j] = f32x4{S[i][j][0] * eg[i].x, S[i][j][1] * eg[i].y, S[i][j][2] * eg[i].z,
+                                        S[i][j][3] * eg[i].w};
+#pragma unroll
+                        for (int ks = 0; ks < C / 32; ++ks) S[i][j] = mma<1>(Akb[i][ks], Bv[j][ks], S[i][j]);
+                    }
+                }
+            if (n + 1 < nc) put_state(stg(n + 1));
+            if (n + NS < nc) dma_chunk(n + NS, sdma);
+        } else if constexpr (MODE == 0) {
+            // O = Qp S + Aqk V', row block wr (the chunk-start state is in Bs)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                f32x4 O = zero4();
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) O = mma<1>(Aq[ks], Bs[j][ks], O);
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    if (ks <= wr / 2) O = mma<1>(Aa[ks], Bv[j][ks], O);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) st1<ST>(sst + (BS * wr + 4 * g4 + e) * LDU + BS * j + r16, O[e]);
+            }
+        }
+        if (n + 1 < nc) preload(snext);
+    };
+    // unrolled NS times so that every set is named statically
+    for (int n = 0; n < nc; n += NS) {
+        step(n, set0, set1, set0);
+        if (n + 1 < nc) step(n + 1, set1, NS == 3 ? set2 : set0, set1);
+        if (NS == 3 && n + 2 < nc) step(n + 2, set2, set0, set2);
+    }
+    lds_barrier();
+    if (role == 1) flush(nc - 1);
+
+    if (MODE == 0 && a.s_final) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j)
+                    *reinterpret_cast<float4*>(a.s_final + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4) =
+                        make_float4(S[i][j][0], S[i][j][1], S[i][j][2], S[i][j][3]);
+    }
+}
+
 template <int D, int CS>
 struct Dh3Layout {
     static constexpr int DC = D / CS, NS = 3;
@@ -1614,7 +1890,10 @@ template <int D> struct RowSplit { static constexpr int CS = (D >= 128) ? 4 : 2;
 
 template <int D, typename ST, int MODE>
 static hipError_t launch_recur_t(const RecurArgs& a, hipStream_t st) {
-    if constexpr (std::is_same<ST, uint16_t>::value && D >= 64) {
+    if constexpr (std::is_same<ST, uint16_t>::value && D == 64) {
+        constexpr int CS2 = RowSplit<D>::CS;
+        hipLaunchKernelGGL((kda_recur4_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
+    } else if constexpr (std::is_same<ST, uint16_t>::value && D >= 64) {
         constexpr int CS2 = RowSplit<D>::CS;
         hipLaunchKernelGGL((kda_recur3_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(256), 0, st, a);
     } else if constexpr (std::is_same<ST, uint16_t>::value) {
