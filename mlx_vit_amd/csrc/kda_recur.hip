@@ -1881,6 +1881,276 @@ __global__ __launch_bounds__(256) void kda_dh3_kernel(const DhArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// kda_dh4_kernel: kda_dh3_kernel with the work split between two wave roles
+// (512 threads).  Waves 0-3 run the reverse state chain: dV' (row block wr),
+// the dS update of state rows wr, wr + 4, dS^T / dh / dV' staging, and read
+// the next chunk's operands.  Waves 4-7 flush the staged dh and dV', bring the
+// slabs by DMA (after barrier B, when the step's set is free), and transpose
+// the next chunk's dO tile into dOT so that the chain waves read it as B
+// fragments with row reads instead of column gathers.  Two staging tiles
+// suffice: a tile is flushed before barrier B and refilled after it.
+// ----------------------------------------------------------------------------
+template <int D, int CS>
+struct Dh4Layout {
+    using B3 = Dh3Layout<D, CS>;
+    static constexpr int DC = B3::DC, NS = B3::NS, SET_BYTES = B3::SET_BYTES;
+    static constexpr int LDR = B3::LDR, LDU = B3::LDU, LDC = B3::LDC, LDO = C + 4;
+    static constexpr int XS_OFF = B3::XS_OFF, XV_OFF = B3::XV_OFF;
+    static constexpr int DOT_OFF = B3::STG_OFF;                                // dO^T [2][DC][LDO] bf16
+    static constexpr int DOT_BYTES = DC * LDO * 2;
+    static constexpr int STG_OFF = DOT_OFF + 2 * DOT_BYTES;
+    static constexpr int STG_BYTES = B3::STG_BYTES, NSTG = 2;
+    static constexpr int XBYTES = STG_OFF + NSTG * STG_BYTES;
+    static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "reverse recurrence LDS");
+    static_assert(DOT_OFF % 16 == 0 && STG_OFF % 16 == 0, "16-byte aligned tiles");
+};
+
+template <int D, int CS>
+__global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
+    using ST = uint16_t;
+    using B3 = Dh3Layout<D, CS>;
+    using Lay = Dh4Layout<D, CS>;
+    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4, NS = Lay::NS;
+    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC, LDO = Lay::LDO;
+    constexpr int RB_D = B3::RB_D, RB_C = B3::RB_C, RB_U = B3::RB_U;
+    static_assert(NS == 3, "three DMA sets");
+    __shared__ __align__(1024) char set0[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set1[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set2[Lay::SET_BYTES];
+    __shared__ __align__(16) char smem[Lay::XBYTES];
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 8);
+    const int role = w >> 2, wr = w & 3;
+    const int lb = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int nc = a.nc;
+    const char* gAqkT = static_cast<const char*>(a.AqkT);
+    const char* gKb = static_cast<const char*>(a.Kb);
+    const char* gQpT = static_cast<const char*>(a.QpT);
+    const char* gWT = static_cast<const char*>(a.WT);
+    const char* gdO = static_cast<const char*>(a.dout);
+    const char* gEg = reinterpret_cast<const char*>(a.eG);
+
+    auto stg = [&](int k) __attribute__((always_inline)) {
+        return reinterpret_cast<ST*>(smem + Lay::STG_OFF + (k % Lay::NSTG) * Lay::STG_BYTES);
+    };
+    auto dot = [&](int k) __attribute__((always_inline)) {
+        return reinterpret_cast<ST*>(smem + Lay::DOT_OFF + (k & 1) * Lay::DOT_BYTES);
+    };
+    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
+    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
+
+    // step k's slabs (chunk nc-1-k) -> LDS set (k % NS), by the role-1 waves
+    using TA = DmaTile<C, RB_C, 4>;
+    using TB = DmaTile<C, RB_D, 4>;
+    using TQ = DmaTile<D, RB_C, 4>;
+    using TO = DmaTile<C, RB_U, 4>;
+    constexpr int L = B3::L;
+    uint32_t oA[TA::COUNT], oB[TB::COUNT], oQ[TQ::COUNT], oO[TO::COUNT];
+    TA::offsets(oA, RB_C, wr, l);
+    TB::offsets(oB, RB_D, wr, l);
+    TQ::offsets(oQ, RB_C, wr, l);
+    TO::offsets(oO, (size_t)a.H * D * 2, wr, l);
+    const uint32_t oE = (uint32_t)((D / 4) * 4 * wr + 16 * (l < D / 16 ? l : 0));
+    auto dma_step = [&](int k, char* sb) __attribute__((always_inline)) {
+        const int n = nc - 1 - k;
+        const size_t ch = (size_t)bh * nc + n;
+        const int t0 = n * C, valid = min(C, a.T - t0);
+        TA::issue_s(gAqkT + ch * C * C * 2, oA, sb + B3::AQKT_OFF, wr);
+        TB::issue_s(gKb + ch * C * D * 2, oB, sb + B3::KB_OFF, wr);
+        TQ::issue_s(gQpT + ch * C * D * 2, oQ, sb + B3::QPT_OFF, wr);
+        TQ::issue_s(gWT + ch * C * D * 2, oQ, sb + B3::WT_OFF, wr);
+        const char* gdo = gdO + ((((size_t)b * a.T + t0) * a.H + h) * D + c0) * 2;
+        if (valid == C) TO::issue_s(gdo, oO, sb + B3::DO_OFF, wr);
+        else TO::issue(gdo, (size_t)a.H * D * 2, sb + B3::DO_OFF, wr, l, valid);
+        if (l < D / 16) dma16_s(gEg + ch * D * 4, oE, sb + B3::EG_OFF + D * wr);
+    };
+    // dO tile of a set -> dOT[n][t] (role-1 waves; rows past T read as zero)
+    auto transpose_do = [&](int k, const char* sb) __attribute__((always_inline)) {
+        const ST* sdO = reinterpret_cast<const ST*>(sb + B3::DO_OFF);
+        ST* o = dot(k);
+        const int t1 = tid - 256, nn = t1 % DC, tg = t1 / DC;      // column, group of 8 rows
+        const int valid = a.T - (nc - 1 - k) * C;
+        for (int g8 = tg; g8 < C / 8; g8 += 256 / DC) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = 8 * g8 + e;
+                v[e] = (t < valid) ? ld_sw<RB_U>(sdO, t, nn) : 0.f;
+            }
+            const short4v lo = pack4(v), hi = pack4(v + 4);
+            *reinterpret_cast<short4v*>(o + nn * LDO + 8 * g8) = lo;
+            *reinterpret_cast<short4v*>(o + nn * LDO + 8 * g8 + 4) = hi;
+        }
+    };
+    auto flush = [&](int k) __attribute__((always_inline)) {   // role-1 waves
+        const ST* sst = stg(k);
+        const int t1 = tid - 256;
+        const size_t ch = (size_t)bh * nc + (nc - 1 - k);
+        tile_out_at<ST, D, DC>(t1, sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
+        tile_out_at<ST, C, DC>(t1, sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
+    };
+
+    int mt[MT];
+    bool own[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        mt[i] = wr + 4 * i;
+        own[i] = role == 0 && mt[i] < NT;
+    }
+    f32x4 dS[MT][NTW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            dS[i][j] = zero4();
+            if (own[i] && a.dsf) {
+                const float4 x = *reinterpret_cast<const float4*>(
+                    a.dsf + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4);
+                dS[i][j] = f32x4{x.x, x.y, x.z, x.w};
+            }
+        }
+    auto put_state = [&](ST* sst) __attribute__((always_inline)) {   // chain waves
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(dS[i][j]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, dS[i][j][e]);
+                }
+    };
+
+    Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
+    float4 eg[MT];
+    auto preload = [&](int k, const char* sb) __attribute__((always_inline)) {   // chain waves
+        const ST* sAqkT = reinterpret_cast<const ST*>(sb + B3::AQKT_OFF);
+        const ST* sKb = reinterpret_cast<const ST*>(sb + B3::KB_OFF);
+        const ST* sQpT = reinterpret_cast<const ST*>(sb + B3::QPT_OFF);
+        const ST* sWT = reinterpret_cast<const ST*>(sb + B3::WT_OFF);
+        const float* seG = reinterpret_cast<const float*>(sb + B3::EG_OFF);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            if (ks >= wr / 2) Aat[ks] = ldfrag_sw<RB_C>(sAqkT, BS * wr, 32 * ks);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) Akb[ks] = ldfrag_sw<RB_D>(sKb, BS * wr, 32 * ks);
+        const ST* o = dot(k);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) Bo[j][ks] = ldfrag<1, ST>(o, LDO, BS * j, 32 * ks);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i]) {
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) {
+                    Aqt[i][ks] = ldfrag_sw<RB_C>(sQpT, BS * mt[i], 32 * ks);
+                    Awt[i][ks] = ldfrag_sw<RB_C>(sWT, BS * mt[i], 32 * ks);
+                }
+                eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
+            }
+    };
+
+    // prologue: steps 0 .. NS-1 in flight; step 0's dO transposed, its operands read
+    if (role == 0) put_state(stg(0));
+    if (role == 1) {
+        dma_step(0, set0);
+        if (nc > 1) dma_step(1, set1);
+        if (nc > 2) dma_step(2, set2);
+        dma_wait_chunks<L>(min(NS, nc) - 1);
+    }
+    lds_barrier();
+    if (role == 1) transpose_do(0, set0);
+    lds_barrier();
+    if (role == 0) preload(0, set0);
+
+    // step k: chunk nc-1-k in set k % NS
+    auto step = [&](int k, char* scur, const char* snext) __attribute__((always_inline)) {
+        ST* sst = stg(k);
+        lds_barrier();                                          // A(k): dS^T in xs
+        if (role == 0) {
+            Frag8 Bs[NTW][D / 32];
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, BS * j, 32 * ks);
+            // dV' = Aqk^T dO + Kb dS, row block wr
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                f32x4 dV = zero4();
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    if (ks >= wr / 2) dV = mma<1>(Aat[ks], Bo[j][ks], dV);
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) dV = mma<1>(Akb[ks], Bs[j][ks], dV);
+                *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * wr + 4 * g4) = pack4bf(negacc(dV));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * wr + 4 * g4 + e) * LDU + BS * j + r16, dV[e]);
+            }
+        } else {
+            if (k > 0) flush(k - 1);
+            if (k + 1 < nc) {
+                // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight)
+                dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
+                transpose_do(k + 1, snext);
+            }
+        }
+        lds_barrier();                                          // B(k): -dV'^T in xv, dOT of k+1
+        if (role == 0) {
+            Frag8 Bvn[NTW][C / 32];    // -dV'
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) Bvn[j][ks] = ldfrag<1, ST>(xv, LDC, BS * j, 32 * ks);
+            // dS <- diag(e^G) dS + Qp^T dO - W^T dV'
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+                if (own[i]) {
+#pragma unroll
+                    for (int j = 0; j < NTW; ++j) {
+                        dS[i][j] = f32x4{dS[i][j][0] * eg[i].x, dS[i][j][1] * eg[i].y, dS[i][j][2] * eg[i].z,
+                                         dS[i][j][3] * eg[i].w};
+#pragma unroll
+                        for (int ks = 0; ks < C / 32; ++ks) {
+                            dS[i][j] = mma<1>(Awt[i][ks], Bvn[j][ks], dS[i][j]);
+                            dS[i][j] = mma<1>(Aqt[i][ks], Bo[j][ks], dS[i][j]);
+                        }
+                    }
+                }
+            if (k + 1 < nc) {
+                put_state(stg(k + 1));
+                preload(k + 1, snext);
+            }
+        } else {
+            // set k % NS is free: chunk k's operands are in the chain waves'
+            // registers and its dO was transposed in step k-1
+            if (k + NS < nc) dma_step(k + NS, scur);
+        }
+    };
+    for (int k = 0; k < nc; k += 3) {
+        step(k, set0, set1);
+        if (k + 1 < nc) step(k + 1, set1, set2);
+        if (k + 2 < nc) step(k + 2, set2, set0);
+    }
+    lds_barrier();
+    if (role == 1) flush(nc - 1);
+
+    if (a.ds0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (own[i])
+#pragma unroll
+                for (int j = 0; j < NTW; ++j)
+                    *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4) =
+                        make_float4(dS[i][j][0], dS[i][j][1], dS[i][j][2], dS[i][j][3]);
+    }
+}
+
+// ----------------------------------------------------------------------------
 // launchers
 // ----------------------------------------------------------------------------
 // D = 128 splits the state's dv columns over two workgroups per (batch, head)
@@ -1910,7 +2180,7 @@ template <int D, typename ST>
 static hipError_t launch_dh_t(const DhArgs& a, hipStream_t st) {
     if constexpr (std::is_same<ST, uint16_t>::value && D >= 64) {
         constexpr int CS2 = RowSplit<D>::CS;
-        hipLaunchKernelGGL((kda_dh3_kernel<D, CS2>), dim3(a.BH * CS2), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((kda_dh4_kernel<D, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
     } else if constexpr (std::is_same<ST, uint16_t>::value) {
         constexpr int CS2 = RowSplit<D>::CS;
         hipLaunchKernelGGL((kda_dh2_kernel<D, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
