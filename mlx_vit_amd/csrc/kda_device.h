@@ -495,6 +495,17 @@ __device__ __forceinline__ void dma16_s(const void* gbase, uint32_t off, void* l
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(gbase), "{m0}"(m) : "memory");
 }
 
+// 32-bit LDS address of a (non-null) shared-memory pointer, computed once so
+// that each DMA only adds a constant to it
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    __builtin_assume(p != nullptr);
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void_t*)p);
+}
+// dma16_s with the LDS destination as a 32-bit address (wave-uniform)
+__device__ __forceinline__ void dma16_s32(const void* gbase, uint32_t off, uint32_t m) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(gbase), "{m0}"(m) : "memory");
+}
+
 // s_waitcnt immediates (gfx9 layout: vmcnt [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
 template <int N>
 __device__ __forceinline__ void dma_wait() {
@@ -543,6 +554,12 @@ struct DmaTile {
     __device__ __forceinline__ static void issue_s(const char* g, const uint32_t (&off)[COUNT], char* lds, int first) {
 #pragma unroll
         for (int k = 0; k < COUNT; ++k) dma16_s(g, off[k], lds + 1024 * (first + STEP * k));
+    }
+    // the same with the destination as a 32-bit LDS address
+    __device__ __forceinline__ static void issue_s32(const char* g, const uint32_t (&off)[COUNT], uint32_t lds,
+                                                     int first) {
+#pragma unroll
+        for (int k = 0; k < COUNT; ++k) dma16_s32(g, off[k], lds + 1024 * (first + STEP * k));
     }
     __device__ __forceinline__ static void issue(const char* g, size_t GS, char* lds, int first, int lane,
                                                  int valid_rows = NR) {

@@ -1414,18 +1414,19 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
     TK::offsets(oK, RB_C, wr, l);
     TA::offsets(oA, RB_C, wr, l);
     const uint32_t oE = (uint32_t)((D / 4) * 4 * wr + 16 * (l < D / 16 ? l : 0));
-    auto dma_chunk = [&](int c, char* sb) __attribute__((always_inline)) {
+    auto dma_chunk = [&](int c, char* sbp) __attribute__((always_inline)) {
         const size_t ch = (size_t)bh * nc + c;
+        const uint32_t sb = lds_addr(sbp);
         if (chain_dma) {
-            TW::issue_s(gW + ch * C * D * 2, oW, sb + Lay::W_OFF, wr);
-            TU::issue_s(gU + (ch * C * D + c0) * 2, oU, sb + Lay::U_OFF, wr);
-            TK::issue_s(gKbT + ch * C * D * 2, oK, sb + Lay::KBT_OFF, wr);
-            if (l < D / 16) dma16_s(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + D * wr);
+            TW::issue_s32(gW + ch * C * D * 2, oW, sb + Lay::W_OFF, wr);
+            TU::issue_s32(gU + (ch * C * D + c0) * 2, oU, sb + Lay::U_OFF, wr);
+            TK::issue_s32(gKbT + ch * C * D * 2, oK, sb + Lay::KBT_OFF, wr);
+            if (l < D / 16) dma16_s32(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + D * wr);
         }
         if constexpr (MODE == 0) {
             if (role == 1) {
-                TW::issue_s(gQp + ch * C * D * 2, oW, sb + Lay::QP_OFF, wr);
-                TA::issue_s(gAqk + ch * C * C * 2, oA, sb + Lay::AQK_OFF, wr);
+                TW::issue_s32(gQp + ch * C * D * 2, oW, sb + Lay::QP_OFF, wr);
+                TA::issue_s32(gAqk + ch * C * C * 2, oA, sb + Lay::AQK_OFF, wr);
             }
         }
     };
@@ -1954,18 +1955,19 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     TQ::offsets(oQ, RB_C, wr, l);
     TO::offsets(oO, (size_t)a.H * D * 2, wr, l);
     const uint32_t oE = (uint32_t)((D / 4) * 4 * wr + 16 * (l < D / 16 ? l : 0));
-    auto dma_step = [&](int k, char* sb) __attribute__((always_inline)) {
+    auto dma_step = [&](int k, char* sbp) __attribute__((always_inline)) {
         const int n = nc - 1 - k;
         const size_t ch = (size_t)bh * nc + n;
         const int t0 = n * C, valid = min(C, a.T - t0);
-        TA::issue_s(gAqkT + ch * C * C * 2, oA, sb + B3::AQKT_OFF, wr);
-        TB::issue_s(gKb + ch * C * D * 2, oB, sb + B3::KB_OFF, wr);
-        TQ::issue_s(gQpT + ch * C * D * 2, oQ, sb + B3::QPT_OFF, wr);
-        TQ::issue_s(gWT + ch * C * D * 2, oQ, sb + B3::WT_OFF, wr);
+        const uint32_t sb = lds_addr(sbp);
+        TA::issue_s32(gAqkT + ch * C * C * 2, oA, sb + B3::AQKT_OFF, wr);
+        TB::issue_s32(gKb + ch * C * D * 2, oB, sb + B3::KB_OFF, wr);
+        TQ::issue_s32(gQpT + ch * C * D * 2, oQ, sb + B3::QPT_OFF, wr);
+        TQ::issue_s32(gWT + ch * C * D * 2, oQ, sb + B3::WT_OFF, wr);
         const char* gdo = gdO + ((((size_t)b * a.T + t0) * a.H + h) * D + c0) * 2;
-        if (valid == C) TO::issue_s(gdo, oO, sb + B3::DO_OFF, wr);
-        else TO::issue(gdo, (size_t)a.H * D * 2, sb + B3::DO_OFF, wr, l, valid);
-        if (l < D / 16) dma16_s(gEg + ch * D * 4, oE, sb + B3::EG_OFF + D * wr);
+        if (valid == C) TO::issue_s32(gdo, oO, sb + B3::DO_OFF, wr);
+        else TO::issue(gdo, (size_t)a.H * D * 2, sbp + B3::DO_OFF, wr, l, valid);
+        if (l < D / 16) dma16_s32(gEg + ch * D * 4, oE, sb + B3::EG_OFF + D * wr);
     };
     // dO tile of a set -> dOT[n][t] (role-1 waves; rows past T read as zero)
     auto transpose_do = [&](int k, const char* sb) __attribute__((always_inline)) {
@@ -2092,12 +2094,13 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
                 for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * wr + 4 * g4 + e) * LDU + BS * j + r16, dV[e]);
             }
         } else {
-            if (k > 0) flush(k - 1);
             if (k + 1 < nc) {
-                // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight)
+                // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight);
+                // waited for before this step's flush issues its stores
                 dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
                 transpose_do(k + 1, snext);
             }
+            if (k > 0) flush(k - 1);
         }
         lds_barrier();                                          // B(k): -dV'^T in xv, dOT of k+1
         if (role == 0) {
