@@ -444,10 +444,14 @@ __device__ __forceinline__ void tile_out_at(int t, const ST* lds, int lld, ST* _
 
 template <typename ST, int ROWS, int COLS, int NTH = 256>
 __device__ __forceinline__ void tile_out(const ST* lds, int lld, ST* __restrict__ g, size_t gld, int valid_rows) {
-    constexpr int EPV = 16 / (int)sizeof(ST), VPR = COLS / EPV, NV = ROWS * VPR;
-    for (int v = threadIdx.x; v < NV; v += NTH) {
+    constexpr int EPV = 16 / (int)sizeof(ST), VPR = COLS / EPV, NV = ROWS * VPR, PER = (NV + NTH - 1) / NTH;
+    // a fixed number of unrolled steps (no loop with a data-dependent count), so
+    // the compiler can count the stores in flight exactly
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int v = (int)threadIdx.x + NTH * i;
         const int row = v / VPR, c = (v - row * VPR) * EPV;
-        if (row < valid_rows)
+        if (v < NV && row < valid_rows)
             *reinterpret_cast<uint4*>(g + (size_t)row * gld + c) = *reinterpret_cast<const uint4*>(lds + row * lld + c);
     }
 }

@@ -1884,12 +1884,13 @@ __global__ __launch_bounds__(256) void kda_dh3_kernel(const DhArgs a) {
 // ----------------------------------------------------------------------------
 // kda_dh4_kernel: kda_dh3_kernel with the work split between two wave roles
 // (512 threads).  Waves 0-3 run the reverse state chain: dV' (row block wr),
-// the dS update of state rows wr, wr + 4, dS^T / dh / dV' staging, and read
-// the next chunk's operands.  Waves 4-7 flush the staged dh and dV', bring the
-// slabs by DMA (after barrier B, when the step's set is free), and transpose
-// the next chunk's dO tile into dOT so that the chain waves read it as B
-// fragments with row reads instead of column gathers.  Two staging tiles
-// suffice: a tile is flushed before barrier B and refilled after it.
+// the dS update of state rows wr, wr + 4, dS^T / dh / dV' staging, the flush
+// of the previous step's staged dh and dV', and read the next chunk's
+// operands.  Waves 4-7 bring the slabs by DMA (after barrier B, when the
+// step's set is free) and transpose the next chunk's dO tile into dOT so that
+// the chain waves read it as B fragments with row reads instead of column
+// gathers.  Two staging tiles suffice: a tile is flushed before barrier B and
+// refilled after it.
 // ----------------------------------------------------------------------------
 template <int D, int CS>
 struct Dh4Layout {
@@ -1970,29 +1971,37 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
         if (l < D / 16) dma16_s32(gEg + ch * D * 4, oE, sb + B3::EG_OFF + D * wr);
     };
     // dO tile of a set -> dOT[n][t] (role-1 waves; rows past T read as zero)
+    // All eight reads of a lane are issued unconditionally (rows past T hold
+    // stale LDS bytes and are replaced by zero after the read), so they share
+    // one LDS round trip.
     auto transpose_do = [&](int k, const char* sb) __attribute__((always_inline)) {
-        const ST* sdO = reinterpret_cast<const ST*>(sb + B3::DO_OFF);
+        const char* sdO = sb + B3::DO_OFF;
         ST* o = dot(k);
+        constexpr int GSTEP = 256 / DC, NIT = C / 8 / GSTEP;
+        static_assert(NIT >= 1 && NIT * GSTEP * 8 == C, "transpose covers the tile in whole steps");
         const int t1 = tid - 256, nn = t1 % DC, tg = t1 / DC;      // column, group of 8 rows
         const int valid = a.T - (nc - 1 - k) * C;
-        for (int g8 = tg; g8 < C / 8; g8 += 256 / DC) {
-            float v[8];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int g8 = tg + GSTEP * it;
+            uint32_t u[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int t = 8 * g8 + e;
-                v[e] = (t < valid) ? ld_sw<RB_U>(sdO, t, nn) : 0.f;
+                const uint32_t x = *reinterpret_cast<const uint16_t*>(sdO + Swz<RB_U>::at(t, 2 * nn));
+                u[e] = (t < valid) ? x : 0u;
             }
-            const short4v lo = pack4(v), hi = pack4(v + 4);
-            *reinterpret_cast<short4v*>(o + nn * LDO + 8 * g8) = lo;
-            *reinterpret_cast<short4v*>(o + nn * LDO + 8 * g8 + 4) = hi;
+            *reinterpret_cast<uint2*>(o + nn * LDO + 8 * g8) = make_uint2(u[0] | (u[1] << 16), u[2] | (u[3] << 16));
+            *reinterpret_cast<uint2*>(o + nn * LDO + 8 * g8 + 4) = make_uint2(u[4] | (u[5] << 16), u[6] | (u[7] << 16));
         }
     };
-    auto flush = [&](int k) __attribute__((always_inline)) {   // role-1 waves
+    // Staged dh and dV' of step k -> global, by the chain waves: the side waves
+    // then issue only DMA, so their vmcnt waits count slabs and no stores.
+    auto flush = [&](int k) __attribute__((always_inline)) {   // chain waves
         const ST* sst = stg(k);
-        const int t1 = tid - 256;
         const size_t ch = (size_t)bh * nc + (nc - 1 - k);
-        tile_out_at<ST, D, DC>(t1, sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
-        tile_out_at<ST, C, DC>(t1, sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
+        tile_out_at<ST, D, DC>(tid, sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
+        tile_out_at<ST, C, DC>(tid, sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
     };
 
     int mt[MT];
@@ -2093,14 +2102,11 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * wr + 4 * g4 + e) * LDU + BS * j + r16, dV[e]);
             }
-        } else {
-            if (k + 1 < nc) {
-                // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight);
-                // waited for before this step's flush issues its stores
-                dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
-                transpose_do(k + 1, snext);
-            }
             if (k > 0) flush(k - 1);
+        } else if (k + 1 < nc) {
+            // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight)
+            dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
+            transpose_do(k + 1, snext);
         }
         lds_barrier();                                          // B(k): -dV'^T in xv, dOT of k+1
         if (role == 0) {
@@ -2140,7 +2146,7 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
         if (k + 2 < nc) step(k + 2, set2, set0);
     }
     lds_barrier();
-    if (role == 1) flush(nc - 1);
+    if (role == 0) flush(nc - 1);
 
     if (a.ds0) {
 #pragma unroll
