@@ -134,11 +134,14 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 const float gt = s.g[t][d], x = gt - s.g[r][d];
                 const float el = kexp<PREC>(x);
                 const float qf = qv.get(e), kf = kv.get(e);
+                // anchored path: e^{G - gamma_t} = e^{gamma_r - gamma_t} e^{G - gamma_r}, the
+                // second factor from the table (one exponential fewer per element)
+                const float erx = unsafe ? 1.f : kexp<PREC>(-x);
                 okl[e] = kf * el;
                 oql[e] = qf * el;
-                okr[e] = unsafe ? kf : kf * kexp<PREC>(-x);
+                okr[e] = kf * erx;
                 oqp[e] = oql[e] * s.er[blk][d];
-                okb[e] = bwd ? kf * kexp<PREC>(s.g[C - 1][d] - gt) : 0.f;
+                okb[e] = bwd ? (unsafe ? kf * kexp<PREC>(s.g[C - 1][d] - gt) : okr[e] * s.egr[blk][d]) : 0.f;
             }
             store_vec<ST>(&s.kl[t][c0], okl);
             store_vec<ST>(&s.ql[t][c0], oql);
@@ -150,8 +153,37 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     __syncthreads();
     // PHASE 3
 
-    // pass B: column threads (d, EPV tokens)
-    {
+    // pass B: the transposed copies KbT = (Kr diag(e^{G - gamma_r}))^T and
+    // QpT = (Ql diag(e^{gamma_r}))^T.  Anchored path, bf16: per 16 x 16 tile
+    // (token block i, channel block j) one MFMA forms X diag(s), which leaves
+    // channel d of the tile in lane d % 16 with four consecutive tokens per lane
+    // -- the transposed layout -- written as 8-byte pieces of KbT / QpT rows.
+    // X = Kr or Ql is exact in bf16; the scale s is split into bf16 hi + lo
+    // halves of one K = 32 step, so the product keeps fp32 accuracy until the
+    // final rounding.
+    if (std::is_same<ST, uint16_t>::value && !unsafe) {
+        constexpr int NTT = NB * NT;
+        for (int tix = w; tix < 2 * NTT; tix += 4) {
+            const bool isKb = tix < NTT;
+            const int tt = isKb ? tix : tix - NTT, i = tt / NT, j = tt - i * NT;
+            ST* out = isKb ? oKbT : oQpT;
+            if (out == nullptr) continue;
+            const Frag4 A = ldfrag4<1, ST>(isKb ? &s.kr[0][0] : &s.ql[0][0], LDK, BS * i, BS * j);
+            const float sv = isKb ? s.egr[i][BS * j + r16] : s.er[i][BS * j + r16];
+            const short hi = (short)f2bf(sv), lo = (short)f2bf(sv - bf2f((uint16_t)hi));
+            short4v bh, bl;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool dg = 4 * g4 + e == r16;   // B[k][n] = s[n] on the diagonal
+                bh[e] = dg ? hi : (short)0;
+                bl[e] = dg ? lo : (short)0;
+            }
+            const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat4(A.h, A.h), cat4(bh, bl), zero4(), 0, 0, 0);
+            *reinterpret_cast<uint2*>(out + cCD + (size_t)(BS * j + r16) * C + BS * i + 4 * g4) =
+                make_uint2(pack2bf(c[0], c[1]), pack2bf(c[2], c[3]));
+        }
+    } else {
+        // column threads (d, EPV tokens)
         constexpr int GPC = C / EPV, NV = D * GPC;
         for (int vv = tid; vv < NV; vv += 256) {
             const int d = vv / GPC, tb = (vv - d * GPC) * EPV;
