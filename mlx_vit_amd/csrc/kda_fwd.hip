@@ -38,20 +38,6 @@ struct PrepGeom {
     static constexpr bool STG_IN_G = (int)sizeof(float) * C * CSm::LDG >= C * LDT * (int)sizeof(ST);
 };
 
-// g[c][r] = lds[r][c] for an R x CC tile: each thread gathers one 16-byte
-// output vector (EPV consecutive r of one c) from LDS and stores it.
-template <typename ST, int R, int CC>
-__device__ __forceinline__ void tile_out_T(const ST* lds, int lld, ST* __restrict__ g, size_t gld) {
-    constexpr int EPV = 16 / (int)sizeof(ST), GPC = R / EPV, NV = CC * GPC;
-    for (int vv = threadIdx.x; vv < NV; vv += 256) {
-        const int c = vv / GPC, r0 = (vv - c * GPC) * EPV;
-        float x[EPV];
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) x[e] = ld1<ST>(lds + (r0 + e) * lld + c);
-        store_vec<ST>(g + (size_t)c * gld + r0, x);
-    }
-}
-
 template <int D, typename ST, typename TG, int PREC>
 __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     using G = PrepGeom<D, ST>;
@@ -88,7 +74,14 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     ST* oAqk = static_cast<ST*>(a.Aqk);
     ST* oAqkT = static_cast<ST*>(a.AqkT);
     const bool bwd = oAqkT != nullptr;
-    const bool stT = bwd && oAqk == nullptr;   // Aqk staged transposed (backward-only outputs)
+    // four consecutive elements of a transposed output row, straight from an MFMA
+    // accumulator (lane (g, n) holds rows 4 g .. 4 g + 3 of column n)
+    auto st4 = [](ST* p, const float* x) __attribute__((always_inline)) {
+        if constexpr (std::is_same<ST, uint16_t>::value)
+            *reinterpret_cast<uint2*>(p) = make_uint2(pack2bf(x[0], x[1]), pack2bf(x[2], x[3]));
+        else
+            *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    };
 
     // PHASE 0 (load); v stays in registers until the column pass is done
     Tile<ST, C, D> tv;
@@ -203,7 +196,10 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     __syncthreads();
     // PHASE 4
 
-    ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];   // Aqk / AqkT staging
+    // Aqk is staged row-major for coalesced stores; AqkT is written from the
+    // accumulators (a lane's four rows of one column are four consecutive AqkT
+    // elements)
+    ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];
     if (!unsafe) {
         // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared
         for (int tix = w; tix < 10; tix += 4) {
@@ -220,14 +216,15 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 P = mma<PREC>(Ak, Bk, P);
                 Q = mma<PREC>(Aq, Bk, Q);
             }
+            float aq[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
                 sa[t][sx] = (sx < t) ? P[e] : 0.f;
-                const float aq = (sx <= t) ? Q[e] : 0.f;
-                if (stT) st1<ST>(stA + sx * LDT + t, aq);
-                else st1<ST>(stA + t * LDT + sx, aq);
+                aq[e] = (sx <= t) ? Q[e] : 0.f;
+                if (oAqk) st1<ST>(stA + t * LDT + sx, aq[e]);
             }
+            if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, aq);
         }
         // strictly upper sub-block tiles are zero
         for (int idx = tid; idx < 6 * BS * BS; idx += 256) {
@@ -236,18 +233,21 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
             const int t = BS * i + e / BS, sx = BS * j + (e % BS);
             sa[t][sx] = 0.f;
-            if (stT) st1<ST>(stA + sx * LDT + t, 0.f);
-            else st1<ST>(stA + t * LDT + sx, 0.f);
+            if (oAqk) st1<ST>(stA + t * LDT + sx, 0.f);
+        }
+        if (oAqkT) {
+            const float z[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int u = w; u < 6; u += 4) {   // tile (i, j), i < j
+                const int i = (u < 3) ? 0 : (u < 5) ? 1 : 2;
+                const int j = (u < 3) ? u + 1 : (u < 5) ? u - 1 : 3;
+                st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, z);
+            }
         }
     }
     __syncthreads();
     // PHASE 5
     if (!unsafe) {
         if (oAqk) tile_out<ST, C, C>(stA, LDT, oAqk + cCC, C, C);
-        if (oAqkT) {
-            if (stT) tile_out<ST, C, C>(stA, LDT, oAqkT + cCC, C, C);
-            else tile_out_T<ST, C, C>(stA, LDT, oAqkT + cCC, C);
-        }
         if (a.Akk) tile_out<float, C, C>(&sa[0][0], LDA, a.Akk + cCC, C, C);
     }
     diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
@@ -306,31 +306,28 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     }
     __syncthreads();
     // PHASE 7
-    // staging: W -> kl region, U -> ql region, WT -> kr region (all dead now)
+    // staging: W -> kl region, U -> ql region (both dead now); WT straight from
+    // the accumulators (four consecutive tokens of one channel per lane)
     ST* stW = &s.kl[0][0];
     ST* stU = &s.ql[0][0];
-    ST* stWT = &s.kr[0][0];
 #pragma unroll
     for (int jj = 0; jj < TPW; ++jj)
         if (tok[jj])
 #pragma unroll
-            for (int i = 0; i < NB; ++i)
+            for (int i = 0; i < NB; ++i) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int t = BS * i + 4 * g4 + e, d = dcol[jj];
-                    if (isK[jj]) {
-                        st1<ST>(stW + t * LDK + d, X[jj][i][e]);
-                        if (oWT) st1<ST>(stWT + d * LDT + t, X[jj][i][e]);
-                    } else {
-                        st1<ST>(stU + t * LDK + d, X[jj][i][e]);
-                    }
+                    st1<ST>((isK[jj] ? stW : stU) + t * LDK + d, X[jj][i][e]);
                 }
+                if (isK[jj] && oWT) {
+                    const float x[4] = {X[jj][i][0], X[jj][i][1], X[jj][i][2], X[jj][i][3]};
+                    st4(oWT + cCD + (size_t)dcol[jj] * C + BS * i + 4 * g4, x);
+                }
+            }
     __syncthreads();
     tile_out<ST, C, D>(stW, LDK, oW + cCD, D, C);
     tile_out<ST, C, D>(stU, LDK, oU + cCD, D, C);
-    if constexpr (D <= C) {
-        if (oWT) tile_out<ST, D, C>(stWT, LDT, oWT + cCD, C, D);
-    }
     // PHASE 8
 }
 
