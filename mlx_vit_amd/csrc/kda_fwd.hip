@@ -155,25 +155,37 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     // halves of one K = 32 step, so the product keeps fp32 accuracy until the
     // final rounding.
     if (std::is_same<ST, uint16_t>::value && !unsafe) {
-        constexpr int NTT = NB * NT;
-        for (int tix = w; tix < 2 * NTT; tix += 4) {
-            const bool isKb = tix < NTT;
-            const int tt = isKb ? tix : tix - NTT, i = tt / NT, j = tt - i * NT;
-            ST* out = isKb ? oKbT : oQpT;
-            if (out == nullptr) continue;
-            const Frag4 A = ldfrag4<1, ST>(isKb ? &s.kr[0][0] : &s.ql[0][0], LDK, BS * i, BS * j);
-            const float sv = isKb ? s.egr[i][BS * j + r16] : s.er[i][BS * j + r16];
-            const short hi = (short)f2bf(sv), lo = (short)f2bf(sv - bf2f((uint16_t)hi));
-            short4v bh, bl;
+        // wave w: tiles w, w + 4, ... of each output (NT per wave), unrolled so
+        // that all of a wave's operand reads share one LDS round trip
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool dg = 4 * g4 + e == r16;   // B[k][n] = s[n] on the diagonal
-                bh[e] = dg ? hi : (short)0;
-                bl[e] = dg ? lo : (short)0;
+        for (int o = 0; o < 2; ++o) {
+            ST* out = o ? oQpT : oKbT;
+            if (out == nullptr) continue;
+            const ST* X = o ? &s.ql[0][0] : &s.kr[0][0];
+            Frag4 A[NT];
+            float sv[NT];
+#pragma unroll
+            for (int it = 0; it < NT; ++it) {
+                const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
+                A[it] = ldfrag4<1, ST>(X, LDK, BS * i, BS * j);
+                sv[it] = o ? s.er[i][BS * j + r16] : s.egr[i][BS * j + r16];
             }
-            const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat4(A.h, A.h), cat4(bh, bl), zero4(), 0, 0, 0);
-            *reinterpret_cast<uint2*>(out + cCD + (size_t)(BS * j + r16) * C + BS * i + 4 * g4) =
-                make_uint2(pack2bf(c[0], c[1]), pack2bf(c[2], c[3]));
+#pragma unroll
+            for (int it = 0; it < NT; ++it) {
+                const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
+                const short hi = (short)f2bf(sv[it]), lo = (short)f2bf(sv[it] - bf2f((uint16_t)hi));
+                short4v bh, bl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool dg = 4 * g4 + e == r16;   // B[k][n] = s[n] on the diagonal
+                    bh[e] = dg ? hi : (short)0;
+                    bl[e] = dg ? lo : (short)0;
+                }
+                const f32x4 c =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat4(A[it].h, A[it].h), cat4(bh, bl), zero4(), 0, 0, 0);
+                *reinterpret_cast<uint2*>(out + cCD + (size_t)(BS * j + r16) * C + BS * i + 4 * g4) =
+                    make_uint2(pack2bf(c[0], c[1]), pack2bf(c[2], c[3]));
+            }
         }
     } else {
         // column threads (d, EPV tokens)
