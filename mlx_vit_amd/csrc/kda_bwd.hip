@@ -1067,10 +1067,15 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         __syncthreads();
         if (w < NB) diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii);
     }
-    // V' tiles: one each for waves 0-3, the rest over waves 4-7
-    if (w < NB) vp_tile(w);
-    else
-        for (int tix = w; tix < NB * NT; tix += 8 - NB) vp_tile(tix);
+    // V' tiles round-robin over the waves that are free first: 0-3 (a diagonal
+    // block and its inverse) and 6-7 (one off-diagonal tile); waves 4-5, which
+    // form two off-diagonal tiles, take none
+    static_assert(NB == 4, "wave roles assume four row blocks");
+    {
+        const int slot = (w < 4) ? w : (w >= 6) ? w - 2 : -1;
+        if (slot >= 0)
+            for (int tix = slot; tix < NB * NT; tix += 6) vp_tile(tix);
+    }
     __syncthreads();
 
     f32x4 dqa[MB], dka[MB], dga[MB], dWt[NB];
@@ -1147,9 +1152,10 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     dWt[m] = negacc(dW);
                 }
             }
-            // state-decay term of dG (rh = 1 waves): e^G sum_col dh[d][col] h[d][col],
-            // lane (g4, d) over columns 16 g4 .. 16 g4 + 15 in 16-byte reads
-            if (rh == 1) {
+            // state-decay term of dG (rh = 0 waves, which have the shorter phase 1):
+            // e^G sum_col dh[d][col] h[d][col], lane (g4, d) over columns
+            // 16 g4 .. 16 g4 + 15 in 16-byte reads
+            if (rh == 0) {
 #pragma unroll
                 for (int c8 = 0; c8 < D / 4; c8 += 8) {
                     const int cc = g4 * (D / 4) + c8;
@@ -1180,11 +1186,11 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             }
             dgcol = sum4g(dgcol);
             part = sum4g(part);
-            if (rh == 0 && g4 == 0) xg[d] = dgcol;
+            if (rh == 0 && g4 == 0) xg[d] = dgcol + eGd * part;
         }
         // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves, one each for the
-        // rh = 1 waves (they also form the state-decay term), the rest for the
-        // rh = 0 waves (whose solve starts from registers)
+        // rh = 1 waves (their solve operand Y is gathered from LDS), the rest for
+        // the rh = 0 waves (whose solve starts from registers)
         for (int tix = (w < 4) ? w + 4 : w - 4; tix < 10; tix += (w < 4) ? 4 : 10) {
             int i, j;
             tile_ij(tix, i, j);
@@ -1418,7 +1424,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     float lsum[MB][4];
     if (own) {
         if (rh == 1 && g4 == 3)      // row C-1
-            dga[MB - 1][3] += dgcol + xg[d] + eGd * part;
+            dga[MB - 1][3] += dgcol + xg[d];
         float tot[MB];
 #pragma unroll
         for (int mm = 0; mm < MB; ++mm) {
