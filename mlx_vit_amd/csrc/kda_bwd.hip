@@ -852,6 +852,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     __shared__ L sm;
     __shared__ float xg[D];     // dgamma(C-1) partial of the rh = 0 waves
     __shared__ float xt[D];     // dgamma column totals of the rh = 1 waves
+    __shared__ __align__(16) char pfbuf[256];   // landing bytes of the L2 prefetch
     auto& s = sm.s;
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
@@ -1078,6 +1079,38 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     }
     __syncthreads();
 
+    // L2 prefetch of the chunk this XCD starts next (chunks a CU count apart go to
+    // one XCD and start about when this one ends): one 4-byte DMA per 128-byte
+    // line of its inputs -- the rows of q, k, v, g, dO and the W, U, dV', h, dh
+    // slabs -- so that its loads hit in L2.  The landing bytes are scratch.
+    if (a.pf_ahead > 0 && ch + a.pf_ahead < (int)gridDim.x) {
+        const int pc = ch + a.pf_ahead, pbh = pc / a.nc, pn = pc - pbh * a.nc;
+        const int pb = pbh / a.H, ph = pbh - pb * a.H, pt0 = pn * C, pvalid = min(C, a.T - pt0);
+        const size_t pbase = ((size_t)pb * a.T + pt0) * rs + (size_t)ph * D;
+        constexpr int LCD = C * D * (int)sizeof(ST) / 128, LDD = D * D * (int)sizeof(ST) / 128;
+        constexpr int NL = 5 * C + 3 * LCD + 2 * LDD;
+        const uint32_t m = lds_addr(pfbuf);
+#pragma unroll
+        for (int i = 0; i < (NL + NTH - 1) / NTH; ++i) {
+            const int k = NTH * i + tid;
+            const char* p = nullptr;
+            if (k < 5 * C) {
+                const int ts = k / C, r = k - ts * C;
+                const char* tp = static_cast<const char*>(ts == 0 ? a.q : ts == 1 ? a.k : ts == 2 ? a.v : ts == 3 ? a.dout : a.g);
+                const size_t es = (ts == 4) ? sizeof(TG) : sizeof(ST);
+                if (r < pvalid) p = tp + (pbase + (size_t)r * rs) * es;
+            } else if (k < 5 * C + 3 * LCD) {
+                const int j = k - 5 * C, ts = j / LCD, r = j - ts * LCD;
+                const char* tp = static_cast<const char*>(ts == 0 ? a.W : ts == 1 ? a.U : a.dVp);
+                p = tp + (size_t)pc * C * D * sizeof(ST) + (size_t)r * 128;
+            } else if (k < NL) {
+                const int j = k - 5 * C - 3 * LCD, ts = j / LDD, r = j - ts * LDD;
+                const char* tp = static_cast<const char*>(ts == 0 ? a.h : a.dh);
+                p = tp + (size_t)pc * D * D * sizeof(ST) + (size_t)r * 128;
+            }
+            if (p != nullptr) dma4(p, m);
+        }
+    }
     f32x4 dqa[MB], dka[MB], dga[MB], dWt[NB];
     float dgcol = 0.f, part = 0.f;
 
@@ -1462,6 +1495,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             }
     }
     __syncthreads();
+    dma_wait<0>();   // the prefetch has landed (issued thousands of cycles ago)
     tile_out<ST, C, D, NTH>(&sm.ra.out[0][0][0], LDK, static_cast<ST*>(a.dq) + base, rs, valid);
     tile_out<ST, C, D, NTH>(&sm.ra.out[1][0][0], LDK, static_cast<ST*>(a.dk) + base, rs, valid);
     tile_out<ST, C, D, NTH>(&sm.ra.out[2][0][0], LDK, static_cast<ST*>(a.dv) + base, rs, valid);
@@ -1483,8 +1517,19 @@ template <int D, typename TI, typename TG>
 static hipError_t launch_local_t(const LocalArgs& a, int nchunks, hipStream_t st) {
     if constexpr (std::is_same<TI, float>::value)
         hipLaunchKernelGGL((kda_bwd_local_kernel<D, TI, TG, 3>), dim3(nchunks), dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL((kda_bwd_local3_kernel<D, TI, TG, 1>), dim3(nchunks), dim3(512), 0, st, a);
+    else {
+        // prefetch distance: one chunk per CU (one local-adjoint workgroup fills a CU)
+        static int cus[64];
+        int dev = 0;
+        LocalArgs b = a;
+        b.pf_ahead = 0;
+        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+            if (cus[dev] <= 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                cus[dev] = 0;
+            b.pf_ahead = cus[dev] > 0 ? cus[dev] : 0;
+        }
+        hipLaunchKernelGGL((kda_bwd_local3_kernel<D, TI, TG, 1>), dim3(nchunks), dim3(512), 0, st, b);
+    }
     return hipGetLastError();
 }
 

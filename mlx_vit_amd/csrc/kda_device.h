@@ -510,6 +510,12 @@ __device__ __forceinline__ void dma16_s32(const void* gbase, uint32_t off, uint3
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(gbase), "{m0}"(m) : "memory");
 }
 
+// one 4-byte LDS DMA per active lane (lane l lands at m + 4 l): used to pull
+// whole cache lines into L2 ahead of their use, the LDS bytes being scratch
+__device__ __forceinline__ void dma4(const void* g, uint32_t m) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(m) : "memory");
+}
+
 // s_waitcnt immediates (gfx9 layout: vmcnt [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
 template <int N>
 __device__ __forceinline__ void dma_wait() {

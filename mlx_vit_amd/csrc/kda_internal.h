@@ -53,6 +53,7 @@ struct LocalArgs {
     const float *Akk, *Tii;
     void *dq, *dk, *dv, *dg, *dbeta;
     int T, H, nc;
+    int pf_ahead;   // L2 prefetch distance in chunks (the device's CU count), 0 = none
 };
 
 hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
