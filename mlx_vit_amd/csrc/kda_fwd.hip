@@ -49,7 +49,6 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     __shared__ __align__(16) float tii[NB][BS][BS + 4];   // (I + L_ii)^-1
     __shared__ __align__(16) ST svbuf[G::STAGE_V ? C : 1][G::STAGE_V ? LDK : 8];
     __shared__ __align__(16) ST stgbuf[G::STG_IN_G ? 1 : C][G::STG_IN_G ? 8 : LDT];
-    __shared__ __align__(16) char pfbuf[256];   // landing bytes of the L2 prefetch
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
     __builtin_assume(w >= 0 && w < 4);
@@ -92,18 +91,6 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     const int unsafe = chunk_factors2<D, ST, PREC>(s, flag);
     if (a.eG && tid < D) a.eG[(size_t)ch * D + tid] = kexp<PREC>(s.g[C - 1][tid]);
     // PHASE 2
-    // L2 prefetch of the chunk that starts next on this XCD (chunks one resident
-    // grid apart): one 4-byte DMA per 128-byte line of its q, k, v, g rows, so
-    // that its loads hit in L2.  The landing bytes are scratch.
-    if (a.pf_ahead > 0 && ch + a.pf_ahead < (int)gridDim.x) {
-        const int pc = ch + a.pf_ahead, pbh = pc / a.nc, pn = pc - pbh * a.nc;
-        const int pb = pbh / a.H, ph = pbh - pb * a.H, pt0 = pn * C, pvalid = min(C, a.T - pt0);
-        const size_t pbase = ((size_t)pb * a.T + pt0) * rs + (size_t)ph * D;
-        const int ts = tid / C, r = tid - ts * C;   // 4 tensors x C rows = 256 lines
-        const char* tp = static_cast<const char*>(ts == 0 ? a.q : ts == 1 ? a.k : ts == 2 ? a.v : a.g);
-        const size_t es = (ts == 3) ? sizeof(TG) : sizeof(ST);
-        if (r < pvalid) dma4(tp + (pbase + (size_t)r * rs) * es, lds_addr(pfbuf));
-    }
 
     if (unsafe) {
         // pairwise path: raw q in ql, raw k in kr, exact exp(gamma_t - gamma_s)
@@ -351,7 +338,6 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 }
             }
     __syncthreads();
-    dma_wait<0>();   // the prefetch has landed (issued thousands of cycles ago)
     tile_out<ST, C, D>(stW, LDK, oW + cCD, D, C);
     tile_out<ST, C, D>(stU, LDK, oU + cCD, D, C);
     // PHASE 8
@@ -363,22 +349,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
 template <int D, typename ST, typename TG>
 static hipError_t launch_prep_t(const PrepArgs& a, int nchunks, hipStream_t st) {
     constexpr int PREC = std::is_same<ST, float>::value ? 3 : 1;
-    // prefetch distance: the workgroups resident at once (CUs x workgroups per CU)
-    static int resident[64];
-    int dev = 0;
-    PrepArgs b = a;
-    b.pf_ahead = 0;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-        if (resident[dev] <= 0) {
-            int cus = 0, per = 0;
-            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-                hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &per, reinterpret_cast<const void*>(&kda_prep_kernel<D, ST, TG, PREC>), 256, 0) == hipSuccess)
-                resident[dev] = cus * per;
-        }
-        b.pf_ahead = resident[dev] > 0 ? resident[dev] : 0;
-    }
-    hipLaunchKernelGGL((kda_prep_kernel<D, ST, TG, PREC>), dim3(nchunks), dim3(256), 0, st, b);
+    hipLaunchKernelGGL((kda_prep_kernel<D, ST, TG, PREC>), dim3(nchunks), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

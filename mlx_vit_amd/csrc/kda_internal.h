@@ -25,7 +25,6 @@ struct PrepArgs {
     void *W, *U, *Qp, *QpT, *Kb, *KbT, *WT, *Aqk, *AqkT;
     float *Akk, *Tii, *eG;
     int T, H, nc;
-    int pf_ahead;   // L2 prefetch distance in chunks (resident workgroups), 0 = none
 };
 
 struct RecurArgs {
