@@ -247,9 +247,11 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             sa[t][sx] = 0.f;
             if (oAqk) st1<ST>(stA + t * LDT + sx, 0.f);
         }
-        if (oAqkT) {
+        if (oAqkT && w >= 2) {
+            // waves 2-3 formed two of the ten lower tiles (waves 0-1 three): they
+            // write the six zero tiles
             const float z[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int u = w; u < 6; u += 4) {   // tile (i, j), i < j
+            for (int u = w - 2; u < 6; u += 2) {   // tile (i, j), i < j
                 const int i = (u < 3) ? 0 : (u < 5) ? 1 : 2;
                 const int j = (u < 3) ? u + 1 : (u < 5) ? u - 1 : 3;
                 st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, z);
