@@ -248,6 +248,8 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints ----------------
     if (own) {
         if (!unsafe) {
+            // row and column sides of a pair must agree to fp32 (see below): exact split products
+            constexpr int PX = PREC >= 3 ? 4 : PREC;
 #pragma unroll
             for (int i = 0; i < NB; ++i) {
                 f32x4 dKl = zero4(), dQl = zero4();
@@ -257,14 +259,8 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                     Fr4 B;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) B.v[e] = s.kr[BS * j + 4 * g4 + e][d] * fs;
-                    dKl = mma4<PREC>(frag4(&sp[0][0], C + 4, BS * i, BS * j), B, dKl);
-                    dQl = mma4<PREC>(frag4(&sda[0][0], C + 4, BS * i, BS * j), B, dQl);
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    dka[i][e] += dKl[e] * el[i][e];
-                    dqa[i][e] += dQl[e] * el[i][e];
-                    dga[i][e] += (dKl[e] * kx[i][e] + dQl[e] * qx[i][e]) * el[i][e];
+                    dKl = mma4<PX>(frag4(&sp[0][0], C + 4, BS * i, BS * j), B, dKl);
+                    dQl = mma4<PX>(frag4(&sda[0][0], C + 4, BS * i, BS * j), B, dQl);
                 }
                 Fr4 Bk, Bq;
 #pragma unroll
@@ -272,16 +268,28 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                     Bk.v[e] = s.kl[BS * i + 4 * g4 + e][d];
                     Bq.v[e] = s.ql[BS * i + 4 * g4 + e][d];
                 }
+                // The row-t and column-s contributions of each pair (t, s) to dgamma
+                // cancel in the reverse cumsum below; weight each side by the very
+                // operand values the other side's MFMA used (split to PREC), so that
+                // the cancellation is exact to fp32 and the error stays independent
+                // of the block's decay span.
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dka[i][e] += dKl[e] * el[i][e];
+                    dqa[i][e] += dQl[e] * el[i][e];
+                    dga[i][e] += dKl[e] * mfma_operand<PREC>(Bk.v[e]) + dQl[e] * mfma_operand<PREC>(Bq.v[e]);
+                }
 #pragma unroll
                 for (int j = 0; j <= i; ++j) {
-                    f32x4 dKr = mma4<PREC>(frag4T(&sp[0][0], C + 4, BS * j, BS * i), Bk, zero4());
-                    dKr = mma4<PREC>(frag4T(&sda[0][0], C + 4, BS * j, BS * i), Bq, dKr);
+                    f32x4 dKr = mma4<PX>(frag4T(&sp[0][0], C + 4, BS * j, BS * i), Bk, zero4());
+                    dKr = mma4<PX>(frag4T(&sda[0][0], C + 4, BS * j, BS * i), Bq, dKr);
                     const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float fac = fs * er[j][e];
                         dka[j][e] += dKr[e] * fac;
-                        dga[j][e] -= dKr[e] * kx[j][e] * fac;
+                        // the row side's B operand for this s and block pair
+                        dga[j][e] -= dKr[e] * mfma_operand<PREC>(s.kr[BS * j + 4 * g4 + e][d] * fs);
                     }
                 }
             }
@@ -712,18 +720,19 @@ __global__ __launch_bounds__(256) void kda_bwd_local2_kernel(const LocalArgs a) 
                     dKl = mma4f<PREC>(frag4_from_f32<PREC>(pv), B, dKl);
                     dQl = mma4f<PREC>(ldfrag4<PREC, ST>(&sm.dA[0][0], LDT, BS * i, BS * j), B, dQl);
                 }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    dka[i][e] += dKl[e] * el[i][e];
-                    dqa[i][e] += dQl[e] * el[i][e];
-                    dga[i][e] += (dKl[e] * kx[i][e] + dQl[e] * qx[i][e]) * el[i][e];
-                }
                 float bkv[4], bqv[4], btv[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     bkv[e] = ld1<ST>(&s.kl[BS * i + 4 * g4 + e][d]);
                     bqv[e] = ld1<ST>(&s.ql[BS * i + 4 * g4 + e][d]);
                     btv[e] = s.beta[BS * i + 4 * g4 + e];
+                }
+                // dgamma weighted by the other side's MFMA operands (exact pair cancellation)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dka[i][e] += dKl[e] * el[i][e];
+                    dqa[i][e] += dQl[e] * el[i][e];
+                    dga[i][e] += dKl[e] * mfma_operand<PREC>(bkv[e]) + dQl[e] * mfma_operand<PREC>(bqv[e]);
                 }
                 const Frag4 Bk = frag4_from_f32<PREC>(bkv), Bq = frag4_from_f32<PREC>(bqv);
 #pragma unroll
@@ -742,7 +751,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local2_kernel(const LocalArgs a) 
                     for (int e = 0; e < 4; ++e) {
                         const float fac = fs * er[j][e];
                         dka[j][e] += dKr[e] * fac;
-                        dga[j][e] -= dKr[e] * kx[j][e] * fac;
+                        dga[j][e] -= dKr[e] * mfma_operand<PREC>(ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]) * fs);
                     }
                 }
             }
@@ -1384,11 +1393,15 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                         dQl[e] += Pq[e] * fs;
                     }
                 }
+                // dgamma: weight by the bf16 values the column side's MFMAs read
+                // (K_l, Q_l of row t) so that each pair cancels exactly in the
+                // reverse cumsum, whatever the decay span
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
+                    const int t = BS * i + 4 * g4 + e;
                     dka[mm][e] += dKl[e] * el[mm][e];
                     dqa[mm][e] += dQl[e] * el[mm][e];
-                    dga[mm][e] += (dKl[e] * kx[mm][e] + dQl[e] * qx[mm][e]) * el[mm][e];
+                    dga[mm][e] += dKl[e] * ld1<ST>(&s.kl[t][d]) + dQl[e] * ld1<ST>(&s.ql[t][d]);
                 }
             }
 #pragma unroll
@@ -1415,9 +1428,9 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float c = dKr[e] * er[mm][e];
-                    dka[mm][e] += c;
-                    dga[mm][e] -= c * kx[mm][e];
+                    dka[mm][e] += dKr[e] * er[mm][e];
+                    // the row side's B operand (K_r of row s, raw bf16)
+                    dga[mm][e] -= dKr[e] * ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]);
                 }
             }
         } else {

@@ -115,10 +115,22 @@ __device__ __forceinline__ f32x4 mma4(const Fr4& a, const Fr4& b, f32x4 c) {
             ah[e] = bf2f(f2bf(a.v[e])); al[e] = a.v[e] - ah[e];
             bh[e] = bf2f(f2bf(b.v[e])); bl[e] = b.v[e] - bh[e];
         }
+        // PREC 4 also adds lo * lo: the product of the split operands is then
+        // exact, so two MFMAs that share a split operand agree to fp32
+        if constexpr (PREC >= 4) c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pack4(al), pack4(bl), c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pack4(al), pack4(bh), c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pack4(ah), pack4(bl), c, 0, 0, 0);
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pack4(ah), pack4(bh), c, 0, 0, 0);
     }
+}
+
+// The value an MFMA of precision PREC effectively multiplies for the fp32
+// operand v: bf16(v) at PREC 1, bf16(v) + bf16(v - bf16(v)) with the split.
+template <int PREC>
+__device__ __forceinline__ float mfma_operand(float v) {
+    const float hi = bf2f(f2bf(v));
+    if constexpr (PREC == 1) return hi;
+    else return hi + bf2f(f2bf(v - hi));
 }
 
 // k index of slot e for lane group g (32-wide k-step)

@@ -216,6 +216,23 @@ def test_bwd_strong_decay_pairwise_path():
     _assert_all(_bwd_errors(x, torch.float32), TOL[torch.float32], "bwd strong decay")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("g_scale", [0.5, 1.0, 2.0, 3.0])
+def test_bwd_dg_independent_of_decay_span(dtype, g_scale):
+    """Strong decays that still take the anchored path (16-row spans up to the
+    guard): dgamma sums row and column contributions of every pair that cancel
+    in the reverse cumsum, so both sides must use identical operand values.
+    With mismatched roundings the dg error grew with the span (bf16 4.8e-2,
+    fp32 1e-4 at g_scale 3); it must stay at the level of dq, dk, dv.
+    g is fp32, as the layer produces it (D = 64, D = 32 with fp32 inputs)."""
+    for D in ((64, 32) if dtype == torch.float32 else (64,)):
+        x = _inputs(2, 128, 2, D, dtype, seed=21, grad=True, g_scale=g_scale)
+        x["g"] = x["g"].float()
+        errs = _bwd_errors(x, dtype)
+        _assert_all(errs, TOL[dtype], f"bwd decay span {dtype} g_scale={g_scale} D={D}")
+        assert errs["dg"] <= 3 * max(errs["dq"], errs["dk"], errs["dv"]), errs
+
+
 def test_bwd_parity_bf16_small():
     x = _inputs(2, 300, 4, 64, torch.bfloat16, seed=13, with_state=True, grad=True)
     _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "bwd bf16 small")
