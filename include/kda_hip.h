@@ -115,6 +115,72 @@ int kda_bwd_train(const void* q, const void* k, const void* v, const void* g, co
 int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, int Cm, int N,
                               int upper, void* stream);
 
+/* ---- GatedDeltaLayer ends around the recurrence ----
+ * The layer turns its projections into the recurrence's inputs and its
+ * output back into the residual stream (nope_gdn_mlx.py:796-885).  These
+ * entry points replace the element-wise parts of that path; the projections
+ * themselves stay plain GEMMs.  dtype (0 fp32, 1 bf16) is that of every
+ * activation; g_dtype that of g and dg; parameters and their gradients are
+ * fp32.  Row strides (ld_*) are in elements, multiples of 4; activation
+ * pointers must be 8-byte (bf16) or 16-byte (fp32) aligned.  HD = H * D must
+ * be a multiple of 4 and at most 2048.
+ *
+ * Producer (GatedDeltaLayer.__call__, nope_gdn_mlx.py:796-821, with
+ * ShortCausalConv1d nope_gdn_mlx.py:369-431 and l2_normalize / softplus
+ * nope_gdn_mlx.py:77-86), per row (b, t):
+ *   q = l2norm(silu(conv4(xq))) * scale, k = l2norm(silu(conv4(xk))),
+ *   v = silu(conv4(xv)), g = -exp(A_log[h]) * softplus(xf + dt_bias),
+ *   beta = sigmoid(xb) * beta_mult (2 for allow_neg_eigval, else 1).
+ * conv4 is the causal depthwise convolution of the 4 taps conv_w[i][c][0..3]
+ * (tap 3 multiplies row t, tap 0 row t - 3) plus conv_b[i][c]; l2norm spans
+ * the whole HD row (eps 1e-12), as the reference normalises before splitting
+ * heads.
+ *   xq, xk, xv  [B, T, HD] rows of ld_x; xf [B, T, HD] rows of ld_f;
+ *   xb [B, T, H] rows of ld_b; conv_w [3][HD][4] (q, k, v);
+ *   conv_b [3][HD] or NULL (no bias); dt_bias [HD]; A_log [H];
+ *   q, k, v, g [B, T, H, D] contiguous; beta [B, T, H] contiguous. */
+int kda_layer_producer_fwd(const void* xq, const void* xk, const void* xv, const void* xf, const void* xb,
+                           int64_t ld_x, int64_t ld_f, int64_t ld_b,
+                           const float* conv_w, const float* conv_b, const float* dt_bias, const float* A_log,
+                           void* q, void* k, void* v, void* g, void* beta,
+                           int B, int T, int H, int D, float scale, float beta_mult, int dtype, int g_dtype,
+                           void* stream);
+/* Adjoint of kda_layer_producer_fwd.  dq, dk, dv, dg [B, T, H, D] and dbeta
+ * [B, T, H] contiguous in; dxq, dxk, dxv rows of ld_dx, dxf rows of ld_df,
+ * dxb rows of ld_db out (they may be column slices of one fused buffer).
+ * Parameter gradients are written, not accumulated: dconv_w [3][HD][4],
+ * dconv_b [3][HD] (NULL iff conv_b is NULL), ddt_bias [HD], dA_log [H].
+ * workspace: at least kda_layer_workspace_size(KDA_LAYER_PRODUCER, ...) bytes,
+ * 16-byte aligned.  The gradients are deterministic. */
+int kda_layer_producer_bwd(const void* xq, const void* xk, const void* xv, const void* xf, const void* xb,
+                           int64_t ld_x, int64_t ld_f, int64_t ld_b,
+                           const float* conv_w, const float* conv_b, const float* dt_bias, const float* A_log,
+                           const void* dq, const void* dk, const void* dv, const void* dg, const void* dbeta,
+                           void* dxq, void* dxk, void* dxv, void* dxf, void* dxb,
+                           int64_t ld_dx, int64_t ld_df, int64_t ld_db,
+                           float* dconv_w, float* dconv_b, float* ddt_bias, float* dA_log,
+                           int B, int T, int H, int D, float scale, float beta_mult, int dtype, int g_dtype,
+                           void* workspace, size_t ws_bytes, void* stream);
+
+/* Gated RMSNorm (RMSNormGated, nope_gdn_mlx.py:340-366, applied per head at
+ * nope_gdn_mlx.py:880-885): y = o * rsqrt(mean_d(o^2) + eps) * w * sigmoid(z)
+ * over each head's D channels.  o [rows, H, D] contiguous; z rows of ld_z;
+ * y rows of ld_y; w [D] fp32.  D must be a power of two in [4, 256]. */
+int kda_layer_gated_rmsnorm_fwd(const void* o, const void* z, int64_t ld_z, const float* w,
+                                void* y, int64_t ld_y, int rows, int H, int D, float eps, int dtype,
+                                void* stream);
+/* Adjoint: dy rows of ld_dy in; dout [rows, H, D] contiguous, dz rows of
+ * ld_dz and dw [D] (written, not accumulated) out.  workspace: at least
+ * kda_layer_workspace_size(KDA_LAYER_RMSNORM, ...) bytes with B = 1, T = rows. */
+int kda_layer_gated_rmsnorm_bwd(const void* o, const void* z, int64_t ld_z, const float* w,
+                                const void* dy, int64_t ld_dy, void* dout, void* dz, int64_t ld_dz, float* dw,
+                                int rows, int H, int D, float eps, int dtype,
+                                void* workspace, size_t ws_bytes, void* stream);
+
+#define KDA_LAYER_PRODUCER 0
+#define KDA_LAYER_RMSNORM 1
+size_t kda_layer_workspace_size(int which, int B, int T, int H, int D);
+
 /* ---- launch timing (instrumentation; no counterpart in the reference) ----
  * With profiling on, every kernel launch made by kda_fwd / kda_bwd is
  * bracketed by two HIP events recorded on the launch stream.  Used by the

@@ -21,11 +21,15 @@ KDA_PASS_FWD = 0
 KDA_PASS_BWD = 1
 KDA_PASS_TRAIN = 2
 
+KDA_LAYER_PRODUCER = 0
+KDA_LAYER_RMSNORM = 1
+
 WS_REGIONS = ("W", "U", "Qp", "QpT", "Kb", "KbT", "WT", "Aqk", "AqkT", "Akk", "Tii", "eG",
               "h", "dh", "Vp", "dVp")
 
 # every function the header declares, with its ctypes signature
 _P, _I, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+_L, _F = ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
     "kda_abi_version": ([], _I),
     "kda_last_error": ([], ctypes.c_char_p),
@@ -36,6 +40,12 @@ SIGNATURES = {
     "kda_fwd_train": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_bwd_train": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_solve_unit_triangular": ([_P] * 3 + [_I] * 4 + [_P], _I),
+    "kda_layer_producer_fwd": ([_P] * 5 + [_L] * 3 + [_P] * 9 + [_I] * 4 + [_F] * 2 + [_I] * 2 + [_P], _I),
+    "kda_layer_producer_bwd": ([_P] * 5 + [_L] * 3 + [_P] * 14 + [_L] * 3 + [_P] * 4 + [_I] * 4 + [_F] * 2
+                               + [_I] * 2 + [_P, _Z, _P], _I),
+    "kda_layer_gated_rmsnorm_fwd": ([_P, _P, _L, _P, _P, _L] + [_I] * 3 + [_F, _I, _P], _I),
+    "kda_layer_gated_rmsnorm_bwd": ([_P, _P, _L, _P, _P, _L, _P, _P, _L, _P] + [_I] * 3 + [_F, _I, _P, _Z, _P], _I),
+    "kda_layer_workspace_size": ([_I] * 5, _Z),
     "kda_profile_enable": ([_I], _I),
     "kda_profile_name": ([_I], ctypes.c_char_p),
     "kda_profile_read": ([_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)], _I),

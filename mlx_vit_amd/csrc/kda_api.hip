@@ -490,3 +490,202 @@ int kda_profile_read(int id, double* total_ms, int* launches) {
 }
 
 }  // extern "C"
+
+namespace {
+
+// Activation rows are read and written four channels at a time.
+int check_act(const void* p, const char* name, int dtype) {
+    if (!p) return fail(KDA_E_INVALID, "%s is NULL", name);
+    const size_t al = dtype == KDA_DTYPE_F32 ? 16 : 8;
+    if (!aligned(p, al)) return fail(KDA_E_INVALID, "%s is not %zu-byte aligned", name, al);
+    return KDA_OK;
+}
+
+int check_f32(const void* p, const char* name, size_t al, bool nullable) {
+    if (!p) return nullable ? KDA_OK : fail(KDA_E_INVALID, "%s is NULL", name);
+    if (!aligned(p, al)) return fail(KDA_E_INVALID, "%s is not %zu-byte aligned", name, al);
+    return KDA_OK;
+}
+
+int check_ld(int64_t ld, int64_t min_ld, bool vec, const char* name) {
+    if (ld < min_ld) return fail(KDA_E_INVALID, "%s=%lld is below the row width %lld", name, (long long)ld,
+                                 (long long)min_ld);
+    if (vec && ld % 4 != 0) return fail(KDA_E_INVALID, "%s=%lld is not a multiple of 4", name, (long long)ld);
+    return KDA_OK;
+}
+
+int check_layer(int B, int T, int H, int D, int dtype, int g_dtype) {
+    if (B < 0 || T < 0 || H < 1 || D < 1) return fail(KDA_E_INVALID, "B=%d T=%d H=%d D=%d", B, T, H, D);
+    if (dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_BF16)
+        return fail(KDA_E_UNSUPPORTED, "dtype=%d: expected 0 (fp32) or 1 (bf16)", dtype);
+    if (g_dtype != KDA_DTYPE_F32 && g_dtype != KDA_DTYPE_BF16)
+        return fail(KDA_E_UNSUPPORTED, "g_dtype=%d: expected 0 (fp32) or 1 (bf16)", g_dtype);
+    if (D % 4 != 0) return fail(KDA_E_UNSUPPORTED, "D=%d: must be a multiple of 4", D);
+    if ((int64_t)H * D > 2048) return fail(KDA_E_UNSUPPORTED, "H*D=%d exceeds 2048", H * D);
+    if ((int64_t)B * T > (int64_t)1 << 30) return fail(KDA_E_UNSUPPORTED, "B*T=%lld rows", (long long)B * T);
+    return KDA_OK;
+}
+
+int check_norm(int rows, int H, int D, int dtype) {
+    if (rows < 0 || H < 1 || D < 1) return fail(KDA_E_INVALID, "rows=%d H=%d D=%d", rows, H, D);
+    if (dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_BF16)
+        return fail(KDA_E_UNSUPPORTED, "dtype=%d: expected 0 (fp32) or 1 (bf16)", dtype);
+    if (D < 4 || D > 256 || (D & (D - 1)) != 0)
+        return fail(KDA_E_UNSUPPORTED, "D=%d: must be a power of two in [4, 256]", D);
+    if ((int64_t)H * D > 2048) return fail(KDA_E_UNSUPPORTED, "H*D=%d exceeds 2048", H * D);
+    return KDA_OK;
+}
+
+#define KDA_TRY(x) do { const int rc_ = (x); if (rc_ != KDA_OK) return rc_; } while (0)
+
+int producer_common(const void* xq, const void* xk, const void* xv, const void* xf, const void* xb, int64_t ld_x,
+                    int64_t ld_f, int64_t ld_b, const float* conv_w, const float* conv_b, const float* dt_bias,
+                    const float* A_log, int B, int T, int H, int D, int dtype, int g_dtype) {
+    KDA_TRY(check_layer(B, T, H, D, dtype, g_dtype));
+    const int64_t HD = (int64_t)H * D;
+    KDA_TRY(check_act(xq, "xq", dtype));
+    KDA_TRY(check_act(xk, "xk", dtype));
+    KDA_TRY(check_act(xv, "xv", dtype));
+    KDA_TRY(check_act(xf, "xf", dtype));
+    KDA_TRY(check_scalar(xb, "xb", dtype));
+    KDA_TRY(check_ld(ld_x, HD, true, "ld_x"));
+    KDA_TRY(check_ld(ld_f, HD, true, "ld_f"));
+    KDA_TRY(check_ld(ld_b, H, false, "ld_b"));
+    KDA_TRY(check_f32(conv_w, "conv_w", 16, false));
+    KDA_TRY(check_f32(conv_b, "conv_b", 16, true));
+    KDA_TRY(check_f32(dt_bias, "dt_bias", 16, false));
+    KDA_TRY(check_f32(A_log, "A_log", 4, false));
+    return KDA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kda_layer_producer_fwd(const void* xq, const void* xk, const void* xv, const void* xf, const void* xb,
+                           int64_t ld_x, int64_t ld_f, int64_t ld_b, const float* conv_w, const float* conv_b,
+                           const float* dt_bias, const float* A_log, void* q, void* k, void* v, void* g, void* beta,
+                           int B, int T, int H, int D, float scale, float beta_mult, int dtype, int g_dtype,
+                           void* stream) {
+    KDA_TRY(producer_common(xq, xk, xv, xf, xb, ld_x, ld_f, ld_b, conv_w, conv_b, dt_bias, A_log, B, T, H, D, dtype,
+                            g_dtype));
+    KDA_TRY(check_act(q, "q", dtype));
+    KDA_TRY(check_act(k, "k", dtype));
+    KDA_TRY(check_act(v, "v", dtype));
+    KDA_TRY(check_act(g, "g", g_dtype));
+    KDA_TRY(check_scalar(beta, "beta", dtype));
+    if ((int64_t)B * T == 0) return ok();
+    kda::ProdArgs a{};
+    a.xq = xq; a.xk = xk; a.xv = xv; a.xf = xf; a.xb = xb;
+    a.conv_w = conv_w; a.conv_b = conv_b; a.dt_bias = dt_bias; a.A_log = A_log;
+    a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
+    a.ld_x = ld_x; a.ld_f = ld_f; a.ld_b = ld_b;
+    a.B = B; a.T = T; a.H = H; a.D = D; a.scale = scale; a.beta_mult = beta_mult;
+    const hipError_t e = kda::launch_producer_fwd(a, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16,
+                                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_producer_fwd");
+}
+
+int kda_layer_producer_bwd(const void* xq, const void* xk, const void* xv, const void* xf, const void* xb,
+                           int64_t ld_x, int64_t ld_f, int64_t ld_b, const float* conv_w, const float* conv_b,
+                           const float* dt_bias, const float* A_log, const void* dq, const void* dk, const void* dv,
+                           const void* dg, const void* dbeta, void* dxq, void* dxk, void* dxv, void* dxf, void* dxb,
+                           int64_t ld_dx, int64_t ld_df, int64_t ld_db, float* dconv_w, float* dconv_b,
+                           float* ddt_bias, float* dA_log, int B, int T, int H, int D, float scale, float beta_mult,
+                           int dtype, int g_dtype, void* workspace, size_t ws_bytes, void* stream) {
+    KDA_TRY(producer_common(xq, xk, xv, xf, xb, ld_x, ld_f, ld_b, conv_w, conv_b, dt_bias, A_log, B, T, H, D, dtype,
+                            g_dtype));
+    const int64_t HD = (int64_t)H * D;
+    KDA_TRY(check_act(dq, "dq", dtype));
+    KDA_TRY(check_act(dk, "dk", dtype));
+    KDA_TRY(check_act(dv, "dv", dtype));
+    KDA_TRY(check_act(dg, "dg", g_dtype));
+    KDA_TRY(check_scalar(dbeta, "dbeta", dtype));
+    KDA_TRY(check_act(dxq, "dxq", dtype));
+    KDA_TRY(check_act(dxk, "dxk", dtype));
+    KDA_TRY(check_act(dxv, "dxv", dtype));
+    KDA_TRY(check_act(dxf, "dxf", dtype));
+    KDA_TRY(check_scalar(dxb, "dxb", dtype));
+    KDA_TRY(check_ld(ld_dx, HD, true, "ld_dx"));
+    KDA_TRY(check_ld(ld_df, HD, true, "ld_df"));
+    KDA_TRY(check_ld(ld_db, H, false, "ld_db"));
+    KDA_TRY(check_f32(dconv_w, "dconv_w", 4, false));
+    KDA_TRY(check_f32(ddt_bias, "ddt_bias", 4, false));
+    KDA_TRY(check_f32(dA_log, "dA_log", 4, false));
+    if ((conv_b == nullptr) != (dconv_b == nullptr))
+        return fail(KDA_E_INVALID, "dconv_b must be NULL exactly when conv_b is NULL");
+    KDA_TRY(check_f32(dconv_b, "dconv_b", 4, true));
+    const size_t need = kda::producer_ws_floats(B, T, H, D) * sizeof(float);
+    if (!workspace) return fail(KDA_E_INVALID, "workspace is NULL");
+    if (!aligned(workspace, 16)) return fail(KDA_E_INVALID, "workspace is not 16-byte aligned");
+    if (ws_bytes < need) return fail(KDA_E_WORKSPACE, "workspace has %zu bytes, needs %zu", ws_bytes, need);
+    kda::ProdArgs a{};
+    a.xq = xq; a.xk = xk; a.xv = xv; a.xf = xf; a.xb = xb;
+    a.conv_w = conv_w; a.conv_b = conv_b; a.dt_bias = dt_bias; a.A_log = A_log;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta;
+    a.dxq = dxq; a.dxk = dxk; a.dxv = dxv; a.dxf = dxf; a.dxb = dxb;
+    a.dconv_w = dconv_w; a.dconv_b = dconv_b; a.ddt_bias = ddt_bias; a.dA_log = dA_log;
+    a.part = static_cast<float*>(workspace);
+    a.colsum = a.part + (size_t)kda::producer_partials(B, T) * 17 * HD;
+    a.ld_x = ld_x; a.ld_f = ld_f; a.ld_b = ld_b; a.ld_dx = ld_dx; a.ld_df = ld_df; a.ld_db = ld_db;
+    a.B = B; a.T = T; a.H = H; a.D = D; a.scale = scale; a.beta_mult = beta_mult;
+    const hipError_t e = kda::launch_producer_bwd(a, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16,
+                                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_producer_bwd");
+}
+
+int kda_layer_gated_rmsnorm_fwd(const void* o, const void* z, int64_t ld_z, const float* w, void* y, int64_t ld_y,
+                                int rows, int H, int D, float eps, int dtype, void* stream) {
+    KDA_TRY(check_norm(rows, H, D, dtype));
+    const int64_t HD = (int64_t)H * D;
+    KDA_TRY(check_act(o, "o", dtype));
+    KDA_TRY(check_act(z, "z", dtype));
+    KDA_TRY(check_act(y, "y", dtype));
+    KDA_TRY(check_ld(ld_z, HD, true, "ld_z"));
+    KDA_TRY(check_ld(ld_y, HD, true, "ld_y"));
+    KDA_TRY(check_f32(w, "w", 16, false));
+    if (rows == 0) return ok();
+    kda::NormArgs a{};
+    a.o = o; a.z = z; a.w = w; a.y = y; a.ld_z = ld_z; a.ld_y = ld_y;
+    a.rows = rows; a.H = H; a.D = D; a.eps = eps;
+    const hipError_t e = kda::launch_rmsnorm_fwd(a, dtype == KDA_DTYPE_BF16, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_gated_rmsnorm_fwd");
+}
+
+int kda_layer_gated_rmsnorm_bwd(const void* o, const void* z, int64_t ld_z, const float* w, const void* dy,
+                                int64_t ld_dy, void* dout, void* dz, int64_t ld_dz, float* dw, int rows, int H, int D,
+                                float eps, int dtype, void* workspace, size_t ws_bytes, void* stream) {
+    KDA_TRY(check_norm(rows, H, D, dtype));
+    const int64_t HD = (int64_t)H * D;
+    KDA_TRY(check_act(o, "o", dtype));
+    KDA_TRY(check_act(z, "z", dtype));
+    KDA_TRY(check_act(dy, "dy", dtype));
+    KDA_TRY(check_act(dout, "dout", dtype));
+    KDA_TRY(check_act(dz, "dz", dtype));
+    KDA_TRY(check_ld(ld_z, HD, true, "ld_z"));
+    KDA_TRY(check_ld(ld_dy, HD, true, "ld_dy"));
+    KDA_TRY(check_ld(ld_dz, HD, true, "ld_dz"));
+    KDA_TRY(check_f32(w, "w", 16, false));
+    KDA_TRY(check_f32(dw, "dw", 4, false));
+    const size_t need = kda::rmsnorm_ws_floats(rows, H, D) * sizeof(float);
+    if (!workspace) return fail(KDA_E_INVALID, "workspace is NULL");
+    if (!aligned(workspace, 16)) return fail(KDA_E_INVALID, "workspace is not 16-byte aligned");
+    if (ws_bytes < need) return fail(KDA_E_WORKSPACE, "workspace has %zu bytes, needs %zu", ws_bytes, need);
+    kda::NormArgs a{};
+    a.o = o; a.z = z; a.w = w; a.dy = dy; a.dout = dout; a.dz = dz; a.dw = dw;
+    a.ld_z = ld_z; a.ld_dy = ld_dy; a.ld_dz = ld_dz;
+    a.part = static_cast<float*>(workspace);
+    a.colsum = a.part + (size_t)kda::rmsnorm_partials(rows) * HD;
+    a.rows = rows; a.H = H; a.D = D; a.eps = eps;
+    const hipError_t e = kda::launch_rmsnorm_bwd(a, dtype == KDA_DTYPE_BF16, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_gated_rmsnorm_bwd");
+}
+
+size_t kda_layer_workspace_size(int which, int B, int T, int H, int D) {
+    if (B < 0 || T < 0 || H < 1 || D < 1) return 0;
+    if (which == KDA_LAYER_PRODUCER) return kda::producer_ws_floats(B, T, H, D) * sizeof(float);
+    if (which == KDA_LAYER_RMSNORM) return kda::rmsnorm_ws_floats(B * T, H, D) * sizeof(float);
+    return 0;
+}
+
+}  // extern "C"

@@ -65,4 +65,41 @@ hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm
                         hipStream_t st);
 hipError_t launch_state_copy(const float* src, float* dst, size_t n, hipStream_t st);
 
+// GatedDeltaLayer producer (projection outputs -> q, k, v, g, beta) and its
+// adjoint.  Row strides are in elements; q, k, v, g, dq, dk, dv, dg are
+// contiguous [B, T, H*D], beta and dbeta contiguous [B, T, H].
+struct ProdArgs {
+    const void *xq, *xk, *xv, *xf, *xb;
+    const float *conv_w, *conv_b, *dt_bias, *A_log;   // [3][H*D][4], [3][H*D] or null, [H*D], [H]
+    void *q, *k, *v, *g, *beta;
+    const void *dq, *dk, *dv, *dg, *dbeta;
+    void *dxq, *dxk, *dxv, *dxf, *dxb;
+    float *dconv_w, *dconv_b, *ddt_bias, *dA_log;
+    float *part, *colsum;                              // workspace
+    int64_t ld_x, ld_f, ld_b, ld_dx, ld_df, ld_db;
+    int B, T, H, D;
+    float scale, beta_mult;
+};
+
+// Gated RMSNorm over heads of D channels; o and dout are contiguous [rows][H*D].
+struct NormArgs {
+    const void *o, *z, *dy;
+    const float* w;
+    void *y, *dout, *dz;
+    float* dw;
+    float *part, *colsum;                              // workspace
+    int64_t ld_z, ld_y, ld_dy, ld_dz;
+    int rows, H, D;
+    float eps;
+};
+
+size_t producer_ws_floats(int B, int T, int H, int D);
+size_t rmsnorm_ws_floats(int rows, int H, int D);
+int producer_partials(int B, int T);
+int rmsnorm_partials(int rows);
+hipError_t launch_producer_fwd(const ProdArgs& a, int in_bf16, int g_bf16, hipStream_t st);
+hipError_t launch_producer_bwd(const ProdArgs& a, int in_bf16, int g_bf16, hipStream_t st);
+hipError_t launch_rmsnorm_fwd(const NormArgs& a, int in_bf16, hipStream_t st);
+hipError_t launch_rmsnorm_bwd(const NormArgs& a, int in_bf16, hipStream_t st);
+
 }  // namespace kda

@@ -1,0 +1,212 @@
+"""GPU parity of the GatedDeltaLayer kernels (producer, gated RMSNorm) and of
+the whole layer, through the C ABI, against the CPU restatement in
+oracle/layer_reference.py evaluated in fp64 on the same (dtype-rounded) inputs.
+
+Bars: rel-L2 <= 1e-4 with fp32 activations, <= 1e-2 with bf16 activations,
+for every output and every gradient (inputs and parameters)."""
+import pytest
+import torch
+
+from oracle import kda_reference as R
+from oracle import layer_reference as LR
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float32: 1e-4, torch.bfloat16: 1e-2}
+
+
+def _rel(a, b):
+    return R.rel_l2(a.detach().cpu().double(), b.detach().cpu().double())
+
+
+def _check(errs, tol, case):
+    print(case, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    bad = {k: v for k, v in errs.items() if not (v <= tol)}
+    assert not bad, f"{case}: {bad} above {tol}"
+
+
+def _prod_inputs(B, T, H, D, dtype, seed, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    HD = H * D
+    r = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    acts = dict(qkv=r(B, T, 3 * HD), xf=r(B, T, HD), xb=r(B, T, H))
+    acts = {n: t.to(dtype) for n, t in acts.items()}
+    params = dict(conv_w=torch.rand(3, HD, 4, generator=g) - 0.5,
+                  conv_b=0.1 * r(3, HD) if bias else None, dt_bias=0.1 * r(HD),
+                  A_log=torch.log(1 + 15 * torch.rand(H, generator=g)))
+    cots = dict(dq=r(B, T, H, D).to(dtype), dk=r(B, T, H, D).to(dtype), dv=r(B, T, H, D).to(dtype),
+                dg=r(B, T, H, D), dbeta=r(B, T, H).to(dtype))
+    return acts, params, cots
+
+
+def _prod_reference(acts, params, cots, H, D, mult):
+    HD = H * D
+    leaves = {n: t.double().requires_grad_() for n, t in acts.items()}
+    leaves.update({n: t.double().requires_grad_() for n, t in params.items() if t is not None})
+    xq, xk, xv = leaves["qkv"].split(HD, -1)
+    outs = LR.producer_from_projections(xq, xk, xv, leaves["xf"], leaves["xb"], leaves["conv_w"],
+                                        leaves.get("conv_b"), leaves["dt_bias"], leaves["A_log"], H, D, mult)
+    loss = sum((o * cots[n].double()).sum() for o, n in zip(outs, ("dq", "dk", "dv", "dg", "dbeta")))
+    loss.backward()
+    return outs, {n: t.grad for n, t in leaves.items()}
+
+
+PRODUCER_CASES = [
+    # B, T, H, D, dtype, bias, beta_mult
+    (2, 37, 3, 64, torch.float32, True, 1.0),      # H*D = 192: one wave, a quarter of its lanes idle
+    (1, 100, 12, 64, torch.float32, True, 1.0),    # H*D = 768: three waves per row
+    (2, 5, 2, 32, torch.float32, True, 1.0),       # T shorter than a strip
+    (1, 1, 6, 64, torch.float32, True, 1.0),       # T = 1
+    (1, 70, 16, 128, torch.float32, True, 1.0),    # H*D = 2048: eight waves
+    (3, 33, 4, 32, torch.float32, False, 2.0),     # no conv bias, allow_neg_eigval
+    (2, 77, 12, 64, torch.bfloat16, True, 1.0),
+    (1, 40, 6, 64, torch.bfloat16, False, 2.0),
+]
+
+
+@pytest.mark.parametrize("B,T,H,D,dtype,bias,mult", PRODUCER_CASES)
+def test_producer_parity(B, T, H, D, dtype, bias, mult):
+    from mlx_vit_amd import producer_backward, producer_forward
+    acts, params, cots = _prod_inputs(B, T, H, D, dtype, seed=B * 1000 + T, bias=bias)
+    case = f"producer B={B} T={T} H={H} D={D} {dtype} bias={bias} mult={mult}"
+    print(case, flush=True)
+    da = {n: t.to(DEV) for n, t in acts.items()}
+    dp = {n: (None if t is None else t.to(DEV)) for n, t in params.items()}
+    dc = {n: t.to(DEV) for n, t in cots.items()}
+    outs = producer_forward(da["qkv"], da["xf"], da["xb"], dp["conv_w"], dp["conv_b"], dp["dt_bias"],
+                            dp["A_log"], H, D, D ** -0.5, mult, torch.float32)
+    grads = producer_backward(da["qkv"], da["xf"], da["xb"], dp["conv_w"], dp["conv_b"], dp["dt_bias"],
+                              dp["A_log"], dc["dq"], dc["dk"], dc["dv"], dc["dg"], dc["dbeta"], H, D, D ** -0.5,
+                              mult)
+    torch.cuda.synchronize()
+    ref_outs, ref_grads = _prod_reference(acts, params, cots, H, D, mult)
+    errs = {n: _rel(o, r) for n, o, r in zip(("q", "k", "v", "g", "beta"), outs, ref_outs)}
+    names = ("qkv", "xf", "xb", "conv_w", "conv_b", "dt_bias", "A_log")
+    for n, gr in zip(names, grads):
+        if n == "conv_b" and not bias:
+            assert gr is None
+            continue
+        errs["d" + n] = _rel(gr, ref_grads[n])
+    _check(errs, TOL[dtype], case)
+
+
+def test_producer_strided_rows():
+    """q/k/v read from column slices of a wider fused projection output."""
+    from mlx_vit_amd import producer_forward
+    B, T, H, D = 2, 50, 4, 32
+    HD = H * D
+    acts, params, _ = _prod_inputs(B, T, H, D, torch.float32, seed=7)
+    wide = torch.randn(B, T, 3 * HD + 64)
+    wide[..., 32:32 + 3 * HD] = acts["qkv"]
+    d = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    out_wide = producer_forward(d(wide)[..., 32:32 + 3 * HD], d(acts["xf"]), d(acts["xb"]), d(params["conv_w"]),
+                                d(params["conv_b"]), d(params["dt_bias"]), d(params["A_log"]), H, D, 0.5)
+    out_ref = producer_forward(d(acts["qkv"]), d(acts["xf"]), d(acts["xb"]), d(params["conv_w"]),
+                               d(params["conv_b"]), d(params["dt_bias"]), d(params["A_log"]), H, D, 0.5)
+    for a, b in zip(out_wide, out_ref):
+        assert torch.equal(a, b)
+
+
+def test_producer_full_size_properties():
+    """Config-2 shape in bf16 (B=8, T=1568, H=12, D=64): every q row has norm
+    D^-1/2 and every k row norm 1 (to bf16 rounding), g <= 0, 0 < beta < 1,
+    and the forward matches the fp32 torch restatement on the GPU."""
+    from mlx_vit_amd import producer_forward
+    B, T, H, D = 8, 1568, 12, 64
+    acts, params, _ = _prod_inputs(B, T, H, D, torch.bfloat16, seed=11)
+    da = {n: t.to(DEV) for n, t in acts.items()}
+    dp = {n: t.to(DEV) for n, t in params.items()}
+    q, k, v, g, beta = producer_forward(da["qkv"], da["xf"], da["xb"], dp["conv_w"], dp["conv_b"], dp["dt_bias"],
+                                        dp["A_log"], H, D, D ** -0.5)
+    qn = q.float().reshape(B, T, -1).norm(dim=-1)
+    kn = k.float().reshape(B, T, -1).norm(dim=-1)
+    assert torch.allclose(qn, torch.full_like(qn, D ** -0.5), rtol=4e-3)
+    assert torch.allclose(kn, torch.ones_like(kn), rtol=4e-3)
+    assert bool((g <= 0).all()) and bool((beta > 0).all()) and bool((beta < 1).all())
+    HD = H * D
+    xq, xk, xv = da["qkv"].float().split(HD, -1)
+    ref = LR.producer_from_projections(xq, xk, xv, da["xf"].float(), da["xb"].float(), dp["conv_w"],
+                                       dp["conv_b"], dp["dt_bias"], dp["A_log"], H, D)
+    errs = {n: _rel(o.float(), r) for n, o, r in zip(("q", "k", "v", "g", "beta"), (q, k, v, g, beta), ref)}
+    _check(errs, TOL[torch.bfloat16], "producer full size")
+
+
+NORM_CASES = [
+    (2, 37, 3, 64, torch.float32),
+    (1, 100, 12, 64, torch.float32),
+    (2, 5, 4, 32, torch.float32),
+    (1, 9, 16, 128, torch.float32),
+    (1, 130, 2, 4, torch.float32),
+    (4, 65, 12, 64, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("B,T,H,D,dtype", NORM_CASES)
+def test_gated_rmsnorm_parity(B, T, H, D, dtype):
+    from mlx_vit_amd import gated_rmsnorm_backward, gated_rmsnorm_forward
+    case = f"gated_rmsnorm B={B} T={T} H={H} D={D} {dtype}"
+    print(case, flush=True)
+    g = torch.Generator().manual_seed(T + D)
+    o = torch.randn(B, T, H, D, generator=g).to(dtype)
+    wide = torch.randn(B, T, H * D + 8, generator=g).to(dtype)   # the gate as a strided column slice
+    w = 1 + 0.1 * torch.randn(D, generator=g)
+    dy = torch.randn(B, T, H * D, generator=g).to(dtype)
+    z = wide[..., 8:]
+    y = gated_rmsnorm_forward(o.to(DEV), wide.to(DEV)[..., 8:], w.to(DEV), 1e-5)
+    do, dz, dw = gated_rmsnorm_backward(o.to(DEV), wide.to(DEV)[..., 8:], w.to(DEV), 1e-5, dy.to(DEV))
+    torch.cuda.synchronize()
+    lo, lz, lw = (t.double().requires_grad_() for t in (o, z, w))
+    ref = LR.gated_rms_norm(lo, lw, lz.reshape(B, T, H, D), 1e-5).reshape(B, T, H * D)
+    (ref * dy.double()).sum().backward()
+    errs = {"y": _rel(y, ref), "do": _rel(do, lo.grad), "dz": _rel(dz, lz.grad), "dw": _rel(dw, lw.grad)}
+    _check(errs, TOL[dtype], case)
+
+
+def _layer_params(layer):
+    return {n: p.detach().cpu().double() for n, p in layer.named_parameters()}
+
+
+@pytest.mark.parametrize("dtype,with_state", [(torch.float32, False), (torch.float32, True),
+                                              (torch.bfloat16, False)])
+def test_layer_parity(dtype, with_state):
+    """The whole GatedDeltaLayer (projections, producer, HIP recurrence, gated
+    RMSNorm, o_proj) forward and backward against the fp64 restatement with
+    the step recurrence (nope_gdn_mlx.py:775-885 on the 'compiled' path)."""
+    from mlx_vit_amd import GatedDeltaLayer
+    B, L, hidden, H, D = 2, 100, 96, 3, 32
+    case = f"layer B={B} L={L} hidden={hidden} H={H} D={D} {dtype} state={with_state}"
+    print(case, flush=True)
+    torch.manual_seed(3)
+    layer = GatedDeltaLayer(hidden, H, D)
+    with torch.no_grad():
+        layer.dt_bias.normal_(0, 0.1)
+        layer.o_norm.weight.normal_(1, 0.1)
+    layer = layer.to(dtype)
+    # A_log and dt_bias stay fp32 in a bf16 model (nope_gdn_mlx.py:4959-4963)
+    layer.A_log.data = layer.A_log.data.float()
+    layer.dt_bias.data = layer.dt_bias.data.float()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, L, hidden, generator=g).to(dtype)
+    s0 = 0.1 * torch.randn(B, H, D, D, generator=g) if with_state else None
+    cot = torch.randn(B, L, hidden, generator=g).to(dtype)
+    cot_s = torch.randn(B, H, D, D, generator=g)
+    ref_params = _layer_params(layer)
+    layer = layer.to(DEV)
+    xd = x.to(DEV).requires_grad_()
+    s0d = None if s0 is None else s0.to(DEV).requires_grad_()
+    out, st = layer(xd, s0d)
+    ((out.float() * cot.to(DEV).float()).sum() + (st * cot_s.to(DEV)).sum()).backward()
+    torch.cuda.synchronize()
+
+    rp = {n: t.requires_grad_() for n, t in ref_params.items()}
+    rx = x.double().requires_grad_()
+    rs0 = None if s0 is None else s0.double().requires_grad_()
+    rout, rst = LR.layer_forward(rp, rx, H, D, rs0)
+    ((rout * cot.double()).sum() + (rst * cot_s.double()).sum()).backward()
+    errs = {"out": _rel(out, rout), "state": _rel(st, rst), "dx": _rel(xd.grad, rx.grad)}
+    if s0 is not None:
+        errs["ds0"] = _rel(s0d.grad, rs0.grad)
+    for n, p in layer.named_parameters():
+        errs["d" + n] = _rel(p.grad, rp[n].grad)
+    _check(errs, TOL[dtype], case)
