@@ -17,6 +17,9 @@ times the torch fp32 restatement of the reference's 'compiled' path
 bounded sample, and checks the HIP outputs against the fp64 C oracle.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload cfg2]
+
+``--workload layer`` instead times one GatedDeltaLayer forward + backward
+(hidden 768, H12, D64, bf16) and reports the KDA kernels' share of the step.
 """
 from __future__ import annotations
 
@@ -265,12 +268,104 @@ def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, s
     return baseline, {n: float(f"{e:.3e}") for n, e in errs.items()}
 
 
+LAYER_METRIC = "GatedDeltaLayer fwd+bwd tokens/sec @B8 L1568 hidden768 H12 D64 bf16"
+LAYER_KERNELS = {7: "producer_fwd", 8: "producer_bwd", 9: "rmsnorm_fwd", 10: "rmsnorm_bwd"}
+
+
+def layer_kernel_bytes(B, T, H, D, es=2):
+    """Algorithmic HBM bytes of the layer's element-wise kernels per call (bf16
+    activations, fp32 g / dg): each input read once, each output written once."""
+    N, HD = B * T, H * D
+    return {
+        7: N * ((3 * HD + HD + H) * es + 3 * HD * es + HD * 4 + H * es),
+        8: N * ((3 * HD + HD + H) * es + 3 * HD * es + HD * 4 + H * es + (3 * HD + HD + H) * es),
+        9: N * (2 * HD * es + HD * es),
+        10: N * (3 * HD * es + 2 * HD * es),
+    }
+
+
+def layer_bench(args):
+    """One GatedDeltaLayer (nope_gdn_mlx.py:653-885) forward + backward in bf16
+    (A_log / dt_bias fp32) on x (8, 1568, 768): projections as torch GEMMs, the
+    producer, recurrence and gated-RMSNorm kernels of this library."""
+    import ctypes
+    import torch
+    import mlx_vit_amd as kda
+    from mlx_vit_amd import _lib
+
+    B, T, hidden, H, D = 8, 1568, 768, 12, 64
+    torch.cuda.set_device(0)
+    torch.manual_seed(0)
+    layer = kda.GatedDeltaLayer(hidden, H, D).to(torch.bfloat16)
+    layer.A_log.data = layer.A_log.data.float()
+    layer.dt_bias.data = layer.dt_bias.data.float()
+    layer = layer.cuda()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(B, T, hidden, device="cuda", generator=gen).to(torch.bfloat16).requires_grad_()
+    cot = torch.randn(B, T, hidden, device="cuda", generator=gen).to(torch.bfloat16)
+
+    def step():
+        out, _ = layer(x)
+        out.backward(cot)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+
+    lib = _lib.load()
+    lib.kda_profile_enable(1)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    prof_ms = (time.perf_counter() - t1) / args.steps * 1e3
+    lib.kda_profile_enable(0)
+    lb = layer_kernel_bytes(B, T, H, D)
+    kernels, kda_ms, ew_ms = [], 0.0, 0.0
+    for kid in range(_lib.PROF_NKERNELS):
+        tot, cnt = ctypes.c_double(), ctypes.c_int()
+        _lib.check(lib.kda_profile_read(kid, ctypes.byref(tot), ctypes.byref(cnt)), "kda_profile_read")
+        if cnt.value == 0:
+            continue
+        avg_s = tot.value / cnt.value * 1e-3
+        row = {"name": lib.kda_profile_name(kid).decode(), "launches": cnt.value, "avg_us": round(avg_s * 1e6, 2)}
+        if kid in LAYER_KERNELS:   # the recurrence kernels' rates are reported by the cfg2 workload
+            by = lb[kid]
+            row.update(gbs=round(by / avg_s / 1e9, 1), hbm_frac=round(by / avg_s / PEAK_HBM, 4), alg_bytes=by)
+        kernels.append(row)
+        per_step_ms = tot.value / args.steps
+        if kid in LAYER_KERNELS:
+            ew_ms += per_step_ms
+        else:
+            kda_ms += per_step_ms
+    out = {
+        "metric": LAYER_METRIC, "value": round(B * T * args.steps / elapsed, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x, random-init layer of the reference's architecture)",
+        "config": {"workload": "GatedDeltaLayer fwd+bwd, x (8, 1568, 768), H12 D64, bf16 (A_log, dt_bias fp32)",
+                   "B": B, "T": T, "hidden": hidden, "H": H, "D": D},
+        "profiled_ms_per_step": round(prof_ms, 4),
+        "kda_ms_per_step": round(kda_ms, 4), "elementwise_ms_per_step": round(ew_ms, 4),
+        "kda_share": round(kda_ms / prof_ms, 4), "elementwise_share": round(ew_ms / prof_ms, 4),
+        "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["layer"], default="cfg2")
     ap.add_argument("--cpu-sample-tokens", type=int, default=392)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -285,6 +380,10 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the op on a "
               "single MI355X and reports that GPU's throughput.", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "layer":
+        layer_bench(args)
+        return
 
     import torch
     import mlx_vit_amd as kda

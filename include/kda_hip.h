@@ -182,14 +182,17 @@ int kda_layer_gated_rmsnorm_bwd(const void* o, const void* z, int64_t ld_z, cons
 size_t kda_layer_workspace_size(int which, int B, int T, int H, int D);
 
 /* ---- launch timing (instrumentation; no counterpart in the reference) ----
- * With profiling on, every kernel launch made by kda_fwd / kda_bwd is
- * bracketed by two HIP events recorded on the launch stream.  Used by the
- * benchmark to measure per-kernel durations live; the kernels do the same work
- * either way.  Kernel ids: 0 prep (forward), 1 recurrence (forward), 2 prep
- * (backward), 3 state recompute, 4 reverse state recurrence, 5 local adjoints,
- * 6 prep (training forward).
+ * With profiling on, every kernel launch made by kda_fwd / kda_bwd (and each
+ * kda_layer_* call) is bracketed by two HIP events recorded on the launch
+ * stream.  Used by the benchmark to measure per-kernel durations live; the
+ * kernels do the same work either way.  Kernel ids: 0 prep (forward),
+ * 1 recurrence (forward), 2 prep (backward), 3 state recompute, 4 reverse
+ * state recurrence, 5 local adjoints, 6 prep (training forward), 7 layer
+ * producer (forward), 8 layer producer (backward, with its parameter-gradient
+ * reduction), 9 gated RMSNorm (forward), 10 gated RMSNorm (backward, with its
+ * reduction).
  * kda_profile_read must be called after the streams have completed. */
-#define KDA_PROF_NKERNELS 7
+#define KDA_PROF_NKERNELS 11
 int kda_profile_enable(int on);              /* 1: clear records and start; 0: stop */
 const char* kda_profile_name(int id);
 int kda_profile_read(int id, double* total_ms, int* launches);

@@ -120,11 +120,14 @@ int hip_fail(hipError_t e, const char* where) {
 }
 
 // ---- optional launch timing: an event pair around each launch, on its stream ----
-enum { PROF_PREP_FWD = 0, PROF_RECUR_FWD, PROF_PREP_BWD, PROF_RECUR_H, PROF_DH, PROF_LOCAL, PROF_PREP_TRAIN };
+enum { PROF_PREP_FWD = 0, PROF_RECUR_FWD, PROF_PREP_BWD, PROF_RECUR_H, PROF_DH, PROF_LOCAL, PROF_PREP_TRAIN,
+       PROF_PRODUCER_FWD, PROF_PRODUCER_BWD, PROF_RMSNORM_FWD, PROF_RMSNORM_BWD };
 const char* const kProfNames[KDA_PROF_NKERNELS] = {"kda_prep_kernel(fwd)", "kda_recur_kernel(fwd)",
                                                    "kda_prep_kernel(bwd)", "kda_recur_kernel(states)",
                                                    "kda_dh_kernel", "kda_bwd_local_kernel",
-                                                   "kda_prep_kernel(train)"};
+                                                   "kda_prep_kernel(train)", "producer_fwd_kernel",
+                                                   "producer_bwd_kernel(+reduce)", "rmsnorm_fwd_kernel",
+                                                   "rmsnorm_bwd_kernel(+reduce)"};
 struct Profiler {
     std::mutex mu;
     bool on = false;
@@ -581,8 +584,10 @@ int kda_layer_producer_fwd(const void* xq, const void* xk, const void* xv, const
     a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
     a.ld_x = ld_x; a.ld_f = ld_f; a.ld_b = ld_b;
     a.B = B; a.T = T; a.H = H; a.D = D; a.scale = scale; a.beta_mult = beta_mult;
-    const hipError_t e = kda::launch_producer_fwd(a, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16,
-                                                  static_cast<hipStream_t>(stream));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const hipError_t e = timed(PROF_PRODUCER_FWD, st, [&] {
+        return kda::launch_producer_fwd(a, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16, st);
+    });
     return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_producer_fwd");
 }
 
@@ -629,8 +634,10 @@ int kda_layer_producer_bwd(const void* xq, const void* xk, const void* xv, const
     a.colsum = a.part + (size_t)kda::producer_partials(B, T) * 17 * HD;
     a.ld_x = ld_x; a.ld_f = ld_f; a.ld_b = ld_b; a.ld_dx = ld_dx; a.ld_df = ld_df; a.ld_db = ld_db;
     a.B = B; a.T = T; a.H = H; a.D = D; a.scale = scale; a.beta_mult = beta_mult;
-    const hipError_t e = kda::launch_producer_bwd(a, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16,
-                                                  static_cast<hipStream_t>(stream));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const hipError_t e = timed(PROF_PRODUCER_BWD, st, [&] {
+        return kda::launch_producer_bwd(a, dtype == KDA_DTYPE_BF16, g_dtype == KDA_DTYPE_BF16, st);
+    });
     return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_producer_bwd");
 }
 
@@ -648,7 +655,8 @@ int kda_layer_gated_rmsnorm_fwd(const void* o, const void* z, int64_t ld_z, cons
     kda::NormArgs a{};
     a.o = o; a.z = z; a.w = w; a.y = y; a.ld_z = ld_z; a.ld_y = ld_y;
     a.rows = rows; a.H = H; a.D = D; a.eps = eps;
-    const hipError_t e = kda::launch_rmsnorm_fwd(a, dtype == KDA_DTYPE_BF16, static_cast<hipStream_t>(stream));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const hipError_t e = timed(PROF_RMSNORM_FWD, st, [&] { return kda::launch_rmsnorm_fwd(a, dtype == KDA_DTYPE_BF16, st); });
     return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_gated_rmsnorm_fwd");
 }
 
@@ -677,7 +685,8 @@ int kda_layer_gated_rmsnorm_bwd(const void* o, const void* z, int64_t ld_z, cons
     a.part = static_cast<float*>(workspace);
     a.colsum = a.part + (size_t)kda::rmsnorm_partials(rows) * HD;
     a.rows = rows; a.H = H; a.D = D; a.eps = eps;
-    const hipError_t e = kda::launch_rmsnorm_bwd(a, dtype == KDA_DTYPE_BF16, static_cast<hipStream_t>(stream));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const hipError_t e = timed(PROF_RMSNORM_BWD, st, [&] { return kda::launch_rmsnorm_bwd(a, dtype == KDA_DTYPE_BF16, st); });
     return e == hipSuccess ? ok() : hip_fail(e, "kda_layer_gated_rmsnorm_bwd");
 }
 
