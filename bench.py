@@ -19,7 +19,9 @@ bounded sample, and checks the HIP outputs against the fp64 C oracle.
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload cfg2]
 
 ``--workload layer`` instead times one GatedDeltaLayer forward + backward
-(hidden 768, H12, D64, bf16) and reports the KDA kernels' share of the step.
+(hidden 768, H12, D64, bf16) and reports the KDA kernels' share of the step;
+``--workload model`` times the config-4 training step (12 GDN blocks, 8 clips)
+and reports the same share.
 """
 from __future__ import annotations
 
@@ -360,12 +362,81 @@ def layer_bench(args):
     print(json.dumps(out), flush=True)
 
 
+MODEL_METRIC = "NoPE-GDN ViT-B train step (config 4) clips/sec @B8 16x224x224, 12 GDN blocks, bf16"
+
+
+def model_bench(args):
+    """Config 4: one AdamW training step (forward, label-smoothed loss,
+    backward, global clip, update; train_mlx_k400.py:379-408) of the NoPE-GDN
+    classifier with 12 GDN blocks of width 768 on 8 clips of 16 x 224 x 224,
+    bf16 weights with A_log / dt_bias in fp32, random init, synthetic clips."""
+    import ctypes
+    import torch
+    from mlx_vit_amd import _lib
+    from mlx_vit_amd import model as M
+    from mlx_vit_amd import train as TR
+
+    B = 8
+    torch.cuda.set_device(0)
+    torch.manual_seed(0)
+    model = M.to_bf16(M.config4()).cuda()
+    step = TR.TrainStep(model)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    video = torch.randn(B, 16, 224, 224, 3, device="cuda", generator=gen).to(torch.bfloat16)
+    target = torch.randint(0, 400, (B,), device="cuda", generator=gen)
+    for _ in range(args.warmup):
+        step(video, target)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step(video, target)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    lib = _lib.load()
+    lib.kda_profile_enable(1)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step(video, target)
+    torch.cuda.synchronize()
+    prof_ms = (time.perf_counter() - t1) / args.steps * 1e3
+    lib.kda_profile_enable(0)
+    kernels, kda_ms, ew_ms = [], 0.0, 0.0
+    for kid in range(_lib.PROF_NKERNELS):
+        tot, cnt = ctypes.c_double(), ctypes.c_int()
+        _lib.check(lib.kda_profile_read(kid, ctypes.byref(tot), ctypes.byref(cnt)), "kda_profile_read")
+        if cnt.value == 0:
+            continue
+        kernels.append({"name": lib.kda_profile_name(kid).decode(), "launches": cnt.value,
+                        "avg_us": round(tot.value / cnt.value * 1e3, 2)})
+        if kid in LAYER_KERNELS:
+            ew_ms += tot.value / args.steps
+        else:
+            kda_ms += tot.value / args.steps
+    tokens = B * 1568
+    out = {
+        "metric": MODEL_METRIC, "value": round(B * args.steps / elapsed, 3), "unit": "clips/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) clips, random labels; random-init weights of the reference's architecture)",
+        "config": {"workload": "NoPEGDNClassifier(encoder_depth=0, processor_depth=12, gdn_ratio=12, "
+                               "processor_dim=768, processor_heads=12, num_frames=16, num_classes=400), "
+                               "AdamW step", "global_batch": B, "tokens_per_clip": 1568},
+        "tokens_per_s": round(tokens * args.steps / elapsed, 1), "loss": round(float(loss), 4),
+        "profiled_ms_per_step": round(prof_ms, 3), "kda_ms_per_step": round(kda_ms, 3),
+        "layer_elementwise_ms_per_step": round(ew_ms, 3), "kda_share": round(kda_ms / prof_ms, 4),
+        "layer_elementwise_share": round(ew_ms / prof_ms, 4), "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["layer"], default="cfg2")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["layer", "model"], default="cfg2")
     ap.add_argument("--cpu-sample-tokens", type=int, default=392)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -383,6 +454,9 @@ def main():
 
     if args.workload == "layer":
         layer_bench(args)
+        return
+    if args.workload == "model":
+        model_bench(args)
         return
 
     import torch

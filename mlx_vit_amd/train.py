@@ -1,0 +1,103 @@
+"""Training step of the reference trainer (train_mlx_k400.py) in torch.
+
+* ``cosine_warmup_lr`` -- linear warm-up then cosine decay (train_mlx_k400.py:229-234);
+* ``loss_fn`` -- cross entropy on fp32 logits with label smoothing
+  (train_mlx_k400.py:255-266): (1 - ls) * nll + ls * mean(-log_softmax);
+* ``clip_grads_by_norm`` -- global-norm clipping, scale = min(max_norm /
+  (||g|| + 1e-6), 1) (train_mlx_k400.py:241-252);
+* ``AdamW`` -- MLX's AdamW update, which has no bias correction by default:
+  p <- p (1 - lr wd); m <- b1 m + (1 - b1) g; v <- b2 v + (1 - b2) g^2;
+  p <- p - lr m / (sqrt(v) + eps), with the moments in the parameter's dtype
+  (train_mlx_k400.py:548-549: betas (0.9, 0.95), weight decay 0.05);
+* ``TrainStep`` -- forward, loss, backward, clip, update
+  (train_mlx_k400.py:379-408).
+"""
+from __future__ import annotations
+
+import math
+from typing import Iterable, List
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+def cosine_warmup_lr(step: int, total_steps: int, warmup_steps: int, base_lr: float) -> float:
+    if step < warmup_steps:
+        return base_lr * step / max(1, warmup_steps)
+    progress = (step - warmup_steps) / max(1, total_steps - warmup_steps)
+    return 0.5 * base_lr * (1 + math.cos(math.pi * progress))
+
+
+def loss_fn(logits: torch.Tensor, target: torch.Tensor, label_smoothing: float = 0.0) -> torch.Tensor:
+    logits = logits.float()
+    if label_smoothing > 0:
+        logp = F.log_softmax(logits, dim=-1)
+        nll = -logp.gather(-1, target[:, None]).squeeze(-1)
+        smooth = -logp.mean(dim=-1)
+        return ((1 - label_smoothing) * nll + label_smoothing * smooth).mean()
+    return F.cross_entropy(logits, target)
+
+
+@torch.no_grad()
+def clip_grads_by_norm(params: Iterable[torch.Tensor], max_norm: float) -> torch.Tensor:
+    """Scale every gradient by min(max_norm / (total_norm + 1e-6), 1); returns
+    the total norm (fp32)."""
+    grads = [p.grad for p in params if p.grad is not None]
+    if not grads:
+        return torch.zeros(())
+    norms = torch._foreach_norm([g.float() for g in grads])
+    total = torch.linalg.vector_norm(torch.stack(norms))
+    scale = torch.clamp(max_norm / (total + 1e-6), max=1.0)
+    for g in grads:
+        g.mul_(scale.to(g.dtype))
+    return total
+
+
+class AdamW:
+    """MLX's AdamW (no bias correction), moments in the parameter dtype."""
+
+    def __init__(self, params: Iterable[nn.Parameter], lr: float = 3e-4, betas=(0.9, 0.95), eps: float = 1e-8,
+                 weight_decay: float = 0.05):
+        self.params: List[nn.Parameter] = [p for p in params if p.requires_grad]
+        self.lr, self.betas, self.eps, self.weight_decay = lr, betas, eps, weight_decay
+        self.m = [torch.zeros_like(p) for p in self.params]
+        self.v = [torch.zeros_like(p) for p in self.params]
+
+    @torch.no_grad()
+    def step(self) -> None:
+        b1, b2 = self.betas
+        lr, wd = self.lr, self.weight_decay
+        for p, m, v in zip(self.params, self.m, self.v):
+            if p.grad is None:
+                continue
+            g = p.grad
+            p.mul_(1 - lr * wd)
+            m.mul_(b1).add_(g, alpha=1 - b1)
+            v.mul_(b2).addcmul_(g, g, value=1 - b2)
+            p.addcdiv_(m, v.sqrt().add_(self.eps), value=-lr)
+
+    def zero_grad(self) -> None:
+        for p in self.params:
+            p.grad = None
+
+
+class TrainStep:
+    """One optimisation step: forward, label-smoothed loss, backward, global
+    clip, AdamW update.  Returns the loss (a 0-d fp32 tensor)."""
+
+    def __init__(self, model: nn.Module, lr: float = 3e-4, weight_decay: float = 0.05, betas=(0.9, 0.95),
+                 grad_clip: float = 1.0, label_smoothing: float = 0.1):
+        self.model = model
+        self.opt = AdamW(model.parameters(), lr=lr, betas=betas, weight_decay=weight_decay)
+        self.grad_clip = grad_clip
+        self.label_smoothing = label_smoothing
+
+    def __call__(self, video: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+        self.opt.zero_grad()
+        loss = loss_fn(self.model(video), target, self.label_smoothing)
+        loss.backward()
+        if self.grad_clip > 0:
+            clip_grads_by_norm(self.opt.params, self.grad_clip)
+        self.opt.step()
+        return loss.detach()
