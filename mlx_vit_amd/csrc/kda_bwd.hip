@@ -95,6 +95,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
     int flag = chunk_load<D, TI, TG>(s, q, k, g, beta, base, rs, bbase, a.H, valid);
     chunk_cumsum<D>(s);
     const int unsafe = chunk_factors<D, PREC>(s, flag);
+    if (unsafe) chunk_band<D, 256>(s, __syncthreads_or(flag));
 
     // wave w owns channel tile nt = w: rows t = 16 m + 4 g4 + e, channel d
     const int nt = w;
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                     const int t = BS * m + 4 * g4 + e;
                     const float gt = s.g[t][d];
                     float ak = 0.f, aq = 0.f, ag = 0.f;
-                    for (int sx = 0; sx < C; ++sx) {
+                    for (int sx = s.blo[t]; sx <= s.bhi[t]; ++sx) {
                         const float gs = s.g[sx][d];
                         if (sx <= t) {      // row t: dP[t][sx] (strict), dA[t][sx]
                             const float ex = kexp<PREC>(gt - gs);
@@ -1065,13 +1066,19 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             sm.akk[BS * i + e / BS][BS * j + (e % BS)] = 0.f;
         }
     } else {
-        // pairwise path: raw k in kr, exact exp(gamma_t - gamma_s)
+        // pairwise path: raw k in kr, exact exp(gamma_t - gamma_s), over the
+        // decay band of each row (the band also bounds phase 4's loops)
+        chunk_band<D, NTH>(s, __syncthreads_or(flag));
         for (int p = tid; p < C * C; p += NTH) {
             const int t = p / C, sx = p - t * C;
+            if (!(sx < t && sx >= s.blo[t])) sm.akk[t][sx] = 0.f;
+        }
+        for (int qq = tid; qq < s.bpre[C]; qq += NTH) {
+            const int t = band_row(s, qq), sx = s.blo[t] + qq - s.bpre[t];
+            if (sx == t) continue;
             float ak = 0.f;
-            if (sx < t)
-                for (int dd = 0; dd < D; ++dd)
-                    ak += ld1<ST>(&s.kr[t][dd]) * (ld1<ST>(&s.kr[sx][dd]) * kexp<PREC>(s.g[t][dd] - s.g[sx][dd]));
+            for (int dd = 0; dd < D; ++dd)
+                ak += ld1<ST>(&s.kr[t][dd]) * (ld1<ST>(&s.kr[sx][dd]) * kexp<PREC>(s.g[t][dd] - s.g[sx][dd]));
             sm.akk[t][sx] = ak;
         }
         __syncthreads();
@@ -1442,7 +1449,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     const int t = BS * (2 * rh + mm) + 4 * g4 + e;
                     const float gt = s.g[t][d], bt = s.beta[t];
                     float ak = 0.f, aq = 0.f, ag = 0.f;
-                    for (int sx = 0; sx < C; ++sx) {
+                    for (int sx = s.blo[t]; sx <= s.bhi[t]; ++sx) {
                         const float gs = s.g[sx][d];
                         if (sx <= t) {
                             const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - gs);

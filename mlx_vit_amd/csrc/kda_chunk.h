@@ -36,6 +36,12 @@ struct ChunkLds {
             float er[NB][D];
             float f[6][D];
         };
+        struct {         // pairwise path only, where f is not used; written after er / f
+            float er_keep[NB][D];
+            float bw[C];            // slowest-channel decay cumsum
+            uint16_t bpre[C + 1];   // band-width prefix sums (< 2081)
+            uint8_t blo[C], bhi[C]; // decay band of each row
+        };
         float tmp[256];  // cumsum partial totals; dead before er / f are written
     };
     float beta[C];
@@ -191,6 +197,12 @@ struct ChunkSmem {
             float egr[NB][D];   // e^{G - gamma_16j}
             float f[6][D];      // e^{gamma_16i - gamma_16j}, j < i
         };
+        struct {                // pairwise path only, where egr and f are not used;
+            float er_keep[NB][D];   // written after the factor tables
+            float bw[C];            // slowest-channel decay cumsum
+            uint16_t bpre[C + 1];   // band-width prefix sums (< 2081)
+            uint8_t blo[C], bhi[C]; // decay band of each row
+        };
         float tmp[512];
     };
     float beta[C];
@@ -324,6 +336,94 @@ __device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, 
             for (int g = 0; g < 4; ++g) fc[64 * w + 16 * g + c] = frag4_from_f32<3>(&x[4 * g]);
         }
     }
+}
+
+
+// Decay band of every row for the pairwise path.  With gamma non-increasing in
+// t (every g <= 0), let w_u = min over channels of gamma_{u-1} - gamma_u (the
+// slowest channel's decay at step u) and W its cumsum: every channel decays by
+// at least W_t - W_s between rows s < t, so exp(gamma_t - gamma_s) <
+// e^{-BAND_CUT} in all channels once W_t - W_s > BAND_CUT.  blo[t] / bhi[t] are
+// the first / last rows s with W within BAND_CUT of W_t; pairs outside
+// contribute below 1.8e-35 of an O(1) term and are skipped.  A chunk with any
+// g > 0 or NaN (nonmono) keeps the full range.  Also sets bpre[t] = sum over
+// u < t of (u - blo[u] + 1), bpre[C] the total.  Called by the whole
+// workgroup (barriers inside); the arrays are ready after.
+constexpr float BAND_CUT = 80.0f;
+template <int D, int NTH, typename S>
+__device__ void chunk_band(S& s, int nonmono) {
+    static_assert(C == 64, "one lane per row in the scans below");
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    constexpr int NW = NTH / 64;
+    if (!nonmono) {
+        for (int u = w; u < C; u += NW) {
+            float m = 3.0e38f;
+            if (u > 0)
+                for (int d = lane; d < D; d += 64) m = fminf(m, s.g[u - 1][d] - s.g[u][d]);
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) m = fminf(m, __shfl_xor(m, o));
+            if (lane == 0) s.bw[u] = (u > 0) ? m : 0.f;
+        }
+    }
+    __syncthreads();
+    if (w == 0) {
+        // W = inclusive scan of w over the rows; then the band by binary search
+        float W = nonmono ? 0.f : s.bw[lane];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float x = __shfl_up(W, o);
+            if (lane >= o) W += x;
+        }
+        s.bw[lane] = W;
+        // one wave: its LDS writes are done before its reads below (no barrier here,
+        // the other waves wait at the one after this block)
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        int lo = 0, hi = C - 1;
+        if (!nonmono) {
+            // first s <= t with W_s >= W_t - CUT, last s >= t with W_s <= W_t + CUT
+            int a = 0, b = lane;
+            while (a < b) {
+                const int m = (a + b) >> 1;
+                if (s.bw[m] >= W - BAND_CUT) b = m;
+                else a = m + 1;
+            }
+            lo = a;
+            a = lane;
+            b = C - 1;
+            while (a < b) {
+                const int m = (a + b + 1) >> 1;
+                if (s.bw[m] <= W + BAND_CUT) a = m;
+                else b = m - 1;
+            }
+            hi = a;
+        }
+        s.blo[lane] = (uint8_t)lo;
+        s.bhi[lane] = (uint8_t)hi;
+        // exclusive scan of the band widths (pairs s <= t)
+        const int wdt = lane - lo + 1;
+        int inc = wdt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int x = __shfl_up(inc, o);
+            if (lane >= o) inc += x;
+        }
+        s.bpre[lane] = (uint16_t)(inc - wdt);
+        if (lane == C - 1) s.bpre[C] = (uint16_t)inc;
+    }
+    __syncthreads();
+}
+
+// Row t of the band pair with index q (0 <= q < bpre[C]): the largest t with
+// bpre[t] <= q; the pair is (t, blo[t] + q - bpre[t]).
+template <typename S>
+__device__ __forceinline__ int band_row(const S& s, int q) {
+    int lo = 0, hi = C;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s.bpre[mid] <= q) lo = mid;
+        else hi = mid;
+    }
+    return lo;
 }
 
 }  // namespace kda

@@ -93,16 +93,24 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     // PHASE 2
 
     if (unsafe) {
-        // pairwise path: raw q in ql, raw k in kr, exact exp(gamma_t - gamma_s)
+        // pairwise path: raw q in ql, raw k in kr, exact exp(gamma_t - gamma_s),
+        // over the decay band of each row only (pairs outside it are zero)
+        chunk_band<D, 256>(s, __syncthreads_or(flag));
         for (int p = tid; p < C * C; p += 256) {
             const int t = p / C, sx = p - t * C;
+            if (sx <= t && sx >= s.blo[t]) continue;
+            sa[t][sx] = 0.f;
+            if (a.Akk) a.Akk[cCC + (size_t)t * C + sx] = 0.f;
+            if (oAqk) st1<ST>(oAqk + cCC + (size_t)t * C + sx, 0.f);
+            if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, 0.f);
+        }
+        for (int qq = tid; qq < s.bpre[C]; qq += 256) {
+            const int t = band_row(s, qq), sx = s.blo[t] + qq - s.bpre[t];
             float ak = 0.f, aq = 0.f;
-            if (sx <= t) {
-                for (int d = 0; d < D; ++d) {
-                    const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(s.g[t][d] - s.g[sx][d]);
-                    ak += ld1<ST>(&s.kr[t][d]) * ks;
-                    aq += ld1<ST>(&s.ql[t][d]) * ks;
-                }
+            for (int d = 0; d < D; ++d) {
+                const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(s.g[t][d] - s.g[sx][d]);
+                ak += ld1<ST>(&s.kr[t][d]) * ks;
+                aq += ld1<ST>(&s.ql[t][d]) * ks;
             }
             const float akk = (sx < t) ? ak : 0.f;
             sa[t][sx] = akk;
