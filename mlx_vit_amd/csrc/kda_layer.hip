@@ -33,7 +33,7 @@ namespace {
 constexpr int KC = 4;        // conv taps (ShortCausalConv1d(kernel_size=4))
 constexpr int CPW = 256;     // channels per wave
 constexpr int MAXW = 8;      // H*D <= 2048
-constexpr int PR = 16;       // producer forward: rows per workgroup
+constexpr int PR = 8;        // producer forward: rows per workgroup
 constexpr int BR = 8;        // producer backward: rows per strip
 constexpr int BNS = 4;       // producer backward: strips per workgroup
 constexpr int NR = 16;       // norm: rows per strip
@@ -62,9 +62,16 @@ template <> struct Vec4<uint16_t> {
     }
 };
 
-__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
-// log(1 + e^x) without overflow (nope_gdn_mlx.py:83-86)
-__device__ __forceinline__ float softplus(float x) { return log1pf(__expf(-fabsf(x))) + fmaxf(x, 0.f); }
+// 1 / (1 + e^-x) with the hardware reciprocal (1 ulp); e^-x = inf gives 0
+__device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// log(1 + e^x) without overflow (nope_gdn_mlx.py:83-86): max(x, 0) + log1p(e^-|x|),
+// log1p(e) = log(u) - ((u - 1) - e) / u with u = 1 + e (the rounding of u is
+// compensated to first order), on the hardware log
+__device__ __forceinline__ float softplus(float x) {
+    const float e = __expf(-fabsf(x));
+    const float u = 1.f + e;
+    return fmaxf(x, 0.f) + (__logf(u) - ((u - 1.f) - e) * __builtin_amdgcn_rcpf(u));
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -100,16 +107,16 @@ struct Lanes {
     }
 };
 
-__device__ __forceinline__ void load_taps(const ProdArgs& a, int i, const Lanes& L, float (&wt)[4][KC],
-                                          float (&bias)[4]) {
-    const float4* p = reinterpret_cast<const float4*>(a.conv_w + ((size_t)i * L.HD + L.cc) * KC);
+template <int I>
+__device__ __forceinline__ void load_taps(const ProdArgs& a, const Lanes& L, float (&wt)[4][KC], float (&bias)[4]) {
+    const float4* p = reinterpret_cast<const float4*>(a.conv_w + ((size_t)I * L.HD + L.cc) * KC);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float4 v = p[e];
         wt[e][0] = v.x; wt[e][1] = v.y; wt[e][2] = v.z; wt[e][3] = v.w;
     }
     if (a.conv_b) {
-        const float4 v = *reinterpret_cast<const float4*>(a.conv_b + (size_t)i * L.HD + L.cc);
+        const float4 v = *reinterpret_cast<const float4*>(a.conv_b + (size_t)I * L.HD + L.cc);
         bias[0] = v.x; bias[1] = v.y; bias[2] = v.z; bias[3] = v.w;
     } else {
         bias[0] = bias[1] = bias[2] = bias[3] = 0.f;
@@ -118,6 +125,41 @@ __device__ __forceinline__ void load_taps(const ProdArgs& a, int i, const Lanes&
 
 // ---------------------------------------------------------------- producer, forward
 // Workgroup = (batch row b, strip of PR tokens).
+// Conv + SiLU of PR rows of conv input i at channel quad cc (rows before 0
+// read as zero, rows past T clamp; their results are dropped by the caller).
+// The conv input is a template parameter so that its pointer is a fixed field
+// of the kernel arguments (a runtime choice among xq / xk / xv makes the
+// compiler copy the argument block to scratch memory).
+template <typename ST, int I>
+__device__ __forceinline__ void conv_silu_rows(const ProdArgs& a, const Lanes& L, int t0, size_t rb,
+                                               float (&out)[PR][4]) {
+    const int T = a.T;
+    const ST* x = static_cast<const ST*>(I == 0 ? a.xq : I == 1 ? a.xk : a.xv);
+    float wt[4][KC], bias[4];
+    load_taps<I>(a, L, wt, bias);
+    float xr[PR + KC - 1][4];
+#pragma unroll
+    for (int r = 0; r < PR + KC - 1; ++r) {
+        const int t = t0 - (KC - 1) + r;
+        Vec4<ST>::ld(x + (rb + min(max(t, 0), T - 1)) * a.ld_x + L.cc, xr[r]);
+        if (t < 0) xr[r][0] = xr[r][1] = xr[r][2] = xr[r][3] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < PR; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float y = bias[e];
+#pragma unroll
+            for (int k = 0; k < KC; ++k) y = fmaf(wt[e][k], xr[j + k][e], y);
+            out[j][e] = y * sigm(y);
+        }
+}
+
+// Workgroup = (batch row b, strip of PR tokens).  q and k need the norm of the
+// whole H*D row: a first pass forms the per-row sums of squares (reduced
+// across the workgroup through LDS), and after the barrier q and k are
+// recomputed from their (cached) input rows rather than held in registers,
+// which keeps the kernel at about half the VGPRs and twice the waves.
 template <typename ST, typename GT>
 __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
     __shared__ float red[2][MAXW][PR];
@@ -128,45 +170,33 @@ __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
     const int b = wg / nstrip, t0 = (wg % nstrip) * PR;
     const size_t rb = (size_t)b * T;
 
-    float s[2][PR][4];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const ST* x = static_cast<const ST*>(i == 0 ? a.xq : i == 1 ? a.xk : a.xv);
-        float wt[4][KC], bias[4];
-        load_taps(a, i, L, wt, bias);
-        float xr[PR + KC - 1][4];
-#pragma unroll
-        for (int r = 0; r < PR + KC - 1; ++r) {
-            const int t = t0 - (KC - 1) + r;
-            const int tc = min(max(t, 0), T - 1);
-            Vec4<ST>::ld(x + (rb + tc) * a.ld_x + L.cc, xr[r]);
-            if (t < 0) xr[r][0] = xr[r][1] = xr[r][2] = xr[r][3] = 0.f;
-        }
+    auto row_norms = [&](const float (&sv)[PR][4], int i) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < PR; ++j) {
-            float sv[4];
+            float ss = 0.f;
+            if (L.live)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float y = bias[e];
-#pragma unroll
-                for (int k = 0; k < KC; ++k) y = fmaf(wt[e][k], xr[j + k][e], y);
-                sv[e] = y * sigm(y);
-            }
-            if (i == 2) {
-                if (t0 + j < T && L.live)
-                    Vec4<ST>::st(static_cast<ST*>(a.v) + (rb + t0 + j) * L.HD + L.cc, sv);
-            } else {
-                float ss = 0.f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (!L.live) sv[e] = 0.f;
-                    s[i][j][e] = sv[e];
-                    ss = fmaf(sv[e], sv[e], ss);
-                }
-                ss = wave_sum(ss);
-                if (L.lane == 0) red[i][L.w][j] = ss;
-            }
+                for (int e = 0; e < 4; ++e) ss = fmaf(sv[j][e], sv[j][e], ss);
+            ss = wave_sum(ss);
+            if (L.lane == 0) red[i][L.w][j] = ss;
         }
+    };
+    {
+        float sv[PR][4];
+        conv_silu_rows<ST, 0>(a, L, t0, rb, sv);
+        row_norms(sv, 0);
+    }
+    {
+        float sv[PR][4];
+        conv_silu_rows<ST, 1>(a, L, t0, rb, sv);
+        row_norms(sv, 1);
+    }
+    {
+        float sv[PR][4];
+        conv_silu_rows<ST, 2>(a, L, t0, rb, sv);
+#pragma unroll
+        for (int j = 0; j < PR; ++j)
+            if (t0 + j < T && L.live) Vec4<ST>::st(static_cast<ST*>(a.v) + (rb + t0 + j) * L.HD + L.cc, sv[j]);
     }
 
     // decay gate, in fp32 before the cast to g's dtype (nope_gdn_mlx.py:816-820)
@@ -190,17 +220,16 @@ __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
     if (L.live && L.cc % a.D == 0) {
         const ST* xb = static_cast<const ST*>(a.xb);
         ST* beta = static_cast<ST*>(a.beta);
-        for (int j = 0; j < PR && t0 + j < T; ++j) {
-            const size_t r = rb + t0 + j;
-            st1<ST>(beta + r * a.H + L.h, sigm(ld1<ST>(xb + r * a.ld_b + L.h)) * a.beta_mult);
-        }
+        float xv[PR];   // all loads first: one round trip, not PR
+#pragma unroll
+        for (int j = 0; j < PR; ++j) xv[j] = ld1<ST>(xb + (rb + min(t0 + j, T - 1)) * a.ld_b + L.h);
+#pragma unroll
+        for (int j = 0; j < PR; ++j)
+            if (t0 + j < T) st1<ST>(beta + (rb + t0 + j) * a.H + L.h, sigm(xv[j]) * a.beta_mult);
     }
 
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        ST* out = static_cast<ST*>(i == 0 ? a.q : a.k);
-        const float mult = i == 0 ? a.scale : 1.f;
+    auto finish = [&](const float (&sv)[PR][4], int i, ST* out, float mult) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < PR; ++j) {
             float tot = 0.f;
@@ -208,9 +237,19 @@ __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
             const float inv = mult / fmaxf(sqrtf(tot), L2_EPS);
             float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = s[i][j][e] * inv;
+            for (int e = 0; e < 4; ++e) o[e] = sv[j][e] * inv;
             if (t0 + j < T && L.live) Vec4<ST>::st(out + (rb + t0 + j) * L.HD + L.cc, o);
         }
+    };
+    {
+        float sv[PR][4];
+        conv_silu_rows<ST, 0>(a, L, t0, rb, sv);
+        finish(sv, 0, static_cast<ST*>(a.q), a.scale);
+    }
+    {
+        float sv[PR][4];
+        conv_silu_rows<ST, 1>(a, L, t0, rb, sv);
+        finish(sv, 1, static_cast<ST*>(a.k), 1.f);
     }
 }
 
@@ -218,14 +257,15 @@ __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
 // dy (the adjoint of the conv output) of tensor i for NRW rows from t0; the
 // x rows t0-3 .. t0+NRW-1 come back in xr for the tap gradients.  For q and k
 // the row norms reduce across the workgroup through red (one barrier).
-template <typename ST, int NRW>
-__device__ __forceinline__ void prod_dy_rows(const ProdArgs& a, const Lanes& L, int i, int t0, size_t rb,
+template <typename ST, int NRW, int I>
+__device__ __forceinline__ void prod_dy_rows(const ProdArgs& a, const Lanes& L, int t0, size_t rb,
                                              const float (&wt)[4][KC], const float (&bias)[4],
                                              float (*red)[2][BR], float (&dy)[NRW][4],
                                              float (&xr)[NRW + KC - 1][4]) {
     const int T = a.T;
-    const ST* x = static_cast<const ST*>(i == 0 ? a.xq : i == 1 ? a.xk : a.xv);
-    const ST* d = static_cast<const ST*>(i == 0 ? a.dq : i == 1 ? a.dk : a.dv);
+    constexpr int i = I;
+    const ST* x = static_cast<const ST*>(I == 0 ? a.xq : I == 1 ? a.xk : a.xv);
+    const ST* d = static_cast<const ST*>(I == 0 ? a.dq : I == 1 ? a.dk : a.dv);
 #pragma unroll
     for (int r = 0; r < NRW + KC - 1; ++r) {
         const int t = t0 - (KC - 1) + r;
@@ -293,39 +333,24 @@ __device__ __forceinline__ void prod_dy_rows(const ProdArgs& a, const Lanes& L, 
                            : 0.f;
 }
 
-// Workgroup = (batch row b, segment of BR*BNS tokens).  Each conv input runs
-// its strips from the last to the first so that the dy rows a strip needs
-// beyond its end are the previous strip's (carried in registers); the three
-// rows past the segment are recomputed once.  Partial sums of the parameter
-// gradients go to part[wg][NPV][H*D]:
-//   v = 5 i + k  tap k of conv i     v = 5 i + 4  bias of conv i
-//   v = 15       dt_bias             v = 16       dg * g (summed per head -> dA_log)
-template <typename ST, typename GT>
-__global__ __launch_bounds__(512) void producer_bwd_kernel(const ProdArgs a) {
-    __shared__ float red[2][MAXW][2][BR];
-    const Lanes L(a.H, a.D);
+// One conv input's backward over a segment [tlo, thi) of batch row rb / T.
+template <typename ST, int I>
+__device__ __forceinline__ void prod_bwd_conv(const ProdArgs& a, const Lanes& L, int tlo, int thi, size_t rb,
+                                              float (*red)[MAXW][2][BR], float* part) {
+    constexpr int i = I;
     const int T = a.T;
-    constexpr int SEG = BR * BNS;
-    const int nseg = (T + SEG - 1) / SEG;
-    const int wg = xcd_remap(blockIdx.x, gridDim.x);
-    const int b = wg / nseg, tlo = (wg % nseg) * SEG;
-    const int thi = min(tlo + SEG, T);
     const int nst = (thi - tlo + BR - 1) / BR;
-    const size_t rb = (size_t)b * T;
-    float* part = a.part + (size_t)wg * NPV * L.HD + L.cc;
     int par = 0;
-
-    for (int i = 0; i < 3; ++i) {
         float wt[4][KC], bias[4];
-        load_taps(a, i, L, wt, bias);
-        ST* dx = static_cast<ST*>(i == 0 ? a.dxq : i == 1 ? a.dxk : a.dxv);
+        load_taps<I>(a, L, wt, bias);
+        ST* dx = static_cast<ST*>(I == 0 ? a.dxq : I == 1 ? a.dxk : a.dxv);
         float acc[KC + 1][4];
 #pragma unroll
         for (int k = 0; k <= KC; ++k) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.f;
         float carry[KC - 1][4];
         if (thi < T) {
             float xh[2 * (KC - 1)][4];
-            prod_dy_rows<ST, KC - 1>(a, L, i, thi, rb, wt, bias, red[par], carry, xh);
+            prod_dy_rows<ST, KC - 1, I>(a, L, thi, rb, wt, bias, red[par], carry, xh);
             par ^= 1;
         } else {
 #pragma unroll
@@ -334,7 +359,7 @@ __global__ __launch_bounds__(512) void producer_bwd_kernel(const ProdArgs a) {
         for (int si = nst - 1; si >= 0; --si) {
             const int t0 = tlo + si * BR;
             float dy[BR][4], xr[BR + KC - 1][4];
-            prod_dy_rows<ST, BR>(a, L, i, t0, rb, wt, bias, red[par], dy, xr);
+            prod_dy_rows<ST, BR, I>(a, L, t0, rb, wt, bias, red[par], dy, xr);
             par ^= 1;
 #pragma unroll
             for (int j = 0; j < BR; ++j) {
@@ -369,8 +394,34 @@ __global__ __launch_bounds__(512) void producer_bwd_kernel(const ProdArgs a) {
             for (int k = 0; k <= KC; ++k) Vec4<float>::st(part + (size_t)(5 * i + k) * L.HD, acc[k]);
     }
 
+// Workgroup = (batch row b, segment of BR*BNS tokens) x role: blockIdx.y 0-2
+// takes conv input q, k or v, 3 the decay and write gates, so four
+// independent workgroups share a segment.  A conv input runs its strips from
+// the last to the first so that the dy rows a strip needs beyond its end are
+// the previous strip's (carried in registers); the three rows past the
+// segment are recomputed once.  Partial sums of the parameter gradients go to
+// part[wg][NPV][H*D]:
+//   v = 5 i + k  tap k of conv i     v = 5 i + 4  bias of conv i
+//   v = 15       dt_bias             v = 16       dg * g (summed per head -> dA_log)
+template <typename ST, typename GT>
+__global__ __launch_bounds__(512) void producer_bwd_kernel(const ProdArgs a) {
+    __shared__ float red[2][MAXW][2][BR];
+    const Lanes L(a.H, a.D);
+    const int T = a.T;
+    constexpr int SEG = BR * BNS;
+    const int nseg = (T + SEG - 1) / SEG;
+    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    const int b = wg / nseg, tlo = (wg % nseg) * SEG;
+    const int thi = min(tlo + SEG, T);
+    const size_t rb = (size_t)b * T;
+    float* part = a.part + (size_t)wg * NPV * L.HD + L.cc;
+
+    const int role = blockIdx.y;
+    if (role == 0) prod_bwd_conv<ST, 0>(a, L, tlo, thi, rb, red, part);
+    else if (role == 1) prod_bwd_conv<ST, 1>(a, L, tlo, thi, rb, red, part);
+    else if (role == 2) prod_bwd_conv<ST, 2>(a, L, tlo, thi, rb, red, part);
     // decay gate and write gate over rows [tlo, thi)
-    {
+    else {
         const ST* xf = static_cast<const ST*>(a.xf);
         const GT* dg = static_cast<const GT*>(a.dg);
         ST* dxf = static_cast<ST*>(a.dxf);
@@ -409,10 +460,20 @@ __global__ __launch_bounds__(512) void producer_bwd_kernel(const ProdArgs a) {
             const ST* xb = static_cast<const ST*>(a.xb);
             const ST* dbeta = static_cast<const ST*>(a.dbeta);
             ST* dxb = static_cast<ST*>(a.dxb);
-            for (int t = tlo; t < thi; ++t) {
-                const size_t r = rb + t;
-                const float sb = sigm(ld1<ST>(xb + r * a.ld_b + L.h));
-                st1<ST>(dxb + r * a.ld_db + L.h, ld1<ST>(dbeta + r * a.H + L.h) * a.beta_mult * sb * (1.f - sb));
+            for (int t0 = tlo; t0 < thi; t0 += BR) {
+                float xv[BR], dv[BR];   // all loads of the strip first
+#pragma unroll
+                for (int j = 0; j < BR; ++j) {
+                    const size_t r = rb + min(t0 + j, T - 1);
+                    xv[j] = ld1<ST>(xb + r * a.ld_b + L.h);
+                    dv[j] = ld1<ST>(dbeta + r * a.H + L.h);
+                }
+#pragma unroll
+                for (int j = 0; j < BR; ++j) {
+                    const float sb = sigm(xv[j]);
+                    if (t0 + j < thi)
+                        st1<ST>(dxb + (rb + t0 + j) * a.ld_db + L.h, dv[j] * a.beta_mult * sb * (1.f - sb));
+                }
             }
         }
     }
@@ -577,7 +638,7 @@ hipError_t launch_producer_fwd(const ProdArgs& a, int in_bf16, int g_bf16, hipSt
 hipError_t launch_producer_bwd(const ProdArgs& a, int in_bf16, int g_bf16, hipStream_t st) {
     const int P = producer_partials(a.B, a.T);
     const int HD = a.H * a.D;
-    const dim3 grid(P), block(64 * nwaves(a.H, a.D));
+    const dim3 grid(P, 4), block(64 * nwaves(a.H, a.D));
     if (P == 0) {
         // no rows: the column sums below still write the (zero) parameter gradients
     } else if (in_bf16) {
