@@ -49,8 +49,11 @@ def clip_grads_by_norm(params: Iterable[torch.Tensor], max_norm: float) -> torch
     norms = torch._foreach_norm([g.float() for g in grads])
     total = torch.linalg.vector_norm(torch.stack(norms))
     scale = torch.clamp(max_norm / (total + 1e-6), max=1.0)
+    by_dtype = {}
     for g in grads:
-        g.mul_(scale.to(g.dtype))
+        by_dtype.setdefault(g.dtype, []).append(g)
+    for dt, gs in by_dtype.items():
+        torch._foreach_mul_(gs, scale.to(dt))
     return total
 
 
@@ -66,16 +69,26 @@ class AdamW:
 
     @torch.no_grad()
     def step(self) -> None:
+        """One update over every parameter with a gradient, as multi-tensor
+        (``torch._foreach_*``) ops grouped by dtype: a handful of launches per
+        step instead of several per parameter."""
         b1, b2 = self.betas
         lr, wd = self.lr, self.weight_decay
+        groups = {}
         for p, m, v in zip(self.params, self.m, self.v):
-            if p.grad is None:
-                continue
-            g = p.grad
-            p.mul_(1 - lr * wd)
-            m.mul_(b1).add_(g, alpha=1 - b1)
-            v.mul_(b2).addcmul_(g, g, value=1 - b2)
-            p.addcdiv_(m, v.sqrt().add_(self.eps), value=-lr)
+            if p.grad is not None:
+                groups.setdefault((p.dtype, p.device), []).append((p, m, v))
+        for items in groups.values():
+            ps, ms, vs = (list(t) for t in zip(*items))
+            gs = [p.grad for p in ps]
+            torch._foreach_mul_(ps, 1 - lr * wd)
+            torch._foreach_mul_(ms, b1)
+            torch._foreach_add_(ms, gs, alpha=1 - b1)
+            torch._foreach_mul_(vs, b2)
+            torch._foreach_addcmul_(vs, gs, gs, value=1 - b2)
+            denom = torch._foreach_sqrt(vs)
+            torch._foreach_add_(denom, self.eps)
+            torch._foreach_addcdiv_(ps, ms, denom, value=-lr)
 
     def zero_grad(self) -> None:
         for p in self.params:
