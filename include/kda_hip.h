@@ -138,7 +138,9 @@ int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, 
  *   xq, xk, xv  [B, T, HD] rows of ld_x; xf [B, T, HD] rows of ld_f;
  *   xb [B, T, H] rows of ld_b; conv_w [3][HD][4] (q, k, v);
  *   conv_b [3][HD] or NULL (no bias); dt_bias [HD]; A_log [H];
- *   q, k, v, g [B, T, H, D] contiguous; beta [B, T, H] contiguous. */
+ *   q, k, v, g [B, T, H, D] contiguous; beta [B, T, H] contiguous.
+ * For the scalar-alpha layer (channel_wise_decay=False) xf, dt_bias, A_log and
+ * g are all NULL and no decay gate is formed. */
 int kda_layer_producer_fwd(const void* xq, const void* xk, const void* xv, const void* xf, const void* xb,
                            int64_t ld_x, int64_t ld_f, int64_t ld_b,
                            const float* conv_w, const float* conv_b, const float* dt_bias, const float* A_log,
@@ -151,7 +153,8 @@ int kda_layer_producer_fwd(const void* xq, const void* xk, const void* xv, const
  * Parameter gradients are written, not accumulated: dconv_w [3][HD][4],
  * dconv_b [3][HD] (NULL iff conv_b is NULL), ddt_bias [HD], dA_log [H].
  * workspace: at least kda_layer_workspace_size(KDA_LAYER_PRODUCER, ...) bytes,
- * 16-byte aligned.  The gradients are deterministic. */
+ * 16-byte aligned.  The gradients are deterministic.  Without a decay gate
+ * (xf NULL) dg, dxf, ddt_bias and dA_log are NULL too. */
 int kda_layer_producer_bwd(const void* xq, const void* xk, const void* xv, const void* xf, const void* xb,
                            int64_t ld_x, int64_t ld_f, int64_t ld_b,
                            const float* conv_w, const float* conv_b, const float* dt_bias, const float* A_log,

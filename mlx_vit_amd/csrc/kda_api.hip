@@ -549,15 +549,20 @@ int producer_common(const void* xq, const void* xk, const void* xv, const void* 
     KDA_TRY(check_act(xq, "xq", dtype));
     KDA_TRY(check_act(xk, "xk", dtype));
     KDA_TRY(check_act(xv, "xv", dtype));
-    KDA_TRY(check_act(xf, "xf", dtype));
     KDA_TRY(check_scalar(xb, "xb", dtype));
     KDA_TRY(check_ld(ld_x, HD, true, "ld_x"));
-    KDA_TRY(check_ld(ld_f, HD, true, "ld_f"));
     KDA_TRY(check_ld(ld_b, H, false, "ld_b"));
     KDA_TRY(check_f32(conv_w, "conv_w", 16, false));
     KDA_TRY(check_f32(conv_b, "conv_b", 16, true));
-    KDA_TRY(check_f32(dt_bias, "dt_bias", 16, false));
-    KDA_TRY(check_f32(A_log, "A_log", 4, false));
+    // the decay gate (xf, dt_bias, A_log) is all present or all absent (scalar-alpha layer)
+    if ((xf == nullptr) != (dt_bias == nullptr) || (xf == nullptr) != (A_log == nullptr))
+        return fail(KDA_E_INVALID, "xf, dt_bias and A_log must be all NULL or all non-NULL");
+    if (xf) {
+        KDA_TRY(check_act(xf, "xf", dtype));
+        KDA_TRY(check_ld(ld_f, HD, true, "ld_f"));
+        KDA_TRY(check_f32(dt_bias, "dt_bias", 16, false));
+        KDA_TRY(check_f32(A_log, "A_log", 4, false));
+    }
     return KDA_OK;
 }
 
@@ -575,7 +580,8 @@ int kda_layer_producer_fwd(const void* xq, const void* xk, const void* xv, const
     KDA_TRY(check_act(q, "q", dtype));
     KDA_TRY(check_act(k, "k", dtype));
     KDA_TRY(check_act(v, "v", dtype));
-    KDA_TRY(check_act(g, "g", g_dtype));
+    if ((g == nullptr) != (xf == nullptr)) return fail(KDA_E_INVALID, "g must be NULL exactly when xf is NULL");
+    if (g) KDA_TRY(check_act(g, "g", g_dtype));
     KDA_TRY(check_scalar(beta, "beta", dtype));
     if ((int64_t)B * T == 0) return ok();
     kda::ProdArgs a{};
@@ -604,19 +610,22 @@ int kda_layer_producer_bwd(const void* xq, const void* xk, const void* xv, const
     KDA_TRY(check_act(dq, "dq", dtype));
     KDA_TRY(check_act(dk, "dk", dtype));
     KDA_TRY(check_act(dv, "dv", dtype));
-    KDA_TRY(check_act(dg, "dg", g_dtype));
+    if (xf) KDA_TRY(check_act(dg, "dg", g_dtype));
     KDA_TRY(check_scalar(dbeta, "dbeta", dtype));
     KDA_TRY(check_act(dxq, "dxq", dtype));
     KDA_TRY(check_act(dxk, "dxk", dtype));
     KDA_TRY(check_act(dxv, "dxv", dtype));
-    KDA_TRY(check_act(dxf, "dxf", dtype));
+    if (xf) KDA_TRY(check_act(dxf, "dxf", dtype));
     KDA_TRY(check_scalar(dxb, "dxb", dtype));
     KDA_TRY(check_ld(ld_dx, HD, true, "ld_dx"));
-    KDA_TRY(check_ld(ld_df, HD, true, "ld_df"));
+    if (xf) KDA_TRY(check_ld(ld_df, HD, true, "ld_df"));
     KDA_TRY(check_ld(ld_db, H, false, "ld_db"));
     KDA_TRY(check_f32(dconv_w, "dconv_w", 4, false));
-    KDA_TRY(check_f32(ddt_bias, "ddt_bias", 4, false));
-    KDA_TRY(check_f32(dA_log, "dA_log", 4, false));
+    if ((dg == nullptr) != (xf == nullptr) || (dxf == nullptr) != (xf == nullptr) ||
+        (ddt_bias == nullptr) != (xf == nullptr) || (dA_log == nullptr) != (xf == nullptr))
+        return fail(KDA_E_INVALID, "dg, dxf, ddt_bias and dA_log must be NULL exactly when xf is NULL");
+    KDA_TRY(check_f32(ddt_bias, "ddt_bias", 4, true));
+    KDA_TRY(check_f32(dA_log, "dA_log", 4, true));
     if ((conv_b == nullptr) != (dconv_b == nullptr))
         return fail(KDA_E_INVALID, "dconv_b must be NULL exactly when conv_b is NULL");
     KDA_TRY(check_f32(dconv_b, "dconv_b", 4, true));

@@ -199,8 +199,9 @@ __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
             if (t0 + j < T && L.live) Vec4<ST>::st(static_cast<ST*>(a.v) + (rb + t0 + j) * L.HD + L.cc, sv[j]);
     }
 
-    // decay gate, in fp32 before the cast to g's dtype (nope_gdn_mlx.py:816-820)
-    {
+    // decay gate, in fp32 before the cast to g's dtype (nope_gdn_mlx.py:816-820);
+    // absent for the scalar-alpha layer (g == nullptr)
+    if (a.g) {
         const ST* xf = static_cast<const ST*>(a.xf);
         const float4 dtv = *reinterpret_cast<const float4*>(a.dt_bias + L.cc);
         const float dt[4] = {dtv.x, dtv.y, dtv.z, dtv.w};
@@ -420,41 +421,47 @@ __global__ __launch_bounds__(512) void producer_bwd_kernel(const ProdArgs a) {
     if (role == 0) prod_bwd_conv<ST, 0>(a, L, tlo, thi, rb, red, part);
     else if (role == 1) prod_bwd_conv<ST, 1>(a, L, tlo, thi, rb, red, part);
     else if (role == 2) prod_bwd_conv<ST, 2>(a, L, tlo, thi, rb, red, part);
-    // decay gate and write gate over rows [tlo, thi)
+    // decay gate (when present) and write gate over rows [tlo, thi)
     else {
-        const ST* xf = static_cast<const ST*>(a.xf);
-        const GT* dg = static_cast<const GT*>(a.dg);
-        ST* dxf = static_cast<ST*>(a.dxf);
-        const float4 dtv = *reinterpret_cast<const float4*>(a.dt_bias + L.cc);
-        const float dt[4] = {dtv.x, dtv.y, dtv.z, dtv.w};
-        const float eA = __expf(a.A_log[L.h]);
-        float adt[4] = {0.f, 0.f, 0.f, 0.f}, aA[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int t0 = tlo; t0 < thi; t0 += BR) {
-            float z[BR][4], dgv[BR][4];
-#pragma unroll
-            for (int j = 0; j < BR; ++j) {
-                const size_t r = rb + min(t0 + j, T - 1);
-                Vec4<ST>::ld(xf + r * a.ld_f + L.cc, z[j]);
-                Vec4<GT>::ld(dg + r * L.HD + L.cc, dgv[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < BR; ++j) {
-                const bool ok = t0 + j < thi && L.live;
-                float o[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float zz = z[j][e] + dt[e];
-                    const float gd = ok ? dgv[j][e] : 0.f;
-                    o[e] = -gd * eA * sigm(zz);
-                    adt[e] += o[e];
-                    aA[e] = fmaf(gd, -eA * softplus(zz), aA[e]);
+        if (a.dg) {
+            const ST* xf = static_cast<const ST*>(a.xf);
+            const GT* dg = static_cast<const GT*>(a.dg);
+            ST* dxf = static_cast<ST*>(a.dxf);
+            const float4 dtv = *reinterpret_cast<const float4*>(a.dt_bias + L.cc);
+            const float dt[4] = {dtv.x, dtv.y, dtv.z, dtv.w};
+            const float eA = __expf(a.A_log[L.h]);
+            float adt[4] = {0.f, 0.f, 0.f, 0.f}, aA[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int t0 = tlo; t0 < thi; t0 += BR) {
+                float z[BR][4], dgv[BR][4];
+    #pragma unroll
+                for (int j = 0; j < BR; ++j) {
+                    const size_t r = rb + min(t0 + j, T - 1);
+                    Vec4<ST>::ld(xf + r * a.ld_f + L.cc, z[j]);
+                    Vec4<GT>::ld(dg + r * L.HD + L.cc, dgv[j]);
                 }
-                if (ok) Vec4<ST>::st(dxf + (rb + t0 + j) * a.ld_df + L.cc, o);
+    #pragma unroll
+                for (int j = 0; j < BR; ++j) {
+                    const bool ok = t0 + j < thi && L.live;
+                    float o[4];
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float zz = z[j][e] + dt[e];
+                        const float gd = ok ? dgv[j][e] : 0.f;
+                        o[e] = -gd * eA * sigm(zz);
+                        adt[e] += o[e];
+                        aA[e] = fmaf(gd, -eA * softplus(zz), aA[e]);
+                    }
+                    if (ok) Vec4<ST>::st(dxf + (rb + t0 + j) * a.ld_df + L.cc, o);
+                }
             }
-        }
-        if (L.live) {
-            Vec4<float>::st(part + (size_t)15 * L.HD, adt);
-            Vec4<float>::st(part + (size_t)16 * L.HD, aA);
+            if (L.live) {
+                Vec4<float>::st(part + (size_t)15 * L.HD, adt);
+                Vec4<float>::st(part + (size_t)16 * L.HD, aA);
+            }
+        } else if (L.live) {   // scalar-alpha layer: no decay-gate gradients
+            const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+            Vec4<float>::st(part + (size_t)15 * L.HD, zero);
+            Vec4<float>::st(part + (size_t)16 * L.HD, zero);
         }
         if (L.live && L.cc % a.D == 0) {
             const ST* xb = static_cast<const ST*>(a.xb);
@@ -503,9 +510,9 @@ __global__ __launch_bounds__(256) void producer_finish_kernel(const ProdArgs a) 
             for (int k = 0; k < KC; ++k) a.dconv_w[((size_t)i * HD + c) * KC + k] = cs[(size_t)(5 * i + k) * HD + c];
             if (a.dconv_b) a.dconv_b[(size_t)i * HD + c] = cs[(size_t)(5 * i + KC) * HD + c];
         }
-        a.ddt_bias[c] = cs[(size_t)15 * HD + c];
+        if (a.ddt_bias) a.ddt_bias[c] = cs[(size_t)15 * HD + c];
     }
-    if (c < a.H) {
+    if (a.dA_log && c < a.H) {
         float s = 0.f;
         for (int d = 0; d < a.D; ++d) s += cs[(size_t)16 * HD + (size_t)c * a.D + d];
         a.dA_log[c] = s;

@@ -220,6 +220,29 @@ def chunk_kda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor
     return ChunkKDAFunction.apply(q, k, v, g, beta, initial_state)
 
 
+GDN_LOG_ALPHA_MIN = -80.0
+
+
+def chunk_gdn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, beta: torch.Tensor,
+              initial_state: Optional[torch.Tensor] = None, chunk_size: int = CHUNK
+              ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Scalar-alpha gated delta rule (the reference's original GDN,
+    ``_gdn_step_fused`` nope_gdn_mlx.py:641-650, chunkwise form
+    ``_chunkwise_scalar_wy`` nope_gdn_mlx.py:949-1064), differentiable.
+
+    q, k, v (B, T, H, D); alpha, beta (B, T, H) with alpha in (0, 1].  The step
+    ``S (alpha (I - beta k k^T)) + beta v k^T`` is the KDA step with every
+    channel's decay e^{g} equal to alpha, so this runs the KDA kernels on
+    g = log(alpha) broadcast over D (clamped at -80: e^-80 is below fp32's
+    resolution of any state term).  Autograd through the log and the broadcast
+    gives d alpha = sum_d dg / alpha."""
+    if alpha.dim() != 3 or tuple(alpha.shape) != tuple(q.shape[:3]):
+        raise ValueError(f"alpha must be (B, T, H) = {tuple(q.shape[:3])}; got {tuple(alpha.shape)}")
+    g = torch.clamp(torch.log(alpha.float()), min=GDN_LOG_ALPHA_MIN)
+    g = g.unsqueeze(-1).expand(q.shape).contiguous()
+    return chunk_kda(q, k, v, g, beta, initial_state, chunk_size)
+
+
 def solve_unit_triangular(M: torch.Tensor, b: torch.Tensor, upper: bool = False) -> torch.Tensor:
     """y = M^-1 b for unit-triangular M (BH, C, C), b (BH, C, N); fp32, C <= 64.
     The HIP counterpart of GatedDeltaLayer._metal_solve_triangular(_upper)

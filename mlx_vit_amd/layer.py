@@ -33,7 +33,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .kda import BWD_HEAD_DIMS, CHUNK, FWD_HEAD_DIMS, _DTYPE_CODE, _ptr, _stream
-from .recurrence import HIP_PATH, KDARecurrence
+from .recurrence import GDN_HIP_PATH, HIP_PATH, KDARecurrence
 
 CONV_TAPS = 4
 
@@ -79,25 +79,33 @@ def producer_forward(qkv: torch.Tensor, xf: torch.Tensor, xb: torch.Tensor, conv
     dt = qkv.dtype
     if dt not in _DTYPE_CODE or g_dtype not in _DTYPE_CODE:
         raise ValueError(f"dtype {dt} / g dtype {g_dtype}: use float32 or bfloat16")
-    qkv, xf = _vec_ok(qkv), _vec_ok(xf)
+    gate = xf is not None
+    qkv = _vec_ok(qkv)
     B, T, N = qkv.shape
     if N != 3 * HD:
         raise ValueError(f"qkv has {N} columns; expected 3*H*D = {3 * HD}")
-    if tuple(xf.shape) != (B, T, HD) or tuple(xb.shape) != (B, T, H):
-        raise ValueError(f"xf {tuple(xf.shape)} / xb {tuple(xb.shape)} do not match (B, T) = {(B, T)}")
-    for n, t in (("xf", xf), ("xb", xb)):
-        _check_dtype(n, t, dt)
+    if tuple(xb.shape) != (B, T, H) or (gate and tuple(xf.shape) != (B, T, HD)):
+        raise ValueError(f"xf {None if xf is None else tuple(xf.shape)} / xb {tuple(xb.shape)} do not match "
+                         f"(B, T) = {(B, T)}")
+    _check_dtype("xb", xb, dt)
     if xb.stride(-1) != 1 or (B > 1 and xb.stride(0) != T * xb.stride(1)):
         xb = xb.contiguous()
-    ld_x, ld_f, ld_b = _rows(qkv, "qkv"), _rows(xf, "xf"), _rows(xb, "xb")
+    ld_x, ld_b = _rows(qkv, "qkv"), _rows(xb, "xb")
+    ld_f = 0
+    if gate:
+        _check_dtype("xf", xf, dt)
+        xf = _vec_ok(xf)
+        ld_f = _rows(xf, "xf")
+        dt_bias = dt_bias.to(torch.float32).contiguous()
+        A_log = A_log.to(torch.float32).contiguous()
+    else:
+        dt_bias = A_log = None
     conv_w = conv_w.to(torch.float32).contiguous()
     conv_b = None if conv_b is None else conv_b.to(torch.float32).contiguous()
-    dt_bias = dt_bias.to(torch.float32).contiguous()
-    A_log = A_log.to(torch.float32).contiguous()
     dev = qkv.device
     q = torch.empty((B, T, H, D), dtype=dt, device=dev)
     k, v = torch.empty_like(q), torch.empty_like(q)
-    g = torch.empty((B, T, H, D), dtype=g_dtype, device=dev)
+    g = torch.empty((B, T, H, D), dtype=g_dtype, device=dev) if gate else None
     beta = torch.empty((B, T, H), dtype=dt, device=dev)
     es = qkv.element_size()
     base = qkv.data_ptr()
@@ -118,28 +126,35 @@ def producer_backward(qkv, xf, xb, conv_w, conv_b, dt_bias, A_log, dq, dk, dv, d
     H, D = num_heads, head_dim
     HD = H * D
     dt = qkv.dtype
-    qkv, xf = _vec_ok(qkv), _vec_ok(xf)
+    gate = xf is not None
+    qkv = _vec_ok(qkv)
     B, T, _ = qkv.shape
     if xb.stride(-1) != 1 or (B > 1 and xb.stride(0) != T * xb.stride(1)):
         xb = xb.contiguous()
-    ld_x, ld_f, ld_b = _rows(qkv, "qkv"), _rows(xf, "xf"), _rows(xb, "xb")
-    g_dtype = dg.dtype
+    ld_x, ld_b = _rows(qkv, "qkv"), _rows(xb, "xb")
     dq, dk, dv = (t.to(dt).contiguous() for t in (dq, dk, dv))
     dbeta = dbeta.to(dt).contiguous()
-    dg = dg.contiguous()
     conv_w = conv_w.to(torch.float32).contiguous()
     conv_b = None if conv_b is None else conv_b.to(torch.float32).contiguous()
-    dt_bias = dt_bias.to(torch.float32).contiguous()
-    A_log = A_log.to(torch.float32).contiguous()
     dev = qkv.device
-    dqkv = torch.empty((B, T, 3 * HD), dtype=dt, device=dev)
-    dxf = torch.empty((B, T, HD), dtype=dt, device=dev)
-    dxb = torch.empty((B, T, H), dtype=dt, device=dev)
     f32 = dict(dtype=torch.float32, device=dev)
+    ld_f, g_dtype = 0, torch.float32
+    if gate:
+        xf = _vec_ok(xf)
+        ld_f = _rows(xf, "xf")
+        g_dtype = dg.dtype
+        dg = dg.contiguous()
+        dt_bias = dt_bias.to(torch.float32).contiguous()
+        A_log = A_log.to(torch.float32).contiguous()
+        dxf = torch.empty((B, T, HD), dtype=dt, device=dev)
+        ddt = torch.empty((HD,), **f32)
+        dA = torch.empty((H,), **f32)
+    else:
+        dg = dt_bias = A_log = dxf = ddt = dA = None
+    dqkv = torch.empty((B, T, 3 * HD), dtype=dt, device=dev)
+    dxb = torch.empty((B, T, H), dtype=dt, device=dev)
     dconv_w = torch.empty((3, HD, CONV_TAPS), **f32)
     dconv_b = None if conv_b is None else torch.empty((3, HD), **f32)
-    ddt = torch.empty((HD,), **f32)
-    dA = torch.empty((H,), **f32)
     lib = _lib.load()
     nws = lib.kda_layer_workspace_size(_lib.KDA_LAYER_PRODUCER, B, T, H, D)
     ws = torch.empty(max(nws, 256), dtype=torch.uint8, device=dev)
@@ -149,7 +164,7 @@ def producer_backward(qkv, xf, xb, conv_w, conv_b, dt_bias, A_log, dq, dk, dv, d
         base, base + HD * es, base + 2 * HD * es, _ptr(xf), _ptr(xb), ld_x, ld_f, ld_b,
         _ptr(conv_w), _ptr(conv_b), _ptr(dt_bias), _ptr(A_log),
         _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta),
-        dbase, dbase + HD * es, dbase + 2 * HD * es, _ptr(dxf), _ptr(dxb), 3 * HD, HD, H,
+        dbase, dbase + HD * es, dbase + 2 * HD * es, _ptr(dxf), _ptr(dxb), 3 * HD, HD if gate else 0, H,
         _ptr(dconv_w), _ptr(dconv_b), _ptr(ddt), _ptr(dA),
         B, T, H, D, float(scale), float(beta_mult), _DTYPE_CODE[dt], _DTYPE_CODE[g_dtype],
         _ptr(ws), ws.numel(), _stream(dev))
@@ -205,7 +220,7 @@ class ProducerFunction(torch.autograd.Function):
                                beta_mult, g_dtype)
         ctx.save_for_backward(qkv, xf, xb, conv_w, conv_b, dt_bias, A_log)
         ctx.cfg = (num_heads, head_dim, scale, beta_mult)
-        ctx.pdtypes = (conv_w.dtype, None if conv_b is None else conv_b.dtype, dt_bias.dtype, A_log.dtype)
+        ctx.pdtypes = tuple(None if t is None else t.dtype for t in (conv_w, conv_b, dt_bias, A_log))
         return out
 
     @staticmethod
@@ -217,12 +232,14 @@ class ProducerFunction(torch.autograd.Function):
         dq = torch.zeros((B, T, H, D), dtype=qkv.dtype, **z) if dq is None else dq
         dk = torch.zeros((B, T, H, D), dtype=qkv.dtype, **z) if dk is None else dk
         dv = torch.zeros((B, T, H, D), dtype=qkv.dtype, **z) if dv is None else dv
-        dg = torch.zeros((B, T, H, D), dtype=torch.float32, **z) if dg is None else dg
+        if xf is not None and dg is None:
+            dg = torch.zeros((B, T, H, D), dtype=torch.float32, **z)
         dbeta = torch.zeros((B, T, H), dtype=qkv.dtype, **z) if dbeta is None else dbeta
         dqkv, dxf, dxb, dcw, dcb, ddt, dA = producer_backward(
             qkv, xf, xb, conv_w, conv_b, dt_bias, A_log, dq, dk, dv, dg, dbeta, H, D, scale, beta_mult)
         wt, bt, dtt, at = ctx.pdtypes
-        return (dqkv, dxf, dxb, dcw.to(wt), None if dcb is None else dcb.to(bt), ddt.to(dtt), dA.to(at),
+        cast = lambda t, d: None if t is None else t.to(d)  # noqa: E731
+        return (dqkv, dxf, dxb, dcw.to(wt), cast(dcb, bt), cast(ddt, dtt), cast(dA, at),
                 None, None, None, None, None)
 
 
@@ -278,15 +295,16 @@ class GatedDeltaLayer(nn.Module):
     ``forward(x, state=None, compute_path=None) -> (out, new_state)`` with
     x (B, L, hidden_size) and state (B, H, D, D) fp32 or None.  Construction
     raises ``ValueError`` for configurations the HIP path cannot run, as the
-    reference does for its Metal budgets (nope_gdn_mlx.py:693-735); scalar-alpha
-    GDN (``channel_wise_decay=False``) is not provided."""
+    reference does for its Metal budgets (nope_gdn_mlx.py:693-735).  With
+    ``channel_wise_decay=False`` it is the original scalar-alpha GDN
+    (``a_proj``, path ``hip_chunkwise_gdn``)."""
 
     def __init__(self, hidden_size: int, num_heads: int = 6, head_dim: int = 64, chunk_size: int = CHUNK,
                  channel_wise_decay: bool = True, decay_low_rank: Optional[int] = None,
                  allow_neg_eigval: bool = False, compute_path: Optional[str] = None):
         super().__init__()
         if compute_path is None:
-            compute_path = HIP_PATH
+            compute_path = HIP_PATH if channel_wise_decay else GDN_HIP_PATH
         if head_dim not in FWD_HEAD_DIMS:
             raise ValueError(f"compute_path='{compute_path}' supports head_dim in {FWD_HEAD_DIMS}; "
                              f"got head_dim={head_dim}")
@@ -308,11 +326,14 @@ class GatedDeltaLayer(nn.Module):
         self.q_proj = nn.Linear(hidden_size, total, bias=False)
         self.k_proj = nn.Linear(hidden_size, total, bias=False)
         self.v_proj = nn.Linear(hidden_size, total, bias=False)
-        rank = decay_low_rank or head_dim
-        self.f_proj_1 = nn.Linear(hidden_size, rank, bias=False)
-        self.f_proj_2 = nn.Linear(rank, total, bias=False)
-        self.A_log = nn.Parameter(torch.empty(num_heads).uniform_(1.0, 16.0).log_())
-        self.dt_bias = nn.Parameter(torch.zeros(total))
+        if channel_wise_decay:
+            rank = decay_low_rank or head_dim
+            self.f_proj_1 = nn.Linear(hidden_size, rank, bias=False)
+            self.f_proj_2 = nn.Linear(rank, total, bias=False)
+            self.A_log = nn.Parameter(torch.empty(num_heads).uniform_(1.0, 16.0).log_())
+            self.dt_bias = nn.Parameter(torch.zeros(total))
+        else:
+            self.a_proj = nn.Linear(hidden_size, num_heads, bias=False)
         self.b_proj = nn.Linear(hidden_size, num_heads, bias=False)
         self.q_conv1d = ShortCausalConv1d(total, CONV_TAPS)
         self.k_conv1d = ShortCausalConv1d(total, CONV_TAPS)
@@ -324,17 +345,24 @@ class GatedDeltaLayer(nn.Module):
 
     def produce(self, x: torch.Tensor):
         """(q, k, v, g, beta) for x (B, L, hidden): the layer's inputs to the
-        recurrence (nope_gdn_mlx.py:790-833); g is fp32 as in the reference."""
+        recurrence (nope_gdn_mlx.py:790-833); g is fp32 as in the reference.
+        With scalar-alpha decay the fourth entry is alpha (B, L, H)."""
         H, D = self.num_heads, self.head_dim
         w_qkv = torch.cat([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight], 0)
         qkv = F.linear(x, w_qkv)
-        xf = self.f_proj_2(self.f_proj_1(x))
         xb = self.b_proj(x)
         convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d)
         conv_w = torch.stack([c.weight.reshape(self.total_dim, CONV_TAPS) for c in convs])
         conv_b = None if convs[0].bias is None else torch.stack([c.bias for c in convs])
-        return ProducerFunction.apply(qkv, xf, xb, conv_w, conv_b, self.dt_bias, self.A_log, H, D, self.scale,
-                                      2.0 if self.allow_neg_eigval else 1.0, torch.float32)
+        mult = 2.0 if self.allow_neg_eigval else 1.0
+        if self.channel_wise_decay:
+            xf = self.f_proj_2(self.f_proj_1(x))
+            return ProducerFunction.apply(qkv, xf, xb, conv_w, conv_b, self.dt_bias, self.A_log, H, D,
+                                          self.scale, mult, torch.float32)
+        # scalar-alpha GDN: alpha = sigmoid(a_proj(x)) (nope_gdn_mlx.py:821-823), no decay gate
+        q, k, v, _, beta = ProducerFunction.apply(qkv, None, xb, conv_w, conv_b, None, None, H, D, self.scale,
+                                                  mult, torch.float32)
+        return q, k, v, torch.sigmoid(self.a_proj(x)), beta
 
     def forward(self, x: torch.Tensor, state: Optional[torch.Tensor] = None,
                 compute_path: Optional[str] = None) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -1,5 +1,6 @@
 """The recurrence half of the reference's GatedDeltaLayer: path validation and
-string dispatch, with ``gdn_path='hip_chunkwise_kda'`` as the MI355X path.
+string dispatch, with ``gdn_path='hip_chunkwise_kda'`` as the MI355X path
+(and ``'hip_chunkwise_gdn'`` for scalar-alpha decay, where ``g`` is alpha).
 
 The reference selects a KDA compute path by name at construction and per call
 (``compute_path``, nope_gdn_mlx.py:693-735 and 823-878); every path is a method
@@ -23,10 +24,11 @@ from typing import Optional, Tuple
 
 import torch
 
-from .kda import BWD_HEAD_DIMS, CHUNK, FWD_HEAD_DIMS, chunk_kda
+from .kda import BWD_HEAD_DIMS, CHUNK, FWD_HEAD_DIMS, chunk_gdn, chunk_kda
 
 HIP_PATH = "hip_chunkwise_kda"
-KDA_PATHS = (HIP_PATH,)
+GDN_HIP_PATH = "hip_chunkwise_gdn"   # scalar-alpha GDN on the same kernels
+KDA_PATHS = (HIP_PATH, GDN_HIP_PATH)
 
 
 class KDARecurrence:
@@ -36,11 +38,14 @@ class KDARecurrence:
                  channel_wise_decay: bool = True, compute_path: Optional[str] = None,
                  requires_grad: bool = True):
         if compute_path is None:
-            compute_path = HIP_PATH
-        if not channel_wise_decay:
-            raise ValueError(
-                f"{compute_path} is implemented for channel-wise KDA only "
-                "(channel_wise_decay=True); scalar-alpha GDN is not provided.")
+            compute_path = HIP_PATH if channel_wise_decay else GDN_HIP_PATH
+        # the reference's pairing of paths and decay kinds (nope_gdn_mlx.py:696-705)
+        if compute_path == HIP_PATH and not channel_wise_decay:
+            raise ValueError(f"{HIP_PATH} is only valid for channel-wise KDA (channel_wise_decay=True). "
+                             f"For scalar-alpha use '{GDN_HIP_PATH}'.")
+        if compute_path == GDN_HIP_PATH and channel_wise_decay:
+            raise ValueError(f"{GDN_HIP_PATH} is only valid for scalar-alpha GDN (channel_wise_decay=False). "
+                             f"For channel-wise KDA use '{HIP_PATH}'.")
         self._validate(compute_path, head_dim, chunk_size, requires_grad)
         self.num_heads = num_heads
         self.head_dim = head_dim
@@ -65,8 +70,12 @@ class KDARecurrence:
                  beta: torch.Tensor, state: Optional[torch.Tensor] = None,
                  compute_path: Optional[str] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         path = compute_path or self.compute_path
-        if path == HIP_PATH:
+        if path == HIP_PATH and self.channel_wise_decay:
             return self._hip_chunkwise_kda(q, k, v, g, beta, state)
+        if path == GDN_HIP_PATH and not self.channel_wise_decay:
+            return chunk_gdn(q, k, v, g, beta, state, self.chunk_size)
+        if path in KDA_PATHS:
+            raise ValueError(f"compute_path='{path}' does not match channel_wise_decay={self.channel_wise_decay}")
         raise ValueError(f"Unknown compute_path: {path}")
 
     def _hip_chunkwise_kda(self, q, k, v, g, beta, state):

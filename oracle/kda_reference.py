@@ -135,6 +135,39 @@ def loop_compiled_kda(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
     return torch.stack(outs, dim=1).to(q.dtype), state
 
 
+def gdn_step(state: Tensor, q_t: Tensor, k_t: Tensor, v_t: Tensor, alpha_t: Tensor, beta_t: Tensor,
+             I: Tensor) -> Tuple[Tensor, Tensor]:
+    """nope_gdn_mlx.py:641-650 (``_gdn_step_fused``): scalar-alpha step,
+    ``S (alpha (I - beta k k^T)) + beta v k^T``, then ``o_t = S q_t``."""
+    a = alpha_t[..., None, None]
+    b = beta_t[..., None, None]
+    k_outer = k_t[..., :, None] @ k_t[..., None, :]
+    state = state @ (a * (I - b * k_outer))
+    state = state + b * (v_t[..., :, None] @ k_t[..., None, :])
+    out = (state @ q_t[..., :, None]).squeeze(-1)
+    return state, out
+
+
+def loop_compiled_gdn(q: Tensor, k: Tensor, v: Tensor, alpha: Tensor, beta: Tensor,
+                      state: Optional[Tensor] = None,
+                      compute_dtype: torch.dtype = torch.float32) -> Tuple[Tensor, Tensor]:
+    """nope_gdn_mlx.py:919-947 (``_loop_compiled_gdn``): q, k, v (B, L, H, D),
+    alpha, beta (B, L, H); casts to ``compute_dtype``, zero state when None,
+    output cast back to q's dtype.  Returns (o, final_state)."""
+    B, L, H, D = q.shape
+    cd = compute_dtype
+    q32, k32, v32, a32, b32 = (t.to(cd) for t in (q, k, v, alpha, beta))
+    state = torch.zeros((B, H, D, D), dtype=cd) if state is None else state.to(cd)
+    I = torch.eye(D, dtype=cd)
+    outs: List[Tensor] = []
+    for t in range(L):
+        state, o_t = gdn_step(state, q32[:, t], k32[:, t], v32[:, t], a32[:, t], b32[:, t], I)
+        outs.append(o_t)
+    if L == 0:
+        return torch.zeros_like(q), state
+    return torch.stack(outs, dim=1).to(q.dtype), state
+
+
 def step_forward_rank1(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
                        state: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """Rank-1 form of the same step, nope_gdn_mlx.py:3003-3019 and 3724-3735.

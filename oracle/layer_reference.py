@@ -22,7 +22,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor
 
-from .kda_reference import l2_normalize, loop_compiled_kda, softplus
+from .kda_reference import l2_normalize, loop_compiled_gdn, loop_compiled_kda, softplus
 
 TAPS = 4
 
@@ -61,15 +61,27 @@ def producer_from_projections(xq: Tensor, xk: Tensor, xv: Tensor, xf: Tensor, xb
 
 def producer(params: Dict[str, Tensor], x: Tensor, H: int, D: int,
              allow_neg_eigval: bool = False) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """nope_gdn_mlx.py:790-833: the projections, then ``producer_from_projections``."""
+    """nope_gdn_mlx.py:790-833: the projections, then ``producer_from_projections``.
+    For the scalar-alpha layer (an ``a_proj.weight`` parameter) the fourth
+    result is alpha = sigmoid(a_proj(x)) (B, L, H)."""
     p = params
     HD = H * D
     conv_w = torch.stack([p[f"{n}_conv1d.weight"].reshape(HD, TAPS) for n in "qkv"])
     conv_b = torch.stack([p[f"{n}_conv1d.bias"] for n in "qkv"]) if "q_conv1d.bias" in p else None
+    mult = 2.0 if allow_neg_eigval else 1.0
+    if "a_proj.weight" in p:
+        # scalar-alpha GDN (nope_gdn_mlx.py:821-823): alpha = sigmoid(a_proj(x)) in place of g
+        B, L, _ = x.shape
+        zeros = torch.zeros(B, L, HD, dtype=x.dtype)
+        q, k, v, _, beta = producer_from_projections(
+            x @ p["q_proj.weight"].T, x @ p["k_proj.weight"].T, x @ p["v_proj.weight"].T, zeros,
+            x @ p["b_proj.weight"].T, conv_w, conv_b, torch.zeros(HD, dtype=x.dtype),
+            torch.zeros(H, dtype=x.dtype), H, D, mult)
+        return q, k, v, torch.sigmoid(x @ p["a_proj.weight"].T), beta
     return producer_from_projections(
         x @ p["q_proj.weight"].T, x @ p["k_proj.weight"].T, x @ p["v_proj.weight"].T,
         (x @ p["f_proj_1.weight"].T) @ p["f_proj_2.weight"].T, x @ p["b_proj.weight"].T,
-        conv_w, conv_b, p["dt_bias"], p["A_log"], H, D, 2.0 if allow_neg_eigval else 1.0)
+        conv_w, conv_b, p["dt_bias"], p["A_log"], H, D, mult)
 
 
 def gated_rms_norm(x: Tensor, weight: Tensor, gate: Tensor, eps: float) -> Tensor:
@@ -83,7 +95,10 @@ def layer_forward(params: Dict[str, Tensor], x: Tensor, H: int, D: int, state: O
     """nope_gdn_mlx.py:775-885 with the 'compiled' recurrence: (out, new_state)."""
     B, L, _ = x.shape
     q, k, v, g, beta = producer(params, x, H, D, allow_neg_eigval)
-    o, new_state = loop_compiled_kda(q, k, v, g, beta, state, compute_dtype=x.dtype)
+    if "a_proj.weight" in params:   # g is alpha (B, L, H)
+        o, new_state = loop_compiled_gdn(q, k, v, g, beta, state, compute_dtype=x.dtype)
+    else:
+        o, new_state = loop_compiled_kda(q, k, v, g, beta, state, compute_dtype=x.dtype)
     gate = ((x @ params["g_proj_1.weight"].T) @ params["g_proj_2.weight"].T
             + params["g_proj_2.bias"]).reshape(B, L, H, D)
     y = gated_rms_norm(o.reshape(B, L, H, D), params["o_norm.weight"], gate, eps)

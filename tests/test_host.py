@@ -20,7 +20,8 @@ def test_default_path_is_hip():
 @pytest.mark.parametrize("kwargs,msg", [
     (dict(compute_path="metal_sg"), "Unknown compute_path"),
     (dict(chunk_size=32), "chunk_size"),
-    (dict(channel_wise_decay=False), "channel-wise"),
+    (dict(channel_wise_decay=False, compute_path="hip_chunkwise_kda"), "channel-wise"),
+    (dict(channel_wise_decay=True, compute_path="hip_chunkwise_gdn"), "scalar-alpha"),
     (dict(head_dim=128), "head_dim"),
     (dict(head_dim=48, requires_grad=False), "head_dim"),
 ])

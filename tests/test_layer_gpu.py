@@ -210,3 +210,65 @@ def test_layer_parity(dtype, with_state):
     for n, p in layer.named_parameters():
         errs["d" + n] = _rel(p.grad, rp[n].grad)
     _check(errs, TOL[dtype], case)
+
+
+@pytest.mark.parametrize("B,T,H,D,dtype,with_state", [
+    (2, 100, 3, 64, torch.float32, True),
+    (1, 130, 2, 32, torch.float32, False),
+    (2, 77, 4, 64, torch.bfloat16, True),
+])
+def test_chunk_gdn_parity(B, T, H, D, dtype, with_state):
+    """Scalar-alpha GDN (the reference's original gated delta rule) through the
+    KDA kernels against the fp64 step loop (nope_gdn_mlx.py:641-650, 919-947):
+    outputs and the gradients of q, k, v, alpha, beta and the initial state."""
+    from mlx_vit_amd import chunk_gdn
+    case = f"chunk_gdn B={B} T={T} H={H} D={D} {dtype} state={with_state}"
+    print(case, flush=True)
+    g = torch.Generator().manual_seed(T + D)
+    x = R.make_inputs(B, T, H, D, dtype=dtype, seed=T, with_state=with_state, with_grad=True)
+    alpha = torch.sigmoid(torch.randn(B, T, H, generator=g) + 1.5)   # 0.2 .. 0.98
+    cot_s = torch.randn(B, H, D, D, generator=g)
+    dev = {n: x[n].to(DEV).requires_grad_() for n in ("q", "k", "v", "beta")}
+    a_d = alpha.to(DEV).requires_grad_()
+    s0_d = None if x["s0"] is None else x["s0"].to(DEV).requires_grad_()
+    o, st = chunk_gdn(dev["q"], dev["k"], dev["v"], a_d, dev["beta"], s0_d)
+    ((o.float() * x["do"].to(DEV).float()).sum() + (st * cot_s.to(DEV)).sum()).backward()
+    torch.cuda.synchronize()
+    ref = {n: x[n].double().requires_grad_() for n in ("q", "k", "v", "beta")}
+    a_r = alpha.double().requires_grad_()
+    s0_r = None if x["s0"] is None else x["s0"].double().requires_grad_()
+    ro, rst = R.loop_compiled_gdn(ref["q"], ref["k"], ref["v"], a_r, ref["beta"], s0_r, compute_dtype=torch.float64)
+    ((ro * x["do"].double()).sum() + (rst * cot_s.double()).sum()).backward()
+    errs = {"o": _rel(o, ro), "state": _rel(st, rst), "dalpha": _rel(a_d.grad, a_r.grad)}
+    for n in ("q", "k", "v", "beta"):
+        errs["d" + n] = _rel(dev[n].grad, ref[n].grad)
+    if s0_d is not None:
+        errs["ds0"] = _rel(s0_d.grad, s0_r.grad)
+    _check(errs, TOL[dtype], case)
+
+
+def test_layer_parity_scalar_alpha():
+    """GatedDeltaLayer(channel_wise_decay=False): a_proj gate, producer without
+    the decay gate, path hip_chunkwise_gdn, against the fp64 restatement."""
+    from mlx_vit_amd import GatedDeltaLayer
+    B, L, hidden, H, D = 2, 90, 64, 2, 32
+    torch.manual_seed(5)
+    layer = GatedDeltaLayer(hidden, H, D, channel_wise_decay=False)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(B, L, hidden, generator=g)
+    cot = torch.randn(B, L, hidden, generator=g)
+    cot_s = torch.randn(B, H, D, D, generator=g)
+    ref_params = _layer_params(layer)
+    layer = layer.to(DEV)
+    xd = x.to(DEV).requires_grad_()
+    out, st = layer(xd)
+    ((out * cot.to(DEV)).sum() + (st * cot_s.to(DEV)).sum()).backward()
+    torch.cuda.synchronize()
+    rp = {n: t.requires_grad_() for n, t in ref_params.items()}
+    rx = x.double().requires_grad_()
+    rout, rst = LR.layer_forward(rp, rx, H, D)
+    ((rout * cot.double()).sum() + (rst * cot_s.double()).sum()).backward()
+    errs = {"out": _rel(out, rout), "state": _rel(st, rst), "dx": _rel(xd.grad, rx.grad)}
+    for n, p in layer.named_parameters():
+        errs["d" + n] = _rel(p.grad, rp[n].grad)
+    _check(errs, TOL[torch.float32], "layer scalar alpha")

@@ -115,7 +115,11 @@ def test_layer_forward_t1_closed_form():
 def test_layer_construction_validation():
     from mlx_vit_amd.layer import GatedDeltaLayer
     with pytest.raises(ValueError, match="channel-wise"):
-        GatedDeltaLayer(64, 2, 32, channel_wise_decay=False)
+        GatedDeltaLayer(64, 2, 32, channel_wise_decay=False, compute_path="hip_chunkwise_kda")
+    scalar = GatedDeltaLayer(64, 2, 32, channel_wise_decay=False)
+    names = dict(scalar.named_parameters())
+    assert names["a_proj.weight"].shape == (2, 64) and "A_log" not in names and "f_proj_1.weight" not in names
+    assert scalar.recurrence.compute_path == "hip_chunkwise_gdn"
     with pytest.raises(ValueError, match="head_dim"):
         GatedDeltaLayer(64, 2, 48)
     with pytest.raises(ValueError, match="chunk_size"):
@@ -144,3 +148,23 @@ def test_producer_host_checks():
     with pytest.raises(ValueError, match="do not match"):
         producer_forward(torch.zeros(1, 4, 96), torch.zeros(1, 5, 32), torch.zeros(1, 4, 2),
                          torch.zeros(3, 32, 4), None, torch.zeros(32), torch.zeros(2), 2, 16, 0.25)
+
+
+def test_gdn_step_is_kda_step_with_broadcast_log_alpha():
+    """The scalar-alpha step (nope_gdn_mlx.py:641-650) is the KDA step
+    (nope_gdn_mlx.py:616-638) with every channel's decay e^g = alpha; also
+    pinned by the closed form of one step from a zero state."""
+    g = _gen(7)
+    B, H, D = 2, 3, 5
+    S = torch.randn(B, H, D, D, generator=g, dtype=D64)
+    q, k, v = (torch.randn(B, H, D, generator=g, dtype=D64) for _ in range(3))
+    alpha = torch.rand(B, H, generator=g, dtype=D64) * 0.9 + 0.05
+    beta = torch.rand(B, H, generator=g, dtype=D64)
+    I = torch.eye(D, dtype=D64)
+    s1, o1 = R.gdn_step(S, q, k, v, alpha, beta, I)
+    s2, o2 = R.kda_step(S, q, k, v, torch.log(alpha)[..., None].expand(B, H, D), beta, I)
+    torch.testing.assert_close(s1, s2)
+    torch.testing.assert_close(o1, o2)
+    s0, o0 = R.gdn_step(torch.zeros_like(S), q, k, v, alpha, beta, I)
+    torch.testing.assert_close(s0, beta[..., None, None] * v[..., :, None] * k[..., None, :])
+    torch.testing.assert_close(o0, beta[..., None] * (k * q).sum(-1, keepdim=True) * v)
