@@ -303,23 +303,21 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                     const int t = BS * m + 4 * g4 + e;
                     const float gt = s.g[t][d];
                     float ak = 0.f, aq = 0.f, ag = 0.f;
-                    for (int sx = s.blo[t]; sx <= s.bhi[t]; ++sx) {
-                        const float gs = s.g[sx][d];
-                        if (sx <= t) {      // row t: dP[t][sx] (strict), dA[t][sx]
-                            const float ex = kexp<PREC>(gt - gs);
-                            const float ks = s.kr[sx][d] * ex;
-                            const float pp = sp[t][sx], pa = sda[t][sx];
-                            ak += pp * ks;
-                            aq += pa * ks;
-                            ag += (pp * kx[m][e] + pa * qx[m][e]) * ks;
-                        }
-                        if (sx >= t) {      // column t: dP[sx][t] (strict), dA[sx][t]
-                            const float ex = kexp<PREC>(gs - gt);
-                            const float pp = sp[sx][t], pa = sda[sx][t];
-                            const float c = (pp * s.kr[sx][d] + pa * s.ql[sx][d]) * ex;
-                            ak += c;
-                            ag -= c * kx[m][e];
-                        }
+                    // row t (dP[t][sx] strict, dA[t][sx]) and column t (dP[sx][t],
+                    // dA[sx][t]) as two loops over the decay band
+                    for (int sx = s.blo[t]; sx <= t; ++sx) {
+                        const float ks = s.kr[sx][d] * kexp<PREC>(gt - s.g[sx][d]);
+                        const float pp = sp[t][sx], pa = sda[t][sx];
+                        ak += pp * ks;
+                        aq += pa * ks;
+                        ag += (pp * kx[m][e] + pa * qx[m][e]) * ks;
+                    }
+                    for (int sx = t; sx <= s.bhi[t]; ++sx) {
+                        const float ex = kexp<PREC>(s.g[sx][d] - gt);
+                        const float pp = sp[sx][t], pa = sda[sx][t];
+                        const float c = (pp * s.kr[sx][d] + pa * s.ql[sx][d]) * ex;
+                        ak += c;
+                        ag -= c * kx[m][e];
                     }
                     dka[m][e] += ak;
                     dqa[m][e] += aq;
@@ -1441,7 +1439,9 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                 }
             }
         } else {
-            // pairwise path: raw k in kr, raw q in ql, gamma in g
+            // pairwise path: raw k in kr, raw q in ql, gamma in g.  Row side
+            // (s <= t) and column side (s >= t) run as two loops over the decay
+            // band, so no iteration carries the other side's masked work.
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm)
 #pragma unroll
@@ -1449,22 +1449,19 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     const int t = BS * (2 * rh + mm) + 4 * g4 + e;
                     const float gt = s.g[t][d], bt = s.beta[t];
                     float ak = 0.f, aq = 0.f, ag = 0.f;
-                    for (int sx = s.blo[t]; sx <= s.bhi[t]; ++sx) {
-                        const float gs = s.g[sx][d];
-                        if (sx <= t) {
-                            const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - gs);
-                            const float pp = bt * sdL[t * LDL + sx], pa = ld1<ST>(&sm.dA[t][sx]);
-                            ak += pp * ks;
-                            aq += pa * ks;
-                            ag += (pp * kx[mm][e] + pa * qx[mm][e]) * ks;
-                        }
-                        if (sx >= t) {
-                            const float ex = kexp<PREC>(gs - gt);
-                            const float pp = s.beta[sx] * sdL[sx * LDL + t], pa = ld1<ST>(&sm.dA[sx][t]);
-                            const float c = (pp * ld1<ST>(&s.kr[sx][d]) + pa * ld1<ST>(&s.ql[sx][d])) * ex;
-                            ak += c;
-                            ag -= c * kx[mm][e];
-                        }
+                    for (int sx = s.blo[t]; sx <= t; ++sx) {
+                        const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - s.g[sx][d]);
+                        const float pp = bt * sdL[t * LDL + sx], pa = ld1<ST>(&sm.dA[t][sx]);
+                        ak += pp * ks;
+                        aq += pa * ks;
+                        ag += (pp * kx[mm][e] + pa * qx[mm][e]) * ks;
+                    }
+                    for (int sx = t; sx <= s.bhi[t]; ++sx) {
+                        const float ex = kexp<PREC>(s.g[sx][d] - gt);
+                        const float pp = s.beta[sx] * sdL[sx * LDL + t], pa = ld1<ST>(&sm.dA[sx][t]);
+                        const float c = (pp * ld1<ST>(&s.kr[sx][d]) + pa * ld1<ST>(&s.ql[sx][d])) * ex;
+                        ak += c;
+                        ag -= c * kx[mm][e];
                     }
                     dka[mm][e] += ak;
                     dqa[mm][e] += aq;
