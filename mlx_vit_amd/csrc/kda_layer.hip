@@ -37,7 +37,7 @@ constexpr int PR = 8;        // producer forward: rows per workgroup
 constexpr int BR = 8;        // producer backward: rows per strip
 constexpr int BNS = 4;       // producer backward: strips per workgroup
 constexpr int NR = 16;       // norm: rows per strip
-constexpr int NNS = 4;       // norm backward: strips per workgroup
+constexpr int NNS = 2;       // norm backward: strips per workgroup
 constexpr int NPV = 17;      // producer parameter-gradient values per channel
 constexpr float L2_EPS = 1e-12f;
 
