@@ -22,6 +22,7 @@
 // are HBM- and VALU-bound; nothing here is MFMA-shaped.  Parameter gradients
 // are per-workgroup partial sums in the caller's workspace, summed by a
 // column-reduction kernel, so every result is deterministic (no atomics).
+#include <algorithm>
 #include <cstdint>
 
 #include "kda_internal.h"
@@ -487,17 +488,32 @@ __global__ __launch_bounds__(512) void producer_bwd_kernel(const ProdArgs a) {
 }
 
 // out[col] = sum_p part[p][col]; 64 columns x 4 row slices per workgroup.
+// Column sums of a row-major (P, N) partial-sum buffer in a fixed order:
+// workgroup (x, y) sums rows [P*y/S, P*(y+1)/S) of columns [64x, 64x + 64)
+// into row y of dst, S = gridDim.y.  Four accumulators per lane keep four
+// loads in flight.
 __global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ part, int P, int N,
-                                                     float* __restrict__ out) {
+                                                     float* __restrict__ dst) {
     __shared__ float red[4][64];
     const int l = threadIdx.x & 63, sl = threadIdx.x >> 6;
     const int col = blockIdx.x * 64 + l;
-    float s = 0.f;
-    if (col < N)
-        for (int p = sl; p < P; p += 4) s += part[(size_t)p * N + col];
-    red[sl][l] = s;
+    const int S = gridDim.y, y = blockIdx.y;
+    const int lo = (int)((long long)P * y / S), hi = (int)((long long)P * (y + 1) / S);
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    if (col < N) {
+        const float* c = part + col;
+        int p = lo + sl;
+        for (; p + 12 < hi; p += 16) {
+            s0 += c[(size_t)p * N];
+            s1 += c[(size_t)(p + 4) * N];
+            s2 += c[(size_t)(p + 8) * N];
+            s3 += c[(size_t)(p + 12) * N];
+        }
+        for (; p < hi; p += 4) s0 += c[(size_t)p * N];
+    }
+    red[sl][l] = (s0 + s1) + (s2 + s3);
     __syncthreads();
-    if (sl == 0 && col < N) out[col] = (red[0][l] + red[1][l]) + (red[2][l] + red[3][l]);
+    if (sl == 0 && col < N) dst[(size_t)y * N + col] = (red[0][l] + red[1][l]) + (red[2][l] + red[3][l]);
 }
 
 __global__ __launch_bounds__(256) void producer_finish_kernel(const ProdArgs a) {
@@ -621,14 +637,37 @@ __global__ __launch_bounds__(256) void rmsnorm_finish_kernel(const NormArgs a) {
 
 int nwaves(int H, int D) { return (H * D + CPW - 1) / CPW; }
 
+// Row slices of the first column-sum pass: about 1024 workgroups over the
+// chip, at least 8 rows a slice, at most 64 slices (the second pass sums them).
+int colsum_splits(int P, int N) {
+    const int nbx = (N + 63) / 64;
+    return std::max(1, std::min({(1024 + nbx - 1) / nbx, P / 8, 64}));
+}
+
+// Column sums of part (P, N) into out (N), through stage (colsum_splits rows
+// of N) when the rows are split.
+void launch_colsum(const float* part, int P, int N, float* out, float* stage, hipStream_t st) {
+    const int nbx = (N + 63) / 64, S = colsum_splits(P, N);
+    if (S == 1) {
+        colsum_kernel<<<dim3(nbx, 1), dim3(256), 0, st>>>(part, P, N, out);
+        return;
+    }
+    colsum_kernel<<<dim3(nbx, S), dim3(256), 0, st>>>(part, P, N, stage);
+    colsum_kernel<<<dim3(nbx, 1), dim3(256), 0, st>>>(stage, S, N, out);
+}
+
 }  // namespace
 
 int producer_partials(int B, int T) { return B * ((T + BR * BNS - 1) / (BR * BNS)); }
 size_t producer_ws_floats(int B, int T, int H, int D) {
-    return ((size_t)producer_partials(B, T) + 1) * NPV * (size_t)H * D;
+    const int P = producer_partials(B, T), N = NPV * H * D;
+    return ((size_t)P + 1 + colsum_splits(P, N)) * N;
 }
 int rmsnorm_partials(int rows) { return (rows + NR * NNS - 1) / (NR * NNS); }
-size_t rmsnorm_ws_floats(int rows, int H, int D) { return ((size_t)rmsnorm_partials(rows) + 1) * (size_t)H * D; }
+size_t rmsnorm_ws_floats(int rows, int H, int D) {
+    const int P = rmsnorm_partials(rows), N = H * D;
+    return ((size_t)P + 1 + colsum_splits(P, N)) * N;
+}
 
 hipError_t launch_producer_fwd(const ProdArgs& a, int in_bf16, int g_bf16, hipStream_t st) {
     const dim3 grid(a.B * ((a.T + PR - 1) / PR)), block(64 * nwaves(a.H, a.D));
@@ -656,7 +695,7 @@ hipError_t launch_producer_bwd(const ProdArgs& a, int in_bf16, int g_bf16, hipSt
         else producer_bwd_kernel<float, float><<<grid, block, 0, st>>>(a);
     }
     const int N = NPV * HD;
-    colsum_kernel<<<dim3((N + 63) / 64), dim3(256), 0, st>>>(a.part, P, N, a.colsum);
+    launch_colsum(a.part, P, N, a.colsum, a.colsum + N, st);
     producer_finish_kernel<<<dim3((HD + 255) / 256), dim3(256), 0, st>>>(a);
     return hipGetLastError();
 }
@@ -676,7 +715,7 @@ hipError_t launch_rmsnorm_bwd(const NormArgs& a, int in_bf16, hipStream_t st) {
         if (in_bf16) rmsnorm_bwd_kernel<uint16_t><<<grid, block, 0, st>>>(a);
         else rmsnorm_bwd_kernel<float><<<grid, block, 0, st>>>(a);
     }
-    colsum_kernel<<<dim3((HD + 63) / 64), dim3(256), 0, st>>>(a.part, P, HD, a.colsum);
+    launch_colsum(a.part, P, HD, a.colsum, a.colsum + HD, st);
     rmsnorm_finish_kernel<<<dim3(1), dim3(256), 0, st>>>(a);
     return hipGetLastError();
 }
