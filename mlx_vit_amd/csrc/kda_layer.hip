@@ -34,10 +34,11 @@ namespace {
 constexpr int KC = 4;        // conv taps (ShortCausalConv1d(kernel_size=4))
 constexpr int CPW = 256;     // channels per wave
 constexpr int MAXW = 8;      // H*D <= 2048
-constexpr int PR = 8;        // producer forward: rows per workgroup
+constexpr int PR = 4;        // producer forward: rows per workgroup
 constexpr int BR = 8;        // producer backward: rows per strip
 constexpr int BNS = 4;       // producer backward: strips per workgroup
-constexpr int NR = 16;       // norm: rows per strip
+constexpr int NR = 4;        // norm forward: rows per workgroup
+constexpr int NRB = 4;       // norm backward: rows per strip
 constexpr int NNS = 2;       // norm backward: strips per workgroup
 constexpr int NPV = 17;      // producer parameter-gradient values per channel
 constexpr float L2_EPS = 1e-12f;
@@ -582,18 +583,18 @@ __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(const NormArgs a) {
     const ST* dyp = static_cast<const ST*>(a.dy);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < NNS; ++s) {
-        const int r0 = (wg * NNS + s) * NR;
+        const int r0 = (wg * NNS + s) * NRB;
         if (r0 >= a.rows) break;
-        float ov[NR][4], zv[NR][4], gv[NR][4];
+        float ov[NRB][4], zv[NRB][4], gv[NRB][4];
 #pragma unroll
-        for (int j = 0; j < NR; ++j) {
+        for (int j = 0; j < NRB; ++j) {
             const size_t r = min(r0 + j, a.rows - 1);
             Vec4<ST>::ld(o + r * L.HD + L.cc, ov[j]);
             Vec4<ST>::ld(z + r * a.ld_z + L.cc, zv[j]);
             Vec4<ST>::ld(dyp + r * a.ld_dy + L.cc, gv[j]);
         }
 #pragma unroll
-        for (int j = 0; j < NR; ++j) {
+        for (int j = 0; j < NRB; ++j) {
             const bool ok = r0 + j < a.rows && L.live;
             float ss = 0.f;
 #pragma unroll
@@ -663,7 +664,7 @@ size_t producer_ws_floats(int B, int T, int H, int D) {
     const int P = producer_partials(B, T), N = NPV * H * D;
     return ((size_t)P + 1 + colsum_splits(P, N)) * N;
 }
-int rmsnorm_partials(int rows) { return (rows + NR * NNS - 1) / (NR * NNS); }
+int rmsnorm_partials(int rows) { return (rows + NRB * NNS - 1) / (NRB * NNS); }
 size_t rmsnorm_ws_floats(int rows, int H, int D) {
     const int P = rmsnorm_partials(rows), N = H * D;
     return ((size_t)P + 1 + colsum_splits(P, N)) * N;
