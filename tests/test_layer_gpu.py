@@ -62,6 +62,10 @@ PRODUCER_CASES = [
     (3, 33, 4, 32, torch.float32, False, 2.0),     # no conv bias, allow_neg_eigval
     (2, 77, 12, 64, torch.bfloat16, True, 1.0),
     (1, 40, 6, 64, torch.bfloat16, False, 2.0),
+    # enough row segments (>= 16) that the parameter-gradient column sums run
+    # as two passes over row slices
+    (2, 300, 4, 64, torch.float32, True, 1.0),
+    (4, 260, 3, 64, torch.bfloat16, True, 1.0),
 ]
 
 
