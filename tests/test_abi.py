@@ -56,6 +56,24 @@ def test_workspace_sizes():
     assert lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) == 0 or lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) >= 0
 
 
+@pytest.mark.parametrize("B,T,H,D", [(8, 1568, 12, 64), (1, 1, 3, 64), (2, 300, 4, 64), (1, 70, 16, 128),
+                                     (4, 65, 12, 64)])
+def test_layer_workspace_sizes(B, T, H, D):
+    """The backward workspaces hold one partial-sum row per workgroup (32 tokens
+    of one batch row for the producer, 8 rows for the norm), the summed row,
+    and 1 to 64 rows of slice sums; every row is H*D values per parameter
+    gradient (17 for the producer), fp32."""
+    lib = _lib.load()
+    HD = H * D
+    for which, rows, vals in ((_lib.KDA_LAYER_PRODUCER, B * -(-T // 32), 17),
+                              (_lib.KDA_LAYER_RMSNORM, -(-(B * T) // 8), 1)):
+        got = lib.kda_layer_workspace_size(which, B, T, H, D)
+        row = 4 * vals * HD
+        assert got % row == 0
+        assert (rows + 2) * row <= got <= (rows + 1 + 64) * row, (which, got, rows)
+    assert lib.kda_layer_workspace_size(7, B, T, H, D) == 0
+
+
 def test_workspace_offsets_disjoint():
     lib = _lib.load()
     for pass_ in (0, 1, 2):
