@@ -34,7 +34,7 @@ namespace {
 constexpr int KC = 4;        // conv taps (ShortCausalConv1d(kernel_size=4))
 constexpr int CPW = 256;     // channels per wave
 constexpr int MAXW = 8;      // H*D <= 2048
-constexpr int PR = 4;        // producer forward: rows per workgroup
+constexpr int PR = 2;        // producer forward: rows per workgroup
 constexpr int BR = 8;        // producer backward: rows per strip
 constexpr int BNS = 4;       // producer backward: strips per workgroup
 constexpr int NR = 4;        // norm forward: rows per workgroup
@@ -160,8 +160,9 @@ __device__ __forceinline__ void conv_silu_rows(const ProdArgs& a, const Lanes& L
 // Workgroup = (batch row b, strip of PR tokens).  q and k need the norm of the
 // whole H*D row: a first pass forms the per-row sums of squares (reduced
 // across the workgroup through LDS), and after the barrier q and k are
-// recomputed from their (cached) input rows rather than held in registers,
-// which keeps the kernel at about half the VGPRs and twice the waves.
+// scaled by their inverse norms and stored, held in registers across the
+// barrier (70 VGPRs at PR = 2; at 4 rows recomputing them after the barrier
+// was 15% slower than holding them).
 template <typename ST, typename GT>
 __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
     __shared__ float red[2][MAXW][PR];
@@ -183,16 +184,11 @@ __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
             if (L.lane == 0) red[i][L.w][j] = ss;
         }
     };
-    {
-        float sv[PR][4];
-        conv_silu_rows<ST, 0>(a, L, t0, rb, sv);
-        row_norms(sv, 0);
-    }
-    {
-        float sv[PR][4];
-        conv_silu_rows<ST, 1>(a, L, t0, rb, sv);
-        row_norms(sv, 1);
-    }
+    float sq[PR][4], sk[PR][4];
+    conv_silu_rows<ST, 0>(a, L, t0, rb, sq);
+    row_norms(sq, 0);
+    conv_silu_rows<ST, 1>(a, L, t0, rb, sk);
+    row_norms(sk, 1);
     {
         float sv[PR][4];
         conv_silu_rows<ST, 2>(a, L, t0, rb, sv);
@@ -244,16 +240,8 @@ __global__ __launch_bounds__(512) void producer_fwd_kernel(const ProdArgs a) {
             if (t0 + j < T && L.live) Vec4<ST>::st(out + (rb + t0 + j) * L.HD + L.cc, o);
         }
     };
-    {
-        float sv[PR][4];
-        conv_silu_rows<ST, 0>(a, L, t0, rb, sv);
-        finish(sv, 0, static_cast<ST*>(a.q), a.scale);
-    }
-    {
-        float sv[PR][4];
-        conv_silu_rows<ST, 1>(a, L, t0, rb, sv);
-        finish(sv, 1, static_cast<ST*>(a.k), 1.f);
-    }
+    finish(sq, 0, static_cast<ST*>(a.q), a.scale);
+    finish(sk, 1, static_cast<ST*>(a.k), 1.f);
 }
 
 // ---------------------------------------------------------------- producer, backward
