@@ -517,10 +517,16 @@ __global__ __launch_bounds__(256) void producer_finish_kernel(const ProdArgs a) 
         }
         if (a.ddt_bias) a.ddt_bias[c] = cs[(size_t)15 * HD + c];
     }
-    if (a.dA_log && c < a.H) {
-        float s = 0.f;
-        for (int d = 0; d < a.D; ++d) s += cs[(size_t)16 * HD + (size_t)c * a.D + d];
-        a.dA_log[c] = s;
+    // dA_log[h] = sum over the head's D channels: one wave per head, the
+    // lanes over channels (the loop bound is the same for the whole wave)
+    if (a.dA_log) {
+        const int lane = threadIdx.x & 63;
+        for (int h = blockIdx.x * 4 + (threadIdx.x >> 6); h < a.H; h += gridDim.x * 4) {
+            float s = 0.f;
+            for (int d = lane; d < a.D; d += 64) s += cs[(size_t)16 * HD + (size_t)h * a.D + d];
+            s = wave_sum(s);
+            if (lane == 0) a.dA_log[h] = s;
+        }
     }
 }
 
