@@ -63,17 +63,28 @@ def op_counts(B, T, H, D, backward):
 
 
 def kernel_counts(B, T, H, D, es=2):
-    """Per-launch algorithmic FLOPs and compulsory HBM bytes of each library
-    kernel (ids as in kda_profile_name).
+    """Per-launch figures of each library kernel (ids as in kda_profile_name):
+    (flops, alg_bytes, ws_bytes).
 
-    FLOPs: the dense products each kernel owns, full rectangles, 2 per MAC, per
-    padded token-head.  Bytes: every input and output tensor of the kernel
-    touched once -- (B, T, H, *) tensors over the T valid tokens, workspace slabs
-    over every chunk -- with the library's storage types: operands and the
-    W/U/Qp/Kb/V'/dV'/A/h/dh workspace in the input dtype (``es`` bytes), Akk,
-    the diagonal-block inverses, e^G and the states in fp32.  With bf16 inputs
-    (``es`` = 2) the local-adjoint kernel recomputes Akk, the inverses and V', so
-    no kernel writes or reads them."""
+    flops: the dense products the kernel owns, full rectangles, 2 per MAC, per
+    padded token-head.
+
+    alg_bytes: the op's minimum HBM traffic (the forward reads q, k,
+    v, g, beta once and writes o; the backward reads q, k, v, g, beta, dO once
+    and writes dq, dk, dv, dg, dbeta; states fp32, read or written once),
+    attributed to the kernel that moves it -- prep the forward's inputs, the
+    forward recurrence o and the states, the reverse carry dS_T / dS_0, the
+    local-adjoint kernel the whole backward I/O.  Per valid token-head at D = 64
+    bf16: 514 B (prep), 128 B (recur fwd), 1,156 B (local).  The state
+    recompute moves no op-level bytes at all.
+
+    ws_bytes: every input and output tensor of the kernel touched once,
+    workspace slabs included (the inter-kernel traffic of this design) -- (B, T,
+    H, *) tensors over the T valid tokens, workspace slabs over every chunk --
+    with the library's storage types: operands and the W/U/Qp/Kb/V'/dV'/A/h/dh
+    workspace in the input dtype (``es`` bytes), Akk, the diagonal-block
+    inverses, e^G and the states in fp32.  With bf16 inputs the local-adjoint
+    kernel recomputes Akk, the inverses and V', so no kernel moves them."""
     nc = -(-T // C)
     N = B * H * nc              # chunks
     n = N * C                   # padded token-heads
@@ -95,7 +106,14 @@ def kernel_counts(B, T, H, D, es=2):
         6: n * (8 * C * D + (2.0 / 3.0) * C * C),
     }
     io_in = nt * (4 * D + 1) * es                       # q, k, v, g, beta
-    by = {
+    alg = {
+        0: io_in, 2: io_in, 6: io_in,                   # the forward's inputs
+        1: nt * D * es + state,                         # o, S_final (S_0 with an initial state)
+        3: 0,
+        4: 2 * state,                                   # dS_T in, dS_0 out (bounded above by these)
+        5: nt * (5 * D + 1) * es + nt * (4 * D + 1) * es,   # q k v g beta dO in; dq dk dv dg dbeta out
+    }
+    ws = {
         0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp KbT Aqk eG
         1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state,                      # -> o, S_final
         2: io_in + N * (6 * CD * es + CC * es + x * (CC + TII) * f4 + D * f4),             # -> W U KbT WT QpT Kb AqkT [Akk Tii] eG
@@ -105,7 +123,7 @@ def kernel_counts(B, T, H, D, es=2):
            + nt * (4 * D + 1) * es,                                                         # -> dq dk dv dg dbeta
         6: io_in + N * (7 * CD * es + 2 * CC * es + x * (CC + TII) * f4 + D * f4),         # -> both sets
     }
-    return fl, by
+    return fl, alg, ws
 
 
 def make_inputs_gpu(B, T, H, D, with_state, seed=0):
@@ -224,7 +242,9 @@ def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, s
     """Time the torch fp32 restatement of the reference 'compiled' path on the
     host cores (bounded sample: the same B, H, D over `sample_tokens` steps),
     and measure rel-L2 of the HIP results against the fp64 C oracle on the
-    same seeded inputs (drawn on the CPU so the oracle can regenerate them)."""
+    same seeded inputs at the full workload size (drawn on the CPU so the
+    oracle can regenerate them), through the same entry points as the timed
+    step (kda_fwd_train + kda_bwd_train for a fwd+bwd workload)."""
     import torch
     from oracle import cref
     from oracle import kda_reference as R
@@ -253,11 +273,16 @@ def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, s
     x = R.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=seed, with_state=with_state, with_grad=backward)
     dev = lambda t: None if t is None else t.to("cuda")
     q, k, v, g, beta, s0 = (dev(x[nm]) for nm in ("q", "k", "v", "g", "beta", "s0"))
-    o, sf = kda.kda_forward(q, k, v, g, beta, s0)
+    # through the entry points the timed step calls: the training pair for a
+    # fwd+bwd workload, the plain forward otherwise
+    if backward:
+        o, sf, ws = kda.kda_forward_train(q, k, v, g, beta, s0)
+    else:
+        o, sf = kda.kda_forward(q, k, v, g, beta, s0)
     ref = cref.forward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"])
     errs = {"o": R.rel_l2(o.cpu(), ref["o"]), "s_final": R.rel_l2(sf.cpu(), ref["s_final"])}
     if backward:
-        grads = kda.kda_backward(q, k, v, g, beta, s0, dev(x["do"]))
+        grads = kda.kda_backward_train(q, k, v, g, beta, s0, dev(x["do"]), None, ws)
         rb = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"])
         for nm, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads):
             errs[nm] = R.rel_l2(gr.cpu(), rb[nm])
@@ -501,7 +526,7 @@ def main():
     prof_ms_per_step = (time.perf_counter() - t1) / args.steps * 1e3
     lib.kda_profile_enable(0)
     import ctypes
-    fl, by = kernel_counts(B, T, H, D)
+    fl, alg, wsb = kernel_counts(B, T, H, D)
     kernels = []
     for kid in range(_lib.PROF_NKERNELS):
         tot, cnt = ctypes.c_double(), ctypes.c_int()
@@ -509,12 +534,18 @@ def main():
         if cnt.value == 0:
             continue
         avg_s = tot.value / cnt.value * 1e-3
+        name = lib.kda_profile_name(kid).decode()
+        traffic = load_traffic(name)
         kernels.append({
-            "name": lib.kda_profile_name(kid).decode(), "launches": cnt.value, "avg_us": round(avg_s * 1e6, 2),
+            "name": name, "launches": cnt.value, "avg_us": round(avg_s * 1e6, 2),
             "tflops": round(fl[kid] / avg_s / 1e12, 2), "mfma_frac": round(fl[kid] / avg_s / PEAK_BF16, 4),
-            "gbs": round(by[kid] / avg_s / 1e9, 1), "hbm_frac": round(by[kid] / avg_s / PEAK_HBM, 4),
-            "alg_flops": fl[kid], "alg_bytes": by[kid], "_avg_s": avg_s, "_id": kid,
+            "alg_bytes": alg[kid], "alg_gbs": round(alg[kid] / avg_s / 1e9, 1),
+            "hbm_frac": round(alg[kid] / avg_s / PEAK_HBM, 4),
+            "ws_bytes": wsb[kid], "ws_gbs": round(wsb[kid] / avg_s / 1e9, 1),
+            "pmc_bytes": traffic, "pmc_over_alg": (round(traffic / alg[kid], 3) if traffic and alg[kid] else None),
+            "alg_flops": fl[kid], "_avg_s": avg_s,
         })
+    # the dominant kernel (most time per step) and its roofline on the op's own bytes
     dom = max(kernels, key=lambda r: r["avg_us"] * r["launches"])
     t_mfma, t_hbm = dom["alg_flops"] / PEAK_BF16, dom["alg_bytes"] / PEAK_HBM
     if t_mfma >= t_hbm:
@@ -524,12 +555,14 @@ def main():
         rl = {"bound": "hbm", "achieved": round(dom["alg_bytes"] / dom["_avg_s"] / 1e9, 2),
               "peak": PEAK_HBM / 1e9, "unit": "GB/s"}
     rl["frac"] = round(rl["achieved"] / rl["peak"], 5)
-    rl["traffic"] = load_traffic(dom["name"])
+    rl["traffic"] = dom["pmc_bytes"]
     rl["kernel"] = dom["name"]
     rl["avg_us"] = dom["avg_us"]
+    rl["alg_bytes"] = dom["alg_bytes"]
+    rl["ws_bytes"] = dom["ws_bytes"]
+    rl["traffic_over_alg"] = dom["pmc_over_alg"]
     for r in kernels:
         r.pop("_avg_s")
-        r.pop("_id")
 
     op_flops, op_bytes = op_counts(B, T, H, D, backward)
     step_s = ms_per_step * 1e-3

@@ -176,6 +176,18 @@ hipError_t timed(int id, hipStream_t st, F&& launch) {
 // ----------------------------------------------------------------------------
 namespace kda {
 
+int device_cu_count(int dev) {
+    constexpr int MAXDEV = 64;
+    static std::once_flag once[MAXDEV];
+    static int cus[MAXDEV];
+    if (dev < 0 || dev >= MAXDEV) return 0;
+    std::call_once(once[dev], [dev] {
+        int n = 0;
+        cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) ? n : 0;
+    });
+    return cus[dev];
+}
+
 __global__ __launch_bounds__(256) void kda_state_copy_kernel(const float* __restrict__ src, float* __restrict__ dst,
                                                              size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)

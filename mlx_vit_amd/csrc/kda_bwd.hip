@@ -4,7 +4,7 @@
 // are recomputed (prep + kda_recur_kernel MODE 1), the reverse state carry
 // (kda_dh_kernel, kda_recur.hip) stores dS at each chunk end and dV', then:
 //
-//   kda_bwd_local2_kernel (bf16 operands) / kda_bwd_local_kernel (fp32 operands)
+//   kda_bwd_local3_kernel (bf16 operands) / kda_bwd_local_kernel (fp32 operands)
 //                     one workgroup per chunk, fully parallel: every remaining
 //                     adjoint of the chunk -- output / state products, the
 //                     transposed WY solve (nope_gdn_mlx.py:2637-2641, as block
@@ -261,7 +261,13 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) B.v[e] = s.kr[BS * j + 4 * g4 + e][d] * fs;
                     dKl = mma4<PX>(frag4(&sp[0][0], C + 4, BS * i, BS * j), B, dKl);
-                    dQl = mma4<PX>(frag4(&sda[0][0], C + 4, BS * i, BS * j), B, dQl);
+                    Fr4 Aq = frag4(&sda[0][0], C + 4, BS * i, BS * j);
+                    if (j == i) {   // the diagonal pairs (t, t) are added apart, below
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (4 * g4 + e == r16) Aq.v[e] = 0.f;
+                    }
+                    dQl = mma4<PX>(Aq, B, dQl);
                 }
                 Fr4 Bk, Bq;
 #pragma unroll
@@ -283,7 +289,13 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
 #pragma unroll
                 for (int j = 0; j <= i; ++j) {
                     f32x4 dKr = mma4<PX>(frag4T(&sp[0][0], C + 4, BS * j, BS * i), Bk, zero4());
-                    dKr = mma4<PX>(frag4T(&sda[0][0], C + 4, BS * j, BS * i), Bq, dKr);
+                    Fr4 Aq = frag4T(&sda[0][0], C + 4, BS * j, BS * i);
+                    if (j == i) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (4 * g4 + e == r16) Aq.v[e] = 0.f;
+                    }
+                    dKr = mma4<PX>(Aq, Bq, dKr);
                     const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -305,14 +317,14 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                     float ak = 0.f, aq = 0.f, ag = 0.f;
                     // row t (dP[t][sx] strict, dA[t][sx]) and column t (dP[sx][t],
                     // dA[sx][t]) as two loops over the decay band
-                    for (int sx = s.blo[t]; sx <= t; ++sx) {
+                    for (int sx = s.blo[t]; sx < t; ++sx) {
                         const float ks = s.kr[sx][d] * kexp<PREC>(gt - s.g[sx][d]);
                         const float pp = sp[t][sx], pa = sda[t][sx];
                         ak += pp * ks;
                         aq += pa * ks;
                         ag += (pp * kx[m][e] + pa * qx[m][e]) * ks;
                     }
-                    for (int sx = t; sx <= s.bhi[t]; ++sx) {
+                    for (int sx = t + 1; sx <= s.bhi[t]; ++sx) {
                         const float ex = kexp<PREC>(s.g[sx][d] - gt);
                         const float pp = sp[sx][t], pa = sda[sx][t];
                         const float c = (pp * s.kr[sx][d] + pa * s.ql[sx][d]) * ex;
@@ -325,6 +337,19 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
                 }
             }
         }
+        // The diagonal pairs (t, t) of A_qk (weight 1): dq_t += dA_tt k_t and
+        // dk_t += dA_tt q_t, and nothing in dgamma_t, whose row and column terms
+        // of such a pair are equal and opposite (summed into the two sides they
+        // would dominate both, and the fp32 rounding of those sums would survive
+        // the cancellation into dg).
+#pragma unroll
+        for (int m = 0; m < NB; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * m + 4 * g4 + e;
+                dqa[m][e] += sda[t][t] * kx[m][e];
+                dka[m][e] += sda[t][t] * qx[m][e];
+            }
 
         // PHASE 5
         // ---------------- phase 5: dG, reverse cumsum, stores ----------------
@@ -376,14 +401,20 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// local adjoints, bf16 operands (kda_bwd_local_kernel above serves fp32 inputs)
+// LDS plan of the bf16 local-adjoint kernel (kda_bwd_local3_kernel below;
+// kda_bwd_local_kernel above serves fp32 inputs).
 //
 // Every global operand of the chunk arrives in one batch of 16-byte loads and
 // lives in LDS; LDS regions are reused once their phase is over:
+//   s          the chunk's q, k, gamma and anchored operands (ChunkSmem); the
+//              g region later holds the solve's split A fragments and dL
 //   region A   dO, V', h, dh (phase 1) -> dR (phases 2-3) -> dq/dk/dv/dg staging
-//   region B   dV', v (phases 1-2)     -> dL (phases 3-4)
-// Wave w owns dk-channel tile w (D = 64: all four waves); all per-(t, d)
-// adjoints of that tile accumulate in its registers.
+//   region B   dV', v (phases 1-2)     -> dL when it does not fit in s.g (phases 3-4)
+//   W, U       the chunk's WY factors (phases 1 and 3)
+//   akk, tii   the recomputed A_kk and the inverted diagonal blocks of I + L
+//   dA         dA_qk = tril(dO V'^T, -1) (phase 1 -> phase 4); its diagonal is
+//              kept apart in dAd (see phase 4)
+// At D = 64, bf16: 155,648 bytes, one workgroup per CU.
 // ----------------------------------------------------------------------------
 template <int D, typename ST>
 struct alignas(16) LocalSmem {
@@ -414,427 +445,6 @@ struct alignas(16) LocalSmem {
     float dbeta[C];
 };
 
-template <int D, typename ST, typename TG, int PREC>
-__global__ __launch_bounds__(256) void kda_bwd_local2_kernel(const LocalArgs a) {
-    using L = LocalSmem<D, ST>;
-    constexpr int NT = D / BS, LDK = L::LDK, LDT = L::LDT, LDA = L::LDA, LDR = L::LDR;
-    __shared__ L sm;
-    auto& s = sm.s;
-
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
-    const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int t0 = n * C, valid = min(C, a.T - t0);
-    const size_t rs = (size_t)a.H * D;
-    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
-    const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
-    const size_t cCD = (size_t)ch * C * D, cCC = (size_t)ch * C * C, cDD = (size_t)ch * D * D;
-
-    // ---------------- phase 0: one batch of loads ----------------
-    int flag = 0;
-    {
-        Tile<ST, C, D> tq, tk, tv, tdo, tW, tU, tVp, tdVp;
-        Tile<TG, C, D> tg;
-        Tile<ST, D, D> th, tdh;
-        Tile<float, C, C> takk;
-        Tile<float, NB * BS, BS> ttii;
-        tq.load(static_cast<const ST*>(a.q) + base, rs, valid);
-        tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
-        tv.load(static_cast<const ST*>(a.v) + base, rs, valid);
-        tdo.load(static_cast<const ST*>(a.dout) + base, rs, valid);
-        tg.load(static_cast<const TG*>(a.g) + base, rs, valid);
-        tW.load(static_cast<const ST*>(a.W) + cCD, D);
-        tU.load(static_cast<const ST*>(a.U) + cCD, D);
-        tVp.load(static_cast<const ST*>(a.Vp) + cCD, D);
-        tdVp.load(static_cast<const ST*>(a.dVp) + cCD, D);
-        th.load(static_cast<const ST*>(a.h) + cDD, D);
-        tdh.load(static_cast<const ST*>(a.dh) + cDD, D);
-        takk.load(a.Akk + cCC, C);
-        ttii.load(a.Tii + (size_t)ch * NB * BS * BS, BS);
-        const float bt = (tid < valid) ? ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)tid * a.H) : 0.f;
-        tq.store(&s.ql[0][0], LDK);
-        tk.store(&s.kr[0][0], LDK);
-        tv.store(&sm.rb.p2.v[0][0], LDK);
-        tdo.store(&sm.ra.p1.dO[0][0], LDK);
-        tW.store(&sm.W[0][0], LDK);
-        tU.store(&sm.U[0][0], LDK);
-        tVp.store(&sm.ra.p1.Vp[0][0], LDK);
-        tdVp.store(&sm.rb.p2.dVp[0][0], LDK);
-        th.store(&sm.ra.p1.h[0][0], LDK);
-        tdh.store(&sm.ra.p1.dh[0][0], LDK);
-        takk.store(&sm.akk[0][0], LDA);
-        ttii.store(&sm.tii[0][0][0], BS + 4);
-        constexpr int EPV = Tile<TG, C, D>::EPV, VPR = Tile<TG, C, D>::VPR;
-#pragma unroll
-        for (int i = 0; i < Tile<TG, C, D>::PER; ++i) {
-            const int vv = tid + 256 * i, row = vv / VPR, c = (vv - row * VPR) * EPV;
-            const Vec16<TG> x{tg.get(i)};
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                const float gv = x.get(e);
-                s.g[row][c + e] = gv;
-                if (!(gv <= 0.f)) flag = 1;
-            }
-        }
-        if (tid < C) {
-            s.beta[tid] = bt;
-            sm.dbeta[tid] = 0.f;
-        }
-    }
-    __syncthreads();
-    chunk_cumsum2<D, ST>(s);
-    const int unsafe = chunk_factors2<D, ST, PREC>(s, flag);
-
-    // per-lane values of the owned (t, d): rows t = 16 m + 4 g4 + e, channel d
-    const int nt = w;
-    const bool own = nt < NT;
-    const int d = own ? nt * BS + r16 : 0;
-    float kx[NB][4], qx[NB][4], el[NB][4], er[NB][4], eb[NB][4], erb[NB];
-    {
-        const float G = s.g[C - 1][d];
-#pragma unroll
-        for (int m = 0; m < NB; ++m) {
-            const float gr = s.g[BS * m][d];
-            erb[m] = s.er[m][d];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * m + 4 * g4 + e;
-                const float gt = s.g[t][d];
-                kx[m][e] = ld1<ST>(&s.kr[t][d]);
-                qx[m][e] = ld1<ST>(&s.ql[t][d]);
-                el[m][e] = kexp<PREC>(gt - gr);
-                er[m][e] = unsafe ? 0.f : kexp<PREC>(gr - gt);
-                eb[m][e] = kexp<PREC>(G - gt);
-            }
-        }
-    }
-    __syncthreads();
-    if (!unsafe) {
-        // anchored operands in place (pass A of the prep kernel, without outputs)
-        constexpr int EPV = 16 / (int)sizeof(ST), VPR = D / EPV;
-        for (int vv = tid; vv < C * VPR; vv += 256) {
-            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, r = t & ~(BS - 1);
-            const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
-            const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
-            float okl[EPV], oql[EPV], okr[EPV];
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                const float x = s.g[t][c0 + e] - s.g[r][c0 + e];
-                const float e1 = kexp<PREC>(x), e2 = kexp<PREC>(-x);
-                okl[e] = kv.get(e) * e1;
-                oql[e] = qv.get(e) * e1;
-                okr[e] = kv.get(e) * e2;
-            }
-            store_vec<ST>(&s.kl[t][c0], okl);
-            store_vec<ST>(&s.ql[t][c0], oql);
-            store_vec<ST>(&s.kr[t][c0], okr);
-        }
-    }
-    __syncthreads();
-
-    f32x4 dqa[NB], dka[NB], dga[NB], dWt[NB];
-    float dgcol = 0.f;
-
-    // ---------------- phase 1: products over dv ----------------
-    {
-        const ST* sdO = &sm.ra.p1.dO[0][0];
-        const ST* sVp = &sm.ra.p1.Vp[0][0];
-        const ST* sdVp = &sm.rb.p2.dVp[0][0];
-        const ST* sh = &sm.ra.p1.h[0][0];
-        const ST* sdh = &sm.ra.p1.dh[0][0];
-        if (own) {
-            Frag8 Ao[NB][D / 32], Av[NB][D / 32], Ad[NB][D / 32], Bh[D / 32], Bdh[D / 32];
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                Bh[ks] = ldfrag<PREC, ST>(sh, LDK, BS * nt, 32 * ks);
-                Bdh[ks] = ldfrag<PREC, ST>(sdh, LDK, BS * nt, 32 * ks);
-#pragma unroll
-                for (int m = 0; m < NB; ++m) {
-                    Ao[m][ks] = ldfrag<PREC, ST>(sdO, LDK, BS * m, 32 * ks);
-                    Av[m][ks] = ldfrag<PREC, ST>(sVp, LDK, BS * m, 32 * ks);
-                    Ad[m][ks] = ldfrag<PREC, ST>(sdVp, LDK, BS * m, 32 * ks);
-                }
-            }
-            // state-decay term of dG: e^G sum_col dh[d][col] h[d][col]
-            float part = 0.f;
-#pragma unroll
-            for (int c = 0; c < D / 4; ++c) {
-                const int cc = g4 * (D / 4) + c;
-                part += ld1<ST>(sdh + d * LDK + cc) * ld1<ST>(sh + d * LDK + cc);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int m = 0; m < NB; ++m) {
-                f32x4 dQp = zero4(), dKb = zero4(), dW = zero4();
-#pragma unroll
-                for (int ks = 0; ks < D / 32; ++ks) {
-                    dQp = mma<PREC>(Ao[m][ks], Bh[ks], dQp);
-                    dKb = mma<PREC>(Av[m][ks], Bdh[ks], dKb);
-                    dW = mma<PREC>(Ad[m][ks], Bh[ks], dW);
-                }
-                dWt[m] = negacc(dW);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float egt = erb[m] * el[m][e];                  // e^{gamma_t}
-                    const float kbv = kx[m][e] * eb[m][e];                // Kb
-                    dqa[m][e] = dQp[e] * egt;
-                    dka[m][e] = dKb[e] * eb[m][e];
-                    dga[m][e] = dQp[e] * qx[m][e] * egt - dKb[e] * kbv;
-                    dgcol += dKb[e] * kbv;
-                }
-            }
-            dgcol = sum4g(dgcol) + kexp<PREC>(s.g[C - 1][d]) * sum4g(part);
-        }
-        // dAqk = tril(dO V'^T): 10 lower tiles over the 4 waves
-        for (int tix = w; tix < 10; tix += 4) {
-            int i, j;
-            tile_ij(tix, i, j);
-            Frag8 A[D / 32], B[D / 32];
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                A[ks] = ldfrag<PREC, ST>(sdO, LDK, BS * i, 32 * ks);
-                B[ks] = ldfrag<PREC, ST>(sVp, LDK, BS * j, 32 * ks);
-            }
-            f32x4 acc = zero4();
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) acc = mma<PREC>(A[ks], B[ks], acc);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
-                st1<ST>(&sm.dA[t][sx], (sx <= t) ? acc[e] : 0.f);
-            }
-        }
-    }
-    __syncthreads();   // phase-1 operands (region A) are dead from here
-
-    // ---------------- phase 2: transposed WY solve ----------------
-    f32x4 dRv[NB];
-    if (own) {
-        f32x4 dRk[NB];
-        const ST* sdVp = &sm.rb.p2.dVp[0][0];
-#pragma unroll
-        for (int i = NB - 1; i >= 0; --i) {
-            f32x4 Yk = dWt[i], Yv;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) Yv[e] = ld1<ST>(sdVp + (BS * i + 4 * g4 + e) * LDK + d);
-#pragma unroll
-            for (int j = i + 1; j < NB; ++j) {
-                // A[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a]
-                float av[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int rb = BS * j + 4 * g4 + e;
-                    av[e] = -s.beta[rb] * sm.akk[rb][BS * i + r16];
-                }
-                const Frag4 A = frag4_from_f32<3>(av);
-                Yk = mma4f<3>(A, accfrag4<3>(dRk[j]), Yk);
-                Yv = mma4f<3>(A, accfrag4<3>(dRv[j]), Yv);
-            }
-            float tv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) tv[e] = sm.tii[i][4 * g4 + e][r16];     // A[a][b] = T_ii[b][a]
-            const Frag4 Tt = frag4_from_f32<3>(tv);
-            dRk[i] = mma4f<3>(Tt, accfrag4<3>(Yk), zero4());
-            dRv[i] = mma4f<3>(Tt, accfrag4<3>(Yv), zero4());
-        }
-#pragma unroll
-        for (int m = 0; m < NB; ++m)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * m + 4 * g4 + e;
-                const float bt = s.beta[t], egt = erb[m] * el[m][e];
-                dka[m][e] += bt * egt * dRk[m][e];
-                dga[m][e] += dRk[m][e] * bt * egt * kx[m][e];
-                sm.ra.dR[t][d] = dRk[m][e];
-                sm.ra.dR[t][D + d] = dRv[m][e];
-            }
-    }
-    __syncthreads();
-    // dbeta, part 1: sum_d dV~[t][d] v[t][d] + dK~[t][d] e^{gamma_t} k[t][d]; 4 threads per row
-    {
-        const int t = tid >> 2, qd = tid & 3;
-        float acc = 0.f;
-        for (int dd = qd * (D / 4); dd < (qd + 1) * (D / 4); ++dd) {
-            const float egk = unsafe ? ld1<ST>(&s.kr[t][dd]) * kexp<PREC>(s.g[t][dd])
-                                     : ld1<ST>(&s.kl[t][dd]) * s.er[t / BS][dd];
-            acc += sm.ra.dR[t][D + dd] * ld1<ST>(&sm.rb.p2.v[t][dd]) + sm.ra.dR[t][dd] * egk;
-        }
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        if (qd == 0) sm.dbeta[t] = acc;
-    }
-    __syncthreads();   // v and dV' (region B) are dead from here
-
-    // ---------------- phase 3: dL = -tril(dR X^T, -1) ----------------
-    for (int tix = w; tix < 10; tix += 4) {
-        int i, j;
-        tile_ij(tix, i, j);
-        Frag8 A[2 * D / 32], B[2 * D / 32];
-#pragma unroll
-        for (int ks = 0; ks < 2 * D / 32; ++ks) {
-            A[ks] = ldfrag<3, float>(&sm.ra.dR[0][0], LDR, BS * i, 32 * ks);
-            B[ks] = (32 * ks < D) ? ldfrag<3, ST>(&sm.W[0][0], LDK, BS * j, 32 * ks)
-                                  : ldfrag<3, ST>(&sm.U[0][0], LDK, BS * j, 32 * ks - D);
-        }
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 2 * D / 32; ++ks) acc = mma<3>(A[ks], B[ks], acc);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
-            sm.rb.dL[t][sx] = (sx < t) ? -acc[e] : 0.f;
-        }
-    }
-    __syncthreads();
-    // dbeta, part 2: sum_s dL[t][s] Akk[t][s]
-    {
-        const int t = tid >> 2, qd = tid & 3;
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < C / 4; ++c) {
-            const int sx = qd * (C / 4) + c;
-            acc += sm.rb.dL[t][sx] * sm.akk[t][sx];
-        }
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        if (qd == 0) sm.dbeta[t] += acc;
-    }
-
-    // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints (dP = diag(beta) dL) ----------------
-    if (own) {
-        if (!unsafe) {
-#pragma unroll
-            for (int i = 0; i < NB; ++i) {
-                const float bi = s.beta[BS * i + r16];
-                f32x4 dKl = zero4(), dQl = zero4();
-#pragma unroll
-                for (int j = 0; j <= i; ++j) {
-                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
-                    float bv[4], pv[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) bv[e] = ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]) * fs;
-                    const float4 x = *reinterpret_cast<const float4*>(&sm.rb.dL[BS * i + r16][BS * j + 4 * g4]);
-                    pv[0] = bi * x.x; pv[1] = bi * x.y; pv[2] = bi * x.z; pv[3] = bi * x.w;
-                    const Frag4 B = frag4_from_f32<PREC>(bv);
-                    dKl = mma4f<PREC>(frag4_from_f32<PREC>(pv), B, dKl);
-                    dQl = mma4f<PREC>(ldfrag4<PREC, ST>(&sm.dA[0][0], LDT, BS * i, BS * j), B, dQl);
-                }
-                float bkv[4], bqv[4], btv[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    bkv[e] = ld1<ST>(&s.kl[BS * i + 4 * g4 + e][d]);
-                    bqv[e] = ld1<ST>(&s.ql[BS * i + 4 * g4 + e][d]);
-                    btv[e] = s.beta[BS * i + 4 * g4 + e];
-                }
-                // dgamma weighted by the other side's MFMA operands (exact pair cancellation)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    dka[i][e] += dKl[e] * el[i][e];
-                    dqa[i][e] += dQl[e] * el[i][e];
-                    dga[i][e] += dKl[e] * mfma_operand<PREC>(bkv[e]) + dQl[e] * mfma_operand<PREC>(bqv[e]);
-                }
-                const Frag4 Bk = frag4_from_f32<PREC>(bkv), Bq = frag4_from_f32<PREC>(bqv);
-#pragma unroll
-                for (int j = 0; j <= i; ++j) {
-                    float pv[4], av[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int t = BS * i + 4 * g4 + e;
-                        pv[e] = btv[e] * sm.rb.dL[t][BS * j + r16];      // dP^T
-                        av[e] = ld1<ST>(&sm.dA[t][BS * j + r16]);        // dA^T
-                    }
-                    f32x4 dKr = mma4f<PREC>(frag4_from_f32<PREC>(pv), Bk, zero4());
-                    dKr = mma4f<PREC>(frag4_from_f32<PREC>(av), Bq, dKr);
-                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float fac = fs * er[j][e];
-                        dka[j][e] += dKr[e] * fac;
-                        dga[j][e] -= dKr[e] * mfma_operand<PREC>(ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]) * fs);
-                    }
-                }
-            }
-        } else {
-            // pairwise path: raw k in kr, raw q in ql, gamma in g
-#pragma unroll
-            for (int m = 0; m < NB; ++m)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int t = BS * m + 4 * g4 + e;
-                    const float gt = s.g[t][d], bt = s.beta[t];
-                    float ak = 0.f, aq = 0.f, ag = 0.f;
-                    for (int sx = 0; sx < C; ++sx) {
-                        const float gs = s.g[sx][d];
-                        if (sx <= t) {
-                            const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - gs);
-                            const float pp = bt * sm.rb.dL[t][sx], pa = ld1<ST>(&sm.dA[t][sx]);
-                            ak += pp * ks;
-                            aq += pa * ks;
-                            ag += (pp * kx[m][e] + pa * qx[m][e]) * ks;
-                        }
-                        if (sx >= t) {
-                            const float ex = kexp<PREC>(gs - gt);
-                            const float pp = s.beta[sx] * sm.rb.dL[sx][t], pa = ld1<ST>(&sm.dA[sx][t]);
-                            const float c = (pp * ld1<ST>(&s.kr[sx][d]) + pa * ld1<ST>(&s.ql[sx][d])) * ex;
-                            ak += c;
-                            ag -= c * kx[m][e];
-                        }
-                    }
-                    dka[m][e] += ak;
-                    dqa[m][e] += aq;
-                    dga[m][e] += ag;
-                }
-        }
-
-        // ---------------- phase 5: dG, reverse cumsum ----------------
-        if (g4 == 3) dga[NB - 1][3] += dgcol;        // row C-1
-        float lsum[NB][4], tot[NB];
-#pragma unroll
-        for (int m = 0; m < NB; ++m) {
-            float run = 0.f;
-#pragma unroll
-            for (int e = 3; e >= 0; --e) { run += dga[m][e]; lsum[m][e] = run; }
-            tot[m] = run;
-        }
-        float after_m = 0.f;
-#pragma unroll
-        for (int m = NB - 1; m >= 0; --m) {
-            const float t0v = __shfl(tot[m], r16, 64);
-            const float t1v = __shfl(tot[m], r16 + 16, 64);
-            const float t2v = __shfl(tot[m], r16 + 32, 64);
-            const float t3v = __shfl(tot[m], r16 + 48, 64);
-            const float later = (g4 < 1 ? t1v : 0.f) + (g4 < 2 ? t2v : 0.f) + (g4 < 3 ? t3v : 0.f);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) lsum[m][e] += later + after_m;
-            after_m += t0v + t1v + t2v + t3v;
-        }
-        // staging in region A: its last readers (phase 3) finished before the barrier after phase 3
-#pragma unroll
-        for (int m = 0; m < NB; ++m)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * m + 4 * g4 + e;
-                st1<ST>(&sm.ra.out[0][t][d], dqa[m][e]);
-                st1<ST>(&sm.ra.out[1][t][d], dka[m][e]);
-                st1<ST>(&sm.ra.out[2][t][d], s.beta[t] * dRv[m][e]);
-                st1<ST>(&sm.ra.out[3][t][d], lsum[m][e]);
-            }
-    }
-    __syncthreads();
-    tile_out<ST, C, D>(&sm.ra.out[0][0][0], LDK, static_cast<ST*>(a.dq) + base, rs, valid);
-    tile_out<ST, C, D>(&sm.ra.out[1][0][0], LDK, static_cast<ST*>(a.dk) + base, rs, valid);
-    tile_out<ST, C, D>(&sm.ra.out[2][0][0], LDK, static_cast<ST*>(a.dv) + base, rs, valid);
-    if constexpr (std::is_same<TG, ST>::value) {
-        tile_out<ST, C, D>(&sm.ra.out[3][0][0], LDK, static_cast<ST*>(a.dg) + base, rs, valid);
-    } else {
-        for (int idx = tid; idx < C * D; idx += 256) {
-            const int t = idx / D, dd = idx - t * D;
-            if (t < valid) st1<TG>(static_cast<TG*>(a.dg) + base + (size_t)t * rs + dd, ld1<ST>(&sm.ra.out[3][t][dd]));
-        }
-    }
-    if (tid < valid) st1<ST>(static_cast<ST*>(a.dbeta) + bbase + (size_t)tid * a.H, sm.dbeta[tid]);
-}
-
 // ----------------------------------------------------------------------------
 // local adjoints, bf16 operands, 8 waves (two per SIMD, so each hides the
 // other's latencies).  Wave w owns channel tile ct = w % 4 and row half
@@ -851,7 +461,7 @@ __global__ __launch_bounds__(256) void kda_bwd_local2_kernel(const LocalArgs a) 
 //            through one LDS total per channel
 // A_kk, its diagonal-block inverses and V' = U - W h are recomputed here from
 // what is already in LDS instead of being read from the workspace.
-// LDS regions and their reuse are those of kda_bwd_local2_kernel.
+// LDS regions and their reuse: the plan above LocalSmem.
 // ----------------------------------------------------------------------------
 template <int D, typename ST, typename TG, int PREC>
 __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) {
@@ -1390,7 +1000,13 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     const float4 x = *reinterpret_cast<const float4*>(sdL + (BS * i + r16) * LDL + BS * j + 4 * g4);
                     const float pv[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
                     const f32x4 Pk = mma4f<1>(frag4_from_f32<1>(pv), B, zero4());
-                    const f32x4 Pq = mma4f<1>(ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * i, BS * j), B, zero4());
+                    Frag4 Aq = ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * i, BS * j);
+                    if (j == i) {   // the diagonal pairs (t, t) are added apart, below
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (4 * g4 + e == r16) Aq.h[e] = 0;
+                    }
+                    const f32x4 Pq = mma4f<1>(Aq, B, zero4());
                     const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -1423,7 +1039,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     for (int e = 0; e < 4; ++e) {
                         const int t = BS * i + 4 * g4 + e;
                         pv[e] = s.beta[t] * sdL[t * LDL + BS * j + r16];   // dP^T
-                        av[e] = ld1<ST>(&sm.dA[t][BS * j + r16]);           // dA^T
+                        av[e] = (i == j && 4 * g4 + e == r16) ? 0.f : ld1<ST>(&sm.dA[t][BS * j + r16]);   // dA^T
                     }
                     f32x4 P = mma4f<1>(frag4_from_f32<1>(pv), colfrag(&s.kl[0][0], LDK, BS * i), zero4());
                     P = mma4f<1>(frag4_from_f32<1>(av), colfrag(&s.ql[0][0], LDK, BS * i), P);
@@ -1440,7 +1056,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             }
         } else {
             // pairwise path: raw k in kr, raw q in ql, gamma in g.  Row side
-            // (s <= t) and column side (s >= t) run as two loops over the decay
+            // (s < t) and column side (s > t) run as two loops over the decay
             // band, so no iteration carries the other side's masked work.
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm)
@@ -1449,14 +1065,14 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     const int t = BS * (2 * rh + mm) + 4 * g4 + e;
                     const float gt = s.g[t][d], bt = s.beta[t];
                     float ak = 0.f, aq = 0.f, ag = 0.f;
-                    for (int sx = s.blo[t]; sx <= t; ++sx) {
+                    for (int sx = s.blo[t]; sx < t; ++sx) {
                         const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - s.g[sx][d]);
                         const float pp = bt * sdL[t * LDL + sx], pa = ld1<ST>(&sm.dA[t][sx]);
                         ak += pp * ks;
                         aq += pa * ks;
                         ag += (pp * kx[mm][e] + pa * qx[mm][e]) * ks;
                     }
-                    for (int sx = t; sx <= s.bhi[t]; ++sx) {
+                    for (int sx = t + 1; sx <= s.bhi[t]; ++sx) {
                         const float ex = kexp<PREC>(s.g[sx][d] - gt);
                         const float pp = s.beta[sx] * sdL[sx * LDL + t], pa = ld1<ST>(&sm.dA[sx][t]);
                         const float c = (pp * ld1<ST>(&s.kr[sx][d]) + pa * ld1<ST>(&s.ql[sx][d])) * ex;
@@ -1468,6 +1084,21 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     dga[mm][e] += ag;
                 }
         }
+        // The diagonal pairs (t, t) of A_qk (weight e^0 = 1): dq_t += dA_tt k_t and
+        // dk_t += dA_tt q_t.  Their row and column terms of dgamma_t are equal and
+        // opposite, so they are left out of it altogether: summed into the row and
+        // column sides they would dominate both (the off-diagonal pairs carry
+        // decayed weights), and the fp32 rounding of those sums, relative to the
+        // diagonal term, would survive the cancellation into dg.
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * (2 * rh + mm) + 4 * g4 + e;
+                const float a = ld1<ST>(&sm.dA[t][t]);
+                dqa[mm][e] += a * kx[mm][e];
+                dka[mm][e] += a * qx[mm][e];
+            }
     }
 
     // ---------------- phase 5: dG, reverse cumsum over the two row halves ----------------
@@ -1536,15 +1167,9 @@ static hipError_t launch_local_t(const LocalArgs& a, int nchunks, hipStream_t st
         hipLaunchKernelGGL((kda_bwd_local_kernel<D, TI, TG, 3>), dim3(nchunks), dim3(256), 0, st, a);
     else {
         // prefetch distance: one chunk per CU (one local-adjoint workgroup fills a CU)
-        static int cus[64];
         int dev = 0;
         LocalArgs b = a;
-        b.pf_ahead = 0;
-        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-            if (cus[dev] <= 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-                cus[dev] = 0;
-            b.pf_ahead = cus[dev] > 0 ? cus[dev] : 0;
-        }
+        b.pf_ahead = (hipGetDevice(&dev) == hipSuccess) ? device_cu_count(dev) : 0;
         hipLaunchKernelGGL((kda_bwd_local3_kernel<D, TI, TG, 1>), dim3(nchunks), dim3(512), 0, st, b);
     }
     return hipGetLastError();

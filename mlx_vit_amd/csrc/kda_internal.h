@@ -56,6 +56,10 @@ struct LocalArgs {
     int pf_ahead;   // L2 prefetch distance in chunks (the device's CU count), 0 = none
 };
 
+// Compute-unit count of device `dev` (0 if it cannot be queried), looked up
+// once per device under std::call_once, so concurrent callers are safe.
+int device_cu_count(int dev);
+
 hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
 // mode 0: O and the final state; 1: the chunk-start states h
 hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st);

@@ -1069,7 +1069,8 @@ __global__ __launch_bounds__(512) void kda_dh2_kernel(const DhArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// bf16 recurrences, row split, LDS-DMA fed (kda_recur3_kernel / kda_dh3_kernel).
+// bf16 recurrences, row split, LDS-DMA fed (kda_recur3_kernel; the reverse
+// carry kda_dh4_kernel below uses the same slab sets, Dh3Layout).
 //
 // CS workgroups per (batch, head) own DC = D / CS state columns each.  Wave w
 // owns row block w of the chunk's [C][DC] tiles and state row blocks w, w + 4.
@@ -1653,237 +1654,10 @@ struct Dh3Layout {
                              DmaTile<C, RB_U, 4>::COUNT + 1;
 };
 
-// Reverse state recurrence, same pipeline as kda_recur3_kernel, loop step k on
-// chunk nc-1-k:
-//   A(k)  flush step k-1; DMA step k+NS; dV' = Aqk^T dO + Kb dS (row block w);
-//         write -dV'^T and dV'; wait for step k+1's DMA
-//   B(k)  dS <- diag(e^G) dS + Qp^T dO - W^T dV'; write dS^T and dS (the next
-//         chunk's chunk-end adjoint); read step k+1's A operands
-template <int D, int CS>
-__global__ __launch_bounds__(256) void kda_dh3_kernel(const DhArgs a) {
-    using ST = uint16_t;
-    using Lay = Dh3Layout<D, CS>;
-    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4, NS = Lay::NS;
-    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
-    constexpr int RB_D = Lay::RB_D, RB_C = Lay::RB_C, RB_U = Lay::RB_U;
-    __shared__ __align__(1024) char set0[Lay::SET_BYTES];
-    __shared__ __align__(1024) char set1[Lay::SET_BYTES];
-    __shared__ __align__(1024) char set2[Lay::SET_BYTES];
-    __shared__ __align__(16) char smem[Lay::XBYTES];
-
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
-    __builtin_assume(w >= 0 && w < 4);
-    const int lb = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int nc = a.nc;
-    const char* gAqkT = static_cast<const char*>(a.AqkT);
-    const char* gKb = static_cast<const char*>(a.Kb);
-    const char* gQpT = static_cast<const char*>(a.QpT);
-    const char* gWT = static_cast<const char*>(a.WT);
-    const char* gdO = static_cast<const char*>(a.dout);
-    const char* gEg = reinterpret_cast<const char*>(a.eG);
-
-    auto stg = [&](int k) __attribute__((always_inline)) {
-        return reinterpret_cast<ST*>(smem + Lay::STG_OFF + (k % Lay::NSTG) * Lay::STG_BYTES);
-    };
-    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
-    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
-
-    // step k's slabs (chunk nc-1-k) -> LDS set sb = set (k % NS)
-    using TA = DmaTile<C, RB_C, 4>;
-    using TB = DmaTile<C, RB_D, 4>;
-    using TQ = DmaTile<D, RB_C, 4>;
-    using TO = DmaTile<C, RB_U, 4>;
-    uint32_t oA[TA::COUNT], oB[TB::COUNT], oQ[TQ::COUNT], oO[TO::COUNT];
-    TA::offsets(oA, RB_C, w, l);
-    TB::offsets(oB, RB_D, w, l);
-    TQ::offsets(oQ, RB_C, w, l);
-    TO::offsets(oO, (size_t)a.H * D * 2, w, l);
-    const uint32_t oE = (uint32_t)((D / 4) * 4 * w + 16 * (l < D / 16 ? l : 0));
-    auto dma_step = [&](int k, char* sb) __attribute__((always_inline)) {
-        const int n = nc - 1 - k;
-        const size_t ch = (size_t)bh * nc + n;
-        const int t0 = n * C, valid = min(C, a.T - t0);
-        TA::issue_s(gAqkT + ch * C * C * 2, oA, sb + Lay::AQKT_OFF, w);
-        TB::issue_s(gKb + ch * C * D * 2, oB, sb + Lay::KB_OFF, w);
-        TQ::issue_s(gQpT + ch * C * D * 2, oQ, sb + Lay::QPT_OFF, w);
-        TQ::issue_s(gWT + ch * C * D * 2, oQ, sb + Lay::WT_OFF, w);
-        const char* gdo = gdO + ((((size_t)b * a.T + t0) * a.H + h) * D + c0) * 2;
-        if (valid == C) TO::issue_s(gdo, oO, sb + Lay::DO_OFF, w);
-        else TO::issue(gdo, (size_t)a.H * D * 2, sb + Lay::DO_OFF, w, l, valid);
-        if (l < D / 16) dma16_s(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + D * w);
-    };
-    auto flush = [&](int k) __attribute__((always_inline)) {
-        const ST* sst = stg(k);
-        const size_t ch = (size_t)bh * nc + (nc - 1 - k);
-        tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
-        tile_out<ST, C, DC>(sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
-    };
-
-    int mt[MT];
-    bool own[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        mt[i] = w + 4 * i;
-        own[i] = mt[i] < NT;
-    }
-    f32x4 dS[MT][NTW];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-            dS[i][j] = zero4();
-            if (own[i] && a.dsf) {
-                const float4 x = *reinterpret_cast<const float4*>(
-                    a.dsf + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4);
-                dS[i][j] = f32x4{x.x, x.y, x.z, x.w};
-            }
-        }
-    auto put_state = [&](ST* sst) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-            if (own[i])
-#pragma unroll
-                for (int j = 0; j < NTW; ++j) {
-                    *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(dS[i][j]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, dS[i][j][e]);
-                }
-    };
-
-    Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
-    float4 eg[MT];
-    auto preload = [&](const char* sb) __attribute__((always_inline)) {
-        const ST* sAqkT = reinterpret_cast<const ST*>(sb + Lay::AQKT_OFF);
-        const ST* sKb = reinterpret_cast<const ST*>(sb + Lay::KB_OFF);
-        const ST* sQpT = reinterpret_cast<const ST*>(sb + Lay::QPT_OFF);
-        const ST* sWT = reinterpret_cast<const ST*>(sb + Lay::WT_OFF);
-        const ST* sdO = reinterpret_cast<const ST*>(sb + Lay::DO_OFF);
-        const float* seG = reinterpret_cast<const float*>(sb + Lay::EG_OFF);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-            if (ks >= w / 2) Aat[ks] = ldfrag_sw<RB_C>(sAqkT, BS * w, 32 * ks);
-#pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) Akb[ks] = ldfrag_sw<RB_D>(sKb, BS * w, 32 * ks);
-        // dO as B operand (k = t, n = column): gathered from its row-major tile
-#pragma unroll
-        for (int j = 0; j < NTW; ++j)
-#pragma unroll
-            for (int ks = 0; ks < C / 32; ++ks) {
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[e] = ld_sw<RB_U>(sdO, 32 * ks + 4 * g4 + e, BS * j + r16);
-                    v[4 + e] = ld_sw<RB_U>(sdO, 32 * ks + 16 + 4 * g4 + e, BS * j + r16);
-                }
-                Bo[j][ks] = frag_from_f32<1>(v);
-            }
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-            if (own[i]) {
-#pragma unroll
-                for (int ks = 0; ks < C / 32; ++ks) {
-                    Aqt[i][ks] = ldfrag_sw<RB_C>(sQpT, BS * mt[i], 32 * ks);
-                    Awt[i][ks] = ldfrag_sw<RB_C>(sWT, BS * mt[i], 32 * ks);
-                }
-                eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
-            }
-    };
-
-    // prologue: steps 0 .. NS-1 in flight; the last chunk's rows past T are
-    // not loaded, so they are zeroed in LDS
-    put_state(stg(0));
-    dma_step(0, set0);
-    if (nc > 1) dma_step(1, set1);
-    if (nc > 2) dma_step(2, set2);
-    {
-        const int valid = a.T - (nc - 1) * C;
-        if (valid < C) {
-            char* dO0 = set0 + Lay::DO_OFF;
-            for (int idx = tid; idx < C * RB_U / 16; idx += 256)
-                if (idx / (RB_U / 16) >= valid) *reinterpret_cast<uint4*>(dO0 + 16 * idx) = make_uint4(0u, 0u, 0u, 0u);
-        }
-    }
-    dma_wait_chunks<Lay::L>(min(NS, nc) - 1);
-    lds_barrier();
-    preload(set0);
-
-    auto step = [&](int k, char* sdma, const char* snext) __attribute__((always_inline)) {
-        ST* sst = stg(k);
-        lds_barrier();                                          // A(k)
-        if (k > 0) flush(k - 1);
-        if (k + NS < nc) dma_step(k + NS, sdma);
-
-        Frag8 Bs[NTW][D / 32];
-#pragma unroll
-        for (int j = 0; j < NTW; ++j)
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, BS * j, 32 * ks);
-        // dV' = Aqk^T dO + Kb dS, row block w
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-            f32x4 dV = zero4();
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-                if (ks >= w / 2) dV = mma<1>(Aat[ks], Bo[j][ks], dV);
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) dV = mma<1>(Akb[ks], Bs[j][ks], dV);
-            *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * w + 4 * g4) = pack4bf(negacc(dV));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * w + 4 * g4 + e) * LDU + BS * j + r16, dV[e]);
-        }
-        dma_wait_chunks<Lay::L>(min(nc - 1, k + NS) - (k + 1));
-        lds_barrier();                                          // B(k)
-
-        Frag8 Bvn[NTW][C / 32];    // -dV'
-#pragma unroll
-        for (int j = 0; j < NTW; ++j)
-#pragma unroll
-            for (int ks = 0; ks < C / 32; ++ks) Bvn[j][ks] = ldfrag<1, ST>(xv, LDC, BS * j, 32 * ks);
-        // dS <- diag(e^G) dS + Qp^T dO - W^T dV'
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-            if (own[i]) {
-#pragma unroll
-                for (int j = 0; j < NTW; ++j) {
-                    dS[i][j] = f32x4{dS[i][j][0] * eg[i].x, dS[i][j][1] * eg[i].y, dS[i][j][2] * eg[i].z,
-                                     dS[i][j][3] * eg[i].w};
-#pragma unroll
-                    for (int ks = 0; ks < C / 32; ++ks) {
-                        dS[i][j] = mma<1>(Awt[i][ks], Bvn[j][ks], dS[i][j]);
-                        dS[i][j] = mma<1>(Aqt[i][ks], Bo[j][ks], dS[i][j]);
-                    }
-                }
-            }
-        if (k + 1 < nc) {
-            put_state(stg(k + 1));
-            preload(snext);
-        }
-    };
-    for (int k = 0; k < nc; k += 3) {
-        step(k, set0, set1);
-        if (k + 1 < nc) step(k + 1, set1, set2);
-        if (k + 2 < nc) step(k + 2, set2, set0);
-    }
-    lds_barrier();
-    flush(nc - 1);
-
-    if (a.ds0) {
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-            if (own[i])
-#pragma unroll
-                for (int j = 0; j < NTW; ++j)
-                    *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + c0 + BS * j + r16) * D + BS * mt[i] + 4 * g4) =
-                        make_float4(dS[i][j][0], dS[i][j][1], dS[i][j][2], dS[i][j][3]);
-    }
-}
-
 // ----------------------------------------------------------------------------
-// kda_dh4_kernel: kda_dh3_kernel with the work split between two wave roles
-// (512 threads).  Waves 0-3 run the reverse state chain: dV' (row block wr),
+// kda_dh4_kernel: the reverse state recurrence (loop step k on chunk
+// nc-1-k), the pipeline of kda_recur3_kernel with the work split between
+// two wave roles (512 threads).  Waves 0-3 run the reverse state chain: dV' (row block wr),
 // the dS update of state rows wr, wr + 4, dS^T / dh / dV' staging, the flush
 // of the previous step's staged dh and dV', and read the next chunk's
 // operands.  Waves 4-7 bring the slabs by DMA (after barrier B, when the

@@ -9,13 +9,15 @@
   p <- p (1 - lr wd); m <- b1 m + (1 - b1) g; v <- b2 v + (1 - b2) g^2;
   p <- p - lr m / (sqrt(v) + eps), with the moments in the parameter's dtype
   (train_mlx_k400.py:548-549: betas (0.9, 0.95), weight decay 0.05);
-* ``TrainStep`` -- forward, loss, backward, clip, update
-  (train_mlx_k400.py:379-408).
+* ``TrainStep`` -- the per-step body of the reference's epoch loop
+  (train_mlx_k400.py:379-408, 417-441): learning rate from
+  ``cosine_warmup_lr`` at the global step (when a schedule is given), forward,
+  loss, backward, clip, update, then the EMA update (when an EMA is given).
 """
 from __future__ import annotations
 
 import math
-from typing import Iterable, List
+from typing import Iterable, List, Optional
 
 import torch
 import torch.nn as nn
@@ -96,21 +98,39 @@ class AdamW:
 
 
 class TrainStep:
-    """One optimisation step: forward, label-smoothed loss, backward, global
-    clip, AdamW update.  Returns the loss (a 0-d fp32 tensor)."""
+    """One optimisation step: learning rate, forward, label-smoothed loss,
+    backward, global clip, AdamW update, EMA update.  Returns the loss (a 0-d
+    fp32 tensor).
+
+    With ``total_steps`` set, the learning rate of step ``global_step`` is
+    ``cosine_warmup_lr(global_step, total_steps, warmup_steps, lr)`` (the
+    reference sets it before each step, train_mlx_k400.py:427-429); without it
+    the rate stays ``lr``.  ``ema`` (a ``checkpoint.ModelEMA``) is updated after
+    every optimiser step (train_mlx_k400.py:440-441).  ``global_step`` starts at
+    ``step_offset`` and advances by one per call."""
 
     def __init__(self, model: nn.Module, lr: float = 3e-4, weight_decay: float = 0.05, betas=(0.9, 0.95),
-                 grad_clip: float = 1.0, label_smoothing: float = 0.1):
+                 grad_clip: float = 1.0, label_smoothing: float = 0.1, total_steps: Optional[int] = None,
+                 warmup_steps: int = 0, ema=None, step_offset: int = 0):
         self.model = model
         self.opt = AdamW(model.parameters(), lr=lr, betas=betas, weight_decay=weight_decay)
+        self.base_lr = lr
         self.grad_clip = grad_clip
         self.label_smoothing = label_smoothing
+        self.total_steps, self.warmup_steps = total_steps, warmup_steps
+        self.ema = ema
+        self.global_step = step_offset
 
     def __call__(self, video: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+        if self.total_steps is not None:
+            self.opt.lr = cosine_warmup_lr(self.global_step, self.total_steps, self.warmup_steps, self.base_lr)
         self.opt.zero_grad()
         loss = loss_fn(self.model(video), target, self.label_smoothing)
         loss.backward()
         if self.grad_clip > 0:
             clip_grads_by_norm(self.opt.params, self.grad_clip)
         self.opt.step()
+        if self.ema is not None:
+            self.ema.update(self.model)
+        self.global_step += 1
         return loss.detach()

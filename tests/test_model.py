@@ -106,3 +106,40 @@ def test_adamw_closed_form_first_step():
     opt.step()
     expect = p0 * (1 - 0.01 * 0.05) - 0.01 * (0.1 * grad) / (math.sqrt(0.05) * grad.abs() + 1e-8)
     torch.testing.assert_close(p.detach(), expect)
+
+
+def test_train_step_schedule_and_ema():
+    """TrainStep sets the learning rate from cosine_warmup_lr at each global
+    step before the update and moves the EMA shadow after it
+    (train_mlx_k400.py:427-441).  Checked on a linear model with one fixed
+    batch against a hand-run copy of the same sequence."""
+    from mlx_vit_amd.checkpoint import ModelEMA, to_mlx_key
+    torch.manual_seed(5)
+    model = torch.nn.Linear(6, 4)
+    ref = torch.nn.Linear(6, 4)
+    ref.load_state_dict(model.state_dict())
+    ema = ModelEMA(model, decay=0.5)
+    step = TR.TrainStep(model, lr=0.1, grad_clip=0.0, label_smoothing=0.0, total_steps=8, warmup_steps=2, ema=ema,
+                        step_offset=1)
+    ropt = TR.AdamW(ref.parameters(), lr=0.1)
+    shadow = {n: p.detach().clone() for n, p in ref.named_parameters()}
+    x = torch.randn(3, 6)
+    y = torch.tensor([0, 2, 3])
+    for k in range(1, 5):
+        step(x, y)
+        ropt.lr = TR.cosine_warmup_lr(k, 8, 2, 0.1)
+        ropt.zero_grad()
+        TR.loss_fn(ref(x), y).backward()
+        ropt.step()
+        for n, p in ref.named_parameters():
+            shadow[n] = 0.5 * shadow[n] + 0.5 * p.detach()
+        assert step.opt.lr == pytest.approx(ropt.lr)
+    assert step.global_step == 5
+    for n, p in model.named_parameters():
+        torch.testing.assert_close(p.detach(), dict(ref.named_parameters())[n].detach())
+        torch.testing.assert_close(ema.shadow[to_mlx_key(n)], shadow[n])
+    # warm-up from step 0: the first update has learning rate 0 (weights unchanged but for no decay)
+    m2 = torch.nn.Linear(6, 4)
+    w0 = m2.weight.detach().clone()
+    TR.TrainStep(m2, lr=0.1, grad_clip=0.0, total_steps=8, warmup_steps=2)(x, y)
+    torch.testing.assert_close(m2.weight.detach(), w0)

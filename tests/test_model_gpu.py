@@ -3,10 +3,13 @@
 Parity: a small hybrid classifier (encoder block, three GDN blocks, one NoPE
 block, temporal head) in fp32 on the GPU against an fp64 CPU copy whose GDN
 layers run the CPU restatement of the layer (oracle/layer_reference.py): loss
-and every parameter gradient within rel-L2 1e-4, except the decay-gate
-parameters (2e-3, for the reason given at ``DECAY_GATE``).  Training: the config-4 model
-in bf16 takes optimisation steps with finite losses and changing weights, and
-a small model overfits one batch."""
+and every parameter gradient within rel-L2 1e-4.  The layer's own decay
+initialisation (A = e^{A_log} in [1, 16]) puts heads at -2 to -10 per step,
+where the decay-gate gradients (A_log, dt_bias, f_proj) are the most
+ill-conditioned sums in the model.  Training: the config-4 model (batch 8 of
+16x224x224 clips) in bf16 takes optimisation steps with finite losses,
+changing weights, the cosine schedule and the EMA, and a small model overfits
+one batch."""
 import copy
 import types
 
@@ -63,23 +66,8 @@ def test_classifier_parity_fp32():
         errs[n] = R.rel_l2(p.grad.cpu().double(), rp[n].grad)
     worst = sorted(errs.items(), key=lambda kv: -kv[1])[:6]
     print("classifier parity worst", {k: f"{v:.2e}" for k, v in worst}, flush=True)
-    bad = {k: v for k, v in errs.items() if not (v <= _tol(k))}
+    bad = {k: v for k, v in errs.items() if not (v <= 1e-4)}
     assert not bad, bad
-
-
-# The gradients of the decay-gate parameters are sums over every token of dg
-# (times g or sigmoid terms).  Heads whose per-step decay exceeds the anchored
-# path's span guard (here A = e^{A_log} of 9 to 14, g of -6 to -10 per step)
-# take the pairwise path, where the in-chunk cumulative log-decay reaches ~600
-# and exp(gamma_t - gamma_s) formed from two fp32 cumsums carries a relative
-# error of about |gamma| 2^-24 ~ 4e-5 that is coherent across a chunk.  The op's
-# own dg stays <= 1.4e-5 at such decays (test_bwd_dg_pairwise_strong_decay);
-# summed over 160 tokens these four gradients reach ~7e-4.
-DECAY_GATE = ("A_log", "dt_bias", "f_proj_1", "f_proj_2")
-
-
-def _tol(name):
-    return 2e-3 if any(s in name for s in DECAY_GATE) else 1e-4
 
 
 def test_small_model_overfits_one_batch():
@@ -99,23 +87,30 @@ def test_small_model_overfits_one_batch():
 
 def test_config4_train_steps_bf16():
     """The config-4 model (12 GDN blocks, 768 wide, 1568 tokens per clip) in bf16
-    with A_log / dt_bias in fp32: two optimisation steps on a batch of 2 clips."""
+    with A_log / dt_bias in fp32: two optimisation steps on a batch of 8 clips
+    (the stated configuration), with the warm-up schedule and the EMA."""
+    from mlx_vit_amd import checkpoint as CK
     from mlx_vit_amd import model as M
     from mlx_vit_amd import train as TR
     torch.manual_seed(4)
     model = M.to_bf16(M.config4()).to(DEV)
-    before = model.backbone.processor_blocks[5].layer.q_proj.weight.detach().clone()
-    a_before = model.backbone.processor_blocks[5].layer.A_log.detach().clone()
-    step = TR.TrainStep(model)
+    blk = model.backbone.processor_blocks[5].layer
+    before = blk.q_proj.weight.detach().clone()
+    a_before = blk.A_log.detach().clone()
+    ema = CK.ModelEMA(model, decay=0.9)
+    step = TR.TrainStep(model, lr=3e-4, total_steps=100, warmup_steps=5, ema=ema, step_offset=1)
     g = torch.Generator(device=DEV).manual_seed(5)
-    video = torch.randn(2, 16, 224, 224, 3, device=DEV, generator=g).to(torch.bfloat16)
-    target = torch.tensor([7, 123], device=DEV)
+    video = torch.randn(8, 16, 224, 224, 3, device=DEV, generator=g).to(torch.bfloat16)
+    target = torch.randint(0, 400, (8,), device=DEV, generator=g)
     losses = [step(video, target).item() for _ in range(2)]
-    print("config4 losses", losses, flush=True)
+    print("config4 B=8 losses", losses, "lr", step.opt.lr, flush=True)
     assert all(torch.isfinite(torch.tensor(losses)))
     assert abs(losses[0] - torch.log(torch.tensor(400.0)).item()) < 1.0
-    blk = model.backbone.processor_blocks[5].layer
+    assert step.opt.lr == TR.cosine_warmup_lr(2, 100, 5, 3e-4)
     assert not torch.equal(blk.q_proj.weight, before)
     assert blk.A_log.dtype == torch.float32 and not torch.equal(blk.A_log, a_before)
+    key = CK.to_mlx_key("backbone.processor_blocks.5.layer.A_log")
+    # after two updates the shadow sits strictly between the start and the weights
+    assert not torch.equal(ema.shadow[key], a_before) and not torch.equal(ema.shadow[key], blk.A_log.detach())
     for n, p in model.named_parameters():
         assert torch.isfinite(p).all(), n
