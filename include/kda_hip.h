@@ -86,6 +86,23 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
             int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
             void* workspace, size_t ws_bytes, void* stream);
 
+/* kda_fwd without a workspace argument: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The kernels of
+ * kda_fwd run on a static device array of KDA_NOALLOC_MAX_WORKSPACE bytes that
+ * the library holds on each GPU it runs on until the process ends; no call
+ * allocates or frees anything.  Shapes whose kda_fwd workspace
+ * (kda_workspace_size(KDA_PASS_FWD, ...)) exceeds that size are rejected with
+ * KDA_E_WORKSPACE before any device work (128 MiB: config 1, B8 H12 T1568 D64
+ * bf16, needs 98.9 MB).  Results are bit-identical to kda_fwd.  Every call on
+ * one GPU shares that GPU's array, so calls that overlap on one GPU (on
+ * different streams, or from several threads without ordering) race;
+ * stream-ordered calls on one stream do not. */
+#define KDA_NOALLOC_MAX_WORKSPACE ((size_t)128 << 20)
+int kda_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                    const float* s0, void* o, float* s_final,
+                    int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* stream);
+
 /* Training pair.  kda_fwd_train computes what kda_fwd computes and also keeps,
  * in its (pass 2) workspace, every per-chunk factor the backward needs: W, U,
  * the decay-scaled Q / K operands and their transposes, A_qk and its transpose,

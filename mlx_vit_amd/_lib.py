@@ -21,6 +21,8 @@ KDA_PASS_FWD = 0
 KDA_PASS_BWD = 1
 KDA_PASS_TRAIN = 2
 
+NOALLOC_MAX_WORKSPACE = 128 << 20   # KDA_NOALLOC_MAX_WORKSPACE
+
 KDA_LAYER_PRODUCER = 0
 KDA_LAYER_RMSNORM = 1
 
@@ -38,6 +40,7 @@ SIGNATURES = {
     "kda_fwd": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_bwd": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_fwd_train": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
+    "kda_fwd_noalloc": ([_P] * 8 + [_I] * 7 + [_P], _I),
     "kda_bwd_train": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_solve_unit_triangular": ([_P] * 3 + [_I] * 4 + [_P], _I),
     "kda_layer_producer_fwd": ([_P] * 5 + [_L] * 3 + [_P] * 9 + [_I] * 4 + [_F] * 2 + [_I] * 2 + [_P], _I),

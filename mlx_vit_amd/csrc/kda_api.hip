@@ -162,7 +162,8 @@ void prof_stop(int id, int idx, hipStream_t st) {
     (void)hipEventRecord(P.pool[id][idx].second, st);
 }
 template <typename F>
-hipError_t timed(int id, hipStream_t st, F&& launch) {
+hipError_t timed(int id, hipStream_t st, F&& launch, bool prof = true) {
+    if (!prof) return launch();
     const int pi = prof_start(id, st);
     const hipError_t e = launch();
     prof_stop(id, pi, st);
@@ -266,7 +267,7 @@ int check_workspace(void* workspace, size_t ws_bytes, const Layout& L) {
 // Prep: the forward's outputs (pass 0), the backward's (pass 1) or both (pass 2).
 hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                             void* ws, const Layout& L, int T, int H, int D, int nchunks, int in_bf16, int g_bf16,
-                            hipStream_t st) {
+                            hipStream_t st, bool prof = true) {
     kda::PrepArgs pa = {};
     pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
     pa.W = region(ws, L, KDA_WS_W);
@@ -283,12 +284,14 @@ hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* 
     pa.Tii = fregion(ws, L, KDA_WS_TII);
     pa.T = T; pa.H = H; pa.nc = (T + kda::C - 1) / kda::C;
     const int id = pass == KDA_PASS_FWD ? PROF_PREP_FWD : pass == KDA_PASS_BWD ? PROF_PREP_BWD : PROF_PREP_TRAIN;
-    return timed(id, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, nchunks, st); });
+    return timed(id, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, nchunks, st); }, prof);
 }
 
+// prof = false: no launch timing (the profiler's event pool never grows), for
+// the entry point that must not allocate
 int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
-            size_t ws_bytes, void* stream) {
+            size_t ws_bytes, void* stream, bool prof = true) {
     int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, pass == KDA_PASS_TRAIN);
     if (rc) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -309,7 +312,8 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
 
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
-    hipError_t e = launch_prep_pass(pass, q, k, v, g, beta, workspace, L, T, H, D, BH * nc, in_bf16, g_bf16, st);
+    hipError_t e =
+        launch_prep_pass(pass, q, k, v, g, beta, workspace, L, T, H, D, BH * nc, in_bf16, g_bf16, st, prof);
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     kda::RecurArgs ra = {};
@@ -321,9 +325,34 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     ra.eG = fregion(workspace, L, KDA_WS_EG);
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-    e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 0, st); });
+    e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 0, st); }, prof);
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
     return ok();
+}
+
+// ---- the forward without a caller workspace ----
+// Its workspace is this file-scope device array: one copy per GPU the library
+// runs on, held until the process ends.  Host code never uses the name
+// `scratch` as an address (on the host it is a stand-in, not device memory):
+// the device address comes from hipGetSymbolAddress, once per device, with
+// that device current.
+static __device__ __align__(256) unsigned char scratch[KDA_NOALLOC_MAX_WORKSPACE];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on device `dev` (the current device), looked up
+// once per device; nullptr with the HIP error in *err if the lookup failed.
+void* scratch_ptr(int dev, hipError_t* err) {
+    static std::once_flag once[kMaxDevices];
+    static void* ptr[kMaxDevices];
+    static hipError_t status[kMaxDevices];
+    std::call_once(once[dev], [dev] {
+        void* p = nullptr;
+        status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        ptr[dev] = (status[dev] == hipSuccess) ? p : nullptr;
+    });
+    *err = status[dev];
+    return ptr[dev];
 }
 
 // pass 1: prep from the inputs, then the backward; pass 2: the workspace holds
@@ -438,6 +467,28 @@ int kda_fwd(const void* q, const void* k, const void* v, const void* g, const vo
             size_t ws_bytes, void* stream) {
     return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
                    ws_bytes, stream);
+}
+
+int kda_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+                    void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+                    void* stream) {
+    int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, false);
+    if (rc) return rc;
+    Layout L;
+    make_layout(KDA_PASS_FWD, B, T, H, D, dtype, L);
+    if (L.total > KDA_NOALLOC_MAX_WORKSPACE)
+        return fail(KDA_E_WORKSPACE,
+                    "kda_fwd_noalloc: B=%d T=%d H=%d D=%d needs %zu bytes of workspace, above the %zu bytes of its "
+                    "static scratch; call kda_fwd with a caller workspace",
+                    B, T, H, D, L.total, (size_t)KDA_NOALLOC_MAX_WORKSPACE);
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "kda_fwd_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(KDA_E_UNSUPPORTED, "kda_fwd_noalloc: device %d >= %d", dev, kMaxDevices);
+    void* ws = scratch_ptr(dev, &e);
+    if (!ws) return hip_fail(e, "kda_fwd_noalloc: hipGetSymbolAddress(scratch)");
+    return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, ws,
+                   KDA_NOALLOC_MAX_WORKSPACE, stream, /*prof=*/false);
 }
 
 int kda_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
