@@ -43,7 +43,14 @@ WORKLOADS = {
              "KDA fwd+VJP (training pair), B8 H12 T1568 D64 bf16 (config 2)"),
     "cfg1": (8, 1568, 12, 64, False, False, "KDA fwd, B8 H12 T1568 D64 bf16 (config 1)"),
     "cfg3": (1, 32768, 16, 128, False, True, "KDA fwd, B1 H16 T32768 D128 bf16, fp32 S0 (config 3)"),
+    # config 2's shape with the decay of the reference layer at initialisation:
+    # g = -A_h softplus(x), A_h = e^{A_log} ~ U[1, 16] per head (nope_gdn_mlx.py:749),
+    # x ~ N(0, 0.5^2) for the gate projection plus dt_bias (zero at init)
+    "cfg2-layerdecay": (8, 1568, 12, 64, True, False,
+                        "KDA fwd+VJP (training pair), B8 H12 T1568 D64 bf16, layer-init decay "
+                        "g = -A_h softplus(N(0, 0.5^2)), A_h ~ U[1, 16]"),
 }
+LAYER_DECAY = {"cfg2-layerdecay"}
 
 
 def op_counts(B, T, H, D, backward):
@@ -126,8 +133,10 @@ def kernel_counts(B, T, H, D, es=2):
     return fl, alg, ws
 
 
-def make_inputs_gpu(B, T, H, D, with_state, seed=0):
-    """Synthetic inputs with the configs' distributions, drawn on the GPU."""
+def make_inputs_gpu(B, T, H, D, with_state, seed=0, layer_decay=False):
+    """Synthetic inputs with the configs' distributions, drawn on the GPU.  With
+    ``layer_decay`` g follows the reference layer at initialisation instead:
+    -A_h softplus(N(0, 0.5^2)) with A_h ~ U[1, 16] per head."""
     import torch
     gen = torch.Generator(device="cuda").manual_seed(seed)
     shp = (B, T, H, D)
@@ -138,7 +147,12 @@ def make_inputs_gpu(B, T, H, D, with_state, seed=0):
     k = l2n(torch.randn(shp, generator=gen, device="cuda"))
     v = torch.randn(shp, generator=gen, device="cuda")
     beta = torch.sigmoid(torch.randn((B, T, H), generator=gen, device="cuda"))
-    g = -torch.nn.functional.softplus(torch.randn(shp, generator=gen, device="cuda")) * 0.1
+    if layer_decay:
+        A = torch.empty(H, device="cuda").uniform_(1.0, 16.0, generator=gen)
+        g = -A[None, None, :, None] * torch.nn.functional.softplus(
+            0.5 * torch.randn(shp, generator=gen, device="cuda"))
+    else:
+        g = -torch.nn.functional.softplus(torch.randn(shp, generator=gen, device="cuda")) * 0.1
     s0 = torch.randn((B, H, D, D), generator=gen, device="cuda") * 0.02 if with_state else None
     do = torch.randn(shp, generator=gen, device="cuda")
     bf = torch.bfloat16
@@ -492,7 +506,7 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb)
-    q, k, v, g, beta, s0, do = make_inputs_gpu(B, T, H, D, with_state)
+    q, k, v, g, beta, s0, do = make_inputs_gpu(B, T, H, D, with_state, layer_decay=args.workload in LAYER_DECAY)
     ws = torch.empty(kda.workspace_bytes(2 if backward else 0, B, T, H, D), dtype=torch.uint8, device="cuda")
 
     def step():

@@ -484,6 +484,8 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
     const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
     const size_t cCD = (size_t)ch * C * D, cDD = (size_t)ch * D * D;
+    // one LDS word for the workgroup's decay flags: a pad column of akk, never data
+    int* flagw = reinterpret_cast<int*>(&sm.akk[0][C]);
 
     // ---------------- phase 0: loads ----------------
     // All loads are issued here, in the order they are needed (q, k, g, beta of
@@ -529,10 +531,13 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             }
         }
         if (tid < C) sm.dbeta[tid] = 0.f;
+        if (tid == 0) *flagw = 0;
     }
     __syncthreads();
     chunk_cumsum2<D, ST, NTH>(s);
-    const int unsafe = chunk_factors2<D, ST, PREC, NTH>(s, flag);
+    const int dfl = chunk_factors2<D, ST, PREC, NTH>(s, flag, flagw);
+    const bool unsafe = (dfl & 16) != 0;           // g > 0 or NaN: every pair pairwise
+    const int pmask = unsafe ? 0 : (dfl & 15);     // diagonal blocks beyond the span guard
     if (tid < C) s.beta[tid] = (tid < valid) ? braw : 0.f;
     tW.store(&sm.W[0][0], LDK);
     tU.store(&sm.U[0][0], LDK);
@@ -542,39 +547,79 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     const bool own = ct < NT;
     const int d = own ? ct * BS + r16 : 0;
     constexpr int MB = NB / 2;
-    float kx[MB][4], qx[MB][4], el[MB][4], er[MB][4], eb[MB][4], erb[MB], eGd;
+    // el = e^{a_t}, er = e^{b_t} (the anchored operand factors), eb = e^{G - gamma_t},
+    // erb = e^{gamma_{16m-1}}, so e^{gamma_t} = erb el; at = a_t and fdm = e^{-T_m}
+    // serve the pairwise diagonal tiles and the diagonal tile factor of phase 4
+    float kx[MB][4], qx[MB][4], el[MB][4], er[MB][4], eb[MB][4], at[MB][4], erb[MB], fdm[MB], eGd;
     {
-        const float G = s.g[C - 1][d];
-        eGd = kexp<PREC>(G);
+        const float Tb[NB] = {s.g[BS - 1][d], s.g[2 * BS - 1][d], s.g[3 * BS - 1][d], s.g[4 * BS - 1][d]};
+        eGd = kexp<PREC>((Tb[0] + Tb[1]) + (Tb[2] + Tb[3]));
 #pragma unroll
         for (int mm = 0; mm < MB; ++mm) {
             const int m = 2 * rh + mm;
-            const float gr = s.g[BS * m][d];
-            erb[mm] = s.er[m][d];
+            erb[mm] = fac_ep(s, m, d);
+            fdm[mm] = s.fac[FAC_FD + m][d];
+            float sfx = 0.f;   // G - gamma_{16m+15}
+#pragma unroll
+            for (int mq = m + 1; mq < NB; ++mq) sfx += Tb[mq];
+            const float eqm = fac_eq(s, m, d);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * m + 4 * g4 + e;
-                const float gt = s.g[t][d];
+                const float a_t = s.g[t][d], b_t = Tb[m] - a_t;
                 kx[mm][e] = ld1<ST>(&s.kr[t][d]);
                 qx[mm][e] = ld1<ST>(&s.ql[t][d]);
-                el[mm][e] = kexp<PREC>(gt - gr);
-                er[mm][e] = unsafe ? 0.f : kexp<PREC>(gr - gt);
-                eb[mm][e] = kexp<PREC>(G - gt);
+                at[mm][e] = a_t;
+                el[mm][e] = kexp<PREC>(a_t);
+                er[mm][e] = unsafe ? 0.f : kexp<PREC>(b_t);
+                eb[mm][e] = unsafe ? kexp<PREC>(b_t + sfx) : er[mm][e] * eqm;
             }
+        }
+    }
+    // Diagonal tiles of the blocks in pmask, from raw k (before the transform
+    // overwrites it): wave w < 4 forms block w's tile with 4-row sub-anchors on
+    // MFMA; blocks in qmask (4-row sub-blocks beyond the guard too) pair by
+    // pair, A_kk[t][s] = sum_d k_t k_s e^{a_t - a_s}, one tile entry per thread
+    // and step.  The other tiles are formed by MFMA below.
+    const int qmask = pmask & (dfl >> 5);
+    if (pmask) {
+        if (w < NB && (((pmask & ~qmask) >> w) & 1)) {
+            f32x4 P, Q;
+            subanchor_tile<D, ST, PREC, false>(s, w, P, Q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * w + 4 * g4 + e, sx = BS * w + r16;
+                sm.akk[t][sx] = (sx < t) ? P[e] : 0.f;
+            }
+        }
+        const int nent = __popc(qmask) * BS * BS;
+        for (int pp = tid; pp < nent; pp += NTH) {
+            const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
+            int blk = 0;
+            for (int mq = qmask, c = 0;; mq &= mq - 1, ++c)
+                if (c == kb) { blk = __ffs(mq) - 1; break; }
+            const int t = BS * blk + e / BS, sx = BS * blk + e % BS;
+            float ak = 0.f;
+            if (sx < t)
+#pragma unroll 2
+                for (int dd = 0; dd < D; ++dd)
+                    ak += ld1<ST>(&s.kr[t][dd]) * (ld1<ST>(&s.kr[sx][dd]) * kexp<PREC>(s.g[t][dd] - s.g[sx][dd]));
+            sm.akk[t][sx] = ak;
         }
     }
     __syncthreads();
     if (!unsafe) {
+        // K_l = K e^{a}, Q_l = Q e^{a}, K_r = K e^{b}, b = T_blk - a
         constexpr int EPV = 16 / (int)sizeof(ST), VPR = D / EPV;
         for (int vv = tid; vv < C * VPR; vv += NTH) {
-            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, r = t & ~(BS - 1);
+            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, te = (t & ~(BS - 1)) + BS - 1;
             const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
             const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
             float okl[EPV], oql[EPV], okr[EPV];
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
-                const float x = s.g[t][c0 + e] - s.g[r][c0 + e];
-                const float e1 = kexp<PREC>(x), e2 = kexp<PREC>(-x);
+                const float x = s.g[t][c0 + e];
+                const float e1 = kexp<PREC>(x), e2 = kexp<PREC>(s.g[te][c0 + e] - x);
                 okl[e] = kv.get(e) * e1;
                 oql[e] = qv.get(e) * e1;
                 okr[e] = kv.get(e) * e2;
@@ -607,13 +652,15 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     // writes, no barrier); waves 4-7 form the off-diagonal tiles; V' is split
     // over all eight waves.
     auto akk_tile = [&](int i, int j) __attribute__((always_inline)) {
+        // B operand: K_r of block j times the tile's channel factor (F_ij, 1
+        // between adjacent blocks, e^{-T_i} on the diagonal), as prep forms it
+        const float* fsc = &s.fac[(j == i) ? FAC_FD + i : (j == i - 1) ? 0 : fac_f_row(i, j)][0];
         f32x4 P = zero4();
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
             const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
-            const Frag8 Bk = (j < i) ? ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
-                                                              &s.f[pair_idx(i, j)][32 * ks])
-                                     : ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks);
+            const Frag8 Bk = (j == i - 1) ? ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
+                                          : ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks, fsc + 32 * ks);
             P = mma<PREC>(Ak, Bk, P);
         }
 #pragma unroll
@@ -656,7 +703,8 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     };
     if (!unsafe) {
         if (w < NB) {
-            akk_tile(w, w);
+            // a diagonal tile of pmask was formed pair by pair before the transform
+            if (!((pmask >> w) & 1)) akk_tile(w, w);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back its own tile
             diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii, FC ? fc : nullptr);
         } else {
@@ -674,19 +722,16 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             sm.akk[BS * i + e / BS][BS * j + (e % BS)] = 0.f;
         }
     } else {
-        // pairwise path: raw k in kr, exact exp(gamma_t - gamma_s), over the
-        // decay band of each row (the band also bounds phase 4's loops)
-        chunk_band<D, NTH>(s, __syncthreads_or(flag));
+        // every pair pairwise (g > 0 or NaN in the chunk): raw k in kr, exact
+        // exp(gamma_t - gamma_s)
         for (int p = tid; p < C * C; p += NTH) {
             const int t = p / C, sx = p - t * C;
-            if (!(sx < t && sx >= s.blo[t])) sm.akk[t][sx] = 0.f;
-        }
-        for (int qq = tid; qq < s.bpre[C]; qq += NTH) {
-            const int t = band_row(s, qq), sx = s.blo[t] + qq - s.bpre[t];
-            if (sx == t) continue;
             float ak = 0.f;
-            for (int dd = 0; dd < D; ++dd)
-                ak += ld1<ST>(&s.kr[t][dd]) * (ld1<ST>(&s.kr[sx][dd]) * kexp<PREC>(s.g[t][dd] - s.g[sx][dd]));
+            if (sx < t)
+#pragma unroll 1
+                for (int dd = 0; dd < D; ++dd)
+                    ak += ld1<ST>(&s.kr[t][dd]) *
+                          (ld1<ST>(&s.kr[sx][dd]) * kexp<PREC>(chunk_gamma(s, t, dd) - chunk_gamma(s, sx, dd)));
             sm.akk[t][sx] = ak;
         }
         __syncthreads();
@@ -918,8 +963,8 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         const int t = tid >> 3, qd = tid & 7;
         float acc = 0.f;
         for (int dd = qd * (D / 8); dd < (qd + 1) * (D / 8); ++dd) {
-            const float egk = unsafe ? ld1<ST>(&s.kr[t][dd]) * kexp<PREC>(s.g[t][dd])
-                                     : ld1<ST>(&s.kl[t][dd]) * s.er[t / BS][dd];
+            const float egk = unsafe ? ld1<ST>(&s.kr[t][dd]) * kexp<PREC>(chunk_gamma(s, t, dd))
+                                     : ld1<ST>(&s.kl[t][dd]) * fac_ep(s, t / BS, dd);
             acc += sm.ra.dR[t][D + dd] * ld1<ST>(&sm.rb.p2.v[t][dd]) + sm.ra.dR[t][dd] * egk;
         }
         acc += __shfl_xor(acc, 1, 64);
@@ -978,8 +1023,9 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints, own rows ----------------
     if (own) {
         if (!unsafe) {
-            // The decay factor f_ij = e^{gamma_16i - gamma_16j} is per channel, so it
-            // scales the accumulated product instead of the B operand.
+            // The tile factor (F_ij between blocks, e^{-T_i} on the diagonal) is per
+            // channel, so it scales the accumulated product instead of the B operand.
+            // Diagonal tiles of blocks in pmask are evaluated pair by pair below.
             auto colfrag = [&](const ST* M, int ld, int row0) __attribute__((always_inline)) {
                 // B[k][n] = M[row0 + k][d] for the lane's k = 4 g4 + 0..3, raw bf16
                 Frag4 f;
@@ -990,12 +1036,12 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm) {
                 const int i = 2 * rh + mm;
-                // rows of block i: dK_l = sum_{j <= i} f_ij dP[i][j] K_r[j], dQ_l likewise with dA
+                // rows of block i: dK_l = sum_{j <= i} F_ij dP[i][j] K_r[j], dQ_l likewise with dA
                 const float bi = s.beta[BS * i + r16];
                 f32x4 dKl = zero4(), dQl = zero4();
 #pragma unroll
                 for (int j = 0; j < NB; ++j) {
-                    if (j > i) continue;
+                    if (j > i || (j == i && ((pmask >> i) & 1))) continue;
                     const Frag4 B = colfrag(&s.kr[0][0], LDK, BS * j);
                     const float4 x = *reinterpret_cast<const float4*>(sdL + (BS * i + r16) * LDL + BS * j + 4 * g4);
                     const float pv[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
@@ -1007,7 +1053,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                             if (4 * g4 + e == r16) Aq.h[e] = 0;
                     }
                     const f32x4 Pq = mma4f<1>(Aq, B, zero4());
-                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
+                    const float fs = (j < i) ? fac_tile(s, i, j, d) : fdm[mm];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         dKl[e] += Pk[e] * fs;
@@ -1028,12 +1074,12 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm) {
                 const int j = 2 * rh + mm;
-                // rows of block j: dK_r = sum_{i >= j} f_ij (dP[i][j]^T K_l[i] + dA[i][j]^T Q_l[i]),
-                // then times e^{gamma_r - gamma}
+                // rows of block j: dK_r = sum_{i >= j} F_ij (dP[i][j]^T K_l[i] + dA[i][j]^T Q_l[i]),
+                // then times e^{b}
                 f32x4 dKr = zero4();
 #pragma unroll
                 for (int i = 0; i < NB; ++i) {
-                    if (i < j) continue;
+                    if (i < j || (i == j && ((pmask >> j) & 1))) continue;
                     float pv[4], av[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -1043,7 +1089,7 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     }
                     f32x4 P = mma4f<1>(frag4_from_f32<1>(pv), colfrag(&s.kl[0][0], LDK, BS * i), zero4());
                     P = mma4f<1>(frag4_from_f32<1>(av), colfrag(&s.ql[0][0], LDK, BS * i), P);
-                    const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
+                    const float fs = (j < i) ? fac_tile(s, i, j, d) : fdm[mm];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) dKr[e] += P[e] * fs;
                 }
@@ -1054,26 +1100,149 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
                     dga[mm][e] -= dKr[e] * ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]);
                 }
             }
+            // Diagonal tiles of own blocks in pmask & ~qmask, with the 4-row
+            // sub-anchors of subanchor_tile: pair (t, s), t in sub-block p, s in
+            // sub-block q <= p, splits as e^{a_t - a_{r_p}} * e^{a_{r_p} - a_s}.
+            // Everything comes from the lane's own rows (row 16 m + 4 g + e of
+            // channel d is register e of lane (g, d)), plus the anchors a_{r_p},
+            // rows 4 p - 1 of the block, from lanes (p - 1, d).
+            //   A_t = bf16(K_t e^{a_t - a_{r_g}}), Aq_t likewise with Q: the row
+            //     factor of the lane's rows;
+            //   B^p_s = bf16(K_s e^{a_{r_p} - a_s}) for p >= g (0 for p < g).
+            // Row side, pass p: rows t of sub-block p (dP / dA masked to them)
+            // against B^p; a lane's rows come from pass p = g.  Column side, pass
+            // p: dP^T / dA^T against A / Aq of rows t in sub-block p (the lanes
+            // g == p), combined with B^p of the lane's own rows.  Each pair's two
+            // dgamma terms multiply the same bf16 A_t and B^p_s, so they cancel
+            // exactly in the reverse cumsum.
+#pragma unroll
+            for (int mm = 0; mm < MB; ++mm) {
+                const int m = 2 * rh + mm;
+                if (!(((pmask & ~qmask) >> m) & 1)) continue;
+                float arp[NB];
+                arp[0] = 0.f;
+#pragma unroll
+                for (int p = 1; p < NB; ++p) arp[p] = __shfl(at[mm][3], 16 * (p - 1) + r16, 64);
+                const float arg = (g4 == 0) ? arp[0] : (g4 == 1) ? arp[1] : (g4 == 2) ? arp[2] : arp[3];
+                float eo[4], av[4], aqv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    eo[e] = kexp<PREC>(at[mm][e] - arg);
+                    av[e] = bf2f(f2bf(kx[mm][e] * eo[e]));
+                    aqv[e] = bf2f(f2bf(qx[mm][e] * eo[e]));
+                }
+                const Frag4 Ak = frag4_from_f32<1>(av), Aq = frag4_from_f32<1>(aqv);
+                // row-side A operands (rows t = 16 m + r16) and column-side A
+                // operands (rows s = 16 m + r16, k = t = 16 m + 4 g + e)
+                const float bi = s.beta[BS * m + r16];
+                const float4 x = *reinterpret_cast<const float4*>(sdL + (BS * m + r16) * LDL + BS * m + 4 * g4);
+                const float pr[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
+                Frag4 Ar = frag4_from_f32<1>(pr), Aqr = ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * m, BS * m);
+                float pc[4], ac[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = BS * m + 4 * g4 + e;
+                    if (4 * g4 + e == r16) Aqr.h[e] = 0;   // the diagonal pairs are added apart, below
+                    pc[e] = s.beta[t] * sdL[t * LDL + BS * m + r16];
+                    ac[e] = (4 * g4 + e == r16) ? 0.f : ld1<ST>(&sm.dA[t][BS * m + r16]);
+                }
+                const Frag4 Ac = frag4_from_f32<1>(pc), Aqc = frag4_from_f32<1>(ac);
+                const Frag4 z4{short4v{0, 0, 0, 0}, short4v{0, 0, 0, 0}};
+                f32x4 rk = zero4(), rq = zero4();
+                float ck[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int p = 0; p < NB; ++p) {
+                    float f[4], bv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        f[e] = (p >= g4) ? kexp<PREC>(arp[p] - at[mm][e]) : 0.f;
+                        bv[e] = bf2f(f2bf(kx[mm][e] * f[e]));
+                    }
+                    const Frag4 Bp = frag4_from_f32<1>(bv);
+                    const bool rowp = (r16 >> 2) == p, colp = g4 == p;
+                    rk = mma4f<1>(rowp ? Ar : z4, Bp, rk);
+                    rq = mma4f<1>(rowp ? Aqr : z4, Bp, rq);
+                    f32x4 c = mma4f<1>(Ac, colp ? Ak : z4, zero4());
+                    c = mma4f<1>(Aqc, colp ? Aq : z4, c);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ck[e] += c[e] * f[e];
+                        cg[e] += c[e] * bv[e];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dka[mm][e] += rk[e] * eo[e] + ck[e];
+                    dqa[mm][e] += rq[e] * eo[e];
+                    dga[mm][e] += rk[e] * av[e] + rq[e] * aqv[e] - cg[e];
+                }
+            }
+            // Diagonal tiles of own blocks in qmask (4-row spans beyond the guard
+            // too), pair by pair with the exact weight e^{a_t - a_s}, from the
+            // raw k, q and a of the block's rows (shuffled from the lanes that own
+            // them).  Row side (s < t) and column side (s > t) of each own row t;
+            // the diagonal s = t is added apart, below.
+#pragma unroll
+            for (int mm = 0; mm < MB; ++mm) {
+                const int m = 2 * rh + mm;
+                if (!((qmask >> m) & 1)) continue;
+                float ak[4] = {0.f, 0.f, 0.f, 0.f}, aq[4] = {0.f, 0.f, 0.f, 0.f}, ag[4] = {0.f, 0.f, 0.f, 0.f};
+                // a rolled loop (rare path, kept compact): the source register is picked by selects
+#pragma unroll 1
+                for (int sq = 0; sq < BS; ++sq) {
+                    const int src = 16 * (sq >> 2) + r16, sr = BS * m + sq, es = sq & 3;
+                    const float kv = (es == 0) ? kx[mm][0] : (es == 1) ? kx[mm][1] : (es == 2) ? kx[mm][2] : kx[mm][3];
+                    const float qv = (es == 0) ? qx[mm][0] : (es == 1) ? qx[mm][1] : (es == 2) ? qx[mm][2] : qx[mm][3];
+                    const float av = (es == 0) ? at[mm][0] : (es == 1) ? at[mm][1] : (es == 2) ? at[mm][2] : at[mm][3];
+                    const float Ks = __shfl(kv, src, 64);
+                    const float Qs = __shfl(qv, src, 64);
+                    const float As = __shfl(av, src, 64);
+                    const float bs = s.beta[sr];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int tr = 4 * g4 + e, t = BS * m + tr;
+                        if (sq < tr) {
+                            const float ks = Ks * kexp<PREC>(at[mm][e] - As);
+                            const float pp = s.beta[t] * sdL[t * LDL + sr], pa = ld1<ST>(&sm.dA[t][sr]);
+                            ak[e] += pp * ks;
+                            aq[e] += pa * ks;
+                            ag[e] += (pp * kx[mm][e] + pa * qx[mm][e]) * ks;
+                        } else if (sq > tr) {
+                            const float pp = bs * sdL[sr * LDL + t], pa = ld1<ST>(&sm.dA[sr][t]);
+                            const float c = (pp * Ks + pa * Qs) * kexp<PREC>(As - at[mm][e]);
+                            ak[e] += c;
+                            ag[e] -= c * kx[mm][e];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dka[mm][e] += ak[e];
+                    dqa[mm][e] += aq[e];
+                    dga[mm][e] += ag[e];
+                }
+            }
         } else {
-            // pairwise path: raw k in kr, raw q in ql, gamma in g.  Row side
-            // (s < t) and column side (s > t) run as two loops over the decay
-            // band, so no iteration carries the other side's masked work.
+            // every pair pairwise (g > 0 or NaN in the chunk): raw k in kr, raw q in
+            // ql, a in g.  Row side (s < t) and column side (s > t) as two loops.
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int t = BS * (2 * rh + mm) + 4 * g4 + e;
-                    const float gt = s.g[t][d], bt = s.beta[t];
+                    const float gt = chunk_gamma(s, t, d), bt = s.beta[t];
                     float ak = 0.f, aq = 0.f, ag = 0.f;
-                    for (int sx = s.blo[t]; sx < t; ++sx) {
-                        const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - s.g[sx][d]);
+#pragma unroll 1
+                    for (int sx = 0; sx < t; ++sx) {
+                        const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(gt - chunk_gamma(s, sx, d));
                         const float pp = bt * sdL[t * LDL + sx], pa = ld1<ST>(&sm.dA[t][sx]);
                         ak += pp * ks;
                         aq += pa * ks;
                         ag += (pp * kx[mm][e] + pa * qx[mm][e]) * ks;
                     }
-                    for (int sx = t + 1; sx <= s.bhi[t]; ++sx) {
-                        const float ex = kexp<PREC>(s.g[sx][d] - gt);
+#pragma unroll 1
+                    for (int sx = t + 1; sx < C; ++sx) {
+                        const float ex = kexp<PREC>(chunk_gamma(s, sx, d) - gt);
                         const float pp = s.beta[sx] * sdL[sx * LDL + t], pa = ld1<ST>(&sm.dA[sx][t]);
                         const float c = (pp * ld1<ST>(&s.kr[sx][d]) + pa * ld1<ST>(&s.ql[sx][d])) * ex;
                         ak += c;

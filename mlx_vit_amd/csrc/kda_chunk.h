@@ -1,8 +1,11 @@
 // kda_chunk.h -- workgroup-level phases shared by the per-chunk kernels
-// (forward prep and backward local adjoints).  One workgroup = 256 threads =
-// 4 waves works on one (batch, head, chunk) of C = 64 tokens.
+// (forward prep and backward local adjoints), which work on one (batch, head,
+// chunk) of C = 64 tokens per workgroup.
 //
-// Anchored decay products.  For rows t, s of one chunk with gamma the in-chunk
+// ChunkLds and its phases serve the fp32 local-adjoint kernel; ChunkSmem (below)
+// the prep and bf16 local-adjoint kernels, with block-end anchoring.
+//
+// Anchored decay products (ChunkLds).  For rows t, s of one chunk with gamma the in-chunk
 // cumulative log-decay, the pair weight exp(gamma_t - gamma_s) (s <= t) is split
 // at the anchor r = 16 * (t / 16), the first row of t's 16-row sub-block:
 //     exp(gamma_t - gamma_r) * exp(gamma_r - gamma_s).
@@ -180,6 +183,24 @@ __device__ void diag_inverse(const float* __restrict__ L, float (*tii)[BS][BS + 
 // ============================================================================
 namespace kda {
 
+// Block-end anchored decay products (the ChunkSmem kernels: prep and the bf16
+// local adjoints).  Rows fall in NB blocks of BS = 16; with gamma the in-chunk
+// cumulative log-decay and gamma_{-1} = 0, block i spans rows 16i .. 16i+15:
+//   a_t = gamma_t - gamma_{16i-1}        in-block inclusive cumsum of g (<= 0)
+//   b_t = gamma_{16i+15} - gamma_t = T_i - a_t,  T_i = a_{16i+15}  (<= 0)
+// For s in block j < i, t in block i the pair weight splits into factors that
+// are all <= 1, whatever the decay:
+//   e^{gamma_t - gamma_s} = e^{a_t} * F_ij * e^{b_s},   F_ij = e^{T_{j+1} + ... + T_{i-1}}
+// so K_l = K e^{a} and Q_l = Q e^{a} are the row operands, K_r = K e^{b} the
+// column operand, and F_ij (1 for adjacent blocks) scales the product per
+// channel.  On the diagonal tile (s, t in block i) the weight is
+// e^{a_t} e^{-T_i} e^{b_s}: the factor e^{-T_i} >= 1 is the block's decay
+// span, kept when span_i = -T_i <= SPAN_MAX; a block with a larger span has its
+// diagonal tile evaluated pair by pair, e^{a_t - a_s}, and only that tile.
+// Every exponent is a sum of in-block cumsums and block totals, so its fp32
+// error scales with one block's span, not with the chunk's whole decay.
+// A chunk with g > 0 or a NaN anywhere (outside the layer's domain, where the
+// factors could exceed 1) is evaluated entirely pair by pair.
 template <int D, typename ST>
 struct ChunkSmem {
     // fp32 storage at D = 128 drops the row pad to fit in 160 KB
@@ -187,26 +208,39 @@ struct ChunkSmem {
     static constexpr int PS = TIGHT ? 0 : 16 / (int)sizeof(ST);
     static constexpr int LDK = D + PS;     // ST rows
     static constexpr int LDG = D + (TIGHT ? 0 : 4);   // fp32 rows
-    ST kl[C][LDK];     // k e^{g_t - g_r}
-    ST ql[C][LDK];     // raw q, then q e^{g_t - g_r}
-    ST kr[C][LDK];     // raw k, then k e^{g_r - g_t} (anchored path)
-    float g[C][LDG];   // raw g, then gamma
+    ST kl[C][LDK];     // k e^{a_t}
+    ST ql[C][LDK];     // raw q, then q e^{a_t}
+    ST kr[C][LDK];     // raw k, then k e^{b_t} (anchored chunks)
+    float g[C][LDG];   // raw g, then a (in-block inclusive cumsum)
     union {
-        struct {
-            float er[NB][D];    // e^{gamma_16j}
-            float egr[NB][D];   // e^{G - gamma_16j}
-            float f[6][D];      // e^{gamma_16i - gamma_16j}, j < i
-        };
-        struct {                // pairwise path only, where egr and f are not used;
-            float er_keep[NB][D];   // written after the factor tables
-            float bw[C];            // slowest-channel decay cumsum
-            uint16_t bpre[C + 1];   // band-width prefix sums (< 2081)
-            uint8_t blo[C], bhi[C]; // decay band of each row
-        };
-        float tmp[512];
+        float fac[14][D];   // factor tables, rows FAC_* below
+        float tmp[512];     // cumsum partials; dead before fac is written
     };
     float beta[C];
 };
+
+// rows of ChunkSmem::fac, per channel
+constexpr int FAC_EP = 0;   // + i - 1, i = 1..3: e^{gamma_{16i-1}} = e^{T_0 + .. + T_{i-1}}
+constexpr int FAC_EQ = 3;   // + j, j = 0..2:     e^{G - gamma_{16j+15}} = e^{T_{j+1} + .. + T_3}
+constexpr int FAC_F = 6;    // (2,0), (3,1), (3,0): F_ij for non-adjacent blocks
+constexpr int FAC_FD = 9;   // + i, i = 0..3:     e^{min(-T_i, SPAN_MAX)}
+// e^{gamma_{16i-1}}: e^{gamma} at the end of the block before i (1 for i = 0)
+template <int D, typename ST>
+__device__ __forceinline__ float fac_ep(const ChunkSmem<D, ST>& s, int i, int d) {
+    return i == 0 ? 1.f : s.fac[FAC_EP + i - 1][d];
+}
+// e^{G - gamma_{16j+15}}: the decay from the end of block j to the chunk end (1 for j = 3)
+template <int D, typename ST>
+__device__ __forceinline__ float fac_eq(const ChunkSmem<D, ST>& s, int j, int d) {
+    return j == NB - 1 ? 1.f : s.fac[FAC_EQ + j][d];
+}
+// row of F_ij, j < i - 1 (adjacent blocks have F = 1 and no row)
+__device__ __forceinline__ int fac_f_row(int i, int j) { return FAC_F + ((i == 2) ? 0 : (j == 1) ? 1 : 2); }
+// the per-channel factor of tile (i, j), j <= i: F_ij, or e^{-T_i} on the diagonal
+template <int D, typename ST>
+__device__ __forceinline__ float fac_tile(const ChunkSmem<D, ST>& s, int i, int j, int d) {
+    return (j == i) ? s.fac[FAC_FD + i][d] : (j == i - 1) ? 1.f : s.fac[fac_f_row(i, j)][d];
+}
 
 // All 16-byte loads of one chunk of q, k, g, beta (and optionally v) are issued
 // before anything is written to LDS; every wave's q, k, g, beta requests enter
@@ -250,47 +284,149 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& 
     return flag;
 }
 
+// In place: g -> a, the inclusive cumsum of g inside each 16-row block.
+// NTH threads, NTH / D parts of RP rows per channel; parts shorter than a
+// block add the totals of the earlier parts of their block.
 template <int D, typename ST, int NTH = 256>
 __device__ __forceinline__ void chunk_cumsum2(ChunkSmem<D, ST>& s) {
     constexpr int PARTS = NTH / D, RP = C / PARTS;
     static_assert(PARTS * D <= 512, "cumsum partials fit tmp");
+    static_assert(RP % BS == 0 || BS % RP == 0, "parts align with blocks");
     const int tid = threadIdx.x, d = tid % D, p = tid / D;
     float run = 0.f;
 #pragma unroll
     for (int r = 0; r < RP; ++r) {
+        if (r % BS == 0) run = 0.f;
         run += s.g[p * RP + r][d];
         s.g[p * RP + r][d] = run;
     }
-    s.tmp[p * D + d] = run;
-    __syncthreads();
-    float off = 0.f;
-    for (int pp = 0; pp < p; ++pp) off += s.tmp[pp * D + d];
-    if (p > 0) {
+    if constexpr (RP < BS) {
+        constexpr int PPB = BS / RP;   // parts per block
+        s.tmp[p * D + d] = run;
+        __syncthreads();
+        float off = 0.f;
+        for (int pp = p - p % PPB; pp < p; ++pp) off += s.tmp[pp * D + d];
+        if (p % PPB) {
 #pragma unroll
-        for (int r = 0; r < RP; ++r) s.g[p * RP + r][d] += off;
+            for (int r = 0; r < RP; ++r) s.g[p * RP + r][d] += off;
+        }
     }
     __syncthreads();
 }
 
-// factor tables + span guard; returns nonzero (uniform) for the pairwise path
+// OR of x over the workgroup through one LDS word (*w, zeroed by the caller
+// before an earlier barrier).  Ends with a barrier.  The result is returned
+// through readfirstlane, so the compiler knows it is uniform and branches on
+// it with scalar branches.
+template <int NTH>
+__device__ __forceinline__ int block_or(int x, int* w) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x |= __shfl_xor(x, o);
+    if ((threadIdx.x & 63) == 0 && x) atomicOr(w, x);
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(*w);
+}
+
+// Factor tables and the decay flags, from a (the in-block cumsums) and the
+// load's g > 0 / NaN flag.  Returns, uniform over the workgroup, bit 4 set when
+// the chunk must be evaluated pair by pair (g > 0 or NaN), bit i (0..3) set
+// when diagonal block i's span exceeds SPAN_MAX, and bit 5 + i set when one of
+// that block's 4-row sub-blocks does too (see subanchor_tile).  flagw: one
+// zeroed LDS word.
 template <int D, typename ST, int PREC, int NTH = 256>
-__device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag) {
-    const int tid = threadIdx.x;
-    for (int idx = tid; idx < NB * D; idx += NTH) {
-        const int j = idx / D, d = idx % D;
-        const float g0 = s.g[BS * j][d];
-        const float span = g0 - s.g[BS * j + BS - 1][d];
-        if (!(span <= SPAN_MAX)) flag = 1;
-        s.er[j][d] = kexp<PREC>(g0);
-        s.egr[j][d] = kexp<PREC>(s.g[C - 1][d] - g0);
+__device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag, int* flagw) {
+    constexpr int TPC = NTH / D;   // threads per channel
+    static_assert(TPC >= 1 && NTH % D == 0, "whole channels per workgroup");
+    const int tid = threadIdx.x, d = tid % D, r = tid / D;
+    int m = flag ? 16 : 0;
+    // the channel's four block totals, read together
+    const float T0 = s.g[BS - 1][d], T1 = s.g[2 * BS - 1][d], T2 = s.g[3 * BS - 1][d], T3 = s.g[4 * BS - 1][d];
+    const float T12 = T1 + T2;
+    // table rows r, r + TPC, ...: exponents are sums of block totals (FAC_*)
+    for (int row = r; row < 13; row += TPC) {
+        const float x = (row == 0) ? T0 : (row == 1) ? T0 + T1 : (row == 2) ? (T0 + T1) + T2
+                      : (row == 3) ? T1 + (T2 + T3) : (row == 4) ? T2 + T3 : (row == 5) ? T3
+                      : (row == 6) ? T1 : (row == 7) ? T2 : (row == 8) ? T12
+                      : fminf(-((row == 9) ? T0 : (row == 10) ? T1 : (row == 11) ? T2 : T3), SPAN_MAX);
+        s.fac[row][d] = kexp<PREC>(x);
     }
-    for (int idx = tid; idx < 6 * D; idx += NTH) {
-        const int p = idx / D, d = idx % D;
-        const int i = (p >= 3) ? 3 : (p >= 1) ? 2 : 1;
-        const int j = p - pair_idx(i, 0);
-        s.f[p][d] = kexp<PREC>(s.g[BS * i][d] - s.g[BS * j][d]);
+    // span guards of blocks r, r + TPC, ...: the whole block and its 4-row sub-blocks
+    for (int i = r; i < NB; i += TPC) {
+        const float T = (i == 0) ? T0 : (i == 1) ? T1 : (i == 2) ? T2 : T3;
+        if (!(-T <= SPAN_MAX)) m |= 1 << i;
+        const float c0 = s.g[BS * i + 3][d], c1 = s.g[BS * i + 7][d], c2 = s.g[BS * i + 11][d];
+        if (!(-c0 <= SUB_SPAN_MAX) || !(c0 - c1 <= SUB_SPAN_MAX) || !(c1 - c2 <= SUB_SPAN_MAX) ||
+            !(c2 - T <= SUB_SPAN_MAX))
+            m |= 32 << i;
     }
-    return __syncthreads_or(flag);
+    return block_or<NTH>(m, flagw);
+}
+
+// The diagonal tile (i, i) of K K^T . e^{a_t - a_s} (and, with WITH_Q, of
+// Q K^T . e^{a_t - a_s}) for a block whose 16-row span exceeds SPAN_MAX, from
+// the raw rows of k (kr) and q (ql) and a, by one wave, before the transform.
+// Anchors r_p = 16 i + 4 p - 1 (a_{16i-1} = 0) split the block into 4-row
+// sub-blocks; pass p multiplies rows t of sub-block p, K_t e^{a_t - a_{r_p}}
+// (<= 1), with rows s of sub-blocks <= p, K_s e^{a_{r_p} - a_s} (<= 1 before
+// sub-block p, <= e^{4-row span} inside it), and the four passes accumulate
+// into one tile (a pass contributes only to its own rows).  Valid when every
+// 4-row span is <= SPAN_MAX.  Lane (g, n) holds rows 4 g .. 4 g + 3, column n
+// of the tile; entries above the diagonal are not masked.
+template <int D, typename ST, int PREC, bool WITH_Q>
+__device__ __forceinline__ void subanchor_tile(const ChunkSmem<D, ST>& s, int i, f32x4& P, f32x4& Q) {
+    const int l = lane_id(), r16 = l & 15, g4 = l >> 4, q = r16 >> 2;
+    const int row = BS * i + r16;
+    P = zero4();
+    Q = zero4();
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        float kv[8], qv[8], av[8], ar[NB][8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c = 32 * ks + 16 * h + 4 * g4;
+            const float4 k4 = ld4<ST>(&s.kr[row][c]), q4 = ld4<ST>(&s.ql[row][c]);
+            const float4 a4 = *reinterpret_cast<const float4*>(&s.g[row][c]);
+            kv[4 * h] = k4.x; kv[4 * h + 1] = k4.y; kv[4 * h + 2] = k4.z; kv[4 * h + 3] = k4.w;
+            qv[4 * h] = q4.x; qv[4 * h + 1] = q4.y; qv[4 * h + 2] = q4.z; qv[4 * h + 3] = q4.w;
+            av[4 * h] = a4.x; av[4 * h + 1] = a4.y; av[4 * h + 2] = a4.z; av[4 * h + 3] = a4.w;
+#pragma unroll
+            for (int p = 0; p < NB; ++p) {
+                const float4 r4 = p ? *reinterpret_cast<const float4*>(&s.g[BS * i + 4 * p - 1][c])
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                ar[p][4 * h] = r4.x; ar[p][4 * h + 1] = r4.y; ar[p][4 * h + 2] = r4.z; ar[p][4 * h + 3] = r4.w;
+            }
+        }
+        float ea[8];   // e^{a_t - a_{r_q}}, the lane's row in its own sub-block q
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float arq = (q == 0) ? ar[0][e] : (q == 1) ? ar[1][e] : (q == 2) ? ar[2][e] : ar[3][e];
+            ea[e] = kexp<PREC>(av[e] - arq);
+        }
+#pragma unroll
+        for (int p = 0; p < NB; ++p) {
+            float aa[8], aq[8], bb[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                aa[e] = (q == p) ? kv[e] * ea[e] : 0.f;
+                aq[e] = (q == p) ? qv[e] * ea[e] : 0.f;
+                bb[e] = (q <= p) ? kv[e] * kexp<PREC>(ar[p][e] - av[e]) : 0.f;
+            }
+            const Frag8 B = frag_from_f32<PREC>(bb);
+            P = mma<PREC>(frag_from_f32<PREC>(aa), B, P);
+            if constexpr (WITH_Q) Q = mma<PREC>(frag_from_f32<PREC>(aq), B, Q);
+        }
+    }
+}
+
+// gamma_t of row t, channel d, from a (any chunk): a_t plus the totals of the
+// blocks before t's
+template <int D, typename ST>
+__device__ __forceinline__ float chunk_gamma(const ChunkSmem<D, ST>& s, int t, int d) {
+    float x = s.g[t][d];
+    if (t >= BS) x += s.g[BS - 1][d];
+    if (t >= 2 * BS) x += s.g[2 * BS - 1][d];
+    if (t >= 3 * BS) x += s.g[3 * BS - 1][d];
+    return x;
 }
 
 // Register-resident inverses of the four 16x16 diagonal blocks of I + L,

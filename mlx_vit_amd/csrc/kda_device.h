@@ -35,6 +35,9 @@ constexpr int C = 64;       // chunk length (tokens)
 constexpr int BS = 16;      // sub-block edge = MFMA tile edge
 constexpr int NB = C / BS;  // sub-blocks per chunk
 constexpr float SPAN_MAX = 60.0f;  // largest in-block decay span the anchored MFMA path accepts
+// largest 4-row decay span the sub-anchored diagonal tiles accept: their
+// operands reach e^{span} |k|, e^80 |k| staying far inside the fp32 / bf16 range
+constexpr float SUB_SPAN_MAX = 80.0f;
 
 // ----------------------------------------------------------------------------
 // scalar conversions (bf16 is carried as raw uint16_t bits)

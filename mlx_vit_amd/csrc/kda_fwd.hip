@@ -20,9 +20,13 @@ namespace kda {
 //
 // Phases (barriers between them):
 //   load      all 16-byte loads of q, k, g (and v) issued first, then LDS
-//   cumsum    gamma; factor tables; span guard (uniform anchored / pairwise)
-//   pass A    row-major threads (t, 8 channels): anchored operands kl, ql, kr
-//             in place; Qp (forward) / Kb (backward) as 16-byte stores
+//   cumsum    a (in-block cumsums of g); factor tables; decay flags: the
+//             chunk's g > 0 / NaN, the diagonal blocks beyond the span guard
+//   diagonal  those blocks' diagonal tiles from raw q, k: 4-row sub-anchors on
+//             MFMA, or pair by pair beyond the 4-row guard too (every pair for
+//             a chunk with g > 0)
+//   pass A    row-major threads (t, 8 channels): block-end anchored operands
+//             kl, ql, kr in place; Qp (forward) / Kb (backward) as 16-byte stores
 //   pass B    column threads (d, 8 tokens): KbT, QpT as 16-byte stores
 //   products  Akk -> fp32 LDS, Aqk -> LDS staging -> coalesced stores
 //   inverse   diagonal 16x16 blocks of I + L in registers
@@ -83,34 +87,40 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
     };
 
+    // one LDS word for the workgroup's decay flags: a pad column of sa, never data
+    int* flagw = reinterpret_cast<int*>(&sa[0][C]);
+    if (tid == 0) *flagw = 0;
     // PHASE 0 (load); v stays in registers until the column pass is done
     Tile<ST, C, D> tv;
     const int flag = chunk_load2<D, ST, TG, G::STAGE_V>(s, tv, q, k, v, g, beta, base, rs, bbase, a.H, valid);
     // PHASE 1
     chunk_cumsum2<D, ST>(s);
-    const int unsafe = chunk_factors2<D, ST, PREC>(s, flag);
-    if (a.eG && tid < D) a.eG[(size_t)ch * D + tid] = kexp<PREC>(s.g[C - 1][tid]);
+    const int dfl = chunk_factors2<D, ST, PREC>(s, flag, flagw);
+    const bool unsafe = (dfl & 16) != 0;           // g > 0 or NaN: every pair pairwise
+    const int pmask = unsafe ? 0 : (dfl & 15);     // diagonal blocks beyond the span guard
+    if (a.eG && tid < D) {
+        const float G = (s.g[BS - 1][tid] + s.g[2 * BS - 1][tid]) + (s.g[3 * BS - 1][tid] + s.g[C - 1][tid]);
+        a.eG[(size_t)ch * D + tid] = kexp<PREC>(G);
+    }
     // PHASE 2
 
+    // A_qk of the pairwise diagonal-tile entries this thread owns: kept in
+    // registers until the tile is staged (the staging buffer may be the g region)
+    constexpr int NPW = NB * BS * BS / 256;
+    float paq[NPW], saq[4];
+    const int qmask = pmask & (dfl >> 5);           // ... whose 4-row sub-blocks also exceed it
     if (unsafe) {
-        // pairwise path: raw q in ql, raw k in kr, exact exp(gamma_t - gamma_s),
-        // over the decay band of each row only (pairs outside it are zero)
-        chunk_band<D, 256>(s, __syncthreads_or(flag));
+        // every pair s <= t from raw q (ql), raw k (kr), exact exp(gamma_t - gamma_s)
         for (int p = tid; p < C * C; p += 256) {
             const int t = p / C, sx = p - t * C;
-            if (sx <= t && sx >= s.blo[t]) continue;
-            sa[t][sx] = 0.f;
-            if (a.Akk) a.Akk[cCC + (size_t)t * C + sx] = 0.f;
-            if (oAqk) st1<ST>(oAqk + cCC + (size_t)t * C + sx, 0.f);
-            if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, 0.f);
-        }
-        for (int qq = tid; qq < s.bpre[C]; qq += 256) {
-            const int t = band_row(s, qq), sx = s.blo[t] + qq - s.bpre[t];
             float ak = 0.f, aq = 0.f;
-            for (int d = 0; d < D; ++d) {
-                const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(s.g[t][d] - s.g[sx][d]);
-                ak += ld1<ST>(&s.kr[t][d]) * ks;
-                aq += ld1<ST>(&s.ql[t][d]) * ks;
+            if (sx <= t) {
+#pragma unroll 1
+                for (int d = 0; d < D; ++d) {
+                    const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(chunk_gamma(s, t, d) - chunk_gamma(s, sx, d));
+                    ak += ld1<ST>(&s.kr[t][d]) * ks;
+                    aq += ld1<ST>(&s.ql[t][d]) * ks;
+                }
             }
             const float akk = (sx < t) ? ak : 0.f;
             sa[t][sx] = akk;
@@ -119,30 +129,85 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, aq);
         }
         __syncthreads();
+    } else if (pmask) {
+        // Diagonal tiles of the blocks in pmask, from raw q, k (pass A overwrites
+        // them).  Wave w forms block w's tile with 4-row sub-anchors on MFMA;
+        // blocks whose 4-row sub-blocks also exceed the guard (qmask) are
+        // evaluated one entry (t, s) per thread and step, e^{a_t - a_s}.  A_kk
+        // goes to sa now (its tile is not formed below), A_qk^T to its output;
+        // A_qk stays in registers until its tile is staged.
+        if (((pmask & ~qmask) >> w) & 1) {
+            f32x4 P, Q;
+            subanchor_tile<D, ST, PREC, true>(s, w, P, Q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * w + 4 * g4 + e, sx = BS * w + r16;
+                sa[t][sx] = (sx < t) ? P[e] : 0.f;
+                saq[e] = (sx <= t) ? Q[e] : 0.f;
+            }
+            if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * w + r16) * C + BS * w + 4 * g4, saq);
+        }
+        if (qmask) {
+            const int nent = __popc(qmask) * BS * BS;
+#pragma unroll
+            for (int it = 0; it < NPW; ++it) {
+                const int pp = tid + 256 * it;
+                paq[it] = 0.f;
+                if (pp < nent) {
+                    const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
+                    int blk = 0;
+                    for (int m = qmask, c = 0;; m &= m - 1, ++c)
+                        if (c == kb) { blk = __ffs(m) - 1; break; }
+                    const int t = BS * blk + e / BS, sx = BS * blk + e % BS;
+                    float ak = 0.f, aq = 0.f;
+                    if (sx <= t) {
+#pragma unroll 2
+                        for (int d = 0; d < D; ++d) {
+                            const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(s.g[t][d] - s.g[sx][d]);
+                            ak += ld1<ST>(&s.kr[t][d]) * ks;
+                            aq += ld1<ST>(&s.ql[t][d]) * ks;
+                        }
+                    }
+                    sa[t][sx] = (sx < t) ? ak : 0.f;
+                    paq[it] = aq;
+                    if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, aq);
+                }
+            }
+        }
+        __syncthreads();   // raw q, k are read above and overwritten by pass A
     }
 
-    // pass A: row threads (t, EPV channels)
+    // pass A: row threads (t, EPV channels).  K_l = K e^{a}, Q_l = Q e^{a},
+    // K_r = K e^{b} (anchored chunks; raw K otherwise), Qp = Q_l e^{gamma_{16i-1}},
+    // Kb = K_r e^{G - gamma_{16i+15}}
     {
         constexpr int VPR = D / EPV, NV = C * VPR;
         for (int vv = tid; vv < NV; vv += 256) {
-            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, r = t & ~(BS - 1), blk = t / BS;
+            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, blk = t / BS;
             const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
             const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
             float okl[EPV], oql[EPV], okr[EPV], oqp[EPV], okb[EPV];
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
                 const int d = c0 + e;
-                const float gt = s.g[t][d], x = gt - s.g[r][d];
-                const float el = kexp<PREC>(x);
+                const float at = s.g[t][d], bt = s.g[BS * blk + BS - 1][d] - at;
+                const float el = kexp<PREC>(at);
                 const float qf = qv.get(e), kf = kv.get(e);
-                // anchored path: e^{G - gamma_t} = e^{gamma_r - gamma_t} e^{G - gamma_r}, the
-                // second factor from the table (one exponential fewer per element)
-                const float erx = unsafe ? 1.f : kexp<PREC>(-x);
                 okl[e] = kf * el;
                 oql[e] = qf * el;
-                okr[e] = kf * erx;
-                oqp[e] = oql[e] * s.er[blk][d];
-                okb[e] = bwd ? (unsafe ? kf * kexp<PREC>(s.g[C - 1][d] - gt) : okr[e] * s.egr[blk][d]) : 0.f;
+                okr[e] = unsafe ? kf : kf * kexp<PREC>(bt);
+                oqp[e] = oql[e] * fac_ep(s, blk, d);
+                if (bwd) {
+                    if (unsafe) {
+                        float gsfx = bt;   // G - gamma_t
+                        for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];
+                        okb[e] = kf * kexp<PREC>(gsfx);
+                    } else {
+                        okb[e] = okr[e] * fac_eq(s, blk, d);
+                    }
+                } else {
+                    okb[e] = 0.f;
+                }
             }
             store_vec<ST>(&s.kl[t][c0], okl);
             store_vec<ST>(&s.ql[t][c0], oql);
@@ -154,12 +219,12 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     __syncthreads();
     // PHASE 3
 
-    // pass B: the transposed copies KbT = (Kr diag(e^{G - gamma_r}))^T and
-    // QpT = (Ql diag(e^{gamma_r}))^T.  Anchored path, bf16: per 16 x 16 tile
-    // (token block i, channel block j) one MFMA forms X diag(s), which leaves
+    // pass B: the transposed copies KbT = (K_r diag(e^{G - gamma_{16i+15}}))^T and
+    // QpT = (Q_l diag(e^{gamma_{16i-1}}))^T.  Anchored chunks, bf16: per 16 x 16
+    // tile (token block i, channel block j) one MFMA forms X diag(s), which leaves
     // channel d of the tile in lane d % 16 with four consecutive tokens per lane
     // -- the transposed layout -- written as 8-byte pieces of KbT / QpT rows.
-    // X = Kr or Ql is exact in bf16; the scale s is split into bf16 hi + lo
+    // X = K_r or Q_l is exact in bf16; the scale s is split into bf16 hi + lo
     // halves of one K = 32 step, so the product keeps fp32 accuracy until the
     // final rounding.
     if (std::is_same<ST, uint16_t>::value && !unsafe) {
@@ -176,7 +241,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             for (int it = 0; it < NT; ++it) {
                 const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
                 A[it] = ldfrag4<1, ST>(X, LDK, BS * i, BS * j);
-                sv[it] = o ? s.er[i][BS * j + r16] : s.egr[i][BS * j + r16];
+                sv[it] = o ? fac_ep(s, i, BS * j + r16) : fac_eq(s, i, BS * j + r16);
             }
 #pragma unroll
             for (int it = 0; it < NT; ++it) {
@@ -205,8 +270,14 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             for (int e = 0; e < EPV; ++e) {
                 const int t = tb + e, blk = t / BS;
                 const float kr = ld1<ST>(&s.kr[t][d]);
-                okb[e] = unsafe ? kr * kexp<PREC>(s.g[C - 1][d] - s.g[t][d]) : kr * s.egr[blk][d];
-                oqp[e] = ld1<ST>(&s.ql[t][d]) * s.er[blk][d];
+                if (unsafe) {
+                    float gsfx = s.g[BS * blk + BS - 1][d] - s.g[t][d];   // G - gamma_t
+                    for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];
+                    okb[e] = kr * kexp<PREC>(gsfx);
+                } else {
+                    okb[e] = kr * fac_eq(s, blk, d);
+                }
+                oqp[e] = ld1<ST>(&s.ql[t][d]) * fac_ep(s, blk, d);
             }
             if (oKbT) store_vec<ST>(oKbT + cCD + (size_t)d * C + tb, okb);
             if (oQpT) store_vec<ST>(oQpT + cCD + (size_t)d * C + tb, oqp);
@@ -221,18 +292,23 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     // elements)
     ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];
     if (!unsafe) {
-        // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared
+        // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared: K_r of
+        // block j times the tile's channel factor (F_ij, 1 between adjacent
+        // blocks, e^{-T_i} on the diagonal).  Diagonal tiles of blocks in pmask
+        // were formed pair by pair.
         for (int tix = w; tix < 10; tix += 4) {
             int i, j;
             tile_ij(tix, i, j);
+            if (j == i && ((pmask >> i) & 1)) continue;
+            const float* fsc = &s.fac[(j == i) ? FAC_FD + i : (j == i - 1) ? 0 : fac_f_row(i, j)][0];
             f32x4 P = zero4(), Q = zero4();
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
                 const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
                 const Frag8 Aq = ldfrag<PREC, ST>(&s.ql[0][0], LDK, BS * i, 32 * ks);
-                const Frag8 Bk = (j < i) ? ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
-                                                                  &s.f[pair_idx(i, j)][32 * ks])
-                                         : ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks);
+                const Frag8 Bk = (j == i - 1) ? ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
+                                              : ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
+                                                                        fsc + 32 * ks);
                 P = mma<PREC>(Ak, Bk, P);
                 Q = mma<PREC>(Aq, Bk, Q);
             }
@@ -245,6 +321,25 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 if (oAqk) st1<ST>(stA + t * LDT + sx, aq[e]);
             }
             if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, aq);
+        }
+        // the diagonal entries of A_qk formed in phase 2, from registers
+        if (oAqk && (((pmask & ~qmask) >> w) & 1)) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) st1<ST>(stA + (BS * w + 4 * g4 + e) * LDT + BS * w + r16, saq[e]);
+        }
+        if (oAqk && qmask) {
+            const int nent = __popc(qmask) * BS * BS;
+#pragma unroll
+            for (int it = 0; it < NPW; ++it) {
+                const int pp = tid + 256 * it;
+                if (pp < nent) {
+                    const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
+                    int blk = 0;
+                    for (int m = qmask, c = 0;; m &= m - 1, ++c)
+                        if (c == kb) { blk = __ffs(m) - 1; break; }
+                    st1<ST>(stA + (BS * blk + e / BS) * LDT + BS * blk + e % BS, paq[it]);
+                }
+            }
         }
         // strictly upper sub-block tiles are zero
         for (int idx = tid; idx < 6 * BS * BS; idx += 256) {
@@ -303,7 +398,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 float rv = 0.f;
                 if (tok[jj]) {
                     if (isK[jj]) {
-                        rv = s.beta[t] * s.er[i][d] * ld1<ST>(&s.kl[t][d]);
+                        rv = s.beta[t] * fac_ep(s, i, d) * ld1<ST>(&s.kl[t][d]);
                     } else if constexpr (G::STAGE_V) {
                         rv = s.beta[t] * ld1<ST>(&svbuf[t][d]);
                     } else {

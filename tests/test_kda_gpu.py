@@ -242,6 +242,43 @@ def test_bwd_dg_pairwise_strong_decay(g_scale):
     _assert_all(_bwd_errors(x, torch.float32), TOL[torch.float32], f"bwd pairwise strong decay g_scale={g_scale}")
 
 
+def _block_scaled(x, scales):
+    """g scaled per 16-row block of each 64-token chunk (scales[i] for block i), so
+    that some diagonal blocks exceed the anchored span guard and others do not."""
+    T = x["g"].shape[1]
+    f = torch.tensor([scales[(t % 64) // 16] for t in range(T)], dtype=torch.float32)
+    x["g"] = (x["g"].float() * f[None, :, None, None]).to(x["g"].dtype)
+    return x
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("scales", [(12.0, 0.1, 12.0, 0.1), (0.1, 0.1, 0.1, 14.0), (16.0, 16.0, 0.3, 6.0)])
+def test_mixed_span_blocks(dtype, scales):
+    """Per-block decays: 16-row blocks beyond the span guard (their diagonal
+    tiles pair by pair) next to weakly decaying ones (MFMA), with the block-end
+    factors between them spanning hundreds of nats.  Forward and backward."""
+    x = _inputs(2, 200, 2, 64, dtype, seed=31, with_state=True, grad=True, g_scale=1.0)
+    x = _block_scaled(x, scales)
+    x["g"] = x["g"].float()
+    _assert_all(_fwd_errors(x, dtype), TOL[dtype], f"fwd mixed spans {dtype} {scales}")
+    _assert_all(_bwd_errors(x, dtype), TOL[dtype], f"bwd mixed spans {dtype} {scales}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_positive_decay_chunks(dtype):
+    """g > 0 in some chunks (outside the layer's domain, but the op and the
+    reference's step loop accept it): those chunks are evaluated pair by pair
+    from the exact exp(gamma_t - gamma_s); the others stay anchored."""
+    x = _inputs(1, 260, 2, 64, dtype, seed=32, with_state=True, grad=True, g_scale=0.3)
+    g = x["g"].float()
+    gen = torch.Generator().manual_seed(33)
+    g[:, 64:128] = torch.randn(g[:, 64:128].shape, generator=gen) * 0.05     # chunk 1: mixed signs
+    g[:, 200:203] = 0.02                                                      # chunk 3: a few positive rows
+    x["g"] = g
+    _assert_all(_fwd_errors(x, dtype), TOL[dtype], f"fwd positive decay {dtype}")
+    _assert_all(_bwd_errors(x, dtype), TOL[dtype], f"bwd positive decay {dtype}")
+
+
 def test_bwd_parity_bf16_small():
     x = _inputs(2, 300, 4, 64, torch.bfloat16, seed=13, with_state=True, grad=True)
     _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "bwd bf16 small")
