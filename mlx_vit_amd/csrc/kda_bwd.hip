@@ -445,6 +445,19 @@ struct alignas(16) LocalSmem {
     float dbeta[C];
 };
 
+// The chunk's indices and its phase-0 tiles, handed from the kernel to its tail.
+struct Local3Chunk {
+    static constexpr int NPF = 2;   // prefetch lines per thread
+    int tid, w, l, r16, g4, ct, rh, valid;
+    size_t rs, base, bbase;
+    const char* pf[NPF];            // the thread's prefetch line addresses, or null
+};
+template <int D, typename ST>
+struct Local3Tiles {
+    Tile<ST, C, D, 512> W, U, dO, v, dVp;
+    Tile<ST, D, D, 512> h, dh;
+};
+
 // ----------------------------------------------------------------------------
 // local adjoints, bf16 operands, 8 waves (two per SIMD, so each hides the
 // other's latencies).  Wave w owns channel tile ct = w % 4 and row half
@@ -463,81 +476,20 @@ struct alignas(16) LocalSmem {
 // what is already in LDS instead of being read from the workspace.
 // LDS regions and their reuse: the plan above LocalSmem.
 // ----------------------------------------------------------------------------
-template <int D, typename ST, typename TG, int PREC>
-__global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) {
+template <int D, typename ST, typename TG, int PREC, bool STRONG>
+__device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>& sm, float* xg, float* xt,
+                                            char* pfbuf, const Local3Chunk& c, Local3Tiles<D, ST>& tl, float braw,
+                                            int dfl) {
     using L = LocalSmem<D, ST>;
     constexpr int NTH = 512, NT = D / BS, LDK = L::LDK, LDT = L::LDT, LDA = L::LDA, LDR = L::LDR;
-    __shared__ L sm;
-    __shared__ float xg[D];     // dgamma(C-1) partial of the rh = 0 waves
-    __shared__ float xt[D];     // dgamma column totals of the rh = 1 waves
-    __shared__ __align__(16) char pfbuf[256];   // landing bytes of the L2 prefetch
     auto& s = sm.s;
-
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
-              g4 = l >> 4;
+    const int tid = c.tid, w = c.w, l = c.l, r16 = c.r16, g4 = c.g4, ct = c.ct, rh = c.rh, valid = c.valid;
     __builtin_assume(w >= 0 && w < 8);
-    const int ct = w & 3, rh = w >> 2;
-    const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int t0 = n * C, valid = min(C, a.T - t0);
-    const size_t rs = (size_t)a.H * D;
-    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
-    const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
-    const size_t cCD = (size_t)ch * C * D, cDD = (size_t)ch * D * D;
-    // one LDS word for the workgroup's decay flags: a pad column of akk, never data
-    int* flagw = reinterpret_cast<int*>(&sm.akk[0][C]);
-
-    // ---------------- phase 0: loads ----------------
-    // All loads are issued here, in the order they are needed (q, k, g, beta of
-    // all waves first); only q, k, g and beta are waited for before the cumsum.  W, U, h and the phase-1
-    // operands stay in registers (4 per thread per tile) until the cumsum and the
-    // anchored transform are done, so their latency hides behind those phases.
-    int flag = 0;
-    Tile<ST, C, D, NTH> tW, tU, tdo, tv, tdVp;
-    Tile<ST, D, D, NTH> th, tdh;
-    float braw;
-    {
-        Tile<ST, C, D, NTH> tq, tk;
-        Tile<TG, C, D, NTH> tg;
-        tq.load(static_cast<const ST*>(a.q) + base, rs, valid);
-        tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
-        tg.load(static_cast<const TG*>(a.g) + base, rs, valid);
-        braw = ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)min(tid, valid - 1) * a.H);
-        // Every wave's q, k, g, beta requests enter the CU's memory pipeline before
-        // any wave's later tiles, so no wave waits behind another's 80 KB.
-        __builtin_amdgcn_s_barrier();
-        tW.load(static_cast<const ST*>(a.W) + cCD, D);
-        tU.load(static_cast<const ST*>(a.U) + cCD, D);
-        th.load(static_cast<const ST*>(a.h) + cDD, D);
-        tdo.load(static_cast<const ST*>(a.dout) + base, rs, valid);
-        tv.load(static_cast<const ST*>(a.v) + base, rs, valid);
-        tdVp.load(static_cast<const ST*>(a.dVp) + cCD, D);
-        tdh.load(static_cast<const ST*>(a.dh) + cDD, D);
-        tq.store(&s.ql[0][0], LDK);
-        tk.store(&s.kr[0][0], LDK);
-        using TGT = Tile<TG, C, D, NTH>;
-#pragma unroll
-        for (int i = 0; i < TGT::PER; ++i) {
-            const int vv = tid + NTH * i;
-            if (TGT::NV % NTH == 0 || vv < TGT::NV) {
-                const int row = vv / TGT::VPR, c = (vv - row * TGT::VPR) * TGT::EPV;
-                const Vec16<TG> x{tg.get(i)};
-#pragma unroll
-                for (int e = 0; e < TGT::EPV; ++e) {
-                    const float gv = x.get(e);
-                    s.g[row][c + e] = gv;
-                    if (!(gv <= 0.f)) flag = 1;
-                }
-            }
-        }
-        if (tid < C) sm.dbeta[tid] = 0.f;
-        if (tid == 0) *flagw = 0;
-    }
-    __syncthreads();
-    chunk_cumsum2<D, ST, NTH>(s);
-    const int dfl = chunk_factors2<D, ST, PREC, NTH>(s, flag, flagw);
-    const bool unsafe = (dfl & 16) != 0;           // g > 0 or NaN: every pair pairwise
-    const int pmask = unsafe ? 0 : (dfl & 15);     // diagonal blocks beyond the span guard
+    const size_t rs = c.rs, base = c.base, bbase = c.bbase;
+    auto &tW = tl.W, &tU = tl.U, &tdo = tl.dO, &tv = tl.v, &tdVp = tl.dVp;
+    auto &th = tl.h, &tdh = tl.dh;
+    const bool unsafe = STRONG && (dfl & 16) != 0;           // g > 0 or NaN: every pair pairwise
+    const int pmask = (STRONG && !unsafe) ? (dfl & 15) : 0;  // diagonal blocks beyond the span guard
     if (tid < C) s.beta[tid] = (tid < valid) ? braw : 0.f;
     tW.store(&sm.W[0][0], LDK);
     tU.store(&sm.U[0][0], LDK);
@@ -748,37 +700,13 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     }
     __syncthreads();
 
-    // L2 prefetch of the chunk this XCD starts next (chunks a CU count apart go to
-    // one XCD and start about when this one ends): one 4-byte DMA per 128-byte
-    // line of its inputs -- the rows of q, k, v, g, dO and the W, U, dV', h, dh
-    // slabs -- so that its loads hit in L2.  The landing bytes are scratch.
-    if (a.pf_ahead > 0 && ch + a.pf_ahead < (int)gridDim.x) {
-        const int pc = ch + a.pf_ahead, pbh = pc / a.nc, pn = pc - pbh * a.nc;
-        const int pb = pbh / a.H, ph = pbh - pb * a.H, pt0 = pn * C, pvalid = min(C, a.T - pt0);
-        const size_t pbase = ((size_t)pb * a.T + pt0) * rs + (size_t)ph * D;
-        constexpr int LCD = C * D * (int)sizeof(ST) / 128, LDD = D * D * (int)sizeof(ST) / 128;
-        constexpr int NL = 5 * C + 3 * LCD + 2 * LDD;
+    // L2 prefetch of the chunk this XCD starts next: its line addresses were
+    // formed by the kernel (Local3Chunk::pf).  The landing bytes are scratch.
+    {
         const uint32_t m = lds_addr(pfbuf);
 #pragma unroll
-        for (int i = 0; i < (NL + NTH - 1) / NTH; ++i) {
-            const int k = NTH * i + tid;
-            const char* p = nullptr;
-            if (k < 5 * C) {
-                const int ts = k / C, r = k - ts * C;
-                const char* tp = static_cast<const char*>(ts == 0 ? a.q : ts == 1 ? a.k : ts == 2 ? a.v : ts == 3 ? a.dout : a.g);
-                const size_t es = (ts == 4) ? sizeof(TG) : sizeof(ST);
-                if (r < pvalid) p = tp + (pbase + (size_t)r * rs) * es;
-            } else if (k < 5 * C + 3 * LCD) {
-                const int j = k - 5 * C, ts = j / LCD, r = j - ts * LCD;
-                const char* tp = static_cast<const char*>(ts == 0 ? a.W : ts == 1 ? a.U : a.dVp);
-                p = tp + (size_t)pc * C * D * sizeof(ST) + (size_t)r * 128;
-            } else if (k < NL) {
-                const int j = k - 5 * C - 3 * LCD, ts = j / LDD, r = j - ts * LDD;
-                const char* tp = static_cast<const char*>(ts == 0 ? a.h : a.dh);
-                p = tp + (size_t)pc * D * D * sizeof(ST) + (size_t)r * 128;
-            }
-            if (p != nullptr) dma4(p, m);
-        }
+        for (int i = 0; i < Local3Chunk::NPF; ++i)
+            if (c.pf[i] != nullptr) dma4(c.pf[i], m);
     }
     f32x4 dqa[MB], dka[MB], dga[MB], dWt[NB];
     float dgcol = 0.f, part = 0.f;
@@ -1325,6 +1253,127 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         }
     }
     if (tid < valid) st1<ST>(static_cast<ST*>(a.dbeta) + bbase + (size_t)tid * a.H, sm.dbeta[tid]);
+}
+
+// The bf16 local-adjoint kernel: phase 0 (loads), the in-block cumsum and the
+// factor tables, then local3_tail above.
+template <int D, typename ST, typename TG, int PREC>
+__global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) {
+    using L = LocalSmem<D, ST>;
+    constexpr int NTH = 512, LDK = L::LDK;
+    __shared__ L sm;
+    __shared__ float xg[D];     // dgamma(C-1) partial of the rh = 0 waves
+    __shared__ float xt[D];     // dgamma column totals of the rh = 1 waves
+    __shared__ __align__(16) char pfbuf[256];   // landing bytes of the L2 prefetch
+    auto& s = sm.s;
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
+              g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 8);
+    const int ct = w & 3, rh = w >> 2;
+    const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int t0 = n * C, valid = min(C, a.T - t0);
+    const size_t rs = (size_t)a.H * D;
+    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
+    const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
+    const size_t cCD = (size_t)ch * C * D, cDD = (size_t)ch * D * D;
+    // one LDS word for the workgroup's decay flags: a pad column of akk, never data
+    int* flagw = reinterpret_cast<int*>(&sm.akk[0][C]);
+
+    // ---------------- phase 0: loads ----------------
+    // All loads are issued here, in the order they are needed (q, k, g, beta of
+    // all waves first); only q, k, g and beta are waited for before the cumsum.  W, U, h and the phase-1
+    // operands stay in registers (4 per thread per tile) until the cumsum and the
+    // anchored transform are done, so their latency hides behind those phases.
+    int flag = 0;
+    Local3Tiles<D, ST> tl;
+    auto &tW = tl.W, &tU = tl.U, &tdo = tl.dO, &tv = tl.v, &tdVp = tl.dVp;
+    auto &th = tl.h, &tdh = tl.dh;
+    float braw;
+    {
+        Tile<ST, C, D, NTH> tq, tk;
+        Tile<TG, C, D, NTH> tg;
+        tq.load(static_cast<const ST*>(a.q) + base, rs, valid);
+        tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
+        tg.load(static_cast<const TG*>(a.g) + base, rs, valid);
+        braw = ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)min(tid, valid - 1) * a.H);
+        // Every wave's q, k, g, beta requests enter the CU's memory pipeline before
+        // any wave's later tiles, so no wave waits behind another's 80 KB.
+        __builtin_amdgcn_s_barrier();
+        tW.load(static_cast<const ST*>(a.W) + cCD, D);
+        tU.load(static_cast<const ST*>(a.U) + cCD, D);
+        th.load(static_cast<const ST*>(a.h) + cDD, D);
+        tdo.load(static_cast<const ST*>(a.dout) + base, rs, valid);
+        tv.load(static_cast<const ST*>(a.v) + base, rs, valid);
+        tdVp.load(static_cast<const ST*>(a.dVp) + cCD, D);
+        tdh.load(static_cast<const ST*>(a.dh) + cDD, D);
+        tq.store(&s.ql[0][0], LDK);
+        tk.store(&s.kr[0][0], LDK);
+        using TGT = Tile<TG, C, D, NTH>;
+#pragma unroll
+        for (int i = 0; i < TGT::PER; ++i) {
+            const int vv = tid + NTH * i;
+            if (TGT::NV % NTH == 0 || vv < TGT::NV) {
+                const int row = vv / TGT::VPR, c = (vv - row * TGT::VPR) * TGT::EPV;
+                const Vec16<TG> x{tg.get(i)};
+#pragma unroll
+                for (int e = 0; e < TGT::EPV; ++e) {
+                    const float gv = x.get(e);
+                    s.g[row][c + e] = gv;
+                    if (!(gv <= 0.f)) flag = 1;
+                }
+            }
+        }
+        if (tid < C) sm.dbeta[tid] = 0.f;
+        if (tid == 0) *flagw = 0;
+    }
+    __syncthreads();
+    chunk_cumsum2<D, ST, NTH>(s);
+    const int dfl = chunk_factors2<D, ST, PREC, NTH>(s, flag, flagw);
+    // The rest is instantiated twice.  Chunks whose 16-row blocks all stay within
+    // the span guard (every chunk at ordinary decays) run a copy with the
+    // sub-anchored and pairwise code compiled out, so that code shapes neither
+    // that copy's register allocation nor its schedule.
+    Local3Chunk c{tid, w, l, r16, g4, ct, rh, valid, rs, base, bbase, {nullptr, nullptr}};
+    // L2 prefetch of the chunk this XCD starts next (chunks a CU count apart go to
+    // one XCD and start about when this one ends): one 4-byte DMA per 128-byte
+    // line of its inputs -- the rows of q, k, v, g, dO and the W, U, dV', h, dh
+    // slabs -- so that its loads hit in L2.  The addresses are formed here, from
+    // the argument block; the tail issues the DMA once the chunk's own loads are
+    // in.
+    if (a.pf_ahead > 0 && ch + a.pf_ahead < (int)gridDim.x) {
+        const int pc = ch + a.pf_ahead, pbh = pc / a.nc, pn = pc - pbh * a.nc;
+        const int pb = pbh / a.H, ph = pbh - pb * a.H, pt0 = pn * C, pvalid = min(C, a.T - pt0);
+        const size_t pbase = ((size_t)pb * a.T + pt0) * rs + (size_t)ph * D;
+        constexpr int LCD = C * D * (int)sizeof(ST) / 128, LDD = D * D * (int)sizeof(ST) / 128;
+        constexpr int NL = 5 * C + 3 * LCD + 2 * LDD;
+        static_assert((NL + NTH - 1) / NTH <= Local3Chunk::NPF, "prefetch lines per thread");
+#pragma unroll
+        for (int i = 0; i < (NL + NTH - 1) / NTH; ++i) {
+            const int k = NTH * i + tid;
+            const char* p = nullptr;
+            if (k < 5 * C) {
+                const int ts = k / C, r = k - ts * C;
+                const char* tp = static_cast<const char*>(ts == 0 ? a.q : ts == 1 ? a.k : ts == 2 ? a.v : ts == 3 ? a.dout : a.g);
+                const size_t es = (ts == 4) ? sizeof(TG) : sizeof(ST);
+                if (r < pvalid) p = tp + (pbase + (size_t)r * rs) * es;
+            } else if (k < 5 * C + 3 * LCD) {
+                const int j = k - 5 * C, ts = j / LCD, r = j - ts * LCD;
+                const char* tp = static_cast<const char*>(ts == 0 ? a.W : ts == 1 ? a.U : a.dVp);
+                p = tp + (size_t)pc * C * D * sizeof(ST) + (size_t)r * 128;
+            } else if (k < NL) {
+                const int j = k - 5 * C - 3 * LCD, ts = j / LDD, r = j - ts * LDD;
+                const char* tp = static_cast<const char*>(ts == 0 ? a.h : a.dh);
+                p = tp + (size_t)pc * D * D * sizeof(ST) + (size_t)r * 128;
+            }
+            c.pf[i] = p;
+        }
+    }
+    if (__builtin_expect((dfl & 31) != 0, 0))
+        local3_tail<D, ST, TG, PREC, true>(a, sm, xg, xt, pfbuf, c, tl, braw, dfl);
+    else
+        local3_tail<D, ST, TG, PREC, false>(a, sm, xg, xt, pfbuf, c, tl, braw, dfl);
 }
 
 // ----------------------------------------------------------------------------

@@ -96,356 +96,370 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     // PHASE 1
     chunk_cumsum2<D, ST>(s);
     const int dfl = chunk_factors2<D, ST, PREC>(s, flag, flagw);
-    const bool unsafe = (dfl & 16) != 0;           // g > 0 or NaN: every pair pairwise
-    const int pmask = unsafe ? 0 : (dfl & 15);     // diagonal blocks beyond the span guard
-    if (a.eG && tid < D) {
-        const float G = (s.g[BS - 1][tid] + s.g[2 * BS - 1][tid]) + (s.g[3 * BS - 1][tid] + s.g[C - 1][tid]);
-        a.eG[(size_t)ch * D + tid] = kexp<PREC>(G);
-    }
-    // PHASE 2
+    // The rest of the kernel is instantiated twice.  Chunks whose 16-row blocks
+    // all stay within the span guard (every chunk at ordinary decays) run a copy
+    // with the sub-anchored and pairwise code compiled out, so that code shapes
+    // neither the common copy's register allocation nor its schedule.
+    const auto a_Akk = a.Akk;
+    const auto a_Tii = a.Tii;
+    const auto a_eG = a.eG;
+    auto tail = [&](auto strong_c) __attribute__((always_inline)) {
+        constexpr bool STRONG = decltype(strong_c)::value;
+        const bool unsafe = STRONG && (dfl & 16) != 0;           // g > 0 or NaN: every pair pairwise
+        const int pmask = (STRONG && !unsafe) ? (dfl & 15) : 0;  // diagonal blocks beyond the span guard
+        if (a_eG && tid < D) {
+            const float G = (s.g[BS - 1][tid] + s.g[2 * BS - 1][tid]) + (s.g[3 * BS - 1][tid] + s.g[C - 1][tid]);
+            a_eG[(size_t)ch * D + tid] = kexp<PREC>(G);
+        }
+        // PHASE 2
 
-    // A_qk of the pairwise diagonal-tile entries this thread owns: kept in
-    // registers until the tile is staged (the staging buffer may be the g region)
-    constexpr int NPW = NB * BS * BS / 256;
-    float paq[NPW], saq[4];
-    const int qmask = pmask & (dfl >> 5);           // ... whose 4-row sub-blocks also exceed it
-    if (unsafe) {
-        // every pair s <= t from raw q (ql), raw k (kr), exact exp(gamma_t - gamma_s)
-        for (int p = tid; p < C * C; p += 256) {
-            const int t = p / C, sx = p - t * C;
-            float ak = 0.f, aq = 0.f;
-            if (sx <= t) {
+        // A_qk of the pairwise diagonal-tile entries this thread owns: kept in
+        // registers until the tile is staged (the staging buffer may be the g region)
+        constexpr int NPW = NB * BS * BS / 256;
+        float paq[NPW], saq[4];
+        const int qmask = pmask & (dfl >> 5);           // ... whose 4-row sub-blocks also exceed it
+        if (unsafe) {
+            // every pair s <= t from raw q (ql), raw k (kr), exact exp(gamma_t - gamma_s)
+            for (int p = tid; p < C * C; p += 256) {
+                const int t = p / C, sx = p - t * C;
+                float ak = 0.f, aq = 0.f;
+                if (sx <= t) {
 #pragma unroll 1
-                for (int d = 0; d < D; ++d) {
-                    const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(chunk_gamma(s, t, d) - chunk_gamma(s, sx, d));
-                    ak += ld1<ST>(&s.kr[t][d]) * ks;
-                    aq += ld1<ST>(&s.ql[t][d]) * ks;
-                }
-            }
-            const float akk = (sx < t) ? ak : 0.f;
-            sa[t][sx] = akk;
-            if (a.Akk) a.Akk[cCC + (size_t)t * C + sx] = akk;
-            if (oAqk) st1<ST>(oAqk + cCC + (size_t)t * C + sx, aq);
-            if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, aq);
-        }
-        __syncthreads();
-    } else if (pmask) {
-        // Diagonal tiles of the blocks in pmask, from raw q, k (pass A overwrites
-        // them).  Wave w forms block w's tile with 4-row sub-anchors on MFMA;
-        // blocks whose 4-row sub-blocks also exceed the guard (qmask) are
-        // evaluated one entry (t, s) per thread and step, e^{a_t - a_s}.  A_kk
-        // goes to sa now (its tile is not formed below), A_qk^T to its output;
-        // A_qk stays in registers until its tile is staged.
-        if (((pmask & ~qmask) >> w) & 1) {
-            f32x4 P, Q;
-            subanchor_tile<D, ST, PREC, true>(s, w, P, Q);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * w + 4 * g4 + e, sx = BS * w + r16;
-                sa[t][sx] = (sx < t) ? P[e] : 0.f;
-                saq[e] = (sx <= t) ? Q[e] : 0.f;
-            }
-            if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * w + r16) * C + BS * w + 4 * g4, saq);
-        }
-        if (qmask) {
-            const int nent = __popc(qmask) * BS * BS;
-#pragma unroll
-            for (int it = 0; it < NPW; ++it) {
-                const int pp = tid + 256 * it;
-                paq[it] = 0.f;
-                if (pp < nent) {
-                    const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
-                    int blk = 0;
-                    for (int m = qmask, c = 0;; m &= m - 1, ++c)
-                        if (c == kb) { blk = __ffs(m) - 1; break; }
-                    const int t = BS * blk + e / BS, sx = BS * blk + e % BS;
-                    float ak = 0.f, aq = 0.f;
-                    if (sx <= t) {
-#pragma unroll 2
-                        for (int d = 0; d < D; ++d) {
-                            const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(s.g[t][d] - s.g[sx][d]);
-                            ak += ld1<ST>(&s.kr[t][d]) * ks;
-                            aq += ld1<ST>(&s.ql[t][d]) * ks;
-                        }
+                    for (int d = 0; d < D; ++d) {
+                        const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(chunk_gamma(s, t, d) - chunk_gamma(s, sx, d));
+                        ak += ld1<ST>(&s.kr[t][d]) * ks;
+                        aq += ld1<ST>(&s.ql[t][d]) * ks;
                     }
-                    sa[t][sx] = (sx < t) ? ak : 0.f;
-                    paq[it] = aq;
-                    if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, aq);
                 }
+                const float akk = (sx < t) ? ak : 0.f;
+                sa[t][sx] = akk;
+                if (a_Akk) a_Akk[cCC + (size_t)t * C + sx] = akk;
+                if (oAqk) st1<ST>(oAqk + cCC + (size_t)t * C + sx, aq);
+                if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, aq);
             }
-        }
-        __syncthreads();   // raw q, k are read above and overwritten by pass A
-    }
-
-    // pass A: row threads (t, EPV channels).  K_l = K e^{a}, Q_l = Q e^{a},
-    // K_r = K e^{b} (anchored chunks; raw K otherwise), Qp = Q_l e^{gamma_{16i-1}},
-    // Kb = K_r e^{G - gamma_{16i+15}}
-    {
-        constexpr int VPR = D / EPV, NV = C * VPR;
-        for (int vv = tid; vv < NV; vv += 256) {
-            const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, blk = t / BS;
-            const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
-            const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
-            float okl[EPV], oql[EPV], okr[EPV], oqp[EPV], okb[EPV];
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                const int d = c0 + e;
-                const float at = s.g[t][d], bt = s.g[BS * blk + BS - 1][d] - at;
-                const float el = kexp<PREC>(at);
-                const float qf = qv.get(e), kf = kv.get(e);
-                okl[e] = kf * el;
-                oql[e] = qf * el;
-                okr[e] = unsafe ? kf : kf * kexp<PREC>(bt);
-                oqp[e] = oql[e] * fac_ep(s, blk, d);
-                if (bwd) {
-                    if (unsafe) {
-                        float gsfx = bt;   // G - gamma_t
-                        for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];
-                        okb[e] = kf * kexp<PREC>(gsfx);
-                    } else {
-                        okb[e] = okr[e] * fac_eq(s, blk, d);
-                    }
-                } else {
-                    okb[e] = 0.f;
-                }
-            }
-            store_vec<ST>(&s.kl[t][c0], okl);
-            store_vec<ST>(&s.ql[t][c0], oql);
-            store_vec<ST>(&s.kr[t][c0], okr);
-            if (oQp) store_vec<ST>(oQp + cCD + (size_t)t * D + c0, oqp);
-            if (oKb) store_vec<ST>(oKb + cCD + (size_t)t * D + c0, okb);
-        }
-    }
-    __syncthreads();
-    // PHASE 3
-
-    // pass B: the transposed copies KbT = (K_r diag(e^{G - gamma_{16i+15}}))^T and
-    // QpT = (Q_l diag(e^{gamma_{16i-1}}))^T.  Anchored chunks, bf16: per 16 x 16
-    // tile (token block i, channel block j) one MFMA forms X diag(s), which leaves
-    // channel d of the tile in lane d % 16 with four consecutive tokens per lane
-    // -- the transposed layout -- written as 8-byte pieces of KbT / QpT rows.
-    // X = K_r or Q_l is exact in bf16; the scale s is split into bf16 hi + lo
-    // halves of one K = 32 step, so the product keeps fp32 accuracy until the
-    // final rounding.
-    if (std::is_same<ST, uint16_t>::value && !unsafe) {
-        // wave w: tiles w, w + 4, ... of each output (NT per wave), unrolled so
-        // that all of a wave's operand reads share one LDS round trip
-#pragma unroll
-        for (int o = 0; o < 2; ++o) {
-            ST* out = o ? oQpT : oKbT;
-            if (out == nullptr) continue;
-            const ST* X = o ? &s.ql[0][0] : &s.kr[0][0];
-            Frag4 A[NT];
-            float sv[NT];
-#pragma unroll
-            for (int it = 0; it < NT; ++it) {
-                const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
-                A[it] = ldfrag4<1, ST>(X, LDK, BS * i, BS * j);
-                sv[it] = o ? fac_ep(s, i, BS * j + r16) : fac_eq(s, i, BS * j + r16);
-            }
-#pragma unroll
-            for (int it = 0; it < NT; ++it) {
-                const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
-                const short hi = (short)f2bf(sv[it]), lo = (short)f2bf(sv[it] - bf2f((uint16_t)hi));
-                short4v bh, bl;
+            __syncthreads();
+        } else if (pmask) {
+            // Diagonal tiles of the blocks in pmask, from raw q, k (pass A overwrites
+            // them).  Wave w forms block w's tile with 4-row sub-anchors on MFMA;
+            // blocks whose 4-row sub-blocks also exceed the guard (qmask) are
+            // evaluated one entry (t, s) per thread and step, e^{a_t - a_s}.  A_kk
+            // goes to sa now (its tile is not formed below), A_qk^T to its output;
+            // A_qk stays in registers until its tile is staged.
+            if (((pmask & ~qmask) >> w) & 1) {
+                f32x4 P, Q;
+                subanchor_tile<D, ST, PREC, true>(s, w, P, Q);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const bool dg = 4 * g4 + e == r16;   // B[k][n] = s[n] on the diagonal
-                    bh[e] = dg ? hi : (short)0;
-                    bl[e] = dg ? lo : (short)0;
+                    const int t = BS * w + 4 * g4 + e, sx = BS * w + r16;
+                    sa[t][sx] = (sx < t) ? P[e] : 0.f;
+                    saq[e] = (sx <= t) ? Q[e] : 0.f;
                 }
-                const f32x4 c =
-                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat4(A[it].h, A[it].h), cat4(bh, bl), zero4(), 0, 0, 0);
-                *reinterpret_cast<uint2*>(out + cCD + (size_t)(BS * j + r16) * C + BS * i + 4 * g4) =
-                    make_uint2(pack2bf(c[0], c[1]), pack2bf(c[2], c[3]));
+                if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * w + r16) * C + BS * w + 4 * g4, saq);
             }
-        }
-    } else {
-        // column threads (d, EPV tokens)
-        constexpr int GPC = C / EPV, NV = D * GPC;
-        for (int vv = tid; vv < NV; vv += 256) {
-            const int d = vv / GPC, tb = (vv - d * GPC) * EPV;
-            float okb[EPV], oqp[EPV];
+            if (qmask) {
+                const int nent = __popc(qmask) * BS * BS;
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                const int t = tb + e, blk = t / BS;
-                const float kr = ld1<ST>(&s.kr[t][d]);
-                if (unsafe) {
-                    float gsfx = s.g[BS * blk + BS - 1][d] - s.g[t][d];   // G - gamma_t
-                    for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];
-                    okb[e] = kr * kexp<PREC>(gsfx);
-                } else {
-                    okb[e] = kr * fac_eq(s, blk, d);
-                }
-                oqp[e] = ld1<ST>(&s.ql[t][d]) * fac_ep(s, blk, d);
-            }
-            if (oKbT) store_vec<ST>(oKbT + cCD + (size_t)d * C + tb, okb);
-            if (oQpT) store_vec<ST>(oQpT + cCD + (size_t)d * C + tb, oqp);
-        }
-    }
-    if constexpr (G::STAGE_V) tv.store(&svbuf[0][0], LDK);   // first read by the forward substitution
-    __syncthreads();
-    // PHASE 4
-
-    // Aqk is staged row-major for coalesced stores; AqkT is written from the
-    // accumulators (a lane's four rows of one column are four consecutive AqkT
-    // elements)
-    ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];
-    if (!unsafe) {
-        // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared: K_r of
-        // block j times the tile's channel factor (F_ij, 1 between adjacent
-        // blocks, e^{-T_i} on the diagonal).  Diagonal tiles of blocks in pmask
-        // were formed pair by pair.
-        for (int tix = w; tix < 10; tix += 4) {
-            int i, j;
-            tile_ij(tix, i, j);
-            if (j == i && ((pmask >> i) & 1)) continue;
-            const float* fsc = &s.fac[(j == i) ? FAC_FD + i : (j == i - 1) ? 0 : fac_f_row(i, j)][0];
-            f32x4 P = zero4(), Q = zero4();
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
-                const Frag8 Aq = ldfrag<PREC, ST>(&s.ql[0][0], LDK, BS * i, 32 * ks);
-                const Frag8 Bk = (j == i - 1) ? ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
-                                              : ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
-                                                                        fsc + 32 * ks);
-                P = mma<PREC>(Ak, Bk, P);
-                Q = mma<PREC>(Aq, Bk, Q);
-            }
-            float aq[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
-                sa[t][sx] = (sx < t) ? P[e] : 0.f;
-                aq[e] = (sx <= t) ? Q[e] : 0.f;
-                if (oAqk) st1<ST>(stA + t * LDT + sx, aq[e]);
-            }
-            if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, aq);
-        }
-        // the diagonal entries of A_qk formed in phase 2, from registers
-        if (oAqk && (((pmask & ~qmask) >> w) & 1)) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) st1<ST>(stA + (BS * w + 4 * g4 + e) * LDT + BS * w + r16, saq[e]);
-        }
-        if (oAqk && qmask) {
-            const int nent = __popc(qmask) * BS * BS;
-#pragma unroll
-            for (int it = 0; it < NPW; ++it) {
-                const int pp = tid + 256 * it;
-                if (pp < nent) {
-                    const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
-                    int blk = 0;
-                    for (int m = qmask, c = 0;; m &= m - 1, ++c)
-                        if (c == kb) { blk = __ffs(m) - 1; break; }
-                    st1<ST>(stA + (BS * blk + e / BS) * LDT + BS * blk + e % BS, paq[it]);
-                }
-            }
-        }
-        // strictly upper sub-block tiles are zero
-        for (int idx = tid; idx < 6 * BS * BS; idx += 256) {
-            const int tile = idx / (BS * BS), e = idx - tile * BS * BS;
-            const int i = (tile < 3) ? 0 : (tile < 5) ? 1 : 2;
-            const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
-            const int t = BS * i + e / BS, sx = BS * j + (e % BS);
-            sa[t][sx] = 0.f;
-            if (oAqk) st1<ST>(stA + t * LDT + sx, 0.f);
-        }
-        if (oAqkT && w >= 2) {
-            // waves 2-3 formed two of the ten lower tiles (waves 0-1 three): they
-            // write the six zero tiles
-            const float z[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int u = w - 2; u < 6; u += 2) {   // tile (i, j), i < j
-                const int i = (u < 3) ? 0 : (u < 5) ? 1 : 2;
-                const int j = (u < 3) ? u + 1 : (u < 5) ? u - 1 : 3;
-                st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, z);
-            }
-        }
-    }
-    __syncthreads();
-    // PHASE 5
-    if (!unsafe) {
-        if (oAqk) tile_out<ST, C, C>(stA, LDT, oAqk + cCC, C, C);
-        if (a.Akk) tile_out<float, C, C>(&sa[0][0], LDA, a.Akk + cCC, C, C);
-    }
-    diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
-    __syncthreads();
-    // PHASE 6
-    if (a.Tii && tid < NB * BS * BS / 4) {
-        const int i = tid / (BS * BS / 4), e4 = (tid - i * (BS * BS / 4)) * 4;
-        *reinterpret_cast<float4*>(a.Tii + (size_t)ch * NB * BS * BS + i * BS * BS + e4) =
-            *reinterpret_cast<const float4*>(&tii[i][e4 / BS][e4 % BS]);
-    }
-
-    // block forward substitution; the wave's column tiles of [Kt | beta V] advance together
-    f32x4 X[TPW][NB];
-    bool tok[TPW], isK[TPW];
-    int dcol[TPW];
-#pragma unroll
-    for (int jj = 0; jj < TPW; ++jj) {
-        const int ct = w + 4 * jj;
-        tok[jj] = ct < NCT;
-        isK[jj] = ct < NT;
-        dcol[jj] = (isK[jj] ? ct : ct - NT) * BS + r16;
-    }
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        f32x4 Y[TPW];
-#pragma unroll
-        for (int jj = 0; jj < TPW; ++jj)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = BS * i + 4 * g4 + e, d = dcol[jj];
-                float rv = 0.f;
-                if (tok[jj]) {
-                    if (isK[jj]) {
-                        rv = s.beta[t] * fac_ep(s, i, d) * ld1<ST>(&s.kl[t][d]);
-                    } else if constexpr (G::STAGE_V) {
-                        rv = s.beta[t] * ld1<ST>(&svbuf[t][d]);
-                    } else {
-                        rv = (t < valid) ? s.beta[t] * ld1<ST>(v + base + (size_t)t * rs + d) : 0.f;
+                for (int it = 0; it < NPW; ++it) {
+                    const int pp = tid + 256 * it;
+                    paq[it] = 0.f;
+                    if (pp < nent) {
+                        const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
+                        int blk = 0;
+                        for (int m = qmask, c = 0;; m &= m - 1, ++c)
+                            if (c == kb) { blk = __ffs(m) - 1; break; }
+                        const int t = BS * blk + e / BS, sx = BS * blk + e % BS;
+                        float ak = 0.f, aq = 0.f;
+                        if (sx <= t) {
+#pragma unroll 2
+                            for (int d = 0; d < D; ++d) {
+                                const float ks = ld1<ST>(&s.kr[sx][d]) * kexp<PREC>(s.g[t][d] - s.g[sx][d]);
+                                ak += ld1<ST>(&s.kr[t][d]) * ks;
+                                aq += ld1<ST>(&s.ql[t][d]) * ks;
+                            }
+                        }
+                        sa[t][sx] = (sx < t) ? ak : 0.f;
+                        paq[it] = aq;
+                        if (oAqkT) st1<ST>(oAqkT + cCC + (size_t)sx * C + t, aq);
                     }
                 }
-                Y[jj][e] = rv;
             }
-        const float brow = -s.beta[BS * i + r16];
+            __syncthreads();   // raw q, k are read above and overwritten by pass A
+        }
+
+        // pass A: row threads (t, EPV channels).  K_l = K e^{a}, Q_l = Q e^{a},
+        // K_r = K e^{b} (anchored chunks; raw K otherwise), Qp = Q_l e^{gamma_{16i-1}},
+        // Kb = K_r e^{G - gamma_{16i+15}}
+        {
+            constexpr int VPR = D / EPV, NV = C * VPR;
+            for (int vv = tid; vv < NV; vv += 256) {
+                const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, blk = t / BS;
+                const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
+                const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
+                float okl[EPV], oql[EPV], okr[EPV], oqp[EPV], okb[EPV];
 #pragma unroll
-        for (int j = 0; j < i; ++j) {
-            const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
-            const float lv[4] = {brow * x.x, brow * x.y, brow * x.z, brow * x.w};
-            const Frag4 A = frag4_from_f32<3>(lv);
+                for (int e = 0; e < EPV; ++e) {
+                    const int d = c0 + e;
+                    const float at = s.g[t][d], bt = s.g[BS * blk + BS - 1][d] - at;
+                    const float el = kexp<PREC>(at);
+                    const float qf = qv.get(e), kf = kv.get(e);
+                    okl[e] = kf * el;
+                    oql[e] = qf * el;
+                    okr[e] = unsafe ? kf : kf * kexp<PREC>(bt);
+                    oqp[e] = oql[e] * fac_ep(s, blk, d);
+                    if (bwd) {
+                        if (unsafe) {
+                            float gsfx = bt;   // G - gamma_t
+                            for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];
+                            okb[e] = kf * kexp<PREC>(gsfx);
+                        } else {
+                            okb[e] = okr[e] * fac_eq(s, blk, d);
+                        }
+                    } else {
+                        okb[e] = 0.f;
+                    }
+                }
+                store_vec<ST>(&s.kl[t][c0], okl);
+                store_vec<ST>(&s.ql[t][c0], oql);
+                store_vec<ST>(&s.kr[t][c0], okr);
+                if (oQp) store_vec<ST>(oQp + cCD + (size_t)t * D + c0, oqp);
+                if (oKb) store_vec<ST>(oKb + cCD + (size_t)t * D + c0, okb);
+            }
+        }
+        __syncthreads();
+        // PHASE 3
+
+        // pass B: the transposed copies KbT = (K_r diag(e^{G - gamma_{16i+15}}))^T and
+        // QpT = (Q_l diag(e^{gamma_{16i-1}}))^T.  Anchored chunks, bf16: per 16 x 16
+        // tile (token block i, channel block j) one MFMA forms X diag(s), which leaves
+        // channel d of the tile in lane d % 16 with four consecutive tokens per lane
+        // -- the transposed layout -- written as 8-byte pieces of KbT / QpT rows.
+        // X = K_r or Q_l is exact in bf16; the scale s is split into bf16 hi + lo
+        // halves of one K = 32 step, so the product keeps fp32 accuracy until the
+        // final rounding.
+        if (std::is_same<ST, uint16_t>::value && !unsafe) {
+            // wave w: tiles w, w + 4, ... of each output (NT per wave), unrolled so
+            // that all of a wave's operand reads share one LDS round trip
+#pragma unroll
+            for (int o = 0; o < 2; ++o) {
+                ST* out = o ? oQpT : oKbT;
+                if (out == nullptr) continue;
+                const ST* X = o ? &s.ql[0][0] : &s.kr[0][0];
+                Frag4 A[NT];
+                float sv[NT];
+#pragma unroll
+                for (int it = 0; it < NT; ++it) {
+                    const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
+                    A[it] = ldfrag4<1, ST>(X, LDK, BS * i, BS * j);
+                    sv[it] = o ? fac_ep(s, i, BS * j + r16) : fac_eq(s, i, BS * j + r16);
+                }
+#pragma unroll
+                for (int it = 0; it < NT; ++it) {
+                    const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
+                    const short hi = (short)f2bf(sv[it]), lo = (short)f2bf(sv[it] - bf2f((uint16_t)hi));
+                    short4v bh, bl;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool dg = 4 * g4 + e == r16;   // B[k][n] = s[n] on the diagonal
+                        bh[e] = dg ? hi : (short)0;
+                        bl[e] = dg ? lo : (short)0;
+                    }
+                    const f32x4 c =
+                        __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat4(A[it].h, A[it].h), cat4(bh, bl), zero4(), 0, 0, 0);
+                    *reinterpret_cast<uint2*>(out + cCD + (size_t)(BS * j + r16) * C + BS * i + 4 * g4) =
+                        make_uint2(pack2bf(c[0], c[1]), pack2bf(c[2], c[3]));
+                }
+            }
+        } else {
+            // column threads (d, EPV tokens)
+            constexpr int GPC = C / EPV, NV = D * GPC;
+            for (int vv = tid; vv < NV; vv += 256) {
+                const int d = vv / GPC, tb = (vv - d * GPC) * EPV;
+                float okb[EPV], oqp[EPV];
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    const int t = tb + e, blk = t / BS;
+                    const float kr = ld1<ST>(&s.kr[t][d]);
+                    if (unsafe) {
+                        float gsfx = s.g[BS * blk + BS - 1][d] - s.g[t][d];   // G - gamma_t
+                        for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];
+                        okb[e] = kr * kexp<PREC>(gsfx);
+                    } else {
+                        okb[e] = kr * fac_eq(s, blk, d);
+                    }
+                    oqp[e] = ld1<ST>(&s.ql[t][d]) * fac_ep(s, blk, d);
+                }
+                if (oKbT) store_vec<ST>(oKbT + cCD + (size_t)d * C + tb, okb);
+                if (oQpT) store_vec<ST>(oQpT + cCD + (size_t)d * C + tb, oqp);
+            }
+        }
+        if constexpr (G::STAGE_V) tv.store(&svbuf[0][0], LDK);   // first read by the forward substitution
+        __syncthreads();
+        // PHASE 4
+
+        // Aqk is staged row-major for coalesced stores; AqkT is written from the
+        // accumulators (a lane's four rows of one column are four consecutive AqkT
+        // elements)
+        ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];
+        if (!unsafe) {
+            // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared: K_r of
+            // block j times the tile's channel factor (F_ij, 1 between adjacent
+            // blocks, e^{-T_i} on the diagonal).  Diagonal tiles of blocks in pmask
+            // were formed pair by pair.
+            for (int tix = w; tix < 10; tix += 4) {
+                int i, j;
+                tile_ij(tix, i, j);
+                if (j == i && ((pmask >> i) & 1)) continue;
+                const float* fsc = &s.fac[(j == i) ? FAC_FD + i : (j == i - 1) ? 0 : fac_f_row(i, j)][0];
+                f32x4 P = zero4(), Q = zero4();
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) {
+                    const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
+                    const Frag8 Aq = ldfrag<PREC, ST>(&s.ql[0][0], LDK, BS * i, 32 * ks);
+                    const Frag8 Bk = (j == i - 1) ? ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
+                                                  : ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
+                                                                            fsc + 32 * ks);
+                    P = mma<PREC>(Ak, Bk, P);
+                    Q = mma<PREC>(Aq, Bk, Q);
+                }
+                float aq[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
+                    sa[t][sx] = (sx < t) ? P[e] : 0.f;
+                    aq[e] = (sx <= t) ? Q[e] : 0.f;
+                    if (oAqk) st1<ST>(stA + t * LDT + sx, aq[e]);
+                }
+                if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, aq);
+            }
+            // the diagonal entries of A_qk formed in phase 2, from registers
+            if (oAqk && (((pmask & ~qmask) >> w) & 1)) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) st1<ST>(stA + (BS * w + 4 * g4 + e) * LDT + BS * w + r16, saq[e]);
+            }
+            if (oAqk && qmask) {
+                const int nent = __popc(qmask) * BS * BS;
+#pragma unroll
+                for (int it = 0; it < NPW; ++it) {
+                    const int pp = tid + 256 * it;
+                    if (pp < nent) {
+                        const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
+                        int blk = 0;
+                        for (int m = qmask, c = 0;; m &= m - 1, ++c)
+                            if (c == kb) { blk = __ffs(m) - 1; break; }
+                        st1<ST>(stA + (BS * blk + e / BS) * LDT + BS * blk + e % BS, paq[it]);
+                    }
+                }
+            }
+            // strictly upper sub-block tiles are zero
+            for (int idx = tid; idx < 6 * BS * BS; idx += 256) {
+                const int tile = idx / (BS * BS), e = idx - tile * BS * BS;
+                const int i = (tile < 3) ? 0 : (tile < 5) ? 1 : 2;
+                const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
+                const int t = BS * i + e / BS, sx = BS * j + (e % BS);
+                sa[t][sx] = 0.f;
+                if (oAqk) st1<ST>(stA + t * LDT + sx, 0.f);
+            }
+            if (oAqkT && w >= 2) {
+                // waves 2-3 formed two of the ten lower tiles (waves 0-1 three): they
+                // write the six zero tiles
+                const float z[4] = {0.f, 0.f, 0.f, 0.f};
+                for (int u = w - 2; u < 6; u += 2) {   // tile (i, j), i < j
+                    const int i = (u < 3) ? 0 : (u < 5) ? 1 : 2;
+                    const int j = (u < 3) ? u + 1 : (u < 5) ? u - 1 : 3;
+                    st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, z);
+                }
+            }
+        }
+        __syncthreads();
+        // PHASE 5
+        if (!unsafe) {
+            if (oAqk) tile_out<ST, C, C>(stA, LDT, oAqk + cCC, C, C);
+            if (a_Akk) tile_out<float, C, C>(&sa[0][0], LDA, a_Akk + cCC, C, C);
+        }
+        diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
+        __syncthreads();
+        // PHASE 6
+        if (a_Tii && tid < NB * BS * BS / 4) {
+            const int i = tid / (BS * BS / 4), e4 = (tid - i * (BS * BS / 4)) * 4;
+            *reinterpret_cast<float4*>(a_Tii + (size_t)ch * NB * BS * BS + i * BS * BS + e4) =
+                *reinterpret_cast<const float4*>(&tii[i][e4 / BS][e4 % BS]);
+        }
+
+        // block forward substitution; the wave's column tiles of [Kt | beta V] advance together
+        f32x4 X[TPW][NB];
+        bool tok[TPW], isK[TPW];
+        int dcol[TPW];
+#pragma unroll
+        for (int jj = 0; jj < TPW; ++jj) {
+            const int ct = w + 4 * jj;
+            tok[jj] = ct < NCT;
+            isK[jj] = ct < NT;
+            dcol[jj] = (isK[jj] ? ct : ct - NT) * BS + r16;
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            f32x4 Y[TPW];
 #pragma unroll
             for (int jj = 0; jj < TPW; ++jj)
-                if (tok[jj]) Y[jj] = mma4f<3>(A, accfrag4<3>(X[jj][j]), Y[jj]);
-        }
-        const Frag4 Tf = ldfrag4<3, float>(&tii[i][0][0], BS + 4, 0, 0);
-#pragma unroll
-        for (int jj = 0; jj < TPW; ++jj) X[jj][i] = tok[jj] ? mma4f<3>(Tf, accfrag4<3>(Y[jj]), zero4()) : zero4();
-    }
-    __syncthreads();
-    // PHASE 7
-    // staging: W -> kl region, U -> ql region (both dead now); WT straight from
-    // the accumulators (four consecutive tokens of one channel per lane)
-    ST* stW = &s.kl[0][0];
-    ST* stU = &s.ql[0][0];
-#pragma unroll
-    for (int jj = 0; jj < TPW; ++jj)
-        if (tok[jj])
-#pragma unroll
-            for (int i = 0; i < NB; ++i) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int t = BS * i + 4 * g4 + e, d = dcol[jj];
-                    st1<ST>((isK[jj] ? stW : stU) + t * LDK + d, X[jj][i][e]);
+                    float rv = 0.f;
+                    if (tok[jj]) {
+                        if (isK[jj]) {
+                            rv = s.beta[t] * fac_ep(s, i, d) * ld1<ST>(&s.kl[t][d]);
+                        } else if constexpr (G::STAGE_V) {
+                            rv = s.beta[t] * ld1<ST>(&svbuf[t][d]);
+                        } else {
+                            rv = (t < valid) ? s.beta[t] * ld1<ST>(v + base + (size_t)t * rs + d) : 0.f;
+                        }
+                    }
+                    Y[jj][e] = rv;
                 }
-                if (isK[jj] && oWT) {
-                    const float x[4] = {X[jj][i][0], X[jj][i][1], X[jj][i][2], X[jj][i][3]};
-                    st4(oWT + cCD + (size_t)dcol[jj] * C + BS * i + 4 * g4, x);
-                }
+            const float brow = -s.beta[BS * i + r16];
+#pragma unroll
+            for (int j = 0; j < i; ++j) {
+                const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
+                const float lv[4] = {brow * x.x, brow * x.y, brow * x.z, brow * x.w};
+                const Frag4 A = frag4_from_f32<3>(lv);
+#pragma unroll
+                for (int jj = 0; jj < TPW; ++jj)
+                    if (tok[jj]) Y[jj] = mma4f<3>(A, accfrag4<3>(X[jj][j]), Y[jj]);
             }
-    __syncthreads();
-    tile_out<ST, C, D>(stW, LDK, oW + cCD, D, C);
-    tile_out<ST, C, D>(stU, LDK, oU + cCD, D, C);
-    // PHASE 8
+            const Frag4 Tf = ldfrag4<3, float>(&tii[i][0][0], BS + 4, 0, 0);
+#pragma unroll
+            for (int jj = 0; jj < TPW; ++jj) X[jj][i] = tok[jj] ? mma4f<3>(Tf, accfrag4<3>(Y[jj]), zero4()) : zero4();
+        }
+        __syncthreads();
+        // PHASE 7
+        // staging: W -> kl region, U -> ql region (both dead now); WT straight from
+        // the accumulators (four consecutive tokens of one channel per lane)
+        ST* stW = &s.kl[0][0];
+        ST* stU = &s.ql[0][0];
+#pragma unroll
+        for (int jj = 0; jj < TPW; ++jj)
+            if (tok[jj])
+#pragma unroll
+                for (int i = 0; i < NB; ++i) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = BS * i + 4 * g4 + e, d = dcol[jj];
+                        st1<ST>((isK[jj] ? stW : stU) + t * LDK + d, X[jj][i][e]);
+                    }
+                    if (isK[jj] && oWT) {
+                        const float x[4] = {X[jj][i][0], X[jj][i][1], X[jj][i][2], X[jj][i][3]};
+                        st4(oWT + cCD + (size_t)dcol[jj] * C + BS * i + 4 * g4, x);
+                    }
+                }
+        __syncthreads();
+        tile_out<ST, C, D>(stW, LDK, oW + cCD, D, C);
+        tile_out<ST, C, D>(stU, LDK, oU + cCD, D, C);
+        // PHASE 8
+    };
+    if (dfl & 31)
+        tail(std::true_type{});
+    else
+        tail(std::false_type{});
 }
 
 // ----------------------------------------------------------------------------
