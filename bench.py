@@ -341,6 +341,7 @@ def layer_bench(args):
     layer.A_log.data = layer.A_log.data.float()
     layer.dt_bias.data = layer.dt_bias.data.float()
     layer = layer.cuda()
+    layer.fused_output_norm = not args.unfused_norm
     gen = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(B, T, hidden, device="cuda", generator=gen).to(torch.bfloat16).requires_grad_()
     cot = torch.randn(B, T, hidden, device="cuda", generator=gen).to(torch.bfloat16)
@@ -392,7 +393,7 @@ def layer_bench(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) x, random-init layer of the reference's architecture)",
         "config": {"workload": "GatedDeltaLayer fwd+bwd, x (8, 1568, 768), H12 D64, bf16 (A_log, dt_bias fp32)",
-                   "B": B, "T": T, "hidden": hidden, "H": H, "D": D},
+                   "B": B, "T": T, "hidden": hidden, "H": H, "D": D, "fused_output_norm": not args.unfused_norm},
         "profiled_ms_per_step": round(prof_ms, 4),
         "kda_ms_per_step": round(kda_ms, 4), "elementwise_ms_per_step": round(ew_ms, 4),
         "kda_share": round(kda_ms / prof_ms, 4), "elementwise_share": round(ew_ms / prof_ms, 4),
@@ -411,6 +412,7 @@ def model_bench(args):
     bf16 weights with A_log / dt_bias in fp32, random init, synthetic clips."""
     import ctypes
     import torch
+    import mlx_vit_amd as kda
     from mlx_vit_amd import _lib
     from mlx_vit_amd import model as M
     from mlx_vit_amd import train as TR
@@ -419,6 +421,9 @@ def model_bench(args):
     torch.cuda.set_device(0)
     torch.manual_seed(0)
     model = M.to_bf16(M.config4()).cuda()
+    for mod in model.modules():
+        if isinstance(mod, kda.GatedDeltaLayer):
+            mod.fused_output_norm = not args.unfused_norm
     step = TR.TrainStep(model)
     gen = torch.Generator(device="cuda").manual_seed(0)
     video = torch.randn(B, 16, 224, 224, 3, device="cuda", generator=gen).to(torch.bfloat16)
@@ -478,6 +483,9 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["layer", "model"], default="cfg2")
     ap.add_argument("--cpu-sample-tokens", type=int, default=392)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--unfused-norm", action="store_true",
+                    help="layer / model workloads: run the output norm as its own kernel instead of fused into "
+                         "the recurrence's store")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one plain fp32 streaming kernel of this many MiB first (PMC byte-counter scale)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),

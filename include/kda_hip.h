@@ -124,6 +124,24 @@ int kda_bwd_train(const void* q, const void* k, const void* v, const void* g, co
                   int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
                   void* workspace, size_t ws_bytes, void* stream);
 
+/* Forward (pass KDA_PASS_FWD, workspace as kda_fwd) or training forward
+ * (KDA_PASS_TRAIN, as kda_fwd_train) with the layer's output norm fused into
+ * the store of o: besides o and the final state it writes
+ *     y = o * rsqrt(mean_d o^2 + eps) * norm_w * sigmoid(z)
+ * per head of D channels, y and z [B, T, *] with row strides ld_y and ld_z
+ * (elements, multiples of 16 bytes; head h at column h*D), z and y in dtype,
+ * norm_w fp32 [D].  o is still written: the norm's backward
+ * (kda_layer_gated_rmsnorm_bwd) reads it.  Supported: bf16 with D = 64, fp32
+ * with D in {32, 64} (KDA_E_UNSUPPORTED otherwise).
+ * Replaces the recurrence call and the following RMSNormGated of
+ * GatedDeltaLayer.__call__ (nope_gdn_mlx.py:823-885, RMSNormGated
+ * nope_gdn_mlx.py:340-366): o_norm(o, gate) applied to the path's output. */
+int kda_fwd_gated(int pass, const void* q, const void* k, const void* v, const void* g,
+                  const void* beta, const float* s0, const void* z, int64_t ld_z,
+                  const float* norm_w, float eps, void* o, void* y, int64_t ld_y, float* s_final,
+                  int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+                  void* workspace, size_t ws_bytes, void* stream);
+
 /* y = M^-1 b for unit-triangular M (only the strict lower, or with upper != 0
  * the strict upper, part of M is read); M [BH, Cm, Cm], b and y [BH, Cm, N],
  * fp32, 1 <= Cm <= 64, N >= 1.

@@ -42,6 +42,7 @@ SIGNATURES = {
     "kda_fwd_train": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_fwd_noalloc": ([_P] * 8 + [_I] * 7 + [_P], _I),
     "kda_bwd_train": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
+    "kda_fwd_gated": ([_I] + [_P] * 7 + [_L, _P, _F, _P, _P, _L, _P] + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_solve_unit_triangular": ([_P] * 3 + [_I] * 4 + [_P], _I),
     "kda_layer_producer_fwd": ([_P] * 5 + [_L] * 3 + [_P] * 9 + [_I] * 4 + [_F] * 2 + [_I] * 2 + [_P], _I),
     "kda_layer_producer_bwd": ([_P] * 5 + [_L] * 3 + [_P] * 14 + [_L] * 3 + [_P] * 4 + [_I] * 4 + [_F] * 2

@@ -289,9 +289,19 @@ hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* 
 
 // prof = false: no launch timing (the profiler's event pool never grows), for
 // the entry point that must not allocate
+// The layer's gated RMSNorm fused into the forward's O store (kda_fwd_gated).
+struct Epilogue {
+    const void* z;
+    int64_t ld_z;
+    const float* w;
+    float eps;
+    void* y;
+    int64_t ld_y;
+};
+
 int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
-            size_t ws_bytes, void* stream, bool prof = true) {
+            size_t ws_bytes, void* stream, bool prof = true, const Epilogue* epi = nullptr) {
     int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, pass == KDA_PASS_TRAIN);
     if (rc) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -325,6 +335,9 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     ra.eG = fregion(workspace, L, KDA_WS_EG);
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
+    if (epi) {
+        ra.z = epi->z; ra.ld_z = epi->ld_z; ra.nw = epi->w; ra.eps = epi->eps; ra.y = epi->y; ra.ld_y = epi->ld_y;
+    }
     e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 0, st); }, prof);
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
     return ok();
@@ -496,6 +509,33 @@ int kda_fwd_train(const void* q, const void* k, const void* v, const void* g, co
                   void* workspace, size_t ws_bytes, void* stream) {
     return run_fwd(KDA_PASS_TRAIN, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
                    ws_bytes, stream);
+}
+
+int kda_fwd_gated(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  const float* s0, const void* z, int64_t ld_z, const float* norm_w, float eps, void* o, void* y,
+                  int64_t ld_y, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+                  void* workspace, size_t ws_bytes, void* stream) {
+    if (pass != KDA_PASS_FWD && pass != KDA_PASS_TRAIN)
+        return fail(KDA_E_INVALID, "kda_fwd_gated: pass=%d, expected %d (forward) or %d (training)", pass,
+                    KDA_PASS_FWD, KDA_PASS_TRAIN);
+    int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, pass == KDA_PASS_TRAIN);
+    if (rc) return rc;
+    if (!kda::recur_epilogue_supported(D, dtype == KDA_DTYPE_BF16))
+        return fail(KDA_E_UNSUPPORTED, "kda_fwd_gated: D=%d with dtype=%d has no fused epilogue (bf16: D=64; "
+                    "fp32: D in {32, 64})", D, dtype);
+    const int64_t epv = 16 / (dtype == KDA_DTYPE_BF16 ? 2 : 4);
+    if ((size_t)B * T * H > 0) {
+        if ((rc = check_io(z, "z", dtype, false)) || (rc = check_io(y, "y", dtype, false)) ||
+            (rc = check_io(norm_w, "norm_w", KDA_DTYPE_F32, false)))
+            return rc;
+        if (ld_z < (int64_t)H * D || ld_z % epv || ld_y < (int64_t)H * D || ld_y % epv)
+            return fail(KDA_E_INVALID, "kda_fwd_gated: ld_z=%lld and ld_y=%lld must be >= H*D=%d and multiples of %lld",
+                        (long long)ld_z, (long long)ld_y, H * D, (long long)epv);
+        if (!(eps >= 0.f)) return fail(KDA_E_INVALID, "kda_fwd_gated: eps=%g must be >= 0", (double)eps);
+    }
+    const Epilogue epi{z, ld_z, norm_w, eps, y, ld_y};
+    return run_fwd(pass, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace, ws_bytes,
+                   stream, true, &epi);
 }
 
 int kda_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,

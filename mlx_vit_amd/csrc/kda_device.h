@@ -366,6 +366,30 @@ template <> __device__ __forceinline__ void store_vec<float>(float* p, const flo
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// 1 / (1 + e^-x) with the hardware reciprocal (1 ulp); e^-x = inf gives 0
+__device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+
+// The layer's gated RMSNorm, y = o rsqrt(mean_d o^2 + eps) w sigmoid(z) per
+// head of D channels (RMSNormGated, nope_gdn_mlx.py:340-366), on one 16-byte
+// piece of a row: o and z hold EPV channels of the row, w their weights; the
+// row's other D / EPV - 1 pieces are in the neighbouring lanes (an aligned
+// group of consecutive lanes), which must all call this together.
+template <typename ST, int D>
+__device__ __forceinline__ void gated_rmsnorm_piece(const uint4& o, const uint4& z, const float* w, float eps,
+                                                    float* y) {
+    constexpr int EPV = 16 / (int)sizeof(ST), VPR = D / EPV;
+    static_assert(VPR >= 1 && VPR <= 64 && (VPR & (VPR - 1)) == 0, "row pieces in an aligned lane group");
+    const Vec16<ST> ov{o}, zv{z};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) ss = fmaf(ov.get(e), ov.get(e), ss);
+#pragma unroll
+    for (int m = 1; m < VPR; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    const float rs = rsqrtf(ss * (1.f / (float)D) + eps);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) y[e] = ov.get(e) * rs * w[e] * sigm(zv.get(e));
+}
+
 // ----------------------------------------------------------------------------
 // cooperative 16-byte tile copies (256 threads)
 // ----------------------------------------------------------------------------
@@ -468,6 +492,35 @@ __device__ __forceinline__ void tile_out(const ST* lds, int lld, ST* __restrict_
         const int row = v / VPR, c = (v - row * VPR) * EPV;
         if (v < NV && row < valid_rows)
             *reinterpret_cast<uint4*>(g + (size_t)row * gld + c) = *reinterpret_cast<const uint4*>(lds + row * lld + c);
+    }
+}
+
+// tile_out for a [ROWS][D] output tile with the gated RMSNorm fused: each row
+// is stored as o and as y = gated_rmsnorm(o, z) (gated_rmsnorm_piece).  The
+// VPR = D / EPV threads of a row are consecutive lanes; z rows past
+// valid_rows are clamped (read, not used), so every lane reaches the shuffles.
+template <typename ST, int ROWS, int D, int NTH = 256>
+__device__ __forceinline__ void tile_out_gated(int t, const ST* lds, int lld, ST* __restrict__ go, size_t gld,
+                                               ST* __restrict__ gy, size_t ld_y, const ST* __restrict__ gz,
+                                               size_t ld_z, const float* __restrict__ nw, float eps,
+                                               int valid_rows) {
+    constexpr int EPV = 16 / (int)sizeof(ST), VPR = D / EPV, NV = ROWS * VPR;
+    static_assert(NV % NTH == 0 && NTH % VPR == 0, "whole rows per pass");
+    const int c = (t % VPR) * EPV;
+    float w[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) w[e] = nw[c + e];
+#pragma unroll
+    for (int i = 0; i < NV / NTH; ++i) {
+        const int row = (t + NTH * i) / VPR, rz = min(row, valid_rows - 1);
+        const uint4 ov = *reinterpret_cast<const uint4*>(lds + row * lld + c);
+        const uint4 zv = *reinterpret_cast<const uint4*>(gz + (size_t)rz * ld_z + c);
+        float y[EPV];
+        gated_rmsnorm_piece<ST, D>(ov, zv, w, eps, y);
+        if (row < valid_rows) {
+            *reinterpret_cast<uint4*>(go + (size_t)row * gld + c) = ov;
+            store_vec<ST>(gy + (size_t)row * ld_y + c, y);
+        }
     }
 }
 

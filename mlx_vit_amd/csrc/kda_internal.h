@@ -35,6 +35,14 @@ struct RecurArgs {
     void* o;
     void *h, *Vp;
     int T, H, nc, BH;
+    // Forward only: the layer's gated RMSNorm fused into the O store when y is
+    // set, y = o rsqrt(mean_d o^2 + eps) nw sigmoid(z) per head; z and y are
+    // [B, T, *] with row strides ld_z and ld_y (elements), head h at column h D.
+    const void* z;
+    const float* nw;
+    void* y;
+    int64_t ld_z, ld_y;
+    float eps;
 };
 
 struct DhArgs {
@@ -61,8 +69,10 @@ struct LocalArgs {
 int device_cu_count(int dev);
 
 hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
-// mode 0: O and the final state; 1: the chunk-start states h
+// mode 0: O and the final state (and y when a.y is set); 1: the chunk-start states h
 hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st);
+// whether launch_recur can fuse the gated RMSNorm for this head size and dtype
+bool recur_epilogue_supported(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
 hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,

@@ -64,8 +64,6 @@ template <> struct Vec4<uint16_t> {
     }
 };
 
-// 1 / (1 + e^-x) with the hardware reciprocal (1 ulp); e^-x = inf gives 0
-__device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 // log(1 + e^x) without overflow (nope_gdn_mlx.py:83-86): max(x, 0) + log1p(e^-|x|),
 // log1p(e) = log(u) - ((u - 1) - e) / u with u = 1 + e (the rounding of u is
 // compensated to first order), on the hardware log

@@ -95,7 +95,7 @@ struct DhLayout {
 //   wait for the loads, write them to LDS set (n+1)&1; barrier.
 // With NBUF = 1 an extra barrier separates the compute from the overwrite.
 // ----------------------------------------------------------------------------
-template <int D, typename ST, int PREC, int MODE, int CS>
+template <int D, typename ST, int PREC, int MODE, int CS, bool EPI = false>
 __global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
     using Lay = RecurLayout<D, ST, MODE, CS>;
     constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, TPW = (NTW + 3) / 4;
@@ -170,8 +170,18 @@ __global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
         const ST* sst = stg((Lay::NBUF == 2) ? (n & 1) : 0);
         if constexpr (MODE == 0) {
             const int t0 = n * C, valid = min(C, a.T - t0);
-            tile_out<ST, C, DC>(sst, LDU, static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
-                                (size_t)a.H * D, valid);
+            ST* go = static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0;
+            if constexpr (EPI) {
+                // whole rows (CS = 1): the gated RMSNorm on the staged tile, z read here
+                static_assert(CS == 1, "the fused epilogue needs whole output rows");
+                const size_t rb = (size_t)b * a.T + t0;
+                tile_out_gated<ST, C, D>((int)threadIdx.x, sst, LDU, go, (size_t)a.H * D,
+                                         static_cast<ST*>(a.y) + rb * a.ld_y + (size_t)h * D, (size_t)a.ld_y,
+                                         static_cast<const ST*>(a.z) + rb * a.ld_z + (size_t)h * D,
+                                         (size_t)a.ld_z, a.nw, a.eps, valid);
+            } else {
+                tile_out<ST, C, DC>(sst, LDU, go, (size_t)a.H * D, valid);
+            }
         } else {
             const size_t ch = (size_t)bh * a.nc + n;
             tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
@@ -1626,6 +1636,317 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
     }
 }
 
+// ----------------------------------------------------------------------------
+// kda_recur5_kernel: the bf16 forward recurrence with one 16-wave workgroup per
+// (batch, head), so that every output row is whole inside one workgroup and the
+// flush can apply the layer's gated RMSNorm (EPI):
+//   y = o rsqrt(mean_d o^2 + eps) w sigmoid(z)
+// (RMSNormGated, nope_gdn_mlx.py:340-366, applied to the recurrence output at
+// nope_gdn_mlx.py:880-885), storing y beside o.
+//   chain waves 0-7: wave w, wr = w % 4, hf = w / 4, owns row block wr of the
+//     chunk tiles and state columns DH hf .. DH hf + DH - 1 (DH = D / 2): the
+//     work of a kda_recur4_kernel chain wave (V' = U - W S of its rows and
+//     columns, V'^T out; after B the state update of state row block wr, S^T
+//     out), and after the update the DMA of all of a later chunk's slabs.
+//   side waves 8-15: wave w computes O = Qp S + Aqk V' for row block wr and
+//     the columns of half hf (Qp S after A, beside the chain's V'; Aqk V' after
+//     B) into the staging tile, and flushes 16 bytes of each of the previous
+//     chunk's staged rows (after A; with EPI after the staging, where the
+//     norm's work waits on no barrier); the eight lanes of a row are adjacent.
+//     With EPI the chain waves bring the chunk's gate rows with its slabs, and
+//     the side waves copy their flush pieces of them into registers before B
+//     (the set is refilled after B), one register set per parity of the chunk.
+//     The side waves issue no global load and no DMA: their only vector-memory
+//     operations are the flush stores, so no wait of theirs can stall on a load
+//     in flight.
+// Barriers and wait counts follow kda_recur4_kernel; the slabs are read once
+// per (batch, head) instead of once per column half.  LDS sets: NS = 3 (DMA
+// three chunks ahead), with EPI NS = 2 (each set also holds the gate tile).
+// ----------------------------------------------------------------------------
+template <int D, bool EPI>
+struct Recur5Layout {
+    static constexpr int NS = EPI ? 2 : 3;
+    static constexpr int RB = 2 * D, RB_C = 2 * C;                     // swizzled row bytes
+    static constexpr int W_OFF = 0;                                    // [C][D]
+    static constexpr int U_OFF = W_OFF + C * RB;                       // [C][D]
+    static constexpr int QP_OFF = U_OFF + C * RB;                      // [C][D]
+    static constexpr int KBT_OFF = QP_OFF + C * RB;                    // [D][C]
+    static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                 // [C][C]
+    static constexpr int EG_OFF = AQK_OFF + C * RB_C;                  // [D] fp32
+    static constexpr int Z_OFF = EG_OFF + 4 * D;                       // [C][D] gate rows (EPI)
+    static constexpr int SET_BYTES = ((EPI ? Z_OFF + C * RB : Z_OFF) + 1023) & ~1023;
+    // exchange tiles with a 4-element pad (see Recur3Layout), staging rows with 16 bytes
+    static constexpr int PS = 8, PX = 4, LDR = D + PX, LDU = D + PS, LDC = C + PX;
+    static constexpr int XS_OFF = 0;                                   // S^T  [D][LDR] bf16
+    static constexpr int XV_OFF = XS_OFF + D * LDR * 2;                // V'^T [D][LDC] bf16
+    static constexpr int STG_OFF = XV_OFF + D * LDC * 2;               // O    [C][LDU] bf16, two
+    static constexpr int STG_BYTES = (C * LDU * 2 + 15) & ~15;
+    static constexpr int NW_OFF = STG_OFF + 2 * STG_BYTES;            // norm weight [D] fp32
+    static constexpr int XBYTES = NW_OFF + 4 * D;
+    static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "recurrence LDS");
+};
+
+template <int D, bool EPI>
+__global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
+    using ST = uint16_t;
+    using Lay = Recur5Layout<D, EPI>;
+    constexpr int NS = Lay::NS, LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC, RB = Lay::RB, RB_C = Lay::RB_C;
+    constexpr int DH = D / 2, NTW = DH / BS;
+    static_assert(D == 64, "chain wave wr owns state row block wr: four row blocks");
+    __shared__ __align__(1024) char set0[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set1[Lay::SET_BYTES];
+    __shared__ __align__(1024) char set2[NS == 3 ? Lay::SET_BYTES : 16];
+    __shared__ __align__(16) char smem[Lay::XBYTES];
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < 16);
+    const bool chain = w < 8;
+    const int wr = w & 3, cb = DH * ((w >> 2) & 1);
+    const int bh = xcd_remap(blockIdx.x, gridDim.x);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int nc = a.nc;
+    const char* gW = static_cast<const char*>(a.W);
+    const char* gU = static_cast<const char*>(a.U);
+    const char* gQp = static_cast<const char*>(a.Qp);
+    const char* gKbT = static_cast<const char*>(a.KbT);
+    const char* gAqk = static_cast<const char*>(a.Aqk);
+    const char* gEg = reinterpret_cast<const char*>(a.eG);
+
+    auto stg = [&](int c) __attribute__((always_inline)) {
+        return reinterpret_cast<ST*>(smem + Lay::STG_OFF + (c & 1) * Lay::STG_BYTES);
+    };
+    ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
+    ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
+
+    // every slab tile is eight 1 KB blocks: one per chain wave
+    using TR = DmaTile<C, RB, 8>;     // W, U, Qp
+    using TC = DmaTile<D, RB_C, 8>;   // Kb^T, Aqk
+    constexpr int L_CHAIN = 3 * TR::COUNT + 2 * TC::COUNT + 1 + (EPI ? 1 : 0);   // + e^G (32 B), gate rows
+    static_assert(C == D && 4 * D == 8 * 32, "square tiles; e^G: two 16-byte lanes per chain wave");
+    uint32_t oR[TR::COUNT], oC[TC::COUNT];
+    TR::offsets(oR, RB, chain ? w : 0, l);
+    TC::offsets(oC, RB_C, chain ? w : 0, l);
+    const uint32_t oE = (uint32_t)(32 * w + 16 * (l & 1));
+    // one chunk's slabs into an LDS set, by the chain waves after their state update
+    auto dma_chunk = [&](int c, char* sbp) __attribute__((always_inline)) {
+        const size_t ch = (size_t)bh * nc + c;
+        const uint32_t sb = lds_addr(sbp);
+        TR::issue_s32(gW + ch * C * D * 2, oR, sb + Lay::W_OFF, w);
+        TR::issue_s32(gU + ch * C * D * 2, oR, sb + Lay::U_OFF, w);
+        TC::issue_s32(gKbT + ch * C * D * 2, oC, sb + Lay::KBT_OFF, w);
+        if (l < 2) dma16_s32(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + 32 * w);
+        TR::issue_s32(gQp + ch * C * D * 2, oR, sb + Lay::QP_OFF, w);
+        TC::issue_s32(gAqk + ch * C * C * 2, oC, sb + Lay::AQK_OFF, w);
+        if constexpr (EPI) {
+            // the chunk's gate rows, [C][D] swizzled like the slabs: wave w's
+            // 1 KB block is rows 8 w .. 8 w + 7, lane l row 8 w + l / 8 and the
+            // 16-byte column piece that lands at piece l % 8 (rows past T
+            // repeat the last row, so every lane issues)
+            const int t0 = c * C, valid = min(C, a.T - t0);
+            const int rr = 8 * w + (l >> 3), pc = (l & 7) ^ (rr & Swz<RB>::M);
+            const ST* gz = static_cast<const ST*>(a.z) + ((size_t)b * a.T + t0 + min(rr, valid - 1)) * a.ld_z +
+                           (size_t)h * D + 8 * pc;
+            dma16(gz, sbp + Lay::Z_OFF + 1024 * w);
+        }
+    };
+
+    // Registers carried from one chunk step to the next, shared by the roles:
+    //   Ax: chain W rows (A of V' = U - W S), side Qp rows;
+    //   Ay: chain Kb^T rows (A of the state update), side Aqk rows;
+    //   Rx: chain U of its rows and columns, side (EPI) its flush piece of the
+    //       gate rows of even chunks, as raw bits (Rz[0]: odd chunks).
+    Frag8 Ax[D / 32], Ay[2];
+    f32x4 Rx[NTW], Rz[1];
+    float4 eg;
+
+    // side waves: the flush thread t1 = tid - 512 owns the 16-byte piece
+    // (row t1 / 8, columns 8 (t1 % 8) ..) of a staged tile
+    const int t1 = tid - 512, frow = t1 >> 3, fcol = (t1 & 7) * 8;
+    float* snw = reinterpret_cast<float*>(smem + Lay::NW_OFF);
+    if constexpr (EPI) {
+        if (!chain && t1 < D) snw[t1] = a.nw[t1];
+    }
+    // this thread's flush piece of a chunk's gate rows, from its LDS set
+    auto read_gate = [&](const char* sb, f32x4& Z) __attribute__((always_inline)) {
+        Z = __builtin_bit_cast(f32x4, *reinterpret_cast<const uint4*>(sb + Lay::Z_OFF + Swz<RB>::at(frow, 2 * fcol)));
+    };
+    // side waves: chunk n's staged rows (with EPI and its gate piece Z)
+    auto flush = [&](int n, const f32x4& Z) __attribute__((always_inline)) {
+        const ST* sst = stg(n);
+        const int t0 = n * C, valid = min(C, a.T - t0);
+        const uint4 ov = *reinterpret_cast<const uint4*>(sst + frow * LDU + fcol);
+        ST* go = static_cast<ST*>(a.o) + (((size_t)b * a.T + t0 + frow) * a.H + h) * D + fcol;
+        if constexpr (!EPI) {
+            if (frow < valid) *reinterpret_cast<uint4*>(go) = ov;
+        } else {
+            float nwv[8], y[8];
+            *reinterpret_cast<float4*>(&nwv[0]) = *reinterpret_cast<const float4*>(snw + fcol);
+            *reinterpret_cast<float4*>(&nwv[4]) = *reinterpret_cast<const float4*>(snw + fcol + 4);
+            gated_rmsnorm_piece<ST, D>(ov, __builtin_bit_cast(uint4, Z), nwv, a.eps, y);
+            if (frow < valid) {
+                *reinterpret_cast<uint4*>(go) = ov;
+                store_vec<ST>(static_cast<ST*>(a.y) + ((size_t)b * a.T + t0 + frow) * a.ld_y + (size_t)h * D + fcol,
+                              y);
+            }
+        }
+    };
+
+    // chain waves: fp32 state tiles, rows 16 wr + 4 g4 + e, columns cb + 16 j + r16
+    f32x4 S[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+        S[j] = zero4();
+        if (chain && a.s0) {
+            const float4 x = *reinterpret_cast<const float4*>(a.s0 + ((size_t)bh * D + cb + BS * j + r16) * D +
+                                                              BS * wr + 4 * g4);
+            S[j] = f32x4{x.x, x.y, x.z, x.w};
+        }
+    }
+    auto put_state = [&]() __attribute__((always_inline)) {   // chain waves: S^T for the B operands
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+            *reinterpret_cast<uint2*>(xs + (cb + BS * j + r16) * LDR + BS * wr + 4 * g4) = pack4bf(S[j]);
+    };
+
+    // one chunk's A operands, read ahead from its LDS set
+    auto preload_kb = [&](const char* sb) __attribute__((always_inline)) {   // chain waves
+        const ST* sKbT = reinterpret_cast<const ST*>(sb + Lay::KBT_OFF);
+#pragma unroll
+        for (int ks = 0; ks < C / 32; ++ks) Ay[ks] = ldfrag_sw<RB_C>(sKbT, BS * wr, 32 * ks);
+        eg = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(sb + Lay::EG_OFF) + BS * wr + 4 * g4);
+    };
+    auto preload_chain = [&](const char* sb) __attribute__((always_inline)) {
+        const ST* sW = reinterpret_cast<const ST*>(sb + Lay::W_OFF);
+        const ST* sU = reinterpret_cast<const ST*>(sb + Lay::U_OFF);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) Ax[ks] = ldfrag_sw<RB>(sW, BS * wr, 32 * ks);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Rx[j][e] = ld_sw<RB>(sU, BS * wr + 4 * g4 + e, cb + BS * j + r16);
+    };
+    auto preload_side = [&](const char* sb) __attribute__((always_inline)) {
+        const ST* sQp = reinterpret_cast<const ST*>(sb + Lay::QP_OFF);
+        const ST* sAqk = reinterpret_cast<const ST*>(sb + Lay::AQK_OFF);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) Ax[ks] = ldfrag_sw<RB>(sQp, BS * wr, 32 * ks);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            if (ks <= wr / 2) Ay[ks] = ldfrag_sw<RB_C>(sAqk, BS * wr, 32 * ks);
+    };
+
+    auto chain_step = [&](int n, char* sdma, const char* snext, const char* scur) __attribute__((always_inline)) {
+        lds_barrier();                                          // A(n): S^T of chunk n in xs
+        Frag8 Bs[NTW][D / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) Bs[j][ks] = ldfrag<1, ST>(xs, LDR, cb + BS * j, 32 * ks);
+        // V' = U - W S, row block wr, this wave's columns
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            f32x4 P = zero4();
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) P = mma<1>(Ax[ks], Bs[j][ks], P);
+            f32x4 Vp;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Vp[e] = Rx[j][e] - P[e];
+            *reinterpret_cast<uint2*>(xv + (cb + BS * j + r16) * LDC + BS * wr + 4 * g4) = pack4bf(Vp);
+        }
+        preload_kb(scur);
+        // chunk n+1's slabs landed; chunks up to n+NS-1 may stay in flight
+        dma_wait_chunks<L_CHAIN>(min(nc - 1, n + NS - 1) - (n + 1));
+        lds_barrier();                                          // B(n): V'^T in xv, chunk n+1 visible
+        Frag8 Bv[NTW][C / 32];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) Bv[j][ks] = ldfrag<1, ST>(xv, LDC, cb + BS * j, 32 * ks);
+        // S <- diag(e^G) S + Kb^T V'
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            S[j] = f32x4{S[j][0] * eg.x, S[j][1] * eg.y, S[j][2] * eg.z, S[j][3] * eg.w};
+#pragma unroll
+            for (int ks = 0; ks < C / 32; ++ks) S[j] = mma<1>(Ay[ks], Bv[j][ks], S[j]);
+        }
+        if (n + 1 < nc) put_state();
+        // set n % NS is free now (chunk n's operands are all in registers)
+        if (n + NS < nc) dma_chunk(n + NS, sdma);
+        if (n + 1 < nc) preload_chain(snext);
+    };
+    auto side_step = [&](int n, const char* snext, const char* scur, f32x4& Zc, const f32x4& Zp)
+        __attribute__((always_inline)) {
+        lds_barrier();                                          // A(n)
+        // O = Qp S + Aqk V', row block wr, columns of half hf: the Qp S half from
+        // the chunk-start state in xs before barrier B (beside the chain's V'),
+        // the Aqk V' half after it
+        f32x4 O[NTW];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            O[j] = zero4();
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                O[j] = mma<1>(Ax[ks], ldfrag<1, ST>(xs, LDR, cb + BS * j, 32 * ks), O[j]);
+        }
+        if (!EPI && n > 0) flush(n - 1, Zp);
+        if constexpr (EPI) read_gate(scur, Zc);                 // before B: the set is refilled after it
+        lds_barrier();                                          // B(n)
+        ST* sst = stg(n);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (ks <= wr / 2) O[j] = mma<1>(Ay[ks], ldfrag<1, ST>(xv, LDC, cb + BS * j, 32 * ks), O[j]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                st1<ST>(sst + (BS * wr + 4 * g4 + e) * LDU + cb + BS * j + r16, O[j][e]);
+        }
+        if (EPI && n > 0) flush(n - 1, Zp);
+        if (n + 1 < nc) preload_side(snext);
+    };
+
+    // Each role runs its own loop (the same barriers in the same order), so no
+    // control-flow path joins the two roles' code: a join would make the
+    // compiler's wait counts for one role's loads apply to the other's.
+    // prologue: chunks 0 .. NS-1 in flight, chunk 0 landed and read
+    if (chain) {
+        put_state();
+        dma_chunk(0, set0);
+        if (nc > 1) dma_chunk(1, set1);
+        if (NS == 3 && nc > 2) dma_chunk(2, set2);
+        dma_wait_chunks<L_CHAIN>(min(NS, nc) - 1);
+        lds_barrier();
+        preload_chain(set0);
+        // unrolled NS times so that every set is named statically
+        for (int n = 0; n < nc; n += NS) {
+            chain_step(n, set0, set1, set0);
+            if (n + 1 < nc) chain_step(n + 1, set1, NS == 3 ? set2 : set0, set1);
+            if (NS == 3 && n + 2 < nc) chain_step(n + 2, set2, set0, set2);
+        }
+        lds_barrier();
+        if (a.s_final) {
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+                *reinterpret_cast<float4*>(a.s_final + ((size_t)bh * D + cb + BS * j + r16) * D + BS * wr + 4 * g4) =
+                    make_float4(S[j][0], S[j][1], S[j][2], S[j][3]);
+        }
+    } else {
+        lds_barrier();
+        preload_side(set0);
+        static_assert(!EPI || NS == 2, "gate register sets alternate with the LDS sets");
+        for (int n = 0; n < nc; n += NS) {
+            side_step(n, set1, set0, Rx[0], Rz[0]);
+            if (n + 1 < nc) side_step(n + 1, NS == 3 ? set2 : set0, set1, Rz[0], Rx[0]);
+            if (NS == 3 && n + 2 < nc) side_step(n + 2, set0, set2, Rx[0], Rz[0]);
+        }
+        lds_barrier();
+        if ((nc - 1) & 1)   // a static pick of the register set (a selected array would live in scratch)
+            flush(nc - 1, Rz[0]);
+        else
+            flush(nc - 1, Rx[0]);
+    }
+}
+
 template <int D, int CS>
 struct Dh3Layout {
     static constexpr int DC = D / CS, NS = 3;
@@ -1943,6 +2264,17 @@ template <int D> struct RowSplit { static constexpr int CS = (D >= 128) ? 4 : 2;
 
 template <int D, typename ST, int MODE>
 static hipError_t launch_recur_t(const RecurArgs& a, hipStream_t st) {
+    if (a.y != nullptr) {
+        // the forward with the gated RMSNorm fused into the O store: kernels whose
+        // workgroup holds whole output rows
+        if constexpr (MODE == 0 && std::is_same<ST, uint16_t>::value && D == 64)
+            hipLaunchKernelGGL((kda_recur5_kernel<D, true>), dim3(a.BH), dim3(1024), 0, st, a);
+        else if constexpr (MODE == 0 && std::is_same<ST, float>::value && D <= 64)
+            hipLaunchKernelGGL((kda_recur_kernel<D, ST, 3, 0, 1, true>), dim3(a.BH), dim3(256), 0, st, a);
+        else
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     if constexpr (std::is_same<ST, uint16_t>::value && D == 64) {
         constexpr int CS2 = RowSplit<D>::CS;
         hipLaunchKernelGGL((kda_recur4_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
@@ -1988,6 +2320,8 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
         return in_bf16 ? launch_recur_t<128, uint16_t, 0>(a, st) : launch_recur_t<128, float, 0>(a, st);
     return hipErrorInvalidValue;
 }
+
+bool recur_epilogue_supported(int D, int in_bf16) { return in_bf16 ? D == 64 : (D == 32 || D == 64); }
 
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st) {
     if (D == 32) return in_bf16 ? launch_dh_t<32, uint16_t>(a, st) : launch_dh_t<32, float>(a, st);

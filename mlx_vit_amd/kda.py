@@ -180,6 +180,53 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
     return dq, dk, dv, dg, dbeta, ds0
 
 
+def gated_supported(D: int, dtype: torch.dtype) -> bool:
+    """Whether ``kda_forward_gated`` has a fused kernel for this head size and dtype."""
+    return (dtype == torch.bfloat16 and D == 64) or (dtype == torch.float32 and D in (32, 64))
+
+
+def kda_forward_gated(q, k, v, g, beta, initial_state, gate: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                      train: bool = False, workspace: Optional[torch.Tensor] = None):
+    """The forward with the layer's output norm fused into the store of o
+    (``kda_fwd_gated``): ``y = rms_norm(o) * norm_weight * sigmoid(gate)`` per
+    head, the RMSNormGated the reference layer applies to the path's output
+    (nope_gdn_mlx.py:340-366, 880-885).  gate (B, T, H*D) in q's dtype.
+    Returns (y (B, T, H*D), o, final_state, workspace); with ``train`` the
+    workspace is the training pair's (pass it to ``kda_backward_train``)."""
+    _check_chunk(CHUNK)
+    q, k, v, g, beta, s0 = _prepare(q, k, v, g, beta, initial_state)
+    B, T, H, D = q.shape
+    if not gated_supported(D, q.dtype):
+        raise ValueError(f"kda_forward_gated: no fused kernel for head_dim={D} with {q.dtype}")
+    if tuple(gate.shape) != (B, T, H * D):
+        raise ValueError(f"gate shape {tuple(gate.shape)} != {(B, T, H * D)}")
+    if gate.dtype != q.dtype:
+        raise ValueError(f"gate has dtype {gate.dtype}; expected {q.dtype}")
+    if gate.device != q.device:
+        raise ValueError(f"gate is on {gate.device}, q on {q.device}")
+    epv = 16 // q.element_size()
+    if gate.stride(2) != 1 or gate.stride(1) % epv or gate.storage_offset() % epv or \
+            (B > 1 and gate.stride(0) != T * gate.stride(1)):
+        gate = gate.contiguous()
+    ld_z = gate.stride(1) if T > 0 else H * D
+    w = norm_weight.detach().to(device=q.device, dtype=torch.float32).contiguous()
+    if tuple(w.shape) != (D,):
+        raise ValueError(f"norm_weight shape {tuple(w.shape)} != {(D,)}")
+    lib = _lib.load()
+    dev = q.device
+    o = torch.empty_like(q)
+    y = torch.empty((B, T, H * D), dtype=q.dtype, device=dev)
+    s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    pass_ = _lib.KDA_PASS_TRAIN if train else _lib.KDA_PASS_FWD
+    ws = workspace if workspace is not None else _workspace(pass_, B, T, H, D, dev, q.dtype)
+    rc = lib.kda_fwd_gated(pass_, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(gate), ld_z,
+                           _ptr(w), float(eps), _ptr(o), _ptr(y), H * D, _ptr(s_final),
+                           B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                           _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "kda_fwd_gated")
+    return y, o, s_final, ws
+
+
 class ChunkKDAFunction(torch.autograd.Function):
     """Autograd wrapper (the role of mx.custom_function in
     nope_gdn_mlx.py:2725-2808).  When a gradient is needed the forward keeps its

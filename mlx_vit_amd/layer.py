@@ -14,8 +14,10 @@ and maps the result back to ``hidden``:
   layout (no head-folding transposes, nope_gdn_mlx.py:845-849);
 * the recurrence is ``compute_path='hip_chunkwise_kda'`` (``KDARecurrence``);
 * the epilogue ``rms_norm(o) * sigmoid(gate)`` (RMSNormGated,
-  nope_gdn_mlx.py:340-366, 880-885) is one HIP kernel,
-  ``kda_layer_gated_rmsnorm_fwd``, followed by the ``o_proj`` GEMM.
+  nope_gdn_mlx.py:340-366, 880-885) is applied by the recurrence kernel as it
+  stores o (``kda_fwd_gated``: bf16 at head_dim 64, fp32 at 32 and 64; the
+  standalone kernel ``kda_layer_gated_rmsnorm_fwd`` otherwise), followed by
+  the ``o_proj`` GEMM.
 
 Parameter names and shapes follow the reference (``q_conv1d.weight`` is
 ``(H*D, 4, 1)`` like MLX's depthwise Conv1d weight, ``A_log (H,)``,
@@ -32,7 +34,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from .kda import BWD_HEAD_DIMS, CHUNK, FWD_HEAD_DIMS, _DTYPE_CODE, _ptr, _stream
+from .kda import (BWD_HEAD_DIMS, CHUNK, FWD_HEAD_DIMS, _DTYPE_CODE, _ptr, _stream, gated_supported,
+                  kda_backward, kda_backward_train, kda_forward_gated)
 from .recurrence import GDN_HIP_PATH, HIP_PATH, KDARecurrence
 
 CONV_TAPS = 4
@@ -260,6 +263,37 @@ class GatedRMSNormFunction(torch.autograd.Function):
         return do, dz, dw.to(weight.dtype), None
 
 
+class ChunkKDAGatedFunction(torch.autograd.Function):
+    """The recurrence and the output norm as one autograd node: the forward
+    runs ``kda_fwd_gated`` (norm fused into the store of o; with a gradient
+    needed, the training forward, whose workspace the backward reuses), the
+    backward runs the norm's adjoint and then the recurrence's VJP."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, gate, norm_weight, eps):
+        train = any(ctx.needs_input_grad)
+        y, o, s_final, ws = kda_forward_gated(q, k, v, g, beta, initial_state, gate, norm_weight, eps, train=train)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state, o, gate, norm_weight)
+        ctx.ws = ws if train else None
+        ctx.eps = eps
+        ctx.has_state = initial_state is not None
+        return y, s_final
+
+    @staticmethod
+    def backward(ctx, dy, ds_final):
+        q, k, v, g, beta, s0, o, gate, w = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros(gate.shape, dtype=o.dtype, device=o.device)
+        do, dz, dw = gated_rmsnorm_backward(o, gate, w, ctx.eps, dy)
+        if ctx.ws is not None:
+            dq, dk, dv, dg, dbeta, ds0 = kda_backward_train(q, k, v, g, beta, s0, do, ds_final, ctx.ws)
+            ctx.ws = None
+        else:
+            dq, dk, dv, dg, dbeta, ds0 = kda_backward(q, k, v, g, beta, s0, do, ds_final)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+                ds0 if ctx.has_state else None, dz.to(gate.dtype), dw.to(w.dtype), None)
+
+
 class ShortCausalConv1d(nn.Module):
     """Parameter holder of one depthwise causal conv (nope_gdn_mlx.py:409-431):
     ``weight (channels, kernel_size, 1)`` U(+-1/sqrt(K)), ``bias (channels,)``
@@ -342,6 +376,9 @@ class GatedDeltaLayer(nn.Module):
         self.g_proj_2 = nn.Linear(head_dim, total, bias=True)
         self.o_norm = RMSNormGated(head_dim, eps=1e-5)
         self.o_proj = nn.Linear(total, hidden_size, bias=False)
+        # the output norm fused into the recurrence's store where a kernel has it
+        # (kda_fwd_gated); False runs the standalone norm kernels
+        self.fused_output_norm = True
 
     def produce(self, x: torch.Tensor):
         """(q, k, v, g, beta) for x (B, L, hidden): the layer's inputs to the
@@ -369,7 +406,13 @@ class GatedDeltaLayer(nn.Module):
         if x.dim() != 3 or x.shape[-1] != self.hidden_size:
             raise ValueError(f"x must be (B, L, {self.hidden_size}); got {tuple(x.shape)}")
         q, k, v, g, beta = self.produce(x)
-        o, new_state = self.recurrence(q, k, v, g, beta, state, compute_path)
         gate = self.g_proj_2(self.g_proj_1(x))
-        y = self.o_norm(o, gate)
+        path = compute_path or self.compute_path
+        if (self.fused_output_norm and path == HIP_PATH and self.channel_wise_decay and gate.dtype == q.dtype
+                and gated_supported(self.head_dim, q.dtype)):
+            y, new_state = ChunkKDAGatedFunction.apply(q, k, v, g, beta, state, gate, self.o_norm.weight,
+                                                       self.o_norm.eps)
+        else:
+            o, new_state = self.recurrence(q, k, v, g, beta, state, compute_path)
+            y = self.o_norm(o, gate)
         return self.o_proj(y), new_state

@@ -167,22 +167,95 @@ def test_gated_rmsnorm_parity(B, T, H, D, dtype):
     _check(errs, TOL[dtype], case)
 
 
+GATED_CASES = [
+    # B, T, H, D, dtype, with_state, train, gate column offset (a strided gate)
+    (2, 100, 3, 64, torch.bfloat16, True, False, 8),     # ragged last chunk
+    (1, 1, 4, 64, torch.bfloat16, False, True, 0),       # T = 1
+    (3, 64, 2, 64, torch.bfloat16, False, True, 8),      # one whole chunk
+    (2, 200, 12, 64, torch.bfloat16, True, True, 0),     # four chunks (the LDS sets wrap)
+    (2, 100, 3, 64, torch.float32, True, True, 4),
+    (1, 77, 2, 32, torch.float32, False, False, 0),
+]
+
+
+@pytest.mark.parametrize("B,T,H,D,dtype,with_state,train,pad", GATED_CASES)
+def test_fwd_gated_parity(B, T, H, D, dtype, with_state, train, pad):
+    """kda_fwd_gated: y against the fp64 C oracle's o followed by the fp64
+    gated RMSNorm; o and the final state bit-identical to the unfused forward
+    (kda_fwd / kda_fwd_train); y against the standalone norm kernel on that o;
+    with the training pass, kda_bwd_train on its workspace bit-identical to the
+    unfused training pair."""
+    from oracle import cref
+    from mlx_vit_amd import (gated_rmsnorm_forward, kda_backward_train, kda_forward, kda_forward_gated,
+                             kda_forward_train)
+    case = f"fwd_gated B={B} T={T} H={H} D={D} {dtype} state={with_state} train={train} pad={pad}"
+    print(case, flush=True)
+    x = R.make_inputs(B, T, H, D, dtype=dtype, seed=T + D, with_state=with_state, with_grad=True)
+    gen = torch.Generator().manual_seed(11)
+    wide = torch.randn(B, T, H * D + pad, generator=gen).to(dtype)
+    w = 1 + 0.1 * torch.randn(D, generator=gen)
+    d = {n: (None if t is None else t.to(DEV)) for n, t in x.items()}
+    args = (d["q"], d["k"], d["v"], d["g"], d["beta"], d["s0"])
+    wd = wide.to(DEV)
+    y, o, sf, ws = kda_forward_gated(*args, wd[..., pad:], w.to(DEV), 1e-5, train=train)
+    if train:
+        o_u, sf_u, ws_u = kda_forward_train(*args)
+    else:
+        o_u, sf_u = kda_forward(*args)
+    y_u = gated_rmsnorm_forward(o_u, wd[..., pad:], w.to(DEV), 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_u), f"{case}: o differs from the unfused forward"
+    assert torch.equal(sf, sf_u), f"{case}: final state differs from the unfused forward"
+    ref_o = cref.forward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"])["o"]
+    z = wide[..., pad:].double().reshape(B, T, H, D)
+    ref = LR.gated_rms_norm(ref_o, w.double(), z, 1e-5).reshape(B, T, H * D)
+    errs = {"y": _rel(y, ref), "y_vs_standalone": _rel(y, y_u)}
+    if train:
+        g1 = kda_backward_train(*args, d["do"], None, ws)
+        g2 = kda_backward_train(*args, d["do"], None, ws_u)
+        torch.cuda.synchronize()
+        for n, a, b in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), g1, g2):
+            assert torch.equal(a, b), f"{case}: {n} from the gated forward's workspace differs"
+    _check(errs, TOL[dtype], case)
+    assert errs["y_vs_standalone"] <= (2e-3 if dtype == torch.bfloat16 else 1e-6), case
+
+
+def test_fwd_gated_rejects():
+    """Unsupported head sizes and bad gate strides raise ValueError."""
+    from mlx_vit_amd import kda_forward_gated
+    x = R.make_inputs(1, 10, 2, 32, dtype=torch.bfloat16, seed=1)
+    d = {n: (None if t is None else t.to(DEV)) for n, t in x.items()}
+    z = torch.randn(1, 10, 64, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no fused kernel"):
+        kda_forward_gated(d["q"], d["k"], d["v"], d["g"], d["beta"], None, z, torch.ones(32, device=DEV), 1e-5)
+    x = R.make_inputs(1, 10, 2, 64, dtype=torch.bfloat16, seed=1)
+    d = {n: (None if t is None else t.to(DEV)) for n, t in x.items()}
+    with pytest.raises(ValueError, match="gate shape"):
+        kda_forward_gated(d["q"], d["k"], d["v"], d["g"], d["beta"], None, z, torch.ones(64, device=DEV), 1e-5)
+
+
 def _layer_params(layer):
     return {n: p.detach().cpu().double() for n, p in layer.named_parameters()}
 
 
-@pytest.mark.parametrize("dtype,with_state", [(torch.float32, False), (torch.float32, True),
-                                              (torch.bfloat16, False)])
-def test_layer_parity(dtype, with_state):
+@pytest.mark.parametrize("dtype,with_state,D,fused", [
+    (torch.float32, False, 32, True), (torch.float32, True, 32, True), (torch.bfloat16, False, 32, True),
+    (torch.float32, True, 64, True), (torch.float32, True, 64, False), (torch.bfloat16, True, 64, True),
+    (torch.bfloat16, True, 64, False)])
+def test_layer_parity(dtype, with_state, D, fused):
     """The whole GatedDeltaLayer (projections, producer, HIP recurrence, gated
     RMSNorm, o_proj) forward and backward against the fp64 restatement with
-    the step recurrence (nope_gdn_mlx.py:775-885 on the 'compiled' path)."""
+    the step recurrence (nope_gdn_mlx.py:775-885 on the 'compiled' path), with
+    the output norm fused into the recurrence's store where a kernel has it
+    (fused) or as the standalone kernel."""
     from mlx_vit_amd import GatedDeltaLayer
-    B, L, hidden, H, D = 2, 100, 96, 3, 32
-    case = f"layer B={B} L={L} hidden={hidden} H={H} D={D} {dtype} state={with_state}"
+    B, L, H = 2, 100, 3
+    hidden = H * D
+    case = f"layer B={B} L={L} hidden={hidden} H={H} D={D} {dtype} state={with_state} fused={fused}"
     print(case, flush=True)
     torch.manual_seed(3)
     layer = GatedDeltaLayer(hidden, H, D)
+    layer.fused_output_norm = fused
     with torch.no_grad():
         layer.dt_bias.normal_(0, 0.1)
         layer.o_norm.weight.normal_(1, 0.1)
