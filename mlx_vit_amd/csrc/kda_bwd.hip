@@ -515,12 +515,13 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
             for (int mq = m + 1; mq < NB; ++mq) sfx += Tb[mq];
             const float eqm = fac_eq(s, m, d);
+            // raw k and q of the lane's rows, column d (transposing reads)
+            ld_col4(&s.kr[0][0], LDK, BS * ct, BS * m, kx[mm]);
+            ld_col4(&s.ql[0][0], LDK, BS * ct, BS * m, qx[mm]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * m + 4 * g4 + e;
                 const float a_t = s.g[t][d], b_t = Tb[m] - a_t;
-                kx[mm][e] = ld1<ST>(&s.kr[t][d]);
-                qx[mm][e] = ld1<ST>(&s.ql[t][d]);
                 at[mm][e] = a_t;
                 el[mm][e] = kexp<PREC>(a_t);
                 er[mm][e] = unsafe ? 0.f : kexp<PREC>(b_t);
@@ -636,16 +637,8 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
             const Frag8 A = ldfrag<PREC, ST>(&sm.W[0][0], LDK, BS * m, 32 * ks);
-            uint16_t hv[8];   // B[k][n] = h[k][n], k in the fragment's slot order
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hv[e] = sh[(32 * ks + 4 * g4 + e) * LDK + BS * c + r16];
-                hv[4 + e] = sh[(32 * ks + 16 + 4 * g4 + e) * LDK + BS * c + r16];
-            }
-            Frag8 B;
-            B.h = __builtin_bit_cast(bf16x8, make_uint4(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16),
-                                                        hv[4] | ((uint32_t)hv[5] << 16), hv[6] | ((uint32_t)hv[7] << 16)));
-            P = mma<PREC>(A, B, P);
+            // B[k][n] = h[k][n]: h is stored with k along its rows, read transposed
+            P = mma<PREC>(A, ldfragT(sh, LDK, BS * c, 32 * ks), P);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -956,10 +949,7 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
             // Diagonal tiles of blocks in pmask are evaluated pair by pair below.
             auto colfrag = [&](const ST* M, int ld, int row0) __attribute__((always_inline)) {
                 // B[k][n] = M[row0 + k][d] for the lane's k = 4 g4 + 0..3, raw bf16
-                Frag4 f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) f.h[e] = (short)M[(row0 + 4 * g4 + e) * ld + d];
-                return f;
+                return ldfrag4T_tr(M, ld, BS * ct, row0);
             };
 #pragma unroll
             for (int mm = 0; mm < MB; ++mm) {
@@ -991,12 +981,14 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                 // dgamma: weight by the bf16 values the column side's MFMAs read
                 // (K_l, Q_l of row t) so that each pair cancels exactly in the
                 // reverse cumsum, whatever the decay span
+                float klv[4], qlv[4];
+                ld_col4(&s.kl[0][0], LDK, BS * ct, BS * i, klv);
+                ld_col4(&s.ql[0][0], LDK, BS * ct, BS * i, qlv);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int t = BS * i + 4 * g4 + e;
                     dka[mm][e] += dKl[e] * el[mm][e];
                     dqa[mm][e] += dQl[e] * el[mm][e];
-                    dga[mm][e] += dKl[e] * ld1<ST>(&s.kl[t][d]) + dQl[e] * ld1<ST>(&s.ql[t][d]);
+                    dga[mm][e] += dKl[e] * klv[e] + dQl[e] * qlv[e];
                 }
             }
 #pragma unroll
@@ -1021,11 +1013,12 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
                     for (int e = 0; e < 4; ++e) dKr[e] += P[e] * fs;
                 }
+                float krv[4];   // the row side's B operand (K_r of row s, raw bf16)
+                ld_col4(&s.kr[0][0], LDK, BS * ct, BS * j, krv);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     dka[mm][e] += dKr[e] * er[mm][e];
-                    // the row side's B operand (K_r of row s, raw bf16)
-                    dga[mm][e] -= dKr[e] * ld1<ST>(&s.kr[BS * j + 4 * g4 + e][d]);
+                    dga[mm][e] -= dKr[e] * krv[e];
                 }
             }
             // Diagonal tiles of own blocks in pmask & ~qmask, with the 4-row

@@ -29,6 +29,7 @@ namespace kda {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
+typedef short short8v __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int C = 64;       // chunk length (tokens)
@@ -275,6 +276,44 @@ __device__ __forceinline__ Frag4 ldfrag4T(const ST* M, int ld, int row0, int k0)
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = ld1<ST>(M + (size_t)(k0 + 4 * g + e) * ld + row0 + r);
     return frag4_from_f32<PREC>(v);
+}
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  In each group of 16
+// lanes the sixteen 8-byte pieces the lanes address are 64 16-bit elements in
+// lane order (the piece of lane j holds positions 4 j .. 4 j + 3), and lane i
+// of the group receives positions i, 16 + i, 32 + i, 48 + i.  So when lane j of
+// group g addresses row k0 + 4 g + j / 4, columns n0 + 4 (j % 4) .. + 3 of a
+// row-major bf16 tile M[k][n], lane (n = i, g) receives M[k0 + 4 g + e][n0 + i],
+// e = 0..3: the k-slots 4 g .. 4 g + 3 of an MFMA operand that is stored with k
+// along the rows (the lane layout was checked on the device with in-bounds
+// addresses).  Each address must be 8-byte aligned.
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+__device__ __forceinline__ short4v ld_tr4(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(const_cast<uint16_t*>(p)));
+}
+// B fragment (16x16x32, ldfrag's k-slot order) B[k][n] = M[k0 + k][n0 + n] of a
+// row-major bf16 tile whose rows are k (row stride ld elements)
+__device__ __forceinline__ Frag8 ldfragT(const uint16_t* M, int ld, int n0, int k0) {
+    const int l = lane_id(), j = l & 15, g = l >> 4;
+    const uint16_t* p = M + (size_t)(k0 + 4 * g + (j >> 2)) * ld + n0 + 4 * (j & 3);
+    const short4v x = ld_tr4(p), y = ld_tr4(p + (size_t)16 * ld);
+    Frag8 f;
+    f.h = __builtin_bit_cast(bf16x8, short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
+    return f;
+}
+// the same for a 16x16x16 operand (k-slots 4 g .. 4 g + 3)
+__device__ __forceinline__ Frag4 ldfrag4T_tr(const uint16_t* M, int ld, int n0, int k0) {
+    const int l = lane_id(), j = l & 15, g = l >> 4;
+    Frag4 f;
+    f.h = ld_tr4(M + (size_t)(k0 + 4 * g + (j >> 2)) * ld + n0 + 4 * (j & 3));
+    return f;
+}
+// four rows k0 + 4 g + e, e = 0..3, of column n0 + (l % 16) as floats
+__device__ __forceinline__ void ld_col4(const uint16_t* M, int ld, int n0, int k0, float* v) {
+    const int l = lane_id(), j = l & 15, g = l >> 4;
+    const short4v x = ld_tr4(M + (size_t)(k0 + 4 * g + (j >> 2)) * ld + n0 + 4 * (j & 3));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = bf2f((uint16_t)x[e]);
 }
 
 // ldfrag with every k-slot multiplied by scale[k - k0]
