@@ -63,9 +63,12 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
     const size_t CD = N * kda::C * D * es, CC = N * kda::C * kda::C * es, DD = N * (size_t)D * D * es;
     const size_t TI = N * kda::NB * kda::BS * kda::BS * 4, EG = N * D * 4;
     size_t sz[KDA_WS_NREGIONS] = {0};
+    // bf16 D = 64: the recurrences read Kb through transposing LDS reads, no Kb^T
+    const bool no_kbt = dtype == KDA_DTYPE_BF16 && D == 64;
     sz[KDA_WS_W] = CD;
     sz[KDA_WS_U] = CD;
-    sz[KDA_WS_KBT] = CD;
+    sz[KDA_WS_KBT] = no_kbt ? 0 : CD;
+    sz[KDA_WS_KB] = no_kbt ? CD : 0;
     sz[KDA_WS_EG] = EG;
     if (pass != KDA_PASS_BWD) {
         sz[KDA_WS_QP] = CD;
@@ -331,6 +334,7 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     ra.U = region(workspace, L, KDA_WS_U);
     ra.Qp = region(workspace, L, KDA_WS_QP);
     ra.KbT = region(workspace, L, KDA_WS_KBT);
+    ra.Kb = region(workspace, L, KDA_WS_KB);
     ra.Aqk = region(workspace, L, KDA_WS_AQK);
     ra.eG = fregion(workspace, L, KDA_WS_EG);
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
@@ -421,6 +425,7 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
     if (!(pass == KDA_PASS_TRAIN && kda::fwd_writes_states(D, in_bf16))) {
         kda::RecurArgs ra = {};
         ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
+        ra.Kb = region(workspace, L, KDA_WS_KB);
         ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
         e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
         if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");

@@ -293,6 +293,14 @@ __device__ __forceinline__ short4v ld_tr4(const uint16_t* p) {
 }
 // B fragment (16x16x32, ldfrag's k-slot order) B[k][n] = M[k0 + k][n0 + n] of a
 // row-major bf16 tile whose rows are k (row stride ld elements)
+__device__ __forceinline__ Frag8 ldfragT(const uint16_t* M, int ld, int n0, int k0) {
+    const int l = lane_id(), j = l & 15, g = l >> 4;
+    const uint16_t* p = M + (size_t)(k0 + 4 * g + (j >> 2)) * ld + n0 + 4 * (j & 3);
+    const short4v x = ld_tr4(p), y = ld_tr4(p + (size_t)16 * ld);
+    Frag8 f;
+    f.h = __builtin_bit_cast(bf16x8, short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
+    return f;
+}
 // Eight consecutive rows of one column of an [n][ld] bf16 LDS tile X, for
 // writing its transpose as 16-byte row pieces: lane i of each 16-lane group
 // receives X[n0 + 8 (i / 4) + c][k0 + i % 4], c = 0..7, with two transposing
@@ -305,14 +313,17 @@ __device__ __forceinline__ short8v ld_tr_rows8(const uint16_t* X, int ld, int n0
     return short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
 }
 
-__device__ __forceinline__ Frag8 ldfragT(const uint16_t* M, int ld, int n0, int k0) {
-    const int l = lane_id(), j = l & 15, g = l >> 4;
-    const uint16_t* p = M + (size_t)(k0 + 4 * g + (j >> 2)) * ld + n0 + 4 * (j & 3);
-    const short4v x = ld_tr4(p), y = ld_tr4(p + (size_t)16 * ld);
-    Frag8 f;
-    f.h = __builtin_bit_cast(bf16x8, short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
-    return f;
+// The same for a 16-row tile X[16][ld]: lane i of each 16-lane group receives
+// X[8 ((i / 4) % 2) + c][k0 + 4 (i / 8) + i % 4], c = 0..7 (the group covers
+// columns k0..k0+7 of all 16 rows).  Row k0 + 4 (i / 8) + i % 4 of the
+// transpose, its columns 8 ((i / 4) % 2) .. + 7.
+__device__ __forceinline__ short8v ld_tr_rows8_16(const uint16_t* X, int ld, int k0) {
+    const int j = lane_id() & 15, a = j & 3;
+    const uint16_t* p = X + (size_t)(8 * (a & 1) + (j >> 2)) * ld + k0 + 4 * (a >> 1);
+    const short4v x = ld_tr4(p), y = ld_tr4(p + (size_t)4 * ld);
+    return short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
 }
+
 // the same for a 16x16x16 operand (k-slots 4 g .. 4 g + 3)
 __device__ __forceinline__ Frag4 ldfrag4T_tr(const uint16_t* M, int ld, int n0, int k0) {
     const int l = lane_id(), j = l & 15, g = l >> 4;
@@ -714,6 +725,30 @@ __device__ __forceinline__ Frag8 ldfrag_sw(const uint16_t* M, int row0, int k0) 
     f.h = __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
     return f;
 }
+// ldfragT on a swizzled tile: the A (or B) fragment whose row (n) index runs
+// along the tile's columns n0.. and whose k index along its rows k0..  Each
+// lane's 8-byte piece lies inside one 16-byte chunk, which the swizzle keeps
+// whole.
+template <int RB>
+__device__ __forceinline__ Frag8 ldfragT_sw(const uint16_t* M, int n0, int k0) {
+    const int l = lane_id(), j = l & 15, g = l >> 4, r = k0 + 4 * g + (j >> 2), b = 2 * (n0 + 4 * (j & 3));
+    const char* base = reinterpret_cast<const char*>(M);
+    const short4v x = ld_tr4(reinterpret_cast<const uint16_t*>(base + Swz<RB>::at(r, b)));
+    const short4v y = ld_tr4(reinterpret_cast<const uint16_t*>(base + Swz<RB>::at(r + 16, b)));
+    Frag8 f;
+    f.h = __builtin_bit_cast(bf16x8, short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
+    return f;
+}
+// ld_col4 on a swizzled tile: rows k0 + 4 g + e of column n0 + (l % 16), the
+// accumulator layout of a 16-row block
+template <int RB>
+__device__ __forceinline__ f32x4 ld_col4_sw(const uint16_t* M, int n0, int k0) {
+    const int l = lane_id(), j = l & 15, g = l >> 4;
+    const short4v x = ld_tr4(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(M) +
+                                                                Swz<RB>::at(k0 + 4 * g + (j >> 2), 2 * (n0 + 4 * (j & 3)))));
+    return f32x4{bf2f((uint16_t)x[0]), bf2f((uint16_t)x[1]), bf2f((uint16_t)x[2]), bf2f((uint16_t)x[3])};
+}
+
 // one bf16 element (row r, column c) of a swizzled tile, as float
 template <int RB>
 __device__ __forceinline__ float ld_sw(const uint16_t* M, int r, int c) {

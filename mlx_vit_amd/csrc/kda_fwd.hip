@@ -26,7 +26,7 @@ namespace kda {
 //             MFMA, or pair by pair beyond the 4-row guard too (every pair for
 //             a chunk with g > 0)
 //   pass A    row-major threads (t, 8 channels): block-end anchored operands
-//             kl, ql, kr in place; Qp (forward) / Kb (backward) as 16-byte stores
+//             kl, ql, kr in place; Qp, Kb (where requested) as 16-byte stores
 //   pass B    column threads (d, 8 tokens): KbT, QpT as 16-byte stores
 //   products  Akk -> fp32 LDS, Aqk -> LDS staging -> coalesced stores
 //   inverse   diagonal 16x16 blocks of I + L in registers
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                     oql[e] = qf * el;
                     okr[e] = unsafe ? kf : kf * kexp<PREC>(bt);
                     oqp[e] = oql[e] * fac_ep(s, blk, d);
-                    if (bwd) {
+                    if (oKb) {
                         if (unsafe) {
                             float gsfx = bt;   // G - gamma_t
                             for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];

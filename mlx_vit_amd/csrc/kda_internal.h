@@ -6,6 +6,8 @@
 // inputs) except eG, Akk and Tii, which are always fp32:
 //   W, U, Qp, Kb, Vp, dVp      [C][D]  row-major (token, channel)
 //   WT, QpT, KbT               [D][C]  transposed copies for MFMA A operands
+//                                      (bf16 D = 64: no KbT; its kernels read Kb
+//                                      with transposing LDS reads)
 //   Aqk                        [C][C]  (token t, token s), zero above the diagonal
 //   AqkT                       [C][C]  transpose of Aqk
 //   Akk                        [C][C]  fp32, strictly lower, without the beta row scale
@@ -29,6 +31,7 @@ struct PrepArgs {
 
 struct RecurArgs {
     const void *W, *U, *Qp, *KbT, *Aqk;
+    const void* Kb;   // bf16 D = 64 kernels read Kb (transposed in LDS) instead of Kb^T
     const float* eG;
     const float* s0;
     float* s_final;

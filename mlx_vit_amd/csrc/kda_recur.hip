@@ -1103,7 +1103,7 @@ struct Recur3Layout {
     static constexpr int W_OFF = 0;                                           // [C][D]
     static constexpr int U_OFF = W_OFF + C * RB_W;                            // [C][DC]
     static constexpr int QP_OFF = U_OFF + C * RB_U;                           // [C][D]   (MODE 0)
-    static constexpr int KBT_OFF = QP_OFF + (MODE == 0 ? C * RB_W : 0);        // [D][C]
+    static constexpr int KBT_OFF = QP_OFF + (MODE == 0 ? C * RB_W : 0);        // Kb^T [D][C] (recur3), Kb [C][D] (recur4)
     static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                        // [C][C]   (MODE 0)
     static constexpr int EG_OFF = AQK_OFF + (MODE == 0 ? C * RB_C : 0);        // [D] fp32
     static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
@@ -1366,7 +1366,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
 // = waves 4-7.  Wave wr = w % 4 of a role owns row block wr of the chunk tiles.
 //   chain waves: V' = U - W S (row block wr), write V'^T; after B: state update
 //                of state rows wr, wr + 4, write S^T (MODE 1: and h); read the
-//                next chunk's W, U, Kb^T, e^G operands
+//                next chunk's W, U, Kb^T (transposing reads of Kb), e^G operands
 //   role-1 waves: flush the previous chunk's outputs; MODE 0: O = Qp S + Aqk V'
 //                (row block wr) after B, read the next chunk's Qp, Aqk operands
 //   MODE 2: the forward of MODE 0 that also writes the chunk-start states h:
@@ -1401,7 +1401,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
     const char* gW = static_cast<const char*>(a.W);
     const char* gU = static_cast<const char*>(a.U);
     const char* gQp = static_cast<const char*>(a.Qp);
-    const char* gKbT = static_cast<const char*>(a.KbT);
+    const char* gKb = static_cast<const char*>(a.Kb);
     const char* gAqk = static_cast<const char*>(a.Aqk);
     const char* gEg = reinterpret_cast<const char*>(a.eG);
 
@@ -1411,22 +1411,20 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
     ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
     ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
 
-    using TW = DmaTile<C, RB_W, 4>;
+    using TW = DmaTile<C, RB_W, 4>;   // W, Kb, Qp
     using TU = DmaTile<C, RB_U, 4>;
-    using TK = DmaTile<D, RB_C, 4>;
     using TA = DmaTile<C, RB_C, 4>;
-    // which role brings the state-chain slabs (W, U, Kb^T, e^G) and how many DMA
+    // which role brings the state-chain slabs (W, U, Kb, e^G) and how many DMA
     // instructions per chunk this wave issues
     constexpr int CHAIN_ROLE = FWD ? 0 : 1;
-    constexpr int L_CHAIN = TW::COUNT + TU::COUNT + TK::COUNT + 1;
+    constexpr int L_CHAIN = 2 * TW::COUNT + TU::COUNT + 1;
     constexpr int L_OUT = FWD ? TW::COUNT + TA::COUNT : 0;
     constexpr int L0 = (CHAIN_ROLE == 0) ? L_CHAIN : 0;
     constexpr int L1 = ((CHAIN_ROLE == 1) ? L_CHAIN : 0) + L_OUT;
     const bool chain_dma = role == CHAIN_ROLE;
-    uint32_t oW[TW::COUNT], oU[TU::COUNT], oK[TK::COUNT], oA[TA::COUNT];
+    uint32_t oW[TW::COUNT], oU[TU::COUNT], oA[TA::COUNT];
     TW::offsets(oW, RB_W, wr, l);
     TU::offsets(oU, (size_t)D * 2, wr, l);
-    TK::offsets(oK, RB_C, wr, l);
     TA::offsets(oA, RB_C, wr, l);
     const uint32_t oE = (uint32_t)((D / 4) * 4 * wr + 16 * (l < D / 16 ? l : 0));
     auto dma_chunk = [&](int c, char* sbp) __attribute__((always_inline)) {
@@ -1435,7 +1433,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
         if (chain_dma) {
             TW::issue_s32(gW + ch * C * D * 2, oW, sb + Lay::W_OFF, wr);
             TU::issue_s32(gU + (ch * C * D + c0) * 2, oU, sb + Lay::U_OFF, wr);
-            TK::issue_s32(gKbT + ch * C * D * 2, oK, sb + Lay::KBT_OFF, wr);
+            TW::issue_s32(gKb + ch * C * D * 2, oW, sb + Lay::KBT_OFF, wr);   // Kb, [C][D]
             if (l < D / 16) dma16_s32(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + D * wr);
         }
         if constexpr (FWD) {
@@ -1514,7 +1512,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
         for (int i = 0; i < MT; ++i)
             if (own[i]) {
 #pragma unroll
-                for (int ks = 0; ks < C / 32; ++ks) Akb[i][ks] = ldfrag_sw<RB_C>(sKbT, BS * mt[i], 32 * ks);
+                for (int ks = 0; ks < C / 32; ++ks) Akb[i][ks] = ldfragT_sw<RB_W>(sKbT, BS * mt[i], 32 * ks);
                 eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
             }
     };
@@ -1685,8 +1683,8 @@ struct Recur5Layout {
     static constexpr int W_OFF = 0;                                    // [C][D]
     static constexpr int U_OFF = W_OFF + C * RB;                       // [C][D]
     static constexpr int QP_OFF = U_OFF + C * RB;                      // [C][D]
-    static constexpr int KBT_OFF = QP_OFF + C * RB;                    // [D][C]
-    static constexpr int AQK_OFF = KBT_OFF + D * RB_C;                 // [C][C]
+    static constexpr int KB_OFF = QP_OFF + C * RB;                     // [C][D]
+    static constexpr int AQK_OFF = KB_OFF + C * RB;                    // [C][C]
     static constexpr int EG_OFF = AQK_OFF + C * RB_C;                  // [D] fp32
     static constexpr int Z_OFF = EG_OFF + 4 * D;                       // [C][D] gate rows (EPI)
     static constexpr int SET_BYTES = ((EPI ? Z_OFF + C * RB : Z_OFF) + 1023) & ~1023;
@@ -1723,7 +1721,7 @@ __global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
     const char* gW = static_cast<const char*>(a.W);
     const char* gU = static_cast<const char*>(a.U);
     const char* gQp = static_cast<const char*>(a.Qp);
-    const char* gKbT = static_cast<const char*>(a.KbT);
+    const char* gKb = static_cast<const char*>(a.Kb);
     const char* gAqk = static_cast<const char*>(a.Aqk);
     const char* gEg = reinterpret_cast<const char*>(a.eG);
 
@@ -1734,9 +1732,9 @@ __global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
     ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
 
     // every slab tile is eight 1 KB blocks: one per chain wave
-    using TR = DmaTile<C, RB, 8>;     // W, U, Qp
-    using TC = DmaTile<D, RB_C, 8>;   // Kb^T, Aqk
-    constexpr int L_CHAIN = 3 * TR::COUNT + 2 * TC::COUNT + 1 + (EPI ? 1 : 0);   // + e^G (32 B), gate rows
+    using TR = DmaTile<C, RB, 8>;     // W, U, Qp, Kb
+    using TC = DmaTile<D, RB_C, 8>;   // Aqk
+    constexpr int L_CHAIN = 4 * TR::COUNT + TC::COUNT + 1 + (EPI ? 1 : 0);   // + e^G (32 B), gate rows
     static_assert(C == D && 4 * D == 8 * 32, "square tiles; e^G: two 16-byte lanes per chain wave");
     uint32_t oR[TR::COUNT], oC[TC::COUNT];
     TR::offsets(oR, RB, chain ? w : 0, l);
@@ -1748,7 +1746,7 @@ __global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
         const uint32_t sb = lds_addr(sbp);
         TR::issue_s32(gW + ch * C * D * 2, oR, sb + Lay::W_OFF, w);
         TR::issue_s32(gU + ch * C * D * 2, oR, sb + Lay::U_OFF, w);
-        TC::issue_s32(gKbT + ch * C * D * 2, oC, sb + Lay::KBT_OFF, w);
+        TR::issue_s32(gKb + ch * C * D * 2, oR, sb + Lay::KB_OFF, w);
         if (l < 2) dma16_s32(gEg + ch * D * 4, oE, sb + Lay::EG_OFF + 32 * w);
         TR::issue_s32(gQp + ch * C * D * 2, oR, sb + Lay::QP_OFF, w);
         TC::issue_s32(gAqk + ch * C * C * 2, oC, sb + Lay::AQK_OFF, w);
@@ -1767,7 +1765,8 @@ __global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
 
     // Registers carried from one chunk step to the next, shared by the roles:
     //   Ax: chain W rows (A of V' = U - W S), side Qp rows;
-    //   Ay: chain Kb^T rows (A of the state update), side Aqk rows;
+    //   Ay: chain Kb^T rows (A of the state update, transposing reads of Kb),
+    //       side Aqk rows;
     //   Rx: chain U of its rows and columns, side (EPI) its flush piece of the
     //       gate rows of even chunks, as raw bits (Rz[0]: odd chunks).
     Frag8 Ax[D / 32], Ay[2];
@@ -1825,9 +1824,9 @@ __global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
 
     // one chunk's A operands, read ahead from its LDS set
     auto preload_kb = [&](const char* sb) __attribute__((always_inline)) {   // chain waves
-        const ST* sKbT = reinterpret_cast<const ST*>(sb + Lay::KBT_OFF);
+        const ST* sKb = reinterpret_cast<const ST*>(sb + Lay::KB_OFF);
 #pragma unroll
-        for (int ks = 0; ks < C / 32; ++ks) Ay[ks] = ldfrag_sw<RB_C>(sKbT, BS * wr, 32 * ks);
+        for (int ks = 0; ks < C / 32; ++ks) Ay[ks] = ldfragT_sw<RB>(sKb, BS * wr, 32 * ks);
         eg = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(sb + Lay::EG_OFF) + BS * wr + 4 * g4);
     };
     auto preload_chain = [&](const char* sb) __attribute__((always_inline)) {
@@ -2305,6 +2304,7 @@ static hipError_t launch_recur_t(const RecurArgs& a, hipStream_t st) {
         return hipGetLastError();
     }
     if constexpr (std::is_same<ST, uint16_t>::value && D == 64) {
+        if (a.Kb == nullptr) return hipErrorInvalidValue;
         constexpr int CS2 = RowSplit<D>::CS;
         if (MODE == 0 && a.h)   // the training forward: O and the chunk-start states
             hipLaunchKernelGGL((kda_recur4_kernel<D, 2, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);

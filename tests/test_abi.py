@@ -40,12 +40,13 @@ def test_workspace_sizes():
     fwd = lib.kda_workspace_size(0, 8, 1568, 12, 64, 64, 1)
     bwd = lib.kda_workspace_size(1, 8, 1568, 12, 64, 64, 1)
     N = 8 * 12 * 25
-    # forward: W, U, Qp, KbT (C*D) + Aqk (C*C) in the input dtype, eG (D) in fp32
+    # forward: W, U, Qp, Kb (bf16; fp32: KbT) (C*D) + Aqk (C*C) in the input dtype, eG (D) in fp32
     assert fwd == 2 * (4 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
     assert lib.kda_workspace_size(0, 8, 1568, 12, 64, 64, 0) == 4 * (4 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
-    # backward, bf16: W, U, KbT, WT, QpT, Kb, dVp (C*D), h, dh (D*D), AqkT (C*C) in bf16 and
-    # eG (D) in fp32; the forward's Qp and Aqk are not kept
-    assert bwd == 2 * (7 * N * 64 * 64 + 2 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
+    # backward, bf16: W, U, WT, QpT, Kb, dVp (C*D), h, dh (D*D), AqkT (C*C) in bf16 and
+    # eG (D) in fp32; the forward's Qp and Aqk are not kept, and no KbT (the
+    # recurrences read Kb transposed)
+    assert bwd == 2 * (6 * N * 64 * 64 + 2 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
     assert bwd > fwd
     # backward, fp32: also V' (C*D), Akk (C*C) and the diagonal-block inverses (4*16*16)
     bwd32 = lib.kda_workspace_size(1, 8, 1568, 12, 64, 64, 0)
