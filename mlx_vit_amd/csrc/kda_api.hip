@@ -63,22 +63,23 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
     const size_t CD = N * kda::C * D * es, CC = N * kda::C * kda::C * es, DD = N * (size_t)D * D * es;
     const size_t TI = N * kda::NB * kda::BS * kda::BS * 4, EG = N * D * 4;
     size_t sz[KDA_WS_NREGIONS] = {0};
-    // bf16 D = 64: the recurrences read Kb through transposing LDS reads, no Kb^T
-    const bool no_kbt = dtype == KDA_DTYPE_BF16 && D == 64;
+    // bf16 D = 64: the recurrences read Kb, Qp, W and Aqk through transposing LDS
+    // reads, so no transposed slab exists and both passes use Qp and Aqk
+    const bool tr = dtype == KDA_DTYPE_BF16 && D == 64;
     sz[KDA_WS_W] = CD;
     sz[KDA_WS_U] = CD;
-    sz[KDA_WS_KBT] = no_kbt ? 0 : CD;
-    sz[KDA_WS_KB] = no_kbt ? CD : 0;
+    sz[KDA_WS_KBT] = tr ? 0 : CD;
+    sz[KDA_WS_KB] = tr ? CD : 0;
     sz[KDA_WS_EG] = EG;
-    if (pass != KDA_PASS_BWD) {
+    if (pass != KDA_PASS_BWD || tr) {
         sz[KDA_WS_QP] = CD;
         sz[KDA_WS_AQK] = CC;
     }
     if (pass != KDA_PASS_FWD) {
-        sz[KDA_WS_WT] = CD;
-        sz[KDA_WS_QPT] = CD;
+        sz[KDA_WS_WT] = tr ? 0 : CD;
+        sz[KDA_WS_QPT] = tr ? 0 : CD;
         sz[KDA_WS_KB] = CD;
-        sz[KDA_WS_AQKT] = CC;
+        sz[KDA_WS_AQKT] = tr ? 0 : CC;
         sz[KDA_WS_H] = DD;
         sz[KDA_WS_DH] = DD;
         sz[KDA_WS_DVP] = CD;
@@ -433,6 +434,9 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
 
     kda::DhArgs da = {};
     da.AqkT = region(workspace, L, KDA_WS_AQKT);
+    da.Aqk = region(workspace, L, KDA_WS_AQK);
+    da.Qp = region(workspace, L, KDA_WS_QP);
+    da.W = W;
     da.Kb = region(workspace, L, KDA_WS_KB);
     da.QpT = region(workspace, L, KDA_WS_QPT);
     da.WT = region(workspace, L, KDA_WS_WT);

@@ -77,7 +77,6 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     ST* oWT = static_cast<ST*>(a.WT);
     ST* oAqk = static_cast<ST*>(a.Aqk);
     ST* oAqkT = static_cast<ST*>(a.AqkT);
-    const bool bwd = oAqkT != nullptr;
     // four consecutive elements of a transposed output row, straight from an MFMA
     // accumulator (lane (g, n) holds rows 4 g .. 4 g + 3 of column n)
     auto st4 = [](ST* p, const float* x) __attribute__((always_inline)) {

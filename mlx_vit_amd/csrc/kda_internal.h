@@ -6,10 +6,11 @@
 // inputs) except eG, Akk and Tii, which are always fp32:
 //   W, U, Qp, Kb, Vp, dVp      [C][D]  row-major (token, channel)
 //   WT, QpT, KbT               [D][C]  transposed copies for MFMA A operands
-//                                      (bf16 D = 64: no KbT; its kernels read Kb
-//                                      with transposing LDS reads)
+//                                      (bf16 D = 64: none of them; its kernels
+//                                      read Kb, Qp, W, Aqk with transposing LDS
+//                                      reads)
 //   Aqk                        [C][C]  (token t, token s), zero above the diagonal
-//   AqkT                       [C][C]  transpose of Aqk
+//   AqkT                       [C][C]  transpose of Aqk (not at bf16 D = 64)
 //   Akk                        [C][C]  fp32, strictly lower, without the beta row scale
 //   Tii                        [4][16][16] fp32 inverses of the diagonal blocks of I + L
 //   eG                         [D]     fp32, e^{gamma of the chunk's last row}
@@ -52,6 +53,7 @@ struct RecurArgs {
 
 struct DhArgs {
     const void *AqkT, *Kb, *QpT, *WT;
+    const void *Aqk, *Qp, *W;   // bf16 D = 64 reads these transposed instead of the T slabs
     const float* eG;
     const void* dout;
     const float* dsf;

@@ -1973,11 +1973,12 @@ template <int D, int CS>
 struct Dh3Layout {
     static constexpr int DC = D / CS, NS = 3;
     static constexpr int RB_D = 2 * D, RB_C = 2 * C, RB_U = 2 * DC;
-    static constexpr int AQKT_OFF = 0;                                        // [C][C]
-    static constexpr int KB_OFF = AQKT_OFF + C * RB_C;                        // [C][D]
-    static constexpr int QPT_OFF = KB_OFF + C * RB_D;                         // [D][C]
-    static constexpr int WT_OFF = QPT_OFF + D * RB_C;                         // [D][C]
-    static constexpr int DO_OFF = WT_OFF + D * RB_C;                          // [C][DC] (t, own columns)
+    // Aqk, Qp and W are read transposed (Aqk^T, Qp^T, W^T) with transposing LDS reads
+    static constexpr int AQK_OFF = 0;                                         // [C][C]
+    static constexpr int KB_OFF = AQK_OFF + C * RB_C;                         // [C][D]
+    static constexpr int QP_OFF = KB_OFF + C * RB_D;                          // [C][D]
+    static constexpr int W_OFF = QP_OFF + C * RB_D;                           // [C][D]
+    static constexpr int DO_OFF = W_OFF + C * RB_D;                           // [C][DC] (t, own columns)
     static constexpr int EG_OFF = DO_OFF + C * RB_U;                          // [D] fp32
     static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
     // Staging rows (LDU) keep a 16-byte pad for 16-byte row access.  The
@@ -1993,8 +1994,8 @@ struct Dh3Layout {
     static constexpr int NSTG = 3;
     static constexpr int XBYTES = STG_OFF + NSTG * STG_BYTES;
     static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "reverse recurrence LDS");
-    static constexpr int L = DmaTile<C, RB_C, 4>::COUNT + DmaTile<C, RB_D, 4>::COUNT + 2 * DmaTile<D, RB_C, 4>::COUNT +
-                             DmaTile<C, RB_U, 4>::COUNT + 1;
+    static constexpr int L =
+        DmaTile<C, RB_C, 4>::COUNT + 3 * DmaTile<C, RB_D, 4>::COUNT + DmaTile<C, RB_U, 4>::COUNT + 1;
 };
 
 // ----------------------------------------------------------------------------
@@ -2045,10 +2046,10 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     const int bh = lb / CS, c0 = (lb - bh * CS) * DC;
     const int b = bh / a.H, h = bh - b * a.H;
     const int nc = a.nc;
-    const char* gAqkT = static_cast<const char*>(a.AqkT);
+    const char* gAqk = static_cast<const char*>(a.Aqk);
     const char* gKb = static_cast<const char*>(a.Kb);
-    const char* gQpT = static_cast<const char*>(a.QpT);
-    const char* gWT = static_cast<const char*>(a.WT);
+    const char* gQp = static_cast<const char*>(a.Qp);
+    const char* gW = static_cast<const char*>(a.W);
     const char* gdO = static_cast<const char*>(a.dout);
     const char* gEg = reinterpret_cast<const char*>(a.eG);
 
@@ -2062,15 +2063,13 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
 
     // step k's slabs (chunk nc-1-k) -> LDS set (k % NS), by the role-1 waves
-    using TA = DmaTile<C, RB_C, 4>;
-    using TB = DmaTile<C, RB_D, 4>;
-    using TQ = DmaTile<D, RB_C, 4>;
+    using TA = DmaTile<C, RB_C, 4>;   // Aqk
+    using TB = DmaTile<C, RB_D, 4>;   // Kb, Qp, W
     using TO = DmaTile<C, RB_U, 4>;
     constexpr int L = B3::L;
-    uint32_t oA[TA::COUNT], oB[TB::COUNT], oQ[TQ::COUNT], oO[TO::COUNT];
+    uint32_t oA[TA::COUNT], oB[TB::COUNT], oO[TO::COUNT];
     TA::offsets(oA, RB_C, wr, l);
     TB::offsets(oB, RB_D, wr, l);
-    TQ::offsets(oQ, RB_C, wr, l);
     TO::offsets(oO, (size_t)a.H * D * 2, wr, l);
     const uint32_t oE = (uint32_t)((D / 4) * 4 * wr + 16 * (l < D / 16 ? l : 0));
     auto dma_step = [&](int k, char* sbp) __attribute__((always_inline)) {
@@ -2078,10 +2077,10 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
         const size_t ch = (size_t)bh * nc + n;
         const int t0 = n * C, valid = min(C, a.T - t0);
         const uint32_t sb = lds_addr(sbp);
-        TA::issue_s32(gAqkT + ch * C * C * 2, oA, sb + B3::AQKT_OFF, wr);
+        TA::issue_s32(gAqk + ch * C * C * 2, oA, sb + B3::AQK_OFF, wr);
         TB::issue_s32(gKb + ch * C * D * 2, oB, sb + B3::KB_OFF, wr);
-        TQ::issue_s32(gQpT + ch * C * D * 2, oQ, sb + B3::QPT_OFF, wr);
-        TQ::issue_s32(gWT + ch * C * D * 2, oQ, sb + B3::WT_OFF, wr);
+        TB::issue_s32(gQp + ch * C * D * 2, oB, sb + B3::QP_OFF, wr);
+        TB::issue_s32(gW + ch * C * D * 2, oB, sb + B3::W_OFF, wr);
         const char* gdo = gdO + ((((size_t)b * a.T + t0) * a.H + h) * D + c0) * 2;
         if (valid == C) TO::issue_s32(gdo, oO, sb + B3::DO_OFF, wr);
         else TO::issue(gdo, (size_t)a.H * D * 2, sbp + B3::DO_OFF, wr, l, valid);
@@ -2156,14 +2155,14 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
     float4 eg[MT];
     auto preload = [&](int k, const char* sb) __attribute__((always_inline)) {   // chain waves
-        const ST* sAqkT = reinterpret_cast<const ST*>(sb + B3::AQKT_OFF);
+        const ST* sAqk = reinterpret_cast<const ST*>(sb + B3::AQK_OFF);
         const ST* sKb = reinterpret_cast<const ST*>(sb + B3::KB_OFF);
-        const ST* sQpT = reinterpret_cast<const ST*>(sb + B3::QPT_OFF);
-        const ST* sWT = reinterpret_cast<const ST*>(sb + B3::WT_OFF);
+        const ST* sQp = reinterpret_cast<const ST*>(sb + B3::QP_OFF);
+        const ST* sW = reinterpret_cast<const ST*>(sb + B3::W_OFF);
         const float* seG = reinterpret_cast<const float*>(sb + B3::EG_OFF);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            if (ks >= wr / 2) Aat[ks] = ldfrag_sw<RB_C>(sAqkT, BS * wr, 32 * ks);
+            if (ks >= wr / 2) Aat[ks] = ldfragT_sw<RB_C>(sAqk, BS * wr, 32 * ks);
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) Akb[ks] = ldfrag_sw<RB_D>(sKb, BS * wr, 32 * ks);
         const ST* o = dot(k);
@@ -2176,8 +2175,8 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
             if (own[i]) {
 #pragma unroll
                 for (int ks = 0; ks < C / 32; ++ks) {
-                    Aqt[i][ks] = ldfrag_sw<RB_C>(sQpT, BS * mt[i], 32 * ks);
-                    Awt[i][ks] = ldfrag_sw<RB_C>(sWT, BS * mt[i], 32 * ks);
+                    Aqt[i][ks] = ldfragT_sw<RB_D>(sQp, BS * mt[i], 32 * ks);
+                    Awt[i][ks] = ldfragT_sw<RB_D>(sW, BS * mt[i], 32 * ks);
                 }
                 eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
             }
@@ -2326,6 +2325,7 @@ static hipError_t launch_recur_t(const RecurArgs& a, hipStream_t st) {
 template <int D, typename ST>
 static hipError_t launch_dh_t(const DhArgs& a, hipStream_t st) {
     if constexpr (std::is_same<ST, uint16_t>::value && D >= 64) {
+        if (!a.Aqk || !a.Qp || !a.W || !a.Kb) return hipErrorInvalidValue;
         constexpr int CS2 = RowSplit<D>::CS;
         hipLaunchKernelGGL((kda_dh4_kernel<D, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
     } else if constexpr (std::is_same<ST, uint16_t>::value) {

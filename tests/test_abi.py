@@ -43,17 +43,21 @@ def test_workspace_sizes():
     # forward: W, U, Qp, Kb (bf16; fp32: KbT) (C*D) + Aqk (C*C) in the input dtype, eG (D) in fp32
     assert fwd == 2 * (4 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
     assert lib.kda_workspace_size(0, 8, 1568, 12, 64, 64, 0) == 4 * (4 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
-    # backward, bf16: W, U, WT, QpT, Kb, dVp (C*D), h, dh (D*D), AqkT (C*C) in bf16 and
-    # eG (D) in fp32; the forward's Qp and Aqk are not kept, and no KbT (the
-    # recurrences read Kb transposed)
-    assert bwd == 2 * (6 * N * 64 * 64 + 2 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
+    # backward, bf16: W, U, Qp, Kb, dVp (C*D), h, dh (D*D), Aqk (C*C) in bf16 and
+    # eG (D) in fp32; no transposed slab (the recurrences read Kb, Qp, W and Aqk
+    # with transposing LDS reads)
+    assert bwd == 2 * (5 * N * 64 * 64 + 2 * N * 64 * 64 + N * 64 * 64) + 4 * N * 64
     assert bwd > fwd
     # backward, fp32: also V' (C*D), Akk (C*C) and the diagonal-block inverses (4*16*16)
     bwd32 = lib.kda_workspace_size(1, 8, 1568, 12, 64, 64, 0)
     assert bwd32 == 4 * (8 * N * 64 * 64 + 2 * N * 64 * 64 + N * 64 * 64) + 4 * (N * 64 * 64 + N * 1024 + N * 64)
-    # the training pair's workspace holds both passes' regions
+    # the training pair's workspace holds both passes' regions (at bf16 the
+    # forward's regions are a subset of the backward's)
     train = lib.kda_workspace_size(2, 8, 1568, 12, 64, 64, 1)
-    assert train == fwd + bwd - 2 * (3 * N * 64 * 64) - 4 * N * 64
+    assert train == bwd
+    fwd32 = lib.kda_workspace_size(0, 8, 1568, 12, 64, 64, 0)
+    train32 = lib.kda_workspace_size(2, 8, 1568, 12, 64, 64, 0)
+    assert train32 == fwd32 + bwd32 - 4 * (3 * N * 64 * 64) - 4 * N * 64
     assert lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) == 0 or lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) >= 0
 
 
