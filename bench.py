@@ -101,7 +101,8 @@ def kernel_counts(B, T, H, D, es=2):
     CD, CC, DD, TII = C * D, C * C, D * D, 4 * 16 * 16
     state = B * H * DD * f4
     x = 0 if es == 2 else 1     # Akk, inverses and V' exist in the workspace (fp32 only)
-    hf = 1 if (es == 2 and D == 64) else 0   # the training forward writes h
+    tr = es == 2 and D == 64    # bf16 D = 64: no transposed slabs; the training forward writes h
+    hf = 1 if tr else 0
     fl = {
         0: n * (8 * C * D + (2.0 / 3.0) * C * C),       # Akk, Aqk, W, U, solve
         1: n * (6 * D * D + 2 * C * D),                 # W S, Qp S, Kb^T V', Aqk V'
@@ -123,14 +124,17 @@ def kernel_counts(B, T, H, D, es=2):
         5: nt * (5 * D + 1) * es + nt * (4 * D + 1) * es,   # q k v g beta dO in; dq dk dv dg dbeta out
     }
     ws = {
-        0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp KbT Aqk eG
+        0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp Kb(T) Aqk eG
         1: N * (4 * CD * es + CC * es + D * f4 + hf * DD * es) + nt * D * es + state,       # -> o, S_final [h]
-        2: io_in + N * (6 * CD * es + CC * es + x * (CC + TII) * f4 + D * f4),             # -> W U KbT WT QpT Kb AqkT [Akk Tii] eG
+        # -> W U Qp Kb Aqk eG (bf16 D = 64) | W U KbT WT QpT Kb AqkT [Akk Tii] eG
+        2: io_in + (N * (4 * CD * es + CC * es + D * f4) if tr else
+                    N * (6 * CD * es + CC * es + x * (CC + TII) * f4 + D * f4)),
         3: N * (3 * CD * es + D * f4 + DD * es + x * CD * es),                              # -> h [V']
-        4: N * (CC * es + 3 * CD * es + D * f4 + DD * es + CD * es) + nt * D * es + state,  # -> dh, dV', dS0
+        4: N * (CC * es + 3 * CD * es + D * f4 + DD * es + CD * es) + nt * D * es + state,  # Aqk(T) Kb Qp(T) W(T) -> dh, dV', dS0
         5: io_in + nt * D * es + N * ((3 + x) * CD * es + 2 * DD * es + x * (CC + TII) * f4)
            + nt * (4 * D + 1) * es,                                                         # -> dq dk dv dg dbeta
-        6: io_in + N * (7 * CD * es + 2 * CC * es + x * (CC + TII) * f4 + D * f4),         # -> both sets
+        6: io_in + (N * (4 * CD * es + CC * es + D * f4) if tr else                      # -> both sets
+                    N * (7 * CD * es + 2 * CC * es + x * (CC + TII) * f4 + D * f4)),
     }
     return fl, alg, ws
 

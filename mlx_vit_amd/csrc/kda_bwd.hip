@@ -879,14 +879,33 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                 dvo[mm][e] = bt * sm.ra.dR[t][D + d];
             }
     }
-    // dbeta, part 1: sum_d dV~[t][d] v[t][d] + dK~[t][d] e^{gamma_t} k[t][d]; 8 threads per row
+    // dbeta, part 1: sum_d dV~[t][d] v[t][d] + dK~[t][d] e^{gamma_t} k[t][d]; 8 threads per row,
+    // each over D / 8 consecutive channels (vector reads; a wave's rows share one block)
     {
-        const int t = tid >> 3, qd = tid & 7;
+        const int t = tid >> 3, qd = tid & 7, d0 = qd * (D / 8);
         float acc = 0.f;
-        for (int dd = qd * (D / 8); dd < (qd + 1) * (D / 8); ++dd) {
-            const float egk = unsafe ? ld1<ST>(&s.kr[t][dd]) * kexp<PREC>(chunk_gamma(s, t, dd))
-                                     : ld1<ST>(&s.kl[t][dd]) * fac_ep(s, t / BS, dd);
-            acc += sm.ra.dR[t][D + dd] * ld1<ST>(&sm.rb.p2.v[t][dd]) + sm.ra.dR[t][dd] * egk;
+        if (!unsafe) {
+            const float* fe = (t >= BS) ? &s.fac[FAC_EP + t / BS - 1][d0] : nullptr;
+#pragma unroll
+            for (int c4 = 0; c4 < D / 8; c4 += 4) {
+                const float4 rv = *reinterpret_cast<const float4*>(&sm.ra.dR[t][D + d0 + c4]);
+                const float4 rk = *reinterpret_cast<const float4*>(&sm.ra.dR[t][d0 + c4]);
+                const float4 vv = ld4<ST>(&sm.rb.p2.v[t][d0 + c4]);
+                float4 kv = ld4<ST>(&s.kl[t][d0 + c4]);
+                if (fe) {
+                    const float4 f = *reinterpret_cast<const float4*>(fe + c4);
+                    kv = make_float4(kv.x * f.x, kv.y * f.y, kv.z * f.z, kv.w * f.w);
+                }
+                acc += rv.x * vv.x + rk.x * kv.x;
+                acc += rv.y * vv.y + rk.y * kv.y;
+                acc += rv.z * vv.z + rk.z * kv.z;
+                acc += rv.w * vv.w + rk.w * kv.w;
+            }
+        } else {
+            for (int dd = d0; dd < d0 + D / 8; ++dd) {
+                const float egk = ld1<ST>(&s.kr[t][dd]) * kexp<PREC>(chunk_gamma(s, t, dd));
+                acc += sm.ra.dR[t][D + dd] * ld1<ST>(&sm.rb.p2.v[t][dd]) + sm.ra.dR[t][dd] * egk;
+            }
         }
         acc += __shfl_xor(acc, 1, 64);
         acc += __shfl_xor(acc, 2, 64);
