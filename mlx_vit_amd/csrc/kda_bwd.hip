@@ -922,6 +922,13 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
     constexpr int LDL = DL_IN_G ? LDG : LDA;
     static_assert(!DL_IN_G || LDG == LDA, "one dL stride");
     if (!dl_g) __syncthreads();   // v and dV' (region B) are dead from here
+    // With dL in the g region, the bf16 P = beta_t dL[t][s] -- the A operand of
+    // phase 4's row and column sides, as both round it -- also goes to the dV'
+    // tile of region B (dead since phase 1), so that phase 4 reads it as
+    // fragments: rows by row reads, columns by transposing reads.
+    constexpr bool PB = DL_IN_G && L::LDK >= C + 8;
+    const bool pb = PB && dl_g;
+    ST* sP = &sm.rb.p2.dVp[0][0];
 
     // ---------------- phase 3: dL = -tril(dR X^T, -1) ----------------
     for (int tix = w; tix < 10; tix += 8) {
@@ -941,7 +948,9 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
-            sdL[t * LDL + sx] = (sx < t) ? -acc[e] : 0.f;
+            const float v = (sx < t) ? -acc[e] : 0.f;
+            sdL[t * LDL + sx] = v;
+            if (pb) st1<ST>(sP + t * LDK + sx, s.beta[t] * v);
         }
     }
     __syncthreads();
@@ -980,9 +989,15 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                 for (int j = 0; j < NB; ++j) {
                     if (j > i || (j == i && ((pmask >> i) & 1))) continue;
                     const Frag4 B = colfrag(&s.kr[0][0], LDK, BS * j);
-                    const float4 x = *reinterpret_cast<const float4*>(sdL + (BS * i + r16) * LDL + BS * j + 4 * g4);
-                    const float pv[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
-                    const f32x4 Pk = mma4f<1>(frag4_from_f32<1>(pv), B, zero4());
+                    Frag4 Ap;
+                    if (pb) {
+                        Ap = ldfrag4<1, ST>(sP, LDK, BS * i, BS * j);
+                    } else {
+                        const float4 x = *reinterpret_cast<const float4*>(sdL + (BS * i + r16) * LDL + BS * j + 4 * g4);
+                        const float pv[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
+                        Ap = frag4_from_f32<1>(pv);
+                    }
+                    const f32x4 Pk = mma4f<1>(Ap, B, zero4());
                     Frag4 Aq = ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * i, BS * j);
                     if (j == i) {   // the diagonal pairs (t, t) are added apart, below
 #pragma unroll
@@ -1019,15 +1034,28 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
                 for (int i = 0; i < NB; ++i) {
                     if (i < j || (i == j && ((pmask >> j) & 1))) continue;
-                    float pv[4], av[4];
+                    Frag4 Ap, Aa;   // dP^T, dA^T: rows s = 16 j + r16, k = t = 16 i + 4 g4 + e
+                    if (pb) {
+                        Ap = ldfrag4T_tr(sP, LDK, BS * j, BS * i);
+                        Aa = ldfrag4T_tr(&sm.dA[0][0], LDT, BS * j, BS * i);
+                        if (i == j) {   // the diagonal pairs are added apart, below
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int t = BS * i + 4 * g4 + e;
-                        pv[e] = s.beta[t] * sdL[t * LDL + BS * j + r16];   // dP^T
-                        av[e] = (i == j && 4 * g4 + e == r16) ? 0.f : ld1<ST>(&sm.dA[t][BS * j + r16]);   // dA^T
+                            for (int e = 0; e < 4; ++e)
+                                if (4 * g4 + e == r16) Aa.h[e] = 0;
+                        }
+                    } else {
+                        float pv[4], av[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int t = BS * i + 4 * g4 + e;
+                            pv[e] = s.beta[t] * sdL[t * LDL + BS * j + r16];
+                            av[e] = (i == j && 4 * g4 + e == r16) ? 0.f : ld1<ST>(&sm.dA[t][BS * j + r16]);
+                        }
+                        Ap = frag4_from_f32<1>(pv);
+                        Aa = frag4_from_f32<1>(av);
                     }
-                    f32x4 P = mma4f<1>(frag4_from_f32<1>(pv), colfrag(&s.kl[0][0], LDK, BS * i), zero4());
-                    P = mma4f<1>(frag4_from_f32<1>(av), colfrag(&s.ql[0][0], LDK, BS * i), P);
+                    f32x4 P = mma4f<1>(Ap, colfrag(&s.kl[0][0], LDK, BS * i), zero4());
+                    P = mma4f<1>(Aa, colfrag(&s.ql[0][0], LDK, BS * i), P);
                     const float fs = (j < i) ? fac_tile(s, i, j, d) : fdm[mm];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) dKr[e] += P[e] * fs;
