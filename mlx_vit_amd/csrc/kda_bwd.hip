@@ -1326,6 +1326,9 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     // all waves first); only q, k, g and beta are waited for before the cumsum.  W, U, h and the phase-1
     // operands stay in registers (4 per thread per tile) until the cumsum and the
     // anchored transform are done, so their latency hides behind those phases.
+    // g is loaded as lane (row 16 b + r16 of block b, 8 channels): the 16 rows of
+    // a block and 8 channels sit in the 16 lanes of one DPP row, so that the
+    // in-block cumsum a is a four-step lane scan before g reaches LDS.
     int flag = 0;
     Local3Tiles<D, ST> tl;
     auto &tW = tl.W, &tU = tl.U, &tdo = tl.dO, &tv = tl.v, &tdVp = tl.dVp;
@@ -1333,10 +1336,18 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     float braw;
     {
         Tile<ST, C, D, NTH> tq, tk;
-        Tile<TG, C, D, NTH> tg;
+        constexpr int NCG = D / 8, WPB = NCG / 4, GV = 8 * (int)sizeof(TG) / 16, GE = 16 / (int)sizeof(TG);
+        static_assert(NCG % 4 == 0 && NB * WPB <= 8, "one lane per row and 8 channels of g");
+        const bool gl = w < NB * WPB;
+        const int grow = BS * (w / WPB) + r16, gc = 8 * (4 * (w % WPB) + g4);
+        uint4 graw[GV];
         tq.load(static_cast<const ST*>(a.q) + base, rs, valid);
         tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
-        tg.load(static_cast<const TG*>(a.g) + base, rs, valid);
+        if (gl) {
+            const TG* gp = static_cast<const TG*>(a.g) + base + (size_t)min(grow, valid - 1) * rs + gc;
+#pragma unroll
+            for (int vq = 0; vq < GV; ++vq) graw[vq] = *reinterpret_cast<const uint4*>(gp + GE * vq);
+        }
         braw = ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)min(tid, valid - 1) * a.H);
         // Every wave's q, k, g, beta requests enter the CU's memory pipeline before
         // any wave's later tiles, so no wave waits behind another's 80 KB.
@@ -1350,26 +1361,27 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         tdh.load(static_cast<const ST*>(a.dh) + cDD, D);
         tq.store(&s.ql[0][0], LDK);
         tk.store(&s.kr[0][0], LDK);
-        using TGT = Tile<TG, C, D, NTH>;
+        if (gl) {
+            // rows past T read as zero; a = in-block inclusive cumsum of g
+            float x[8];
 #pragma unroll
-        for (int i = 0; i < TGT::PER; ++i) {
-            const int vv = tid + NTH * i;
-            if (TGT::NV % NTH == 0 || vv < TGT::NV) {
-                const int row = vv / TGT::VPR, c = (vv - row * TGT::VPR) * TGT::EPV;
-                const Vec16<TG> x{tg.get(i)};
+            for (int vq = 0; vq < GV; ++vq) {
+                const Vec16<TG> xv{graw[vq]};
 #pragma unroll
-                for (int e = 0; e < TGT::EPV; ++e) {
-                    const float gv = x.get(e);
-                    s.g[row][c + e] = gv;
-                    if (!(gv <= 0.f)) flag = 1;
-                }
+                for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid) ? xv.get(e) : 0.f;
             }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (!(x[e] <= 0.f)) flag = 1;
+                x[e] = row16_scan(x[e]);
+            }
+            *reinterpret_cast<float4*>(&s.g[grow][gc]) = make_float4(x[0], x[1], x[2], x[3]);
+            *reinterpret_cast<float4*>(&s.g[grow][gc + 4]) = make_float4(x[4], x[5], x[6], x[7]);
         }
         if (tid < C) sm.dbeta[tid] = 0.f;
         if (tid == 0) *flagw = 0;
     }
     __syncthreads();
-    chunk_cumsum2<D, ST, NTH>(s);
     const int dfl = chunk_factors2<D, ST, PREC, NTH>(s, flag, flagw);
     // The rest is instantiated twice.  Chunks whose 16-row blocks all stay within
     // the span guard (every chunk at ordinary decays) run a copy with the

@@ -428,6 +428,16 @@ template <> __device__ __forceinline__ void store_vec<float>(float* p, const flo
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// Inclusive prefix sum over the 16 lanes of each DPP row (lanes 16 r .. 16 r +
+// 15), in lane order: four row_shr steps, lanes without a source adding 0
+__device__ __forceinline__ float row16_scan(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
+    return x;
+}
+
 // 1 / (1 + e^-x) with the hardware reciprocal (1 ulp); e^-x = inf gives 0
 __device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
