@@ -211,11 +211,8 @@ struct ChunkSmem {
     ST kl[C][LDK];     // k e^{a_t}
     ST ql[C][LDK];     // raw q, then q e^{a_t}
     ST kr[C][LDK];     // raw k, then k e^{b_t} (anchored chunks)
-    float g[C][LDG];   // raw g, then a (in-block inclusive cumsum)
-    union {
-        float fac[14][D];   // factor tables, rows FAC_* below
-        float tmp[512];     // cumsum partials; dead before fac is written
-    };
+    float g[C][LDG];   // a (in-block inclusive cumsum of g, formed at load)
+    float fac[14][D];  // factor tables, rows FAC_* below
     float beta[C];
 };
 
@@ -245,19 +242,33 @@ __device__ __forceinline__ float fac_tile(const ChunkSmem<D, ST>& s, int i, int 
 // All 16-byte loads of one chunk of q, k, g, beta (and optionally v) are issued
 // before anything is written to LDS; every wave's q, k, g, beta requests enter
 // the memory pipeline before any v request.  v stays in tv for the caller to
-// store once its latency is hidden.  Rows >= valid are zero.  Returns 1 if this
-// thread saw g > 0 or a NaN.
+// store once its latency is hidden.  Rows >= valid are zero.  g is loaded as
+// lane (row 16 w + r16 of block w, channel groups g4, g4 + 4, .. of 8
+// channels): the 16 rows of a block sit in the 16 lanes of one DPP row, so s.g
+// receives a, the inclusive cumsum of g inside each 16-row block, computed by
+// a four-step lane scan.  256 threads.  Returns 1 if this thread saw g > 0 or
+// a NaN.
 template <int D, typename ST, typename TG, bool WITH_V>
 __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& tv, const ST* __restrict__ q,
                                            const ST* __restrict__ k, const ST* __restrict__ v,
                                            const TG* __restrict__ g, const ST* __restrict__ beta, size_t base,
                                            size_t rstride, size_t bbase, int H, int valid) {
+    constexpr int NCG = D / 8, CPL = NCG / 4, GV = 8 * (int)sizeof(TG) / 16, GE = 16 / (int)sizeof(TG);
+    static_assert(NCG % 4 == 0 && NB == 4, "four waves of 16 rows, 8-channel groups");
     Tile<ST, C, D> tq, tk;
-    Tile<TG, C, D> tg;
+    const int tid = threadIdx.x, w = tid >> 6, r16 = tid & 15, g4 = (tid >> 4) & 3;
+    const int grow = BS * w + r16;
+    uint4 graw[CPL][GV];
     tq.load(q + base, rstride, valid);
     tk.load(k + base, rstride, valid);
-    tg.load(g + base, rstride, valid);
-    const int tid = threadIdx.x;
+    {
+        const TG* gp = g + base + (size_t)min(grow, valid - 1) * rstride;
+#pragma unroll
+        for (int cp = 0; cp < CPL; ++cp)
+#pragma unroll
+            for (int vq = 0; vq < GV; ++vq)
+                graw[cp][vq] = *reinterpret_cast<const uint4*>(gp + 8 * (g4 + 4 * cp) + GE * vq);
+    }
     const float braw = ld1<ST>(beta + bbase + (size_t)min(tid, valid - 1) * H);
     if constexpr (WITH_V) {
         __builtin_amdgcn_s_barrier();
@@ -266,52 +277,27 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& 
     tq.store(&s.ql[0][0], ChunkSmem<D, ST>::LDK);
     tk.store(&s.kr[0][0], ChunkSmem<D, ST>::LDK);
     int flag = 0;
-    constexpr int EPV = Tile<TG, C, D>::EPV, VPR = Tile<TG, C, D>::VPR;
 #pragma unroll
-    for (int i = 0; i < Tile<TG, C, D>::PER; ++i) {
-        const int vv = tid + 256 * i;
-        const int row = vv / VPR, c = (vv - row * VPR) * EPV;
-        const Vec16<TG> x{tg.get(i)};
+    for (int cp = 0; cp < CPL; ++cp) {
+        float x[8];
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) {
-            const float gv = x.get(e);
-            s.g[row][c + e] = gv;
-            if (!(gv <= 0.f)) flag = 1;
+        for (int vq = 0; vq < GV; ++vq) {
+            const Vec16<TG> xv{graw[cp][vq]};
+#pragma unroll
+            for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid) ? xv.get(e) : 0.f;
         }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if (!(x[e] <= 0.f)) flag = 1;
+            x[e] = row16_scan(x[e]);
+        }
+        float* dst = &s.g[grow][8 * (g4 + 4 * cp)];
+        *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(x[4], x[5], x[6], x[7]);
     }
     if (tid < C) s.beta[tid] = (tid < valid) ? braw : 0.f;
     __syncthreads();
     return flag;
-}
-
-// In place: g -> a, the inclusive cumsum of g inside each 16-row block.
-// NTH threads, NTH / D parts of RP rows per channel; parts shorter than a
-// block add the totals of the earlier parts of their block.
-template <int D, typename ST, int NTH = 256>
-__device__ __forceinline__ void chunk_cumsum2(ChunkSmem<D, ST>& s) {
-    constexpr int PARTS = NTH / D, RP = C / PARTS;
-    static_assert(PARTS * D <= 512, "cumsum partials fit tmp");
-    static_assert(RP % BS == 0 || BS % RP == 0, "parts align with blocks");
-    const int tid = threadIdx.x, d = tid % D, p = tid / D;
-    float run = 0.f;
-#pragma unroll
-    for (int r = 0; r < RP; ++r) {
-        if (r % BS == 0) run = 0.f;
-        run += s.g[p * RP + r][d];
-        s.g[p * RP + r][d] = run;
-    }
-    if constexpr (RP < BS) {
-        constexpr int PPB = BS / RP;   // parts per block
-        s.tmp[p * D + d] = run;
-        __syncthreads();
-        float off = 0.f;
-        for (int pp = p - p % PPB; pp < p; ++pp) off += s.tmp[pp * D + d];
-        if (p % PPB) {
-#pragma unroll
-            for (int r = 0; r < RP; ++r) s.g[p * RP + r][d] += off;
-        }
-    }
-    __syncthreads();
 }
 
 // OR of x over the workgroup through one LDS word (*w, zeroed by the caller

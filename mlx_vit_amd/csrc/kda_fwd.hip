@@ -19,8 +19,9 @@ namespace kda {
 // prep
 //
 // Phases (barriers between them):
-//   load      all 16-byte loads of q, k, g (and v) issued first, then LDS
-//   cumsum    a (in-block cumsums of g); factor tables; decay flags: the
+//   load      all 16-byte loads of q, k, g (and v) issued first, then LDS;
+//             a (in-block cumsums of g) by a lane scan on the way
+//   factors   factor tables; decay flags: the
 //             chunk's g > 0 / NaN, the diagonal blocks beyond the span guard
 //   diagonal  those blocks' diagonal tiles from raw q, k: 4-row sub-anchors on
 //             MFMA, or pair by pair beyond the 4-row guard too (every pair for
@@ -93,7 +94,6 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     Tile<ST, C, D> tv;
     const int flag = chunk_load2<D, ST, TG, G::STAGE_V>(s, tv, q, k, v, g, beta, base, rs, bbase, a.H, valid);
     // PHASE 1
-    chunk_cumsum2<D, ST>(s);
     const int dfl = chunk_factors2<D, ST, PREC>(s, flag, flagw);
     // The rest of the kernel is instantiated twice.  Chunks whose 16-row blocks
     // all stay within the span guard (every chunk at ordinary decays) run a copy
