@@ -187,34 +187,46 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
 
         // pass A: row threads (t, EPV channels).  K_l = K e^{a}, Q_l = Q e^{a},
         // K_r = K e^{b} (anchored chunks; raw K otherwise), Qp = Q_l e^{gamma_{16i-1}},
-        // Kb = K_r e^{G - gamma_{16i+15}}
+        // Kb = K_r e^{G - gamma_{16i+15}}.  Every LDS operand is read as 16-byte
+        // vectors up front; the factor rows of the first / last block (which are
+        // 1) are read from a neighbouring row and replaced, so that no load sits
+        // behind a branch.
         {
             constexpr int VPR = D / EPV, NV = C * VPR;
+            auto ld_row = [](const float* p, float* x) __attribute__((always_inline)) {
+#pragma unroll
+                for (int q4 = 0; q4 < EPV / 4; ++q4) {
+                    const float4 v4 = *reinterpret_cast<const float4*>(p + 4 * q4);
+                    x[4 * q4] = v4.x; x[4 * q4 + 1] = v4.y; x[4 * q4 + 2] = v4.z; x[4 * q4 + 3] = v4.w;
+                }
+            };
             for (int vv = tid; vv < NV; vv += 256) {
                 const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, blk = t / BS;
                 const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
                 const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
+                float at[EPV], te[EPV], fp[EPV], fq[EPV];
+                ld_row(&s.g[t][c0], at);
+                ld_row(&s.g[BS * blk + BS - 1][c0], te);
+                ld_row(&s.fac[FAC_EP + (blk > 0 ? blk - 1 : 0)][c0], fp);
+                ld_row(&s.fac[FAC_EQ + (blk < NB - 1 ? blk : NB - 2)][c0], fq);
                 float okl[EPV], oql[EPV], okr[EPV], oqp[EPV], okb[EPV];
 #pragma unroll
                 for (int e = 0; e < EPV; ++e) {
-                    const int d = c0 + e;
-                    const float at = s.g[t][d], bt = s.g[BS * blk + BS - 1][d] - at;
-                    const float el = kexp<PREC>(at);
+                    const float bt = te[e] - at[e];
+                    const float el = kexp<PREC>(at[e]);
                     const float qf = qv.get(e), kf = kv.get(e);
                     okl[e] = kf * el;
                     oql[e] = qf * el;
                     okr[e] = unsafe ? kf : kf * kexp<PREC>(bt);
-                    oqp[e] = oql[e] * fac_ep(s, blk, d);
-                    if (oKb) {
-                        if (unsafe) {
-                            float gsfx = bt;   // G - gamma_t
-                            for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][d];
-                            okb[e] = kf * kexp<PREC>(gsfx);
-                        } else {
-                            okb[e] = okr[e] * fac_eq(s, blk, d);
-                        }
-                    } else {
-                        okb[e] = 0.f;
+                    oqp[e] = (blk > 0) ? oql[e] * fp[e] : oql[e];
+                    okb[e] = (blk < NB - 1) ? okr[e] * fq[e] : okr[e];
+                }
+                if (unsafe && oKb) {
+#pragma unroll
+                    for (int e = 0; e < EPV; ++e) {
+                        float gsfx = te[e] - at[e];   // G - gamma_t
+                        for (int m = blk + 1; m < NB; ++m) gsfx += s.g[BS * m + BS - 1][c0 + e];
+                        okb[e] = kv.get(e) * kexp<PREC>(gsfx);
                     }
                 }
                 store_vec<ST>(&s.kl[t][c0], okl);
