@@ -304,11 +304,15 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& 
 // before an earlier barrier).  Ends with a barrier.  The result is returned
 // through readfirstlane, so the compiler knows it is uniform and branches on
 // it with scalar branches.
-template <int NTH>
+// The wave's OR is formed bit by bit with ballots (one compare each, no LDS
+// round trip); x must fit in NBITS bits.
+template <int NTH, int NBITS = 9>
 __device__ __forceinline__ int block_or(int x, int* w) {
+    int wm = 0;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x |= __shfl_xor(x, o);
-    if ((threadIdx.x & 63) == 0 && x) atomicOr(w, x);
+    for (int b = 0; b < NBITS; ++b)
+        if (__ballot((x >> b) & 1)) wm |= 1 << b;
+    if ((threadIdx.x & 63) == 0 && wm) atomicOr(w, wm);
     __syncthreads();
     return __builtin_amdgcn_readfirstlane(*w);
 }
@@ -325,8 +329,11 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag, int
     static_assert(TPC >= 1 && NTH % D == 0, "whole channels per workgroup");
     const int tid = threadIdx.x, d = tid % D, r = tid / D;
     int m = flag ? 16 : 0;
-    // the channel's four block totals, read together
+    // the channel's four block totals and (one thread per block, TPC >= NB) the
+    // block's sub-block ends, all read together
     const float T0 = s.g[BS - 1][d], T1 = s.g[2 * BS - 1][d], T2 = s.g[3 * BS - 1][d], T3 = s.g[4 * BS - 1][d];
+    const int ib = (r < NB) ? r : NB - 1;
+    const float e0 = s.g[BS * ib + 3][d], e1 = s.g[BS * ib + 7][d], e2 = s.g[BS * ib + 11][d];
     const float T12 = T1 + T2;
     // table rows r, r + TPC, ...: exponents are sums of block totals (FAC_*)
     for (int row = r; row < 13; row += TPC) {
@@ -340,7 +347,9 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag, int
     for (int i = r; i < NB; i += TPC) {
         const float T = (i == 0) ? T0 : (i == 1) ? T1 : (i == 2) ? T2 : T3;
         if (!(-T <= SPAN_MAX)) m |= 1 << i;
-        const float c0 = s.g[BS * i + 3][d], c1 = s.g[BS * i + 7][d], c2 = s.g[BS * i + 11][d];
+        const bool pre = TPC >= NB;   // this thread's only block, read above
+        const float c0 = pre ? e0 : s.g[BS * i + 3][d], c1 = pre ? e1 : s.g[BS * i + 7][d];
+        const float c2 = pre ? e2 : s.g[BS * i + 11][d];
         if (!(-c0 <= SUB_SPAN_MAX) || !(c0 - c1 <= SUB_SPAN_MAX) || !(c1 - c2 <= SUB_SPAN_MAX) ||
             !(c2 - T <= SUB_SPAN_MAX))
             m |= 32 << i;
