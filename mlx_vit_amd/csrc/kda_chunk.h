@@ -425,48 +425,46 @@ __device__ __forceinline__ float chunk_gamma(const ChunkSmem<D, ST>& s, int t, i
 }
 
 // Register-resident inverses of the four 16x16 diagonal blocks of I + L,
-// L[t][s] = beta_t Akk[t][s]: wave w inverts block w, lane c (< 16) owns
-// column c.  All 36 row reads of the block's strict lower part are issued
-// before the substitution starts (one LDS round trip instead of one per row);
-// beta_t scales the row sum: x_t = [t == c] - beta_t sum_{s<t} Akk[t][s] x_s.
+// L[t][s] = beta_t Akk[t][s]: wave w inverts block w by forward substitution,
+// x_t = [t == c] - beta_t sum_{s<t} Akk[t][s] x_s for column c.  Lane
+// (c = l / 4, p = l % 4) owns column c and the quarter s = 4 p .. 4 p + 3 of
+// each row sum; the four partial sums of a column meet by two quad-permute
+// DPP adds, so every step is a handful of dependent VALU operations on all 64
+// lanes.  The block's rows are read before the substitution starts (one
+// 16-byte read per row and lane, the same for the 16 lanes of a quarter).
 // With fc != nullptr the block's transpose is also written as split (PREC 3)
 // MFMA A fragments, fc[64 w + lane] = fragment of lane (g, r) holding
 // T_ww[4g + e][r], so that other waves load it with one 16-byte read per lane.
 template <int LDA>
 __device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, const float* __restrict__ beta,
                                                  float (*tii)[BS][BS + 4], Frag4* fc = nullptr) {
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), c = threadIdx.x & 63;
-    if (c < BS) {
-        const float* Ab = akk + (size_t)(BS * w) * LDA + BS * w;
-        float4 R[BS][BS / 4];
-        float bt[BS];
+    static_assert(BS == 16, "four quarters of four");
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l >> 2, p = l & 3;
+    const float* Ab = akk + (size_t)(BS * w) * LDA + BS * w + 4 * p;
+    float4 R[BS];   // R[t] = Akk[t][4 p .. 4 p + 3] of the block, zero at s >= t
+    float bt[BS];
 #pragma unroll
-        for (int t = 1; t < BS; ++t) {
-            bt[t] = beta[BS * w + t];
-#pragma unroll
-            for (int j4 = 0; j4 < (t + 3) / 4; ++j4) R[t][j4] = *reinterpret_cast<const float4*>(Ab + t * LDA + 4 * j4);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        float x[BS];
-        x[0] = (c == 0) ? 1.f : 0.f;
-#pragma unroll
-        for (int t = 1; t < BS; ++t) {
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 0; j < t; ++j) {
-                const float4 r = R[t][j / 4];
-                const float a = (j % 4 == 0) ? r.x : (j % 4 == 1) ? r.y : (j % 4 == 2) ? r.z : r.w;
-                acc += a * x[j];
-            }
-            x[t] = ((t == c) ? 1.f : 0.f) - bt[t] * acc;
-        }
-#pragma unroll
-        for (int t = 0; t < BS; ++t) tii[w][t][c] = x[t];
-        if (fc) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) fc[64 * w + 16 * g + c] = frag4_from_f32<3>(&x[4 * g]);
-        }
+    for (int t = 1; t < BS; ++t) {
+        bt[t] = beta[BS * w + t];
+        const float4 r = *reinterpret_cast<const float4*>(Ab + t * LDA);
+        R[t] = make_float4(4 * p < t ? r.x : 0.f, 4 * p + 1 < t ? r.y : 0.f, 4 * p + 2 < t ? r.z : 0.f,
+                           4 * p + 3 < t ? r.w : 0.f);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    float xq[4] = {0.f, 0.f, 0.f, 0.f};   // x_{4p} .. x_{4p+3}
+    if (p == 0) xq[0] = (c == 0) ? 1.f : 0.f;
+#pragma unroll
+    for (int t = 1; t < BS; ++t) {
+        float part = R[t].x * xq[0] + R[t].y * xq[1];
+        part += R[t].z * xq[2] + R[t].w * xq[3];
+        part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0xB1, 0xf, 0xf, false));
+        part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x4E, 0xf, 0xf, false));
+        const float xt = ((t == c) ? 1.f : 0.f) - bt[t] * part;
+        if ((t >> 2) == p) xq[t & 3] = xt;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tii[w][4 * p + e][c] = xq[e];
+    if (fc) fc[64 * w + 16 * p + c] = frag4_from_f32<3>(xq);
 }
 
 
