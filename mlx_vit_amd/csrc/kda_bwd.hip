@@ -682,14 +682,17 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
         __syncthreads();
         if (w < NB) diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii);
     }
-    // V' tiles round-robin over the waves that are free first: 0-3 (a diagonal
-    // block and its inverse) and 6-7 (one off-diagonal tile); waves 4-5, which
-    // form two off-diagonal tiles, take none
+    // V' tiles by measured finish times of the work above: waves 0-3 (a
+    // diagonal tile and its inverse) take two each, waves 4-5 (two
+    // off-diagonal tiles) one, waves 6-7 (one off-diagonal tile) three
     static_assert(NB == 4, "wave roles assume four row blocks");
     {
-        const int slot = (w < 4) ? w : (w >= 6) ? w - 2 : -1;
-        if (slot >= 0)
-            for (int tix = slot; tix < NB * NT; tix += 6) vp_tile(tix);
+        const int v0 = (w < 4) ? 2 * w : (w < 6) ? w + 4 : 3 * w - 8;   // 0 2 4 6 | 8 9 | 10 13
+        const int vn = (w < 4) ? 2 : (w < 6) ? 1 : 3;
+        for (int i = 0; i < vn; ++i) {
+            const int tix = v0 + i;
+            if (tix < NB * NT) vp_tile(tix);
+        }
     }
     __syncthreads();
 
