@@ -712,12 +712,15 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
     f32x4 Y[NB];
     Frag4 At[NB], Aij[6];
     if (own) {
+        if (rh) {
+            // column d of dV', rows 16 i + 4 g4 + e (transposing reads)
 #pragma unroll
-        for (int i = 0; i < NB; ++i)
-            if (rh) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) Y[i][e] = ld1<ST>(&sm.rb.p2.dVp[BS * i + 4 * g4 + e][d]);
+            for (int i = 0; i < NB; ++i) {
+                float yv[4];
+                ld_col4(&sm.rb.p2.dVp[0][0], LDK, BS * ct, BS * i, yv);
+                Y[i] = f32x4{yv[0], yv[1], yv[2], yv[3]};
             }
+        }
         if (FC && !unsafe) {
 #pragma unroll
             for (int i = 0; i < NB; ++i) At[i] = fc[64 * i + l];
@@ -814,10 +817,10 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
             part = sum4g(part);
             if (rh == 0 && g4 == 0) xg[d] = dgcol + eGd * part;
         }
-        // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves, one each for the
-        // rh = 1 waves (their solve operand Y is gathered from LDS), the rest for
-        // the rh = 0 waves (whose solve starts from registers)
-        for (int tix = (w < 4) ? w + 4 : w - 4; tix < 10; tix += (w < 4) ? 4 : 10) {
+        // dAqk = tril(dO V'^T): 10 lower tiles over the 8 waves, one each and the
+        // last two for waves 4-5 (the rh = 1 waves end phase 1 before the rh = 0
+        // waves, which also form dW)
+        for (int tix = (w < 4) ? w + 4 : w - 4; tix < 10; tix += (w < 4) ? 10 : 8) {
             int i, j;
             tile_ij(tix, i, j);
             Frag8 A[D / 32], B[D / 32];

@@ -410,23 +410,48 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             f32x4 Y[TPW];
+            // right-hand sides, rows t = 16 i + 4 g4 + e of column d: bf16 columns by
+            // transposing reads, beta of the lane's four rows as one vector
+            const float4 b4 = *reinterpret_cast<const float4*>(&s.beta[BS * i + 4 * g4]);
+            const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-            for (int jj = 0; jj < TPW; ++jj)
+            for (int jj = 0; jj < TPW; ++jj) {
+                const int d = dcol[jj];
+                float col[4] = {0.f, 0.f, 0.f, 0.f};
+                float fe = 1.f;
+                if constexpr (std::is_same<ST, uint16_t>::value) {
+                    if (tok[jj]) {
+                        const int ct = d - r16;
+                        if (isK[jj]) ld_col4(&s.kl[0][0], LDK, ct, BS * i, col);
+                        else if constexpr (G::STAGE_V) ld_col4(&svbuf[0][0], LDK, ct, BS * i, col);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = BS * i + 4 * g4 + e;
+                        if (tok[jj]) {
+                            if (isK[jj]) col[e] = ld1<ST>(&s.kl[t][d]);
+                            else if constexpr (G::STAGE_V) col[e] = ld1<ST>(&svbuf[t][d]);
+                        }
+                    }
+                }
+                if (tok[jj] && isK[jj]) fe = fac_ep(s, i, d);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int t = BS * i + 4 * g4 + e, d = dcol[jj];
+                    const int t = BS * i + 4 * g4 + e;
                     float rv = 0.f;
                     if (tok[jj]) {
                         if (isK[jj]) {
-                            rv = s.beta[t] * fac_ep(s, i, d) * ld1<ST>(&s.kl[t][d]);
+                            rv = bv[e] * fe * col[e];
                         } else if constexpr (G::STAGE_V) {
-                            rv = s.beta[t] * ld1<ST>(&svbuf[t][d]);
+                            rv = bv[e] * col[e];
                         } else {
-                            rv = (t < valid) ? s.beta[t] * ld1<ST>(v + base + (size_t)t * rs + d) : 0.f;
+                            rv = (t < valid) ? bv[e] * ld1<ST>(v + base + (size_t)t * rs + d) : 0.f;
                         }
                     }
                     Y[jj][e] = rv;
                 }
+            }
             const float brow = -s.beta[BS * i + r16];
 #pragma unroll
             for (int j = 0; j < i; ++j) {
