@@ -5,8 +5,8 @@ A step is one forward + backward (VJP) pass of the op over one batch of
 synthetic inputs already resident in HBM: config 2, B=8, H=12, T=1568, D=64,
 chunk 64, bf16 q/k/v/g/beta, dO ~ N(0,1) bf16, zero initial state -- run as a
 training step does, through the training pair (kda_fwd_train keeps the
-per-chunk factors and, with bf16 inputs at D = 64, the chunk-start states;
-kda_bwd_train consumes them).  Prints ONE JSON line.  ``value`` is tokens/s = B*T*steps / wall time of
+per-chunk factors, kda_bwd_train recomputes the chunk-boundary states from
+them).  Prints ONE JSON line.  ``value`` is tokens/s = B*T*steps / wall time of
 the timed steps.
 
 Per-kernel durations come from HIP events the library records around each of
@@ -83,8 +83,7 @@ def kernel_counts(B, T, H, D, es=2):
     forward recurrence o and the states, the reverse carry dS_T / dS_0, the
     local-adjoint kernel the whole backward I/O.  Per valid token-head at D = 64
     bf16: 514 B (prep), 128 B (recur fwd), 1,156 B (local).  The state
-    recompute moves no op-level bytes at all (and does not run in the training
-    pair at bf16 D = 64, whose forward writes the chunk-start states h).
+    recompute moves no op-level bytes at all.
 
     ws_bytes: every input and output tensor of the kernel touched once,
     workspace slabs included (the inter-kernel traffic of this design) -- (B, T,
@@ -101,8 +100,7 @@ def kernel_counts(B, T, H, D, es=2):
     CD, CC, DD, TII = C * D, C * C, D * D, 4 * 16 * 16
     state = B * H * DD * f4
     x = 0 if es == 2 else 1     # Akk, inverses and V' exist in the workspace (fp32 only)
-    tr = es == 2 and D == 64    # bf16 D = 64: no transposed slabs; the training forward writes h
-    hf = 1 if tr else 0
+    tr = es == 2 and D == 64    # bf16 D = 64: no transposed slabs
     fl = {
         0: n * (8 * C * D + (2.0 / 3.0) * C * C),       # Akk, Aqk, W, U, solve
         1: n * (6 * D * D + 2 * C * D),                 # W S, Qp S, Kb^T V', Aqk V'
@@ -125,7 +123,7 @@ def kernel_counts(B, T, H, D, es=2):
     }
     ws = {
         0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp Kb(T) Aqk eG
-        1: N * (4 * CD * es + CC * es + D * f4 + hf * DD * es) + nt * D * es + state,       # -> o, S_final [h]
+        1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state,                      # -> o, S_final
         # -> W U Qp Kb Aqk eG (bf16 D = 64) | W U KbT WT QpT Kb AqkT [Akk Tii] eG
         2: io_in + (N * (4 * CD * es + CC * es + D * f4) if tr else
                     N * (6 * CD * es + CC * es + x * (CC + TII) * f4 + D * f4)),
@@ -184,8 +182,7 @@ PROFILE_ROLES = {
     # rocprof kernel symbol fragment -> profile names in dispatch order within a
     # fwd+bwd step (the training pair: one prep launch, in its training mode)
     "kda_prep_kernel": ["kda_prep_kernel(train)"],
-    # (bf16 D = 64: no state recompute; the training forward writes h)
-    "kda_recur": ["kda_recur_kernel(fwd)"],
+    "kda_recur": ["kda_recur_kernel(fwd)", "kda_recur_kernel(states)"],
     "kda_dh": ["kda_dh_kernel"],
     "kda_bwd_local": ["kda_bwd_local_kernel"],
 }

@@ -340,8 +340,6 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     ra.eG = fregion(workspace, L, KDA_WS_EG);
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-    // the training forward leaves the chunk-start states for kda_bwd_train
-    if (pass == KDA_PASS_TRAIN && kda::fwd_writes_states(D, in_bf16)) ra.h = region(workspace, L, KDA_WS_H);
     if (epi) {
         ra.z = epi->z; ra.ld_z = epi->ld_z; ra.nw = epi->w; ra.eps = epi->eps; ra.y = epi->y; ra.ld_y = epi->ld_y;
     }
@@ -377,8 +375,7 @@ void* scratch_ptr(int dev, hipError_t* err) {
 
 // pass 1: prep from the inputs, then the backward; pass 2: the workspace holds
 // the per-chunk factors kda_fwd_train wrote for the same inputs, so the prep is
-// skipped, and where fwd_writes_states holds also the chunk-start states, so
-// their recompute is skipped too.
+// skipped.  Either way the chunk-boundary states are recomputed.
 int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
             int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
@@ -421,16 +418,13 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
     void* Vp = region(workspace, L, KDA_WS_VP);
     void* dVp = region(workspace, L, KDA_WS_DVP);
 
-    // chunk-boundary states, recomputed from the per-chunk factors unless the
-    // training forward wrote them
-    if (!(pass == KDA_PASS_TRAIN && kda::fwd_writes_states(D, in_bf16))) {
-        kda::RecurArgs ra = {};
-        ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
-        ra.Kb = region(workspace, L, KDA_WS_KB);
-        ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-        e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
-        if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
-    }
+    // chunk-boundary states, recomputed from the per-chunk factors
+    kda::RecurArgs ra = {};
+    ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
+    ra.Kb = region(workspace, L, KDA_WS_KB);
+    ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
+    e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
+    if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
 
     kda::DhArgs da = {};
     da.AqkT = region(workspace, L, KDA_WS_AQKT);

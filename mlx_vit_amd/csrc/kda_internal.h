@@ -39,8 +39,7 @@ struct RecurArgs {
     void* o;
     void *h, *Vp;
     int T, H, nc, BH;
-    // h: mode 1 writes the chunk-start states there; mode 0 too when set (the
-    // training forward, where fwd_writes_states allows it).
+    // h: mode 1 writes the chunk-start states there
     // Forward only: the layer's gated RMSNorm fused into the O store when y is
     // set, y = o rsqrt(mean_d o^2 + eps) nw sigmoid(z) per head; z and y are
     // [B, T, *] with row strides ld_z and ld_y (elements), head h at column h D.
@@ -80,9 +79,6 @@ hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nc
 hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st);
 // whether launch_recur can fuse the gated RMSNorm for this head size and dtype
 bool recur_epilogue_supported(int D, int in_bf16);
-// whether the forward (mode 0) can also write the chunk-start states h (a.h
-// set), so that the training backward need not recompute them
-bool fwd_writes_states(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
 hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,

@@ -1369,9 +1369,6 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
 //                next chunk's W, U, Kb^T (transposing reads of Kb), e^G operands
 //   role-1 waves: flush the previous chunk's outputs; MODE 0: O = Qp S + Aqk V'
 //                (row block wr) after B, read the next chunk's Qp, Aqk operands
-//   MODE 2: the forward of MODE 0 that also writes the chunk-start states h:
-//                the role-1 waves copy chunk n's state from the S^T exchange
-//                tile (there between A(n) and B(n)) to h, transposed
 //   DMA: chunk n+NS is brought after barrier B(n), once chunk n's operands (the
 //        chain waves read its Kb^T and e^G between A(n) and B(n)) have left its
 //        LDS set: MODE 0 the chain waves bring W, U, Kb^T, e^G after their state
@@ -1381,7 +1378,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
 template <int D, int MODE, int CS>
 __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
     using ST = uint16_t;
-    constexpr bool FWD = MODE != 1;   // O and the final state
+    constexpr bool FWD = MODE == 0;   // O and the final state
     using Lay = Recur3Layout<D, FWD ? 0 : 1, CS>;
     constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4, NS = Lay::NS;
     constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
@@ -1571,15 +1568,6 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
             preload_kb(scur);
         } else {
             if (n > 0) flush(n - 1);
-            if constexpr (MODE == 2) {
-                // h of chunk n = the state in xs (S^T: row = column of h), one
-                // 16-byte piece of a row of h per thread
-                static_assert(DC == 32 && D * DC / 8 == 256, "one 16-byte piece of h per role-1 thread");
-                const int t1 = tid - 256, i = t1 & 15, row = 4 * (t1 >> 4) + (i & 3), col = 8 * (i >> 2);
-                const short8v x = ld_tr_rows8(xs, LDR, 0, 4 * (t1 >> 4));
-                *reinterpret_cast<short8v*>(static_cast<ST*>(a.h) + ((size_t)bh * nc + n) * D * D + (size_t)row * D +
-                                            c0 + col) = x;
-            }
         }
         // chunk n+1's slabs landed; chunks up to n+NS-1 (issued after earlier B
         // barriers) may stay in flight
@@ -1670,8 +1658,6 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
 //     The side waves issue no global load and no DMA: their only vector-memory
 //     operations are the flush stores, so no wait of theirs can stall on a load
 //     in flight.
-// HST: the side waves also copy chunk n's state from the S^T exchange tile
-// (there between A(n) and B(n)) to the chunk-start states h, transposed.
 // Barriers and wait counts follow kda_recur4_kernel; the slabs are read once
 // per (batch, head) instead of once per column half.  LDS sets: NS = 3 (DMA
 // three chunks ahead), with EPI NS = 2 (each set also holds the gate tile).
@@ -1699,7 +1685,7 @@ struct Recur5Layout {
     static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "recurrence LDS");
 };
 
-template <int D, bool EPI, bool HST>
+template <int D, bool EPI>
 __global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
     using ST = uint16_t;
     using Lay = Recur5Layout<D, EPI>;
@@ -1903,14 +1889,6 @@ __global__ __launch_bounds__(1024) void kda_recur5_kernel(const RecurArgs a) {
                 O[j] = mma<1>(Ax[ks], ldfrag<1, ST>(xs, LDR, cb + BS * j, 32 * ks), O[j]);
         }
         if (!EPI && n > 0) flush(n - 1, Zp);
-        if constexpr (HST) {
-            // h of chunk n, row t1 / 8, columns 8 (t1 % 8) .. + 7
-            static_assert(D * D / 8 == 512, "one 16-byte piece of h per side thread");
-            const int i = t1 & 15, gq = t1 >> 4, row = 4 * (gq & 15) + (i & 3), col = 32 * (gq >> 4) + 8 * (i >> 2);
-            const short8v x = ld_tr_rows8(xs, LDR, 32 * (gq >> 4), 4 * (gq & 15));
-            *reinterpret_cast<short8v*>(static_cast<ST*>(a.h) + ((size_t)bh * nc + n) * D * D + (size_t)row * D + col) =
-                x;
-        }
         if constexpr (EPI) read_gate(scur, Zc);                 // before B: the set is refilled after it
         lds_barrier();                                          // B(n)
         ST* sst = stg(n);
@@ -2285,18 +2263,12 @@ template <int D> struct RowSplit { static constexpr int CS = (D >= 128) ? 4 : 2;
 
 template <int D, typename ST, int MODE>
 static hipError_t launch_recur_t(const RecurArgs& a, hipStream_t st) {
-    // the forward writes the chunk-start states h only where fwd_writes_states says so
-    if (MODE == 0 && a.h != nullptr && !fwd_writes_states(D, std::is_same<ST, uint16_t>::value))
-        return hipErrorInvalidValue;
     if (a.y != nullptr) {
         // the forward with the gated RMSNorm fused into the O store: kernels whose
         // workgroup holds whole output rows
-        if constexpr (MODE == 0 && std::is_same<ST, uint16_t>::value && D == 64) {
-            if (a.h)
-                hipLaunchKernelGGL((kda_recur5_kernel<D, true, true>), dim3(a.BH), dim3(1024), 0, st, a);
-            else
-                hipLaunchKernelGGL((kda_recur5_kernel<D, true, false>), dim3(a.BH), dim3(1024), 0, st, a);
-        } else if constexpr (MODE == 0 && std::is_same<ST, float>::value && D <= 64)
+        if constexpr (MODE == 0 && std::is_same<ST, uint16_t>::value && D == 64)
+            hipLaunchKernelGGL((kda_recur5_kernel<D, true>), dim3(a.BH), dim3(1024), 0, st, a);
+        else if constexpr (MODE == 0 && std::is_same<ST, float>::value && D <= 64)
             hipLaunchKernelGGL((kda_recur_kernel<D, ST, 3, 0, 1, true>), dim3(a.BH), dim3(256), 0, st, a);
         else
             return hipErrorInvalidValue;
@@ -2305,10 +2277,7 @@ static hipError_t launch_recur_t(const RecurArgs& a, hipStream_t st) {
     if constexpr (std::is_same<ST, uint16_t>::value && D == 64) {
         if (a.Kb == nullptr) return hipErrorInvalidValue;
         constexpr int CS2 = RowSplit<D>::CS;
-        if (MODE == 0 && a.h)   // the training forward: O and the chunk-start states
-            hipLaunchKernelGGL((kda_recur4_kernel<D, 2, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
-        else
-            hipLaunchKernelGGL((kda_recur4_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
+        hipLaunchKernelGGL((kda_recur4_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(512), 0, st, a);
     } else if constexpr (std::is_same<ST, uint16_t>::value && D >= 64) {
         constexpr int CS2 = RowSplit<D>::CS;
         hipLaunchKernelGGL((kda_recur3_kernel<D, MODE, CS2>), dim3(a.BH * CS2), dim3(256), 0, st, a);
@@ -2354,8 +2323,6 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
 }
 
 bool recur_epilogue_supported(int D, int in_bf16) { return in_bf16 ? D == 64 : (D == 32 || D == 64); }
-
-bool fwd_writes_states(int D, int in_bf16) { return in_bf16 && D == 64; }
 
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st) {
     if (D == 32) return in_bf16 ? launch_dh_t<32, uint16_t>(a, st) : launch_dh_t<32, float>(a, st);

@@ -231,9 +231,8 @@ class ChunkKDAFunction(torch.autograd.Function):
     """Autograd wrapper (the role of mx.custom_function in
     nope_gdn_mlx.py:2725-2808).  When a gradient is needed the forward keeps its
     inputs and the per-chunk factors of kda_forward_train -- not the U / S
-    trajectories the reference keeps.  With bf16 inputs at D = 64 the training
-    forward also leaves the chunk-start states there; otherwise the backward
-    recomputes them from those factors."""
+    trajectories the reference keeps; the backward recomputes the
+    chunk-boundary states from those factors."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, initial_state):

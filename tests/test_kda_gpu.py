@@ -316,14 +316,12 @@ def test_bwd_parity_config2_full():
 @pytest.mark.parametrize("B,T,H,D,dtype,g_scale", [
     (2, 100, 3, 64, torch.bfloat16, 0.1),
     (1, 130, 2, 64, torch.bfloat16, 6.0),     # pairwise path writes both A_qk layouts directly
-    (2, 333, 3, 64, torch.bfloat16, 0.1),     # six chunks: the forward's h copy past the LDS set wrap
+    (2, 333, 3, 64, torch.bfloat16, 0.1),     # six chunks: the recurrences' LDS sets wrap
     (1, 65, 2, 32, torch.float32, 0.1),
     (1, 1, 1, 64, torch.float32, 0.1),
 ])
 def test_training_pair_equals_standalone_calls(B, T, H, D, dtype, g_scale):
-    """kda_fwd_train / kda_bwd_train reproduce kda_fwd / kda_bwd bit for bit
-    (with bf16 at D = 64 the training forward writes the chunk-start states that
-    kda_bwd recomputes, so this also checks them bit for bit)."""
+    """kda_fwd_train / kda_bwd_train reproduce kda_fwd / kda_bwd bit for bit."""
     kda = _kda()
     x = _inputs(B, T, H, D, dtype, seed=16, with_state=True, grad=True, g_scale=g_scale)
     q, k, v, g, beta = _dev(x)
