@@ -301,6 +301,18 @@ __device__ __forceinline__ Frag8 ldfragT(const uint16_t* M, int ld, int n0, int 
     f.h = __builtin_bit_cast(bf16x8, short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
     return f;
 }
+// Eight consecutive rows of one column of an [n][ld] bf16 LDS tile X, for
+// writing its transpose as 16-byte row pieces: lane i of each 16-lane group
+// receives X[n0 + 8 (i / 4) + c][k0 + i % 4], c = 0..7, with two transposing
+// reads (the group covers columns k0..k0+3 of rows n0..n0+31).  Rows of X
+// must be 8-byte aligned at column k0.
+__device__ __forceinline__ short8v ld_tr_rows8(const uint16_t* X, int ld, int n0, int k0) {
+    const int j = lane_id() & 15;
+    const uint16_t* p = X + (size_t)(n0 + 8 * (j & 3) + (j >> 2)) * ld + k0;
+    const short4v x = ld_tr4(p), y = ld_tr4(p + (size_t)4 * ld);
+    return short8v{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+
 // the same for a 16x16x16 operand (k-slots 4 g .. 4 g + 3)
 __device__ __forceinline__ Frag4 ldfrag4T_tr(const uint16_t* M, int ld, int n0, int k0) {
     const int l = lane_id(), j = l & 15, g = l >> 4;

@@ -1448,18 +1448,22 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
             if constexpr (L1 > 0) dma_wait_chunks<L1>(k);
         }
     };
-    auto flush = [&](int n) __attribute__((always_inline)) {   // role-1 waves
+    auto flush = [&](int n) __attribute__((always_inline)) {   // role-1 waves, MODE 0: O
         const ST* sst = stg(n);
         const int t1 = tid - 256;
-        if constexpr (FWD) {
-            const int t0 = n * C, valid = min(C, a.T - t0);
-            tile_out_at<ST, C, DC>(t1, sst, LDU,
-                                   static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
-                                   (size_t)a.H * D, valid);
-        } else {
-            const size_t ch = (size_t)bh * nc + n;
-            tile_out_at<ST, D, DC>(t1, sst, LDU, static_cast<ST*>(a.h) + ch * D * D + c0, D, D);
-        }
+        const int t0 = n * C, valid = min(C, a.T - t0);
+        tile_out_at<ST, C, DC>(t1, sst, LDU, static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
+                               (size_t)a.H * D, valid);
+    };
+    // MODE 1, role-1 waves: h of chunk n is the state in xs (S^T, there between
+    // A(n) and B(n)), copied to global as 16-byte row pieces of h by
+    // transposing reads, so the chain waves stage nothing for it
+    auto copy_h = [&](int n) __attribute__((always_inline)) {
+        static_assert(DC == 32 && D * DC / 8 == 256, "one 16-byte piece of h per role-1 thread");
+        const int t1 = tid - 256, i = t1 & 15, row = 4 * (t1 >> 4) + (i & 3), col = 8 * (i >> 2);
+        const short8v x = ld_tr_rows8(xs, LDR, 0, 4 * (t1 >> 4));
+        *reinterpret_cast<short8v*>(static_cast<ST*>(a.h) + ((size_t)bh * nc + n) * D * D + (size_t)row * D + c0 +
+                                    col) = x;
     };
 
     int mt[MT];
@@ -1481,19 +1485,14 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
                 S[i][j] = f32x4{x.x, x.y, x.z, x.w};
             }
         }
-    // S^T for the B operands (and, for the backward, the chunk-start state)
-    auto put_state = [&](ST* sst) __attribute__((always_inline)) {   // chain waves
+    // S^T for the B operands (and, for MODE 1, the copy to h)
+    auto put_state = [&]() __attribute__((always_inline)) {   // chain waves
 #pragma unroll
         for (int i = 0; i < MT; ++i)
             if (own[i])
 #pragma unroll
-                for (int j = 0; j < NTW; ++j) {
+                for (int j = 0; j < NTW; ++j)
                     *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(S[i][j]);
-                    if constexpr (MODE == 1)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, S[i][j][e]);
-                }
     };
 
     // one chunk's A operands, read ahead from its LDS set (each role its own)
@@ -1520,9 +1519,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) Aw[ks] = ldfrag_sw<RB_W>(sW, BS * wr, 32 * ks);
 #pragma unroll
-            for (int j = 0; j < NTW; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) Uv[j][e] = ld_sw<RB_U>(sU, BS * wr + 4 * g4 + e, BS * j + r16);
+            for (int j = 0; j < NTW; ++j) Uv[j] = ld_col4_sw<RB_U>(sU, BS * j, BS * wr);
         } else if constexpr (FWD) {
             const ST* sQp = reinterpret_cast<const ST*>(sb + Lay::QP_OFF);
             const ST* sAqk = reinterpret_cast<const ST*>(sb + Lay::AQK_OFF);
@@ -1535,7 +1532,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
     };
 
     // prologue: chunks 0 .. NS-1 in flight, chunk 0 landed and read
-    if (role == 0) put_state(stg(0));
+    if (role == 0) put_state();
     dma_chunk(0, set0);
     if (nc > 1) dma_chunk(1, set1);
     if (NS == 3 && nc > 2) dma_chunk(2, set2);
@@ -1566,8 +1563,10 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
                 *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * wr + 4 * g4) = pack4bf(Vp);
             }
             preload_kb(scur);
-        } else {
+        } else if constexpr (FWD) {
             if (n > 0) flush(n - 1);
+        } else {
+            copy_h(n);
         }
         // chunk n+1's slabs landed; chunks up to n+NS-1 (issued after earlier B
         // barriers) may stay in flight
@@ -1597,7 +1596,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
                         for (int ks = 0; ks < C / 32; ++ks) S[i][j] = mma<1>(Akb[i][ks], Bv[j][ks], S[i][j]);
                     }
                 }
-            if (n + 1 < nc) put_state(stg(n + 1));
+            if (n + 1 < nc) put_state();
             if (n + NS < nc) dma_chunk(n + NS, sdma);
         } else if constexpr (FWD) {
             // O = Qp S + Aqk V', row block wr (the chunk-start state is in Bs)
@@ -1622,7 +1621,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
         if (NS == 3 && n + 2 < nc) step(n + 2, set2, set0, set2);
     }
     lds_barrier();
-    if (role == 1) flush(nc - 1);
+    if (FWD && role == 1) flush(nc - 1);
 
     if (FWD && a.s_final) {
 #pragma unroll
