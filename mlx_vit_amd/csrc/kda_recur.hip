@@ -1979,13 +1979,12 @@ struct Dh3Layout {
 // kda_dh4_kernel: the reverse state recurrence (loop step k on chunk
 // nc-1-k), the pipeline of kda_recur3_kernel with the work split between
 // two wave roles (512 threads).  Waves 0-3 run the reverse state chain: dV' (row block wr),
-// the dS update of state rows wr, wr + 4, dS^T / dh / dV' staging, the flush
-// of the previous step's staged dh and dV', and read the next chunk's
-// operands.  Waves 4-7 bring the slabs by DMA (after barrier B, when the
-// step's set is free) and transpose the next chunk's dO tile into dOT so that
-// the chain waves read it as B fragments with row reads instead of column
-// gathers.  Two staging tiles suffice: a tile is flushed before barrier B and
-// refilled after it.
+// the dS update of state rows wr, wr + 4, the dS^T and -dV'^T exchange tiles,
+// and read the next chunk's operands.  Waves 4-7 bring the slabs by DMA (after
+// barrier B, when the step's set is free), transpose the next chunk's dO tile
+// into dOT so that the chain waves read it as B fragments with row reads
+// instead of column gathers, and copy the step's outputs straight from the
+// exchange tiles: dh from dS^T before barrier B, dV' from -dV'^T after it.
 // ----------------------------------------------------------------------------
 template <int D, int CS>
 struct Dh4Layout {
@@ -1995,11 +1994,9 @@ struct Dh4Layout {
     static constexpr int XS_OFF = B3::XS_OFF, XV_OFF = B3::XV_OFF;
     static constexpr int DOT_OFF = B3::STG_OFF;                                // dO^T [2][DC][LDO] bf16
     static constexpr int DOT_BYTES = DC * LDO * 2;
-    static constexpr int STG_OFF = DOT_OFF + 2 * DOT_BYTES;
-    static constexpr int STG_BYTES = B3::STG_BYTES, NSTG = 2;
-    static constexpr int XBYTES = STG_OFF + NSTG * STG_BYTES;
+    static constexpr int XBYTES = DOT_OFF + 2 * DOT_BYTES;
     static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "reverse recurrence LDS");
-    static_assert(DOT_OFF % 16 == 0 && STG_OFF % 16 == 0, "16-byte aligned tiles");
+    static_assert(DOT_OFF % 16 == 0, "16-byte aligned tiles");
 };
 
 template <int D, int CS>
@@ -2030,9 +2027,6 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     const char* gdO = static_cast<const char*>(a.dout);
     const char* gEg = reinterpret_cast<const char*>(a.eG);
 
-    auto stg = [&](int k) __attribute__((always_inline)) {
-        return reinterpret_cast<ST*>(smem + Lay::STG_OFF + (k % Lay::NSTG) * Lay::STG_BYTES);
-    };
     auto dot = [&](int k) __attribute__((always_inline)) {
         return reinterpret_cast<ST*>(smem + Lay::DOT_OFF + (k & 1) * Lay::DOT_BYTES);
     };
@@ -2088,13 +2082,22 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
             *reinterpret_cast<uint2*>(o + nn * LDO + 8 * g8 + 4) = make_uint2(u[4] | (u[5] << 16), u[6] | (u[7] << 16));
         }
     };
-    // Staged dh and dV' of step k -> global, by the chain waves: the side waves
-    // then issue only DMA, so their vmcnt waits count slabs and no stores.
-    auto flush = [&](int k) __attribute__((always_inline)) {   // chain waves
-        const ST* sst = stg(k);
+    // Outputs of step k, by the role-1 waves from the exchange tiles, as 16-byte
+    // row pieces by transposing reads (one piece per thread and tile): dh from
+    // dS^T in xs (there between A(k) and B(k)), dV' from -dV'^T in xv (there
+    // between B(k) and A(k+1)), negated back
+    static_assert(DC == 32 && D * DC / 8 == 256 && C * DC / 8 == 256, "one 16-byte piece per role-1 thread");
+    const int t1 = tid - 256, pi = t1 & 15, prow = 4 * (t1 >> 4) + (pi & 3), pcol = c0 + 8 * (pi >> 2);
+    auto copy_dh = [&](int k) __attribute__((always_inline)) {
         const size_t ch = (size_t)bh * nc + (nc - 1 - k);
-        tile_out_at<ST, D, DC>(tid, sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
-        tile_out_at<ST, C, DC>(tid, sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
+        const short8v x = ld_tr_rows8(xs, LDR, 0, 4 * (t1 >> 4));
+        *reinterpret_cast<short8v*>(static_cast<ST*>(a.dh) + ch * D * D + (size_t)prow * D + pcol) = x;
+    };
+    auto copy_dvp = [&](int k) __attribute__((always_inline)) {
+        const size_t ch = (size_t)bh * nc + (nc - 1 - k);
+        const short8v x = ld_tr_rows8(xv, LDC, 0, 4 * (t1 >> 4)) ^ short8v{(short)0x8000, (short)0x8000,
+            (short)0x8000, (short)0x8000, (short)0x8000, (short)0x8000, (short)0x8000, (short)0x8000};
+        *reinterpret_cast<short8v*>(static_cast<ST*>(a.dVp) + ch * C * D + (size_t)prow * D + pcol) = x;
     };
 
     int mt[MT];
@@ -2116,17 +2119,13 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
                 dS[i][j] = f32x4{x.x, x.y, x.z, x.w};
             }
         }
-    auto put_state = [&](ST* sst) __attribute__((always_inline)) {   // chain waves
+    auto put_state = [&]() __attribute__((always_inline)) {   // chain waves
 #pragma unroll
         for (int i = 0; i < MT; ++i)
             if (own[i])
 #pragma unroll
-                for (int j = 0; j < NTW; ++j) {
+                for (int j = 0; j < NTW; ++j)
                     *reinterpret_cast<uint2*>(xs + (BS * j + r16) * LDR + BS * mt[i] + 4 * g4) = pack4bf(dS[i][j]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        st1<ST>(sst + (BS * mt[i] + 4 * g4 + e) * LDU + BS * j + r16, dS[i][j][e]);
-                }
     };
 
     Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
@@ -2160,7 +2159,7 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     };
 
     // prologue: steps 0 .. NS-1 in flight; step 0's dO transposed, its operands read
-    if (role == 0) put_state(stg(0));
+    if (role == 0) put_state();
     if (role == 1) {
         dma_step(0, set0);
         if (nc > 1) dma_step(1, set1);
@@ -2174,7 +2173,6 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
 
     // step k: chunk nc-1-k in set k % NS
     auto step = [&](int k, char* scur, const char* snext) __attribute__((always_inline)) {
-        ST* sst = stg(k);
         lds_barrier();                                          // A(k): dS^T in xs
         if (role == 0) {
             Frag8 Bs[NTW][D / 32];
@@ -2192,14 +2190,14 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < D / 32; ++ks) dV = mma<1>(Akb[ks], Bs[j][ks], dV);
                 *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * wr + 4 * g4) = pack4bf(negacc(dV));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) st1<ST>(sst + D * LDU + (BS * wr + 4 * g4 + e) * LDU + BS * j + r16, dV[e]);
             }
-            if (k > 0) flush(k - 1);
-        } else if (k + 1 < nc) {
-            // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight)
-            dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
-            transpose_do(k + 1, snext);
+        } else {
+            if (k + 1 < nc) {
+                // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight)
+                dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
+                transpose_do(k + 1, snext);
+            }
+            copy_dh(k);   // after the wait: a store issued before it would hold the count
         }
         lds_barrier();                                          // B(k): -dV'^T in xv, dOT of k+1
         if (role == 0) {
@@ -2224,13 +2222,14 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
                     }
                 }
             if (k + 1 < nc) {
-                put_state(stg(k + 1));
+                put_state();
                 preload(k + 1, snext);
             }
         } else {
             // set k % NS is free: chunk k's operands are in the chain waves'
             // registers and its dO was transposed in step k-1
             if (k + NS < nc) dma_step(k + NS, scur);
+            copy_dvp(k);
         }
     };
     for (int k = 0; k < nc; k += 3) {
@@ -2238,8 +2237,6 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
         if (k + 1 < nc) step(k + 1, set1, set2);
         if (k + 2 < nc) step(k + 2, set2, set0);
     }
-    lds_barrier();
-    if (role == 0) flush(nc - 1);
 
     if (a.ds0) {
 #pragma unroll
