@@ -398,6 +398,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
 
         // block forward substitution; the wave's column tiles of [Kt | beta V] advance together
         f32x4 X[TPW][NB];
+        Frag4 XB[TPW][NB - 1];   // X's split-bf16 B fragments, formed once for the later blocks
         bool tok[TPW], isK[TPW];
         int dcol[TPW];
 #pragma unroll
@@ -460,11 +461,14 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 const Frag4 A = frag4_from_f32<3>(lv);
 #pragma unroll
                 for (int jj = 0; jj < TPW; ++jj)
-                    if (tok[jj]) Y[jj] = mma4f<3>(A, accfrag4<3>(X[jj][j]), Y[jj]);
+                    if (tok[jj]) Y[jj] = mma4f<3>(A, XB[jj][j], Y[jj]);
             }
             const Frag4 Tf = ldfrag4<3, float>(&tii[i][0][0], BS + 4, 0, 0);
 #pragma unroll
-            for (int jj = 0; jj < TPW; ++jj) X[jj][i] = tok[jj] ? mma4f<3>(Tf, accfrag4<3>(Y[jj]), zero4()) : zero4();
+            for (int jj = 0; jj < TPW; ++jj) {
+                X[jj][i] = tok[jj] ? mma4f<3>(Tf, accfrag4<3>(Y[jj]), zero4()) : zero4();
+                if (i < NB - 1) XB[jj][i] = accfrag4<3>(X[jj][i]);
+            }
         }
         __syncthreads();
         // PHASE 7
