@@ -243,21 +243,23 @@ __device__ __forceinline__ float fac_tile(const ChunkSmem<D, ST>& s, int i, int 
 // before anything is written to LDS; every wave's q, k, g, beta requests enter
 // the memory pipeline before any v request.  v stays in tv for the caller to
 // store once its latency is hidden.  Rows >= valid are zero.  g is loaded as
-// lane (row 16 w + r16 of block w, channel groups g4, g4 + 4, .. of 8
-// channels): the 16 rows of a block sit in the 16 lanes of one DPP row, so s.g
-// receives a, the inclusive cumsum of g inside each 16-row block, computed by
-// a four-step lane scan.  256 threads.  Returns 1 if this thread saw g > 0 or
-// a NaN.
-template <int D, typename ST, typename TG, bool WITH_V>
-__device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& tv, const ST* __restrict__ q,
+// lane (row 16 b + r16 of block b, 8-channel groups): the 16 rows of a block
+// sit in the 16 lanes of one DPP row, so s.g receives a, the inclusive cumsum
+// of g inside each 16-row block, computed by a four-step lane scan.  NTH
+// threads: NTH / 256 waves per block, wave w covering block w / (NTH / 256)
+// and the channel groups 4 (w % (NTH / 256)) + g4 + 4 (NTH / 256) cp.
+// Returns 1 if this thread saw g > 0 or a NaN.
+template <int D, typename ST, typename TG, bool WITH_V, int NTH = 256>
+__device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D, NTH>& tv, const ST* __restrict__ q,
                                            const ST* __restrict__ k, const ST* __restrict__ v,
                                            const TG* __restrict__ g, const ST* __restrict__ beta, size_t base,
                                            size_t rstride, size_t bbase, int H, int valid) {
-    constexpr int NCG = D / 8, CPL = NCG / 4, GV = 8 * (int)sizeof(TG) / 16, GE = 16 / (int)sizeof(TG);
-    static_assert(NCG % 4 == 0 && NB == 4, "four waves of 16 rows, 8-channel groups");
-    Tile<ST, C, D> tq, tk;
+    constexpr int WPB = NTH / 256, NCG = D / 8, CPL = NCG / (4 * WPB), GV = 8 * (int)sizeof(TG) / 16,
+                  GE = 16 / (int)sizeof(TG);
+    static_assert(NB == 4 && NCG % (4 * WPB) == 0, "whole 8-channel groups per lane");
+    Tile<ST, C, D, NTH> tq, tk;
     const int tid = threadIdx.x, w = tid >> 6, r16 = tid & 15, g4 = (tid >> 4) & 3;
-    const int grow = BS * w + r16;
+    const int grow = BS * (w / WPB) + r16, gc0 = 4 * (w % WPB) + g4;
     uint4 graw[CPL][GV];
     tq.load(q + base, rstride, valid);
     tk.load(k + base, rstride, valid);
@@ -267,7 +269,7 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& 
         for (int cp = 0; cp < CPL; ++cp)
 #pragma unroll
             for (int vq = 0; vq < GV; ++vq)
-                graw[cp][vq] = *reinterpret_cast<const uint4*>(gp + 8 * (g4 + 4 * cp) + GE * vq);
+                graw[cp][vq] = *reinterpret_cast<const uint4*>(gp + 8 * (gc0 + 4 * WPB * cp) + GE * vq);
     }
     const float braw = ld1<ST>(beta + bbase + (size_t)min(tid, valid - 1) * H);
     if constexpr (WITH_V) {
@@ -291,7 +293,7 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D>& 
             if (!(x[e] <= 0.f)) flag = 1;
             x[e] = row16_scan(x[e]);
         }
-        float* dst = &s.g[grow][8 * (g4 + 4 * cp)];
+        float* dst = &s.g[grow][8 * (gc0 + 4 * WPB * cp)];
         *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
         *reinterpret_cast<float4*>(dst + 4) = make_float4(x[4], x[5], x[6], x[7]);
     }

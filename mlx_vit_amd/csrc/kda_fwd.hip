@@ -43,11 +43,13 @@ struct PrepGeom {
     static constexpr bool STG_IN_G = (int)sizeof(float) * C * CSm::LDG >= C * LDT * (int)sizeof(ST);
 };
 
-template <int D, typename ST, typename TG, int PREC>
-__global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
+template <int D, typename ST, typename TG, int PREC, int NTH>
+__global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
     using G = PrepGeom<D, ST>;
+    constexpr int NW = NTH / 64;   // waves
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
     constexpr int LDK = G::LDK, LDA = G::LDA, LDT = G::LDT, NT = D / BS, NCT = 2 * NT;
-    constexpr int TPW = (NCT + 3) / 4;
+    constexpr int TPW = (NCT + NW - 1) / NW;
     constexpr int EPV = 16 / (int)sizeof(ST);
     __shared__ ChunkSmem<D, ST> s;
     __shared__ __align__(16) float sa[C][LDA];            // Akk, fp32, strictly lower, unscaled
@@ -56,7 +58,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     __shared__ __align__(16) ST stgbuf[G::STG_IN_G ? 1 : C][G::STG_IN_G ? 8 : LDT];
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, g4 = l >> 4;
-    __builtin_assume(w >= 0 && w < 4);
+    __builtin_assume(w >= 0 && w < NW);
     const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
     const int b = bh / a.H, h = bh - b * a.H;
     const int t0 = n * C, valid = min(C, a.T - t0);
@@ -91,10 +93,10 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
     int* flagw = reinterpret_cast<int*>(&sa[0][C]);
     if (tid == 0) *flagw = 0;
     // PHASE 0 (load); v stays in registers until the column pass is done
-    Tile<ST, C, D> tv;
-    const int flag = chunk_load2<D, ST, TG, G::STAGE_V>(s, tv, q, k, v, g, beta, base, rs, bbase, a.H, valid);
+    Tile<ST, C, D, NTH> tv;
+    const int flag = chunk_load2<D, ST, TG, G::STAGE_V, NTH>(s, tv, q, k, v, g, beta, base, rs, bbase, a.H, valid);
     // PHASE 1
-    const int dfl = chunk_factors2<D, ST, PREC>(s, flag, flagw);
+    const int dfl = chunk_factors2<D, ST, PREC, NTH>(s, flag, flagw);
     // The rest of the kernel is instantiated twice.  Chunks whose 16-row blocks
     // all stay within the span guard (every chunk at ordinary decays) run a copy
     // with the sub-anchored and pairwise code compiled out, so that code shapes
@@ -114,12 +116,12 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
 
         // A_qk of the pairwise diagonal-tile entries this thread owns: kept in
         // registers until the tile is staged (the staging buffer may be the g region)
-        constexpr int NPW = NB * BS * BS / 256;
+        constexpr int NPW = NB * BS * BS / NTH;
         float paq[NPW], saq[4];
         const int qmask = pmask & (dfl >> 5);           // ... whose 4-row sub-blocks also exceed it
         if (unsafe) {
             // every pair s <= t from raw q (ql), raw k (kr), exact exp(gamma_t - gamma_s)
-            for (int p = tid; p < C * C; p += 256) {
+            for (int p = tid; p < C * C; p += NTH) {
                 const int t = p / C, sx = p - t * C;
                 float ak = 0.f, aq = 0.f;
                 if (sx <= t) {
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 const int nent = __popc(qmask) * BS * BS;
 #pragma unroll
                 for (int it = 0; it < NPW; ++it) {
-                    const int pp = tid + 256 * it;
+                    const int pp = tid + NTH * it;
                     paq[it] = 0.f;
                     if (pp < nent) {
                         const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                     x[4 * q4] = v4.x; x[4 * q4 + 1] = v4.y; x[4 * q4 + 2] = v4.z; x[4 * q4 + 3] = v4.w;
                 }
             };
-            for (int vv = tid; vv < NV; vv += 256) {
+            for (int vv = tid; vv < NV; vv += NTH) {
                 const int t = vv / VPR, c0 = (vv - t * VPR) * EPV, blk = t / BS;
                 const Vec16<ST> qv{*reinterpret_cast<const uint4*>(&s.ql[t][c0])};
                 const Vec16<ST> kv{*reinterpret_cast<const uint4*>(&s.kr[t][c0])};
@@ -248,24 +250,25 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
         // halves of one K = 32 step, so the product keeps fp32 accuracy until the
         // final rounding.
         if (std::is_same<ST, uint16_t>::value && !unsafe) {
-            // wave w: tiles w, w + 4, ... of each output (NT per wave), unrolled so
-            // that all of a wave's operand reads share one LDS round trip
+            // wave w: tiles w, w + NW, ... of each output (NB NT / NW per wave),
+            // unrolled so that all of a wave's operand reads share one LDS round trip
+            constexpr int PBT = NB * NT / NW;
 #pragma unroll
             for (int o = 0; o < 2; ++o) {
                 ST* out = o ? oQpT : oKbT;
                 if (out == nullptr) continue;
                 const ST* X = o ? &s.ql[0][0] : &s.kr[0][0];
-                Frag4 A[NT];
-                float sv[NT];
+                Frag4 A[PBT];
+                float sv[PBT];
 #pragma unroll
-                for (int it = 0; it < NT; ++it) {
-                    const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
+                for (int it = 0; it < PBT; ++it) {
+                    const int tt = w + NW * it, i = tt / NT, j = tt - i * NT;
                     A[it] = ldfrag4<1, ST>(X, LDK, BS * i, BS * j);
                     sv[it] = o ? fac_ep(s, i, BS * j + r16) : fac_eq(s, i, BS * j + r16);
                 }
 #pragma unroll
-                for (int it = 0; it < NT; ++it) {
-                    const int tt = w + 4 * it, i = tt / NT, j = tt - i * NT;
+                for (int it = 0; it < PBT; ++it) {
+                    const int tt = w + NW * it, i = tt / NT, j = tt - i * NT;
                     const short hi = (short)f2bf(sv[it]), lo = (short)f2bf(sv[it] - bf2f((uint16_t)hi));
                     short4v bh, bl;
 #pragma unroll
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
         } else {
             // column threads (d, EPV tokens)
             constexpr int GPC = C / EPV, NV = D * GPC;
-            for (int vv = tid; vv < NV; vv += 256) {
+            for (int vv = tid; vv < NV; vv += NTH) {
                 const int d = vv / GPC, tb = (vv - d * GPC) * EPV;
                 float okb[EPV], oqp[EPV];
 #pragma unroll
@@ -316,7 +319,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
             // block j times the tile's channel factor (F_ij, 1 between adjacent
             // blocks, e^{-T_i} on the diagonal).  Diagonal tiles of blocks in pmask
             // were formed pair by pair.
-            for (int tix = w; tix < 10; tix += 4) {
+            for (int tix = w; tix < 10; tix += NW) {
                 int i, j;
                 tile_ij(tix, i, j);
                 if (j == i && ((pmask >> i) & 1)) continue;
@@ -351,7 +354,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 const int nent = __popc(qmask) * BS * BS;
 #pragma unroll
                 for (int it = 0; it < NPW; ++it) {
-                    const int pp = tid + 256 * it;
+                    const int pp = tid + NTH * it;
                     if (pp < nent) {
                         const int kb = pp / (BS * BS), e = pp - kb * BS * BS;
                         int blk = 0;
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 }
             }
             // strictly upper sub-block tiles are zero
-            for (int idx = tid; idx < 6 * BS * BS; idx += 256) {
+            for (int idx = tid; idx < 6 * BS * BS; idx += NTH) {
                 const int tile = idx / (BS * BS), e = idx - tile * BS * BS;
                 const int i = (tile < 3) ? 0 : (tile < 5) ? 1 : 2;
                 const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
@@ -370,11 +373,11 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                 sa[t][sx] = 0.f;
                 if (oAqk) st1<ST>(stA + t * LDT + sx, 0.f);
             }
-            if (oAqkT && w >= 2) {
-                // waves 2-3 formed two of the ten lower tiles (waves 0-1 three): they
-                // write the six zero tiles
+            constexpr int ZW = 10 % NW;   // waves >= ZW formed one tile fewer of the ten
+            if (oAqkT && w >= ZW) {
+                // they write the six zero tiles
                 const float z[4] = {0.f, 0.f, 0.f, 0.f};
-                for (int u = w - 2; u < 6; u += 2) {   // tile (i, j), i < j
+                for (int u = w - ZW; u < 6; u += NW - ZW) {   // tile (i, j), i < j
                     const int i = (u < 3) ? 0 : (u < 5) ? 1 : 2;
                     const int j = (u < 3) ? u + 1 : (u < 5) ? u - 1 : 3;
                     st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, z);
@@ -384,10 +387,10 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
         __syncthreads();
         // PHASE 5
         if (!unsafe) {
-            if (oAqk) tile_out<ST, C, C>(stA, LDT, oAqk + cCC, C, C);
-            if (a_Akk) tile_out<float, C, C>(&sa[0][0], LDA, a_Akk + cCC, C, C);
+            if (oAqk) tile_out<ST, C, C, NTH>(stA, LDT, oAqk + cCC, C, C);
+            if (a_Akk) tile_out<float, C, C, NTH>(&sa[0][0], LDA, a_Akk + cCC, C, C);
         }
-        diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
+        if (w < NB) diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
         __syncthreads();
         // PHASE 6
         if (a_Tii && tid < NB * BS * BS / 4) {
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
         int dcol[TPW];
 #pragma unroll
         for (int jj = 0; jj < TPW; ++jj) {
-            const int ct = w + 4 * jj;
+            const int ct = w + NW * jj;
             tok[jj] = ct < NCT;
             isK[jj] = ct < NT;
             dcol[jj] = (isK[jj] ? ct : ct - NT) * BS + r16;
@@ -492,8 +495,8 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
                     }
                 }
         __syncthreads();
-        tile_out<ST, C, D>(stW, LDK, oW + cCD, D, C);
-        tile_out<ST, C, D>(stU, LDK, oU + cCD, D, C);
+        tile_out<ST, C, D, NTH>(stW, LDK, oW + cCD, D, C);
+        tile_out<ST, C, D, NTH>(stU, LDK, oU + cCD, D, C);
         // PHASE 8
     };
     if (dfl & 31)
@@ -505,10 +508,15 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const PrepArgs a) {
 // ----------------------------------------------------------------------------
 // launchers
 // ----------------------------------------------------------------------------
+#ifndef KDA_PREP_NTH
+#define KDA_PREP_NTH 512
+#endif
 template <int D, typename ST, typename TG>
 static hipError_t launch_prep_t(const PrepArgs& a, int nchunks, hipStream_t st) {
     constexpr int PREC = std::is_same<ST, float>::value ? 3 : 1;
-    hipLaunchKernelGGL((kda_prep_kernel<D, ST, TG, PREC>), dim3(nchunks), dim3(256), 0, st, a);
+    // eight waves per chunk where the registers allow four waves per SIMD
+    constexpr int NTH = (D == 64) ? KDA_PREP_NTH : 256;
+    hipLaunchKernelGGL((kda_prep_kernel<D, ST, TG, PREC, NTH>), dim3(nchunks), dim3(NTH), 0, st, a);
     return hipGetLastError();
 }
 
