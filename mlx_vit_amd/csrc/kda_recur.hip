@@ -1448,12 +1448,19 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
             if constexpr (L1 > 0) dma_wait_chunks<L1>(k);
         }
     };
-    auto flush = [&](int n) __attribute__((always_inline)) {   // role-1 waves, MODE 0: O
-        const ST* sst = stg(n);
-        const int t1 = tid - 256;
+    // MODE 0: O of chunk n is staged transposed, O^T [DC][LDO] (a lane's four
+    // rows of one column are one 8-byte write), and flushed by the role-1 waves
+    // as 16-byte row pieces by transposing reads
+    constexpr int LDO = C + 4;
+    static_assert(DC * LDO * 2 <= Lay::STG_BYTES, "O^T staging fits a staging tile");
+    auto flush = [&](int n) __attribute__((always_inline)) {   // role-1 waves
+        static_assert(DC == 32 && C * DC / 8 == 256, "one 16-byte piece of O per role-1 thread");
+        const int t1 = tid - 256, i = t1 & 15, row = 4 * (t1 >> 4) + (i & 3), col = 8 * (i >> 2);
         const int t0 = n * C, valid = min(C, a.T - t0);
-        tile_out_at<ST, C, DC>(t1, sst, LDU, static_cast<ST*>(a.o) + (((size_t)b * a.T + t0) * a.H + h) * D + c0,
-                               (size_t)a.H * D, valid);
+        const short8v x = ld_tr_rows8(stg(n), LDO, 0, 4 * (t1 >> 4));
+        if (row < valid)
+            *reinterpret_cast<short8v*>(static_cast<ST*>(a.o) + (((size_t)b * a.T + t0 + row) * a.H + h) * D + c0 +
+                                        col) = x;
     };
     // MODE 1, role-1 waves: h of chunk n is the state in xs (S^T, there between
     // A(n) and B(n)), copied to global as 16-byte row pieces of h by
@@ -1497,6 +1504,7 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
 
     // one chunk's A operands, read ahead from its LDS set (each role its own)
     Frag8 Aw[D / 32], Aq[D / 32], Aa[2], Akb[MT][C / 32];
+    f32x4 Ov[NTW];   // role 1, MODE 0: the chunk's Qp S part of O, across barrier B
     f32x4 Uv[NTW];
     float4 eg[MT];
     // chain waves: the state-update operands (Kb^T rows, e^G) of a chunk, read
@@ -1564,6 +1572,14 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
             }
             preload_kb(scur);
         } else if constexpr (FWD) {
+            // O = Qp S + Aqk V': the Qp S part now, from the chunk-start state
+            // (beside the chain's V'), the Aqk V' part after barrier B
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                Ov[j] = zero4();
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) Ov[j] = mma<1>(Aq[ks], Bs[j][ks], Ov[j]);
+            }
             if (n > 0) flush(n - 1);
         } else {
             copy_h(n);
@@ -1599,17 +1615,14 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
             if (n + 1 < nc) put_state();
             if (n + NS < nc) dma_chunk(n + NS, sdma);
         } else if constexpr (FWD) {
-            // O = Qp S + Aqk V', row block wr (the chunk-start state is in Bs)
+            // O += Aqk V', row block wr; staged as O^T
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
-                f32x4 O = zero4();
-#pragma unroll
-                for (int ks = 0; ks < D / 32; ++ks) O = mma<1>(Aq[ks], Bs[j][ks], O);
+                f32x4 O = Ov[j];
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
                     if (ks <= wr / 2) O = mma<1>(Aa[ks], Bv[j][ks], O);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) st1<ST>(sst + (BS * wr + 4 * g4 + e) * LDU + BS * j + r16, O[e]);
+                *reinterpret_cast<uint2*>(sst + (BS * j + r16) * LDO + BS * wr + 4 * g4) = pack4bf(O);
             }
         }
         if (n + 1 < nc) preload(snext);
