@@ -2142,6 +2142,7 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     };
 
     Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
+    f32x4 dVa[NTW];   // the chunk's A_qk^T dO part of dV', formed with its operands
     float4 eg[MT];
     auto preload = [&](int k, const char* sb) __attribute__((always_inline)) {   // chain waves
         const ST* sAqk = reinterpret_cast<const ST*>(sb + B3::AQK_OFF);
@@ -2169,6 +2170,14 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
                 }
                 eg[i] = *reinterpret_cast<const float4*>(seG + BS * mt[i] + 4 * g4);
             }
+        // A_qk^T dO does not depend on the chain: formed here, off barrier A's path
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            dVa[j] = zero4();
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (ks >= wr / 2) dVa[j] = mma<1>(Aat[ks], Bo[j][ks], dVa[j]);
+        }
     };
 
     // prologue: steps 0 .. NS-1 in flight; step 0's dO transposed, its operands read
@@ -2196,10 +2205,7 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
             // dV' = Aqk^T dO + Kb dS, row block wr
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
-                f32x4 dV = zero4();
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    if (ks >= wr / 2) dV = mma<1>(Aat[ks], Bo[j][ks], dV);
+                f32x4 dV = dVa[j];
 #pragma unroll
                 for (int ks = 0; ks < D / 32; ++ks) dV = mma<1>(Akb[ks], Bs[j][ks], dV);
                 *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * wr + 4 * g4) = pack4bf(negacc(dV));
