@@ -31,6 +31,8 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef short short8v __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int C = 64;       // chunk length (tokens)
 constexpr int BS = 16;      // sub-block edge = MFMA tile edge
@@ -47,6 +49,20 @@ __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint
 
 // round to nearest even (v_cvt_pk_bf16_f32; NaN stays NaN)
 __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// Two floats to a packed bf16 pair, a in the low half: one v_cvt_pk_bf16_f32
+// with both sources (converting each alone and merging the halves costs four
+// VALU operations).  Same rounding as f2bf.
+__device__ __forceinline__ uint32_t pack2bf(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+// the two halves of a packed pair back as floats
+__device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+// packed pair of (v - the value of v's bf16 pair): the lo parts of a bf16 hi + lo split
+__device__ __forceinline__ uint32_t pack2bf_rest(float a, float b, uint32_t h) {
+    return pack2bf(a - bf_lo(h), b - bf_hi(h));
+}
 
 template <typename T> __device__ __forceinline__ float ld1(const T* p);
 template <> __device__ __forceinline__ float ld1<float>(const float* p) { return *p; }
@@ -83,10 +99,12 @@ __device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
 template <int PREC>
 __device__ __forceinline__ f32x4 mma8(const Fr8& a, const Fr8& b, f32x4 c) {
     if constexpr (PREC == 1) {
-        bf16x8 A, B;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { A[e] = (__bf16)a.v[e]; B[e] = (__bf16)b.v[e]; }
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, c, 0, 0, 0);
+        const uint4 A = make_uint4(pack2bf(a.v[0], a.v[1]), pack2bf(a.v[2], a.v[3]), pack2bf(a.v[4], a.v[5]),
+                                   pack2bf(a.v[6], a.v[7]));
+        const uint4 B = make_uint4(pack2bf(b.v[0], b.v[1]), pack2bf(b.v[2], b.v[3]), pack2bf(b.v[4], b.v[5]),
+                                   pack2bf(b.v[6], b.v[7]));
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A), __builtin_bit_cast(bf16x8, B), c,
+                                                       0, 0, 0);
     } else {
         bf16x8 Ah, Al, Bh, Bl;
 #pragma unroll
@@ -102,10 +120,7 @@ __device__ __forceinline__ f32x4 mma8(const Fr8& a, const Fr8& b, f32x4 c) {
 }
 
 __device__ __forceinline__ short4v pack4(const float* v) {
-    short4v r;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = (short)f2bf(v[e]);
-    return r;
+    return __builtin_bit_cast(short4v, make_uint2(pack2bf(v[0], v[1]), pack2bf(v[2], v[3])));
 }
 
 template <int PREC>
@@ -206,27 +221,30 @@ __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 struct Frag8 { bf16x8 h, l; };
 struct Frag4 { short4v h, l; };
 
+// hi = bf16(v), lo = bf16(v - hi) (PREC >= 2), converted a pair at a time
 template <int PREC>
 __device__ __forceinline__ Frag8 frag_from_f32(const float* v) {
     Frag8 f;
+    uint32_t h[4], lo[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const __bf16 hi = (__bf16)v[e];
-        f.h[e] = hi;
-        if constexpr (PREC >= 2) f.l[e] = (__bf16)(v[e] - (float)hi);
+    for (int p = 0; p < 4; ++p) {
+        h[p] = pack2bf(v[2 * p], v[2 * p + 1]);
+        if constexpr (PREC >= 2) lo[p] = pack2bf_rest(v[2 * p], v[2 * p + 1], h[p]);
     }
+    f.h = __builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3]));
+    f.l = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
     return f;
 }
 
 template <int PREC>
 __device__ __forceinline__ Frag4 frag4_from_f32(const float* v) {
     Frag4 f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint16_t hi = f2bf(v[e]);
-        f.h[e] = (short)hi;
-        if constexpr (PREC >= 2) f.l[e] = (short)f2bf(v[e] - bf2f(hi));
-    }
+    const uint32_t h0 = pack2bf(v[0], v[1]), h1 = pack2bf(v[2], v[3]);
+    f.h = __builtin_bit_cast(short4v, make_uint2(h0, h1));
+    if constexpr (PREC >= 2)
+        f.l = __builtin_bit_cast(short4v, make_uint2(pack2bf_rest(v[0], v[1], h0), pack2bf_rest(v[2], v[3], h1)));
+    else
+        f.l = short4v{0, 0, 0, 0};
     return f;
 }
 
@@ -402,10 +420,6 @@ template <> struct Vec16<float> {
         return __uint_as_float((i == 0) ? u.x : (i == 1) ? u.y : (i == 2) ? u.z : u.w);
     }
 };
-
-__device__ __forceinline__ uint32_t pack2bf(float a, float b) {
-    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
-}
 
 // 16 bytes of storage elements from floats (8 bf16 or 4 fp32)
 template <typename ST> __device__ __forceinline__ void store_vec(ST* p, const float* v);
