@@ -221,6 +221,7 @@ constexpr int FAC_EP = 0;   // + i - 1, i = 1..3: e^{gamma_{16i-1}} = e^{T_0 + .
 constexpr int FAC_EQ = 3;   // + j, j = 0..2:     e^{G - gamma_{16j+15}} = e^{T_{j+1} + .. + T_3}
 constexpr int FAC_F = 6;    // (2,0), (3,1), (3,0): F_ij for non-adjacent blocks
 constexpr int FAC_FD = 9;   // + i, i = 0..3:     e^{min(-T_i, SPAN_MAX)}
+constexpr int FAC_ONE = 13;  // 1: the factor of the blocks the rows above skip
 // e^{gamma_{16i-1}}: e^{gamma} at the end of the block before i (1 for i = 0)
 template <int D, typename ST>
 __device__ __forceinline__ float fac_ep(const ChunkSmem<D, ST>& s, int i, int d) {
@@ -329,7 +330,10 @@ template <int D, typename ST, int PREC, int NTH = 256>
 __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag, int* flagw) {
     constexpr int TPC = NTH / D;   // threads per channel
     static_assert(TPC >= 1 && NTH % D == 0, "whole channels per workgroup");
-    const int tid = threadIdx.x, d = tid % D, r = tid / D;
+    const int tid = threadIdx.x, d = tid % D;
+    // whole waves per table row where D is a multiple of the wave size: the row
+    // selects below are then scalar
+    const int r = (D % 64 == 0) ? __builtin_amdgcn_readfirstlane(tid / D) : tid / D;
     int m = flag ? 16 : 0;
     // the channel's four block totals and (one thread per block, TPC >= NB) the
     // block's sub-block ends, all read together
@@ -338,13 +342,14 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag, int
     const float e0 = s.g[BS * ib + 3][d], e1 = s.g[BS * ib + 7][d], e2 = s.g[BS * ib + 11][d];
     const float T12 = T1 + T2;
     // table rows r, r + TPC, ...: exponents are sums of block totals (FAC_*)
-    for (int row = r; row < 13; row += TPC) {
+    for (int row = r; row < FAC_ONE; row += TPC) {
         const float x = (row == 0) ? T0 : (row == 1) ? T0 + T1 : (row == 2) ? (T0 + T1) + T2
                       : (row == 3) ? T1 + (T2 + T3) : (row == 4) ? T2 + T3 : (row == 5) ? T3
                       : (row == 6) ? T1 : (row == 7) ? T2 : (row == 8) ? T12
                       : fminf(-((row == 9) ? T0 : (row == 10) ? T1 : (row == 11) ? T2 : T3), SPAN_MAX);
         s.fac[row][d] = kexp<PREC>(x);
     }
+    if (r == TPC - 1) s.fac[FAC_ONE][d] = 1.f;
     // span guards of blocks r, r + TPC, ...: the whole block and its 4-row sub-blocks
     for (int i = r; i < NB; i += TPC) {
         const float T = (i == 0) ? T0 : (i == 1) ? T1 : (i == 2) ? T2 : T3;

@@ -190,9 +190,9 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
         // pass A: row threads (t, EPV channels).  K_l = K e^{a}, Q_l = Q e^{a},
         // K_r = K e^{b} (anchored chunks; raw K otherwise), Qp = Q_l e^{gamma_{16i-1}},
         // Kb = K_r e^{G - gamma_{16i+15}}.  Every LDS operand is read as 16-byte
-        // vectors up front; the factor rows of the first / last block (which are
-        // 1) are read from a neighbouring row and replaced, so that no load sits
-        // behind a branch.
+        // vectors up front; the factor of the first / last block (1) is the
+        // table's ones row, so that no load sits behind a branch and no product
+        // behind a select.
         {
             constexpr int VPR = D / EPV, NV = C * VPR;
             auto ld_row = [](const float* p, float* x) __attribute__((always_inline)) {
@@ -209,8 +209,8 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
                 float at[EPV], te[EPV], fp[EPV], fq[EPV];
                 ld_row(&s.g[t][c0], at);
                 ld_row(&s.g[BS * blk + BS - 1][c0], te);
-                ld_row(&s.fac[FAC_EP + (blk > 0 ? blk - 1 : 0)][c0], fp);
-                ld_row(&s.fac[FAC_EQ + (blk < NB - 1 ? blk : NB - 2)][c0], fq);
+                ld_row(&s.fac[blk > 0 ? FAC_EP + blk - 1 : FAC_ONE][c0], fp);
+                ld_row(&s.fac[blk < NB - 1 ? FAC_EQ + blk : FAC_ONE][c0], fq);
                 float okl[EPV], oql[EPV], okr[EPV], oqp[EPV], okb[EPV];
 #pragma unroll
                 for (int e = 0; e < EPV; ++e) {
@@ -220,8 +220,8 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
                     okl[e] = kf * el;
                     oql[e] = qf * el;
                     okr[e] = unsafe ? kf : kf * kexp<PREC>(bt);
-                    oqp[e] = (blk > 0) ? oql[e] * fp[e] : oql[e];
-                    okb[e] = (blk < NB - 1) ? okr[e] * fq[e] : okr[e];
+                    oqp[e] = oql[e] * fp[e];   // the ones row for the first block
+                    okb[e] = okr[e] * fq[e];   // ... and for the last
                 }
                 if (unsafe && oKb) {
 #pragma unroll
@@ -314,6 +314,29 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
         // accumulators (a lane's four rows of one column are four consecutive AqkT
         // elements)
         ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];
+        // Split A operands of the solve (bf16 hi, lo of each fp32 value; rows of
+        // 16 hi | 16 lo | pad), formed once in phase 5 and read by every wave as
+        // fragments: the diagonal-block inverses over their own fp32 rows in tii
+        // (the same bytes per block), the six off-diagonal blocks -beta A_kk in
+        // the g region behind the A_qk staging.  Where that does not fit, each
+        // wave splits its own operands.
+        constexpr int SPR = 2 * BS + 8, SPB = BS * SPR;
+        constexpr int STGB = G::STG_IN_G ? C * LDT * (int)sizeof(ST) : 0;
+        constexpr bool SPL = (int)sizeof(tii[0]) == SPB * 2 && STGB + 6 * SPB * 2 <= (int)sizeof(s.g);
+        uint16_t* spl = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(&s.g[0][0]) + STGB);
+        // lane (r, g) puts / gets A[r][4 g .. 4 g + 3] of a split block
+        auto put_split = [&](uint16_t* b, const float* v) __attribute__((always_inline)) {
+            const uint32_t h0 = pack2bf(v[0], v[1]), h1 = pack2bf(v[2], v[3]);
+            *reinterpret_cast<uint2*>(b + r16 * SPR + 4 * g4) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(b + r16 * SPR + BS + 4 * g4) =
+                make_uint2(pack2bf_rest(v[0], v[1], h0), pack2bf_rest(v[2], v[3], h1));
+        };
+        auto get_split = [&](const uint16_t* b) __attribute__((always_inline)) {
+            Frag4 f;
+            f.h = __builtin_bit_cast(short4v, *reinterpret_cast<const uint2*>(b + r16 * SPR + 4 * g4));
+            f.l = __builtin_bit_cast(short4v, *reinterpret_cast<const uint2*>(b + r16 * SPR + BS + 4 * g4));
+            return f;
+        };
         if (!unsafe) {
             // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared: K_r of
             // block j times the tile's channel factor (F_ij, 1 between adjacent
@@ -390,10 +413,35 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
             if (oAqk) tile_out<ST, C, C, NTH>(stA, LDT, oAqk + cCC, C, C);
             if (a_Akk) tile_out<float, C, C, NTH>(&sa[0][0], LDA, a_Akk + cCC, C, C);
         }
-        if (w < NB) diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
+        if (w < NB) {
+            diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
+            if constexpr (SPL) {
+                // the block's split rows replace its fp32 rows: the wave reads back
+                // what its lanes wrote (in order within the wave), then overwrites
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                const float4 x = *reinterpret_cast<const float4*>(&tii[w][r16][4 * g4]);
+                if (a_Tii)
+                    *reinterpret_cast<float4*>(a_Tii + (size_t)ch * NB * BS * BS + w * BS * BS + r16 * BS + 4 * g4) = x;
+                const float v4[4] = {x.x, x.y, x.z, x.w};
+                put_split(reinterpret_cast<uint16_t*>(&tii[w][0][0]), v4);
+            }
+        }
+        if constexpr (SPL) {
+            // the solve's off-diagonal A operands -beta_t A_kk[t][s], split once
+            // here instead of in every wave (block pair p = (i, j), i > j)
+            constexpr int LW0 = (NW > NB) ? NB : 0, LWN = NW - LW0;
+            if (w >= LW0)
+                for (int p = w - LW0; p < 6; p += LWN) {
+                    const int i = (p < 1) ? 1 : (p < 3) ? 2 : 3, j = p - i * (i - 1) / 2;
+                    const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
+                    const float br = -s.beta[BS * i + r16];
+                    const float lv[4] = {br * x.x, br * x.y, br * x.z, br * x.w};
+                    put_split(spl + p * SPB, lv);
+                }
+        }
         __syncthreads();
         // PHASE 6
-        if (a_Tii && tid < NB * BS * BS / 4) {
+        if (!SPL && a_Tii && tid < NB * BS * BS / 4) {
             const int i = tid / (BS * BS / 4), e4 = (tid - i * (BS * BS / 4)) * 4;
             *reinterpret_cast<float4*>(a_Tii + (size_t)ch * NB * BS * BS + i * BS * BS + e4) =
                 *reinterpret_cast<const float4*>(&tii[i][e4 / BS][e4 % BS]);
@@ -459,14 +507,20 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
             const float brow = -s.beta[BS * i + r16];
 #pragma unroll
             for (int j = 0; j < i; ++j) {
-                const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
-                const float lv[4] = {brow * x.x, brow * x.y, brow * x.z, brow * x.w};
-                const Frag4 A = frag4_from_f32<3>(lv);
+                Frag4 A;
+                if constexpr (SPL) {
+                    A = get_split(spl + (i * (i - 1) / 2 + j) * SPB);
+                } else {
+                    const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
+                    const float lv[4] = {brow * x.x, brow * x.y, brow * x.z, brow * x.w};
+                    A = frag4_from_f32<3>(lv);
+                }
 #pragma unroll
                 for (int jj = 0; jj < TPW; ++jj)
                     if (tok[jj]) Y[jj] = mma4f<3>(A, XB[jj][j], Y[jj]);
             }
-            const Frag4 Tf = ldfrag4<3, float>(&tii[i][0][0], BS + 4, 0, 0);
+            const Frag4 Tf = SPL ? get_split(reinterpret_cast<const uint16_t*>(&tii[i][0][0]))
+                                 : ldfrag4<3, float>(&tii[i][0][0], BS + 4, 0, 0);
 #pragma unroll
             for (int jj = 0; jj < TPW; ++jj) {
                 X[jj][i] = tok[jj] ? mma4f<3>(Tf, accfrag4<3>(Y[jj]), zero4()) : zero4();
