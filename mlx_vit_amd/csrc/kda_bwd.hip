@@ -412,8 +412,8 @@ __global__ __launch_bounds__(256) void kda_bwd_local_kernel(const LocalArgs a) {
 //   region B   dV', v (phases 1-2)     -> dL when it does not fit in s.g (phases 3-4)
 //   W, U       the chunk's WY factors (phases 1 and 3)
 //   akk, tii   the recomputed A_kk and the inverted diagonal blocks of I + L
-//   dA         dA_qk = tril(dO V'^T, -1) (phase 1 -> phase 4); its diagonal is
-//              kept apart in dAd (see phase 4)
+//   dA         dA_qk = tril(dO V'^T, -1) (phase 1 -> phase 4); its diagonal
+//              is kept apart in pad column C (see phase 4)
 // At D = 64, bf16: 155,648 bytes, one workgroup per CU.
 // ----------------------------------------------------------------------------
 template <int D, typename ST>
@@ -835,7 +835,8 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
-                st1<ST>(&sm.dA[t][sx], (sx <= t) ? acc[e] : 0.f);
+                st1<ST>(&sm.dA[t][sx], (sx < t) ? acc[e] : 0.f);
+                if (sx == t) st1<ST>(&sm.dA[t][C], acc[e]);   // the diagonal, in the pad column
             }
         }
     }
@@ -1004,12 +1005,8 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                         Ap = frag4_from_f32<1>(pv);
                     }
                     const f32x4 Pk = mma4f<1>(Ap, B, zero4());
-                    Frag4 Aq = ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * i, BS * j);
-                    if (j == i) {   // the diagonal pairs (t, t) are added apart, below
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (4 * g4 + e == r16) Aq.h[e] = 0;
-                    }
+                    // dA is strictly lower: the diagonal pairs (t, t) are added apart, below
+                    const Frag4 Aq = ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * i, BS * j);
                     const f32x4 Pq = mma4f<1>(Aq, B, zero4());
                     const float fs = (j < i) ? fac_tile(s, i, j, d) : fdm[mm];
 #pragma unroll
@@ -1044,18 +1041,13 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                     if (pb) {
                         Ap = ldfrag4T_tr(sP, LDK, BS * j, BS * i);
                         Aa = ldfrag4T_tr(&sm.dA[0][0], LDT, BS * j, BS * i);
-                        if (i == j) {   // the diagonal pairs are added apart, below
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (4 * g4 + e == r16) Aa.h[e] = 0;
-                        }
                     } else {
                         float pv[4], av[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int t = BS * i + 4 * g4 + e;
                             pv[e] = s.beta[t] * sdL[t * LDL + BS * j + r16];
-                            av[e] = (i == j && 4 * g4 + e == r16) ? 0.f : ld1<ST>(&sm.dA[t][BS * j + r16]);
+                            av[e] = ld1<ST>(&sm.dA[t][BS * j + r16]);
                         }
                         Ap = frag4_from_f32<1>(pv);
                         Aa = frag4_from_f32<1>(av);
@@ -1111,14 +1103,14 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                 const float bi = s.beta[BS * m + r16];
                 const float4 x = *reinterpret_cast<const float4*>(sdL + (BS * m + r16) * LDL + BS * m + 4 * g4);
                 const float pr[4] = {bi * x.x, bi * x.y, bi * x.z, bi * x.w};
+                // (dA is strictly lower: the diagonal pairs are added apart, below)
                 Frag4 Ar = frag4_from_f32<1>(pr), Aqr = ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * m, BS * m);
                 float pc[4], ac[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int t = BS * m + 4 * g4 + e;
-                    if (4 * g4 + e == r16) Aqr.h[e] = 0;   // the diagonal pairs are added apart, below
                     pc[e] = s.beta[t] * sdL[t * LDL + BS * m + r16];
-                    ac[e] = (4 * g4 + e == r16) ? 0.f : ld1<ST>(&sm.dA[t][BS * m + r16]);
+                    ac[e] = ld1<ST>(&sm.dA[t][BS * m + r16]);
                 }
                 const Frag4 Ac = frag4_from_f32<1>(pc), Aqc = frag4_from_f32<1>(ac);
                 const Frag4 z4{short4v{0, 0, 0, 0}, short4v{0, 0, 0, 0}};
@@ -1238,7 +1230,7 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * (2 * rh + mm) + 4 * g4 + e;
-                const float a = ld1<ST>(&sm.dA[t][t]);
+                const float a = ld1<ST>(&sm.dA[t][C]);
                 dqa[mm][e] += a * kx[mm][e];
                 dka[mm][e] += a * qx[mm][e];
             }

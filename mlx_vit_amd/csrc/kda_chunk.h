@@ -438,7 +438,9 @@ __device__ __forceinline__ float chunk_gamma(const ChunkSmem<D, ST>& s, int t, i
 // each row sum; the four partial sums of a column meet by two quad-permute
 // DPP adds, so every step is a handful of dependent VALU operations on all 64
 // lanes.  The block's rows are read before the substitution starts (one
-// 16-byte read per row and lane, the same for the 16 lanes of a quarter).
+// 16-byte read per row and lane, the same for the 16 lanes of a quarter);
+// akk must hold zeros on and above the block's diagonal, as every writer of
+// A_kk stores them.
 // With fc != nullptr the block's transpose is also written as split (PREC 3)
 // MFMA A fragments, fc[64 w + lane] = fragment of lane (g, r) holding
 // T_ww[4g + e][r], so that other waves load it with one 16-byte read per lane.
@@ -448,14 +450,12 @@ __device__ __forceinline__ void diag_inverse_reg(const float* __restrict__ akk, 
     static_assert(BS == 16, "four quarters of four");
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l >> 2, p = l & 3;
     const float* Ab = akk + (size_t)(BS * w) * LDA + BS * w + 4 * p;
-    float4 R[BS];   // R[t] = Akk[t][4 p .. 4 p + 3] of the block, zero at s >= t
+    float4 R[BS];   // R[t] = Akk[t][4 p .. 4 p + 3] of the block (zero at s >= t in akk)
     float bt[BS];
 #pragma unroll
     for (int t = 1; t < BS; ++t) {
         bt[t] = beta[BS * w + t];
-        const float4 r = *reinterpret_cast<const float4*>(Ab + t * LDA);
-        R[t] = make_float4(4 * p < t ? r.x : 0.f, 4 * p + 1 < t ? r.y : 0.f, 4 * p + 2 < t ? r.z : 0.f,
-                           4 * p + 3 < t ? r.w : 0.f);
+        R[t] = *reinterpret_cast<const float4*>(Ab + t * LDA);
     }
     __builtin_amdgcn_sched_barrier(0);
     float xq[4] = {0.f, 0.f, 0.f, 0.f};   // x_{4p} .. x_{4p+3}
