@@ -30,7 +30,9 @@ namespace kda {
 //             kl, ql, kr in place; Qp, Kb (where requested) as 16-byte stores
 //   pass B    column threads (d, 8 tokens): KbT, QpT as 16-byte stores
 //   products  Akk -> fp32 LDS, Aqk -> LDS staging -> coalesced stores
-//   inverse   diagonal 16x16 blocks of I + L in registers
+//   inverse   diagonal 16x16 blocks of I + L in registers (eight waves: waves
+//             0-3 form and invert the diagonal tiles beside the products of
+//             waves 4-7)
 //   solve     block forward substitution, every tile of a wave interleaved;
 //             W, U (and WT) staged in LDS, stored coalesced
 // ----------------------------------------------------------------------------
@@ -315,8 +317,8 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
         // elements)
         ST* stA = G::STG_IN_G ? reinterpret_cast<ST*>(&s.g[0][0]) : &stgbuf[0][0];
         // Split A operands of the solve (bf16 hi, lo of each fp32 value; rows of
-        // 16 hi | 16 lo | pad), formed once in phase 5 and read by every wave as
-        // fragments: the diagonal-block inverses over their own fp32 rows in tii
+        // 16 hi | 16 lo | pad), formed once per chunk by the waves that form or
+        // invert the blocks and read by every wave as fragments: the diagonal-block inverses over their own fp32 rows in tii
         // (the same bytes per block), the six off-diagonal blocks -beta A_kk in
         // the g region behind the A_qk staging.  Where that does not fit, each
         // wave splits its own operands.
@@ -337,15 +339,40 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
             f.l = __builtin_bit_cast(short4v, *reinterpret_cast<const uint2*>(b + r16 * SPR + BS + 4 * g4));
             return f;
         };
+        // the diagonal block's inverse (wave w < NB, block w) and, with SPL, its
+        // split rows over its fp32 rows: the wave reads back what its lanes wrote
+        // (in order within the wave), then overwrites
+        auto invert_block = [&]() __attribute__((always_inline)) {
+            diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
+            if constexpr (SPL) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                const float4 x = *reinterpret_cast<const float4*>(&tii[w][r16][4 * g4]);
+                if (a_Tii)
+                    *reinterpret_cast<float4*>(a_Tii + (size_t)ch * NB * BS * BS + w * BS * BS + r16 * BS + 4 * g4) = x;
+                const float v4[4] = {x.x, x.y, x.z, x.w};
+                put_split(reinterpret_cast<uint16_t*>(&tii[w][0][0]), v4);
+            }
+        };
+        // the solve's off-diagonal A operand -beta_t A_kk[t][s] of block pair (i, j),
+        // i > j, split once instead of in every wave
+        auto split_pair = [&](int i, int j) __attribute__((always_inline)) {
+            const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
+            const float br = -s.beta[BS * i + r16];
+            const float lv[4] = {br * x.x, br * x.y, br * x.z, br * x.w};
+            put_split(spl + (i * (i - 1) / 2 + j) * SPB, lv);
+        };
+        // With eight waves and the split operands, waves 0-3 form the diagonal
+        // tiles and invert them at once (their own LDS writes, no barrier) while
+        // waves 4-7 form the six off-diagonal tiles and split them: the inverses
+        // run beside the products instead of after them.
+        constexpr bool EARLY = SPL && NW == 2 * NB;
+        constexpr int OFFD[6] = {1, 3, 4, 6, 7, 8};   // tile_ij indices of the blocks below the diagonal
         if (!unsafe) {
             // 10 lower sub-block tiles of Akk and Aqk; the B operand is shared: K_r of
             // block j times the tile's channel factor (F_ij, 1 between adjacent
             // blocks, e^{-T_i} on the diagonal).  Diagonal tiles of blocks in pmask
             // were formed pair by pair.
-            for (int tix = w; tix < 10; tix += NW) {
-                int i, j;
-                tile_ij(tix, i, j);
-                if (j == i && ((pmask >> i) & 1)) continue;
+            auto form_tile = [&](int i, int j) __attribute__((always_inline)) {
                 const float* fsc = &s.fac[(j == i) ? FAC_FD + i : (j == i - 1) ? 0 : fac_f_row(i, j)][0];
                 f32x4 P = zero4(), Q = zero4();
 #pragma unroll
@@ -367,6 +394,24 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
                     if (oAqk) st1<ST>(stA + t * LDT + sx, aq[e]);
                 }
                 if (oAqkT) st4(oAqkT + cCC + (size_t)(BS * j + r16) * C + BS * i + 4 * g4, aq);
+            };
+            if constexpr (EARLY) {
+                if (w < NB) {
+                    if (!((pmask >> w) & 1)) form_tile(w, w);
+                } else {
+                    for (int o = w - NB; o < 6; o += NW - NB) {
+                        int i, j;
+                        tile_ij(OFFD[o], i, j);
+                        form_tile(i, j);
+                    }
+                }
+            } else {
+                for (int tix = w; tix < 10; tix += NW) {
+                    int i, j;
+                    tile_ij(tix, i, j);
+                    if (j == i && ((pmask >> i) & 1)) continue;
+                    form_tile(i, j);
+                }
             }
             // the diagonal entries of A_qk formed in phase 2, from registers
             if (oAqk && (((pmask & ~qmask) >> w) & 1)) {
@@ -407,39 +452,37 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
                 }
             }
         }
+        if constexpr (EARLY) {
+            // the wave's own tiles (unsafe chunks: A_kk formed pair by pair above)
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (w < NB) {
+                invert_block();
+            } else {
+                for (int o = w - NB; o < 6; o += NW - NB) {
+                    int i, j;
+                    tile_ij(OFFD[o], i, j);
+                    split_pair(i, j);
+                }
+            }
+        }
         __syncthreads();
         // PHASE 5
         if (!unsafe) {
             if (oAqk) tile_out<ST, C, C, NTH>(stA, LDT, oAqk + cCC, C, C);
             if (a_Akk) tile_out<float, C, C, NTH>(&sa[0][0], LDA, a_Akk + cCC, C, C);
         }
-        if (w < NB) {
-            diag_inverse_reg<LDA>(&sa[0][0], s.beta, tii);
+        if constexpr (!EARLY) {
+            if (w < NB) invert_block();
             if constexpr (SPL) {
-                // the block's split rows replace its fp32 rows: the wave reads back
-                // what its lanes wrote (in order within the wave), then overwrites
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                const float4 x = *reinterpret_cast<const float4*>(&tii[w][r16][4 * g4]);
-                if (a_Tii)
-                    *reinterpret_cast<float4*>(a_Tii + (size_t)ch * NB * BS * BS + w * BS * BS + r16 * BS + 4 * g4) = x;
-                const float v4[4] = {x.x, x.y, x.z, x.w};
-                put_split(reinterpret_cast<uint16_t*>(&tii[w][0][0]), v4);
+                constexpr int LW0 = (NW > NB) ? NB : 0, LWN = NW - LW0;
+                if (w >= LW0)
+                    for (int p = w - LW0; p < 6; p += LWN) {
+                        const int i = (p < 1) ? 1 : (p < 3) ? 2 : 3;
+                        split_pair(i, p - i * (i - 1) / 2);
+                    }
             }
+            __syncthreads();
         }
-        if constexpr (SPL) {
-            // the solve's off-diagonal A operands -beta_t A_kk[t][s], split once
-            // here instead of in every wave (block pair p = (i, j), i > j)
-            constexpr int LW0 = (NW > NB) ? NB : 0, LWN = NW - LW0;
-            if (w >= LW0)
-                for (int p = w - LW0; p < 6; p += LWN) {
-                    const int i = (p < 1) ? 1 : (p < 3) ? 2 : 3, j = p - i * (i - 1) / 2;
-                    const float4 x = *reinterpret_cast<const float4*>(&sa[BS * i + r16][BS * j + 4 * g4]);
-                    const float br = -s.beta[BS * i + r16];
-                    const float lv[4] = {br * x.x, br * x.y, br * x.z, br * x.w};
-                    put_split(spl + p * SPB, lv);
-                }
-        }
-        __syncthreads();
         // PHASE 6
         if (!SPL && a_Tii && tid < NB * BS * BS / 4) {
             const int i = tid / (BS * BS / 4), e4 = (tid - i * (BS * BS / 4)) * 4;
