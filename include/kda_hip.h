@@ -10,7 +10,11 @@
  * dtype / g_dtype: 0 = fp32, 1 = bf16 (raw bfloat16 bits).  q, k, v, beta, o
  * and dq, dk, dv, dbeta use `dtype`; g and dg use `g_dtype`.  Arithmetic is
  * fp32 with an fp32 state; bf16 inputs use bf16 MFMA operands.
- * chunk must be 64.  D must be 32, 64 or 128 (forward) and 32 or 64 (backward).
+ * chunk is the reference's chunk_size: 8, 16, 32 or 64 (nope_gdn_mlx.py:676,
+ * 4839-4856); the result does not depend on it (the reference's own
+ * equivalence criterion, nope_gdn_mlx.py:4836-4914), and the kernels block at
+ * 64 whatever its value.  D must be 32, 64 or 128 (forward) and 32 or 64
+ * (backward).
  * stream is a hipStream_t (NULL = default stream).  Every call is stream
  * ordered and allocates nothing: the caller passes a device workspace of at
  * least kda_workspace_size() bytes (256-byte aligned).

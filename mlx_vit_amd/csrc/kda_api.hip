@@ -38,7 +38,10 @@ struct Layout {
 
 int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, bool bwd) {
     if (B < 0 || T < 0 || H < 0) return fail(KDA_E_INVALID, "negative size: B=%d T=%d H=%d", B, T, H);
-    if (chunk != kda::C) return fail(KDA_E_UNSUPPORTED, "chunk=%d: only chunk=64 is supported", chunk);
+    // the reference's chunk sizes; the kernels block at kda::C whatever the value
+    // (the chunked recurrence's result does not depend on the chunk size)
+    if (chunk != 8 && chunk != 16 && chunk != 32 && chunk != kda::C)
+        return fail(KDA_E_UNSUPPORTED, "chunk=%d: expected 8, 16, 32 or 64", chunk);
     if (bwd) {
         if (D != 32 && D != 64)
             return fail(KDA_E_UNSUPPORTED, "D=%d: the backward supports D in {32, 64}", D);

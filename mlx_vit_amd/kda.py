@@ -24,6 +24,11 @@ import torch
 from . import _lib
 
 CHUNK = 64
+# The chunk sizes the reference's layer is used with (nope_gdn_mlx.py:676, 4839-4856,
+# 5035).  The chunked recurrence's result does not depend on the chunk size (the
+# reference's own equivalence criterion, nope_gdn_mlx.py:4836-4914), so the
+# kernels block at CHUNK whatever the caller's value.
+CHUNK_SIZES = (8, 16, 32, 64)
 FWD_HEAD_DIMS = (32, 64, 128)
 BWD_HEAD_DIMS = (32, 64)
 
@@ -74,8 +79,8 @@ def _prepare(q, k, v, g, beta, initial_state):
 
 
 def _check_chunk(chunk_size: int) -> None:
-    if chunk_size != CHUNK:
-        raise ValueError(f"chunk_size={chunk_size}: the HIP kernels use chunk_size=64")
+    if chunk_size not in CHUNK_SIZES:
+        raise ValueError(f"chunk_size={chunk_size}: expected one of {CHUNK_SIZES}")
 
 
 def workspace_bytes(pass_: int, B: int, T: int, H: int, D: int, dtype: torch.dtype = torch.bfloat16) -> int:
@@ -112,7 +117,7 @@ def kda_forward(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
     ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_FWD, B, T, H, D, dev, q.dtype)
     rc = lib.kda_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
-                     B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                     B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
                      _ptr(ws), ws.numel(), _stream(dev))
     _lib.check(rc, "kda_fwd")
     return o, s_final
@@ -135,7 +140,7 @@ def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CH
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
     ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_TRAIN, B, T, H, D, dev, q.dtype)
     rc = lib.kda_fwd_train(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
-                           B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                           B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
                            _ptr(ws), ws.numel(), _stream(dev))
     _lib.check(rc, "kda_fwd_train")
     return o, s_final, ws
@@ -174,7 +179,7 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
     fn = lib.kda_bwd_train if _train else lib.kda_bwd
     rc = fn(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ds0),
-            B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+            B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
             _ptr(ws), ws.numel(), _stream(dev))
     _lib.check(rc, "kda_bwd_train" if _train else "kda_bwd")
     return dq, dk, dv, dg, dbeta, ds0
@@ -235,13 +240,14 @@ class ChunkKDAFunction(torch.autograd.Function):
     chunk-boundary states from those factors."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, initial_state):
+    def forward(ctx, q, k, v, g, beta, initial_state, chunk_size=CHUNK):
         if any(ctx.needs_input_grad):
-            o, s_final, ws = kda_forward_train(q, k, v, g, beta, initial_state)
+            o, s_final, ws = kda_forward_train(q, k, v, g, beta, initial_state, chunk_size)
         else:
-            (o, s_final), ws = kda_forward(q, k, v, g, beta, initial_state), None
+            (o, s_final), ws = kda_forward(q, k, v, g, beta, initial_state, chunk_size), None
         ctx.save_for_backward(q, k, v, g, beta, initial_state)
         ctx.ws = ws
+        ctx.chunk_size = chunk_size
         ctx.has_state = initial_state is not None
         return o, s_final
 
@@ -251,20 +257,23 @@ class ChunkKDAFunction(torch.autograd.Function):
         if do is None:
             do = torch.zeros_like(q)
         if ctx.ws is not None:
-            dq, dk, dv, dg, dbeta, ds0 = kda_backward_train(q, k, v, g, beta, s0, do, ds_final, ctx.ws)
+            dq, dk, dv, dg, dbeta, ds0 = kda_backward_train(q, k, v, g, beta, s0, do, ds_final, ctx.ws,
+                                                            ctx.chunk_size)
             ctx.ws = None
         else:
-            dq, dk, dv, dg, dbeta, ds0 = kda_backward(q, k, v, g, beta, s0, do, ds_final)
+            dq, dk, dv, dg, dbeta, ds0 = kda_backward(q, k, v, g, beta, s0, do, ds_final, ctx.chunk_size)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
-                ds0 if ctx.has_state else None)
+                ds0 if ctx.has_state else None, None)
 
 
 def chunk_kda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
               initial_state: Optional[torch.Tensor] = None, chunk_size: int = CHUNK
               ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """KDA chunkwise recurrence, differentiable.  Returns (o, final_state)."""
+    """KDA chunkwise recurrence, differentiable.  Returns (o, final_state).
+    chunk_size is the reference's blocking parameter (8, 16, 32 or 64); the
+    result does not depend on it."""
     _check_chunk(chunk_size)
-    return ChunkKDAFunction.apply(q, k, v, g, beta, initial_state)
+    return ChunkKDAFunction.apply(q, k, v, g, beta, initial_state, chunk_size)
 
 
 GDN_LOG_ALPHA_MIN = -80.0

@@ -24,7 +24,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from .kda import BWD_HEAD_DIMS, CHUNK, FWD_HEAD_DIMS, chunk_gdn, chunk_kda
+from .kda import BWD_HEAD_DIMS, CHUNK, CHUNK_SIZES, FWD_HEAD_DIMS, chunk_gdn, chunk_kda
 
 HIP_PATH = "hip_chunkwise_kda"
 GDN_HIP_PATH = "hip_chunkwise_gdn"   # scalar-alpha GDN on the same kernels
@@ -58,8 +58,8 @@ class KDARecurrence:
     def _validate(path: str, head_dim: int, chunk_size: int, requires_grad: bool) -> None:
         if path not in KDA_PATHS:
             raise ValueError(f"Unknown compute_path: {path}")
-        if chunk_size != CHUNK:
-            raise ValueError(f"compute_path='{path}' requires chunk_size={CHUNK}; got {chunk_size}")
+        if chunk_size not in CHUNK_SIZES:
+            raise ValueError(f"compute_path='{path}' requires chunk_size in {CHUNK_SIZES}; got {chunk_size}")
         dims = BWD_HEAD_DIMS if requires_grad else FWD_HEAD_DIMS
         if head_dim not in dims:
             raise ValueError(

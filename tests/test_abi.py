@@ -61,6 +61,16 @@ def test_workspace_sizes():
     assert lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) == 0 or lib.kda_workspace_size(0, 1, 0, 1, 64, 64, 1) >= 0
 
 
+def test_reference_chunk_sizes():
+    """chunk is the reference's chunk_size: 8, 16, 32 and 64 are accepted and
+    give the same workspace (the kernels block at 64); others are rejected."""
+    lib = _lib.load()
+    sizes = {c: lib.kda_workspace_size(2, 2, 300, 3, 64, c, 1) for c in (8, 16, 32, 64)}
+    assert len(set(sizes.values())) == 1 and sizes[64] > 0
+    assert lib.kda_workspace_size(2, 2, 300, 3, 64, 48, 1) == 0
+    assert "chunk" in _lib.last_error()
+
+
 @pytest.mark.parametrize("B,T,H,D", [(8, 1568, 12, 64), (1, 1, 3, 64), (2, 300, 4, 64), (1, 70, 16, 128),
                                      (4, 65, 12, 64)])
 def test_layer_workspace_sizes(B, T, H, D):
@@ -91,7 +101,7 @@ def test_workspace_offsets_disjoint():
 
 
 @pytest.mark.parametrize("B,T,H,D,chunk,dtype,gdt,code", [
-    (1, 64, 1, 64, 32, 1, 1, _lib.KDA_E_UNSUPPORTED),    # chunk
+    (1, 64, 1, 64, 48, 1, 1, _lib.KDA_E_UNSUPPORTED),    # chunk
     (1, 64, 1, 48, 64, 1, 1, _lib.KDA_E_UNSUPPORTED),    # head dim
     (1, 64, 1, 64, 64, 2, 1, _lib.KDA_E_UNSUPPORTED),    # dtype
     (1, 64, 1, 64, 64, 1, 5, _lib.KDA_E_UNSUPPORTED),    # g dtype

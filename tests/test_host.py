@@ -19,7 +19,7 @@ def test_default_path_is_hip():
 
 @pytest.mark.parametrize("kwargs,msg", [
     (dict(compute_path="metal_sg"), "Unknown compute_path"),
-    (dict(chunk_size=32), "chunk_size"),
+    (dict(chunk_size=48), "chunk_size"),
     (dict(channel_wise_decay=False, compute_path="hip_chunkwise_kda"), "channel-wise"),
     (dict(channel_wise_decay=True, compute_path="hip_chunkwise_gdn"), "scalar-alpha"),
     (dict(head_dim=128), "head_dim"),
@@ -30,6 +30,12 @@ def test_construction_errors(kwargs, msg):
     args.update(kwargs)
     with pytest.raises(ValueError, match=msg):
         kda.KDARecurrence(**args)
+
+
+@pytest.mark.parametrize("c", [8, 16, 32, 64])
+def test_reference_chunk_sizes_accepted(c):
+    # the reference's chunk sizes; the result does not depend on the blocking
+    assert kda.KDARecurrence(num_heads=2, head_dim=64, chunk_size=c).chunk_size == c
 
 
 def test_inference_allows_head_dim_128():

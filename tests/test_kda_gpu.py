@@ -428,6 +428,37 @@ def test_deterministic_repeat():
         assert torch.equal(u, w)
 
 
+@pytest.mark.parametrize("C", [8, 16, 32])
+def test_reference_chunk_sizes_match_chunkwise_oracle(C):
+    """chunk_size 8 / 16 / 32 (the reference's other blockings): forward and
+    VJP against the oracle's chunkwise restatement of the reference's algorithm
+    at that C (nope_gdn_mlx.py:2318-2456, 2579-2720), fp32 to 1e-4 with a ragged
+    last chunk and an initial state; the kernels block at 64 whatever C is, so
+    the result also equals the chunk_size=64 call bit for bit."""
+    kda = _kda()
+    B, T, H, D = 1, 100, 2, 64
+    x = _inputs(B, T, H, D, torch.float32, seed=29, with_state=True, grad=True)
+    q, k, v, g, beta = _dev(x)
+    s0, do = x["s0"].to(DEV), x["do"].to(DEV)
+    o, sf = kda.kda_forward(q, k, v, g, beta, s0, chunk_size=C)
+    grads = kda.kda_backward(q, k, v, g, beta, s0, do, None, chunk_size=C)
+    o64, sf64 = kda.kda_forward(q, k, v, g, beta, s0)
+    grads64 = kda.kda_backward(q, k, v, g, beta, s0, do, None)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o64) and torch.equal(sf, sf64)
+    for u, w in zip(grads, grads64):
+        assert torch.equal(u, w)
+    fo = [R.fold_heads(x[n].double()) for n in ("q", "k", "v", "g", "beta")]
+    s0f = x["s0"].double().reshape(B * H, D, D)
+    ro, rs = R.chunkwise_forward(*fo, s0f, C)
+    rg = R.chunkwise_backward(*fo, s0f, R.fold_heads(x["do"].double()), None, C)
+    errs = {"o": R.rel_l2(o.cpu(), R.unfold_heads(ro, B, H)), "s_final": R.rel_l2(sf.cpu(), rs.reshape(B, H, D, D))}
+    for n, gr, rr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads, rg):
+        rr = rr.reshape(B, H, D, D) if n == "ds0" else R.unfold_heads(rr, B, H)
+        errs[n] = R.rel_l2(gr.cpu(), rr)
+    _assert_all(errs, TOL[torch.float32], f"chunk_size {C}")
+
+
 # ---------------------------------------------------------------- triangular solve KAT
 
 @pytest.mark.parametrize("upper", [False, True])

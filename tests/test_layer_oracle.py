@@ -123,7 +123,8 @@ def test_layer_construction_validation():
     with pytest.raises(ValueError, match="head_dim"):
         GatedDeltaLayer(64, 2, 48)
     with pytest.raises(ValueError, match="chunk_size"):
-        GatedDeltaLayer(64, 2, 32, chunk_size=32)
+        GatedDeltaLayer(64, 2, 32, chunk_size=48)
+    assert GatedDeltaLayer(64, 2, 32, chunk_size=32).chunk_size == 32
     with pytest.raises(ValueError, match="Unknown compute_path"):
         GatedDeltaLayer(64, 2, 32, compute_path="metal")
     with pytest.raises(ValueError, match="2048"):
