@@ -535,14 +535,22 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
     // pair, A_kk[t][s] = sum_d k_t k_s e^{a_t - a_s}, one tile entry per thread
     // and step.  The other tiles are formed by MFMA below.
     const int qmask = pmask & (dfl >> 5);
+    // With two k-steps (D = 64) waves w and w + 4 share block w's sub-anchored
+    // tile, a channel half each: the second half's partial product waits in the
+    // dA tile (dead until phase 1) and wave w adds it before inverting the block.
+    constexpr bool SUBSPLIT = D / 32 == 2;
+    float (*sub2)[BS][BS] = reinterpret_cast<float (*)[BS][BS]>(&sm.dA[0][0]);
+    static_assert(!SUBSPLIT || sizeof(sm.dA) >= sizeof(float) * NB * BS * BS, "second halves fit the dA tile");
     if (pmask) {
-        if (w < NB && (((pmask & ~qmask) >> w) & 1)) {
+        const int blk = SUBSPLIT ? (w & (NB - 1)) : w, half = SUBSPLIT ? (w >> 2) : 0;
+        if ((SUBSPLIT || w < NB) && (((pmask & ~qmask) >> blk) & 1)) {
             f32x4 P, Q;
-            subanchor_tile<D, ST, PREC, false>(s, w, P, Q);
+            subanchor_tile<D, ST, PREC, false>(s, blk, P, Q, SUBSPLIT ? half : -1);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int t = BS * w + 4 * g4 + e, sx = BS * w + r16;
-                sm.akk[t][sx] = (sx < t) ? P[e] : 0.f;
+                const int t = BS * blk + 4 * g4 + e, sx = BS * blk + r16;
+                if (half == 0) sm.akk[t][sx] = (sx < t) ? P[e] : 0.f;
+                else sub2[blk][4 * g4 + e][r16] = P[e];
             }
         }
         const int nent = __popc(qmask) * BS * BS;
@@ -648,8 +656,17 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
     };
     if (!unsafe) {
         if (w < NB) {
-            // a diagonal tile of pmask was formed pair by pair before the transform
-            if (!((pmask >> w) & 1)) akk_tile(w, w);
+            // a diagonal tile of pmask was formed before the transform (sub-anchored:
+            // its second channel half is added here)
+            if (!((pmask >> w) & 1)) {
+                akk_tile(w, w);
+            } else if (SUBSPLIT && !((qmask >> w) & 1)) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = BS * w + 4 * g4 + e, sx = BS * w + r16;
+                    if (sx < t) sm.akk[t][sx] += sub2[w][4 * g4 + e][r16];
+                }
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back its own tile
             diag_inverse_reg<LDA>(&sm.akk[0][0], s.beta, sm.tii, FC ? fc : nullptr);
         } else {

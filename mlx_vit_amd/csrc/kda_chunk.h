@@ -373,15 +373,18 @@ __device__ __forceinline__ int chunk_factors2(ChunkSmem<D, ST>& s, int flag, int
 // sub-block p, <= e^{4-row span} inside it), and the four passes accumulate
 // into one tile (a pass contributes only to its own rows).  Valid when every
 // 4-row span is <= SPAN_MAX.  Lane (g, n) holds rows 4 g .. 4 g + 3, column n
-// of the tile; entries above the diagonal are not masked.
+// of the tile; entries above the diagonal are not masked.  With ksel >= 0 only
+// the 32 channels of k-step ksel contribute (a partial product, so that two
+// waves can share a tile).
 template <int D, typename ST, int PREC, bool WITH_Q>
-__device__ __forceinline__ void subanchor_tile(const ChunkSmem<D, ST>& s, int i, f32x4& P, f32x4& Q) {
+__device__ __forceinline__ void subanchor_tile(const ChunkSmem<D, ST>& s, int i, f32x4& P, f32x4& Q, int ksel = -1) {
     const int l = lane_id(), r16 = l & 15, g4 = l >> 4, q = r16 >> 2;
     const int row = BS * i + r16;
     P = zero4();
     Q = zero4();
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
+        if (ksel >= 0 && ks != ksel) continue;
         float kv[8], qv[8], av[8], ar[NB][8];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
