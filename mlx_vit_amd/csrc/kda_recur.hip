@@ -1993,23 +1993,19 @@ struct Dh3Layout {
 // nc-1-k), the pipeline of kda_recur3_kernel with the work split between
 // two wave roles (512 threads).  Waves 0-3 run the reverse state chain: dV' (row block wr),
 // the dS update of state rows wr, wr + 4, the dS^T and -dV'^T exchange tiles,
-// and read the next chunk's operands.  Waves 4-7 bring the slabs by DMA (after
-// barrier B, when the step's set is free), transpose the next chunk's dO tile
-// into dOT so that the chain waves read it as B fragments with row reads
-// instead of column gathers, and copy the step's outputs straight from the
-// exchange tiles: dh from dS^T before barrier B, dV' from -dV'^T after it.
+// and read the next chunk's operands (dO^T by transposing reads of the set's
+// dO tile).  Waves 4-7 bring the slabs by DMA (after barrier B, when the
+// step's set is free) and copy the step's outputs straight from the exchange
+// tiles: dh from dS^T before barrier B, dV' from -dV'^T after it.
 // ----------------------------------------------------------------------------
 template <int D, int CS>
 struct Dh4Layout {
     using B3 = Dh3Layout<D, CS>;
     static constexpr int DC = B3::DC, NS = B3::NS, SET_BYTES = B3::SET_BYTES;
-    static constexpr int LDR = B3::LDR, LDU = B3::LDU, LDC = B3::LDC, LDO = C + 4;
+    static constexpr int LDR = B3::LDR, LDU = B3::LDU, LDC = B3::LDC;
     static constexpr int XS_OFF = B3::XS_OFF, XV_OFF = B3::XV_OFF;
-    static constexpr int DOT_OFF = B3::STG_OFF;                                // dO^T [2][DC][LDO] bf16
-    static constexpr int DOT_BYTES = DC * LDO * 2;
-    static constexpr int XBYTES = DOT_OFF + 2 * DOT_BYTES;
+    static constexpr int XBYTES = B3::STG_OFF;                                 // the two exchange tiles
     static_assert(NS * SET_BYTES + XBYTES <= 160 * 1024, "reverse recurrence LDS");
-    static_assert(DOT_OFF % 16 == 0, "16-byte aligned tiles");
 };
 
 template <int D, int CS>
@@ -2018,7 +2014,7 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     using B3 = Dh3Layout<D, CS>;
     using Lay = Dh4Layout<D, CS>;
     constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, MT = (NT + 3) / 4, NS = Lay::NS;
-    constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC, LDO = Lay::LDO;
+    constexpr int LDR = Lay::LDR, LDC = Lay::LDC;
     constexpr int RB_D = B3::RB_D, RB_C = B3::RB_C, RB_U = B3::RB_U;
     static_assert(NS == 3, "three DMA sets");
     __shared__ __align__(1024) char set0[Lay::SET_BYTES];
@@ -2040,9 +2036,6 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     const char* gdO = static_cast<const char*>(a.dout);
     const char* gEg = reinterpret_cast<const char*>(a.eG);
 
-    auto dot = [&](int k) __attribute__((always_inline)) {
-        return reinterpret_cast<ST*>(smem + Lay::DOT_OFF + (k & 1) * Lay::DOT_BYTES);
-    };
     ST* xs = reinterpret_cast<ST*>(smem + Lay::XS_OFF);
     ST* xv = reinterpret_cast<ST*>(smem + Lay::XV_OFF);
 
@@ -2070,30 +2063,14 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
         else TO::issue(gdo, (size_t)a.H * D * 2, sbp + B3::DO_OFF, wr, l, valid);
         if (l < D / 16) dma16_s32(gEg + ch * D * 4, oE, sb + B3::EG_OFF + D * wr);
     };
-    // dO tile of a set -> dOT[n][t] (role-1 waves; rows past T read as zero)
-    // All eight reads of a lane are issued unconditionally (rows past T hold
-    // stale LDS bytes and are replaced by zero after the read), so they share
-    // one LDS round trip.
-    auto transpose_do = [&](int k, const char* sb) __attribute__((always_inline)) {
-        const char* sdO = sb + B3::DO_OFF;
-        ST* o = dot(k);
-        constexpr int GSTEP = 256 / DC, NIT = C / 8 / GSTEP;
-        static_assert(NIT >= 1 && NIT * GSTEP * 8 == C, "transpose covers the tile in whole steps");
-        const int t1 = tid - 256, nn = t1 % DC, tg = t1 / DC;      // column, group of 8 rows
-        const int valid = a.T - (nc - 1 - k) * C;
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int g8 = tg + GSTEP * it;
-            uint32_t u[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int t = 8 * g8 + e;
-                const uint32_t x = *reinterpret_cast<const uint16_t*>(sdO + Swz<RB_U>::at(t, 2 * nn));
-                u[e] = (t < valid) ? x : 0u;
-            }
-            *reinterpret_cast<uint2*>(o + nn * LDO + 8 * g8) = make_uint2(u[0] | (u[1] << 16), u[2] | (u[3] << 16));
-            *reinterpret_cast<uint2*>(o + nn * LDO + 8 * g8 + 4) = make_uint2(u[4] | (u[5] << 16), u[6] | (u[7] << 16));
-        }
+    // The rows of the partial chunk's dO tile past T (not loaded by the DMA) are
+    // cleared once, by the role-1 waves, so that its dO^T fragments read zeros
+    // there: 16 bytes per thread, whole rows, so the swizzle does not matter.
+    auto clear_do_tail = [&](char* sb) __attribute__((always_inline)) {
+        static_assert(C * RB_U == 256 * 16, "one 16-byte piece per role-1 thread");
+        const int t1 = tid - 256, row = t1 / (RB_U / 16);
+        const int valid = a.T - (nc - 1) * C;
+        if (row >= valid) *reinterpret_cast<uint4*>(sb + B3::DO_OFF + 16 * t1) = make_uint4(0u, 0u, 0u, 0u);
     };
     // Outputs of step k, by the role-1 waves from the exchange tiles, as 16-byte
     // row pieces by transposing reads (one piece per thread and tile): dh from
@@ -2144,7 +2121,7 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
     Frag8 Aat[2], Akb[D / 32], Aqt[MT][C / 32], Awt[MT][C / 32], Bo[NTW][C / 32];
     f32x4 dVa[NTW];   // the chunk's A_qk^T dO part of dV', formed with its operands
     float4 eg[MT];
-    auto preload = [&](int k, const char* sb) __attribute__((always_inline)) {   // chain waves
+    auto preload = [&](const char* sb) __attribute__((always_inline)) {   // chain waves
         const ST* sAqk = reinterpret_cast<const ST*>(sb + B3::AQK_OFF);
         const ST* sKb = reinterpret_cast<const ST*>(sb + B3::KB_OFF);
         const ST* sQp = reinterpret_cast<const ST*>(sb + B3::QP_OFF);
@@ -2155,11 +2132,11 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
             if (ks >= wr / 2) Aat[ks] = ldfragT_sw<RB_C>(sAqk, BS * wr, 32 * ks);
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) Akb[ks] = ldfrag_sw<RB_D>(sKb, BS * wr, 32 * ks);
-        const ST* o = dot(k);
+        const ST* sdO = reinterpret_cast<const ST*>(sb + B3::DO_OFF);
 #pragma unroll
         for (int j = 0; j < NTW; ++j)
 #pragma unroll
-            for (int ks = 0; ks < C / 32; ++ks) Bo[j][ks] = ldfrag<1, ST>(o, LDO, BS * j, 32 * ks);
+            for (int ks = 0; ks < C / 32; ++ks) Bo[j][ks] = ldfragT_sw<RB_U>(sdO, BS * j, 32 * ks);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
             if (own[i]) {
@@ -2180,18 +2157,17 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
         }
     };
 
-    // prologue: steps 0 .. NS-1 in flight; step 0's dO transposed, its operands read
+    // prologue: steps 0 .. NS-1 in flight; step 0's operands read
     if (role == 0) put_state();
     if (role == 1) {
         dma_step(0, set0);
         if (nc > 1) dma_step(1, set1);
         if (nc > 2) dma_step(2, set2);
         dma_wait_chunks<L>(min(NS, nc) - 1);
+        if (a.T < nc * C) clear_do_tail(set0);
     }
     lds_barrier();
-    if (role == 1) transpose_do(0, set0);
-    lds_barrier();
-    if (role == 0) preload(0, set0);
+    if (role == 0) preload(set0);
 
     // step k: chunk nc-1-k in set k % NS
     auto step = [&](int k, char* scur, const char* snext) __attribute__((always_inline)) {
@@ -2211,14 +2187,11 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
                 *reinterpret_cast<uint2*>(xv + (BS * j + r16) * LDC + BS * wr + 4 * g4) = pack4bf(negacc(dV));
             }
         } else {
-            if (k + 1 < nc) {
-                // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight)
-                dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
-                transpose_do(k + 1, snext);
-            }
+            // step k+1's slabs landed (chunks up to k+NS-1 may stay in flight)
+            if (k + 1 < nc) dma_wait_chunks<L>(min(nc - 1, k + NS - 1) - (k + 1));
             copy_dh(k);   // after the wait: a store issued before it would hold the count
         }
-        lds_barrier();                                          // B(k): -dV'^T in xv, dOT of k+1
+        lds_barrier();                                          // B(k): -dV'^T in xv, step k+1's slabs
         if (role == 0) {
             Frag8 Bvn[NTW][C / 32];    // -dV'
 #pragma unroll
@@ -2242,11 +2215,11 @@ __global__ __launch_bounds__(512) void kda_dh4_kernel(const DhArgs a) {
                 }
             if (k + 1 < nc) {
                 put_state();
-                preload(k + 1, snext);
+                preload(snext);
             }
         } else {
-            // set k % NS is free: chunk k's operands are in the chain waves'
-            // registers and its dO was transposed in step k-1
+            // set k % NS is free: chunk k's operands, dO^T included, are in the
+            // chain waves' registers
             if (k + NS < nc) dma_step(k + NS, scur);
             copy_dvp(k);
         }
