@@ -98,7 +98,16 @@ def workspace_offsets(pass_: int, B: int, T: int, H: int, D: int) -> dict:
     return {name: int(arr[i]) for i, name in enumerate(_lib.WS_REGIONS)}
 
 
-def _workspace(pass_: int, B: int, T: int, H: int, D: int, dev: torch.device, dtype) -> torch.Tensor:
+def _workspace(pass_: int, B: int, T: int, H: int, D: int, dev: torch.device, dtype,
+               given: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The caller's workspace (checked: a contiguous uint8 tensor on the
+    inputs' device; its size is checked by the library) or a new one."""
+    if given is not None:
+        if not isinstance(given, torch.Tensor) or given.dtype != torch.uint8 or not given.is_contiguous():
+            raise ValueError("workspace must be a contiguous torch.uint8 tensor")
+        if given.device != dev:
+            raise ValueError(f"workspace is on {given.device}, q on {dev}")
+        return given
     n = workspace_bytes(pass_, B, T, H, D, dtype)
     return torch.empty(max(n, 256), dtype=torch.uint8, device=dev)
 
@@ -115,7 +124,7 @@ def kda_forward(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
     dev = q.device
     o = torch.empty_like(q)
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
-    ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_FWD, B, T, H, D, dev, q.dtype)
+    ws = _workspace(_lib.KDA_PASS_FWD, B, T, H, D, dev, q.dtype, workspace)
     rc = lib.kda_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
                      B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
                      _ptr(ws), ws.numel(), _stream(dev))
@@ -138,7 +147,7 @@ def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CH
     dev = q.device
     o = torch.empty_like(q)
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
-    ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_TRAIN, B, T, H, D, dev, q.dtype)
+    ws = _workspace(_lib.KDA_PASS_TRAIN, B, T, H, D, dev, q.dtype, workspace)
     rc = lib.kda_fwd_train(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
                            B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
                            _ptr(ws), ws.numel(), _stream(dev))
@@ -163,10 +172,14 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
         raise ValueError(f"head_dim={D}: the backward supports {BWD_HEAD_DIMS}")
     if tuple(do.shape) != (B, T, H, D):
         raise ValueError(f"do shape {tuple(do.shape)} != {(B, T, H, D)}")
+    if do.device != q.device:
+        raise ValueError(f"do is on {do.device}, q on {q.device}")
     do = do.to(q.dtype).contiguous()
     if ds_final is not None:
         if tuple(ds_final.shape) != (B, H, D, D):
             raise ValueError(f"ds_final shape {tuple(ds_final.shape)} != {(B, H, D, D)}")
+        if ds_final.device != q.device:
+            raise ValueError(f"ds_final is on {ds_final.device}, q on {q.device}")
         ds_final = ds_final.to(torch.float32).contiguous()
     lib = _lib.load()
     dev = q.device
@@ -175,7 +188,7 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
     ds0 = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
     if _train and workspace is None:
         raise ValueError("kda_backward_train needs the workspace returned by kda_forward_train")
-    ws = workspace if workspace is not None else _workspace(_lib.KDA_PASS_BWD, B, T, H, D, dev, q.dtype)
+    ws = _workspace(_lib.KDA_PASS_BWD, B, T, H, D, dev, q.dtype, workspace)
     fn = lib.kda_bwd_train if _train else lib.kda_bwd
     rc = fn(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ds0),
@@ -223,7 +236,7 @@ def kda_forward_gated(q, k, v, g, beta, initial_state, gate: torch.Tensor, norm_
     y = torch.empty((B, T, H * D), dtype=q.dtype, device=dev)
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
     pass_ = _lib.KDA_PASS_TRAIN if train else _lib.KDA_PASS_FWD
-    ws = workspace if workspace is not None else _workspace(pass_, B, T, H, D, dev, q.dtype)
+    ws = _workspace(pass_, B, T, H, D, dev, q.dtype, workspace)
     rc = lib.kda_fwd_gated(pass_, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(gate), ld_z,
                            _ptr(w), float(eps), _ptr(o), _ptr(y), H * D, _ptr(s_final),
                            B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],

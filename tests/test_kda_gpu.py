@@ -406,6 +406,27 @@ def test_recurrence_dispatch_matches_op():
         rec(q, k, v, g, beta, compute_path="metal")
 
 
+def test_host_arguments_on_other_devices_are_rejected():
+    """Tensors the library reads through device pointers must be on q's
+    device: a host do, ds_final or workspace is refused before any launch, as
+    is a workspace that is not a contiguous byte tensor."""
+    kda = _kda()
+    x = _inputs(1, 64, 2, 64, torch.bfloat16, seed=23)
+    q, k, v, g, beta = _dev(x)
+    do = torch.randn(1, 64, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="do is on"):
+        kda.kda_backward(q, k, v, g, beta, None, do)
+    with pytest.raises(ValueError, match="ds_final is on"):
+        kda.kda_backward(q, k, v, g, beta, None, do.to(DEV), torch.zeros(1, 2, 64, 64))
+    n = kda.workspace_bytes(0, 1, 64, 2, 64)
+    with pytest.raises(ValueError, match="workspace is on"):
+        kda.kda_forward(q, k, v, g, beta, workspace=torch.empty(n, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="uint8"):
+        kda.kda_forward(q, k, v, g, beta, workspace=torch.empty(n // 4 + 1, dtype=torch.float32, device=DEV))
+    o, _ = kda.kda_forward(q, k, v, g, beta, workspace=torch.empty(n, dtype=torch.uint8, device=DEV))
+    assert torch.equal(o, kda.kda_forward(q, k, v, g, beta)[0])
+
+
 def test_empty_sequence():
     kda = _kda()
     q = torch.zeros(1, 0, 2, 64, device=DEV)
