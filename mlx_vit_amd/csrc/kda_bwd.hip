@@ -447,7 +447,7 @@ struct alignas(16) LocalSmem {
 
 // The chunk's indices and its phase-0 tiles, handed from the kernel to its tail.
 struct Local3Chunk {
-    static constexpr int NPF = 2;   // prefetch lines per thread
+    static constexpr int NPF = 1;   // prefetch lines per thread
     int tid, w, l, r16, g4, ct, rh, valid;
     size_t rs, base, bbase;
     const char* pf[NPF];            // the thread's prefetch line addresses, or null
@@ -1402,37 +1402,30 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     // the span guard (every chunk at ordinary decays) run a copy with the
     // sub-anchored and pairwise code compiled out, so that code shapes neither
     // that copy's register allocation nor its schedule.
-    Local3Chunk c{tid, w, l, r16, g4, ct, rh, valid, rs, base, bbase, {nullptr, nullptr}};
+    Local3Chunk c{tid, w, l, r16, g4, ct, rh, valid, rs, base, bbase, {nullptr}};
     // L2 prefetch of the chunk this XCD starts next (chunks a CU count apart go to
     // one XCD and start about when this one ends): one 4-byte DMA per 128-byte
-    // line of its inputs -- the rows of q, k, v, g, dO and the W, U, dV', h, dh
-    // slabs -- so that its loads hit in L2.  The addresses are formed here, from
-    // the argument block; the tail issues the DMA once the chunk's own loads are
-    // in.
+    // line of the rows of q, k and g, the inputs a chunk waits for before its
+    // cumsum, so that those loads hit in L2 (without it the kernel takes 4% longer).
+    // The other inputs' latency hides behind the cumsum and factor phases:
+    // prefetching them as well (80 KB per chunk in all) gave no gain and more
+    // lines evicted before use.  The addresses are formed here, from the argument
+    // block; the tail issues the DMA once the chunk's own loads are in.
     if (a.pf_ahead > 0 && ch + a.pf_ahead < (int)gridDim.x) {
         const int pc = ch + a.pf_ahead, pbh = pc / a.nc, pn = pc - pbh * a.nc;
         const int pb = pbh / a.H, ph = pbh - pb * a.H, pt0 = pn * C, pvalid = min(C, a.T - pt0);
         const size_t pbase = ((size_t)pb * a.T + pt0) * rs + (size_t)ph * D;
-        constexpr int LCD = C * D * (int)sizeof(ST) / 128, LDD = D * D * (int)sizeof(ST) / 128;
-        constexpr int NL = 5 * C + 3 * LCD + 2 * LDD;
+        constexpr int NL = 3 * C;
         static_assert((NL + NTH - 1) / NTH <= Local3Chunk::NPF, "prefetch lines per thread");
 #pragma unroll
         for (int i = 0; i < (NL + NTH - 1) / NTH; ++i) {
             const int k = NTH * i + tid;
             const char* p = nullptr;
-            if (k < 5 * C) {
+            if (k < NL) {
                 const int ts = k / C, r = k - ts * C;
-                const char* tp = static_cast<const char*>(ts == 0 ? a.q : ts == 1 ? a.k : ts == 2 ? a.v : ts == 3 ? a.dout : a.g);
-                const size_t es = (ts == 4) ? sizeof(TG) : sizeof(ST);
+                const char* tp = static_cast<const char*>(ts == 0 ? a.q : ts == 1 ? a.k : a.g);
+                const size_t es = (ts == 2) ? sizeof(TG) : sizeof(ST);
                 if (r < pvalid) p = tp + (pbase + (size_t)r * rs) * es;
-            } else if (k < 5 * C + 3 * LCD) {
-                const int j = k - 5 * C, ts = j / LCD, r = j - ts * LCD;
-                const char* tp = static_cast<const char*>(ts == 0 ? a.W : ts == 1 ? a.U : a.dVp);
-                p = tp + (size_t)pc * C * D * sizeof(ST) + (size_t)r * 128;
-            } else if (k < NL) {
-                const int j = k - 5 * C - 3 * LCD, ts = j / LDD, r = j - ts * LDD;
-                const char* tp = static_cast<const char*>(ts == 0 ? a.h : a.dh);
-                p = tp + (size_t)pc * D * D * sizeof(ST) + (size_t)r * 128;
             }
             c.pf[i] = p;
         }
