@@ -256,13 +256,71 @@ def pmc_summary(fetch_dir, write_dir, calib_mb):
     return out
 
 
-def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, seed=0):
+def layer_decay_g(B, T, H, D, seed):
+    """g of the reference layer at initialisation, drawn on the CPU:
+    -A_h softplus(N(0, 0.5^2)) with A_h ~ U[1, 16] per head (the distribution
+    make_inputs_gpu draws for the layer-decay workloads)."""
+    import torch
+    gen = torch.Generator(device="cpu").manual_seed(seed + 1000)
+    A = torch.empty(H).uniform_(1.0, 16.0, generator=gen)
+    return -A[None, None, :, None] * torch.nn.functional.softplus(0.5 * torch.randn((B, T, H, D), generator=gen))
+
+
+def pmc_mfma_summary(util_dir, raw_dir=None):
+    """Per-kernel MFMA use from rocprofv3 PMC runs, averaged over dispatches:
+    ``mfma_busy`` = rocprofv3's derived MfmaUtil / 100 (SQ_VALU_MFMA_BUSY_CYCLES
+    summed over the SIMDs / (GRBM_GUI_ACTIVE x SIMD count)), and the MFMA
+    FLOPs the hardware issued per dispatch (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512,
+    rocprofv3's MfmaFlopsBF16) -- the split-bf16 products of the fp32-accurate
+    solves included.  With ``raw_dir`` (a second run of SQ_VALU_MFMA_BUSY_CYCLES
+    and GRBM_GUI_ACTIVE) the raw counters are reported beside them."""
+    out = {"source": "rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_BF16"}
+    per = {}
+    counters = [("MfmaUtil", util_dir, "util_pct"), ("SQ_INSTS_VALU_MFMA_MOPS_BF16", util_dir, "mops_bf16")]
+    if raw_dir:
+        counters += [("SQ_VALU_MFMA_BUSY_CYCLES", raw_dir, "mfma_busy_cycles"), ("GRBM_GUI_ACTIVE", raw_dir, "gui_active")]
+    for counter, root, key in counters:
+        seen = {}
+        for _, name, v in _pmc_rows(root, counter):
+            for frag, roles in PROFILE_ROLES.items():
+                if frag in name:
+                    i = seen.get(frag, 0)
+                    seen[frag] = i + 1
+                    per.setdefault(roles[i % len(roles)], {}).setdefault(key, []).append(v)
+    for name, rec in per.items():
+        r = {k: round(sum(v) / len(v), 3) for k, v in rec.items()}
+        r["dispatches"] = len(rec.get("util_pct", []))
+        if "util_pct" in r:
+            r["mfma_busy"] = round(r["util_pct"] / 100.0, 5)
+        if "mops_bf16" in r:
+            r["mfma_flops_bf16"] = round(r.pop("mops_bf16") * 512)
+        out[name] = r
+    return out
+
+
+def load_mfma(kernel_name):
+    """Counter-derived MFMA use of a kernel from the committed summary
+    (profiles/mfma.json): (busy fraction, MFMA FLOPs per dispatch) or Nones."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "mfma.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel_name)
+        if rec is None:
+            return None, None
+        return rec.get("mfma_busy"), rec.get("mfma_flops_bf16")
+    except (OSError, ValueError, KeyError):
+        return None, None
+
+
+def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, seed=0, layer_decay=False):
     """Time the torch fp32 restatement of the reference 'compiled' path on the
     host cores (bounded sample: the same B, H, D over `sample_tokens` steps),
     and measure rel-L2 of the HIP results against the fp64 C oracle on the
     same seeded inputs at the full workload size (drawn on the CPU so the
     oracle can regenerate them), through the same entry points as the timed
-    step (kda_fwd_train + kda_bwd_train for a fwd+bwd workload)."""
+    step (kda_fwd_train + kda_bwd_train for a fwd+bwd workload).  With
+    ``layer_decay`` the parity inputs carry the layer-init decay the timed
+    workload uses (layer_decay_g), not make_inputs' default."""
     import torch
     from oracle import cref
     from oracle import kda_reference as R
@@ -289,6 +347,8 @@ def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, s
     cpu_tps = B * Ts / t_med
     # --- parity at the full workload size
     x = R.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=seed, with_state=with_state, with_grad=backward)
+    if layer_decay:
+        x["g"] = layer_decay_g(B, T, H, D, seed).to(torch.bfloat16)
     dev = lambda t: None if t is None else t.to("cuda")
     q, k, v, g, beta, s0 = (dev(x[nm]) for nm in ("q", "k", "v", "g", "beta", "s0"))
     # through the entry points the timed step calls: the training pair for a
@@ -345,7 +405,7 @@ def layer_bench(args):
     layer.A_log.data = layer.A_log.data.float()
     layer.dt_bias.data = layer.dt_bias.data.float()
     layer = layer.cuda()
-    layer.fused_output_norm = not args.unfused_norm
+    layer.fused_output_norm = args.fused_norm
     gen = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(B, T, hidden, device="cuda", generator=gen).to(torch.bfloat16).requires_grad_()
     cot = torch.randn(B, T, hidden, device="cuda", generator=gen).to(torch.bfloat16)
@@ -397,7 +457,7 @@ def layer_bench(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) x, random-init layer of the reference's architecture)",
         "config": {"workload": "GatedDeltaLayer fwd+bwd, x (8, 1568, 768), H12 D64, bf16 (A_log, dt_bias fp32)",
-                   "B": B, "T": T, "hidden": hidden, "H": H, "D": D, "fused_output_norm": not args.unfused_norm},
+                   "B": B, "T": T, "hidden": hidden, "H": H, "D": D, "fused_output_norm": args.fused_norm},
         "profiled_ms_per_step": round(prof_ms, 4),
         "kda_ms_per_step": round(kda_ms, 4), "elementwise_ms_per_step": round(ew_ms, 4),
         "kda_share": round(kda_ms / prof_ms, 4), "elementwise_share": round(ew_ms / prof_ms, 4),
@@ -427,7 +487,7 @@ def model_bench(args):
     model = M.to_bf16(M.config4()).cuda()
     for mod in model.modules():
         if isinstance(mod, kda.GatedDeltaLayer):
-            mod.fused_output_norm = not args.unfused_norm
+            mod.fused_output_norm = args.fused_norm
     step = TR.TrainStep(model)
     gen = torch.Generator(device="cuda").manual_seed(0)
     video = torch.randn(B, 16, 224, 224, 3, device="cuda", generator=gen).to(torch.bfloat16)
@@ -487,16 +547,22 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["layer", "model"], default="cfg2")
     ap.add_argument("--cpu-sample-tokens", type=int, default=392)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--unfused-norm", action="store_true",
-                    help="layer / model workloads: run the output norm as its own kernel instead of fused into "
-                         "the recurrence's store")
+    ap.add_argument("--fused-norm", action="store_true",
+                    help="layer / model workloads: fuse the output norm into the forward recurrence's store "
+                         "(kda_fwd_gated) instead of the layer's default standalone norm kernel")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one plain fp32 streaming kernel of this many MiB first (PMC byte-counter scale)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE output directories and exit")
+    ap.add_argument("--pmc-mfma", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_BF16 output (and optionally a "
+                         "second directory of SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE) and exit")
     args = ap.parse_args()
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calibration_mb or 512), indent=1))
+        return
+    if args.pmc_mfma:
+        print(json.dumps(pmc_mfma_summary(*args.pmc_mfma[:2]), indent=1))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the op on a "
@@ -562,6 +628,7 @@ def main():
         avg_s = tot.value / cnt.value * 1e-3
         name = lib.kda_profile_name(kid).decode()
         traffic = load_traffic(name)
+        mfma_busy, mfma_hw_flops = load_mfma(name)
         kernels.append({
             "name": name, "launches": cnt.value, "avg_us": round(avg_s * 1e6, 2),
             "tflops": round(fl[kid] / avg_s / 1e12, 2), "mfma_frac": round(fl[kid] / avg_s / PEAK_BF16, 4),
@@ -570,6 +637,11 @@ def main():
             "ws_bytes": wsb[kid], "ws_gbs": round(wsb[kid] / avg_s / 1e9, 1),
             "pmc_bytes": traffic, "pmc_over_alg": (round(traffic / alg[kid], 3) if traffic and alg[kid] else None),
             "alg_flops": fl[kid], "_avg_s": avg_s,
+            # from the committed rocprofv3 counter summary (profiles/mfma.json): the
+            # MFMA pipe's busy share, and the MFMA FLOPs the hardware issued per
+            # dispatch over this run's duration, as a fraction of bf16 dense peak
+            "mfma_busy": mfma_busy,
+            "mfma_hw_frac": (round(mfma_hw_flops / avg_s / PEAK_BF16, 4) if mfma_hw_flops else None),
         })
     # the dominant kernel (most time per step) and its roofline on the op's own bytes
     dom = max(kernels, key=lambda r: r["avg_us"] * r["launches"])
@@ -587,6 +659,7 @@ def main():
     rl["alg_bytes"] = dom["alg_bytes"]
     rl["ws_bytes"] = dom["ws_bytes"]
     rl["traffic_over_alg"] = dom["pmc_over_alg"]
+    rl["mfma_busy"] = dom["mfma_busy"]
     for r in kernels:
         r.pop("_avg_s")
 
@@ -606,7 +679,8 @@ def main():
         "profiled_ms_per_step": round(prof_ms_per_step, 4),
     }
     if not args.no_cpu_baseline:
-        cb, errs = cpu_baseline_leg(B, T, H, D, backward, with_state, None, args.cpu_sample_tokens)
+        cb, errs = cpu_baseline_leg(B, T, H, D, backward, with_state, None, args.cpu_sample_tokens,
+                                    layer_decay=args.workload in LAYER_DECAY)
         out["cpu_baseline"] = cb
         out["rel_l2"] = errs
     else:

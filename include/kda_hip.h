@@ -101,7 +101,10 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
  * bf16, needs 98.9 MB).  Results are bit-identical to kda_fwd.  Every call on
  * one GPU shares that GPU's array, so calls that overlap on one GPU (on
  * different streams, or from several threads without ordering) race;
- * stream-ordered calls on one stream do not. */
+ * stream-ordered calls on one stream do not.
+ * The array used is that of the stream's device (the current device for the
+ * NULL stream); q, k, v, g, beta, o and the states must be device memory of
+ * that device, or the call returns KDA_E_INVALID before any device work. */
 #define KDA_NOALLOC_MAX_WORKSPACE ((size_t)128 << 20)
 int kda_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta,
                     const float* s0, void* o, float* s_final,

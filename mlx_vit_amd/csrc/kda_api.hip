@@ -294,8 +294,6 @@ hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* 
     return timed(id, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, nchunks, st); }, prof);
 }
 
-// prof = false: no launch timing (the profiler's event pool never grows), for
-// the entry point that must not allocate
 // The layer's gated RMSNorm fused into the forward's O store (kda_fwd_gated).
 struct Epilogue {
     const void* z;
@@ -306,6 +304,9 @@ struct Epilogue {
     int64_t ld_y;
 };
 
+// The forward's launch sequence (pass 0) or the training forward's (pass 2).
+// prof = false: no launch timing, so the profiler's event pool never grows (for
+// the entry point that must not allocate).
 int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
             size_t ws_bytes, void* stream, bool prof = true, const Epilogue* epi = nullptr) {
@@ -349,31 +350,6 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 0, st); }, prof);
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
     return ok();
-}
-
-// ---- the forward without a caller workspace ----
-// Its workspace is this file-scope device array: one copy per GPU the library
-// runs on, held until the process ends.  Host code never uses the name
-// `scratch` as an address (on the host it is a stand-in, not device memory):
-// the device address comes from hipGetSymbolAddress, once per device, with
-// that device current.
-static __device__ __align__(256) unsigned char scratch[KDA_NOALLOC_MAX_WORKSPACE];
-
-constexpr int kMaxDevices = 64;
-
-// Device address of `scratch` on device `dev` (the current device), looked up
-// once per device; nullptr with the HIP error in *err if the lookup failed.
-void* scratch_ptr(int dev, hipError_t* err) {
-    static std::once_flag once[kMaxDevices];
-    static void* ptr[kMaxDevices];
-    static hipError_t status[kMaxDevices];
-    std::call_once(once[dev], [dev] {
-        void* p = nullptr;
-        status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        ptr[dev] = (status[dev] == hipSuccess) ? p : nullptr;
-    });
-    *err = status[dev];
-    return ptr[dev];
 }
 
 // pass 1: prep from the inputs, then the backward; pass 2: the workspace holds
@@ -456,6 +432,40 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
 }  // namespace
 
 // ----------------------------------------------------------------------------
+// internal entry points for the other C-ABI translation units
+// ----------------------------------------------------------------------------
+namespace kda {
+
+int api_fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int api_hip_fail(hipError_t e, const char* where) { return hip_fail(e, where); }
+
+size_t api_fwd_workspace_bytes(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, int* rc) {
+    *rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, false);
+    if (*rc != KDA_OK) return 0;
+    Layout L;
+    make_layout(KDA_PASS_FWD, B, T, H, D, dtype, L);
+    return L.total;
+}
+
+int api_fwd_on_workspace(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const float* s0, void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype,
+                         int g_dtype, void* workspace, size_t ws_bytes, void* stream) {
+    return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
+                   ws_bytes, stream, /*prof=*/false);
+}
+
+}  // namespace kda
+
+// ----------------------------------------------------------------------------
 // C ABI
 // ----------------------------------------------------------------------------
 extern "C" {
@@ -492,28 +502,6 @@ int kda_fwd(const void* q, const void* k, const void* v, const void* g, const vo
             size_t ws_bytes, void* stream) {
     return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
                    ws_bytes, stream);
-}
-
-int kda_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
-                    void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
-                    void* stream) {
-    int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, false);
-    if (rc) return rc;
-    Layout L;
-    make_layout(KDA_PASS_FWD, B, T, H, D, dtype, L);
-    if (L.total > KDA_NOALLOC_MAX_WORKSPACE)
-        return fail(KDA_E_WORKSPACE,
-                    "kda_fwd_noalloc: B=%d T=%d H=%d D=%d needs %zu bytes of workspace, above the %zu bytes of its "
-                    "static scratch; call kda_fwd with a caller workspace",
-                    B, T, H, D, L.total, (size_t)KDA_NOALLOC_MAX_WORKSPACE);
-    int dev = -1;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_fail(e, "kda_fwd_noalloc: hipGetDevice");
-    if (dev < 0 || dev >= kMaxDevices) return fail(KDA_E_UNSUPPORTED, "kda_fwd_noalloc: device %d >= %d", dev, kMaxDevices);
-    void* ws = scratch_ptr(dev, &e);
-    if (!ws) return hip_fail(e, "kda_fwd_noalloc: hipGetSymbolAddress(scratch)");
-    return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, ws,
-                   KDA_NOALLOC_MAX_WORKSPACE, stream, /*prof=*/false);
 }
 
 int kda_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,

@@ -85,6 +85,18 @@ hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm
                         hipStream_t st);
 hipError_t launch_state_copy(const float* src, float* dst, size_t n, hipStream_t st);
 
+// C-ABI helpers of kda_api.hip for the other C-ABI translation units (the
+// allocation-free forward): the error setters behind kda_last_error(); the
+// forward workspace size of a shape (0, with *rc the error code, for a shape
+// the forward rejects); the forward's launch sequence on a given workspace,
+// without launch timing.
+int api_fail(int code, const char* fmt, ...);
+int api_hip_fail(hipError_t e, const char* where);
+size_t api_fwd_workspace_bytes(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, int* rc);
+int api_fwd_on_workspace(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const float* s0, void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype,
+                         int g_dtype, void* workspace, size_t ws_bytes, void* stream);
+
 // GatedDeltaLayer producer (projection outputs -> q, k, v, g, beta) and its
 // adjoint.  Row strides are in elements; q, k, v, g, dq, dk, dv, dg are
 // contiguous [B, T, H*D], beta and dbeta contiguous [B, T, H].

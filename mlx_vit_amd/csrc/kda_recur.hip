@@ -1,25 +1,32 @@
-// kda_recur.hip -- the two sequential (inter-chunk) recurrences of the KDA op.
+// kda_recur.hip -- the sequential (inter-chunk) recurrences of the KDA op.
 //
-// One 256-thread workgroup per (batch, head) walks the chunks in order; wave w
-// owns dv tiles w, w+4, ... of the state, which stays in accumulator VGPRs as
-// fp32 for the whole sequence.  The chunk's shared operands (workspace slabs
-// written by the prep kernel) are staged in LDS with 16-byte coalesced loads;
-// the next chunk's slabs are loaded into registers while the current chunk is
-// computed and land in the other half of a double buffer (single buffer plus a
-// second barrier when two do not fit in 160 KB).  Per-chunk outputs go through
-// an LDS staging tile and leave as coalesced 16-byte stores.
+// Each walks the chunks of one (batch, head) in order, with the state in fp32
+// MFMA accumulators for the whole sequence and the chunk's workspace slabs
+// (written by the prep kernel) staged in LDS.  The state orientation inside the
+// kernels is Sigma = S^T, [dk][dv].
 //
-//   kda_recur_kernel  (state orientation S[dk][dv])
-//       V' = U - W S;  O = Qp S + Aqk V';  S <- diag(e^G) S + Kb^T V'
+//   forward (MODE 0) and chunk-start state recompute (MODE 1)
+//       V' = U - W Sigma;  O = Qp Sigma + Aqk V';  Sigma <- diag(e^G) Sigma + Kb^T V'
 //     MODE 0 writes O and the final state -- the chunk loop of
 //     nope_gdn_mlx.py:2408-2451 (fused solve/finalize 1519-1942) with the
-//     triangular solve hoisted into the prep kernel.
-//     MODE 1 writes the chunk-start states h for the backward instead (the
-//     fp32 kernel also writes V', which only the fp32 local-adjoint kernel reads).
-//   kda_dh_kernel  (reverse order)
-//       dV' = Aqk^T dO + Kb dS;  dS <- diag(e^G) dS + Qp^T dO - W^T dV'
-//     writing dS at each chunk end and dV'; the final dS is dS0 -- the state
-//     carry of nope_gdn_mlx.py:2705-2706 in W/U form.
+//     triangular solve hoisted into the prep kernel; MODE 1 writes the
+//     chunk-start states h for the backward.
+//   reverse state carry
+//       dV' = Aqk^T dO + Kb dSigma;  dSigma <- diag(e^G) dSigma + Qp^T dO - W^T dV'
+//     writing dSigma at each chunk end and dV'; the last dSigma is dS0 -- the
+//     state carry of nope_gdn_mlx.py:2705-2706 in W/U form.
+//
+// Kernels by shape:
+//   kda_recur4_kernel / kda_dh4_kernel  bf16, D = 64: two 8-wave workgroups per
+//       (batch, head), each owning half of the dv columns; wave roles (state
+//       chain | work beside it), slabs by LDS DMA three chunks ahead
+//   kda_recur5_kernel  bf16, D = 64, forward with the layer's gated RMSNorm
+//       fused into the O store: one 16-wave workgroup per (batch, head)
+//   kda_recur3_kernel  bf16, D = 128 forward: four 4-wave workgroups per
+//       (batch, head), 32 dv columns each
+//   kda_recur2_kernel / kda_dh2_kernel  bf16, D = 32
+//   kda_recur_kernel / kda_dh_kernel    fp32 inputs (the first, generic design:
+//       one 256-thread workgroup per (batch, head), register-staged double buffer)
 #include "kda_internal.h"
 
 namespace kda {

@@ -376,9 +376,10 @@ class GatedDeltaLayer(nn.Module):
         self.g_proj_2 = nn.Linear(head_dim, total, bias=True)
         self.o_norm = RMSNormGated(head_dim, eps=1e-5)
         self.o_proj = nn.Linear(total, hidden_size, bias=False)
-        # the output norm fused into the recurrence's store where a kernel has it
-        # (kda_fwd_gated); False runs the standalone norm kernels
-        self.fused_output_norm = True
+        # True fuses the output norm into the recurrence's store where a kernel
+        # has it (kda_fwd_gated).  Off by default: the fused forward measured
+        # slower than the plain forward plus the standalone norm kernel
+        self.fused_output_norm = False
 
     def produce(self, x: torch.Tensor):
         """(q, k, v, g, beta) for x (B, L, hidden): the layer's inputs to the

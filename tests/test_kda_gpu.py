@@ -306,9 +306,30 @@ def test_bwd_bf16_operands_fp32_gate():
 
 
 def test_bwd_parity_config2_full():
-    """Config 2: fwd + VJP at B=8, H=12, T=1568, D=64 bf16, dO ~ N(0,1) bf16."""
+    """Config 2: fwd + VJP at B=8, H=12, T=1568, D=64 bf16, dO ~ N(0,1) bf16,
+    through both the standalone kda_bwd and the training pair that a training
+    step (and the benchmark) runs: kda_fwd_train, then kda_bwd_train on its
+    workspace.  Both against the fp64 oracle; the pair bit-identical to the
+    standalone calls at this full size too."""
+    kda = _kda()
     x = _inputs(8, 1568, 12, 64, torch.bfloat16, seed=0, grad=True)
-    _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "config2 bwd")
+    q, k, v, g, beta = _dev(x)
+    do = x["do"].to(DEV)
+    o1, sf1 = kda.kda_forward(q, k, v, g, beta, None)
+    g1 = kda.kda_backward(q, k, v, g, beta, None, do, None)
+    o2, sf2, ws = kda.kda_forward_train(q, k, v, g, beta, None)
+    g2 = kda.kda_backward_train(q, k, v, g, beta, None, do, None, ws)
+    torch.cuda.synchronize()
+    ref = cref.forward(x["q"], x["k"], x["v"], x["g"], x["beta"], None)
+    refb = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], None, x["do"])
+    names = ("dq", "dk", "dv", "dg", "dbeta", "ds0")
+    for label, o, sf, grads in (("config2 standalone", o1, sf1, g1), ("config2 training pair", o2, sf2, g2)):
+        errs = {"o": R.rel_l2(o.cpu(), ref["o"]), "s_final": R.rel_l2(sf.cpu(), ref["s_final"])}
+        errs.update({n: R.rel_l2(gr.cpu(), refb[n]) for n, gr in zip(names, grads)})
+        _assert_all(errs, TOL[torch.bfloat16], label)
+    assert torch.equal(o1, o2) and torch.equal(sf1, sf2)
+    for n, a, b in zip(names, g1, g2):
+        assert torch.equal(a, b), n
 
 
 # ---------------------------------------------------------------- training pair

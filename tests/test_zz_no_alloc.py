@@ -3,7 +3,8 @@ through the C ABI, against kda_fwd with a caller workspace on the same inputs.
 Two calls in a row (the second smaller, so it runs over what the first left
 in the array), fp32 and bf16, with and without an initial state: o and the
 final state must be bit-identical to kda_fwd's.  A shape whose workspace
-exceeds the scratch is rejected before any device work."""
+exceeds the scratch, and a buffer that is not device memory of the stream's
+GPU, are rejected before any device work."""
 import ctypes
 
 import pytest
@@ -81,3 +82,27 @@ def test_noalloc_rejects_oversize():
     rc = lib.kda_fwd_noalloc(p, p, p, p, p, None, p, None, B, T, H, D, 64, 1, 1, None)
     assert rc == _lib.KDA_E_WORKSPACE
     assert "static scratch" in _lib.last_error()
+
+
+def test_noalloc_rejects_host_pointer():
+    """A host buffer as q is refused with KDA_E_INVALID before any launch: the
+    kernels would run on the scratch of the stream's GPU, so every buffer must
+    live there.  o stays untouched (NaN)."""
+    import numpy as np
+    lib = _lib.load()
+    B, T, H, D = 1, 70, 2, 64
+    x = _inputs(B, T, H, D, torch.bfloat16, 4, False)
+    host_q = np.zeros(B * T * H * D, dtype=np.uint16)
+    q_host = ctypes.c_void_p(host_q.ctypes.data)
+    o = torch.full_like(x[0], float("nan"))
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.kda_fwd_noalloc(q_host, _p(x[1]), _p(x[2]), _p(x[3]), _p(x[4]), None, _p(o), None,
+                             B, T, H, D, 64, 1, 1, st)
+    assert rc == _lib.KDA_E_INVALID
+    assert "not device memory" in _lib.last_error()
+    torch.cuda.synchronize()
+    assert torch.isnan(o.float()).all()
+    # the refused call leaves no error behind: the next valid call succeeds
+    o2, sf2 = _call("kda_fwd_noalloc", x)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o2.float()).all()
