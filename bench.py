@@ -69,6 +69,14 @@ def op_counts(B, T, H, D, backward):
     return flops, fwd_bytes + bwd_bytes
 
 
+def seg_plan(BH, nc):
+    """Segments of the bf16 D = 128 forward (kda_seg.hip seg_plan): about 256
+    workgroups, at least 4 chunks per segment; (nseg, chunks per segment)."""
+    ns = max(1, min(256 // max(BH, 1), nc // 4))
+    length = -(-nc // ns)
+    return -(-nc // length), length
+
+
 def kernel_counts(B, T, H, D, es=2):
     """Per-launch figures of each library kernel (ids as in kda_profile_name):
     (flops, alg_bytes, ws_bytes).
@@ -113,15 +121,27 @@ def kernel_counts(B, T, H, D, es=2):
         5: n * (6 * D * D + 18 * C * D) + (1 - x) * n * (2 * D * D + C * D),
         6: n * (8 * C * D + (2.0 / 3.0) * C * C),
     }
+    # the segmented forward (bf16 D = 128): maps of segments 0 .. nseg-2 (the
+    # chunk loop on 2D columns, no O), nseg-1 start-state steps, the forward
+    nseg, seg_len = seg_plan(B * H, nc) if (es == 2 and D == 128) else (1, nc)
+    nmap = B * H * max(0, min(nc, (nseg - 1) * seg_len))      # chunks covered by pass A
+    fl[11] = nmap * C * 8 * D * D                       # W Sigma, Kb^T V' on D + D columns
+    fl[12] = B * H * (nseg - 1) * 2 * D * D * D         # M Sigma per segment boundary
+    fl[13] = fl[1]
     io_in = nt * (4 * D + 1) * es                       # q, k, v, g, beta
     alg = {
+        11: 0, 12: 0, 13: nt * D * es + state,          # o, S_final (and S_0)
         0: io_in, 2: io_in, 6: io_in,                   # the forward's inputs
         1: nt * D * es + state,                         # o, S_final (S_0 with an initial state)
         3: 0,
         4: 2 * state,                                   # dS_T in, dS_0 out (bounded above by these)
         5: nt * (5 * D + 1) * es + nt * (4 * D + 1) * es,   # q k v g beta dO in; dq dk dv dg dbeta out
     }
+    segmap = B * H * nseg * DD * f4                     # one [D][D] fp32 per (b, h, segment)
     ws = {
+        11: nmap * (3 * CD * es + D * f4) + 2 * segmap,                                      # W U KbT eG -> X, M
+        12: 3 * segmap,                                                                      # M X -> Sigma_in
+        13: N * (4 * CD * es + CC * es + D * f4) + segmap + nt * D * es + state,            # slabs, Sigma_in -> o
         0: io_in + N * (4 * CD * es + CC * es + D * f4),                                   # -> W U Qp Kb(T) Aqk eG
         1: N * (4 * CD * es + CC * es + D * f4) + nt * D * es + state,                      # -> o, S_final
         # -> W U Qp Kb Aqk eG (bf16 D = 64) | W U KbT WT QpT Kb AqkT [Akk Tii] eG

@@ -45,11 +45,13 @@ extern "C" {
 #define KDA_PASS_BWD 1
 #define KDA_PASS_TRAIN 2   /* kda_fwd_train + kda_bwd_train share one workspace */
 
-/* Workspace regions (see kda_workspace_offsets). */
+/* Workspace regions (see kda_workspace_offsets).  SEGX, SEGM and SEGS exist
+ * only for the bf16 forward at D = 128 when it splits the sequence into
+ * segments: per (b, h, segment) the segment's state map and start state. */
 enum kda_ws_region {
     KDA_WS_W = 0, KDA_WS_U, KDA_WS_QP, KDA_WS_QPT, KDA_WS_KB, KDA_WS_KBT, KDA_WS_WT,
     KDA_WS_AQK, KDA_WS_AQKT, KDA_WS_AKK, KDA_WS_TII, KDA_WS_EG, KDA_WS_H, KDA_WS_DH,
-    KDA_WS_VP, KDA_WS_DVP, KDA_WS_NREGIONS
+    KDA_WS_VP, KDA_WS_DVP, KDA_WS_SEGX, KDA_WS_SEGM, KDA_WS_SEGS, KDA_WS_NREGIONS
 };
 
 /* ABI version of this header (bumped on any signature change). */
@@ -237,9 +239,10 @@ size_t kda_layer_workspace_size(int which, int B, int T, int H, int D);
  * state recurrence, 5 local adjoints, 6 prep (training forward), 7 layer
  * producer (forward), 8 layer producer (backward, with its parameter-gradient
  * reduction), 9 gated RMSNorm (forward), 10 gated RMSNorm (backward, with its
- * reduction).
+ * reduction), 11-13 the segmented forward at D = 128 (bf16): 11 segment maps,
+ * 12 segment start states, 13 the forward of every segment.
  * kda_profile_read must be called after the streams have completed. */
-#define KDA_PROF_NKERNELS 11
+#define KDA_PROF_NKERNELS 14
 int kda_profile_enable(int on);              /* 1: clear records and start; 0: stop */
 const char* kda_profile_name(int id);
 int kda_profile_read(int id, double* total_ms, int* launches);

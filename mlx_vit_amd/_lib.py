@@ -11,6 +11,8 @@ import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkda_hip.so")
 
+ABI_VERSION = 2   # kda_abi_version() of the header this binding follows
+
 KDA_OK = 0
 KDA_E_INVALID = -1
 KDA_E_UNSUPPORTED = -2
@@ -27,7 +29,7 @@ KDA_LAYER_PRODUCER = 0
 KDA_LAYER_RMSNORM = 1
 
 WS_REGIONS = ("W", "U", "Qp", "QpT", "Kb", "KbT", "WT", "Aqk", "AqkT", "Akk", "Tii", "eG",
-              "h", "dh", "Vp", "dVp")
+              "h", "dh", "Vp", "dVp", "SegX", "SegM", "SegS")
 
 # every function the header declares, with its ctypes signature
 _P, _I, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -54,7 +56,7 @@ SIGNATURES = {
     "kda_profile_name": ([_I], ctypes.c_char_p),
     "kda_profile_read": ([_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)], _I),
 }
-PROF_NKERNELS = 11
+PROF_NKERNELS = 14
 
 _lib = None
 _lock = threading.Lock()
@@ -80,7 +82,7 @@ def load():
                 fn = getattr(lib, name)
                 fn.argtypes = args
                 fn.restype = res
-            if lib.kda_abi_version() != 1:
+            if lib.kda_abi_version() != ABI_VERSION:
                 raise RuntimeError("libkda_hip.so ABI version mismatch; rebuild it")
             _lib = lib
     return _lib

@@ -57,6 +57,16 @@ int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, b
     return KDA_OK;
 }
 
+// Whether the forward runs segmented (kda_seg.hip): bf16 at D = 128 whenever
+// the plan has more than one segment.  *nseg / *seg_len: the plan.
+bool seg_forward(int pass, int B, int T, int H, int D, int dtype, int* nseg, int* seg_len) {
+    *nseg = 1;
+    *seg_len = 0;
+    if (pass != KDA_PASS_FWD || dtype != KDA_DTYPE_BF16 || D != 128 || (size_t)B * T * H == 0) return false;
+    kda::seg_plan(B * H, (T + kda::C - 1) / kda::C, nseg, seg_len);
+    return *nseg > 1;
+}
+
 // Region sizes in bytes.  Operand slabs use the input dtype's element size;
 // eG, Akk and Tii are fp32.  Akk, Tii and V' exist for fp32 inputs only.
 void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
@@ -93,6 +103,13 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
             sz[KDA_WS_VP] = CD;
         }
     }
+    int nseg, seg_len;
+    if (seg_forward(pass, B, T, H, D, dtype, &nseg, &seg_len)) {
+        const size_t per = (size_t)B * H * nseg * D * D * 4;
+        sz[KDA_WS_SEGX] = per;
+        sz[KDA_WS_SEGM] = per;
+        sz[KDA_WS_SEGS] = per;
+    }
     size_t cur = 0;
     for (int r = 0; r < KDA_WS_NREGIONS; ++r) {
         if (sz[r] == 0) {
@@ -128,13 +145,15 @@ int hip_fail(hipError_t e, const char* where) {
 
 // ---- optional launch timing: an event pair around each launch, on its stream ----
 enum { PROF_PREP_FWD = 0, PROF_RECUR_FWD, PROF_PREP_BWD, PROF_RECUR_H, PROF_DH, PROF_LOCAL, PROF_PREP_TRAIN,
-       PROF_PRODUCER_FWD, PROF_PRODUCER_BWD, PROF_RMSNORM_FWD, PROF_RMSNORM_BWD };
+       PROF_PRODUCER_FWD, PROF_PRODUCER_BWD, PROF_RMSNORM_FWD, PROF_RMSNORM_BWD, PROF_SEG_MAP, PROF_SEG_SCAN,
+       PROF_SEG_FWD };
 const char* const kProfNames[KDA_PROF_NKERNELS] = {"kda_prep_kernel(fwd)", "kda_recur_kernel(fwd)",
                                                    "kda_prep_kernel(bwd)", "kda_recur_kernel(states)",
                                                    "kda_dh_kernel", "kda_bwd_local_kernel",
                                                    "kda_prep_kernel(train)", "producer_fwd_kernel",
                                                    "producer_bwd_kernel(+reduce)", "rmsnorm_fwd_kernel",
-                                                   "rmsnorm_bwd_kernel(+reduce)"};
+                                                   "rmsnorm_bwd_kernel(+reduce)", "kda_segchain_kernel(map)",
+                                                   "kda_segscan_kernel", "kda_segchain_kernel(fwd)"};
 struct Profiler {
     std::mutex mu;
     bool on = false;
@@ -334,6 +353,30 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
         launch_prep_pass(pass, q, k, v, g, beta, workspace, L, T, H, D, BH * nc, in_bf16, g_bf16, st, prof);
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
+    int nseg, seg_len;
+    if (!epi && seg_forward(pass, B, T, H, D, dtype, &nseg, &seg_len)) {
+        // bf16 D = 128, more than one segment: segment maps, start states, forward
+        kda::SegArgs sa = {};
+        sa.W = region(workspace, L, KDA_WS_W);
+        sa.U = region(workspace, L, KDA_WS_U);
+        sa.Qp = region(workspace, L, KDA_WS_QP);
+        sa.KbT = region(workspace, L, KDA_WS_KBT);
+        sa.Aqk = region(workspace, L, KDA_WS_AQK);
+        sa.eG = fregion(workspace, L, KDA_WS_EG);
+        sa.s0 = s0; sa.s_final = s_final; sa.o = o;
+        sa.segX = fregion(workspace, L, KDA_WS_SEGX);
+        sa.segM = static_cast<uint16_t*>(region(workspace, L, KDA_WS_SEGM));
+        sa.segS = fregion(workspace, L, KDA_WS_SEGS);
+        sa.T = T; sa.H = H; sa.nc = nc; sa.BH = BH; sa.nseg = nseg; sa.seg_len = seg_len;
+        e = timed(PROF_SEG_MAP, st, [&] { return kda::launch_seg_map(sa, st); }, prof);
+        if (e != hipSuccess) return hip_fail(e, "kda_segchain_kernel(map)");
+        e = timed(PROF_SEG_SCAN, st, [&] { return kda::launch_seg_scan(sa, st); }, prof);
+        if (e != hipSuccess) return hip_fail(e, "kda_segscan_kernel");
+        e = timed(PROF_SEG_FWD, st, [&] { return kda::launch_seg_fwd(sa, st); }, prof);
+        if (e != hipSuccess) return hip_fail(e, "kda_segchain_kernel(fwd)");
+        return ok();
+    }
+
     kda::RecurArgs ra = {};
     ra.W = region(workspace, L, KDA_WS_W);
     ra.U = region(workspace, L, KDA_WS_U);
@@ -470,7 +513,7 @@ int api_fwd_on_workspace(const void* q, const void* k, const void* v, const void
 // ----------------------------------------------------------------------------
 extern "C" {
 
-int kda_abi_version(void) { return 1; }
+int kda_abi_version(void) { return 2; }
 
 const char* kda_last_error(void) { return g_err.c_str(); }
 

@@ -666,6 +666,14 @@ __device__ __forceinline__ void dma_wait() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
+// vmcnt wait: all but the last `k` chunks' DMA (L instructions each) complete
+template <int L>
+__device__ __forceinline__ void dma_wait_chunks(int k) {
+    if (k >= 2) dma_wait<2 * L>();
+    else if (k == 1) dma_wait<L>();
+    else dma_wait<0>();
+}
+
 // This wave's LDS writes complete, then the workgroup barrier.  The empty asm
 // statements keep the compiler from moving memory operations across it.
 __device__ __forceinline__ void lds_barrier() {

@@ -612,7 +612,7 @@ template <int D, typename ST, typename TG>
 static hipError_t launch_prep_t(const PrepArgs& a, int nchunks, hipStream_t st) {
     constexpr int PREC = std::is_same<ST, float>::value ? 3 : 1;
     // eight waves per chunk where the registers allow four waves per SIMD
-    constexpr int NTH = (D == 64) ? KDA_PREP_NTH : 256;
+    constexpr int NTH = (D >= 64) ? KDA_PREP_NTH : 256;
     hipLaunchKernelGGL((kda_prep_kernel<D, ST, TG, PREC, NTH>), dim3(nchunks), dim3(NTH), 0, st, a);
     return hipGetLastError();
 }

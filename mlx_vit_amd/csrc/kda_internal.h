@@ -70,6 +70,28 @@ struct LocalArgs {
     int pf_ahead;   // L2 prefetch distance in chunks (the device's CU count), 0 = none
 };
 
+// The bf16 forward at D = 128 split over segments of the sequence (kda_seg.hip):
+// pass A (launch_seg_map) writes each segment's map X, M; pass B
+// (launch_seg_scan) the start state of segments 1 .. nseg - 1; pass C
+// (launch_seg_fwd) O and the final state.  segX, segS: [BH][nseg][D][D] fp32 in
+// the reference orientation [dv][dk]; segM: [BH][nseg][2][D][D] bf16, M^T
+// ([dk_in][dk_out]) split into hi and lo planes (the same bytes as fp32).
+struct SegArgs {
+    const void *W, *U, *Qp, *KbT, *Aqk;
+    const float* eG;
+    const float* s0;
+    float* s_final;
+    void* o;
+    float *segX, *segS;
+    uint16_t* segM;
+    int T, H, nc, BH, nseg, seg_len;
+};
+// segments for BH sequences of nc chunks: a function of the shape only
+void seg_plan(int BH, int nc, int* nseg, int* seg_len);
+hipError_t launch_seg_map(const SegArgs& a, hipStream_t st);
+hipError_t launch_seg_scan(const SegArgs& a, hipStream_t st);
+hipError_t launch_seg_fwd(const SegArgs& a, hipStream_t st);
+
 // Compute-unit count of device `dev` (0 if it cannot be queried), looked up
 // once per device under std::call_once, so concurrent callers are safe.
 int device_cu_count(int dev);

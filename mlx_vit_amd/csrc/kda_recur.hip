@@ -1134,13 +1134,6 @@ struct Recur3Layout {
                              (MODE == 0 ? DmaTile<C, RB_W, 4>::COUNT + DmaTile<C, RB_C, 4>::COUNT : 0) + 1;
 };
 
-// vmcnt wait: all but the last `k` chunks' DMA (L instructions each) complete
-template <int L>
-__device__ __forceinline__ void dma_wait_chunks(int k) {
-    if (k >= 2) dma_wait<2 * L>();
-    else if (k == 1) dma_wait<L>();
-    else dma_wait<0>();
-}
 
 template <int D, int MODE, int CS>
 __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {

@@ -91,10 +91,11 @@ def workspace_bytes(pass_: int, B: int, T: int, H: int, D: int, dtype: torch.dty
     return int(n)
 
 
-def workspace_offsets(pass_: int, B: int, T: int, H: int, D: int) -> dict:
+def workspace_offsets(pass_: int, B: int, T: int, H: int, D: int, dtype: torch.dtype = torch.float32) -> dict:
     lib = _lib.load()
     arr = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
-    _lib.check(lib.kda_workspace_offsets(pass_, B, T, H, D, CHUNK, 0, arr), "kda_workspace_offsets")
+    _lib.check(lib.kda_workspace_offsets(pass_, B, T, H, D, CHUNK, _DTYPE_CODE.get(dtype, 0), arr),
+               "kda_workspace_offsets")
     return {name: int(arr[i]) for i, name in enumerate(_lib.WS_REGIONS)}
 
 

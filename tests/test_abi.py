@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().kda_abi_version() == 1
+    assert _lib.load().kda_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_workspace_sizes():
@@ -91,13 +91,41 @@ def test_layer_workspace_sizes(B, T, H, D):
 
 def test_workspace_offsets_disjoint():
     lib = _lib.load()
-    for pass_ in (0, 1, 2):
-        arr = (ctypes.c_int64 * 16)()
-        assert lib.kda_workspace_offsets(pass_, 2, 300, 3, 64, 64, 1, arr) == 0
+    for pass_, shape in ((0, (2, 300, 3, 64)), (1, (2, 300, 3, 64)), (2, (2, 300, 3, 64)),
+                         (0, (1, 2000, 2, 128)), (0, (1, 32768, 16, 128))):
+        arr = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
+        assert lib.kda_workspace_offsets(pass_, *shape, 64, 1, arr) == 0
         offs = sorted(o for o in arr if o >= 0)
         assert offs[0] == 0 and all(b - a >= 256 and b % 256 == 0 for a, b in zip(offs, offs[1:]))
-        total = lib.kda_workspace_size(pass_, 2, 300, 3, 64, 64, 1)
+        total = lib.kda_workspace_size(pass_, *shape, 64, 1)
         assert offs[-1] < total
+
+
+@pytest.mark.parametrize("B,T,H,D,dtype,nseg", [
+    (1, 32768, 16, 128, 1, 16),   # config 3: 16 (b, h) x 16 segments of 32 chunks
+    (1, 2000, 2, 128, 1, 8),      # 32 chunks: segments of at least 4 chunks
+    (2, 600, 3, 128, 1, 2),
+    (1, 129, 2, 128, 1, 1),       # 3 chunks: one segment, the unsegmented kernel
+    (16, 1024, 16, 128, 1, 1),    # 256 (b, h) fill the GPU by themselves
+    (1, 32768, 16, 128, 0, 1),    # fp32 inputs: not segmented
+    (1, 32768, 16, 64, 1, 1),     # D = 64: not segmented
+])
+def test_segment_plan_regions(B, T, H, D, dtype, nseg):
+    """The bf16 forward at D = 128 is split into segments exactly when the plan
+    (about 256 workgroups, >= 4 chunks per segment) gives more than one; the
+    three segment regions are then B*H*nseg*D*D fp32 each."""
+    lib = _lib.load()
+    arr = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
+    assert lib.kda_workspace_offsets(0, B, T, H, D, 64, dtype, arr) == 0
+    off = dict(zip(_lib.WS_REGIONS, arr))
+    seg = ("SegX", "SegM", "SegS")
+    if nseg == 1:
+        assert all(off[r] == -1 for r in seg)
+        return
+    per = B * H * nseg * D * D * 4
+    for a, b in zip(seg, seg[1:]):
+        assert off[b] - off[a] == per
+    assert lib.kda_workspace_size(0, B, T, H, D, 64, dtype) - off["SegS"] == per
 
 
 @pytest.mark.parametrize("B,T,H,D,chunk,dtype,gdt,code", [

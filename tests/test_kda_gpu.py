@@ -157,6 +157,21 @@ def test_fwd_parity_bf16(B, T, H, D, with_state):
     _assert_all(_fwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], f"fwd bf16 {B},{T},{H},{D},{with_state}")
 
 
+@pytest.mark.parametrize("B,T,H,D,with_state", [
+    (1, 2000, 2, 128, True),     # 8 segments of 4 chunks, ragged last chunk
+    (1, 1700, 2, 128, False),    # 6 segments, the last of 2 chunks
+    (2, 600, 3, 128, True),      # 2 segments for each of six (b, h)
+])
+def test_fwd_parity_bf16_segmented(B, T, H, D, with_state):
+    """The bf16 forward at D = 128 split over segments of the sequence: segment
+    maps (chain from zero / from the identity), the start-state scan, and the
+    forward of every segment from its start state."""
+    kda = _kda()
+    assert kda.workspace_offsets(0, B, T, H, D, torch.bfloat16)["SegX"] >= 0, "segmented path not taken"
+    x = _inputs(B, T, H, D, torch.bfloat16, seed=21, with_state=with_state)
+    _assert_all(_fwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], f"fwd bf16 segmented {B},{T},{H},{D},{with_state}")
+
+
 def test_fwd_parity_config1_full():
     """Config 1: B=8, H=12, T=1568, D=64, bf16 -- full size against the fp64 oracle."""
     x = _inputs(8, 1568, 12, 64, torch.bfloat16, seed=0)
