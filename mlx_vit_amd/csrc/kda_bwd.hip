@@ -619,9 +619,9 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
         f32x4 P = zero4();
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
-            const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
-            const Frag8 Bk = (j == i - 1) ? ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
-                                          : ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks, fsc + 32 * ks);
+            const Frag8 Ak = ldfrag_c<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
+            const Frag8 Bk = (j == i - 1) ? ldfrag_c<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
+                                          : ldfrag_c_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks, fsc + 32 * ks);
             P = mma<PREC>(Ak, Bk, P);
         }
 #pragma unroll
@@ -777,13 +777,15 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
             Frag8 Ao[MB][D / 32], Av[MB][D / 32], Bh[D / 32], Bdh[D / 32];
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                Bh[ks] = ldfrag<PREC, ST>(sh, LDK, BS * ct, 32 * ks);
-                Bdh[ks] = ldfrag<PREC, ST>(sdh, LDK, BS * ct, 32 * ks);
+                // every phase-1 product takes both operands from LDS rows:
+                // contiguous k-slots (ldfrag_c), one 16-byte read per operand
+                Bh[ks] = ldfrag_c<PREC, ST>(sh, LDK, BS * ct, 32 * ks);
+                Bdh[ks] = ldfrag_c<PREC, ST>(sdh, LDK, BS * ct, 32 * ks);
 #pragma unroll
                 for (int mm = 0; mm < MB; ++mm) {
                     const int m = 2 * rh + mm;
-                    Ao[mm][ks] = ldfrag<PREC, ST>(sdO, LDK, BS * m, 32 * ks);
-                    Av[mm][ks] = ldfrag<PREC, ST>(sVp, LDK, BS * m, 32 * ks);
+                    Ao[mm][ks] = ldfrag_c<PREC, ST>(sdO, LDK, BS * m, 32 * ks);
+                    Av[mm][ks] = ldfrag_c<PREC, ST>(sVp, LDK, BS * m, 32 * ks);
                 }
             }
             // dW = -dV' h^T, all row blocks of the channel tile, for the rh = 0
@@ -794,7 +796,7 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                     f32x4 dW = zero4();
 #pragma unroll
                     for (int ks = 0; ks < D / 32; ++ks)
-                        dW = mma<PREC>(ldfrag<PREC, ST>(sdVp, LDK, BS * m, 32 * ks), Bh[ks], dW);
+                        dW = mma<PREC>(ldfrag_c<PREC, ST>(sdVp, LDK, BS * m, 32 * ks), Bh[ks], dW);
                     dWt[m] = negacc(dW);
                 }
             }
@@ -843,8 +845,8 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
             Frag8 A[D / 32], B[D / 32];
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                A[ks] = ldfrag<PREC, ST>(sdO, LDK, BS * i, 32 * ks);
-                B[ks] = ldfrag<PREC, ST>(sVp, LDK, BS * j, 32 * ks);
+                A[ks] = ldfrag_c<PREC, ST>(sdO, LDK, BS * i, 32 * ks);
+                B[ks] = ldfrag_c<PREC, ST>(sVp, LDK, BS * j, 32 * ks);
             }
             f32x4 acc = zero4();
 #pragma unroll
@@ -961,9 +963,9 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
         Frag8 A[2 * D / 32], B[2 * D / 32];
 #pragma unroll
         for (int ks = 0; ks < 2 * D / 32; ++ks) {
-            A[ks] = ldfrag<2, float>(&sm.ra.dR[0][0], LDR, BS * i, 32 * ks);
-            B[ks] = (32 * ks < D) ? ldfrag<1, ST>(&sm.W[0][0], LDK, BS * j, 32 * ks)
-                                  : ldfrag<1, ST>(&sm.U[0][0], LDK, BS * j, 32 * ks - D);
+            A[ks] = ldfrag_c<2, float>(&sm.ra.dR[0][0], LDR, BS * i, 32 * ks);
+            B[ks] = (32 * ks < D) ? ldfrag_c<1, ST>(&sm.W[0][0], LDK, BS * j, 32 * ks)
+                                  : ldfrag_c<1, ST>(&sm.U[0][0], LDK, BS * j, 32 * ks - D);
         }
         // W and U are bf16 here: splitting only dR keeps the fp32 accuracy of the product
         f32x4 acc = zero4();

@@ -268,6 +268,41 @@ __device__ __forceinline__ Frag8 ldfrag(const ST* M, int ld, int row0, int k0) {
     }
 }
 
+// ldfrag with the hardware's own k-slot order instead of the K permutation:
+// slot (g, e) holds k = k0 + 8 g + e, so a lane's eight elements are one
+// contiguous 16-byte piece (bf16; two for fp32).  Only for products whose A
+// and B operands both come from memory rows this way -- never with an
+// accumulator fed back as B, which carries the K permutation.  With rows
+// 16 bytes mod 128 apart (a 16-byte row pad), the eight lanes of a 16-byte
+// LDS read hit eight distinct bank groups.
+template <int PREC, typename ST>
+__device__ __forceinline__ Frag8 ldfrag_c(const ST* M, int ld, int row0, int k0) {
+    const int l = lane_id(), r = l & 15, g = l >> 4;
+    const ST* p = M + (size_t)(row0 + r) * ld + k0 + 8 * g;
+    if constexpr (std::is_same<ST, uint16_t>::value) {
+        Frag8 f;
+        f.h = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+        if constexpr (PREC >= 2) f.l = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+        return f;
+    } else {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        const float4 y = *reinterpret_cast<const float4*>(p + 4);
+        const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+        return frag_from_f32<PREC>(v);
+    }
+}
+// ldfrag_c with every k-slot multiplied by scale[k - k0]
+template <int PREC, typename ST>
+__device__ __forceinline__ Frag8 ldfrag_c_scaled(const ST* M, int ld, int row0, int k0, const float* scale) {
+    const int l = lane_id(), r = l & 15, g = l >> 4;
+    const ST* p = M + (size_t)(row0 + r) * ld + k0 + 8 * g;
+    const float4 x = ld4<ST>(p), y = ld4<ST>(p + 4);
+    const float4 sx = *reinterpret_cast<const float4*>(scale + 8 * g);
+    const float4 sy = *reinterpret_cast<const float4*>(scale + 8 * g + 4);
+    const float v[8] = {x.x * sx.x, x.y * sx.y, x.z * sx.z, x.w * sx.w, y.x * sy.x, y.y * sy.y, y.z * sy.z, y.w * sy.w};
+    return frag_from_f32<PREC>(v);
+}
+
 // 16-wide k-step, row-major k contiguous
 template <int PREC, typename ST>
 __device__ __forceinline__ Frag4 ldfrag4(const ST* M, int ld, int row0, int k0) {

@@ -375,13 +375,15 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
             auto form_tile = [&](int i, int j) __attribute__((always_inline)) {
                 const float* fsc = &s.fac[(j == i) ? FAC_FD + i : (j == i - 1) ? 0 : fac_f_row(i, j)][0];
                 f32x4 P = zero4(), Q = zero4();
+                // both operands are rows of LDS tiles: contiguous k-slots, one
+                // 16-byte read per lane and operand
 #pragma unroll
                 for (int ks = 0; ks < D / 32; ++ks) {
-                    const Frag8 Ak = ldfrag<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
-                    const Frag8 Aq = ldfrag<PREC, ST>(&s.ql[0][0], LDK, BS * i, 32 * ks);
-                    const Frag8 Bk = (j == i - 1) ? ldfrag<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
-                                                  : ldfrag_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
-                                                                            fsc + 32 * ks);
+                    const Frag8 Ak = ldfrag_c<PREC, ST>(&s.kl[0][0], LDK, BS * i, 32 * ks);
+                    const Frag8 Aq = ldfrag_c<PREC, ST>(&s.ql[0][0], LDK, BS * i, 32 * ks);
+                    const Frag8 Bk = (j == i - 1) ? ldfrag_c<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks)
+                                                  : ldfrag_c_scaled<PREC, ST>(&s.kr[0][0], LDK, BS * j, 32 * ks,
+                                                                              fsc + 32 * ks);
                     P = mma<PREC>(Ak, Bk, P);
                     Q = mma<PREC>(Aq, Bk, Q);
                 }
