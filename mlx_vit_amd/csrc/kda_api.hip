@@ -43,8 +43,10 @@ int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, b
     if (chunk != 8 && chunk != 16 && chunk != 32 && chunk != kda::C)
         return fail(KDA_E_UNSUPPORTED, "chunk=%d: expected 8, 16, 32 or 64", chunk);
     if (bwd) {
-        if (D != 32 && D != 64)
-            return fail(KDA_E_UNSUPPORTED, "D=%d: the backward supports D in {32, 64}", D);
+        if (D != 32 && D != 64 && D != 128)
+            return fail(KDA_E_UNSUPPORTED, "D=%d: the backward supports D in {32, 64, 128}", D);
+        if (D == 128 && dtype != KDA_DTYPE_BF16)
+            return fail(KDA_E_UNSUPPORTED, "D=128: the backward supports bf16 operands (dtype=1), got dtype=%d", dtype);
     } else if (D != 32 && D != 64 && D != 128) {
         return fail(KDA_E_UNSUPPORTED, "D=%d: the forward supports D in {32, 64, 128}", D);
     }
@@ -96,8 +98,9 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
         sz[KDA_WS_H] = DD;
         sz[KDA_WS_DH] = DD;
         sz[KDA_WS_DVP] = CD;
-        if (dtype == KDA_DTYPE_F32) {
-            // the bf16 local-adjoint kernel recomputes these from the chunk's inputs
+        if (dtype == KDA_DTYPE_F32 || D == 128) {
+            // the bf16 local-adjoint kernel at D <= 64 recomputes these from the
+            // chunk's inputs; the fp32 one and the one at D = 128 read them
             sz[KDA_WS_AKK] = N * kda::C * kda::C * 4;
             sz[KDA_WS_TII] = TI;
             sz[KDA_WS_VP] = CD;

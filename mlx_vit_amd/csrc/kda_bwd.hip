@@ -1466,6 +1466,7 @@ hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int 
     KDA_LOCAL_CASE(32)
     KDA_LOCAL_CASE(64)
 #undef KDA_LOCAL_CASE
+    if (D == 128) return launch_local_wide(a, D, in_bf16, g_bf16, nchunks, st);
     return hipErrorInvalidValue;
 }
 

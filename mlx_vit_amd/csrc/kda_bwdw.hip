@@ -1,0 +1,470 @@
+// kda_bwdw.hip -- the local-adjoint kernel of the KDA backward at D = 128.
+//
+// kda_bwd_localw_kernel: one 512-thread workgroup per chunk; wave w owns
+// channel tile w (16 channels) of every per-(t, d) adjoint.  Same chunk
+// algebra as the D = 64 kernels (nope_gdn_mlx.py:2579-2720, the transposed WY
+// solve 1209-1286, the M backward kernels 2080-2295, the in-chunk reverse
+// cumsum 2573-2577), with an LDS plan that fits D = 128:
+//   - the chunk's operands that are read as fragments (dO, V', dV', h, dh, W,
+//     U) come straight from global memory (L2): nothing of them is staged;
+//   - A_kk and the inverted diagonal blocks of I + L come from the prep's
+//     workspace, V' from the state recompute's;
+//   - the anchored decay operands of phase 4 (k e^{gamma_t - gamma_r},
+//     q e^{...}, k e^{gamma_r - gamma_t}, r the first row of t's 16-row block)
+//     are the lane's own rows of its own channel, so they live in registers;
+//   - dR = (I + L)^-T [dW | dU] passes through LDS one half (dW columns, then
+//     dU columns) at a time.
+// LDS: gamma and its factor tables, dP / dA (C x C fp32 each), half of dR, the
+// diagonal inverses, the dbeta partials: about 118 KB.
+#include "kda_internal.h"
+
+namespace kda {
+
+namespace {
+
+template <int D>
+struct WideLds {
+    float g[C][D + 4];   // gamma, the in-chunk cumsum of g
+    float er[NB][D];     // e^{gamma_16i}
+    float f[6][D];       // e^{gamma_16i - gamma_16j}, pair_idx(i, j)
+    float tot[NB][D];    // block totals of the cumsum
+    float beta[C];
+};
+
+// rows of a (B, T, H, D) tensor as an fp32-valued A operand; rows at or past
+// `valid` read as zero
+template <typename TI>
+__device__ __forceinline__ Fr8 rows8(const TI* base, size_t rstride, int row0, int k0, int valid) {
+    const int l = lane_id(), r = l & 15, g = l >> 4;
+    Fr8 f;
+    if (row0 + r < valid) {
+        const TI* p = base + (size_t)(row0 + r) * rstride + k0 + 4 * g;
+        const float4 x = ld4<TI>(p), y = ld4<TI>(p + 16);
+        f.v[0] = x.x; f.v[1] = x.y; f.v[2] = x.z; f.v[3] = x.w;
+        f.v[4] = y.x; f.v[5] = y.y; f.v[6] = y.z; f.v[7] = y.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f.v[e] = 0.f;
+    }
+    return f;
+}
+
+__device__ __forceinline__ float sum16w(float x) {
+    x += __shfl_xor(x, 1, 64);
+    x += __shfl_xor(x, 2, 64);
+    x += __shfl_xor(x, 4, 64);
+    x += __shfl_xor(x, 8, 64);
+    return x;
+}
+__device__ __forceinline__ float sum4gw(float x) {
+    x += __shfl_xor(x, 16, 64);
+    x += __shfl_xor(x, 32, 64);
+    return x;
+}
+
+}  // namespace
+
+template <int D, typename TI, typename TG, int PREC>
+__global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a) {
+    constexpr int NT = D / BS, NTH = 4 * D, NW = NTH / 64;
+    static_assert(NW == NT && NB == 4, "one wave per channel tile, one thread per (channel, row block)");
+    __shared__ WideLds<D> s;
+    __shared__ float sp[C][C + 4];          // Akk, then dP = diag(beta) dL
+    __shared__ float sda[C][C + 4];         // dAqk (lower, with the diagonal)
+    __shared__ float sdr[C][D + 4];         // one half of dR: dR_k, then dR_v
+    __shared__ float tii[NB][BS][BS + 4];
+    __shared__ float sdb[NB + NT][C];       // dbeta partials: [j] from dL tiles of column block j, [NB + nt] channel tile nt
+
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
+              g4 = l >> 4;
+    __builtin_assume(w >= 0 && w < NW);
+    const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int t0 = n * C, valid = min(C, a.T - t0);
+    const size_t rs = (size_t)a.H * D;
+    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
+    const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
+    const TI* q = static_cast<const TI*>(a.q);
+    const TI* k = static_cast<const TI*>(a.k);
+    const TI* v = static_cast<const TI*>(a.v);
+    const TG* g = static_cast<const TG*>(a.g);
+    const TI* beta = static_cast<const TI*>(a.beta);
+    const TI* dout = static_cast<const TI*>(a.dout);
+    const size_t cCD = (size_t)ch * C * D, cCC = (size_t)ch * C * C;
+    const TI* hS = static_cast<const TI*>(a.h) + (size_t)ch * D * D;
+    const TI* dhS = static_cast<const TI*>(a.dh) + (size_t)ch * D * D;
+    const TI* Vp = static_cast<const TI*>(a.Vp) + cCD;
+    const TI* dVp = static_cast<const TI*>(a.dVp) + cCD;
+    const TI* Wc = static_cast<const TI*>(a.W) + cCD;
+    const TI* Uc = static_cast<const TI*>(a.U) + cCD;
+
+    // ---------------- phase 0: A_kk, inverses, gamma, factors ----------------
+    for (int idx = tid; idx < C * C; idx += NTH) sp[idx / C][idx % C] = a.Akk[cCC + idx];
+    for (int idx = tid; idx < NB * BS * BS; idx += NTH) {
+        const int i = idx / (BS * BS), e = idx - i * BS * BS;
+        tii[i][e / BS][e % BS] = a.Tii[(size_t)ch * NB * BS * BS + idx];
+    }
+    for (int idx = tid; idx < (NB + NT) * C; idx += NTH) sdb[idx / C][idx % C] = 0.f;
+    if (tid < C) s.beta[tid] = (tid < valid) ? ld1<TI>(beta + bbase + (size_t)tid * a.H) : 0.f;
+    // thread (channel cd, block cb): inclusive cumsum of g over the block's 16
+    // rows (rows past T are g = 0: no decay), then the totals of earlier blocks
+    int flag = 0;
+    {
+        const int cd = tid % D, cb = tid / D;
+        float run = 0.f;
+#pragma unroll 4
+        for (int r = 0; r < BS; ++r) {
+            const int t = BS * cb + r;
+            const float x = (t < valid) ? ld1<TG>(g + base + (size_t)t * rs + cd) : 0.f;
+            if (!(x <= 0.f)) flag = 1;
+            run += x;
+            s.g[t][cd] = run;
+        }
+        s.tot[cb][cd] = run;
+        __syncthreads();
+        float off = 0.f;
+        for (int bb = 0; bb < cb; ++bb) off += s.tot[bb][cd];
+        if (cb > 0)
+#pragma unroll 4
+            for (int r = 0; r < BS; ++r) s.g[BS * cb + r][cd] += off;
+    }
+    __syncthreads();
+    // factor tables and the span guard (a chunk beyond it, or with g > 0 or a
+    // NaN, is evaluated pair by pair)
+    for (int idx = tid; idx < NB * D; idx += NTH) {
+        const int j = idx / D, d = idx % D;
+        if (!(s.g[BS * j][d] - s.g[BS * j + BS - 1][d] <= SPAN_MAX)) flag = 1;
+        s.er[j][d] = kexp<PREC>(s.g[BS * j][d]);
+    }
+    for (int idx = tid; idx < 6 * D; idx += NTH) {
+        const int p = idx / D, d = idx % D;
+        const int i = (p >= 3) ? 3 : (p >= 1) ? 2 : 1, j = p - pair_idx(i, 0);
+        s.f[p][d] = kexp<PREC>(s.g[BS * i][d] - s.g[BS * j][d]);
+    }
+    const int unsafe = __syncthreads_or(flag);
+
+    // wave w owns channel tile w: rows t = 16 m + 4 g4 + e, channel d
+    const int nt = w, d = nt * BS + r16;
+    // raw k, q of the lane's rows; el = e^{gamma_t - gamma_r}, er = e^{gamma_r -
+    // gamma_t} (r = 16 m), eb = e^{G - gamma_t}, erb = e^{gamma_r}
+    float kx[NB][4], qx[NB][4], el[NB][4], er[NB][4], eb[NB][4], erb[NB];
+    {
+        const float G = s.g[C - 1][d];
+#pragma unroll
+        for (int m = 0; m < NB; ++m) {
+            const float gr = s.g[BS * m][d];
+            erb[m] = s.er[m][d];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * m + 4 * g4 + e;
+                const float gt = s.g[t][d];
+                const size_t o = base + (size_t)t * rs + d;
+                kx[m][e] = (t < valid) ? ld1<TI>(k + o) : 0.f;
+                qx[m][e] = (t < valid) ? ld1<TI>(q + o) : 0.f;
+                el[m][e] = kexp<PREC>(gt - gr);
+                er[m][e] = unsafe ? 0.f : kexp<PREC>(gr - gt);
+                eb[m][e] = kexp<PREC>(G - gt);
+            }
+        }
+    }
+
+    f32x4 dqa[NB], dka[NB], dga[NB], dWt[NB];
+#pragma unroll
+    for (int m = 0; m < NB; ++m) { dqa[m] = zero4(); dka[m] = zero4(); dga[m] = zero4(); dWt[m] = zero4(); }
+    float dgcol = 0.f;
+
+    // ---------------- phase 1: products over dv ----------------
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        f32x4 dQp = zero4(), dKb = zero4(), dW = zero4();
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const Fr8 Bh = frag8(hS, D, BS * nt, 32 * ks);
+            const Fr8 Bdh = frag8(dhS, D, BS * nt, 32 * ks);
+            dQp = mma8<PREC>(rows8<TI>(dout + base, rs, BS * m, 32 * ks, valid), Bh, dQp);
+            dKb = mma8<PREC>(frag8(Vp, D, BS * m, 32 * ks), Bdh, dKb);
+            dW = mma8<PREC>(neg(frag8(dVp, D, BS * m, 32 * ks)), Bh, dW);
+        }
+        dWt[m] = dW;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float egt = erb[m] * el[m][e];                 // e^{gamma_t}
+            dqa[m][e] = dQp[e] * egt;
+            dka[m][e] = dKb[e] * eb[m][e];
+            const float kbv = kx[m][e] * eb[m][e];
+            dga[m][e] = dQp[e] * qx[m][e] * egt - dKb[e] * kbv;
+            dgcol += dKb[e] * kbv;
+        }
+    }
+    {
+        // state-decay term of dG: e^G sum_col dh[d][col] h[d][col]
+        float part = 0.f;
+        for (int c = g4 * (D / 4); c < (g4 + 1) * (D / 4); ++c)
+            part += ld1<TI>(dhS + (size_t)d * D + c) * ld1<TI>(hS + (size_t)d * D + c);
+        dgcol = sum4gw(dgcol) + kexp<PREC>(s.g[C - 1][d]) * sum4gw(part);
+    }
+    // dAqk = tril(dO V'^T), 10 lower tiles over the waves
+    for (int tix = w; tix < 10; tix += NW) {
+        int i, j;
+        tile_ij(tix, i, j);
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks)
+            acc = mma8<PREC>(rows8<TI>(dout + base, rs, BS * i, 32 * ks, valid), frag8(Vp, D, BS * j, 32 * ks), acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
+            sda[t][sx] = (sx <= t) ? acc[e] : 0.f;
+        }
+    }
+    // zero upper tiles of sda
+    for (int idx = tid; idx < 6 * BS * BS; idx += NTH) {
+        const int tile = idx / (BS * BS), e = idx - tile * BS * BS;
+        const int i = (tile < 3) ? 0 : (tile < 5) ? 1 : 2;
+        const int j = (tile < 3) ? tile + 1 : (tile < 5) ? tile - 1 : 3;
+        sda[BS * i + e / BS][BS * j + (e % BS)] = 0.f;
+    }
+    __syncthreads();
+
+    // ---------------- phase 2: transposed WY solve (fp32-accurate split products) ----------------
+    f32x4 dRk[NB], dRv[NB];
+    {
+#pragma unroll
+        for (int i = NB - 1; i >= 0; --i) {
+            f32x4 Yk = dWt[i], Yv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Yv[e] = ld1<TI>(dVp + (size_t)(BS * i + 4 * g4 + e) * D + d);
+#pragma unroll
+            for (int j = i + 1; j < NB; ++j) {
+                // A[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a]
+                Fr4 A;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int rb = BS * j + 4 * g4 + e;
+                    A.v[e] = -s.beta[rb] * sp[rb][BS * i + r16];
+                }
+                Yk = mma4<3>(A, acc2frag4(dRk[j]), Yk);
+                Yv = mma4<3>(A, acc2frag4(dRv[j]), Yv);
+            }
+            const Fr4 Tt = frag4T(&tii[i][0][0], BS + 4, 0, 0);     // A[a][b] = T_ii[b][a]
+            dRk[i] = mma4<3>(Tt, acc2frag4(Yk), zero4());
+            dRv[i] = mma4<3>(Tt, acc2frag4(Yv), zero4());
+        }
+        TI* dv = static_cast<TI*>(a.dv);
+#pragma unroll
+        for (int m = 0; m < NB; ++m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * m + 4 * g4 + e;
+                const float bt = s.beta[t];
+                const float egt = erb[m] * el[m][e];
+                const float vv = (t < valid) ? ld1<TI>(v + base + (size_t)t * rs + d) : 0.f;
+                if (t < valid) st1<TI>(dv + base + (size_t)t * rs + d, bt * dRv[m][e]);
+                dka[m][e] += bt * egt * dRk[m][e];
+                dga[m][e] += dRk[m][e] * bt * egt * kx[m][e];
+                const float db = sum16w(dRv[m][e] * vv + dRk[m][e] * egt * kx[m][e]);
+                if (r16 == 0) sdb[NB + nt][t] = db;
+                sdr[t][d] = dRk[m][e];
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---------------- phase 3: dL = -tril(dR [W | U]^T, -1), one half of dR at a time ----------------
+    constexpr int TPW = (10 + NW - 1) / NW;
+    f32x4 accL[TPW];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+        accL[u] = zero4();
+        const int tix = w + NW * u;
+        if (tix < 10) {
+            int i, j;
+            tile_ij(tix, i, j);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                accL[u] = mma8<3>(frag8(&sdr[0][0], D + 4, BS * i, 32 * ks), frag8(Wc, D, BS * j, 32 * ks), accL[u]);
+        }
+    }
+    __syncthreads();   // dR_k read by every wave
+#pragma unroll
+    for (int m = 0; m < NB; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sdr[BS * m + 4 * g4 + e][d] = dRv[m][e];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+        const int tix = w + NW * u;
+        if (tix < 10) {
+            int i, j;
+            tile_ij(tix, i, j);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                accL[u] = mma8<3>(frag8(&sdr[0][0], D + 4, BS * i, 32 * ks), frag8(Uc, D, BS * j, 32 * ks), accL[u]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
+                const float dL = (sx < t) ? -accL[u][e] : 0.f;
+                const float db = sum16w(dL * sp[t][sx]);
+                if (r16 == 0) sdb[j][t] = db;
+                sp[t][sx] = s.beta[t] * dL;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints ----------------
+    if (!unsafe) {
+        // row and column sides of a pair must agree to fp32: exact split products
+        constexpr int PX = PREC >= 3 ? 4 : PREC;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            f32x4 dKl = zero4(), dQl = zero4();
+#pragma unroll
+            for (int j = 0; j <= i; ++j) {
+                const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
+                Fr4 B;   // K_r of the lane's rows of block j (channel d), times F_ij
+#pragma unroll
+                for (int e = 0; e < 4; ++e) B.v[e] = kx[j][e] * er[j][e] * fs;
+                dKl = mma4<PX>(frag4(&sp[0][0], C + 4, BS * i, BS * j), B, dKl);
+                Fr4 Aq = frag4(&sda[0][0], C + 4, BS * i, BS * j);
+                if (j == i) {   // the diagonal pairs (t, t) are added apart, below
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * g4 + e == r16) Aq.v[e] = 0.f;
+                }
+                dQl = mma4<PX>(Aq, B, dQl);
+            }
+            Fr4 Bk, Bq;   // K_l, Q_l of the lane's rows of block i
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                Bk.v[e] = kx[i][e] * el[i][e];
+                Bq.v[e] = qx[i][e] * el[i][e];
+            }
+            // each pair's row-t and column-s terms of dgamma cancel in the reverse
+            // cumsum; weight each side by the operand values the other side's MFMA
+            // used, so that the cancellation is exact to fp32
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dka[i][e] += dKl[e] * el[i][e];
+                dqa[i][e] += dQl[e] * el[i][e];
+                dga[i][e] += dKl[e] * mfma_operand<PREC>(Bk.v[e]) + dQl[e] * mfma_operand<PREC>(Bq.v[e]);
+            }
+#pragma unroll
+            for (int j = 0; j <= i; ++j) {
+                f32x4 dKr = mma4<PX>(frag4T(&sp[0][0], C + 4, BS * j, BS * i), Bk, zero4());
+                Fr4 Aq = frag4T(&sda[0][0], C + 4, BS * j, BS * i);
+                if (j == i) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * g4 + e == r16) Aq.v[e] = 0.f;
+                }
+                dKr = mma4<PX>(Aq, Bq, dKr);
+                const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dka[j][e] += dKr[e] * fs * er[j][e];
+                    // the row side's B operand for this s and block pair
+                    dga[j][e] -= dKr[e] * mfma_operand<PREC>(kx[j][e] * er[j][e] * fs);
+                }
+            }
+        }
+    } else {
+        // pair by pair with the exact weight e^{gamma_t - gamma_s}: raw k and q of
+        // the other rows from global memory, gamma from LDS
+#pragma unroll
+        for (int m = 0; m < NB; ++m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = BS * m + 4 * g4 + e;
+                const float gt = s.g[t][d];
+                float ak = 0.f, aq = 0.f, ag = 0.f;
+                for (int sx = 0; sx < t; ++sx) {
+                    const float ksx = (sx < valid) ? ld1<TI>(k + base + (size_t)sx * rs + d) : 0.f;
+                    const float ks = ksx * kexp<PREC>(gt - s.g[sx][d]);
+                    const float pp = sp[t][sx], pa = sda[t][sx];
+                    ak += pp * ks;
+                    aq += pa * ks;
+                    ag += (pp * kx[m][e] + pa * qx[m][e]) * ks;
+                }
+                for (int sx = t + 1; sx < C; ++sx) {
+                    const float ksx = (sx < valid) ? ld1<TI>(k + base + (size_t)sx * rs + d) : 0.f;
+                    const float qsx = (sx < valid) ? ld1<TI>(q + base + (size_t)sx * rs + d) : 0.f;
+                    const float ex = kexp<PREC>(s.g[sx][d] - gt);
+                    const float pp = sp[sx][t], pa = sda[sx][t];
+                    const float c = (pp * ksx + pa * qsx) * ex;
+                    ak += c;
+                    ag -= c * kx[m][e];
+                }
+                dka[m][e] += ak;
+                dqa[m][e] += aq;
+                dga[m][e] += ag;
+            }
+        }
+    }
+    // the diagonal pairs (t, t) of A_qk (weight 1): dq_t += dA_tt k_t and
+    // dk_t += dA_tt q_t, and nothing in dgamma_t (its row and column terms are
+    // equal and opposite)
+#pragma unroll
+    for (int m = 0; m < NB; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = BS * m + 4 * g4 + e;
+            dqa[m][e] += sda[t][t] * kx[m][e];
+            dka[m][e] += sda[t][t] * qx[m][e];
+        }
+
+    // ---------------- phase 5: dG, reverse cumsum, stores ----------------
+    if (g4 == 3) dga[NB - 1][3] += dgcol;        // row C-1
+    float lsum[NB][4], tots[NB];
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        float run = 0.f;
+#pragma unroll
+        for (int e = 3; e >= 0; --e) { run += dga[m][e]; lsum[m][e] = run; }
+        tots[m] = run;
+    }
+    float after_m = 0.f;   // sum over row tiles > m
+#pragma unroll
+    for (int m = NB - 1; m >= 0; --m) {
+        const float t0v = __shfl(tots[m], r16, 64);
+        const float t1v = __shfl(tots[m], r16 + 16, 64);
+        const float t2v = __shfl(tots[m], r16 + 32, 64);
+        const float t3v = __shfl(tots[m], r16 + 48, 64);
+        const float later = (g4 < 1 ? t1v : 0.f) + (g4 < 2 ? t2v : 0.f) + (g4 < 3 ? t3v : 0.f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lsum[m][e] += later + after_m;
+        after_m += t0v + t1v + t2v + t3v;
+    }
+    TI* dq = static_cast<TI*>(a.dq);
+    TI* dk = static_cast<TI*>(a.dk);
+    TG* dg = static_cast<TG*>(a.dg);
+#pragma unroll
+    for (int m = 0; m < NB; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = BS * m + 4 * g4 + e;
+            if (t < valid) {
+                const size_t o = base + (size_t)t * rs + d;
+                st1<TI>(dq + o, dqa[m][e]);
+                st1<TI>(dk + o, dka[m][e]);
+                st1<TG>(dg + o, lsum[m][e]);
+            }
+        }
+    if (tid < valid) {
+        float db = 0.f;
+#pragma unroll
+        for (int j = 0; j < NB + NT; ++j) db += sdb[j][tid];
+        st1<TI>(static_cast<TI*>(a.dbeta) + bbase + (size_t)tid * a.H, db);
+    }
+}
+
+hipError_t launch_local_wide(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st) {
+    if (D != 128 || !in_bf16) return hipErrorInvalidValue;
+    if (g_bf16)
+        hipLaunchKernelGGL((kda_bwd_localw_kernel<128, uint16_t, uint16_t, 1>), dim3(nchunks), dim3(512), 0, st, a);
+    else
+        hipLaunchKernelGGL((kda_bwd_localw_kernel<128, uint16_t, float, 1>), dim3(nchunks), dim3(512), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace kda

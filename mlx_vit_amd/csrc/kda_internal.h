@@ -103,6 +103,9 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
 bool recur_epilogue_supported(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
+// the local adjoints at D = 128 (bf16 operands; kda_bwdw.hip): reads A_kk, the
+// diagonal-block inverses and V' from the workspace
+hipError_t launch_local_wide(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
 hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,
                         hipStream_t st);
 hipError_t launch_state_copy(const float* src, float* dst, size_t n, hipStream_t st);

@@ -2304,9 +2304,16 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
     KDA_RECUR_CASE(32)
     KDA_RECUR_CASE(64)
 #undef KDA_RECUR_CASE
-    // the backward (MODE 1) supports D <= 64
     if (D == 128 && mode == 0)
         return in_bf16 ? launch_recur_t<128, uint16_t, 0>(a, st) : launch_recur_t<128, float, 0>(a, st);
+    // the backward's state recompute at D = 128 (bf16): the generic kernel, which
+    // also writes V' for the D = 128 local-adjoint kernel; two workgroups per
+    // (batch, head), 64 dv columns each
+    if (D == 128 && mode == 1 && in_bf16) {
+        if (a.Vp == nullptr || a.KbT == nullptr) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((kda_recur_kernel<128, uint16_t, 1, 1, 2>), dim3(a.BH * 2), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     return hipErrorInvalidValue;
 }
 
@@ -2315,6 +2322,12 @@ bool recur_epilogue_supported(int D, int in_bf16) { return in_bf16 ? D == 64 : (
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st) {
     if (D == 32) return in_bf16 ? launch_dh_t<32, uint16_t>(a, st) : launch_dh_t<32, float>(a, st);
     if (D == 64) return in_bf16 ? launch_dh_t<64, uint16_t>(a, st) : launch_dh_t<64, float>(a, st);
+    // D = 128 (bf16): the generic kernel on the transposed slabs, one workgroup per (batch, head)
+    if (D == 128 && in_bf16) {
+        if (!a.AqkT || !a.QpT || !a.WT || !a.Kb) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1>), dim3(a.BH), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     return hipErrorInvalidValue;
 }
 

@@ -30,7 +30,7 @@ CHUNK = 64
 # kernels block at CHUNK whatever the caller's value.
 CHUNK_SIZES = (8, 16, 32, 64)
 FWD_HEAD_DIMS = (32, 64, 128)
-BWD_HEAD_DIMS = (32, 64)
+BWD_HEAD_DIMS = (32, 64, 128)   # 128: bf16 operands only (the library says so otherwise)
 
 _DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
 

@@ -155,16 +155,18 @@ def test_null_and_workspace_errors():
     rc = lib.kda_fwd(misaligned, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 64, 64, 1, 1, fake,
                      1 << 40, None)
     assert rc == _lib.KDA_E_INVALID
-    # the backward supports D in {32, 64}
-    rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 128, 64, 1, 1, fake, 1 << 40, None)
+    # the backward supports D in {32, 64, 128}, and D = 128 with bf16 operands only
+    rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 96, 64, 1, 1, fake, 1 << 40, None)
     assert rc == _lib.KDA_E_UNSUPPORTED and "backward" in _lib.last_error()
+    rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 128, 64, 0, 0, fake, 1 << 40, None)
+    assert rc == _lib.KDA_E_UNSUPPORTED and "bf16" in _lib.last_error()
 
 
 def test_training_pair_argument_errors():
     lib = _lib.load()
     fake = ctypes.c_void_p(1 << 20)
-    # training needs a backward-capable head dim, and the pass-2 workspace
-    rc = lib.kda_fwd_train(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 128, 64, 1, 1,
+    # training needs a backward-capable head dim and dtype, and the pass-2 workspace
+    rc = lib.kda_fwd_train(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 128, 64, 0, 0,
                            fake, 1 << 40, None)
     assert rc == _lib.KDA_E_UNSUPPORTED
     need = lib.kda_workspace_size(2, 1, 64, 1, 64, 64, 1)

@@ -22,7 +22,7 @@ def test_default_path_is_hip():
     (dict(chunk_size=48), "chunk_size"),
     (dict(channel_wise_decay=False, compute_path="hip_chunkwise_kda"), "channel-wise"),
     (dict(channel_wise_decay=True, compute_path="hip_chunkwise_gdn"), "scalar-alpha"),
-    (dict(head_dim=128), "head_dim"),
+    (dict(head_dim=80), "head_dim"),
     (dict(head_dim=48, requires_grad=False), "head_dim"),
 ])
 def test_construction_errors(kwargs, msg):
@@ -38,8 +38,9 @@ def test_reference_chunk_sizes_accepted(c):
     assert kda.KDARecurrence(num_heads=2, head_dim=64, chunk_size=c).chunk_size == c
 
 
-def test_inference_allows_head_dim_128():
+def test_head_dim_128_for_inference_and_training():
     assert kda.KDARecurrence(num_heads=16, head_dim=128, requires_grad=False).head_dim == 128
+    assert kda.KDARecurrence(num_heads=16, head_dim=128).head_dim == 128
 
 
 def test_unknown_path_at_call():

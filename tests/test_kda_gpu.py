@@ -312,6 +312,31 @@ def test_bwd_parity_bf16_cases(B, T, H, D, with_state, with_dsf, g_scale):
                 f"bwd bf16 {B},{T},{H},{D},{with_state},{with_dsf},{g_scale}")
 
 
+@pytest.mark.parametrize("B,T,H,D,with_state,with_dsf,g_scale", [
+    (1, 200, 2, 128, True, True, 0.1),     # ragged last chunk, state + final-state cotangent
+    (2, 64, 3, 128, False, False, 0.1),    # one full chunk, six (b, h)
+    (2, 1, 4, 128, True, False, 0.1),      # single token (eight sequences: one token's rel-L2 over
+                                           # 128 channels is dominated by single bf16 roundings)
+    (1, 130, 2, 128, True, False, 6.0),    # strong decay: every pair pair by pair
+    (1, 150, 2, 128, False, True, 1.0),    # strong but anchored decay
+])
+def test_bwd_parity_bf16_d128(B, T, H, D, with_state, with_dsf, g_scale):
+    """The backward at D = 128 (bf16): the generic state recompute (which writes
+    V'), the generic reverse carry, and the wide local-adjoint kernel reading
+    A_kk and the diagonal inverses from the prep."""
+    x = _inputs(B, T, H, D, torch.bfloat16, seed=24, with_state=with_state, grad=True, g_scale=g_scale)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9)) if with_dsf else None
+    _assert_all(_bwd_errors(x, torch.bfloat16, dsf), TOL[torch.bfloat16],
+                f"bwd bf16 D128 {B},{T},{H},{D},{with_state},{with_dsf},{g_scale}")
+
+
+def test_bwd_d128_fp32_gate():
+    """D = 128 with bf16 q/k/v/beta and a float32 g: dg comes back float32."""
+    x = _inputs(1, 100, 2, 128, torch.bfloat16, seed=25, with_state=True, grad=True)
+    x["g"] = x["g"].float()
+    _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], "bwd bf16 D128, fp32 g")
+
+
 def test_bwd_bf16_operands_fp32_gate():
     """bf16 q/k/v/beta with a float32 g: dg comes back float32."""
     x = _inputs(1, 200, 2, 64, torch.bfloat16, seed=15, with_state=True, grad=True)
@@ -355,6 +380,7 @@ def test_bwd_parity_config2_full():
     (2, 333, 3, 64, torch.bfloat16, 0.1),     # six chunks: the recurrences' LDS sets wrap
     (1, 65, 2, 32, torch.float32, 0.1),
     (1, 1, 1, 64, torch.float32, 0.1),
+    (1, 150, 2, 128, torch.bfloat16, 0.1),    # D = 128
 ])
 def test_training_pair_equals_standalone_calls(B, T, H, D, dtype, g_scale):
     """kda_fwd_train / kda_bwd_train reproduce kda_fwd / kda_bwd bit for bit."""
