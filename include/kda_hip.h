@@ -13,8 +13,8 @@
  * chunk is the reference's chunk_size: 8, 16, 32 or 64 (nope_gdn_mlx.py:676,
  * 4839-4856); the result does not depend on it (the reference's own
  * equivalence criterion, nope_gdn_mlx.py:4836-4914), and the kernels block at
- * 64 whatever its value.  D must be 32, 64 or 128 (forward) and 32 or 64
- * (backward).
+ * 64 whatever its value.  D must be 32, 64, 96 or 128 (96 runs the D = 128
+ * kernels on zero-padded copies in the workspace).
  * stream is a hipStream_t (NULL = default stream).  Every call is stream
  * ordered and allocates nothing: the caller passes a device workspace of at
  * least kda_workspace_size() bytes (256-byte aligned).
@@ -47,11 +47,14 @@ extern "C" {
 
 /* Workspace regions (see kda_workspace_offsets).  SEGX, SEGM and SEGS exist
  * only for the bf16 forward at D = 128 when it splits the sequence into
- * segments: per (b, h, segment) the segment's state map and start state. */
+ * segments: per (b, h, segment) the segment's state map and start state.
+ * PAD exists only at D = 96, which runs the D = 128 kernels on zero-padded
+ * copies: the other regions are then those of D = 128, and PAD (last) holds
+ * the padded operands and outputs. */
 enum kda_ws_region {
     KDA_WS_W = 0, KDA_WS_U, KDA_WS_QP, KDA_WS_QPT, KDA_WS_KB, KDA_WS_KBT, KDA_WS_WT,
     KDA_WS_AQK, KDA_WS_AQKT, KDA_WS_AKK, KDA_WS_TII, KDA_WS_EG, KDA_WS_H, KDA_WS_DH,
-    KDA_WS_VP, KDA_WS_DVP, KDA_WS_SEGX, KDA_WS_SEGM, KDA_WS_SEGS, KDA_WS_NREGIONS
+    KDA_WS_VP, KDA_WS_DVP, KDA_WS_SEGX, KDA_WS_SEGM, KDA_WS_SEGS, KDA_WS_PAD, KDA_WS_NREGIONS
 };
 
 /* ABI version of this header (bumped on any signature change). */
@@ -214,7 +217,9 @@ int kda_layer_producer_bwd(const void* xq, const void* xk, const void* xv, const
 /* Gated RMSNorm (RMSNormGated, nope_gdn_mlx.py:340-366, applied per head at
  * nope_gdn_mlx.py:880-885): y = o * rsqrt(mean_d(o^2) + eps) * w * sigmoid(z)
  * over each head's D channels.  o [rows, H, D] contiguous; z rows of ld_z;
- * y rows of ld_y; w [D] fp32.  D must be a power of two in [4, 256]. */
+ * y rows of ld_y; w [D] fp32.  D must be a multiple of 4 in [4, 256] and
+ * H * D at most 2048; a head takes D / 4 lanes rounded up to a power of two,
+ * and H heads must fit 8 waves of 64 lanes (D = 96: H <= 16). */
 int kda_layer_gated_rmsnorm_fwd(const void* o, const void* z, int64_t ld_z, const float* w,
                                 void* y, int64_t ld_y, int rows, int H, int D, float eps, int dtype,
                                 void* stream);

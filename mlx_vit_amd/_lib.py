@@ -11,7 +11,7 @@ import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkda_hip.so")
 
-ABI_VERSION = 2   # kda_abi_version() of the header this binding follows
+ABI_VERSION = 3   # kda_abi_version() of the header this binding follows
 
 KDA_OK = 0
 KDA_E_INVALID = -1
@@ -29,7 +29,7 @@ KDA_LAYER_PRODUCER = 0
 KDA_LAYER_RMSNORM = 1
 
 WS_REGIONS = ("W", "U", "Qp", "QpT", "Kb", "KbT", "WT", "Aqk", "AqkT", "Akk", "Tii", "eG",
-              "h", "dh", "Vp", "dVp", "SegX", "SegM", "SegS")
+              "h", "dh", "Vp", "dVp", "SegX", "SegM", "SegS", "Pad")
 
 # every function the header declares, with its ctypes signature
 _P, _I, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t

@@ -17,7 +17,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "libkda_hip.so")
-SOURCES = ["kda_fwd.hip", "kda_recur.hip", "kda_bwd.hip", "kda_layer.hip", "kda_api.hip", "kda_noalloc.hip", "kda_seg.hip", "kda_bwdw.hip"]
+SOURCES = ["kda_fwd.hip", "kda_recur.hip", "kda_bwd.hip", "kda_layer.hip", "kda_api.hip", "kda_noalloc.hip", "kda_seg.hip", "kda_bwdw.hip", "kda_pad.hip"]
 ARCH = os.environ.get("KDA_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU ops are disabled for device code; the host pass warns that

@@ -42,14 +42,9 @@ int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, b
     // (the chunked recurrence's result does not depend on the chunk size)
     if (chunk != 8 && chunk != 16 && chunk != 32 && chunk != kda::C)
         return fail(KDA_E_UNSUPPORTED, "chunk=%d: expected 8, 16, 32 or 64", chunk);
-    if (bwd) {
-        if (D != 32 && D != 64 && D != 128)
-            return fail(KDA_E_UNSUPPORTED, "D=%d: the backward supports D in {32, 64, 128}", D);
-        if (D == 128 && dtype != KDA_DTYPE_BF16)
-            return fail(KDA_E_UNSUPPORTED, "D=128: the backward supports bf16 operands (dtype=1), got dtype=%d", dtype);
-    } else if (D != 32 && D != 64 && D != 128) {
-        return fail(KDA_E_UNSUPPORTED, "D=%d: the forward supports D in {32, 64, 128}", D);
-    }
+    if (D != 32 && D != 64 && D != 96 && D != 128)
+        return fail(KDA_E_UNSUPPORTED, "D=%d: the %s supports D in {32, 64, 96, 128}", D,
+                    bwd ? "backward" : "forward");
     if (dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_BF16)
         return fail(KDA_E_UNSUPPORTED, "dtype=%d: expected 0 (fp32) or 1 (bf16)", dtype);
     if (g_dtype != KDA_DTYPE_F32 && g_dtype != KDA_DTYPE_BF16)
@@ -69,9 +64,61 @@ bool seg_forward(int pass, int B, int T, int H, int D, int dtype, int* nseg, int
     return *nseg > 1;
 }
 
+// D = 96 runs the D = 128 kernels on zero-padded copies (kda_pad.hip): the
+// workspace is the D = 128 layout followed by the PAD region, which holds the
+// padded operands and outputs of the pass in these slots.
+constexpr int PAD_D = 128;
+bool padded_head(int D) { return D == 96; }
+enum PadSlot { PS_Q, PS_K, PS_V, PS_G, PS_O, PS_DO, PS_DQ, PS_DK, PS_DV, PS_DG, PS_S0, PS_SF, PS_DSF, PS_DS0, PS_N };
+
+struct PadLayout {
+    size_t off[PS_N];
+    size_t total;
+};
+
+void make_pad_layout(int pass, int B, int T, int H, int dtype, PadLayout& P) {
+    const size_t tok = (size_t)B * T * H * PAD_D, es = (dtype == KDA_DTYPE_BF16) ? 2 : 4;
+    const size_t st = (size_t)B * H * PAD_D * PAD_D * 4;
+    size_t sz[PS_N] = {0};
+    // g and dg take 4 bytes an element: the workspace size does not depend on g_dtype
+    sz[PS_Q] = sz[PS_K] = sz[PS_V] = tok * es;
+    sz[PS_G] = tok * 4;
+    sz[PS_S0] = st;
+    if (pass != KDA_PASS_BWD) {
+        sz[PS_O] = tok * es;
+        sz[PS_SF] = st;
+    }
+    if (pass != KDA_PASS_FWD) {
+        sz[PS_DO] = sz[PS_DQ] = sz[PS_DK] = sz[PS_DV] = tok * es;
+        sz[PS_DG] = tok * 4;
+        sz[PS_DSF] = sz[PS_DS0] = st;
+    }
+    size_t cur = 0;
+    for (int i = 0; i < PS_N; ++i) {
+        P.off[i] = cur;
+        cur += (sz[i] + 255) & ~(size_t)255;
+    }
+    P.total = cur;
+}
+
 // Region sizes in bytes.  Operand slabs use the input dtype's element size;
 // eG, Akk and Tii are fp32.  Akk, Tii and V' exist for fp32 inputs only.
+void make_layout_at(int pass, int B, int T, int H, int D, int dtype, Layout& L);
+
 void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
+    if (!padded_head(D)) {
+        make_layout_at(pass, B, T, H, D, dtype, L);
+        L.off[KDA_WS_PAD] = -1;
+        return;
+    }
+    make_layout_at(pass, B, T, H, PAD_D, dtype, L);
+    PadLayout P;
+    make_pad_layout(pass, B, T, H, dtype, P);
+    L.off[KDA_WS_PAD] = (int64_t)L.total;
+    L.total += P.total;
+}
+
+void make_layout_at(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
     const size_t nc = (size_t)(T + kda::C - 1) / kda::C;
     const size_t N = (size_t)B * H * nc;
     const size_t es = (dtype == KDA_DTYPE_BF16) ? 2 : 4;
@@ -114,7 +161,7 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
         sz[KDA_WS_SEGS] = per;
     }
     size_t cur = 0;
-    for (int r = 0; r < KDA_WS_NREGIONS; ++r) {
+    for (int r = 0; r < KDA_WS_PAD; ++r) {
         if (sz[r] == 0) {
             L.off[r] = -1;
             continue;
@@ -326,12 +373,101 @@ struct Epilogue {
     int64_t ld_y;
 };
 
+int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+            void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
+            size_t ws_bytes, void* stream, bool prof, const Epilogue* epi);
+int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
+            const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
+            int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
+            void* stream);
+
+// The padded head dimension's slots in the workspace (the D = 128 layout
+// first, the PAD region after it), and the copies in and out of them.
+struct PadIo {
+    char* base;
+    PadLayout P;
+    size_t ntok, nbh;
+    int D, es, gs;
+    hipStream_t st;
+    void* slot(int i) const { return base + P.off[i]; }
+    float* fslot(int i) const { return reinterpret_cast<float*>(base + P.off[i]); }
+    // (B, T, H, D) rows in / out; element size es (or gs for g / dg)
+    hipError_t rows_in(const void* src, int i, int esz) const {
+        return kda::launch_resize(src, slot(i), ntok, 1, D, 1, PAD_D, esz, st);
+    }
+    hipError_t rows_out(int i, void* dst, int esz) const {
+        return kda::launch_resize(slot(i), dst, ntok, 1, PAD_D, 1, D, esz, st);
+    }
+    // (B, H, D, D) states in / out, fp32
+    hipError_t state_in(const float* src, int i) const {
+        return kda::launch_resize(src, slot(i), nbh, D, D, PAD_D, PAD_D, 4, st);
+    }
+    hipError_t state_out(int i, float* dst) const {
+        return kda::launch_resize(slot(i), dst, nbh, PAD_D, PAD_D, D, D, 4, st);
+    }
+};
+
+PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, void* ws, const Layout& L, hipStream_t st) {
+    PadIo io;
+    io.base = static_cast<char*>(ws) + L.off[KDA_WS_PAD];
+    make_pad_layout(pass, B, T, H, dtype, io.P);
+    io.ntok = (size_t)B * T * H;
+    io.nbh = (size_t)B * H;
+    io.D = D;
+    io.es = (dtype == KDA_DTYPE_BF16) ? 2 : 4;
+    io.gs = (g_dtype == KDA_DTYPE_BF16) ? 2 : 4;
+    io.st = st;
+    return io;
+}
+
+int run_fwd_padded(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+                   const float* s0, void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype,
+                   int g_dtype, void* ws, const Layout& L, hipStream_t st, bool prof) {
+    const PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
+    hipError_t e;
+    if ((e = io.rows_in(q, PS_Q, io.es)) != hipSuccess || (e = io.rows_in(k, PS_K, io.es)) != hipSuccess ||
+        (e = io.rows_in(v, PS_V, io.es)) != hipSuccess || (e = io.rows_in(g, PS_G, io.gs)) != hipSuccess ||
+        (s0 && (e = io.state_in(s0, PS_S0)) != hipSuccess))
+        return hip_fail(e, "kda_resize_kernel (pad)");
+    const int rc = run_fwd(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
+                           s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_O), s_final ? io.fslot(PS_SF) : nullptr, B, T,
+                           H, PAD_D, chunk, dtype, g_dtype, ws, (size_t)L.off[KDA_WS_PAD], st, prof, nullptr);
+    if (rc != KDA_OK) return rc;
+    if ((e = io.rows_out(PS_O, o, io.es)) != hipSuccess || (s_final && (e = io.state_out(PS_SF, s_final)) != hipSuccess))
+        return hip_fail(e, "kda_resize_kernel (crop)");
+    return ok();
+}
+
+int run_bwd_padded(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+                   const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
+                   void* dbeta, float* ds0, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* ws,
+                   const Layout& L, hipStream_t st) {
+    const PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
+    hipError_t e;
+    if ((e = io.rows_in(q, PS_Q, io.es)) != hipSuccess || (e = io.rows_in(k, PS_K, io.es)) != hipSuccess ||
+        (e = io.rows_in(v, PS_V, io.es)) != hipSuccess || (e = io.rows_in(g, PS_G, io.gs)) != hipSuccess ||
+        (e = io.rows_in(dout, PS_DO, io.es)) != hipSuccess || (s0 && (e = io.state_in(s0, PS_S0)) != hipSuccess) ||
+        (ds_final && (e = io.state_in(ds_final, PS_DSF)) != hipSuccess))
+        return hip_fail(e, "kda_resize_kernel (pad)");
+    const int rc = run_bwd(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
+                           s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_DO), ds_final ? io.fslot(PS_DSF) : nullptr,
+                           io.slot(PS_DQ), io.slot(PS_DK), io.slot(PS_DV), io.slot(PS_DG), dbeta,
+                           ds0 ? io.fslot(PS_DS0) : nullptr, B, T, H, PAD_D, chunk, dtype, g_dtype, ws,
+                           (size_t)L.off[KDA_WS_PAD], st);
+    if (rc != KDA_OK) return rc;
+    if ((e = io.rows_out(PS_DQ, dq, io.es)) != hipSuccess || (e = io.rows_out(PS_DK, dk, io.es)) != hipSuccess ||
+        (e = io.rows_out(PS_DV, dv, io.es)) != hipSuccess || (e = io.rows_out(PS_DG, dg, io.gs)) != hipSuccess ||
+        (ds0 && (e = io.state_out(PS_DS0, ds0)) != hipSuccess))
+        return hip_fail(e, "kda_resize_kernel (crop)");
+    return ok();
+}
+
 // The forward's launch sequence (pass 0) or the training forward's (pass 2).
 // prof = false: no launch timing, so the profiler's event pool never grows (for
 // the entry point that must not allocate).
 int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
-            size_t ws_bytes, void* stream, bool prof = true, const Epilogue* epi = nullptr) {
+            size_t ws_bytes, void* stream, bool prof, const Epilogue* epi) {
     int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, pass == KDA_PASS_TRAIN);
     if (rc) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -349,6 +485,11 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     Layout L;
     make_layout(pass, B, T, H, D, dtype, L);
     if ((rc = check_workspace(workspace, ws_bytes, L))) return rc;
+    if (padded_head(D)) {
+        if (epi) return fail(KDA_E_UNSUPPORTED, "D=%d has no fused epilogue", D);
+        return run_fwd_padded(pass, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
+                              L, st, prof);
+    }
 
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
@@ -426,6 +567,9 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
     Layout L;
     make_layout(pass, B, T, H, D, dtype, L);
     if ((rc = check_workspace(workspace, ws_bytes, L))) return rc;
+    if (padded_head(D))
+        return run_bwd_padded(pass, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D,
+                              chunk, dtype, g_dtype, workspace, L, st);
 
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
@@ -506,7 +650,7 @@ int api_fwd_on_workspace(const void* q, const void* k, const void* v, const void
                          const float* s0, void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype,
                          int g_dtype, void* workspace, size_t ws_bytes, void* stream) {
     return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
-                   ws_bytes, stream, /*prof=*/false);
+                   ws_bytes, stream, /*prof=*/false, nullptr);
 }
 
 }  // namespace kda
@@ -516,7 +660,7 @@ int api_fwd_on_workspace(const void* q, const void* k, const void* v, const void
 // ----------------------------------------------------------------------------
 extern "C" {
 
-int kda_abi_version(void) { return 2; }
+int kda_abi_version(void) { return 3; }
 
 const char* kda_last_error(void) { return g_err.c_str(); }
 
@@ -547,14 +691,14 @@ int kda_fwd(const void* q, const void* k, const void* v, const void* g, const vo
             float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
             size_t ws_bytes, void* stream) {
     return run_fwd(KDA_PASS_FWD, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
-                   ws_bytes, stream);
+                   ws_bytes, stream, true, nullptr);
 }
 
 int kda_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
                   void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
                   void* workspace, size_t ws_bytes, void* stream) {
     return run_fwd(KDA_PASS_TRAIN, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
-                   ws_bytes, stream);
+                   ws_bytes, stream, true, nullptr);
 }
 
 int kda_fwd_gated(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
@@ -682,9 +826,11 @@ int check_norm(int rows, int H, int D, int dtype) {
     if (rows < 0 || H < 1 || D < 1) return fail(KDA_E_INVALID, "rows=%d H=%d D=%d", rows, H, D);
     if (dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_BF16)
         return fail(KDA_E_UNSUPPORTED, "dtype=%d: expected 0 (fp32) or 1 (bf16)", dtype);
-    if (D < 4 || D > 256 || (D & (D - 1)) != 0)
-        return fail(KDA_E_UNSUPPORTED, "D=%d: must be a power of two in [4, 256]", D);
+    if (D < 4 || D > 256 || D % 4 != 0)
+        return fail(KDA_E_UNSUPPORTED, "D=%d: must be a multiple of 4 in [4, 256]", D);
     if ((int64_t)H * D > 2048) return fail(KDA_E_UNSUPPORTED, "H*D=%d exceeds 2048", H * D);
+    if (kda::norm_waves(H, D) > 8)
+        return fail(KDA_E_UNSUPPORTED, "H=%d heads of D=%d: more than 512 threads a row", H, D);
     return KDA_OK;
 }
 

@@ -458,12 +458,21 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     }
 }
 
+// bf16 operands: bf16 MFMA products (PREC 1); fp32: split-bf16 products
+// accurate to fp32 (PREC 3)
 hipError_t launch_local_wide(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st) {
-    if (D != 128 || !in_bf16) return hipErrorInvalidValue;
-    if (g_bf16)
-        hipLaunchKernelGGL((kda_bwd_localw_kernel<128, uint16_t, uint16_t, 1>), dim3(nchunks), dim3(512), 0, st, a);
-    else
-        hipLaunchKernelGGL((kda_bwd_localw_kernel<128, uint16_t, float, 1>), dim3(nchunks), dim3(512), 0, st, a);
+    if (D != 128) return hipErrorInvalidValue;
+    if (in_bf16) {
+        if (g_bf16)
+            hipLaunchKernelGGL((kda_bwd_localw_kernel<128, uint16_t, uint16_t, 1>), dim3(nchunks), dim3(512), 0, st, a);
+        else
+            hipLaunchKernelGGL((kda_bwd_localw_kernel<128, uint16_t, float, 1>), dim3(nchunks), dim3(512), 0, st, a);
+    } else {
+        if (g_bf16)
+            hipLaunchKernelGGL((kda_bwd_localw_kernel<128, float, uint16_t, 3>), dim3(nchunks), dim3(512), 0, st, a);
+        else
+            hipLaunchKernelGGL((kda_bwd_localw_kernel<128, float, float, 3>), dim3(nchunks), dim3(512), 0, st, a);
+    }
     return hipGetLastError();
 }
 

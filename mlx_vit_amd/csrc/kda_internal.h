@@ -18,6 +18,7 @@
 //                                      [dk][dv] orientation
 #pragma once
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <type_traits>
 #include "kda_chunk.h"
 
@@ -103,12 +104,16 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
 bool recur_epilogue_supported(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
-// the local adjoints at D = 128 (bf16 operands; kda_bwdw.hip): reads A_kk, the
-// diagonal-block inverses and V' from the workspace
+// the local adjoints at D = 128 (kda_bwdw.hip): reads A_kk, the diagonal-block
+// inverses and V' from the workspace
 hipError_t launch_local_wide(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
 hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,
                         hipStream_t st);
 hipError_t launch_state_copy(const float* src, float* dst, size_t n, hipStream_t st);
+// n matrices of rs x cs elements (esize bytes each) into rd x cd: the common
+// top-left block copied, the rest zero (kda_pad.hip)
+hipError_t launch_resize(const void* src, void* dst, size_t n, int rs, int cs, int rd, int cd, int esize,
+                         hipStream_t st);
 
 // C-ABI helpers of kda_api.hip for the other C-ABI translation units (the
 // allocation-free forward): the error setters behind kda_last_error(); the
@@ -154,6 +159,9 @@ size_t producer_ws_floats(int B, int T, int H, int D);
 size_t rmsnorm_ws_floats(int rows, int H, int D);
 int producer_partials(int B, int T);
 int rmsnorm_partials(int rows);
+// waves of a norm workgroup: a head takes D / 4 lanes rounded up to a power of
+// two (at most 8 waves: the kernels are bounded at 512 threads)
+int norm_waves(int H, int D);
 hipError_t launch_producer_fwd(const ProdArgs& a, int in_bf16, int g_bf16, hipStream_t st);
 hipError_t launch_producer_bwd(const ProdArgs& a, int in_bf16, int g_bf16, hipStream_t st);
 hipError_t launch_rmsnorm_fwd(const NormArgs& a, int in_bf16, hipStream_t st);

@@ -529,11 +529,34 @@ __global__ __launch_bounds__(256) void producer_finish_kernel(const ProdArgs a) 
 }
 
 // ---------------------------------------------------------------- gated RMSNorm
+// Lanes of the norm kernels: a head takes P lanes of 4 channels, P = D / 4
+// rounded up to a power of two, so that its sums are butterflies over an
+// aligned lane group; a wave holds 64 / P heads.  For D a power of two this is
+// the channel-contiguous map of Lanes (256 channels a wave).  Lanes past a
+// head's D / 4 (D = 96: 8 of 32) are idle: they address channel 0 and add
+// zero to the sums.
+__device__ __forceinline__ int norm_lanes_per_head(int D) {
+    int p = 1;
+    while (4 * p < D) p <<= 1;
+    return p;
+}
+struct NormLanes {
+    int HD, cc, P;
+    bool live;
+    __device__ NormLanes(int H, int D) {
+        HD = H * D;
+        P = norm_lanes_per_head(D);
+        const int lane = threadIdx.x & 63, h = (threadIdx.x >> 6) * (64 / P) + lane / P, c4 = (lane % P) * 4;
+        live = h < H && c4 < D;
+        cc = live ? h * D + c4 : 0;
+    }
+};
+
 template <typename ST>
 __global__ __launch_bounds__(512) void rmsnorm_fwd_kernel(const NormArgs a) {
-    const Lanes L(a.H, a.D);
+    const NormLanes L(a.H, a.D);
     const int r0 = xcd_remap(blockIdx.x, gridDim.x) * NR;
-    const int gl = a.D / 4;
+    const int gl = L.P;
     const float4 wv = *reinterpret_cast<const float4*>(a.w + L.cc % a.D);
     const float wt[4] = {wv.x, wv.y, wv.z, wv.w};
     const float invD = 1.f / (float)a.D;
@@ -545,6 +568,7 @@ __global__ __launch_bounds__(512) void rmsnorm_fwd_kernel(const NormArgs a) {
         const size_t r = min(r0 + j, a.rows - 1);
         Vec4<ST>::ld(o + r * L.HD + L.cc, ov[j]);
         Vec4<ST>::ld(z + r * a.ld_z + L.cc, zv[j]);
+        if (!L.live) ov[j][0] = ov[j][1] = ov[j][2] = ov[j][3] = 0.f;
     }
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
@@ -564,9 +588,9 @@ __global__ __launch_bounds__(512) void rmsnorm_fwd_kernel(const NormArgs a) {
 //   dn = dy w s,  do = r (dn - n mean(dn n)),  dz = dy n w s (1 - s),  dw += dy n s
 template <typename ST>
 __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(const NormArgs a) {
-    const Lanes L(a.H, a.D);
+    const NormLanes L(a.H, a.D);
     const int wg = xcd_remap(blockIdx.x, gridDim.x);
-    const int gl = a.D / 4;
+    const int gl = L.P;
     const float4 wv = *reinterpret_cast<const float4*>(a.w + L.cc % a.D);
     const float wt[4] = {wv.x, wv.y, wv.z, wv.w};
     const float invD = 1.f / (float)a.D;
@@ -584,6 +608,7 @@ __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(const NormArgs a) {
             Vec4<ST>::ld(o + r * L.HD + L.cc, ov[j]);
             Vec4<ST>::ld(z + r * a.ld_z + L.cc, zv[j]);
             Vec4<ST>::ld(dyp + r * a.ld_dy + L.cc, gv[j]);
+            if (!L.live) ov[j][0] = ov[j][1] = ov[j][2] = ov[j][3] = 0.f;
         }
 #pragma unroll
         for (int j = 0; j < NRB; ++j) {
@@ -651,6 +676,14 @@ void launch_colsum(const float* part, int P, int N, float* out, float* stage, hi
 
 }  // namespace
 
+// waves of the norm kernels (NormLanes): 64 / P heads a wave
+int norm_waves(int H, int D) {
+    int p = 1;
+    while (4 * p < D) p <<= 1;
+    const int hpw = 64 / p;
+    return (H + hpw - 1) / hpw;
+}
+
 int producer_partials(int B, int T) { return B * ((T + BR * BNS - 1) / (BR * BNS)); }
 size_t producer_ws_floats(int B, int T, int H, int D) {
     const int P = producer_partials(B, T), N = NPV * H * D;
@@ -694,7 +727,7 @@ hipError_t launch_producer_bwd(const ProdArgs& a, int in_bf16, int g_bf16, hipSt
 }
 
 hipError_t launch_rmsnorm_fwd(const NormArgs& a, int in_bf16, hipStream_t st) {
-    const dim3 grid((a.rows + NR - 1) / NR), block(64 * nwaves(a.H, a.D));
+    const dim3 grid((a.rows + NR - 1) / NR), block(64 * norm_waves(a.H, a.D));
     if (in_bf16) rmsnorm_fwd_kernel<uint16_t><<<grid, block, 0, st>>>(a);
     else rmsnorm_fwd_kernel<float><<<grid, block, 0, st>>>(a);
     return hipGetLastError();
@@ -703,7 +736,7 @@ hipError_t launch_rmsnorm_fwd(const NormArgs& a, int in_bf16, hipStream_t st) {
 hipError_t launch_rmsnorm_bwd(const NormArgs& a, int in_bf16, hipStream_t st) {
     const int P = rmsnorm_partials(a.rows);
     const int HD = a.H * a.D;
-    const dim3 grid(P), block(64 * nwaves(a.H, a.D));
+    const dim3 grid(P), block(64 * norm_waves(a.H, a.D));
     if (P > 0) {
         if (in_bf16) rmsnorm_bwd_kernel<uint16_t><<<grid, block, 0, st>>>(a);
         else rmsnorm_bwd_kernel<float><<<grid, block, 0, st>>>(a);

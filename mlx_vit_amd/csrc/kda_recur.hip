@@ -72,19 +72,22 @@ struct RecurLayout {
     static constexpr int BYTES = STG_OFF + NBUF * STG_BYTES;
 };
 
-template <int D, typename ST>
+// A workgroup owns DC = D / CS columns of dS (its dO, dh and dV' tiles are DC
+// wide); the operand slabs Aqk^T, Kb, Qp^T and W^T are whole.
+template <int D, typename ST, int CS = 1>
 struct DhLayout {
+    static constexpr int DC = D / CS;
     static constexpr int PS = 16 / (int)sizeof(ST);
-    static constexpr int LDR = D + PS, LDC = C + PS;
+    static constexpr int LDR = D + PS, LDC = C + PS, LDU = DC + PS;
     static constexpr int AQKT_OFF = 0;
     static constexpr int KB_OFF = AQKT_OFF + C * LDC;
     static constexpr int QPT_OFF = KB_OFF + C * LDR;
     static constexpr int WT_OFF = QPT_OFF + D * LDC;
     static constexpr int DO_OFF = WT_OFF + D * LDC;
-    static constexpr int SET_ELEMS = DO_OFF + C * LDR;
+    static constexpr int SET_ELEMS = DO_OFF + C * LDU;
     static constexpr int EG_BYTE = SET_ELEMS * (int)sizeof(ST);
     static constexpr int SET_BYTES = (EG_BYTE + D * 4 + 15) & ~15;
-    static constexpr int STG_ELEMS = D * LDR + C * LDR;      // dh, dV'
+    static constexpr int STG_ELEMS = D * LDU + C * LDU;      // dh, dV'
     static constexpr int STG_BYTES = (STG_ELEMS * (int)sizeof(ST) + 15) & ~15;
     static constexpr int NBUF = (2 * SET_BYTES + 2 * STG_BYTES <= 160 * 1024) ? 2 : 1;
     static constexpr int STG_OFF = NBUF * SET_BYTES;
@@ -347,14 +350,21 @@ __global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
 // ----------------------------------------------------------------------------
 // reverse state recurrence (same pipeline, chunks in reverse order)
 // ----------------------------------------------------------------------------
-template <int D, typename ST, int PREC>
+// CS > 1: CS workgroups per (batch, head), DC = D / CS columns each; every A
+// fragment is then used by one column tile of a wave, so fragments are read
+// from LDS where they are used instead of being held for the whole chunk (at
+// D = 128 in fp32 the whole set would take about 430 VGPRs).
+template <int D, typename ST, int PREC, int CS = 1>
 __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
-    using Lay = DhLayout<D, ST>;
-    constexpr int NT = D / BS, TPW = (NT + 3) / 4, LDR = Lay::LDR, LDC = Lay::LDC;
+    using Lay = DhLayout<D, ST, CS>;
+    constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, TPW = (NTW + 3) / 4;
+    constexpr int LDR = Lay::LDR, LDC = Lay::LDC, LDU = Lay::LDU;
+    constexpr bool HOLD = CS == 1;   // A fragments held in registers for the chunk
+    static_assert(Lay::BYTES <= 160 * 1024, "reverse recurrence LDS");
     __shared__ __align__(16) unsigned char smem[Lay::BYTES];
 
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
-    const int bh = blockIdx.x, b = bh / a.H, h = bh - b * a.H;
+    const int bh = blockIdx.x / CS, c0 = (blockIdx.x - bh * CS) * DC, b = bh / a.H, h = bh - b * a.H;
     const ST* gAqkT = static_cast<const ST*>(a.AqkT);
     const ST* gKb = static_cast<const ST*>(a.Kb);
     const ST* gQpT = static_cast<const ST*>(a.QpT);
@@ -365,11 +375,12 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
     auto seg = [&](int buf) __attribute__((always_inline)) { return reinterpret_cast<float*>(smem + buf * Lay::SET_BYTES + Lay::EG_BYTE); };
     auto stg = [&](int sb) __attribute__((always_inline)) { return reinterpret_cast<ST*>(smem + Lay::STG_OFF + sb * Lay::STG_BYTES); };
 
+    // column tile w + 4 j of the workgroup's DC columns; col: within the slice
     bool has[TPW];
     int col[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
-        has[j] = (NT % 4 == 0) || (w + 4 * j) < NT;
+        has[j] = (NTW % 4 == 0) || (w + 4 * j) < NTW;
         col[j] = (w + 4 * j) * BS + r16;
     }
 
@@ -381,13 +392,14 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
             dS[j][mt] = zero4();
             if (has[j] && a.dsf) {
                 const float4 x =
-                    *reinterpret_cast<const float4*>(a.dsf + ((size_t)bh * D + col[j]) * D + BS * mt + 4 * g4);
+                    *reinterpret_cast<const float4*>(a.dsf + ((size_t)bh * D + c0 + col[j]) * D + BS * mt + 4 * g4);
                 dS[j][mt] = f32x4{x.x, x.y, x.z, x.w};
             }
         }
 
     Tile<ST, C, C> pAqkT;
-    Tile<ST, C, D> pKb, pdO;
+    Tile<ST, C, D> pKb;
+    Tile<ST, C, DC> pdO;
     Tile<ST, D, C> pQpT, pWT;
     Tile<float, 1, D> pEg;
 
@@ -399,21 +411,21 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
         pQpT.load(gQpT + ch * C * D, C);
         pWT.load(gWT + ch * C * D, C);
         pEg.load(a.eG + ch * D, D);
-        pdO.load(gdO + (((size_t)b * a.T + t0) * a.H + h) * D, (size_t)a.H * D, valid);
+        pdO.load(gdO + (((size_t)b * a.T + t0) * a.H + h) * D + c0, (size_t)a.H * D, valid);
     };
     auto commit = [&](int buf) __attribute__((always_inline)) {
         pAqkT.store(set(buf) + Lay::AQKT_OFF, LDC);
         pKb.store(set(buf) + Lay::KB_OFF, LDR);
         pQpT.store(set(buf) + Lay::QPT_OFF, LDC);
         pWT.store(set(buf) + Lay::WT_OFF, LDC);
-        pdO.store(set(buf) + Lay::DO_OFF, LDR);
+        pdO.store(set(buf) + Lay::DO_OFF, LDU);
         pEg.store(seg(buf), D);
     };
     auto flush = [&](int it, int n) __attribute__((always_inline)) {   // stores of chunk n (loop step it)
         const ST* sst = stg((Lay::NBUF == 2) ? (it & 1) : 0);
         const size_t ch = (size_t)bh * a.nc + n;
-        tile_out<ST, D, D>(sst, LDR, static_cast<ST*>(a.dh) + ch * D * D, D, D);
-        tile_out<ST, C, D>(sst + D * LDR, LDR, static_cast<ST*>(a.dVp) + ch * C * D, D, C);
+        tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
+        tile_out<ST, C, DC>(sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
     };
 
     issue(a.nc - 1);
@@ -433,23 +445,38 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
         const ST* sdO = set(buf) + Lay::DO_OFF;
         const float* seG = seg(buf);
         ST* dhst = stg(buf);
-        ST* dvst = dhst + D * LDR;
+        ST* dvst = dhst + D * LDU;
 
-        Frag8 Aat[NB][C / 32], Akb[NB][D / 32], Aqt[NT][C / 32], Awt[NT][C / 32];
+        Frag8 Aat[HOLD ? NB : 1][C / 32], Akb[HOLD ? NB : 1][D / 32], Aqt[HOLD ? NT : 1][C / 32],
+            Awt[HOLD ? NT : 1][C / 32];
+        if constexpr (HOLD) {
 #pragma unroll
-        for (int m = 0; m < NB; ++m) {
+            for (int m = 0; m < NB; ++m) {
 #pragma unroll
-            for (int ks = m / 2; ks < C / 32; ++ks) Aat[m][ks] = ldfrag<PREC, ST>(sAqkT, LDC, BS * m, 32 * ks);
+                for (int ks = m / 2; ks < C / 32; ++ks) Aat[m][ks] = ldfrag<PREC, ST>(sAqkT, LDC, BS * m, 32 * ks);
 #pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) Akb[m][ks] = ldfrag<PREC, ST>(sKb, LDR, BS * m, 32 * ks);
-        }
-#pragma unroll
-        for (int mt = 0; mt < NT; ++mt)
-#pragma unroll
-            for (int ks = 0; ks < C / 32; ++ks) {
-                Aqt[mt][ks] = ldfrag<PREC, ST>(sQpT, LDC, BS * mt, 32 * ks);
-                Awt[mt][ks] = ldfrag<PREC, ST>(sWT, LDC, BS * mt, 32 * ks);
+                for (int ks = 0; ks < D / 32; ++ks) Akb[m][ks] = ldfrag<PREC, ST>(sKb, LDR, BS * m, 32 * ks);
             }
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ++ks) {
+                    Aqt[mt][ks] = ldfrag<PREC, ST>(sQpT, LDC, BS * mt, 32 * ks);
+                    Awt[mt][ks] = ldfrag<PREC, ST>(sWT, LDC, BS * mt, 32 * ks);
+                }
+        }
+        auto fAat = [&](int m, int ks) __attribute__((always_inline)) {
+            if constexpr (HOLD) return Aat[m][ks]; else return ldfrag<PREC, ST>(sAqkT, LDC, BS * m, 32 * ks);
+        };
+        auto fAkb = [&](int m, int ks) __attribute__((always_inline)) {
+            if constexpr (HOLD) return Akb[m][ks]; else return ldfrag<PREC, ST>(sKb, LDR, BS * m, 32 * ks);
+        };
+        auto fAqt = [&](int mt, int ks) __attribute__((always_inline)) {
+            if constexpr (HOLD) return Aqt[mt][ks]; else return ldfrag<PREC, ST>(sQpT, LDC, BS * mt, 32 * ks);
+        };
+        auto fAwt = [&](int mt, int ks) __attribute__((always_inline)) {
+            if constexpr (HOLD) return Awt[mt][ks]; else return ldfrag<PREC, ST>(sWT, LDC, BS * mt, 32 * ks);
+        };
         Frag8 Bo[TPW][C / 32], Bs[TPW][D / 32];
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
@@ -457,7 +484,8 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
 #pragma unroll
             for (int m = 0; m < NB; ++m)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dO[m][e] = ld1<ST>(sdO + (BS * m + 4 * g4 + e) * LDR + col[j]);
+                for (int e = 0; e < 4; ++e)
+                    dO[m][e] = has[j] ? ld1<ST>(sdO + (BS * m + 4 * g4 + e) * LDU + col[j]) : 0.f;
 #pragma unroll
             for (int ks = 0; ks < C / 32; ++ks) Bo[j][ks] = accfrag<PREC>(dO[2 * ks], dO[2 * ks + 1]);
 #pragma unroll
@@ -466,7 +494,7 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) st1<ST>(dhst + (BS * mt + 4 * g4 + e) * LDR + col[j], dS[j][mt][e]);
+                    for (int e = 0; e < 4; ++e) st1<ST>(dhst + (BS * mt + 4 * g4 + e) * LDU + col[j], dS[j][mt][e]);
         }
         __builtin_amdgcn_sched_barrier(0);
 
@@ -479,9 +507,9 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
                 dV[j][m] = zero4();
                 if (has[j]) {
 #pragma unroll
-                    for (int ks = m / 2; ks < C / 32; ++ks) dV[j][m] = mma<PREC>(Aat[m][ks], Bo[j][ks], dV[j][m]);
+                    for (int ks = m / 2; ks < C / 32; ++ks) dV[j][m] = mma<PREC>(fAat(m, ks), Bo[j][ks], dV[j][m]);
 #pragma unroll
-                    for (int ks = 0; ks < D / 32; ++ks) dV[j][m] = mma<PREC>(Akb[m][ks], Bs[j][ks], dV[j][m]);
+                    for (int ks = 0; ks < D / 32; ++ks) dV[j][m] = mma<PREC>(fAkb(m, ks), Bs[j][ks], dV[j][m]);
                 }
             }
         // dS <- diag(e^G) dS + Qp^T dO - W^T dV'
@@ -500,8 +528,8 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
                 if (has[j]) {
 #pragma unroll
                     for (int ks = 0; ks < C / 32; ++ks) {
-                        dS[j][mt] = mma<PREC>(Aqt[mt][ks], Bo[j][ks], dS[j][mt]);
-                        dS[j][mt] = mma<PREC>(Awt[mt][ks], Bvn[j][ks], dS[j][mt]);
+                        dS[j][mt] = mma<PREC>(fAqt(mt, ks), Bo[j][ks], dS[j][mt]);
+                        dS[j][mt] = mma<PREC>(fAwt(mt, ks), Bvn[j][ks], dS[j][mt]);
                     }
                 }
             }
@@ -512,7 +540,7 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
 #pragma unroll
                 for (int m = 0; m < NB; ++m)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) st1<ST>(dvst + (BS * m + 4 * g4 + e) * LDR + col[j], dV[j][m][e]);
+                    for (int e = 0; e < 4; ++e) st1<ST>(dvst + (BS * m + 4 * g4 + e) * LDU + col[j], dV[j][m][e]);
 
         order_after_compute();
         if constexpr (Lay::NBUF == 2) {
@@ -533,7 +561,7 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
             if (has[j])
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt)
-                    *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + col[j]) * D + BS * mt + 4 * g4) =
+                    *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + c0 + col[j]) * D + BS * mt + 4 * g4) =
                         make_float4(dS[j][mt][0], dS[j][mt][1], dS[j][mt][2], dS[j][mt][3]);
     }
 }
@@ -2306,12 +2334,15 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
 #undef KDA_RECUR_CASE
     if (D == 128 && mode == 0)
         return in_bf16 ? launch_recur_t<128, uint16_t, 0>(a, st) : launch_recur_t<128, float, 0>(a, st);
-    // the backward's state recompute at D = 128 (bf16): the generic kernel, which
-    // also writes V' for the D = 128 local-adjoint kernel; two workgroups per
+    // the backward's state recompute at D = 128: the generic kernel, which also
+    // writes V' for the D = 128 local-adjoint kernel; two workgroups per
     // (batch, head), 64 dv columns each
-    if (D == 128 && mode == 1 && in_bf16) {
+    if (D == 128 && mode == 1) {
         if (a.Vp == nullptr || a.KbT == nullptr) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((kda_recur_kernel<128, uint16_t, 1, 1, 2>), dim3(a.BH * 2), dim3(256), 0, st, a);
+        if (in_bf16)
+            hipLaunchKernelGGL((kda_recur_kernel<128, uint16_t, 1, 1, 2>), dim3(a.BH * 2), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((kda_recur_kernel<128, float, 3, 1, 2>), dim3(a.BH * 2), dim3(256), 0, st, a);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;
@@ -2322,10 +2353,15 @@ bool recur_epilogue_supported(int D, int in_bf16) { return in_bf16 ? D == 64 : (
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st) {
     if (D == 32) return in_bf16 ? launch_dh_t<32, uint16_t>(a, st) : launch_dh_t<32, float>(a, st);
     if (D == 64) return in_bf16 ? launch_dh_t<64, uint16_t>(a, st) : launch_dh_t<64, float>(a, st);
-    // D = 128 (bf16): the generic kernel on the transposed slabs, one workgroup per (batch, head)
-    if (D == 128 && in_bf16) {
+    // D = 128: the generic kernel on the transposed slabs; bf16: one workgroup
+    // per (batch, head); fp32: four, 32 dS columns each (one operand set and its
+    // staging fit the LDS only at that width)
+    if (D == 128) {
         if (!a.AqkT || !a.QpT || !a.WT || !a.Kb) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1>), dim3(a.BH), dim3(256), 0, st, a);
+        if (in_bf16)
+            hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1>), dim3(a.BH), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((kda_dh_kernel<128, float, 3, 4>), dim3(a.BH * 4), dim3(256), 0, st, a);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;

@@ -344,6 +344,12 @@ class GatedDeltaLayer(nn.Module):
                              f"got head_dim={head_dim}")
         if num_heads * head_dim > 2048:
             raise ValueError(f"num_heads * head_dim = {num_heads * head_dim} exceeds the producer's 2048")
+        # the output norm gives a head D / 4 lanes rounded up to a power of two,
+        # and a row at most 8 waves of 64 lanes
+        lanes = 1 << max(0, (head_dim // 4 - 1).bit_length())
+        if -(-num_heads // max(1, 64 // lanes)) > 8:
+            raise ValueError(f"num_heads={num_heads} heads of head_dim={head_dim} exceed the output norm's "
+                             f"512 threads a row")
         self.recurrence = KDARecurrence(num_heads, head_dim, chunk_size, channel_wise_decay, compute_path,
                                         requires_grad=head_dim in BWD_HEAD_DIMS)
         self.hidden_size = hidden_size

@@ -91,10 +91,15 @@ def gated_rms_norm(x: Tensor, weight: Tensor, gate: Tensor, eps: float) -> Tenso
 
 
 def layer_forward(params: Dict[str, Tensor], x: Tensor, H: int, D: int, state: Optional[Tensor] = None,
-                  allow_neg_eigval: bool = False, eps: float = 1e-5) -> Tuple[Tensor, Tensor]:
-    """nope_gdn_mlx.py:775-885 with the 'compiled' recurrence: (out, new_state)."""
+                  allow_neg_eigval: bool = False, eps: float = 1e-5,
+                  keep: Optional[dict] = None) -> Tuple[Tensor, Tensor]:
+    """nope_gdn_mlx.py:775-885 with the 'compiled' recurrence: (out, new_state).
+    keep: if a dict, receives the decay gate g (B, L, H, D) of the graph, so a
+    caller can read its gradient."""
     B, L, _ = x.shape
     q, k, v, g, beta = producer(params, x, H, D, allow_neg_eigval)
+    if keep is not None:
+        keep["g"] = g
     if "a_proj.weight" in params:   # g is alpha (B, L, H)
         o, new_state = loop_compiled_gdn(q, k, v, g, beta, state, compute_dtype=x.dtype)
     else:

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().kda_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.load().kda_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_workspace_sizes():
@@ -92,13 +92,39 @@ def test_layer_workspace_sizes(B, T, H, D):
 def test_workspace_offsets_disjoint():
     lib = _lib.load()
     for pass_, shape in ((0, (2, 300, 3, 64)), (1, (2, 300, 3, 64)), (2, (2, 300, 3, 64)),
-                         (0, (1, 2000, 2, 128)), (0, (1, 32768, 16, 128))):
+                         (0, (1, 2000, 2, 128)), (0, (1, 32768, 16, 128)), (0, (2, 1568, 8, 96)),
+                         (1, (2, 1568, 8, 96)), (2, (1, 70, 3, 96))):
         arr = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
         assert lib.kda_workspace_offsets(pass_, *shape, 64, 1, arr) == 0
         offs = sorted(o for o in arr if o >= 0)
         assert offs[0] == 0 and all(b - a >= 256 and b % 256 == 0 for a, b in zip(offs, offs[1:]))
         total = lib.kda_workspace_size(pass_, *shape, 64, 1)
         assert offs[-1] < total
+
+
+@pytest.mark.parametrize("pass_,dtype", [(0, 0), (0, 1), (1, 0), (1, 1), (2, 0), (2, 1)])
+def test_d96_workspace_is_d128_plus_pad(pass_, dtype):
+    """D = 96 runs the D = 128 kernels on zero-padded copies: its regions are
+    those of D = 128 at the same offsets, followed by the PAD region (padded
+    q, k, v, g, the pass's outputs or cotangents and the padded states)."""
+    lib = _lib.load()
+    B, T, H = 2, 300, 3
+    a96 = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
+    a128 = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
+    assert lib.kda_workspace_offsets(pass_, B, T, H, 96, 64, dtype, a96) == 0
+    assert lib.kda_workspace_offsets(pass_, B, T, H, 128, 64, dtype, a128) == 0
+    o96, o128 = dict(zip(_lib.WS_REGIONS, a96)), dict(zip(_lib.WS_REGIONS, a128))
+    assert o128["Pad"] == -1
+    assert all(o96[r] == o128[r] for r in _lib.WS_REGIONS if r != "Pad")
+    s128 = lib.kda_workspace_size(pass_, B, T, H, 128, 64, dtype)
+    assert o96["Pad"] == s128
+    tok, es, st = B * T * H * 128, 2 if dtype else 4, B * H * 128 * 128 * 4
+    # q, k, v (es) and g (4 bytes) and s0 always; o and s_final for the forward
+    # passes, dout, dq, dk, dv, dg, ds_final and ds0 for the backward ones
+    nrow = 3 + (1 if pass_ != 1 else 0) + (4 if pass_ != 0 else 0)
+    ng = 1 + (1 if pass_ != 0 else 0)
+    nst = 1 + (1 if pass_ != 1 else 0) + (2 if pass_ != 0 else 0)
+    assert lib.kda_workspace_size(pass_, B, T, H, 96, 64, dtype) - s128 == nrow * tok * es + ng * tok * 4 + nst * st
 
 
 @pytest.mark.parametrize("B,T,H,D,dtype,nseg", [
@@ -155,18 +181,16 @@ def test_null_and_workspace_errors():
     rc = lib.kda_fwd(misaligned, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 64, 64, 1, 1, fake,
                      1 << 40, None)
     assert rc == _lib.KDA_E_INVALID
-    # the backward supports D in {32, 64, 128}, and D = 128 with bf16 operands only
-    rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 96, 64, 1, 1, fake, 1 << 40, None)
+    # the backward supports D in {32, 64, 96, 128}
+    rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 80, 64, 1, 1, fake, 1 << 40, None)
     assert rc == _lib.KDA_E_UNSUPPORTED and "backward" in _lib.last_error()
-    rc = lib.kda_bwd(*([fake] * 14), 1, 64, 1, 128, 64, 0, 0, fake, 1 << 40, None)
-    assert rc == _lib.KDA_E_UNSUPPORTED and "bf16" in _lib.last_error()
 
 
 def test_training_pair_argument_errors():
     lib = _lib.load()
     fake = ctypes.c_void_p(1 << 20)
     # training needs a backward-capable head dim and dtype, and the pass-2 workspace
-    rc = lib.kda_fwd_train(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 128, 64, 0, 0,
+    rc = lib.kda_fwd_train(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 80, 64, 0, 0,
                            fake, 1 << 40, None)
     assert rc == _lib.KDA_E_UNSUPPORTED
     need = lib.kda_workspace_size(2, 1, 64, 1, 64, 64, 1)

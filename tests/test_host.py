@@ -38,9 +38,25 @@ def test_reference_chunk_sizes_accepted(c):
     assert kda.KDARecurrence(num_heads=2, head_dim=64, chunk_size=c).chunk_size == c
 
 
-def test_head_dim_128_for_inference_and_training():
-    assert kda.KDARecurrence(num_heads=16, head_dim=128, requires_grad=False).head_dim == 128
-    assert kda.KDARecurrence(num_heads=16, head_dim=128).head_dim == 128
+@pytest.mark.parametrize("D", [96, 128])
+def test_head_dims_96_and_128_for_inference_and_training(D):
+    assert kda.KDARecurrence(num_heads=16, head_dim=D, requires_grad=False).head_dim == D
+    assert kda.KDARecurrence(num_heads=16, head_dim=D).head_dim == D
+
+
+def test_ssv2_layer_constructs():
+    """The reference's SSv2 layer (train_mlx_ssv2.py:71-80): 8 heads of 96."""
+    from mlx_vit_amd import GatedDeltaLayer
+    layer = GatedDeltaLayer(768, 8, 96)
+    assert layer.head_dim == 96 and layer.total_dim == 768 and layer.recurrence.requires_grad
+
+
+def test_layer_rejects_too_many_norm_lanes():
+    """The output norm gives a head of 96 channels 32 lanes: 17 such heads
+    would need more than the kernel's 8 waves."""
+    from mlx_vit_amd import GatedDeltaLayer
+    with pytest.raises(ValueError, match="output norm"):
+        GatedDeltaLayer(17 * 96, 17, 96)
 
 
 def test_unknown_path_at_call():

@@ -330,6 +330,84 @@ def test_bwd_parity_bf16_d128(B, T, H, D, with_state, with_dsf, g_scale):
                 f"bwd bf16 D128 {B},{T},{H},{D},{with_state},{with_dsf},{g_scale}")
 
 
+@pytest.mark.parametrize("B,T,H,D,with_state,with_dsf,g_scale", [
+    (1, 200, 2, 128, True, True, 0.1),     # ragged last chunk, state + final-state cotangent
+    (2, 64, 3, 128, False, False, 0.1),    # one full chunk
+    (1, 130, 2, 128, True, False, 6.0),    # strong decay: every pair pair by pair
+])
+def test_bwd_parity_fp32_d128(B, T, H, D, with_state, with_dsf, g_scale):
+    """The fp32 backward at D = 128: the state recompute, the reverse carry on
+    four column slices of the state per (batch, head), and the wide
+    local-adjoint kernel with split-bf16 products accurate to fp32."""
+    x = _inputs(B, T, H, D, torch.float32, seed=26, with_state=with_state, grad=True, g_scale=g_scale)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9)) if with_dsf else None
+    _assert_all(_bwd_errors(x, torch.float32, dsf), TOL[torch.float32],
+                f"bwd fp32 D128 {B},{T},{H},{D},{with_state},{with_dsf},{g_scale}")
+
+
+# ---------------------------------------------------------------- head dimension 96
+
+D96_FWD = [
+    (1, 150, 2, torch.float32, True),
+    (2, 70, 3, torch.float32, False),      # ragged last chunk
+    (1, 1, 1, torch.float32, True),        # single token
+    (2, 300, 4, torch.bfloat16, True),
+    (1, 129, 2, torch.bfloat16, False),
+    (2, 1568, 8, torch.bfloat16, True),    # the reference's SSv2 layer: 8 heads x 96, 1568 tokens
+]
+
+
+@pytest.mark.parametrize("B,T,H,dtype,with_state", D96_FWD)
+def test_fwd_parity_d96(B, T, H, dtype, with_state):
+    """D = 96 (the reference's SSv2 model, train_mlx_ssv2.py:71-80): the library
+    pads to 128 channels in its workspace, runs the D = 128 kernels and crops."""
+    kda = _kda()
+    assert kda.workspace_offsets(0, B, T, H, 96, dtype)["Pad"] >= 0
+    x = _inputs(B, T, H, 96, dtype, seed=27, with_state=with_state)
+    _assert_all(_fwd_errors(x, dtype), TOL[dtype], f"fwd D96 {B},{T},{H},{dtype},{with_state}")
+
+
+@pytest.mark.parametrize("B,T,H,dtype,with_state,with_dsf,g_scale", [
+    (1, 150, 2, torch.float32, True, True, 0.1),
+    (2, 70, 3, torch.float32, False, False, 0.1),    # ragged last chunk
+    (1, 1, 1, torch.float32, True, True, 0.1),       # single token
+    (1, 130, 2, torch.float32, True, False, 6.0),    # strong decay
+    (2, 100, 3, torch.bfloat16, True, True, 0.1),
+    (1, 130, 2, torch.bfloat16, True, False, 6.0),
+    (2, 300, 8, torch.bfloat16, False, True, 1.0),
+])
+def test_bwd_parity_d96(B, T, H, dtype, with_state, with_dsf, g_scale):
+    D = 96
+    x = _inputs(B, T, H, D, dtype, seed=28, with_state=with_state, grad=True, g_scale=g_scale)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9)) if with_dsf else None
+    _assert_all(_bwd_errors(x, dtype, dsf), TOL[dtype], f"bwd D96 {B},{T},{H},{dtype},{with_state},{with_dsf},{g_scale}")
+
+
+def test_d96_zero_channels_leave_d128_results():
+    """Padding is exact: D = 96 inputs zero-padded to 128 by hand give, through
+    the D = 128 path, the D = 96 call's outputs and gradients in their first
+    96 channels (bit for bit: the library runs the same kernels on the same
+    padded values)."""
+    kda = _kda()
+    B, T, H = 1, 100, 2
+    x = _inputs(B, T, H, 96, torch.bfloat16, seed=29, with_state=True, grad=True)
+    pad = lambda t: torch.nn.functional.pad(t, (0, 32))                                   # noqa: E731
+    pads = lambda t: torch.nn.functional.pad(t, (0, 32, 0, 32))                           # noqa: E731
+    q, k, v, g, beta = _dev(x)
+    s0, do = x["s0"].to(DEV), x["do"].to(DEV)
+    o96, sf96 = kda.kda_forward(q, k, v, g, beta, s0)
+    gr96 = kda.kda_backward(q, k, v, g, beta, s0, do, None)
+    o128, sf128 = kda.kda_forward(pad(q), pad(k), pad(v), pad(g), beta, pads(s0))
+    gr128 = kda.kda_backward(pad(q), pad(k), pad(v), pad(g), beta, pads(s0), pad(do), None)
+    torch.cuda.synchronize()
+    assert torch.equal(o96, o128[..., :96]) and torch.equal(sf96, sf128[..., :96, :96])
+    for n, a, b in zip(("dq", "dk", "dv", "dg"), gr96[:4], gr128[:4]):
+        assert torch.equal(a, b[..., :96]), n
+    assert torch.equal(gr96[4], gr128[4]) and torch.equal(gr96[5], gr128[5][..., :96, :96])
+    # the padded channels' outputs are zero
+    assert not o128[..., 96:].any() and not sf128[..., 96:, :].any() and not sf128[..., :, 96:].any()
+
+
 def test_bwd_d128_fp32_gate():
     """D = 128 with bf16 q/k/v/beta and a float32 g: dg comes back float32."""
     x = _inputs(1, 100, 2, 128, torch.bfloat16, seed=25, with_state=True, grad=True)
@@ -381,6 +459,9 @@ def test_bwd_parity_config2_full():
     (1, 65, 2, 32, torch.float32, 0.1),
     (1, 1, 1, 64, torch.float32, 0.1),
     (1, 150, 2, 128, torch.bfloat16, 0.1),    # D = 128
+    (1, 100, 2, 128, torch.float32, 0.1),
+    (1, 150, 2, 96, torch.bfloat16, 0.1),     # D = 96: padded inputs in the pair's workspace
+    (2, 70, 2, 96, torch.float32, 0.1),
 ])
 def test_training_pair_equals_standalone_calls(B, T, H, D, dtype, g_scale):
     """kda_fwd_train / kda_bwd_train reproduce kda_fwd / kda_bwd bit for bit."""

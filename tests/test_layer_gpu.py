@@ -66,6 +66,7 @@ PRODUCER_CASES = [
     # as two passes over row slices
     (2, 300, 4, 64, torch.float32, True, 1.0),
     (4, 260, 3, 64, torch.bfloat16, True, 1.0),
+    (2, 37, 8, 96, torch.float32, True, 1.0),      # the SSv2 layer's 8 heads x 96
 ]
 
 
@@ -143,6 +144,9 @@ NORM_CASES = [
     (1, 9, 16, 128, torch.float32),
     (1, 130, 2, 4, torch.float32),
     (4, 65, 12, 64, torch.bfloat16),
+    (2, 37, 8, 96, torch.float32),     # D = 96: 32-lane head groups, 24 live lanes each
+    (1, 20, 5, 96, torch.float32),     # an odd head count: half of the last wave idle
+    (2, 30, 16, 96, torch.bfloat16),   # 16 heads of 96: eight waves
 ]
 
 
@@ -248,9 +252,54 @@ def test_layer_parity(dtype, with_state, D, fused):
     the step recurrence (nope_gdn_mlx.py:775-885 on the 'compiled' path), with
     the output norm fused into the recurrence's store where a kernel has it
     (fused) or as the standalone kernel."""
+    _layer_case(dtype, with_state, D, fused, B=2, L=100, H=3, hidden=3 * D)
+
+
+@pytest.mark.parametrize("dtype,with_state", [(torch.float32, True), (torch.bfloat16, True),
+                                              (torch.bfloat16, False)])
+def test_layer_parity_ssv2_d96(dtype, with_state):
+    """The reference's SSv2 layer, GatedDeltaLayer(768, 8, 96)
+    (train_mlx_ssv2.py:71-80): head dimension 96 through the padded recurrence
+    and the norm's 32-lane head groups."""
+    _layer_case(dtype, with_state, 96, False, B=2, L=100, H=8, hidden=768)
+
+
+def test_layer_training_step_ssv2_d96():
+    """A training step of GatedDeltaLayer(768, 8, 96) in bf16: forward,
+    backward, AdamW update; every parameter gets a finite, nonzero gradient,
+    the update changes the parameters, and the loss of the next forward on the
+    same batch is lower."""
     from mlx_vit_amd import GatedDeltaLayer
-    B, L, H = 2, 100, 3
-    hidden = H * D
+    torch.manual_seed(5)
+    layer = GatedDeltaLayer(768, 8, 96).to(torch.bfloat16)
+    layer.A_log.data = layer.A_log.data.float()
+    layer.dt_bias.data = layer.dt_bias.data.float()
+    layer = layer.to(DEV)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 1568, 768, generator=g).to(torch.bfloat16).to(DEV)
+    target = torch.randn(2, 1568, 768, generator=g).to(torch.bfloat16).to(DEV)
+    # lr 1e-2: an AdamW step of about lr moves even a bf16 weight at 1.0 (spacing 2^-7)
+    opt = torch.optim.AdamW(layer.parameters(), lr=1e-2)
+    before = {n: p.detach().clone() for n, p in layer.named_parameters()}
+    losses = []
+    for _ in range(2):
+        out, _ = layer(x)
+        loss = ((out.float() - target.float()) ** 2).mean()
+        opt.zero_grad()
+        loss.backward()
+        if not losses:
+            for n, p in layer.named_parameters():
+                assert p.grad is not None and torch.isfinite(p.grad).all() and p.grad.abs().sum() > 0, n
+        opt.step()
+        losses.append(loss.item())
+    torch.cuda.synchronize()
+    print("ssv2 layer training step losses", losses, flush=True)
+    assert losses[1] < losses[0]
+    assert all(not torch.equal(before[n], p.detach()) for n, p in layer.named_parameters())
+
+
+def _layer_case(dtype, with_state, D, fused, B, L, H, hidden):
+    from mlx_vit_amd import GatedDeltaLayer
     case = f"layer B={B} L={L} hidden={hidden} H={H} D={D} {dtype} state={with_state} fused={fused}"
     print(case, flush=True)
     torch.manual_seed(3)
@@ -279,13 +328,25 @@ def test_layer_parity(dtype, with_state, D, fused):
     rp = {n: t.requires_grad_() for n, t in ref_params.items()}
     rx = x.double().requires_grad_()
     rs0 = None if s0 is None else s0.double().requires_grad_()
-    rout, rst = LR.layer_forward(rp, rx, H, D, rs0)
+    keep = {}
+    rout, rst = LR.layer_forward(rp, rx, H, D, rs0, keep=keep)
+    keep["g"].retain_grad()
     ((rout * cot.double()).sum() + (rst * cot_s.double()).sum()).backward()
     errs = {"out": _rel(out, rout), "state": _rel(st, rst), "dx": _rel(xd.grad, rx.grad)}
     if s0 is not None:
         errs["ds0"] = _rel(s0d.grad, rs0.grad)
     for n, p in layer.named_parameters():
         errs["d" + n] = _rel(p.grad, rp[n].grad)
+    # dA_log[h] is the signed sum over (b, t, d) of dg * g (dg/dA_log = g): its
+    # error is bounded relative to the sum of the terms' magnitudes, which
+    # cancellation can make far larger than the sum itself (the rel-L2 of an
+    # H-entry vector of such sums is printed, not asserted)
+    terms = (keep["g"].grad * keep["g"]).abs().sum(dim=(0, 1, 3))
+    plain = errs.pop("dA_log")
+    errs["dA_log/sum|terms|"] = (layer.A_log.grad.detach().cpu().double() - rp["A_log"].grad).norm().item() / \
+        terms.norm().item()
+    print(case, f"dA_log rel-L2 {plain:.2e}, cancellation factor {terms.norm().item() / rp['A_log'].grad.norm().item():.1f}",
+          flush=True)
     _check(errs, TOL[dtype], case)
 
 
