@@ -77,7 +77,7 @@ def seg_plan(BH, nc):
     return -(-nc // length), length
 
 
-def kernel_counts(B, T, H, D, es=2):
+def kernel_counts(B, T, H, D, es=2, backward=False):
     """Per-launch figures of each library kernel (ids as in kda_profile_name):
     (flops, alg_bytes, ws_bytes).
 
@@ -99,7 +99,9 @@ def kernel_counts(B, T, H, D, es=2):
     with the library's storage types: operands and the W/U/Qp/Kb/V'/dV'/A/h/dh
     workspace in the input dtype (``es`` bytes), Akk, the diagonal-block
     inverses, e^G and the states in fp32.  With bf16 inputs the local-adjoint
-    kernel recomputes Akk, the inverses and V', so no kernel moves them."""
+    kernel recomputes Akk, the inverses and V', so no kernel moves them.  In a
+    training step at bf16 D = 64 (``backward``) the forward recurrence also
+    writes the chunk-start states h, and the state recompute does not run."""
     nc = -(-T // C)
     N = B * H * nc              # chunks
     n = N * C                   # padded token-heads
@@ -154,6 +156,8 @@ def kernel_counts(B, T, H, D, es=2):
         6: io_in + (N * (4 * CD * es + CC * es + D * f4) if tr else                      # -> both sets
                     N * (7 * CD * es + 2 * CC * es + x * (CC + TII) * f4 + D * f4)),
     }
+    if backward and es == 2 and D == 64:
+        ws[1] += N * DD * es                            # -> h, for the backward
     return fl, alg, ws
 
 
@@ -638,7 +642,7 @@ def main():
     prof_ms_per_step = (time.perf_counter() - t1) / args.steps * 1e3
     lib.kda_profile_enable(0)
     import ctypes
-    fl, alg, wsb = kernel_counts(B, T, H, D)
+    fl, alg, wsb = kernel_counts(B, T, H, D, backward=backward)
     kernels = []
     for kid in range(_lib.PROF_NKERNELS):
         tot, cnt = ctypes.c_double(), ctypes.c_int()
