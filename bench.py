@@ -43,6 +43,8 @@ WORKLOADS = {
              "KDA fwd+VJP (training pair), B8 H12 T1568 D64 bf16 (config 2)"),
     "cfg1": (8, 1568, 12, 64, False, False, "KDA fwd, B8 H12 T1568 D64 bf16 (config 1)"),
     "cfg3": (1, 32768, 16, 128, False, True, "KDA fwd, B1 H16 T32768 D128 bf16, fp32 S0 (config 3)"),
+    # the reference's SSv2 layer (train_mlx_ssv2.py:71-80): 8 heads of 96, 1568 tokens
+    "ssv2-d96": (8, 1568, 8, 96, True, False, "KDA fwd+VJP (training pair), B8 H8 T1568 D96 bf16 (SSv2 layer)"),
     # config 2's shape with the decay of the reference layer at initialisation:
     # g = -A_h softplus(x), A_h = e^{A_log} ~ U[1, 16] per head (nope_gdn_mlx.py:749),
     # x ~ N(0, 0.5^2) for the gate projection plus dt_bias (zero at init)
@@ -78,6 +80,17 @@ def seg_plan(BH, nc):
 
 
 def kernel_counts(B, T, H, D, es=2, backward=False):
+    """kernel_counts_at for the kernels' head dimension: D = 96 runs the D = 128
+    kernels on zero-padded copies, so its FLOPs and workspace bytes are those
+    of D = 128 while its op bytes are D = 96's."""
+    if D == 96:
+        fl, _, ws = kernel_counts_at(B, T, H, 128, es, backward)
+        _, alg, _ = kernel_counts_at(B, T, H, 96, es, backward)
+        return fl, alg, ws
+    return kernel_counts_at(B, T, H, D, es, backward)
+
+
+def kernel_counts_at(B, T, H, D, es=2, backward=False):
     """Per-launch figures of each library kernel (ids as in kda_profile_name):
     (flops, alg_bytes, ws_bytes).
 
@@ -206,7 +219,9 @@ PROFILE_ROLES = {
     # rocprof kernel symbol fragment -> profile names in dispatch order within a
     # fwd+bwd step (the training pair: one prep launch, in its training mode)
     "kda_prep_kernel": ["kda_prep_kernel(train)"],
-    "kda_recur": ["kda_recur_kernel(fwd)", "kda_recur_kernel(states)"],
+    # (a training step at bf16 D = 64 runs no state recompute: the training
+    # forward keeps the chunk-start states)
+    "kda_recur": ["kda_recur_kernel(fwd)"],
     "kda_dh": ["kda_dh_kernel"],
     "kda_bwd_local": ["kda_bwd_local_kernel"],
 }

@@ -443,10 +443,16 @@ int run_bwd_padded(int pass, const void* q, const void* k, const void* v, const 
                    void* dbeta, float* ds0, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* ws,
                    const Layout& L, hipStream_t st) {
     const PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
-    hipError_t e;
-    if ((e = io.rows_in(q, PS_Q, io.es)) != hipSuccess || (e = io.rows_in(k, PS_K, io.es)) != hipSuccess ||
-        (e = io.rows_in(v, PS_V, io.es)) != hipSuccess || (e = io.rows_in(g, PS_G, io.gs)) != hipSuccess ||
-        (e = io.rows_in(dout, PS_DO, io.es)) != hipSuccess || (s0 && (e = io.state_in(s0, PS_S0)) != hipSuccess) ||
+    hipError_t e = hipSuccess;
+    // the training backward finds the padded q, k, v, g and s0 where the
+    // training forward left them (the pair's workspace is unmodified between
+    // the two calls, for the same inputs)
+    if (pass != KDA_PASS_TRAIN &&
+        ((e = io.rows_in(q, PS_Q, io.es)) != hipSuccess || (e = io.rows_in(k, PS_K, io.es)) != hipSuccess ||
+         (e = io.rows_in(v, PS_V, io.es)) != hipSuccess || (e = io.rows_in(g, PS_G, io.gs)) != hipSuccess ||
+         (s0 && (e = io.state_in(s0, PS_S0)) != hipSuccess)))
+        return hip_fail(e, "kda_resize_kernel (pad)");
+    if ((e = io.rows_in(dout, PS_DO, io.es)) != hipSuccess ||
         (ds_final && (e = io.state_in(ds_final, PS_DSF)) != hipSuccess))
         return hip_fail(e, "kda_resize_kernel (pad)");
     const int rc = run_bwd(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,

@@ -69,11 +69,27 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     constexpr int NT = D / BS, NTH = 4 * D, NW = NTH / 64;
     static_assert(NW == NT && NB == 4, "one wave per channel tile, one thread per (channel, row block)");
     __shared__ WideLds<D> s;
-    __shared__ float sp[C][C + 4];          // Akk, then dP = diag(beta) dL
+    __shared__ __align__(16) float sp[C][C + 4];   // Akk, then dP = diag(beta) dL
     __shared__ float sda[C][C + 4];         // dAqk (lower, with the diagonal)
-    __shared__ float sdr[C][D + 4];         // one half of dR: dR_k, then dR_v
-    __shared__ float tii[NB][BS][BS + 4];
+    __shared__ __align__(16) float tii[NB][BS][BS + 4];
     __shared__ float sdb[NB + NT][C];       // dbeta partials: [j] from dL tiles of column block j, [NB + nt] channel tile nt
+    // Staging area.  bf16 (STG): the chunk's raw k and q rows (phase 0 to the
+    // per-lane values), then dO, V', dV' and v (phase 1 and the dA tiles), then one
+    // half of dR (fp32) beside W or U (phases 2-3), each brought in with
+    // coalesced 16-byte loads so that fragments and per-lane values are LDS
+    // reads.  fp32 (no room for the staged tiles): dR only; the rest is read
+    // from global memory.
+    constexpr bool STG = sizeof(TI) == 2;
+    constexpr int LDQ = D + 8, LDR = D + 4;   // bf16 rows with a 16-byte pad; fp32 dR rows
+    constexpr int T_BYTES = C * LDQ * (int)sizeof(TI), R_BYTES = C * LDR * 4;
+    constexpr int STG_BYTES = STG ? ((4 * T_BYTES > R_BYTES + T_BYTES) ? 4 * T_BYTES : R_BYTES + T_BYTES) : R_BYTES;
+    __shared__ __align__(16) unsigned char stg[STG_BYTES];
+    float* sdr = reinterpret_cast<float*>(stg);                      // [C][LDR], one half of dR: dR_k, then dR_v
+    TI* const st0 = reinterpret_cast<TI*>(stg);                       // k | dO
+    TI* const st1p = reinterpret_cast<TI*>(stg + T_BYTES);            // q | V'
+    TI* const st2 = reinterpret_cast<TI*>(stg + 2 * T_BYTES);         // dV'
+    TI* const st3 = reinterpret_cast<TI*>(stg + 3 * T_BYTES);         // v
+    TI* const swu = reinterpret_cast<TI*>(stg + R_BYTES);             // W, then U (beside dR)
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
               g4 = l >> 4;
@@ -99,23 +115,55 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     const TI* Uc = static_cast<const TI*>(a.U) + cCD;
 
     // ---------------- phase 0: A_kk, inverses, gamma, factors ----------------
-    for (int idx = tid; idx < C * C; idx += NTH) sp[idx / C][idx % C] = a.Akk[cCC + idx];
-    for (int idx = tid; idx < NB * BS * BS; idx += NTH) {
-        const int i = idx / (BS * BS), e = idx - i * BS * BS;
-        tii[i][e / BS][e % BS] = a.Tii[(size_t)ch * NB * BS * BS + idx];
+    // every load of the phase issued before any is used: A_kk and the inverses
+    // as 16-byte pieces, g of the thread's 16 rows, k and q rows (bf16)
+    constexpr int AKV = C * C / 4, TIV = NB * BS * BS / 4;
+    float4 akv[(AKV + NTH - 1) / NTH];
+#pragma unroll
+    for (int i = 0; i < (AKV + NTH - 1) / NTH; ++i)
+        if (AKV % NTH == 0 || tid + NTH * i < AKV)
+            akv[i] = reinterpret_cast<const float4*>(a.Akk + cCC)[tid + NTH * i];
+    float4 tiv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < TIV) tiv = reinterpret_cast<const float4*>(a.Tii + (size_t)ch * NB * BS * BS)[tid];
+    const int cd = tid % D, cb = tid / D;
+    // rows past T are read from the last valid row (no branch around a load,
+    // so the sixteen loads are in flight together) and zeroed below
+    float gx[BS];
+#pragma unroll
+    for (int r = 0; r < BS; ++r) {
+        const int t = BS * cb + r;
+        gx[r] = ld1<TG>(g + base + (size_t)min(t, valid - 1) * rs + cd);
+    }
+    Tile<TI, C, D, NTH> tkr, tqr;
+    if constexpr (STG) {
+        tkr.load(k + base, rs, valid);
+        tqr.load(q + base, rs, valid);
+    }
+#pragma unroll
+    for (int i = 0; i < (AKV + NTH - 1) / NTH; ++i)
+        if (AKV % NTH == 0 || tid + NTH * i < AKV) {
+            const int e = 4 * (tid + NTH * i);
+            *reinterpret_cast<float4*>(&sp[e / C][e % C]) = akv[i];
+        }
+    if (tid < TIV) {
+        const int e = 4 * tid, i = e / (BS * BS), r = (e / BS) % BS, c = e % BS;
+        *reinterpret_cast<float4*>(&tii[i][r][c]) = tiv;
     }
     for (int idx = tid; idx < (NB + NT) * C; idx += NTH) sdb[idx / C][idx % C] = 0.f;
     if (tid < C) s.beta[tid] = (tid < valid) ? ld1<TI>(beta + bbase + (size_t)tid * a.H) : 0.f;
+    if constexpr (STG) {
+        tkr.store(st0, LDQ);
+        tqr.store(st1p, LDQ);
+    }
     // thread (channel cd, block cb): inclusive cumsum of g over the block's 16
     // rows (rows past T are g = 0: no decay), then the totals of earlier blocks
     int flag = 0;
     {
-        const int cd = tid % D, cb = tid / D;
         float run = 0.f;
-#pragma unroll 4
+#pragma unroll
         for (int r = 0; r < BS; ++r) {
             const int t = BS * cb + r;
-            const float x = (t < valid) ? ld1<TG>(g + base + (size_t)t * rs + cd) : 0.f;
+            const float x = (t < valid) ? gx[r] : 0.f;
             if (!(x <= 0.f)) flag = 1;
             run += x;
             s.g[t][cd] = run;
@@ -145,9 +193,9 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
 
     // wave w owns channel tile w: rows t = 16 m + 4 g4 + e, channel d
     const int nt = w, d = nt * BS + r16;
-    // raw k, q of the lane's rows; el = e^{gamma_t - gamma_r}, er = e^{gamma_r -
-    // gamma_t} (r = 16 m), eb = e^{G - gamma_t}, erb = e^{gamma_r}
-    float kx[NB][4], qx[NB][4], el[NB][4], er[NB][4], eb[NB][4], erb[NB];
+    // raw k, q of the lane's rows; el = e^{gamma_t - gamma_r} (r = 16 m), eb =
+    // e^{G - gamma_t}, erb = e^{gamma_r}
+    float kx[NB][4], qx[NB][4], el[NB][4], eb[NB][4], erb[NB];
     {
         const float G = s.g[C - 1][d];
 #pragma unroll
@@ -158,11 +206,17 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * m + 4 * g4 + e;
                 const float gt = s.g[t][d];
-                const size_t o = base + (size_t)t * rs + d;
-                kx[m][e] = (t < valid) ? ld1<TI>(k + o) : 0.f;
-                qx[m][e] = (t < valid) ? ld1<TI>(q + o) : 0.f;
+                if constexpr (STG) {
+                    kx[m][e] = ld1<TI>(st0 + t * LDQ + d);
+                    qx[m][e] = ld1<TI>(st1p + t * LDQ + d);
+                } else {
+                    // clamped row, selected after the load: no branch around it
+                    const size_t oc = base + (size_t)min(t, valid - 1) * rs + d;
+                    const float kv = ld1<TI>(k + oc), qv = ld1<TI>(q + oc);
+                    kx[m][e] = (t < valid) ? kv : 0.f;
+                    qx[m][e] = (t < valid) ? qv : 0.f;
+                }
                 el[m][e] = kexp<PREC>(gt - gr);
-                er[m][e] = unsafe ? 0.f : kexp<PREC>(gr - gt);
                 eb[m][e] = kexp<PREC>(G - gt);
             }
         }
@@ -174,16 +228,49 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     float dgcol = 0.f;
 
     // ---------------- phase 1: products over dv ----------------
+    // bf16: dO, V', dV' staged (the k, q rows are in registers now); the B
+    // operands, rows of h and dh of the wave's own channel tile, straight from
+    // global memory, once
+    Frag8 Bh[STG ? D / 32 : 1], Bdh[STG ? D / 32 : 1];
+    if constexpr (STG) {
+        Tile<TI, C, D, NTH> tdo, tvp, tdvp, tvv;
+        tdo.load(dout + base, rs, valid);
+        tvp.load(Vp, D);
+        tdvp.load(dVp, D);
+        tvv.load(v + base, rs, valid);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            Bh[ks] = ldfrag_c<1, TI>(hS, D, BS * nt, 32 * ks);
+            Bdh[ks] = ldfrag_c<1, TI>(dhS, D, BS * nt, 32 * ks);
+        }
+        __syncthreads();   // every lane's k, q reads are done
+        tdo.store(st0, LDQ);
+        tvp.store(st1p, LDQ);
+        tdvp.store(st2, LDQ);
+        tvv.store(st3, LDQ);
+        __syncthreads();
+    }
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
         f32x4 dQp = zero4(), dKb = zero4(), dW = zero4();
+        if constexpr (STG) {
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
-            const Fr8 Bh = frag8(hS, D, BS * nt, 32 * ks);
-            const Fr8 Bdh = frag8(dhS, D, BS * nt, 32 * ks);
-            dQp = mma8<PREC>(rows8<TI>(dout + base, rs, BS * m, 32 * ks, valid), Bh, dQp);
-            dKb = mma8<PREC>(frag8(Vp, D, BS * m, 32 * ks), Bdh, dKb);
-            dW = mma8<PREC>(neg(frag8(dVp, D, BS * m, 32 * ks)), Bh, dW);
+            for (int ks = 0; ks < D / 32; ++ks) {
+                dQp = mma<1>(ldfrag_c<1, TI>(st0, LDQ, BS * m, 32 * ks), Bh[ks], dQp);
+                dKb = mma<1>(ldfrag_c<1, TI>(st1p, LDQ, BS * m, 32 * ks), Bdh[ks], dKb);
+                dW = mma<1>(ldfrag_c<1, TI>(st2, LDQ, BS * m, 32 * ks), Bh[ks], dW);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dW[e] = -dW[e];
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                const Fr8 Bh8 = frag8(hS, D, BS * nt, 32 * ks);
+                const Fr8 Bdh8 = frag8(dhS, D, BS * nt, 32 * ks);
+                dQp = mma8<PREC>(rows8<TI>(dout + base, rs, BS * m, 32 * ks, valid), Bh8, dQp);
+                dKb = mma8<PREC>(frag8(Vp, D, BS * m, 32 * ks), Bdh8, dKb);
+                dW = mma8<PREC>(neg(frag8(dVp, D, BS * m, 32 * ks)), Bh8, dW);
+            }
         }
         dWt[m] = dW;
 #pragma unroll
@@ -199,8 +286,15 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     {
         // state-decay term of dG: e^G sum_col dh[d][col] h[d][col]
         float part = 0.f;
-        for (int c = g4 * (D / 4); c < (g4 + 1) * (D / 4); ++c)
-            part += ld1<TI>(dhS + (size_t)d * D + c) * ld1<TI>(hS + (size_t)d * D + c);
+        float4 xh[D / 16], xd[D / 16];
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+            xh[c] = ld4<TI>(hS + (size_t)d * D + g4 * (D / 4) + 4 * c);
+            xd[c] = ld4<TI>(dhS + (size_t)d * D + g4 * (D / 4) + 4 * c);
+        }
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+            part += (xd[c].x * xh[c].x + xd[c].y * xh[c].y) + (xd[c].z * xh[c].z + xd[c].w * xh[c].w);
         dgcol = sum4gw(dgcol) + kexp<PREC>(s.g[C - 1][d]) * sum4gw(part);
     }
     // dAqk = tril(dO V'^T), 10 lower tiles over the waves
@@ -208,15 +302,39 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
         int i, j;
         tile_ij(tix, i, j);
         f32x4 acc = zero4();
+        if constexpr (STG) {
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks)
-            acc = mma8<PREC>(rows8<TI>(dout + base, rs, BS * i, 32 * ks, valid), frag8(Vp, D, BS * j, 32 * ks), acc);
+            for (int ks = 0; ks < D / 32; ++ks)
+                acc = mma<1>(ldfrag_c<1, TI>(st0, LDQ, BS * i, 32 * ks), ldfrag_c<1, TI>(st1p, LDQ, BS * j, 32 * ks), acc);
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                acc = mma8<PREC>(rows8<TI>(dout + base, rs, BS * i, 32 * ks, valid), frag8(Vp, D, BS * j, 32 * ks),
+                                 acc);
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
             sda[t][sx] = (sx <= t) ? acc[e] : 0.f;
         }
     }
+    // the lane's dV' and v values for the solve (bf16: from the staged tiles,
+    // before the barrier below frees them)
+    f32x4 dvp[NB], vx[NB];
+#pragma unroll
+    for (int m = 0; m < NB; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = BS * m + 4 * g4 + e;
+            if constexpr (STG) {
+                dvp[m][e] = ld1<TI>(st2 + t * LDQ + d);
+                vx[m][e] = ld1<TI>(st3 + t * LDQ + d);
+            } else {
+                dvp[m][e] = ld1<TI>(dVp + (size_t)t * D + d);
+                const float vv = ld1<TI>(v + base + (size_t)min(t, valid - 1) * rs + d);
+                vx[m][e] = (t < valid) ? vv : 0.f;
+            }
+        }
     // zero upper tiles of sda
     for (int idx = tid; idx < 6 * BS * BS; idx += NTH) {
         const int tile = idx / (BS * BS), e = idx - tile * BS * BS;
@@ -228,12 +346,11 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
 
     // ---------------- phase 2: transposed WY solve (fp32-accurate split products) ----------------
     f32x4 dRk[NB], dRv[NB];
+    Tile<TI, C, D, NTH> tw, tu;
     {
 #pragma unroll
         for (int i = NB - 1; i >= 0; --i) {
-            f32x4 Yk = dWt[i], Yv;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) Yv[e] = ld1<TI>(dVp + (size_t)(BS * i + 4 * g4 + e) * D + d);
+            f32x4 Yk = dWt[i], Yv = dvp[i];
 #pragma unroll
             for (int j = i + 1; j < NB; ++j) {
                 // A[a][b] = -L[16j + b][16i + a] = -beta_{16j+b} Akk[16j+b][16i+a]
@@ -250,6 +367,12 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
             dRk[i] = mma4<3>(Tt, acc2frag4(Yk), zero4());
             dRv[i] = mma4<3>(Tt, acc2frag4(Yv), zero4());
         }
+        // bf16: W and U come to the staging area beside dR for phase 3 (loaded
+        // here, after the solve's chain, and stored at its end)
+        if constexpr (STG) {
+            tw.load(Wc, D);
+            tu.load(Uc, D);
+        }
         TI* dv = static_cast<TI*>(a.dv);
 #pragma unroll
         for (int m = 0; m < NB; ++m) {
@@ -258,48 +381,59 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
                 const int t = BS * m + 4 * g4 + e;
                 const float bt = s.beta[t];
                 const float egt = erb[m] * el[m][e];
-                const float vv = (t < valid) ? ld1<TI>(v + base + (size_t)t * rs + d) : 0.f;
+                const float vv = vx[m][e];
                 if (t < valid) st1<TI>(dv + base + (size_t)t * rs + d, bt * dRv[m][e]);
                 dka[m][e] += bt * egt * dRk[m][e];
                 dga[m][e] += dRk[m][e] * bt * egt * kx[m][e];
                 const float db = sum16w(dRv[m][e] * vv + dRk[m][e] * egt * kx[m][e]);
                 if (r16 == 0) sdb[NB + nt][t] = db;
-                sdr[t][d] = dRk[m][e];
+                sdr[t * LDR + d] = dRk[m][e];
             }
         }
     }
+    if constexpr (STG) tw.store(swu, LDQ);
     __syncthreads();
 
     // ---------------- phase 3: dL = -tril(dR [W | U]^T, -1), one half of dR at a time ----------------
+    // bf16: W and U are exact in bf16, so splitting only dR (PREC 2) keeps the
+    // product fp32-accurate; fp32: both split (PREC 3)
     constexpr int TPW = (10 + NW - 1) / NW;
     f32x4 accL[TPW];
+    auto dl_half = [&](const TI* gX) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < TPW; ++u) {
-        accL[u] = zero4();
-        const int tix = w + NW * u;
-        if (tix < 10) {
-            int i, j;
-            tile_ij(tix, i, j);
+        for (int u = 0; u < TPW; ++u) {
+            const int tix = w + NW * u;
+            if (tix < 10) {
+                int i, j;
+                tile_ij(tix, i, j);
 #pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks)
-                accL[u] = mma8<3>(frag8(&sdr[0][0], D + 4, BS * i, 32 * ks), frag8(Wc, D, BS * j, 32 * ks), accL[u]);
+                for (int ks = 0; ks < D / 32; ++ks) {
+                    if constexpr (STG)
+                        accL[u] = mma<2>(ldfrag_c<2, float>(sdr, LDR, BS * i, 32 * ks),
+                                         ldfrag_c<1, TI>(swu, LDQ, BS * j, 32 * ks), accL[u]);
+                    else
+                        accL[u] = mma8<3>(frag8(sdr, LDR, BS * i, 32 * ks), frag8(gX, D, BS * j, 32 * ks), accL[u]);
+                }
+            }
         }
-    }
-    __syncthreads();   // dR_k read by every wave
+    };
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) accL[u] = zero4();
+    dl_half(Wc);
+    __syncthreads();   // dR_k and W read by every wave
 #pragma unroll
     for (int m = 0; m < NB; ++m)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sdr[BS * m + 4 * g4 + e][d] = dRv[m][e];
+        for (int e = 0; e < 4; ++e) sdr[(BS * m + 4 * g4 + e) * LDR + d] = dRv[m][e];
+    if constexpr (STG) tu.store(swu, LDQ);
     __syncthreads();
+    dl_half(Uc);
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
         const int tix = w + NW * u;
         if (tix < 10) {
             int i, j;
             tile_ij(tix, i, j);
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks)
-                accL[u] = mma8<3>(frag8(&sdr[0][0], D + 4, BS * i, 32 * ks), frag8(Uc, D, BS * j, 32 * ks), accL[u]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = BS * i + 4 * g4 + e, sx = BS * j + r16;
@@ -316,6 +450,15 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     if (!unsafe) {
         // row and column sides of a pair must agree to fp32: exact split products
         constexpr int PX = PREC >= 3 ? 4 : PREC;
+        // er = e^{gamma_r - gamma_t} (r = 16 m), formed here rather than with the
+        // other per-lane values so that it is not live across phases 1-3
+        float er[NB][4];
+#pragma unroll
+        for (int m = 0; m < NB; ++m) {
+            const float gr = s.g[BS * m][d];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) er[m][e] = kexp<PREC>(gr - s.g[BS * m + 4 * g4 + e][d]);
+        }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             f32x4 dKl = zero4(), dQl = zero4();
