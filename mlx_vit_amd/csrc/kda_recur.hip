@@ -2358,13 +2358,14 @@ bool recur_epilogue_supported(int D, int in_bf16) { return in_bf16 ? D == 64 : (
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st) {
     if (D == 32) return in_bf16 ? launch_dh_t<32, uint16_t>(a, st) : launch_dh_t<32, float>(a, st);
     if (D == 64) return in_bf16 ? launch_dh_t<64, uint16_t>(a, st) : launch_dh_t<64, float>(a, st);
-    // D = 128: the generic kernel on the transposed slabs; bf16: one workgroup
-    // per (batch, head); fp32: four, 32 dS columns each (one operand set and its
-    // staging fit the LDS only at that width)
+    // D = 128: the generic kernel on the transposed slabs; bf16: two workgroups
+    // per (batch, head), 64 dS columns each (one column tile per wave); fp32:
+    // four, 32 dS columns each (one operand set and its staging fit the LDS
+    // only at that width)
     if (D == 128) {
         if (!a.AqkT || !a.QpT || !a.WT || !a.Kb) return hipErrorInvalidValue;
         if (in_bf16)
-            hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1>), dim3(a.BH), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1, 2>), dim3(a.BH * 2), dim3(256), 0, st, a);
         else
             hipLaunchKernelGGL((kda_dh_kernel<128, float, 3, 4>), dim3(a.BH * 4), dim3(256), 0, st, a);
         return hipGetLastError();
