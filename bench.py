@@ -79,18 +79,18 @@ def seg_plan(BH, nc):
     return -(-nc // length), length
 
 
-def kernel_counts(B, T, H, D, es=2, backward=False):
+def kernel_counts(B, T, H, D, es=2):
     """kernel_counts_at for the kernels' head dimension: D = 96 runs the D = 128
     kernels on zero-padded copies, so its FLOPs and workspace bytes are those
     of D = 128 while its op bytes are D = 96's."""
     if D == 96:
-        fl, _, ws = kernel_counts_at(B, T, H, 128, es, backward)
-        _, alg, _ = kernel_counts_at(B, T, H, 96, es, backward)
+        fl, _, ws = kernel_counts_at(B, T, H, 128, es)
+        _, alg, _ = kernel_counts_at(B, T, H, 96, es)
         return fl, alg, ws
-    return kernel_counts_at(B, T, H, D, es, backward)
+    return kernel_counts_at(B, T, H, D, es)
 
 
-def kernel_counts_at(B, T, H, D, es=2, backward=False):
+def kernel_counts_at(B, T, H, D, es=2):
     """Per-launch figures of each library kernel (ids as in kda_profile_name):
     (flops, alg_bytes, ws_bytes).
 
@@ -112,9 +112,7 @@ def kernel_counts_at(B, T, H, D, es=2, backward=False):
     with the library's storage types: operands and the W/U/Qp/Kb/V'/dV'/A/h/dh
     workspace in the input dtype (``es`` bytes), Akk, the diagonal-block
     inverses, e^G and the states in fp32.  With bf16 inputs the local-adjoint
-    kernel recomputes Akk, the inverses and V', so no kernel moves them.  In a
-    training step at bf16 D = 64 (``backward``) the forward recurrence also
-    writes the chunk-start states h, and the state recompute does not run."""
+    kernel recomputes Akk, the inverses and V', so no kernel moves them."""
     nc = -(-T // C)
     N = B * H * nc              # chunks
     n = N * C                   # padded token-heads
@@ -169,8 +167,6 @@ def kernel_counts_at(B, T, H, D, es=2, backward=False):
         6: io_in + (N * (4 * CD * es + CC * es + D * f4) if tr else                      # -> both sets
                     N * (7 * CD * es + 2 * CC * es + x * (CC + TII) * f4 + D * f4)),
     }
-    if backward and es == 2 and D == 64:
-        ws[1] += N * DD * es                            # -> h, for the backward
     return fl, alg, ws
 
 
@@ -219,9 +215,7 @@ PROFILE_ROLES = {
     # rocprof kernel symbol fragment -> profile names in dispatch order within a
     # fwd+bwd step (the training pair: one prep launch, in its training mode)
     "kda_prep_kernel": ["kda_prep_kernel(train)"],
-    # (a training step at bf16 D = 64 runs no state recompute: the training
-    # forward keeps the chunk-start states)
-    "kda_recur": ["kda_recur_kernel(fwd)"],
+    "kda_recur": ["kda_recur_kernel(fwd)", "kda_recur_kernel(states)"],
     "kda_dh": ["kda_dh_kernel"],
     "kda_bwd_local": ["kda_bwd_local_kernel"],
 }
@@ -657,7 +651,7 @@ def main():
     prof_ms_per_step = (time.perf_counter() - t1) / args.steps * 1e3
     lib.kda_profile_enable(0)
     import ctypes
-    fl, alg, wsb = kernel_counts(B, T, H, D, backward=backward)
+    fl, alg, wsb = kernel_counts(B, T, H, D)
     kernels = []
     for kid in range(_lib.PROF_NKERNELS):
         tot, cnt = ctypes.c_double(), ctypes.c_int()

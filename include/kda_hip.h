@@ -119,11 +119,9 @@ int kda_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, 
  * in its (pass 2) workspace, every per-chunk factor the backward needs: W, U,
  * the decay-scaled Q / K operands and their transposes, A_qk and its transpose,
  * e^G (with fp32 inputs also A_kk and the inverted diagonal blocks of I + L).
- * With bf16 inputs at D = 64 it also keeps the chunk-start states (bf16, the
- * workspace's h region, which the backward needs anyway), so that
- * kda_bwd_train does not recompute them; elsewhere kda_bwd_train recomputes
- * them from the factors and s0.  At D = 96 the pair's workspace also keeps the
- * padded q, k, v, g and s0 for the backward.
+ * No state is kept: kda_bwd_train recomputes the chunk-boundary states from
+ * the factors and s0.  At D = 96 the pair's workspace also keeps the padded
+ * q, k, v, g and s0 for the backward.
  * kda_bwd_train is kda_bwd without its prep: it requires the workspace that
  * kda_fwd_train filled for the same q, k, v, g, beta and s0 (and the same B,
  * T, H, D, dtype), unmodified in between, and returns the same gradients as

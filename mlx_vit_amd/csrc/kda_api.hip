@@ -468,12 +468,6 @@ int run_bwd_padded(int pass, const void* q, const void* k, const void* v, const 
     return ok();
 }
 
-// Whether the training forward (pass 2) writes the chunk-start states h into
-// its workspace, so that kda_bwd_train reads them instead of recomputing them:
-// bf16 at D = 64, where the forward recurrence's chain is the state
-// recompute's (the same h, bit for bit).
-bool train_keeps_h(int D, int dtype) { return dtype == KDA_DTYPE_BF16 && D == 64; }
-
 // The forward's launch sequence (pass 0) or the training forward's (pass 2).
 // prof = false: no launch timing, so the profiler's event pool never grows (for
 // the entry point that must not allocate).
@@ -546,21 +540,8 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     if (epi) {
         ra.z = epi->z; ra.ld_z = epi->ld_z; ra.nw = epi->w; ra.eps = epi->eps; ra.y = epi->y; ra.ld_y = epi->ld_y;
     }
-    const bool keep_h = pass == KDA_PASS_TRAIN && train_keeps_h(D, dtype);
-    if (keep_h && !epi) ra.h = region(workspace, L, KDA_WS_H);
     e = timed(PROF_RECUR_FWD, st, [&] { return kda::launch_recur(ra, D, in_bf16, 0, st); }, prof);
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
-    if (keep_h && epi) {
-        // the fused-norm kernel keeps no states: the state recompute here
-        // instead of in kda_bwd_train
-        kda::RecurArgs rh = ra;
-        rh.z = nullptr; rh.nw = nullptr; rh.y = nullptr; rh.o = nullptr; rh.s_final = nullptr;
-        rh.h = region(workspace, L, KDA_WS_H);
-        rh.Vp = region(workspace, L, KDA_WS_VP);
-        rh.KbT = region(workspace, L, KDA_WS_KBT);
-        e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(rh, D, in_bf16, 1, st); }, prof);
-        if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel (states)");
-    }
     return ok();
 }
 
@@ -612,16 +593,13 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
     void* Vp = region(workspace, L, KDA_WS_VP);
     void* dVp = region(workspace, L, KDA_WS_DVP);
 
-    // chunk-boundary states, recomputed from the per-chunk factors (unless the
-    // training forward left them in the workspace)
-    if (!(pass == KDA_PASS_TRAIN && train_keeps_h(D, dtype))) {
-        kda::RecurArgs ra = {};
-        ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
-        ra.Kb = region(workspace, L, KDA_WS_KB);
-        ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-        e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
-        if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
-    }
+    // chunk-boundary states, recomputed from the per-chunk factors
+    kda::RecurArgs ra = {};
+    ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
+    ra.Kb = region(workspace, L, KDA_WS_KB);
+    ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
+    e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
+    if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
 
     kda::DhArgs da = {};
     da.AqkT = region(workspace, L, KDA_WS_AQKT);

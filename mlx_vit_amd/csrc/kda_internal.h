@@ -40,8 +40,7 @@ struct RecurArgs {
     void* o;
     void *h, *Vp;
     int T, H, nc, BH;
-    // h: mode 1 writes the chunk-start states there; so does mode 0 of the
-    // bf16 D = 64 kernel when h is set (the training forward)
+    // h: mode 1 writes the chunk-start states there
     // Forward only: the layer's gated RMSNorm fused into the O store when y is
     // set, y = o rsqrt(mean_d o^2 + eps) nw sigmoid(z) per head; z and y are
     // [B, T, *] with row strides ld_z and ld_y (elements), head h at column h D.

@@ -1397,8 +1397,7 @@ __global__ __launch_bounds__(256) void kda_recur3_kernel(const RecurArgs a) {
 //                next chunk's W, U, Kb^T (transposing reads of Kb), e^G operands
 //   role-1 waves: flush the previous chunk's outputs; MODE 0: O = Qp S + Aqk V'
 //                (row block wr) after B, read the next chunk's Qp, Aqk operands;
-//                MODE 1, and MODE 0 when a.h is set (the training forward):
-//                copy the chunk-start state to h
+//                MODE 1: copy the chunk-start state to h
 //   DMA: chunk n+NS is brought after barrier B(n), once chunk n's operands (the
 //        chain waves read its Kb^T and e^G between A(n) and B(n)) have left its
 //        LDS set: MODE 0 the chain waves bring W, U, Kb^T, e^G after their state
@@ -1611,9 +1610,6 @@ __global__ __launch_bounds__(512) void kda_recur4_kernel(const RecurArgs a) {
                 for (int ks = 0; ks < D / 32; ++ks) Ov[j] = mma<1>(Aq[ks], Bs[j][ks], Ov[j]);
             }
             if (n > 0) flush(n - 1);
-            // the training forward also keeps the chunk-start states for its
-            // backward (the chain is MODE 1's, so h is the same bits)
-            if (a.h) copy_h(n);
         } else {
             copy_h(n);
         }
