@@ -289,6 +289,57 @@ def pmc_summary(fetch_dir, write_dir, calib_mb):
     return out
 
 
+# waves per SIMD of each library kernel at config 2 (occupancy set by its
+# workgroup size and LDS): the prep runs two 8-wave workgroups per CU
+SIMD_WAVES = {"kda_prep_kernel(train)": 4}
+SQ_CYCLE_COUNTERS = ("SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_VALU",
+                     "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_ANY", "SQ_WAIT_ANY")
+
+
+def pmc_sq_summary(*dirs):
+    """Per-wave SQ counters of each library kernel from rocprofv3 --pmc runs,
+    averaged over dispatches and divided by SQ_WAVES; the cycle counters count
+    in units of 4 cycles and are scaled by 4.  bank_conflict_share =
+    SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; valu_busy_simd = waves per SIMD x
+    VALU active cycles / wave cycles."""
+    names = set()
+    for root in dirs:
+        for dirpath, _, files in os.walk(root):
+            for fn in files:
+                if fn.endswith("counter_collection.csv"):
+                    import csv
+                    with open(os.path.join(dirpath, fn), newline="") as f:
+                        names.update(r["Counter_Name"] for r in csv.DictReader(f))
+    per = {}
+    for counter in sorted(names):
+        for root in dirs:
+            seen = {}
+            for _, name, v in _pmc_rows(root, counter):
+                for frag, roles in PROFILE_ROLES.items():
+                    if frag in name:
+                        i = seen.get(frag, 0)
+                        seen[frag] = i + 1
+                        per.setdefault(roles[i % len(roles)], {}).setdefault(counter, []).append(v)
+    out = {"source": "rocprofv3 --pmc (SQ counters, per wave)"}
+    for kname, rec in per.items():
+        avg = {c: sum(v) / len(v) for c, v in rec.items()}
+        waves = avg.get("SQ_WAVES", 0.0)
+        if not waves:
+            continue
+        r = {"waves": round(waves)}
+        for c, v in avg.items():
+            if c == "SQ_WAVES":
+                continue
+            r[c.lower() + "_per_wave"] = round(v * (4 if c in SQ_CYCLE_COUNTERS else 1) / waves, 1)
+        if avg.get("SQ_LDS_IDX_ACTIVE"):
+            r["bank_conflict_share"] = round(avg.get("SQ_LDS_BANK_CONFLICT", 0.0) / avg["SQ_LDS_IDX_ACTIVE"], 4)
+        if avg.get("SQ_WAVE_CYCLES"):
+            r["valu_busy_simd"] = round(SIMD_WAVES.get(kname, 2) * avg.get("SQ_ACTIVE_INST_VALU", 0.0)
+                                        / avg["SQ_WAVE_CYCLES"], 4)
+        out[kname] = r
+    return out
+
+
 def layer_decay_g(B, T, H, D, seed):
     """g of the reference layer at initialisation, drawn on the CPU:
     -A_h softplus(N(0, 0.5^2)) with A_h ~ U[1, 16] per head (the distribution
@@ -587,12 +638,17 @@ def main():
                     help="run one plain fp32 streaming kernel of this many MiB first (PMC byte-counter scale)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE output directories and exit")
+    ap.add_argument("--pmc-sq", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc SQ counter output directories (per wave, per kernel) and exit")
     ap.add_argument("--pmc-mfma", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_BF16 output (and optionally a "
                          "second directory of SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE) and exit")
     args = ap.parse_args()
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calibration_mb or 512), indent=1))
+        return
+    if args.pmc_sq:
+        print(json.dumps(pmc_sq_summary(*args.pmc_sq), indent=1))
         return
     if args.pmc_mfma:
         print(json.dumps(pmc_mfma_summary(*args.pmc_mfma[:2]), indent=1))
