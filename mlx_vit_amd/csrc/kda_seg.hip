@@ -136,9 +136,7 @@ __device__ __forceinline__ f32x4 quad_transpose(const f32x4& x) {
     return y;
 }
 
-constexpr int SEG_NW = 8;   // waves per workgroup of the chain kernels
-
-template <int D, int PASS>
+template <int D, int PASS, int NW>
 struct SegLayout {
     static constexpr int NS = PASS == 0 ? 2 : 3;                   // LDS sets
     static constexpr int RB_W = 2 * D, RB_C = 2 * C;              // swizzled row bytes
@@ -151,10 +149,10 @@ struct SegLayout {
     static constexpr int SET_BYTES = (EG_OFF + 4 * D + 1023) & ~1023;
     static constexpr int BYTES = NS * SET_BYTES;
     static_assert(BYTES <= 160 * 1024, "segment chain LDS");
-    using TW = DmaTileG<C, RB_W, SEG_NW>;
-    using TK = DmaTileG<D, RB_C, SEG_NW>;
-    using TA = DmaTileG<C, RB_C, SEG_NW>;
-    static constexpr int EG_LANES = 4 * D / 16 / SEG_NW;          // 16-byte lanes of e^G per wave
+    using TW = DmaTileG<C, RB_W, NW>;
+    using TK = DmaTileG<D, RB_C, NW>;
+    using TA = DmaTileG<C, RB_C, NW>;
+    static constexpr int EG_LANES = 4 * D / 16 / NW;              // 16-byte lanes of e^G per wave
     // DMA wave-instructions per wave per chunk (W, U, Kb^T [, Qp, Aqk], e^G)
     static constexpr int LI = 2 * TW::COUNT + TK::COUNT + (PASS == 0 ? TW::COUNT + TA::COUNT : 0) + 1;
 };
@@ -164,28 +162,28 @@ struct SegLayout {
 // Pass C (PASS 0): the forward of one segment from its start state.  Pass A
 // (PASS 1): the segment's map (X, M).  One 512-thread workgroup per (b, h,
 // segment); layout, roles and row order in the file comment.
-template <int D, int PASS>
-__global__ __launch_bounds__(512) void kda_segchain_kernel(const SegArgs a) {
+template <int D, int PASS, int NW>
+__global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) {
     using ST = uint16_t;
-    using Lay = SegLayout<D, PASS>;
+    using Lay = SegLayout<D, PASS, NW>;
     using TW = typename Lay::TW;
     using TK = typename Lay::TK;
     using TA = typename Lay::TA;
-    constexpr int NS = Lay::NS, NI = D / BS, KS = D / 32, NJ = (PASS == 0) ? D / (16 * SEG_NW) : 2 * D / (16 * SEG_NW);
+    constexpr int NS = Lay::NS, NI = D / BS, KS = D / 32, NJ = (PASS == 0) ? D / (16 * NW) : 2 * D / (16 * NW);
     constexpr int RB_W = Lay::RB_W, RB_C = Lay::RB_C, LI = Lay::LI;
     static_assert(NJ >= 1 && NS >= 2 && Lay::EG_LANES >= 1, "whole column tiles per wave");
     __shared__ __align__(1024) char smem[Lay::BYTES];
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
               g4 = l >> 4;
-    __builtin_assume(w >= 0 && w < SEG_NW);
+    __builtin_assume(w >= 0 && w < NW);
     const int nsegw = (PASS == 0) ? a.nseg : a.nseg - 1;   // segments this pass covers
     const int bh = blockIdx.x / nsegw, seg = blockIdx.x - bh * nsegw;
     const int b = bh / a.H, h = bh - b * a.H;
     const int n0 = seg * a.seg_len, L = min(a.nc, n0 + a.seg_len) - n0;
     constexpr int CPW = BS * NJ;                                        // columns per wave
-    const bool ident = PASS == 1 && w >= SEG_NW / 2;                    // identity columns (M)
-    const int cb = (PASS == 0) ? CPW * w : CPW * (w % (SEG_NW / 2));    // first owned column
+    const bool ident = PASS == 1 && w >= NW / 2;                        // identity columns (M)
+    const int cb = (PASS == 0) ? CPW * w : CPW * (w % (NW / 2));        // first owned column
     const size_t seg_ix = (size_t)bh * a.nseg + seg;
 
     // ---- the start state of the owned columns (rows in perm_row order) ----
@@ -463,6 +461,11 @@ __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
     }
 }
 
+// waves per workgroup of the segment maps and the segment forwards (eight: two
+// per SIMD; four waves of 32 columns each read half the LDS operand bytes per
+// step but measured slower, 186 against 155 us for config 3's pass C)
+constexpr int SEG_NW = 8;
+
 void seg_plan(int BH, int nc, int* nseg, int* seg_len) {
     // Fill about SEG_TARGET_WG workgroups (the MI355X's CU count: a fixed design
     // constant, so that the plan -- and with it the workspace size and the
@@ -479,7 +482,8 @@ void seg_plan(int BH, int nc, int* nseg, int* seg_len) {
 
 hipError_t launch_seg_map(const SegArgs& a, hipStream_t st) {
     if (a.nseg < 2) return hipSuccess;
-    hipLaunchKernelGGL((kda_segchain_kernel<128, 1>), dim3(a.BH * (a.nseg - 1)), dim3(64 * SEG_NW), 0, st, a);
+    hipLaunchKernelGGL((kda_segchain_kernel<128, 1, SEG_NW>), dim3(a.BH * (a.nseg - 1)), dim3(64 * SEG_NW), 0,
+                       st, a);
     return hipGetLastError();
 }
 
@@ -490,7 +494,8 @@ hipError_t launch_seg_scan(const SegArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_seg_fwd(const SegArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((kda_segchain_kernel<128, 0>), dim3(a.BH * a.nseg), dim3(64 * SEG_NW), 0, st, a);
+    hipLaunchKernelGGL((kda_segchain_kernel<128, 0, SEG_NW>), dim3(a.BH * a.nseg), dim3(64 * SEG_NW), 0, st,
+                       a);
     return hipGetLastError();
 }
 
