@@ -391,19 +391,23 @@ struct PadIo {
     hipStream_t st;
     void* slot(int i) const { return base + P.off[i]; }
     float* fslot(int i) const { return reinterpret_cast<float*>(base + P.off[i]); }
-    // (B, T, H, D) rows in / out; element size es (or gs for g / dg)
-    hipError_t rows_in(const void* src, int i, int esz) const {
-        return kda::launch_resize(src, slot(i), ntok, 1, D, 1, PAD_D, esz, st);
+    // the copies of one direction, gathered and issued as one launch: (B, T, H, D)
+    // rows in / out (element size es, or gs for g / dg) and (B, H, D, D) fp32
+    // states in / out; a null tensor adds nothing
+    kda::ResizeJob jobs[kda::KDA_RESIZE_MAX_JOBS];
+    int njobs = 0;
+    void rows_in(const void* src, int i, int esz) { jobs[njobs++] = {src, slot(i), ntok, 1, D, 1, PAD_D, esz}; }
+    void rows_out(int i, void* dst, int esz) { jobs[njobs++] = {slot(i), dst, ntok, 1, PAD_D, 1, D, esz}; }
+    void state_in(const float* src, int i) {
+        if (src) jobs[njobs++] = {src, slot(i), nbh, D, D, PAD_D, PAD_D, 4};
     }
-    hipError_t rows_out(int i, void* dst, int esz) const {
-        return kda::launch_resize(slot(i), dst, ntok, 1, PAD_D, 1, D, esz, st);
+    void state_out(int i, float* dst) {
+        if (dst) jobs[njobs++] = {slot(i), dst, nbh, PAD_D, PAD_D, D, D, 4};
     }
-    // (B, H, D, D) states in / out, fp32
-    hipError_t state_in(const float* src, int i) const {
-        return kda::launch_resize(src, slot(i), nbh, D, D, PAD_D, PAD_D, 4, st);
-    }
-    hipError_t state_out(int i, float* dst) const {
-        return kda::launch_resize(slot(i), dst, nbh, PAD_D, PAD_D, D, D, 4, st);
+    hipError_t issue() {
+        const hipError_t e = kda::launch_resize_batch(jobs, njobs, st);
+        njobs = 0;
+        return e;
     }
 };
 
@@ -423,18 +427,21 @@ PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, void*
 int run_fwd_padded(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                    const float* s0, void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype,
                    int g_dtype, void* ws, const Layout& L, hipStream_t st, bool prof) {
-    const PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
+    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
     hipError_t e;
-    if ((e = io.rows_in(q, PS_Q, io.es)) != hipSuccess || (e = io.rows_in(k, PS_K, io.es)) != hipSuccess ||
-        (e = io.rows_in(v, PS_V, io.es)) != hipSuccess || (e = io.rows_in(g, PS_G, io.gs)) != hipSuccess ||
-        (s0 && (e = io.state_in(s0, PS_S0)) != hipSuccess))
-        return hip_fail(e, "kda_resize_kernel (pad)");
+    io.rows_in(q, PS_Q, io.es);
+    io.rows_in(k, PS_K, io.es);
+    io.rows_in(v, PS_V, io.es);
+    io.rows_in(g, PS_G, io.gs);
+    io.state_in(s0, PS_S0);
+    if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (pad)");
     const int rc = run_fwd(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
                            s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_O), s_final ? io.fslot(PS_SF) : nullptr, B, T,
                            H, PAD_D, chunk, dtype, g_dtype, ws, (size_t)L.off[KDA_WS_PAD], st, prof, nullptr);
     if (rc != KDA_OK) return rc;
-    if ((e = io.rows_out(PS_O, o, io.es)) != hipSuccess || (s_final && (e = io.state_out(PS_SF, s_final)) != hipSuccess))
-        return hip_fail(e, "kda_resize_kernel (crop)");
+    io.rows_out(PS_O, o, io.es);
+    io.state_out(PS_SF, s_final);
+    if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (crop)");
     return ok();
 }
 
@@ -442,29 +449,33 @@ int run_bwd_padded(int pass, const void* q, const void* k, const void* v, const 
                    const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
                    void* dbeta, float* ds0, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* ws,
                    const Layout& L, hipStream_t st) {
-    const PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
-    hipError_t e = hipSuccess;
+    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
+    hipError_t e;
     // the training backward finds the padded q, k, v, g and s0 where the
     // training forward left them (the pair's workspace is unmodified between
     // the two calls, for the same inputs)
-    if (pass != KDA_PASS_TRAIN &&
-        ((e = io.rows_in(q, PS_Q, io.es)) != hipSuccess || (e = io.rows_in(k, PS_K, io.es)) != hipSuccess ||
-         (e = io.rows_in(v, PS_V, io.es)) != hipSuccess || (e = io.rows_in(g, PS_G, io.gs)) != hipSuccess ||
-         (s0 && (e = io.state_in(s0, PS_S0)) != hipSuccess)))
-        return hip_fail(e, "kda_resize_kernel (pad)");
-    if ((e = io.rows_in(dout, PS_DO, io.es)) != hipSuccess ||
-        (ds_final && (e = io.state_in(ds_final, PS_DSF)) != hipSuccess))
-        return hip_fail(e, "kda_resize_kernel (pad)");
+    if (pass != KDA_PASS_TRAIN) {
+        io.rows_in(q, PS_Q, io.es);
+        io.rows_in(k, PS_K, io.es);
+        io.rows_in(v, PS_V, io.es);
+        io.rows_in(g, PS_G, io.gs);
+        io.state_in(s0, PS_S0);
+    }
+    io.rows_in(dout, PS_DO, io.es);
+    io.state_in(ds_final, PS_DSF);
+    if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (pad)");
     const int rc = run_bwd(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
                            s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_DO), ds_final ? io.fslot(PS_DSF) : nullptr,
                            io.slot(PS_DQ), io.slot(PS_DK), io.slot(PS_DV), io.slot(PS_DG), dbeta,
                            ds0 ? io.fslot(PS_DS0) : nullptr, B, T, H, PAD_D, chunk, dtype, g_dtype, ws,
                            (size_t)L.off[KDA_WS_PAD], st);
     if (rc != KDA_OK) return rc;
-    if ((e = io.rows_out(PS_DQ, dq, io.es)) != hipSuccess || (e = io.rows_out(PS_DK, dk, io.es)) != hipSuccess ||
-        (e = io.rows_out(PS_DV, dv, io.es)) != hipSuccess || (e = io.rows_out(PS_DG, dg, io.gs)) != hipSuccess ||
-        (ds0 && (e = io.state_out(PS_DS0, ds0)) != hipSuccess))
-        return hip_fail(e, "kda_resize_kernel (crop)");
+    io.rows_out(PS_DQ, dq, io.es);
+    io.rows_out(PS_DK, dk, io.es);
+    io.rows_out(PS_DV, dv, io.es);
+    io.rows_out(PS_DG, dg, io.gs);
+    io.state_out(PS_DS0, ds0);
+    if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (crop)");
     return ok();
 }
 

@@ -110,10 +110,17 @@ hipError_t launch_local_wide(const LocalArgs& a, int D, int in_bf16, int g_bf16,
 hipError_t launch_solve(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,
                         hipStream_t st);
 hipError_t launch_state_copy(const float* src, float* dst, size_t n, hipStream_t st);
-// n matrices of rs x cs elements (esize bytes each) into rd x cd: the common
-// top-left block copied, the rest zero (kda_pad.hip)
-hipError_t launch_resize(const void* src, void* dst, size_t n, int rs, int cs, int rd, int cd, int esize,
-                         hipStream_t st);
+// Resize jobs (kda_pad.hip): n matrices of rs x cs elements (esize bytes each)
+// into rd x cd, the common top-left block copied, the rest zero; up to
+// KDA_RESIZE_MAX_JOBS of them in one launch (jobs with n = 0 skipped)
+constexpr int KDA_RESIZE_MAX_JOBS = 8;
+struct ResizeJob {
+    const void* src;
+    void* dst;
+    size_t n;
+    int rs, cs, rd, cd, esize;
+};
+hipError_t launch_resize_batch(const ResizeJob* jobs, int njobs, hipStream_t st);
 
 // C-ABI helpers of kda_api.hip for the other C-ABI translation units (the
 // allocation-free forward): the error setters behind kda_last_error(); the
