@@ -48,13 +48,20 @@ extern "C" {
 /* Workspace regions (see kda_workspace_offsets).  SEGX, SEGM and SEGS exist
  * only for the bf16 forward at D = 128 when it splits the sequence into
  * segments: per (b, h, segment) the segment's state map and start state.
- * PAD exists only at D = 96, which runs the D = 128 kernels on zero-padded
- * copies: the other regions are then those of D = 128, and PAD (last) holds
- * the padded operands and outputs. */
+ * PAD and PADB exist only at D = 96, which runs the D = 128 kernels on
+ * zero-padded copies: the other regions are then those of D = 128; PAD holds
+ * the padded q, k, v, g, s0 (and, for the forward passes, o and s_final),
+ * PADB the backward's padded dout, dq, dk, dv, dg, ds_final and ds0.
+ * Order: passes 0 and 1 lay the regions out in this order.  Pass 2 puts first
+ * the regions kda_fwd_train writes and kda_bwd_train reads (the kept part,
+ * kda_train_kept_size bytes: W .. EG and PAD) and after them those only the
+ * backward uses (H, DH, VP, DVP, PADB), so that the backward's part can be a
+ * buffer of its own (kda_bwd_train_split). */
 enum kda_ws_region {
     KDA_WS_W = 0, KDA_WS_U, KDA_WS_QP, KDA_WS_QPT, KDA_WS_KB, KDA_WS_KBT, KDA_WS_WT,
     KDA_WS_AQK, KDA_WS_AQKT, KDA_WS_AKK, KDA_WS_TII, KDA_WS_EG, KDA_WS_H, KDA_WS_DH,
-    KDA_WS_VP, KDA_WS_DVP, KDA_WS_SEGX, KDA_WS_SEGM, KDA_WS_SEGS, KDA_WS_PAD, KDA_WS_NREGIONS
+    KDA_WS_VP, KDA_WS_DVP, KDA_WS_SEGX, KDA_WS_SEGM, KDA_WS_SEGS, KDA_WS_PAD, KDA_WS_PADB,
+    KDA_WS_NREGIONS
 };
 
 /* ABI version of this header (bumped on any signature change). */
@@ -72,6 +79,17 @@ size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int d
  * inspect intermediates.  offsets must hold KDA_WS_NREGIONS entries. */
 int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int dtype,
                           int64_t* offsets);
+
+/* Bytes at the start of the training pair's (pass 2) workspace that
+ * kda_fwd_train writes and kda_bwd_train reads -- the per-chunk factors (and,
+ * at D = 96, the padded inputs) -- all a caller must keep between the two
+ * calls; 0 on invalid arguments.  The rest of kda_workspace_size(2, ...) is
+ * the backward's own scratch (the chunk-boundary states and their adjoints,
+ * V' and dV'), which kda_bwd_train_split takes as a separate buffer.  No
+ * counterpart in the reference, whose forward keeps U_traj and S_traj
+ * (nope_gdn_mlx.py:2734-2745): it serves autograd callers that hold only what
+ * the backward needs from the forward. */
+size_t kda_train_kept_size(int B, int T, int H, int D, int chunk, int dtype);
 
 /* Forward: o and (if s_final != NULL) the final state.  s0 == NULL means a zero
  * initial state.
@@ -122,6 +140,8 @@ int kda_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, 
  * No state is kept: kda_bwd_train recomputes the chunk-boundary states from
  * the factors and s0.  At D = 96 the pair's workspace also keeps the padded
  * q, k, v, g and s0 for the backward.
+ * kda_fwd_train needs ws_bytes >= kda_train_kept_size (it writes nothing past
+ * that); kda_bwd_train needs the whole pass-2 workspace, kda_workspace_size(2).
  * kda_bwd_train is kda_bwd without its prep: it requires the workspace that
  * kda_fwd_train filled for the same q, k, v, g, beta and s0 (and the same B,
  * T, H, D, dtype), unmodified in between, and returns the same gradients as
@@ -138,6 +158,20 @@ int kda_bwd_train(const void* q, const void* k, const void* v, const void* g, co
                   void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
                   int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
                   void* workspace, size_t ws_bytes, void* stream);
+
+/* kda_bwd_train with the backward's scratch in a buffer of its own: kept is
+ * the workspace kda_fwd_train filled (kept_bytes >= kda_train_kept_size),
+ * scratch any 256-byte aligned device buffer of scratch_bytes >=
+ * kda_workspace_size(2, ...) - kda_train_kept_size(...) (its contents are
+ * not read; NULL when that difference is 0).  Same gradients as kda_bwd_train,
+ * bit for bit.  No counterpart in the reference (see kda_train_kept_size): for
+ * autograd callers that keep only the forward's factors between the passes. */
+int kda_bwd_train_split(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                        const float* s0, const void* dout, const float* ds_final,
+                        void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
+                        int B, int T, int H, int D, int chunk, int dtype, int g_dtype,
+                        const void* kept, size_t kept_bytes, void* scratch, size_t scratch_bytes,
+                        void* stream);
 
 /* Forward (pass KDA_PASS_FWD, workspace as kda_fwd) or training forward
  * (KDA_PASS_TRAIN, as kda_fwd_train) with the layer's output norm fused into

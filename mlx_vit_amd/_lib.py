@@ -11,7 +11,7 @@ import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkda_hip.so")
 
-ABI_VERSION = 3   # kda_abi_version() of the header this binding follows
+ABI_VERSION = 4   # kda_abi_version() of the header this binding follows
 
 KDA_OK = 0
 KDA_E_INVALID = -1
@@ -29,7 +29,7 @@ KDA_LAYER_PRODUCER = 0
 KDA_LAYER_RMSNORM = 1
 
 WS_REGIONS = ("W", "U", "Qp", "QpT", "Kb", "KbT", "WT", "Aqk", "AqkT", "Akk", "Tii", "eG",
-              "h", "dh", "Vp", "dVp", "SegX", "SegM", "SegS", "Pad")
+              "h", "dh", "Vp", "dVp", "SegX", "SegM", "SegS", "Pad", "PadB")
 
 # every function the header declares, with its ctypes signature
 _P, _I, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -44,6 +44,8 @@ SIGNATURES = {
     "kda_fwd_train": ([_P] * 8 + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_fwd_noalloc": ([_P] * 8 + [_I] * 7 + [_P], _I),
     "kda_bwd_train": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P], _I),
+    "kda_train_kept_size": ([_I] * 6, _Z),
+    "kda_bwd_train_split": ([_P] * 14 + [_I] * 7 + [_P, _Z, _P, _Z, _P], _I),
     "kda_fwd_gated": ([_I] + [_P] * 7 + [_L, _P, _F, _P, _P, _L, _P] + [_I] * 7 + [_P, _Z, _P], _I),
     "kda_solve_unit_triangular": ([_P] * 3 + [_I] * 4 + [_P], _I),
     "kda_layer_producer_fwd": ([_P] * 5 + [_L] * 3 + [_P] * 9 + [_I] * 4 + [_F] * 2 + [_I] * 2 + [_P], _I),

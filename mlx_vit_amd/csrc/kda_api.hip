@@ -34,7 +34,16 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 struct Layout {
     int64_t off[KDA_WS_NREGIONS];
     size_t total;
+    // pass 2: bytes of the regions the training forward writes and the
+    // backward reads (placed first); the backward's own regions follow.
+    // Passes 0 and 1: total.
+    size_t kept;
 };
+
+// regions only the backward writes and reads (the training pair's scratch)
+bool backward_region(int r) {
+    return r == KDA_WS_H || r == KDA_WS_DH || r == KDA_WS_VP || r == KDA_WS_DVP || r == KDA_WS_PADB;
+}
 
 int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, bool bwd) {
     if (B < 0 || T < 0 || H < 0) return fail(KDA_E_INVALID, "negative size: B=%d T=%d H=%d", B, T, H);
@@ -71,9 +80,14 @@ constexpr int PAD_D = 128;
 bool padded_head(int D) { return D == 96; }
 enum PadSlot { PS_Q, PS_K, PS_V, PS_G, PS_O, PS_DO, PS_DQ, PS_DK, PS_DV, PS_DG, PS_S0, PS_SF, PS_DSF, PS_DS0, PS_N };
 
+// The slots of the backward's padded cotangents and gradients live in the
+// PADB region, the others (inputs, the forward's outputs) in PAD.
+bool pad_backward_slot(int i) { return i == PS_DO || (i >= PS_DQ && i <= PS_DG) || i == PS_DSF || i == PS_DS0; }
+
 struct PadLayout {
-    size_t off[PS_N];
-    size_t total;
+    size_t off[PS_N];   // within the slot's region
+    size_t total;       // PAD
+    size_t total_b;     // PADB
 };
 
 void make_pad_layout(int pass, int B, int T, int H, int dtype, PadLayout& P) {
@@ -93,38 +107,25 @@ void make_pad_layout(int pass, int B, int T, int H, int dtype, PadLayout& P) {
         sz[PS_DG] = tok * 4;
         sz[PS_DSF] = sz[PS_DS0] = st;
     }
-    size_t cur = 0;
+    size_t cur = 0, curb = 0;
     for (int i = 0; i < PS_N; ++i) {
-        P.off[i] = cur;
-        cur += (sz[i] + 255) & ~(size_t)255;
+        size_t& c = pad_backward_slot(i) ? curb : cur;
+        P.off[i] = c;
+        c += (sz[i] + 255) & ~(size_t)255;
     }
     P.total = cur;
+    P.total_b = curb;
 }
 
-// Region sizes in bytes.  Operand slabs use the input dtype's element size;
-// eG, Akk and Tii are fp32.  Akk, Tii and V' exist for fp32 inputs only.
-void make_layout_at(int pass, int B, int T, int H, int D, int dtype, Layout& L);
-
-void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
-    if (!padded_head(D)) {
-        make_layout_at(pass, B, T, H, D, dtype, L);
-        L.off[KDA_WS_PAD] = -1;
-        return;
-    }
-    make_layout_at(pass, B, T, H, PAD_D, dtype, L);
-    PadLayout P;
-    make_pad_layout(pass, B, T, H, dtype, P);
-    L.off[KDA_WS_PAD] = (int64_t)L.total;
-    L.total += P.total;
-}
-
-void make_layout_at(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
+// Region sizes in bytes at the kernels' head dimension D.  Operand slabs use
+// the input dtype's element size; eG, Akk and Tii are fp32.  Akk, Tii and V'
+// exist for fp32 inputs and at D = 128 only.
+void region_sizes(int pass, int B, int T, int H, int D, int dtype, size_t* sz) {
     const size_t nc = (size_t)(T + kda::C - 1) / kda::C;
     const size_t N = (size_t)B * H * nc;
     const size_t es = (dtype == KDA_DTYPE_BF16) ? 2 : 4;
     const size_t CD = N * kda::C * D * es, CC = N * kda::C * kda::C * es, DD = N * (size_t)D * D * es;
     const size_t TI = N * kda::NB * kda::BS * kda::BS * 4, EG = N * D * 4;
-    size_t sz[KDA_WS_NREGIONS] = {0};
     // bf16 D = 64: the recurrences read Kb, Qp, W and Aqk through transposing LDS
     // reads, so no transposed slab exists and both passes use Qp and Aqk
     const bool tr = dtype == KDA_DTYPE_BF16 && D == 64;
@@ -160,22 +161,64 @@ void make_layout_at(int pass, int B, int T, int H, int D, int dtype, Layout& L) 
         sz[KDA_WS_SEGM] = per;
         sz[KDA_WS_SEGS] = per;
     }
+}
+
+// Passes 0 and 1: the regions in enum order.  Pass 2: the regions the
+// training forward writes first, then the backward's own.  D = 96: the D = 128
+// regions and the PAD / PADB regions of the padded copies.
+void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
+    size_t sz[KDA_WS_NREGIONS] = {0};
+    region_sizes(pass, B, T, H, padded_head(D) ? PAD_D : D, dtype, sz);
+    if (padded_head(D)) {
+        PadLayout P;
+        make_pad_layout(pass, B, T, H, dtype, P);
+        sz[KDA_WS_PAD] = P.total;
+        sz[KDA_WS_PADB] = P.total_b;
+    }
     size_t cur = 0;
-    for (int r = 0; r < KDA_WS_PAD; ++r) {
+    auto place = [&](int r) {
         if (sz[r] == 0) {
             L.off[r] = -1;
-            continue;
+            return;
         }
         L.off[r] = (int64_t)cur;
         cur += (sz[r] + 255) & ~(size_t)255;
+    };
+    if (pass == KDA_PASS_TRAIN) {
+        for (int r = 0; r < KDA_WS_NREGIONS; ++r)
+            if (!backward_region(r)) place(r);
+        L.kept = cur;
+        for (int r = 0; r < KDA_WS_NREGIONS; ++r)
+            if (backward_region(r)) place(r);
+    } else {
+        for (int r = 0; r < KDA_WS_NREGIONS; ++r) place(r);
+        L.kept = cur;
     }
     L.total = cur;
 }
 
-void* region(void* ws, const Layout& L, int r) {
-    return L.off[r] < 0 ? nullptr : static_cast<void*>(static_cast<char*>(ws) + L.off[r]);
+// The regions' addresses: those below L.kept in `kept`, the others in
+// `scratch` (null: the caller touches none of them).
+struct Ws {
+    void* r[KDA_WS_NREGIONS];
+};
+
+Ws resolve(const Layout& L, void* kept, void* scratch) {
+    Ws w;
+    for (int r = 0; r < KDA_WS_NREGIONS; ++r) {
+        const int64_t o = L.off[r];
+        if (o < 0)
+            w.r[r] = nullptr;
+        else if ((size_t)o < L.kept)
+            w.r[r] = static_cast<char*>(kept) + o;
+        else
+            w.r[r] = scratch ? static_cast<char*>(scratch) + (o - (int64_t)L.kept) : nullptr;
+    }
+    return w;
 }
-float* fregion(void* ws, const Layout& L, int r) { return static_cast<float*>(region(ws, L, r)); }
+
+void* region(const Ws& ws, int r) { return ws.r[r]; }
+float* fregion(const Ws& ws, int r) { return static_cast<float*>(ws.r[r]); }
 
 int check_io(const void* p, const char* name, int /*dtype*/, bool nullable) {
     if (!p) return nullable ? KDA_OK : fail(KDA_E_INVALID, "%s is NULL", name);
@@ -333,31 +376,32 @@ namespace {
 
 bool valid_pass(int pass) { return pass == KDA_PASS_FWD || pass == KDA_PASS_BWD || pass == KDA_PASS_TRAIN; }
 
-int check_workspace(void* workspace, size_t ws_bytes, const Layout& L) {
-    if (!workspace || ws_bytes < L.total)
-        return fail(KDA_E_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? ws_bytes : 0, L.total);
-    if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "workspace is not 256-byte aligned");
+int check_workspace(const void* workspace, size_t ws_bytes, size_t need, const char* name = "workspace") {
+    if (need == 0) return KDA_OK;
+    if (!workspace || ws_bytes < need)
+        return fail(KDA_E_WORKSPACE, "%s of %zu bytes given, %zu needed", name, workspace ? ws_bytes : 0, need);
+    if (!aligned(workspace, 256)) return fail(KDA_E_INVALID, "%s is not 256-byte aligned", name);
     return KDA_OK;
 }
 
 // Prep: the forward's outputs (pass 0), the backward's (pass 1) or both (pass 2).
 hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
-                            void* ws, const Layout& L, int T, int H, int D, int nchunks, int in_bf16, int g_bf16,
+                            const Ws& ws, int T, int H, int D, int nchunks, int in_bf16, int g_bf16,
                             hipStream_t st, bool prof = true) {
     kda::PrepArgs pa = {};
     pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
-    pa.W = region(ws, L, KDA_WS_W);
-    pa.U = region(ws, L, KDA_WS_U);
-    pa.KbT = region(ws, L, KDA_WS_KBT);
-    pa.eG = fregion(ws, L, KDA_WS_EG);
-    pa.Qp = region(ws, L, KDA_WS_QP);
-    pa.Aqk = region(ws, L, KDA_WS_AQK);
-    pa.WT = region(ws, L, KDA_WS_WT);
-    pa.QpT = region(ws, L, KDA_WS_QPT);
-    pa.Kb = region(ws, L, KDA_WS_KB);
-    pa.AqkT = region(ws, L, KDA_WS_AQKT);
-    pa.Akk = fregion(ws, L, KDA_WS_AKK);
-    pa.Tii = fregion(ws, L, KDA_WS_TII);
+    pa.W = region(ws, KDA_WS_W);
+    pa.U = region(ws, KDA_WS_U);
+    pa.KbT = region(ws, KDA_WS_KBT);
+    pa.eG = fregion(ws, KDA_WS_EG);
+    pa.Qp = region(ws, KDA_WS_QP);
+    pa.Aqk = region(ws, KDA_WS_AQK);
+    pa.WT = region(ws, KDA_WS_WT);
+    pa.QpT = region(ws, KDA_WS_QPT);
+    pa.Kb = region(ws, KDA_WS_KB);
+    pa.AqkT = region(ws, KDA_WS_AQKT);
+    pa.Akk = fregion(ws, KDA_WS_AKK);
+    pa.Tii = fregion(ws, KDA_WS_TII);
     pa.T = T; pa.H = H; pa.nc = (T + kda::C - 1) / kda::C;
     const int id = pass == KDA_PASS_FWD ? PROF_PREP_FWD : pass == KDA_PASS_BWD ? PROF_PREP_BWD : PROF_PREP_TRAIN;
     return timed(id, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, nchunks, st); }, prof);
@@ -373,24 +417,24 @@ struct Epilogue {
     int64_t ld_y;
 };
 
-int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
-            void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
-            size_t ws_bytes, void* stream, bool prof, const Epilogue* epi);
-int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
-            const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
-            int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
-            void* stream);
+int fwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+               const float* s0, void* o, float* s_final, int B, int T, int H, int D, int dtype, int g_dtype,
+               const Ws& ws, hipStream_t st, bool prof, const Epilogue* epi);
+int bwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+               const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
+               void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws,
+               hipStream_t st);
 
-// The padded head dimension's slots in the workspace (the D = 128 layout
-// first, the PAD region after it), and the copies in and out of them.
+// The padded head dimension's slots in the workspace's PAD and PADB regions,
+// and the copies in and out of them.
 struct PadIo {
-    char* base;
+    char *base, *base_b;
     PadLayout P;
     size_t ntok, nbh;
     int D, es, gs;
     hipStream_t st;
-    void* slot(int i) const { return base + P.off[i]; }
-    float* fslot(int i) const { return reinterpret_cast<float*>(base + P.off[i]); }
+    void* slot(int i) const { return (pad_backward_slot(i) ? base_b : base) + P.off[i]; }
+    float* fslot(int i) const { return reinterpret_cast<float*>(slot(i)); }
     // the copies of one direction, gathered and issued as one launch: (B, T, H, D)
     // rows in / out (element size es, or gs for g / dg) and (B, H, D, D) fp32
     // states in / out; a null tensor adds nothing
@@ -411,9 +455,10 @@ struct PadIo {
     }
 };
 
-PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, void* ws, const Layout& L, hipStream_t st) {
+PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws, hipStream_t st) {
     PadIo io;
-    io.base = static_cast<char*>(ws) + L.off[KDA_WS_PAD];
+    io.base = static_cast<char*>(ws.r[KDA_WS_PAD]);
+    io.base_b = static_cast<char*>(ws.r[KDA_WS_PADB]);
     make_pad_layout(pass, B, T, H, dtype, io.P);
     io.ntok = (size_t)B * T * H;
     io.nbh = (size_t)B * H;
@@ -426,8 +471,8 @@ PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, void*
 
 int run_fwd_padded(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                    const float* s0, void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype,
-                   int g_dtype, void* ws, const Layout& L, hipStream_t st, bool prof) {
-    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
+                   int g_dtype, const Ws& ws, hipStream_t st, bool prof) {
+    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, st);
     hipError_t e;
     io.rows_in(q, PS_Q, io.es);
     io.rows_in(k, PS_K, io.es);
@@ -435,9 +480,9 @@ int run_fwd_padded(int pass, const void* q, const void* k, const void* v, const 
     io.rows_in(g, PS_G, io.gs);
     io.state_in(s0, PS_S0);
     if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (pad)");
-    const int rc = run_fwd(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
-                           s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_O), s_final ? io.fslot(PS_SF) : nullptr, B, T,
-                           H, PAD_D, chunk, dtype, g_dtype, ws, (size_t)L.off[KDA_WS_PAD], st, prof, nullptr);
+    const int rc = fwd_launch(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
+                              s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_O), s_final ? io.fslot(PS_SF) : nullptr, B,
+                              T, H, PAD_D, dtype, g_dtype, ws, st, prof, nullptr);
     if (rc != KDA_OK) return rc;
     io.rows_out(PS_O, o, io.es);
     io.state_out(PS_SF, s_final);
@@ -447,9 +492,9 @@ int run_fwd_padded(int pass, const void* q, const void* k, const void* v, const 
 
 int run_bwd_padded(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                    const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
-                   void* dbeta, float* ds0, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* ws,
-                   const Layout& L, hipStream_t st) {
-    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, L, st);
+                   void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws,
+                   hipStream_t st) {
+    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, st);
     hipError_t e;
     // the training backward finds the padded q, k, v, g and s0 where the
     // training forward left them (the pair's workspace is unmodified between
@@ -464,11 +509,10 @@ int run_bwd_padded(int pass, const void* q, const void* k, const void* v, const 
     io.rows_in(dout, PS_DO, io.es);
     io.state_in(ds_final, PS_DSF);
     if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (pad)");
-    const int rc = run_bwd(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
-                           s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_DO), ds_final ? io.fslot(PS_DSF) : nullptr,
-                           io.slot(PS_DQ), io.slot(PS_DK), io.slot(PS_DV), io.slot(PS_DG), dbeta,
-                           ds0 ? io.fslot(PS_DS0) : nullptr, B, T, H, PAD_D, chunk, dtype, g_dtype, ws,
-                           (size_t)L.off[KDA_WS_PAD], st);
+    const int rc = bwd_launch(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
+                              s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_DO), ds_final ? io.fslot(PS_DSF) : nullptr,
+                              io.slot(PS_DQ), io.slot(PS_DK), io.slot(PS_DV), io.slot(PS_DG), dbeta,
+                              ds0 ? io.fslot(PS_DS0) : nullptr, B, T, H, PAD_D, dtype, g_dtype, ws, st);
     if (rc != KDA_OK) return rc;
     io.rows_out(PS_DQ, dq, io.es);
     io.rows_out(PS_DK, dk, io.es);
@@ -501,33 +545,40 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
         return rc;
     Layout L;
     make_layout(pass, B, T, H, D, dtype, L);
-    if ((rc = check_workspace(workspace, ws_bytes, L))) return rc;
+    // the training forward writes only the kept part of the pair's workspace
+    if ((rc = check_workspace(workspace, ws_bytes, pass == KDA_PASS_TRAIN ? L.kept : L.total))) return rc;
+    const Ws ws = resolve(L, workspace, nullptr);
     if (padded_head(D)) {
         if (epi) return fail(KDA_E_UNSUPPORTED, "D=%d has no fused epilogue", D);
-        return run_fwd_padded(pass, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, workspace,
-                              L, st, prof);
+        return run_fwd_padded(pass, q, k, v, g, beta, s0, o, s_final, B, T, H, D, chunk, dtype, g_dtype, ws, st,
+                              prof);
     }
+    return fwd_launch(pass, q, k, v, g, beta, s0, o, s_final, B, T, H, D, dtype, g_dtype, ws, st, prof, epi);
+}
 
+// The forward's launches on resolved workspace regions (shapes checked).
+int fwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+               const float* s0, void* o, float* s_final, int B, int T, int H, int D, int dtype, int g_dtype,
+               const Ws& ws, hipStream_t st, bool prof, const Epilogue* epi) {
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
-    hipError_t e =
-        launch_prep_pass(pass, q, k, v, g, beta, workspace, L, T, H, D, BH * nc, in_bf16, g_bf16, st, prof);
+    hipError_t e = launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st, prof);
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     int nseg, seg_len;
     if (!epi && seg_forward(pass, B, T, H, D, dtype, &nseg, &seg_len)) {
         // bf16 D = 128, more than one segment: segment maps, start states, forward
         kda::SegArgs sa = {};
-        sa.W = region(workspace, L, KDA_WS_W);
-        sa.U = region(workspace, L, KDA_WS_U);
-        sa.Qp = region(workspace, L, KDA_WS_QP);
-        sa.KbT = region(workspace, L, KDA_WS_KBT);
-        sa.Aqk = region(workspace, L, KDA_WS_AQK);
-        sa.eG = fregion(workspace, L, KDA_WS_EG);
+        sa.W = region(ws, KDA_WS_W);
+        sa.U = region(ws, KDA_WS_U);
+        sa.Qp = region(ws, KDA_WS_QP);
+        sa.KbT = region(ws, KDA_WS_KBT);
+        sa.Aqk = region(ws, KDA_WS_AQK);
+        sa.eG = fregion(ws, KDA_WS_EG);
         sa.s0 = s0; sa.s_final = s_final; sa.o = o;
-        sa.segX = fregion(workspace, L, KDA_WS_SEGX);
-        sa.segM = static_cast<uint16_t*>(region(workspace, L, KDA_WS_SEGM));
-        sa.segS = fregion(workspace, L, KDA_WS_SEGS);
+        sa.segX = fregion(ws, KDA_WS_SEGX);
+        sa.segM = static_cast<uint16_t*>(region(ws, KDA_WS_SEGM));
+        sa.segS = fregion(ws, KDA_WS_SEGS);
         sa.T = T; sa.H = H; sa.nc = nc; sa.BH = BH; sa.nseg = nseg; sa.seg_len = seg_len;
         e = timed(PROF_SEG_MAP, st, [&] { return kda::launch_seg_map(sa, st); }, prof);
         if (e != hipSuccess) return hip_fail(e, "kda_segchain_kernel(map)");
@@ -539,13 +590,13 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
     }
 
     kda::RecurArgs ra = {};
-    ra.W = region(workspace, L, KDA_WS_W);
-    ra.U = region(workspace, L, KDA_WS_U);
-    ra.Qp = region(workspace, L, KDA_WS_QP);
-    ra.KbT = region(workspace, L, KDA_WS_KBT);
-    ra.Kb = region(workspace, L, KDA_WS_KB);
-    ra.Aqk = region(workspace, L, KDA_WS_AQK);
-    ra.eG = fregion(workspace, L, KDA_WS_EG);
+    ra.W = region(ws, KDA_WS_W);
+    ra.U = region(ws, KDA_WS_U);
+    ra.Qp = region(ws, KDA_WS_QP);
+    ra.KbT = region(ws, KDA_WS_KBT);
+    ra.Kb = region(ws, KDA_WS_KB);
+    ra.Aqk = region(ws, KDA_WS_AQK);
+    ra.eG = fregion(ws, KDA_WS_EG);
     ra.s0 = s0; ra.s_final = s_final; ra.o = o;
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
     if (epi) {
@@ -559,10 +610,12 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
 // pass 1: prep from the inputs, then the backward; pass 2: the workspace holds
 // the per-chunk factors kda_fwd_train wrote for the same inputs, so the prep is
 // skipped.  Either way the chunk-boundary states are recomputed.
+// scratch == nullptr: one workspace of the pass's whole layout; otherwise
+// (pass 2 only) `workspace` holds the kept part and `scratch` the backward's.
 int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
             const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg, void* dbeta, float* ds0,
-            int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
-            void* stream) {
+            int B, int T, int H, int D, int chunk, int dtype, int g_dtype, const void* workspace, size_t ws_bytes,
+            void* scratch, size_t scratch_bytes, bool split, void* stream) {
     int rc = check_shape(B, T, H, D, chunk, dtype, g_dtype, true);
     if (rc) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -583,43 +636,62 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
         return rc;
     Layout L;
     make_layout(pass, B, T, H, D, dtype, L);
-    if ((rc = check_workspace(workspace, ws_bytes, L))) return rc;
+    // the backward reads the kept part of a training workspace, never writes it
+    void* kept = const_cast<void*>(workspace);
+    Ws ws;
+    if (split) {
+        if ((rc = check_workspace(workspace, ws_bytes, L.kept)) ||
+            (rc = check_workspace(scratch, scratch_bytes, L.total - L.kept, "scratch")))
+            return rc;
+        ws = resolve(L, kept, scratch);
+    } else {
+        if ((rc = check_workspace(workspace, ws_bytes, L.total))) return rc;
+        ws = resolve(L, kept, static_cast<char*>(kept) + L.kept);
+    }
     if (padded_head(D))
         return run_bwd_padded(pass, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D,
-                              chunk, dtype, g_dtype, workspace, L, st);
+                              dtype, g_dtype, ws, st);
+    return bwd_launch(pass, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D, dtype,
+                      g_dtype, ws, st);
+}
 
+// The backward's launches on resolved workspace regions (shapes checked).
+int bwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
+               const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
+               void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws,
+               hipStream_t st) {
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
     hipError_t e;
     if (pass == KDA_PASS_BWD) {
-        e = launch_prep_pass(pass, q, k, v, g, beta, workspace, L, T, H, D, BH * nc, in_bf16, g_bf16, st);
+        e = launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st);
         if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
     }
-    void* W = region(workspace, L, KDA_WS_W);
-    void* U = region(workspace, L, KDA_WS_U);
-    void* KbT = region(workspace, L, KDA_WS_KBT);
-    float* eG = fregion(workspace, L, KDA_WS_EG);
-    void* hS = region(workspace, L, KDA_WS_H);
-    void* dhS = region(workspace, L, KDA_WS_DH);
-    void* Vp = region(workspace, L, KDA_WS_VP);
-    void* dVp = region(workspace, L, KDA_WS_DVP);
+    void* W = region(ws, KDA_WS_W);
+    void* U = region(ws, KDA_WS_U);
+    void* KbT = region(ws, KDA_WS_KBT);
+    float* eG = fregion(ws, KDA_WS_EG);
+    void* hS = region(ws, KDA_WS_H);
+    void* dhS = region(ws, KDA_WS_DH);
+    void* Vp = region(ws, KDA_WS_VP);
+    void* dVp = region(ws, KDA_WS_DVP);
 
     // chunk-boundary states, recomputed from the per-chunk factors
     kda::RecurArgs ra = {};
     ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
-    ra.Kb = region(workspace, L, KDA_WS_KB);
+    ra.Kb = region(ws, KDA_WS_KB);
     ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
     e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
 
     kda::DhArgs da = {};
-    da.AqkT = region(workspace, L, KDA_WS_AQKT);
-    da.Aqk = region(workspace, L, KDA_WS_AQK);
-    da.Qp = region(workspace, L, KDA_WS_QP);
+    da.AqkT = region(ws, KDA_WS_AQKT);
+    da.Aqk = region(ws, KDA_WS_AQK);
+    da.Qp = region(ws, KDA_WS_QP);
     da.W = W;
-    da.Kb = region(workspace, L, KDA_WS_KB);
-    da.QpT = region(workspace, L, KDA_WS_QPT);
-    da.WT = region(workspace, L, KDA_WS_WT);
+    da.Kb = region(ws, KDA_WS_KB);
+    da.QpT = region(ws, KDA_WS_QPT);
+    da.WT = region(ws, KDA_WS_WT);
     da.eG = eG; da.dout = dout; da.dsf = ds_final; da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
     da.T = T; da.H = H; da.nc = nc; da.BH = BH;
     e = timed(PROF_DH, st, [&] { return kda::launch_dh(da, D, in_bf16, st); });
@@ -627,7 +699,7 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
 
     kda::LocalArgs la = {};
     la.q = q; la.k = k; la.v = v; la.g = g; la.beta = beta; la.dout = dout;
-    la.W = W; la.U = U; la.Akk = fregion(workspace, L, KDA_WS_AKK); la.Tii = fregion(workspace, L, KDA_WS_TII);
+    la.W = W; la.U = U; la.Akk = fregion(ws, KDA_WS_AKK); la.Tii = fregion(ws, KDA_WS_TII);
     la.h = hS; la.dh = dhS; la.Vp = Vp; la.dVp = dVp;
     la.dq = dq; la.dk = dk; la.dv = dv; la.dg = dg; la.dbeta = dbeta;
     la.T = T; la.H = H; la.nc = nc;
@@ -677,7 +749,7 @@ int api_fwd_on_workspace(const void* q, const void* k, const void* v, const void
 // ----------------------------------------------------------------------------
 extern "C" {
 
-int kda_abi_version(void) { return 3; }
+int kda_abi_version(void) { return 4; }
 
 const char* kda_last_error(void) { return g_err.c_str(); }
 
@@ -691,6 +763,14 @@ size_t kda_workspace_size(int pass, int B, int T, int H, int D, int chunk, int d
     make_layout(pass, B, T, H, D, dtype, L);
     ok();
     return L.total;
+}
+
+size_t kda_train_kept_size(int B, int T, int H, int D, int chunk, int dtype) {
+    if (check_shape(B, T, H, D, chunk, dtype, KDA_DTYPE_F32, true) != KDA_OK) return 0;
+    Layout L;
+    make_layout(KDA_PASS_TRAIN, B, T, H, D, dtype, L);
+    ok();
+    return L.kept;
 }
 
 int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int dtype, int64_t* offsets) {
@@ -750,7 +830,7 @@ int kda_bwd(const void* q, const void* k, const void* v, const void* g, const vo
             int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace, size_t ws_bytes,
             void* stream) {
     return run_bwd(KDA_PASS_BWD, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D, chunk,
-                   dtype, g_dtype, workspace, ws_bytes, stream);
+                   dtype, g_dtype, workspace, ws_bytes, nullptr, 0, false, stream);
 }
 
 int kda_bwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta, const float* s0,
@@ -758,7 +838,16 @@ int kda_bwd_train(const void* q, const void* k, const void* v, const void* g, co
                   float* ds0, int B, int T, int H, int D, int chunk, int dtype, int g_dtype, void* workspace,
                   size_t ws_bytes, void* stream) {
     return run_bwd(KDA_PASS_TRAIN, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D,
-                   chunk, dtype, g_dtype, workspace, ws_bytes, stream);
+                   chunk, dtype, g_dtype, workspace, ws_bytes, nullptr, 0, false, stream);
+}
+
+int kda_bwd_train_split(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                        const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv,
+                        void* dg, void* dbeta, float* ds0, int B, int T, int H, int D, int chunk, int dtype,
+                        int g_dtype, const void* kept, size_t kept_bytes, void* scratch, size_t scratch_bytes,
+                        void* stream) {
+    return run_bwd(KDA_PASS_TRAIN, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D,
+                   chunk, dtype, g_dtype, kept, kept_bytes, scratch, scratch_bytes, true, stream);
 }
 
 int kda_solve_unit_triangular(const float* M, const float* b, float* y, int BH, int Cm, int N, int upper,

@@ -101,17 +101,28 @@ def workspace_offsets(pass_: int, B: int, T: int, H: int, D: int, dtype: torch.d
     return {name: int(arr[i]) for i, name in enumerate(_lib.WS_REGIONS)}
 
 
+def train_kept_bytes(B: int, T: int, H: int, D: int, dtype: torch.dtype = torch.bfloat16) -> int:
+    """Bytes of the training pair's workspace that ``kda_forward_train`` writes
+    and ``kda_backward_train`` reads (the rest is the backward's scratch)."""
+    lib = _lib.load()
+    n = lib.kda_train_kept_size(B, T, H, D, CHUNK, _DTYPE_CODE.get(dtype, 0))
+    if n == 0 and B * T * H > 0:
+        raise ValueError(_lib.last_error())
+    return int(n)
+
+
 def _workspace(pass_: int, B: int, T: int, H: int, D: int, dev: torch.device, dtype,
-               given: Optional[torch.Tensor] = None) -> torch.Tensor:
+               given: Optional[torch.Tensor] = None, nbytes: Optional[int] = None) -> torch.Tensor:
     """The caller's workspace (checked: a contiguous uint8 tensor on the
-    inputs' device; its size is checked by the library) or a new one."""
+    inputs' device; its size is checked by the library) or a new one of
+    ``nbytes`` (default: the pass's whole workspace)."""
     if given is not None:
         if not isinstance(given, torch.Tensor) or given.dtype != torch.uint8 or not given.is_contiguous():
             raise ValueError("workspace must be a contiguous torch.uint8 tensor")
         if given.device != dev:
             raise ValueError(f"workspace is on {given.device}, q on {dev}")
         return given
-    n = workspace_bytes(pass_, B, T, H, D, dtype)
+    n = workspace_bytes(pass_, B, T, H, D, dtype) if nbytes is None else nbytes
     return torch.empty(max(n, 256), dtype=torch.uint8, device=dev)
 
 
@@ -140,7 +151,9 @@ def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CH
                       ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Forward that also keeps the per-chunk factors the backward needs.
     Returns (o, final_state, workspace); pass the workspace, unmodified, to
-    ``kda_backward_train`` with the same inputs."""
+    ``kda_backward_train`` with the same inputs.  A new workspace holds only
+    the kept part (``train_kept_bytes``); a given one may also be the pair's
+    whole workspace (``workspace_bytes(2, ...)``)."""
     _check_chunk(chunk_size)
     q, k, v, g, beta, s0 = _prepare(q, k, v, g, beta, initial_state)
     B, T, H, D = q.shape
@@ -150,7 +163,8 @@ def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CH
     dev = q.device
     o = torch.empty_like(q)
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
-    ws = _workspace(_lib.KDA_PASS_TRAIN, B, T, H, D, dev, q.dtype, workspace)
+    ws = _workspace(_lib.KDA_PASS_TRAIN, B, T, H, D, dev, q.dtype, workspace,
+                    nbytes=train_kept_bytes(B, T, H, D, q.dtype))
     rc = lib.kda_fwd_train(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
                            B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
                            _ptr(ws), ws.numel(), _stream(dev))
@@ -161,7 +175,9 @@ def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CH
 def kda_backward_train(q, k, v, g, beta, initial_state, do, ds_final, workspace: torch.Tensor,
                        chunk_size: int = CHUNK):
     """VJP from the workspace of ``kda_forward_train`` (same inputs): returns
-    (dq, dk, dv, dg, dbeta, d_initial_state)."""
+    (dq, dk, dv, dg, dbeta, d_initial_state).  A workspace of the pair's whole
+    size also serves as the backward's scratch; a kept-part one gets a scratch
+    buffer allocated for the call."""
     return kda_backward(q, k, v, g, beta, initial_state, do, ds_final, chunk_size, workspace, _train=True)
 
 
@@ -192,12 +208,20 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
     if _train and workspace is None:
         raise ValueError("kda_backward_train needs the workspace returned by kda_forward_train")
     ws = _workspace(_lib.KDA_PASS_BWD, B, T, H, D, dev, q.dtype, workspace)
-    fn = lib.kda_bwd_train if _train else lib.kda_bwd
-    rc = fn(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ds0),
-            B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
-            _ptr(ws), ws.numel(), _stream(dev))
-    _lib.check(rc, "kda_bwd_train" if _train else "kda_bwd")
+            B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype])
+    if not _train:
+        _lib.check(lib.kda_bwd(*args, _ptr(ws), ws.numel(), _stream(dev)), "kda_bwd")
+        return dq, dk, dv, dg, dbeta, ds0
+    total = workspace_bytes(_lib.KDA_PASS_TRAIN, B, T, H, D, q.dtype)
+    if ws.numel() >= total:
+        _lib.check(lib.kda_bwd_train(*args, _ptr(ws), ws.numel(), _stream(dev)), "kda_bwd_train")
+    else:
+        n = total - train_kept_bytes(B, T, H, D, q.dtype)
+        scratch = torch.empty(max(n, 256), dtype=torch.uint8, device=dev)
+        _lib.check(lib.kda_bwd_train_split(*args, _ptr(ws), ws.numel(), _ptr(scratch), scratch.numel(),
+                                           _stream(dev)), "kda_bwd_train_split")
     return dq, dk, dv, dg, dbeta, ds0
 
 
@@ -239,7 +263,8 @@ def kda_forward_gated(q, k, v, g, beta, initial_state, gate: torch.Tensor, norm_
     y = torch.empty((B, T, H * D), dtype=q.dtype, device=dev)
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
     pass_ = _lib.KDA_PASS_TRAIN if train else _lib.KDA_PASS_FWD
-    ws = _workspace(pass_, B, T, H, D, dev, q.dtype, workspace)
+    ws = _workspace(pass_, B, T, H, D, dev, q.dtype, workspace,
+                    nbytes=train_kept_bytes(B, T, H, D, q.dtype) if train else None)
     rc = lib.kda_fwd_gated(pass_, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(gate), ld_z,
                            _ptr(w), float(eps), _ptr(o), _ptr(y), H * D, _ptr(s_final),
                            B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],

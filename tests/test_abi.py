@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().kda_abi_version() == _lib.ABI_VERSION == 3
+    assert _lib.load().kda_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_workspace_sizes():
@@ -102,29 +102,66 @@ def test_workspace_offsets_disjoint():
         assert offs[-1] < total
 
 
+def _offsets(lib, pass_, B, T, H, D, dtype):
+    arr = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
+    assert lib.kda_workspace_offsets(pass_, B, T, H, D, 64, dtype, arr) == 0
+    return dict(zip(_lib.WS_REGIONS, arr))
+
+
+BACKWARD_REGIONS = ("h", "dh", "Vp", "dVp", "PadB")
+
+
 @pytest.mark.parametrize("pass_,dtype", [(0, 0), (0, 1), (1, 0), (1, 1), (2, 0), (2, 1)])
 def test_d96_workspace_is_d128_plus_pad(pass_, dtype):
     """D = 96 runs the D = 128 kernels on zero-padded copies: its regions are
-    those of D = 128 at the same offsets, followed by the PAD region (padded
-    q, k, v, g, the pass's outputs or cotangents and the padded states)."""
+    those of D = 128 plus PAD (padded q, k, v, g, s0 and the forward's o and
+    s_final) and PADB (the backward's padded cotangents and gradients).  Passes
+    0 and 1: the D = 128 regions at their offsets, then PAD, then PADB.  Pass 2:
+    the kept regions at their D = 128 offsets and PAD after them; the
+    backward's regions follow, shifted by PAD, and PADB last."""
     lib = _lib.load()
     B, T, H = 2, 300, 3
-    a96 = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
-    a128 = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
-    assert lib.kda_workspace_offsets(pass_, B, T, H, 96, 64, dtype, a96) == 0
-    assert lib.kda_workspace_offsets(pass_, B, T, H, 128, 64, dtype, a128) == 0
-    o96, o128 = dict(zip(_lib.WS_REGIONS, a96)), dict(zip(_lib.WS_REGIONS, a128))
-    assert o128["Pad"] == -1
-    assert all(o96[r] == o128[r] for r in _lib.WS_REGIONS if r != "Pad")
+    o96, o128 = _offsets(lib, pass_, B, T, H, 96, dtype), _offsets(lib, pass_, B, T, H, 128, dtype)
+    assert o128["Pad"] == -1 and o128["PadB"] == -1
     s128 = lib.kda_workspace_size(pass_, B, T, H, 128, 64, dtype)
-    assert o96["Pad"] == s128
     tok, es, st = B * T * H * 128, 2 if dtype else 4, B * H * 128 * 128 * 4
-    # q, k, v (es) and g (4 bytes) and s0 always; o and s_final for the forward
-    # passes, dout, dq, dk, dv, dg, ds_final and ds0 for the backward ones
-    nrow = 3 + (1 if pass_ != 1 else 0) + (4 if pass_ != 0 else 0)
-    ng = 1 + (1 if pass_ != 0 else 0)
-    nst = 1 + (1 if pass_ != 1 else 0) + (2 if pass_ != 0 else 0)
-    assert lib.kda_workspace_size(pass_, B, T, H, 96, 64, dtype) - s128 == nrow * tok * es + ng * tok * 4 + nst * st
+    # PAD: q, k, v (es), g (4 bytes), s0, and o, s_final for the forward passes;
+    # PADB: dout, dq, dk, dv (es), dg (4 bytes), ds_final, ds0 for the backward ones
+    pad = 3 * tok * es + tok * 4 + st + ((tok * es + st) if pass_ != 1 else 0)
+    padb = (4 * tok * es + tok * 4 + 2 * st) if pass_ != 0 else 0
+    assert lib.kda_workspace_size(pass_, B, T, H, 96, 64, dtype) - s128 == pad + padb
+    kernel_regions = [r for r in _lib.WS_REGIONS if r not in ("Pad", "PadB")]
+    if pass_ != 2:
+        assert all(o96[r] == o128[r] for r in kernel_regions)
+        assert o96["Pad"] == s128
+        assert o96["PadB"] == (s128 + pad if pass_ == 1 else -1)
+        return
+    kept128 = lib.kda_train_kept_size(B, T, H, 128, 64, dtype)
+    assert lib.kda_train_kept_size(B, T, H, 96, 64, dtype) == kept128 + pad
+    assert o96["Pad"] == kept128
+    for r in kernel_regions:
+        assert o96[r] == (o128[r] + pad if r in BACKWARD_REGIONS and o128[r] >= 0 else o128[r]), r
+    assert o96["PadB"] == s128 + pad
+
+
+@pytest.mark.parametrize("B,T,H,D,dtype", [(2, 300, 3, 64, 1), (2, 300, 3, 64, 0), (1, 200, 2, 128, 1),
+                                           (1, 200, 2, 128, 0), (2, 70, 3, 96, 1), (1, 65, 2, 32, 0)])
+def test_train_workspace_kept_part_first(B, T, H, D, dtype):
+    """The training pair's workspace: the regions the forward writes and the
+    backward reads come first (kda_train_kept_size bytes), the backward's own
+    regions (h, dh, V', dV', the padded gradients) after them."""
+    lib = _lib.load()
+    off = _offsets(lib, 2, B, T, H, D, dtype)
+    kept = lib.kda_train_kept_size(B, T, H, D, 64, dtype)
+    total = lib.kda_workspace_size(2, B, T, H, D, 64, dtype)
+    assert 0 < kept < total and kept % 256 == 0
+    for r, o in off.items():
+        if o < 0:
+            continue
+        assert (o >= kept) == (r in BACKWARD_REGIONS), (r, o, kept)
+    assert all(off[r] >= 0 for r in ("W", "U", "eG", "h", "dh", "dVp"))
+    # the forward passes' layouts are unchanged by the split
+    assert lib.kda_train_kept_size(B, T, H, 48, 64, dtype) == 0 and b"D=48" in lib.kda_last_error()
 
 
 @pytest.mark.parametrize("B,T,H,D,dtype,nseg", [
@@ -194,12 +231,24 @@ def test_training_pair_argument_errors():
                            fake, 1 << 40, None)
     assert rc == _lib.KDA_E_UNSUPPORTED
     need = lib.kda_workspace_size(2, 1, 64, 1, 64, 64, 1)
-    assert need > lib.kda_workspace_size(0, 1, 64, 1, 64, 64, 1)
+    kept = lib.kda_train_kept_size(1, 64, 1, 64, 64, 1)
+    assert need > kept >= lib.kda_workspace_size(0, 1, 64, 1, 64, 64, 1)
+    # the forward needs the kept part, the single-buffer backward all of it
     rc = lib.kda_fwd_train(fake, fake, fake, fake, fake, None, fake, None, 1, 64, 1, 64, 64, 1, 1,
-                           fake, need - 1, None)
+                           fake, kept - 1, None)
     assert rc == _lib.KDA_E_WORKSPACE
     rc = lib.kda_bwd_train(*([fake] * 14), 1, 64, 1, 64, 64, 1, 1, fake, need - 1, None)
     assert rc == _lib.KDA_E_WORKSPACE
+    # the split backward: the kept part and a scratch buffer of the rest
+    rc = lib.kda_bwd_train_split(*([fake] * 14), 1, 64, 1, 64, 64, 1, 1, fake, kept - 1, fake, need - kept, None)
+    assert rc == _lib.KDA_E_WORKSPACE and "workspace" in _lib.last_error()
+    rc = lib.kda_bwd_train_split(*([fake] * 14), 1, 64, 1, 64, 64, 1, 1, fake, kept, fake, need - kept - 1, None)
+    assert rc == _lib.KDA_E_WORKSPACE and "scratch" in _lib.last_error()
+    rc = lib.kda_bwd_train_split(*([fake] * 14), 1, 64, 1, 64, 64, 1, 1, fake, kept, None, need - kept, None)
+    assert rc == _lib.KDA_E_WORKSPACE and "scratch" in _lib.last_error()
+    misaligned = ctypes.c_void_p((1 << 20) + 16)
+    rc = lib.kda_bwd_train_split(*([fake] * 14), 1, 64, 1, 64, 64, 1, 1, fake, kept, misaligned, need, None)
+    assert rc == _lib.KDA_E_INVALID and "scratch" in _lib.last_error()
     assert lib.kda_workspace_size(3, 1, 64, 1, 64, 64, 1) == 0
 
 

@@ -480,6 +480,48 @@ def test_training_pair_equals_standalone_calls(B, T, H, D, dtype, g_scale):
         assert torch.equal(a, b), n
 
 
+@pytest.mark.parametrize("B,T,H,D,dtype", [
+    (2, 100, 3, 64, torch.bfloat16),
+    (1, 65, 2, 32, torch.float32),
+    (1, 150, 2, 128, torch.bfloat16),
+    (1, 100, 2, 128, torch.float32),
+    (1, 150, 2, 96, torch.bfloat16),          # PAD kept, PADB the backward's
+])
+def test_training_pair_kept_part_and_split_scratch(B, T, H, D, dtype):
+    """kda_fwd_train writes nothing past the kept part of the pair's workspace
+    (kda_train_kept_size bytes); kda_bwd_train leaves the kept part as it was;
+    kda_bwd_train_split on a copy of the kept part and a separate scratch
+    buffer full of NaN bytes gives kda_bwd_train's gradients bit for bit."""
+    from mlx_vit_amd import _lib
+    from mlx_vit_amd import kda as K
+    kda = _kda()
+    lib = _lib.load()
+    x = _inputs(B, T, H, D, dtype, seed=17, with_state=True, grad=True)
+    q, k, v, g, beta = _dev(x)
+    s0, do = x["s0"].to(DEV), x["do"].to(DEV)
+    total = kda.workspace_bytes(2, B, T, H, D, dtype)
+    kept = kda.train_kept_bytes(B, T, H, D, dtype)
+    assert 0 < kept < total
+    ws = torch.full((total,), 0x5A, dtype=torch.uint8, device=DEV)
+    kda.kda_forward_train(q, k, v, g, beta, s0, workspace=ws)
+    torch.cuda.synchronize()
+    assert bool((ws[kept:] == 0x5A).all()), "the training forward wrote past the kept part"
+    kept_copy = ws[:kept].clone()
+    g1 = kda.kda_backward_train(q, k, v, g, beta, s0, do, None, ws)     # one buffer: kda_bwd_train
+    torch.cuda.synchronize()
+    assert torch.equal(ws[:kept], kept_copy), "the backward wrote into the kept part"
+    scratch = torch.full((total - kept,), 0xFF, dtype=torch.uint8, device=DEV)   # NaN in fp32 and bf16
+    g2 = [torch.empty_like(t) for t in (q, k, v, g, beta)] + [torch.empty_like(s0)]
+    rc = lib.kda_bwd_train_split(*(K._ptr(t) for t in (q, k, v, g, beta, s0, do)), None,
+                                 *(K._ptr(t) for t in g2), B, T, H, D, 64, K._DTYPE_CODE[dtype],
+                                 K._DTYPE_CODE[g.dtype], K._ptr(kept_copy), kept, K._ptr(scratch),
+                                 scratch.numel(), K._stream(q.device))
+    _lib.check(rc, "kda_bwd_train_split")
+    torch.cuda.synchronize()
+    for n, a, b in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), g1, g2):
+        assert torch.equal(a, b), n
+
+
 # ---------------------------------------------------------------- committed golden fixtures
 
 def _golden(name):
