@@ -81,8 +81,10 @@ def seg_plan(BH, nc):
 
 def kernel_counts(B, T, H, D, es=2):
     """kernel_counts_at for the kernels' head dimension: D = 96 runs the D = 128
-    kernels on zero-padded copies, so its FLOPs and workspace bytes are those
-    of D = 128 while its op bytes are D = 96's."""
+    kernels with channels 96..127 zero, so its FLOPs and workspace bytes are
+    those of D = 128 (an upper bound for the prep and the local kernel, which
+    read and write 96-channel rows of the op's tensors) while its op bytes are
+    D = 96's."""
     if D == 96:
         fl, _, ws = kernel_counts_at(B, T, H, 128, es)
         _, alg, _ = kernel_counts_at(B, T, H, 96, es)

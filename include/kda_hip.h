@@ -14,7 +14,8 @@
  * 4839-4856); the result does not depend on it (the reference's own
  * equivalence criterion, nope_gdn_mlx.py:4836-4914), and the kernels block at
  * 64 whatever its value.  D must be 32, 64, 96 or 128 (96 runs the D = 128
- * kernels on zero-padded copies in the workspace).
+ * kernels with channels 96..127 zero; o, the states and the backward's dout
+ * pass through zero-padded copies in the workspace).
  * stream is a hipStream_t (NULL = default stream).  Every call is stream
  * ordered and allocates nothing: the caller passes a device workspace of at
  * least kda_workspace_size() bytes (256-byte aligned).
@@ -48,10 +49,10 @@ extern "C" {
 /* Workspace regions (see kda_workspace_offsets).  SEGX, SEGM and SEGS exist
  * only for the bf16 forward at D = 128 when it splits the sequence into
  * segments: per (b, h, segment) the segment's state map and start state.
- * PAD and PADB exist only at D = 96, which runs the D = 128 kernels on
- * zero-padded copies: the other regions are then those of D = 128; PAD holds
- * the padded q, k, v, g, s0 (and, for the forward passes, o and s_final),
- * PADB the backward's padded dout, dq, dk, dv, dg, ds_final and ds0.
+ * PAD and PADB exist only at D = 96, which runs the D = 128 kernels with
+ * channels 96..127 zero: the other regions are then those of D = 128; PAD
+ * holds the padded s0 (and, for the forward passes, o and s_final), PADB the
+ * backward's padded dout, ds_final and ds0.
  * Order: passes 0 and 1 lay the regions out in this order.  Pass 2 puts first
  * the regions kda_fwd_train writes and kda_bwd_train reads (the kept part,
  * kda_train_kept_size bytes: W .. EG and PAD) and after them those only the
@@ -82,7 +83,7 @@ int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int d
 
 /* Bytes at the start of the training pair's (pass 2) workspace that
  * kda_fwd_train writes and kda_bwd_train reads -- the per-chunk factors (and,
- * at D = 96, the padded inputs) -- all a caller must keep between the two
+ * at D = 96, the padded s0) -- all a caller must keep between the two
  * calls; 0 on invalid arguments.  The rest of kda_workspace_size(2, ...) is
  * the backward's own scratch (the chunk-boundary states and their adjoints,
  * V' and dV'), which kda_bwd_train_split takes as a separate buffer.  No
@@ -139,7 +140,7 @@ int kda_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, 
  * e^G (with fp32 inputs also A_kk and the inverted diagonal blocks of I + L).
  * No state is kept: kda_bwd_train recomputes the chunk-boundary states from
  * the factors and s0.  At D = 96 the pair's workspace also keeps the padded
- * q, k, v, g and s0 for the backward.
+ * s0 for the backward.
  * kda_fwd_train needs ws_bytes >= kda_train_kept_size (it writes nothing past
  * that); kda_bwd_train needs the whole pass-2 workspace, kda_workspace_size(2).
  * kda_bwd_train is kda_bwd without its prep: it requires the workspace that

@@ -73,16 +73,18 @@ bool seg_forward(int pass, int B, int T, int H, int D, int dtype, int* nseg, int
     return *nseg > 1;
 }
 
-// D = 96 runs the D = 128 kernels on zero-padded copies (kda_pad.hip): the
-// workspace is the D = 128 layout followed by the PAD region, which holds the
-// padded operands and outputs of the pass in these slots.
+// D = 96 runs the D = 128 kernels.  The prep and the local-adjoint kernel read
+// q, k, v, g (and dout) rows of 96 channels themselves, the missing channels
+// as zero, and write dq, dk, dv, dg rows of 96; o, dout for the reverse carry
+// and the states go through zero-padded copies (kda_pad.hip) in the PAD and
+// PADB regions, in these slots.
 constexpr int PAD_D = 128;
 bool padded_head(int D) { return D == 96; }
-enum PadSlot { PS_Q, PS_K, PS_V, PS_G, PS_O, PS_DO, PS_DQ, PS_DK, PS_DV, PS_DG, PS_S0, PS_SF, PS_DSF, PS_DS0, PS_N };
+enum PadSlot { PS_O, PS_DO, PS_S0, PS_SF, PS_DSF, PS_DS0, PS_N };
 
 // The slots of the backward's padded cotangents and gradients live in the
-// PADB region, the others (inputs, the forward's outputs) in PAD.
-bool pad_backward_slot(int i) { return i == PS_DO || (i >= PS_DQ && i <= PS_DG) || i == PS_DSF || i == PS_DS0; }
+// PADB region, the others (the initial state, the forward's outputs) in PAD.
+bool pad_backward_slot(int i) { return i == PS_DO || i == PS_DSF || i == PS_DS0; }
 
 struct PadLayout {
     size_t off[PS_N];   // within the slot's region
@@ -94,17 +96,13 @@ void make_pad_layout(int pass, int B, int T, int H, int dtype, PadLayout& P) {
     const size_t tok = (size_t)B * T * H * PAD_D, es = (dtype == KDA_DTYPE_BF16) ? 2 : 4;
     const size_t st = (size_t)B * H * PAD_D * PAD_D * 4;
     size_t sz[PS_N] = {0};
-    // g and dg take 4 bytes an element: the workspace size does not depend on g_dtype
-    sz[PS_Q] = sz[PS_K] = sz[PS_V] = tok * es;
-    sz[PS_G] = tok * 4;
     sz[PS_S0] = st;
     if (pass != KDA_PASS_BWD) {
         sz[PS_O] = tok * es;
         sz[PS_SF] = st;
     }
     if (pass != KDA_PASS_FWD) {
-        sz[PS_DO] = sz[PS_DQ] = sz[PS_DK] = sz[PS_DV] = tok * es;
-        sz[PS_DG] = tok * 4;
+        sz[PS_DO] = tok * es;
         sz[PS_DSF] = sz[PS_DS0] = st;
     }
     size_t cur = 0, curb = 0;
@@ -387,8 +385,9 @@ int check_workspace(const void* workspace, size_t ws_bytes, size_t need, const c
 // Prep: the forward's outputs (pass 0), the backward's (pass 1) or both (pass 2).
 hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                             const Ws& ws, int T, int H, int D, int nchunks, int in_bf16, int g_bf16,
-                            hipStream_t st, bool prof = true) {
+                            hipStream_t st, bool prof = true, int dio = 0) {
     kda::PrepArgs pa = {};
+    pa.dio = dio;
     pa.q = q; pa.k = k; pa.v = v; pa.g = g; pa.beta = beta;
     pa.W = region(ws, KDA_WS_W);
     pa.U = region(ws, KDA_WS_U);
@@ -417,13 +416,15 @@ struct Epilogue {
     int64_t ld_y;
 };
 
+// dio: the channels of a q, k, v, g (dout, dq, dk, dv, dg) row when narrower
+// than D (0: D); dout_rec: the reverse carry's dout, D channels a row.
 int fwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                const float* s0, void* o, float* s_final, int B, int T, int H, int D, int dtype, int g_dtype,
-               const Ws& ws, hipStream_t st, bool prof, const Epilogue* epi);
+               const Ws& ws, hipStream_t st, bool prof, const Epilogue* epi, int dio = 0);
 int bwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
-               const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
-               void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws,
-               hipStream_t st);
+               const float* s0, const void* dout, const void* dout_rec, const float* ds_final, void* dq, void* dk,
+               void* dv, void* dg, void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype,
+               const Ws& ws, hipStream_t st, int dio = 0);
 
 // The padded head dimension's slots in the workspace's PAD and PADB regions,
 // and the copies in and out of them.
@@ -431,13 +432,13 @@ struct PadIo {
     char *base, *base_b;
     PadLayout P;
     size_t ntok, nbh;
-    int D, es, gs;
+    int D, es;
     hipStream_t st;
     void* slot(int i) const { return (pad_backward_slot(i) ? base_b : base) + P.off[i]; }
     float* fslot(int i) const { return reinterpret_cast<float*>(slot(i)); }
     // the copies of one direction, gathered and issued as one launch: (B, T, H, D)
-    // rows in / out (element size es, or gs for g / dg) and (B, H, D, D) fp32
-    // states in / out; a null tensor adds nothing
+    // rows in / out (element size es) and (B, H, D, D) fp32 states in / out; a
+    // null tensor adds nothing
     kda::ResizeJob jobs[kda::KDA_RESIZE_MAX_JOBS];
     int njobs = 0;
     void rows_in(const void* src, int i, int esz) { jobs[njobs++] = {src, slot(i), ntok, 1, D, 1, PAD_D, esz}; }
@@ -455,7 +456,7 @@ struct PadIo {
     }
 };
 
-PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws, hipStream_t st) {
+PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, const Ws& ws, hipStream_t st) {
     PadIo io;
     io.base = static_cast<char*>(ws.r[KDA_WS_PAD]);
     io.base_b = static_cast<char*>(ws.r[KDA_WS_PADB]);
@@ -464,7 +465,6 @@ PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, const
     io.nbh = (size_t)B * H;
     io.D = D;
     io.es = (dtype == KDA_DTYPE_BF16) ? 2 : 4;
-    io.gs = (g_dtype == KDA_DTYPE_BF16) ? 2 : 4;
     io.st = st;
     return io;
 }
@@ -472,17 +472,13 @@ PadIo pad_io(int pass, int B, int T, int H, int D, int dtype, int g_dtype, const
 int run_fwd_padded(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                    const float* s0, void* o, float* s_final, int B, int T, int H, int D, int chunk, int dtype,
                    int g_dtype, const Ws& ws, hipStream_t st, bool prof) {
-    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, st);
+    PadIo io = pad_io(pass, B, T, H, D, dtype, ws, st);
     hipError_t e;
-    io.rows_in(q, PS_Q, io.es);
-    io.rows_in(k, PS_K, io.es);
-    io.rows_in(v, PS_V, io.es);
-    io.rows_in(g, PS_G, io.gs);
     io.state_in(s0, PS_S0);
     if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (pad)");
-    const int rc = fwd_launch(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
-                              s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_O), s_final ? io.fslot(PS_SF) : nullptr, B,
-                              T, H, PAD_D, dtype, g_dtype, ws, st, prof, nullptr);
+    const int rc = fwd_launch(pass, q, k, v, g, beta, s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_O),
+                              s_final ? io.fslot(PS_SF) : nullptr, B, T, H, PAD_D, dtype, g_dtype, ws, st, prof,
+                              nullptr, D);
     if (rc != KDA_OK) return rc;
     io.rows_out(PS_O, o, io.es);
     io.state_out(PS_SF, s_final);
@@ -494,30 +490,19 @@ int run_bwd_padded(int pass, const void* q, const void* k, const void* v, const 
                    const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
                    void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws,
                    hipStream_t st) {
-    PadIo io = pad_io(pass, B, T, H, D, dtype, g_dtype, ws, st);
+    PadIo io = pad_io(pass, B, T, H, D, dtype, ws, st);
     hipError_t e;
-    // the training backward finds the padded q, k, v, g and s0 where the
-    // training forward left them (the pair's workspace is unmodified between
-    // the two calls, for the same inputs)
-    if (pass != KDA_PASS_TRAIN) {
-        io.rows_in(q, PS_Q, io.es);
-        io.rows_in(k, PS_K, io.es);
-        io.rows_in(v, PS_V, io.es);
-        io.rows_in(g, PS_G, io.gs);
-        io.state_in(s0, PS_S0);
-    }
+    // the training backward finds the padded s0 where the training forward left
+    // it (the pair's kept part is unmodified between the two calls, for the
+    // same inputs)
+    if (pass != KDA_PASS_TRAIN) io.state_in(s0, PS_S0);
     io.rows_in(dout, PS_DO, io.es);
     io.state_in(ds_final, PS_DSF);
     if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (pad)");
-    const int rc = bwd_launch(pass, io.slot(PS_Q), io.slot(PS_K), io.slot(PS_V), io.slot(PS_G), beta,
-                              s0 ? io.fslot(PS_S0) : nullptr, io.slot(PS_DO), ds_final ? io.fslot(PS_DSF) : nullptr,
-                              io.slot(PS_DQ), io.slot(PS_DK), io.slot(PS_DV), io.slot(PS_DG), dbeta,
-                              ds0 ? io.fslot(PS_DS0) : nullptr, B, T, H, PAD_D, dtype, g_dtype, ws, st);
+    const int rc = bwd_launch(pass, q, k, v, g, beta, s0 ? io.fslot(PS_S0) : nullptr, dout, io.slot(PS_DO),
+                              ds_final ? io.fslot(PS_DSF) : nullptr, dq, dk, dv, dg, dbeta,
+                              ds0 ? io.fslot(PS_DS0) : nullptr, B, T, H, PAD_D, dtype, g_dtype, ws, st, D);
     if (rc != KDA_OK) return rc;
-    io.rows_out(PS_DQ, dq, io.es);
-    io.rows_out(PS_DK, dk, io.es);
-    io.rows_out(PS_DV, dv, io.es);
-    io.rows_out(PS_DG, dg, io.gs);
     io.state_out(PS_DS0, ds0);
     if ((e = io.issue()) != hipSuccess) return hip_fail(e, "kda_resize_batch_kernel (crop)");
     return ok();
@@ -559,10 +544,11 @@ int run_fwd(int pass, const void* q, const void* k, const void* v, const void* g
 // The forward's launches on resolved workspace regions (shapes checked).
 int fwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
                const float* s0, void* o, float* s_final, int B, int T, int H, int D, int dtype, int g_dtype,
-               const Ws& ws, hipStream_t st, bool prof, const Epilogue* epi) {
+               const Ws& ws, hipStream_t st, bool prof, const Epilogue* epi, int dio) {
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
-    hipError_t e = launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st, prof);
+    hipError_t e =
+        launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st, prof, dio);
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     int nseg, seg_len;
@@ -651,20 +637,20 @@ int run_bwd(int pass, const void* q, const void* k, const void* v, const void* g
     if (padded_head(D))
         return run_bwd_padded(pass, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D,
                               dtype, g_dtype, ws, st);
-    return bwd_launch(pass, q, k, v, g, beta, s0, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D, dtype,
-                      g_dtype, ws, st);
+    return bwd_launch(pass, q, k, v, g, beta, s0, dout, dout, ds_final, dq, dk, dv, dg, dbeta, ds0, B, T, H, D,
+                      dtype, g_dtype, ws, st);
 }
 
 // The backward's launches on resolved workspace regions (shapes checked).
 int bwd_launch(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
-               const float* s0, const void* dout, const float* ds_final, void* dq, void* dk, void* dv, void* dg,
-               void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype, const Ws& ws,
-               hipStream_t st) {
+               const float* s0, const void* dout, const void* dout_rec, const float* ds_final, void* dq, void* dk,
+               void* dv, void* dg, void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype,
+               const Ws& ws, hipStream_t st, int dio) {
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
     const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
     hipError_t e;
     if (pass == KDA_PASS_BWD) {
-        e = launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st);
+        e = launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st, true, dio);
         if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
     }
     void* W = region(ws, KDA_WS_W);
@@ -692,7 +678,7 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
     da.Kb = region(ws, KDA_WS_KB);
     da.QpT = region(ws, KDA_WS_QPT);
     da.WT = region(ws, KDA_WS_WT);
-    da.eG = eG; da.dout = dout; da.dsf = ds_final; da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
+    da.eG = eG; da.dout = dout_rec; da.dsf = ds_final; da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
     da.T = T; da.H = H; da.nc = nc; da.BH = BH;
     e = timed(PROF_DH, st, [&] { return kda::launch_dh(da, D, in_bf16, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_dh_kernel");
@@ -702,7 +688,7 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
     la.W = W; la.U = U; la.Akk = fregion(ws, KDA_WS_AKK); la.Tii = fregion(ws, KDA_WS_TII);
     la.h = hS; la.dh = dhS; la.Vp = Vp; la.dVp = dVp;
     la.dq = dq; la.dk = dk; la.dv = dv; la.dg = dg; la.dbeta = dbeta;
-    la.T = T; la.H = H; la.nc = nc;
+    la.T = T; la.H = H; la.nc = nc; la.dio = dio;
     e = timed(PROF_LOCAL, st, [&] { return kda::launch_local(la, D, in_bf16, g_bf16, BH * nc, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_bwd_local_kernel");
     return ok();

@@ -32,12 +32,12 @@ struct WideLds {
 };
 
 // rows of a (B, T, H, D) tensor as an fp32-valued A operand; rows at or past
-// `valid` read as zero
+// `valid` and the k-steps at or past `kvalid` (a multiple of 32) read as zero
 template <typename TI>
-__device__ __forceinline__ Fr8 rows8(const TI* base, size_t rstride, int row0, int k0, int valid) {
+__device__ __forceinline__ Fr8 rows8(const TI* base, size_t rstride, int row0, int k0, int valid, int kvalid) {
     const int l = lane_id(), r = l & 15, g = l >> 4;
     Fr8 f;
-    if (row0 + r < valid) {
+    if (row0 + r < valid && k0 < kvalid) {
         const TI* p = base + (size_t)(row0 + r) * rstride + k0 + 4 * g;
         const float4 x = ld4<TI>(p), y = ld4<TI>(p + 16);
         f.v[0] = x.x; f.v[1] = x.y; f.v[2] = x.z; f.v[3] = x.w;
@@ -97,8 +97,12 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
     const int b = bh / a.H, h = bh - b * a.H;
     const int t0 = n * C, valid = min(C, a.T - t0);
-    const size_t rs = (size_t)a.H * D;
-    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
+    // dio: the channels of a q, k, v, g, dout, dq, dk, dv, dg row (< D for a
+    // narrower head: the rest read as zero and are not written)
+    const int dio = a.dio > 0 ? a.dio : D;
+    const bool narrow = dio < D;
+    const size_t rs = (size_t)a.H * dio;
+    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * dio;
     const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
     const TI* q = static_cast<const TI*>(a.q);
     const TI* k = static_cast<const TI*>(a.k);
@@ -126,18 +130,25 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     float4 tiv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < TIV) tiv = reinterpret_cast<const float4*>(a.Tii + (size_t)ch * NB * BS * BS)[tid];
     const int cd = tid % D, cb = tid / D;
-    // rows past T are read from the last valid row (no branch around a load,
-    // so the sixteen loads are in flight together) and zeroed below
+    // rows past T (and channels past dio) are read from the last valid row
+    // (channel) -- no branch around a load, so the sixteen loads are in flight
+    // together -- and zeroed below
     float gx[BS];
+    const int cdl = min(cd, dio - 1);
 #pragma unroll
     for (int r = 0; r < BS; ++r) {
         const int t = BS * cb + r;
-        gx[r] = ld1<TG>(g + base + (size_t)min(t, valid - 1) * rs + cd);
+        gx[r] = ld1<TG>(g + base + (size_t)min(t, valid - 1) * rs + cdl);
     }
     Tile<TI, C, D, NTH> tkr, tqr;
     if constexpr (STG) {
-        tkr.load(k + base, rs, valid);
-        tqr.load(q + base, rs, valid);
+        if (narrow) {
+            tkr.load(k + base, rs, valid, dio);
+            tqr.load(q + base, rs, valid, dio);
+        } else {
+            tkr.load(k + base, rs, valid);
+            tqr.load(q + base, rs, valid);
+        }
     }
 #pragma unroll
     for (int i = 0; i < (AKV + NTH - 1) / NTH; ++i)
@@ -163,7 +174,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
 #pragma unroll
         for (int r = 0; r < BS; ++r) {
             const int t = BS * cb + r;
-            const float x = (t < valid) ? gx[r] : 0.f;
+            const float x = (t < valid && cd < dio) ? gx[r] : 0.f;
             if (!(x <= 0.f)) flag = 1;
             run += x;
             s.g[t][cd] = run;
@@ -210,11 +221,11 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
                     kx[m][e] = ld1<TI>(st0 + t * LDQ + d);
                     qx[m][e] = ld1<TI>(st1p + t * LDQ + d);
                 } else {
-                    // clamped row, selected after the load: no branch around it
-                    const size_t oc = base + (size_t)min(t, valid - 1) * rs + d;
+                    // clamped row and channel, selected after the load: no branch around it
+                    const size_t oc = base + (size_t)min(t, valid - 1) * rs + min(d, dio - 1);
                     const float kv = ld1<TI>(k + oc), qv = ld1<TI>(q + oc);
-                    kx[m][e] = (t < valid) ? kv : 0.f;
-                    qx[m][e] = (t < valid) ? qv : 0.f;
+                    kx[m][e] = (t < valid && d < dio) ? kv : 0.f;
+                    qx[m][e] = (t < valid && d < dio) ? qv : 0.f;
                 }
                 el[m][e] = kexp<PREC>(gt - gr);
                 eb[m][e] = kexp<PREC>(G - gt);
@@ -234,10 +245,16 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     Frag8 Bh[STG ? D / 32 : 1], Bdh[STG ? D / 32 : 1];
     if constexpr (STG) {
         Tile<TI, C, D, NTH> tdo, tvp, tdvp, tvv;
-        tdo.load(dout + base, rs, valid);
+        if (narrow)
+            tdo.load(dout + base, rs, valid, dio);
+        else
+            tdo.load(dout + base, rs, valid);
         tvp.load(Vp, D);
         tdvp.load(dVp, D);
-        tvv.load(v + base, rs, valid);
+        if (narrow)
+            tvv.load(v + base, rs, valid, dio);
+        else
+            tvv.load(v + base, rs, valid);
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
             Bh[ks] = ldfrag_c<1, TI>(hS, D, BS * nt, 32 * ks);
@@ -267,7 +284,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
             for (int ks = 0; ks < D / 32; ++ks) {
                 const Fr8 Bh8 = frag8(hS, D, BS * nt, 32 * ks);
                 const Fr8 Bdh8 = frag8(dhS, D, BS * nt, 32 * ks);
-                dQp = mma8<PREC>(rows8<TI>(dout + base, rs, BS * m, 32 * ks, valid), Bh8, dQp);
+                dQp = mma8<PREC>(rows8<TI>(dout + base, rs, BS * m, 32 * ks, valid, dio), Bh8, dQp);
                 dKb = mma8<PREC>(frag8(Vp, D, BS * m, 32 * ks), Bdh8, dKb);
                 dW = mma8<PREC>(neg(frag8(dVp, D, BS * m, 32 * ks)), Bh8, dW);
             }
@@ -309,8 +326,8 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
         } else {
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks)
-                acc = mma8<PREC>(rows8<TI>(dout + base, rs, BS * i, 32 * ks, valid), frag8(Vp, D, BS * j, 32 * ks),
-                                 acc);
+                acc = mma8<PREC>(rows8<TI>(dout + base, rs, BS * i, 32 * ks, valid, dio),
+                                 frag8(Vp, D, BS * j, 32 * ks), acc);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -331,8 +348,8 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
                 vx[m][e] = ld1<TI>(st3 + t * LDQ + d);
             } else {
                 dvp[m][e] = ld1<TI>(dVp + (size_t)t * D + d);
-                const float vv = ld1<TI>(v + base + (size_t)min(t, valid - 1) * rs + d);
-                vx[m][e] = (t < valid) ? vv : 0.f;
+                const float vv = ld1<TI>(v + base + (size_t)min(t, valid - 1) * rs + min(d, dio - 1));
+                vx[m][e] = (t < valid && d < dio) ? vv : 0.f;
             }
         }
     // zero upper tiles of sda
@@ -382,7 +399,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
                 const float bt = s.beta[t];
                 const float egt = erb[m] * el[m][e];
                 const float vv = vx[m][e];
-                if (t < valid) st1<TI>(dv + base + (size_t)t * rs + d, bt * dRv[m][e]);
+                if (t < valid && d < dio) st1<TI>(dv + base + (size_t)t * rs + d, bt * dRv[m][e]);
                 dka[m][e] += bt * egt * dRk[m][e];
                 dga[m][e] += dRk[m][e] * bt * egt * kx[m][e];
                 const float db = sum16w(dRv[m][e] * vv + dRk[m][e] * egt * kx[m][e]);
@@ -522,7 +539,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
                 const float gt = s.g[t][d];
                 float ak = 0.f, aq = 0.f, ag = 0.f;
                 for (int sx = 0; sx < t; ++sx) {
-                    const float ksx = (sx < valid) ? ld1<TI>(k + base + (size_t)sx * rs + d) : 0.f;
+                    const float ksx = (sx < valid && d < dio) ? ld1<TI>(k + base + (size_t)sx * rs + d) : 0.f;
                     const float ks = ksx * kexp<PREC>(gt - s.g[sx][d]);
                     const float pp = sp[t][sx], pa = sda[t][sx];
                     ak += pp * ks;
@@ -530,8 +547,8 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
                     ag += (pp * kx[m][e] + pa * qx[m][e]) * ks;
                 }
                 for (int sx = t + 1; sx < C; ++sx) {
-                    const float ksx = (sx < valid) ? ld1<TI>(k + base + (size_t)sx * rs + d) : 0.f;
-                    const float qsx = (sx < valid) ? ld1<TI>(q + base + (size_t)sx * rs + d) : 0.f;
+                    const float ksx = (sx < valid && d < dio) ? ld1<TI>(k + base + (size_t)sx * rs + d) : 0.f;
+                    const float qsx = (sx < valid && d < dio) ? ld1<TI>(q + base + (size_t)sx * rs + d) : 0.f;
                     const float ex = kexp<PREC>(s.g[sx][d] - gt);
                     const float pp = sp[sx][t], pa = sda[sx][t];
                     const float c = (pp * ksx + pa * qsx) * ex;
@@ -586,7 +603,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int t = BS * m + 4 * g4 + e;
-            if (t < valid) {
+            if (t < valid && d < dio) {
                 const size_t o = base + (size_t)t * rs + d;
                 st1<TI>(dq + o, dqa[m][e]);
                 st1<TI>(dk + o, dka[m][e]);

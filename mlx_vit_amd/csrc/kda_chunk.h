@@ -254,28 +254,41 @@ template <int D, typename ST, typename TG, bool WITH_V, int NTH = 256>
 __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D, NTH>& tv, const ST* __restrict__ q,
                                            const ST* __restrict__ k, const ST* __restrict__ v,
                                            const TG* __restrict__ g, const ST* __restrict__ beta, size_t base,
-                                           size_t rstride, size_t bbase, int H, int valid) {
+                                           size_t rstride, size_t bbase, int H, int valid, int dio = D) {
     constexpr int WPB = NTH / 256, NCG = D / 8, CPL = NCG / (4 * WPB), GV = 8 * (int)sizeof(TG) / 16,
                   GE = 16 / (int)sizeof(TG);
     static_assert(NB == 4 && NCG % (4 * WPB) == 0, "whole 8-channel groups per lane");
+    // NARROW: the tensors' rows hold dio < D channels (a multiple of 8); the
+    // tile's channels past dio read as zero
+    constexpr bool NARROW_OK = D == 128;
+    const bool narrow = NARROW_OK && dio < D;
     Tile<ST, C, D, NTH> tq, tk;
     const int tid = threadIdx.x, w = tid >> 6, r16 = tid & 15, g4 = (tid >> 4) & 3;
     const int grow = BS * (w / WPB) + r16, gc0 = 4 * (w % WPB) + g4;
     uint4 graw[CPL][GV];
-    tq.load(q + base, rstride, valid);
-    tk.load(k + base, rstride, valid);
+    if (narrow) {
+        tq.load(q + base, rstride, valid, dio);
+        tk.load(k + base, rstride, valid, dio);
+    } else {
+        tq.load(q + base, rstride, valid);
+        tk.load(k + base, rstride, valid);
+    }
     {
         const TG* gp = g + base + (size_t)min(grow, valid - 1) * rstride;
 #pragma unroll
-        for (int cp = 0; cp < CPL; ++cp)
+        for (int cp = 0; cp < CPL; ++cp) {
+            const int c8 = 8 * (gc0 + 4 * WPB * cp), cc = NARROW_OK ? min(c8, dio - 8) : c8;
 #pragma unroll
-            for (int vq = 0; vq < GV; ++vq)
-                graw[cp][vq] = *reinterpret_cast<const uint4*>(gp + 8 * (gc0 + 4 * WPB * cp) + GE * vq);
+            for (int vq = 0; vq < GV; ++vq) graw[cp][vq] = *reinterpret_cast<const uint4*>(gp + cc + GE * vq);
+        }
     }
     const float braw = ld1<ST>(beta + bbase + (size_t)min(tid, valid - 1) * H);
     if constexpr (WITH_V) {
         __builtin_amdgcn_s_barrier();
-        tv.load(v + base, rstride, valid);
+        if (narrow)
+            tv.load(v + base, rstride, valid, dio);
+        else
+            tv.load(v + base, rstride, valid);
     }
     tq.store(&s.ql[0][0], ChunkSmem<D, ST>::LDK);
     tk.store(&s.kr[0][0], ChunkSmem<D, ST>::LDK);
@@ -283,11 +296,12 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D, N
 #pragma unroll
     for (int cp = 0; cp < CPL; ++cp) {
         float x[8];
+        const bool cok = !NARROW_OK || 8 * (gc0 + 4 * WPB * cp) < dio;
 #pragma unroll
         for (int vq = 0; vq < GV; ++vq) {
             const Vec16<TG> xv{graw[cp][vq]};
 #pragma unroll
-            for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid) ? xv.get(e) : 0.f;
+            for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid && cok) ? xv.get(e) : 0.f;
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {

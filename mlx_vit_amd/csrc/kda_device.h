@@ -541,6 +541,22 @@ struct Tile {
     __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld, int valid_rows) {
         load_at(threadIdx.x, g, gld, valid_rows);
     }
+    // ... and columns at or past valid_cols (a multiple of EPV, >= EPV) too: a
+    // tensor row narrower than the tile, its missing columns zero.  Addresses
+    // are clamped into the valid rows and columns.
+    __device__ __forceinline__ void load(const ST* __restrict__ g, size_t gld, int valid_rows, int valid_cols) {
+        ok = 0u;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int v = threadIdx.x + NTH * i;
+            if (NV % NTH == 0 || v < NV) {
+                const int row = v / VPR, c = (v - row * VPR) * EPV;
+                const int rr = min(row, valid_rows - 1), cc = min(c, valid_cols - EPV);
+                put(i, *reinterpret_cast<const uint4*>(g + (size_t)rr * gld + cc));
+                ok |= (uint32_t)(row < valid_rows && c < valid_cols) << i;
+            }
+        }
+    }
     __device__ __forceinline__ void store(ST* lds, int lld) const { store_at(threadIdx.x, lds, lld); }
 
     // the same with an explicit thread index t in [0, 256) (for a 256-thread

@@ -64,8 +64,10 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
     const int ch = blockIdx.x, bh = ch / a.nc, n = ch - bh * a.nc;
     const int b = bh / a.H, h = bh - b * a.H;
     const int t0 = n * C, valid = min(C, a.T - t0);
-    const size_t rs = (size_t)a.H * D;
-    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * D;
+    // dio: the channels of a q, k, v, g row (< D only at D = 128: the rest read as zero)
+    const int dio = (D == 128 && a.dio > 0) ? a.dio : D;
+    const size_t rs = (size_t)a.H * dio;
+    const size_t base = ((size_t)b * a.T + t0) * rs + (size_t)h * dio;
     const size_t bbase = ((size_t)b * a.T + t0) * a.H + h;
     const ST* q = static_cast<const ST*>(a.q);
     const ST* k = static_cast<const ST*>(a.k);
@@ -96,7 +98,8 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
     if (tid == 0) *flagw = 0;
     // PHASE 0 (load); v stays in registers until the column pass is done
     Tile<ST, C, D, NTH> tv;
-    const int flag = chunk_load2<D, ST, TG, G::STAGE_V, NTH>(s, tv, q, k, v, g, beta, base, rs, bbase, a.H, valid);
+    const int flag =
+        chunk_load2<D, ST, TG, G::STAGE_V, NTH>(s, tv, q, k, v, g, beta, base, rs, bbase, a.H, valid, dio);
     // PHASE 1
     const int dfl = chunk_factors2<D, ST, PREC, NTH>(s, flag, flagw);
     // The rest of the kernel is instantiated twice.  Chunks whose 16-row blocks
@@ -543,7 +546,7 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
                         } else if constexpr (G::STAGE_V) {
                             rv = bv[e] * col[e];
                         } else {
-                            rv = (t < valid) ? bv[e] * ld1<ST>(v + base + (size_t)t * rs + d) : 0.f;
+                            rv = (t < valid && d < dio) ? bv[e] * ld1<ST>(v + base + (size_t)t * rs + d) : 0.f;
                         }
                     }
                     Y[jj][e] = rv;

@@ -29,6 +29,9 @@ struct PrepArgs {
     void *W, *U, *Qp, *QpT, *Kb, *KbT, *WT, *Aqk, *AqkT;
     float *Akk, *Tii, *eG;
     int T, H, nc;
+    // channels of a q, k, v, g row when narrower than the kernel's D (D = 128
+    // only, a multiple of 32; 0 = D): the missing channels are read as zero
+    int dio;
 };
 
 struct RecurArgs {
@@ -69,6 +72,10 @@ struct LocalArgs {
     void *dq, *dk, *dv, *dg, *dbeta;
     int T, H, nc;
     int pf_ahead;   // L2 prefetch distance in chunks (the device's CU count), 0 = none
+    // channels of a q, k, v, g, dout, dq, dk, dv, dg row when narrower than the
+    // kernel's D (the D = 128 kernel only, a multiple of 32; 0 = D): missing
+    // channels are read as zero and not written
+    int dio;
 };
 
 // The bf16 forward at D = 128 split over segments of the sequence (kda_seg.hip):

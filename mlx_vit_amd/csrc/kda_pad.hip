@@ -1,20 +1,23 @@
 // kda_pad.hip -- head-dimension padding for D = 96.
 //
 // The chunk kernels tile the head dimension in 32- and 64-channel units, so a
-// D = 96 call runs them at D = 128 on zero-padded copies.  Zero channels
-// change nothing in the first 96: a zero k (and q) channel keeps its state
-// rows at zero and adds nothing to K K^T or Q K^T, a zero v channel keeps its
-// state columns at zero, and g = 0 (no decay) there touches only those zero
-// rows.  The cropped outputs and gradients therefore equal the D = 96
-// recurrence's.
+// D = 96 call runs them at D = 128 with the channels 96..127 zero.  Zero
+// channels change nothing in the first 96: a zero k (and q) channel keeps its
+// state rows at zero and adds nothing to K K^T or Q K^T, a zero v channel
+// keeps its state columns at zero, and g = 0 (no decay) there touches only
+// those zero rows.  The outputs and gradients of the first 96 channels
+// therefore equal the D = 96 recurrence's.  The prep and the local-adjoint
+// kernel read and write 96-channel rows of q, k, v, g, dout and the gradients
+// themselves; o, the reverse carry's dout and the states are padded or
+// cropped here.
 //
 // kda_resize_batch_kernel: up to KDA_RESIZE_MAX_JOBS jobs in one launch; job j
 // turns n matrices of rs x cs elements into rd x cd, element (r, c) of the
 // output being the input's where r < rs and c < cs, else zero.  Padding
 // (rd >= rs, cd >= cs) and cropping (rd <= rs, cd <= cs) are the same job.
 // Rows move in 16-byte pieces (cs and cd are multiples of 16 bytes); the
-// copies of one direction of a call (q, k, v, g and the state in; o or the
-// gradients out) go in one launch.
+// copies of one direction of a call (dout and the states in; o and the
+// states out) go in one launch.
 #include "kda_internal.h"
 
 namespace kda {

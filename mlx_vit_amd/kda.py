@@ -29,8 +29,8 @@ CHUNK = 64
 # reference's own equivalence criterion, nope_gdn_mlx.py:4836-4914), so the
 # kernels block at CHUNK whatever the caller's value.
 CHUNK_SIZES = (8, 16, 32, 64)
-# 96 (the reference's SSv2 model) runs the D = 128 kernels on zero-padded
-# copies inside the library
+# 96 (the reference's SSv2 model) runs the D = 128 kernels with channels
+# 96..127 zero inside the library
 FWD_HEAD_DIMS = (32, 64, 96, 128)
 BWD_HEAD_DIMS = (32, 64, 96, 128)
 

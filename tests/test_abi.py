@@ -113,22 +113,23 @@ BACKWARD_REGIONS = ("h", "dh", "Vp", "dVp", "PadB")
 
 @pytest.mark.parametrize("pass_,dtype", [(0, 0), (0, 1), (1, 0), (1, 1), (2, 0), (2, 1)])
 def test_d96_workspace_is_d128_plus_pad(pass_, dtype):
-    """D = 96 runs the D = 128 kernels on zero-padded copies: its regions are
-    those of D = 128 plus PAD (padded q, k, v, g, s0 and the forward's o and
-    s_final) and PADB (the backward's padded cotangents and gradients).  Passes
-    0 and 1: the D = 128 regions at their offsets, then PAD, then PADB.  Pass 2:
-    the kept regions at their D = 128 offsets and PAD after them; the
-    backward's regions follow, shifted by PAD, and PADB last."""
+    """D = 96 runs the D = 128 kernels (the prep and the local adjoints read and
+    write 96-channel rows themselves): its regions are those of D = 128 plus
+    PAD (the padded s0 and the forward's padded o and s_final) and PADB (the
+    backward's padded dout, ds_final and ds0).  Passes 0 and 1: the D = 128
+    regions at their offsets, then PAD, then PADB.  Pass 2: the kept regions at
+    their D = 128 offsets and PAD after them; the backward's regions follow,
+    shifted by PAD, and PADB last."""
     lib = _lib.load()
     B, T, H = 2, 300, 3
     o96, o128 = _offsets(lib, pass_, B, T, H, 96, dtype), _offsets(lib, pass_, B, T, H, 128, dtype)
     assert o128["Pad"] == -1 and o128["PadB"] == -1
     s128 = lib.kda_workspace_size(pass_, B, T, H, 128, 64, dtype)
     tok, es, st = B * T * H * 128, 2 if dtype else 4, B * H * 128 * 128 * 4
-    # PAD: q, k, v (es), g (4 bytes), s0, and o, s_final for the forward passes;
-    # PADB: dout, dq, dk, dv (es), dg (4 bytes), ds_final, ds0 for the backward ones
-    pad = 3 * tok * es + tok * 4 + st + ((tok * es + st) if pass_ != 1 else 0)
-    padb = (4 * tok * es + tok * 4 + 2 * st) if pass_ != 0 else 0
+    # PAD: s0, and o (es), s_final for the forward passes; PADB: dout (es),
+    # ds_final, ds0 for the backward ones
+    pad = st + ((tok * es + st) if pass_ != 1 else 0)
+    padb = (tok * es + 2 * st) if pass_ != 0 else 0
     assert lib.kda_workspace_size(pass_, B, T, H, 96, 64, dtype) - s128 == pad + padb
     kernel_regions = [r for r in _lib.WS_REGIONS if r not in ("Pad", "PadB")]
     if pass_ != 2:
