@@ -51,8 +51,16 @@ WORKLOADS = {
     "cfg2-layerdecay": (8, 1568, 12, 64, True, False,
                         "KDA fwd+VJP (training pair), B8 H12 T1568 D64 bf16, layer-init decay "
                         "g = -A_h softplus(N(0, 0.5^2)), A_h ~ U[1, 16]"),
+    # the scalar-alpha sibling (chunk_gdn, nope_gdn_mlx.py:641-650): one decay per
+    # (b, t, h), alpha = e^{-softplus(N(0, 1)) * 0.1}, run as the KDA pair on
+    # g = log(alpha) given once per head (bf16, D = 64), with chunk_gdn's host
+    # work (the log, d alpha = dg / alpha) inside the timed step
+    "gdn-cfg2": (8, 1568, 12, 64, True, False,
+                 "scalar-alpha GDN fwd+VJP (chunk_gdn: the KDA pair on g = log alpha, one decay per head), "
+                 "B8 H12 T1568 D64 bf16"),
 }
 LAYER_DECAY = {"cfg2-layerdecay"}
+SCALAR_DECAY = {"gdn-cfg2"}
 
 
 def op_counts(B, T, H, D, backward):
@@ -172,10 +180,12 @@ def kernel_counts_at(B, T, H, D, es=2):
     return fl, alg, ws
 
 
-def make_inputs_gpu(B, T, H, D, with_state, seed=0, layer_decay=False):
+def make_inputs_gpu(B, T, H, D, with_state, seed=0, layer_decay=False, scalar_decay=False):
     """Synthetic inputs with the configs' distributions, drawn on the GPU.  With
     ``layer_decay`` g follows the reference layer at initialisation instead:
-    -A_h softplus(N(0, 0.5^2)) with A_h ~ U[1, 16] per head."""
+    -A_h softplus(N(0, 0.5^2)) with A_h ~ U[1, 16] per head.  With
+    ``scalar_decay`` the returned g is alpha = e^{-softplus(N(0, 1)) * 0.1} of
+    shape (B, T, H), the scalar-alpha GDN's decay."""
     import torch
     gen = torch.Generator(device="cuda").manual_seed(seed)
     shp = (B, T, H, D)
@@ -190,6 +200,8 @@ def make_inputs_gpu(B, T, H, D, with_state, seed=0, layer_decay=False):
         A = torch.empty(H, device="cuda").uniform_(1.0, 16.0, generator=gen)
         g = -A[None, None, :, None] * torch.nn.functional.softplus(
             0.5 * torch.randn(shp, generator=gen, device="cuda"))
+    elif scalar_decay:
+        g = torch.exp(-torch.nn.functional.softplus(torch.randn((B, T, H), generator=gen, device="cuda")) * 0.1)
     else:
         g = -torch.nn.functional.softplus(torch.randn(shp, generator=gen, device="cuda")) * 0.1
     s0 = torch.randn((B, H, D, D), generator=gen, device="cuda") * 0.02 if with_state else None
@@ -398,7 +410,8 @@ def load_mfma(kernel_name):
         return None, None
 
 
-def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, seed=0, layer_decay=False):
+def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, seed=0, layer_decay=False,
+                     scalar_decay=False):
     """Time the torch fp32 restatement of the reference 'compiled' path on the
     host cores (bounded sample: the same B, H, D over `sample_tokens` steps),
     and measure rel-L2 of the HIP results against the fp64 C oracle on the
@@ -406,7 +419,11 @@ def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, s
     oracle can regenerate them), through the same entry points as the timed
     step (kda_fwd_train + kda_bwd_train for a fwd+bwd workload).  With
     ``layer_decay`` the parity inputs carry the layer-init decay the timed
-    workload uses (layer_decay_g), not make_inputs' default."""
+    workload uses (layer_decay_g), not make_inputs' default; with
+    ``scalar_decay`` one decay per (b, t, h), alpha = e^{-softplus(N(0, 1)) *
+    0.1}: the HIP side gets g = log(alpha) once per head as chunk_gdn passes
+    it, the oracle the same g broadcast over D; dg is compared as the sum over
+    the channels, and d alpha = dg / alpha is checked too."""
     import torch
     from oracle import cref
     from oracle import kda_reference as R
@@ -435,8 +452,16 @@ def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, s
     x = R.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=seed, with_state=with_state, with_grad=backward)
     if layer_decay:
         x["g"] = layer_decay_g(B, T, H, D, seed).to(torch.bfloat16)
+    alpha = None
     dev = lambda t: None if t is None else t.to("cuda")
     q, k, v, g, beta, s0 = (dev(x[nm]) for nm in ("q", "k", "v", "g", "beta", "s0"))
+    if scalar_decay:
+        from mlx_vit_amd.kda import GDN_LOG_ALPHA_MIN
+        gen = torch.Generator(device="cpu").manual_seed(seed + 2000)
+        alpha = torch.exp(-torch.nn.functional.softplus(torch.randn((B, T, H), generator=gen)) * 0.1)
+        gh = torch.clamp(torch.log(alpha), min=GDN_LOG_ALPHA_MIN)
+        x["g"] = gh[..., None].expand(B, T, H, D).contiguous()
+        g = dev(gh)
     # through the entry points the timed step calls: the training pair for a
     # fwd+bwd workload, the plain forward otherwise
     if backward:
@@ -449,7 +474,11 @@ def cpu_baseline_leg(B, T, H, D, backward, with_state, hip_out, sample_tokens, s
         grads = kda.kda_backward_train(q, k, v, g, beta, s0, dev(x["do"]), None, ws)
         rb = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"])
         for nm, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads):
-            errs[nm] = R.rel_l2(gr.cpu(), rb[nm])
+            want = rb[nm].double().sum(-1) if (alpha is not None and nm == "dg") else rb[nm]
+            errs[nm] = R.rel_l2(gr.cpu(), want)
+        if alpha is not None:
+            errs["dalpha"] = R.rel_l2(grads[3].double().cpu() / alpha.double(),
+                                      rb["dg"].double().sum(-1) / alpha.double())
     baseline = {
         "value": round(cpu_tps, 2), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
         "sample": (f"torch fp32 restatement of _loop_compiled_kda (D x D x D step matmul, autograd VJP) "
@@ -675,11 +704,22 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb)
-    q, k, v, g, beta, s0, do = make_inputs_gpu(B, T, H, D, with_state, layer_decay=args.workload in LAYER_DECAY)
+    scalar = args.workload in SCALAR_DECAY
+    q, k, v, g, beta, s0, do = make_inputs_gpu(B, T, H, D, with_state, layer_decay=args.workload in LAYER_DECAY,
+                                               scalar_decay=scalar)
     ws = torch.empty(kda.workspace_bytes(2 if backward else 0, B, T, H, D), dtype=torch.uint8, device="cuda")
 
     def step():
         # a training step runs the training pair; a forward-only workload the plain forward
+        if scalar:
+            # chunk_gdn's path: g = log(alpha), one decay per (b, t, h), the KDA
+            # pair, d alpha = dg / alpha (g is alpha here)
+            from mlx_vit_amd.kda import GDN_LOG_ALPHA_MIN
+            gh = torch.clamp(torch.log(g.float()), min=GDN_LOG_ALPHA_MIN)
+            o, sf, _ = kda.kda_forward_train(q, k, v, gh, beta, s0, workspace=ws)
+            grads = kda.kda_backward_train(q, k, v, gh, beta, s0, do, None, ws)
+            grads[3].div_(g.float())
+            return o
         if backward:
             o, sf, _ = kda.kda_forward_train(q, k, v, g, beta, s0, workspace=ws)
             kda.kda_backward_train(q, k, v, g, beta, s0, do, None, ws)
@@ -771,7 +811,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         cb, errs = cpu_baseline_leg(B, T, H, D, backward, with_state, None, args.cpu_sample_tokens,
-                                    layer_decay=args.workload in LAYER_DECAY)
+                                    layer_decay=args.workload in LAYER_DECAY, scalar_decay=scalar)
         out["cpu_baseline"] = cb
         out["rel_l2"] = errs
     else:

@@ -8,7 +8,8 @@
  *   s0, s_final, ds_final, ds0             [B, H, D, D] fp32, reference
  *                                          orientation S[i_v][j_k] (o_t = S_t q_t)
  * dtype / g_dtype: 0 = fp32, 1 = bf16 (raw bfloat16 bits).  q, k, v, beta, o
- * and dq, dk, dv, dbeta use `dtype`; g and dg use `g_dtype`.  Arithmetic is
+ * and dq, dk, dv, dbeta use `dtype`; g and dg use `g_dtype` (or, with g_dtype
+ * KDA_G_HEAD_F32, are fp32 [B, T, H]: one decay per head).  Arithmetic is
  * fp32 with an fp32 state; bf16 inputs use bf16 MFMA operands.
  * chunk is the reference's chunk_size: 8, 16, 32 or 64 (nope_gdn_mlx.py:676,
  * 4839-4856); the result does not depend on it (the reference's own
@@ -41,6 +42,11 @@ extern "C" {
 
 #define KDA_DTYPE_F32 0
 #define KDA_DTYPE_BF16 1
+/* g_dtype only: g is fp32 [B, T, H], one decay per (b, t, h) shared by the
+ * head's D channels (the scalar-alpha GDN, g = log alpha; the reference's
+ * _gdn_step_fused, nope_gdn_mlx.py:641-650), and dg is fp32 [B, T, H], the
+ * sum over the channels.  bf16 operands at D = 32 or 64 only. */
+#define KDA_G_HEAD_F32 2
 
 #define KDA_PASS_FWD 0
 #define KDA_PASS_BWD 1

@@ -19,6 +19,8 @@ KDA_E_UNSUPPORTED = -2
 KDA_E_WORKSPACE = -3
 KDA_E_HIP = -4
 
+KDA_G_HEAD_F32 = 2   # g_dtype: fp32 g [B, T, H], one decay per head (dg likewise)
+
 KDA_PASS_FWD = 0
 KDA_PASS_BWD = 1
 KDA_PASS_TRAIN = 2

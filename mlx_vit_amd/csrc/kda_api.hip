@@ -56,8 +56,12 @@ int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, b
                     bwd ? "backward" : "forward");
     if (dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_BF16)
         return fail(KDA_E_UNSUPPORTED, "dtype=%d: expected 0 (fp32) or 1 (bf16)", dtype);
-    if (g_dtype != KDA_DTYPE_F32 && g_dtype != KDA_DTYPE_BF16)
-        return fail(KDA_E_UNSUPPORTED, "g_dtype=%d: expected 0 (fp32) or 1 (bf16)", g_dtype);
+    if (g_dtype != KDA_DTYPE_F32 && g_dtype != KDA_DTYPE_BF16 && g_dtype != KDA_G_HEAD_F32)
+        return fail(KDA_E_UNSUPPORTED, "g_dtype=%d: expected 0 (fp32), 1 (bf16) or 2 (fp32, one per head)",
+                    g_dtype);
+    if (g_dtype == KDA_G_HEAD_F32 && (dtype != KDA_DTYPE_BF16 || (D != 32 && D != 64)))
+        return fail(KDA_E_UNSUPPORTED, "g_dtype=2 (one decay per head) needs bf16 operands and D in {32, 64}; "
+                    "got dtype=%d D=%d (broadcast g over the channels instead)", dtype, D);
     const long long nchunks = (long long)B * H * ((T + kda::C - 1) / kda::C);
     if (nchunks > 0x7fffffffLL) return fail(KDA_E_UNSUPPORTED, "B*H*ceil(T/64)=%lld exceeds 2^31-1", nchunks);
     return KDA_OK;
@@ -384,7 +388,7 @@ int check_workspace(const void* workspace, size_t ws_bytes, size_t need, const c
 
 // Prep: the forward's outputs (pass 0), the backward's (pass 1) or both (pass 2).
 hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* v, const void* g, const void* beta,
-                            const Ws& ws, int T, int H, int D, int nchunks, int in_bf16, int g_bf16,
+                            const Ws& ws, int T, int H, int D, int nchunks, int in_bf16, int g_kind,
                             hipStream_t st, bool prof = true, int dio = 0) {
     kda::PrepArgs pa = {};
     pa.dio = dio;
@@ -403,7 +407,7 @@ hipError_t launch_prep_pass(int pass, const void* q, const void* k, const void* 
     pa.Tii = fregion(ws, KDA_WS_TII);
     pa.T = T; pa.H = H; pa.nc = (T + kda::C - 1) / kda::C;
     const int id = pass == KDA_PASS_FWD ? PROF_PREP_FWD : pass == KDA_PASS_BWD ? PROF_PREP_BWD : PROF_PREP_TRAIN;
-    return timed(id, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_bf16, nchunks, st); }, prof);
+    return timed(id, st, [&] { return kda::launch_prep(pa, D, in_bf16, g_kind, nchunks, st); }, prof);
 }
 
 // The layer's gated RMSNorm fused into the forward's O store (kda_fwd_gated).
@@ -546,9 +550,10 @@ int fwd_launch(int pass, const void* q, const void* k, const void* v, const void
                const float* s0, void* o, float* s_final, int B, int T, int H, int D, int dtype, int g_dtype,
                const Ws& ws, hipStream_t st, bool prof, const Epilogue* epi, int dio) {
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
-    const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
+    // g_dtype doubles as the launchers' g kind: 0 fp32, 1 bf16, 2 one fp32 decay per head
+    const int in_bf16 = dtype == KDA_DTYPE_BF16, g_kind = g_dtype;
     hipError_t e =
-        launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st, prof, dio);
+        launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_kind, st, prof, dio);
     if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
 
     int nseg, seg_len;
@@ -647,10 +652,10 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
                void* dv, void* dg, void* dbeta, float* ds0, int B, int T, int H, int D, int dtype, int g_dtype,
                const Ws& ws, hipStream_t st, int dio) {
     const int nc = (T + kda::C - 1) / kda::C, BH = B * H;
-    const int in_bf16 = dtype == KDA_DTYPE_BF16, g_bf16 = g_dtype == KDA_DTYPE_BF16;
+    const int in_bf16 = dtype == KDA_DTYPE_BF16, g_kind = g_dtype;
     hipError_t e;
     if (pass == KDA_PASS_BWD) {
-        e = launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_bf16, st, true, dio);
+        e = launch_prep_pass(pass, q, k, v, g, beta, ws, T, H, D, BH * nc, in_bf16, g_kind, st, true, dio);
         if (e != hipSuccess) return hip_fail(e, "kda_prep_kernel");
     }
     void* W = region(ws, KDA_WS_W);
@@ -689,7 +694,7 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
     la.h = hS; la.dh = dhS; la.Vp = Vp; la.dVp = dVp;
     la.dq = dq; la.dk = dk; la.dv = dv; la.dg = dg; la.dbeta = dbeta;
     la.T = T; la.H = H; la.nc = nc; la.dio = dio;
-    e = timed(PROF_LOCAL, st, [&] { return kda::launch_local(la, D, in_bf16, g_bf16, BH * nc, st); });
+    e = timed(PROF_LOCAL, st, [&] { return kda::launch_local(la, D, in_bf16, g_kind, BH * nc, st); });
     if (e != hipSuccess) return hip_fail(e, "kda_bwd_local_kernel");
     return ok();
 }

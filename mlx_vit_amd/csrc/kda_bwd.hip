@@ -1283,6 +1283,12 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
         if (rh == 1 && g4 == 0) xt[d] = after_m;     // total over rows 32..63
     }
     __syncthreads();   // xt; region A (dR) and B (dL) dead
+    // GH (one decay per (b, t, h)): dg of a row is the sum of its channels'
+    // values, in fp32: over the 16 channels of the wave's tile by lane shuffles,
+    // then over the tiles through gpart[ct][t] (in the dg staging tile's bytes)
+    constexpr bool GH = std::is_same<TG, GHead>::value;
+    float* gpart = reinterpret_cast<float*>(&sm.ra.out[3][0][0]);
+    static_assert(!GH || 4 * C * 4 <= (int)sizeof(sm.ra.out[3]), "dg partials fit the dg staging tile");
     if (own) {
         const float add = rh == 0 ? xt[d] : 0.f;
 #pragma unroll
@@ -1293,7 +1299,12 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                 st1<ST>(&sm.ra.out[0][t][d], dqa[mm][e]);
                 st1<ST>(&sm.ra.out[1][t][d], dka[mm][e]);
                 st1<ST>(&sm.ra.out[2][t][d], dvo[mm][e]);
-                st1<ST>(&sm.ra.out[3][t][d], lsum[mm][e] + add);
+                if constexpr (GH) {
+                    const float rsum = sum16(lsum[mm][e] + add);
+                    if (r16 == 0) gpart[ct * C + t] = rsum;
+                } else {
+                    st1<ST>(&sm.ra.out[3][t][d], lsum[mm][e] + add);
+                }
             }
     }
     __syncthreads();
@@ -1301,7 +1312,14 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
     tile_out<ST, C, D, NTH>(&sm.ra.out[0][0][0], LDK, static_cast<ST*>(a.dq) + base, rs, valid);
     tile_out<ST, C, D, NTH>(&sm.ra.out[1][0][0], LDK, static_cast<ST*>(a.dk) + base, rs, valid);
     tile_out<ST, C, D, NTH>(&sm.ra.out[2][0][0], LDK, static_cast<ST*>(a.dv) + base, rs, valid);
-    if constexpr (std::is_same<TG, ST>::value) {
+    if constexpr (GH) {
+        if (tid < valid) {
+            float x = 0.f;
+#pragma unroll
+            for (int c2 = 0; c2 < NT; ++c2) x += gpart[c2 * C + tid];
+            static_cast<float*>(a.dg)[bbase + (size_t)tid * a.H] = x;
+        }
+    } else if constexpr (std::is_same<TG, ST>::value) {
         tile_out<ST, C, D, NTH>(&sm.ra.out[3][0][0], LDK, static_cast<ST*>(a.dg) + base, rs, valid);
     } else {
         for (int idx = tid; idx < C * D; idx += NTH) {
@@ -1353,17 +1371,26 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
     float braw;
     {
         Tile<ST, C, D, NTH> tq, tk;
-        constexpr int NCG = D / 8, WPB = NCG / 4, GV = 8 * (int)sizeof(TG) / 16, GE = 16 / (int)sizeof(TG);
+        // GH: one decay per (b, t, h), read once per row
+        constexpr bool GH = std::is_same<TG, GHead>::value;
+        using TGE = typename std::conditional<GH, float, TG>::type;
+        constexpr int NCG = D / 8, WPB = NCG / 4, GV = GH ? 1 : 8 * (int)sizeof(TGE) / 16,
+                      GE = 16 / (int)sizeof(TGE);
         static_assert(NCG % 4 == 0 && NB * WPB <= 8, "one lane per row and 8 channels of g");
         const bool gl = w < NB * WPB;
         const int grow = BS * (w / WPB) + r16, gc = 8 * (4 * (w % WPB) + g4);
         uint4 graw[GV];
+        float gh = 0.f;
         tq.load(static_cast<const ST*>(a.q) + base, rs, valid);
         tk.load(static_cast<const ST*>(a.k) + base, rs, valid);
         if (gl) {
-            const TG* gp = static_cast<const TG*>(a.g) + base + (size_t)min(grow, valid - 1) * rs + gc;
+            if constexpr (GH) {
+                gh = static_cast<const float*>(a.g)[bbase + (size_t)min(grow, valid - 1) * a.H];
+            } else {
+                const TGE* gp = static_cast<const TGE*>(a.g) + base + (size_t)min(grow, valid - 1) * rs + gc;
 #pragma unroll
-            for (int vq = 0; vq < GV; ++vq) graw[vq] = *reinterpret_cast<const uint4*>(gp + GE * vq);
+                for (int vq = 0; vq < GV; ++vq) graw[vq] = *reinterpret_cast<const uint4*>(gp + GE * vq);
+            }
         }
         braw = ld1<ST>(static_cast<const ST*>(a.beta) + bbase + (size_t)min(tid, valid - 1) * a.H);
         // Every wave's q, k, g, beta requests enter the CU's memory pipeline before
@@ -1381,11 +1408,16 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         if (gl) {
             // rows past T read as zero; a = in-block inclusive cumsum of g
             float x[8];
+            if constexpr (GH) {
 #pragma unroll
-            for (int vq = 0; vq < GV; ++vq) {
-                const Vec16<TG> xv{graw[vq]};
+                for (int e = 0; e < 8; ++e) x[e] = (grow < valid) ? gh : 0.f;
+            } else {
 #pragma unroll
-                for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid) ? xv.get(e) : 0.f;
+                for (int vq = 0; vq < GV; ++vq) {
+                    const Vec16<TGE> xv{graw[vq]};
+#pragma unroll
+                    for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid) ? xv.get(e) : 0.f;
+                }
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -1417,7 +1449,8 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
         const int pc = ch + a.pf_ahead, pbh = pc / a.nc, pn = pc - pbh * a.nc;
         const int pb = pbh / a.H, ph = pbh - pb * a.H, pt0 = pn * C, pvalid = min(C, a.T - pt0);
         const size_t pbase = ((size_t)pb * a.T + pt0) * rs + (size_t)ph * D;
-        constexpr int NL = 3 * C;
+        // (a decay per (b, t, h) is 4 bytes a row: not worth a line each)
+        constexpr int NL = (std::is_same<TG, GHead>::value ? 2 : 3) * C;
         static_assert((NL + NTH - 1) / NTH <= Local3Chunk::NPF, "prefetch lines per thread");
 #pragma unroll
         for (int i = 0; i < (NL + NTH - 1) / NTH; ++i) {
@@ -1426,7 +1459,8 @@ __global__ __launch_bounds__(512) void kda_bwd_local3_kernel(const LocalArgs a) 
             if (k < NL) {
                 const int ts = k / C, r = k - ts * C;
                 const char* tp = static_cast<const char*>(ts == 0 ? a.q : ts == 1 ? a.k : a.g);
-                const size_t es = (ts == 2) ? sizeof(TG) : sizeof(ST);
+                const size_t es = (ts == 2) ? sizeof(typename std::conditional<std::is_same<TG, GHead>::value, float, TG>::type)
+                                            : sizeof(ST);
                 if (r < pvalid) p = tp + (pbase + (size_t)r * rs) * es;
             }
             c.pf[i] = p;
@@ -1455,7 +1489,16 @@ static hipError_t launch_local_t(const LocalArgs& a, int nchunks, hipStream_t st
     return hipGetLastError();
 }
 
-hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st) {
+// g_kind: 0 fp32 g, 1 bf16 g, 2 one fp32 decay per (b, t, h) (bf16 inputs at
+// D <= 64 only)
+hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_kind, int nchunks, hipStream_t st) {
+    if (g_kind == 2) {
+        if (!in_bf16) return hipErrorInvalidValue;
+        if (D == 32) return launch_local_t<32, uint16_t, GHead>(a, nchunks, st);
+        if (D == 64) return launch_local_t<64, uint16_t, GHead>(a, nchunks, st);
+        return hipErrorInvalidValue;
+    }
+    const int g_bf16 = g_kind == 1;
 #define KDA_LOCAL_CASE(DD)                                                                         \
     if (D == DD) {                                                                                 \
         if (in_bf16) return g_bf16 ? launch_local_t<DD, uint16_t, uint16_t>(a, nchunks, st)        \

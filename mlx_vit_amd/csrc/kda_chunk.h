@@ -255,8 +255,12 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D, N
                                            const ST* __restrict__ k, const ST* __restrict__ v,
                                            const TG* __restrict__ g, const ST* __restrict__ beta, size_t base,
                                            size_t rstride, size_t bbase, int H, int valid, int dio = D) {
-    constexpr int WPB = NTH / 256, NCG = D / 8, CPL = NCG / (4 * WPB), GV = 8 * (int)sizeof(TG) / 16,
-                  GE = 16 / (int)sizeof(TG);
+    // GH: one decay per (b, t, h) (TG = GHead), read once per row and shared by
+    // the lane's channels
+    constexpr bool GH = std::is_same<TG, GHead>::value;
+    using TGE = typename std::conditional<GH, float, TG>::type;
+    constexpr int WPB = NTH / 256, NCG = D / 8, CPL = NCG / (4 * WPB), GV = GH ? 1 : 8 * (int)sizeof(TGE) / 16,
+                  GE = 16 / (int)sizeof(TGE);
     static_assert(NB == 4 && NCG % (4 * WPB) == 0, "whole 8-channel groups per lane");
     // NARROW: the tensors' rows hold dio < D channels (a multiple of 8); the
     // tile's channels past dio read as zero
@@ -266,6 +270,7 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D, N
     const int tid = threadIdx.x, w = tid >> 6, r16 = tid & 15, g4 = (tid >> 4) & 3;
     const int grow = BS * (w / WPB) + r16, gc0 = 4 * (w % WPB) + g4;
     uint4 graw[CPL][GV];
+    float gh = 0.f;
     if (narrow) {
         tq.load(q + base, rstride, valid, dio);
         tk.load(k + base, rstride, valid, dio);
@@ -273,7 +278,9 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D, N
         tq.load(q + base, rstride, valid);
         tk.load(k + base, rstride, valid);
     }
-    {
+    if constexpr (GH) {
+        gh = reinterpret_cast<const float*>(g)[bbase + (size_t)min(grow, valid - 1) * H];
+    } else {
         const TG* gp = g + base + (size_t)min(grow, valid - 1) * rstride;
 #pragma unroll
         for (int cp = 0; cp < CPL; ++cp) {
@@ -297,11 +304,16 @@ __device__ __forceinline__ int chunk_load2(ChunkSmem<D, ST>& s, Tile<ST, C, D, N
     for (int cp = 0; cp < CPL; ++cp) {
         float x[8];
         const bool cok = !NARROW_OK || 8 * (gc0 + 4 * WPB * cp) < dio;
+        if constexpr (GH) {
 #pragma unroll
-        for (int vq = 0; vq < GV; ++vq) {
-            const Vec16<TG> xv{graw[cp][vq]};
+            for (int e = 0; e < 8; ++e) x[e] = (grow < valid) ? gh : 0.f;
+        } else {
 #pragma unroll
-            for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid && cok) ? xv.get(e) : 0.f;
+            for (int vq = 0; vq < GV; ++vq) {
+                const Vec16<TGE> xv{graw[cp][vq]};
+#pragma unroll
+                for (int e = 0; e < GE; ++e) x[GE * vq + e] = (grow < valid && cok) ? xv.get(e) : 0.f;
+            }
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {

@@ -64,6 +64,11 @@ __device__ __forceinline__ uint32_t pack2bf_rest(float a, float b, uint32_t h) {
     return pack2bf(a - bf_lo(h), b - bf_hi(h));
 }
 
+// Element-type tag of a decay given once per (batch, token, head): fp32
+// [B, T, H], shared by the head's D channels (the scalar-alpha GDN, g = log
+// alpha).  Its gradient is the sum over the channels, fp32 [B, T, H] too.
+struct GHead {};
+
 template <typename T> __device__ __forceinline__ float ld1(const T* p);
 template <> __device__ __forceinline__ float ld1<float>(const float* p) { return *p; }
 template <> __device__ __forceinline__ float ld1<uint16_t>(const uint16_t* p) { return bf2f(*p); }

@@ -622,7 +622,16 @@ static hipError_t launch_prep_t(const PrepArgs& a, int nchunks, hipStream_t st) 
     return hipGetLastError();
 }
 
-hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st) {
+// g_kind: 0 fp32 g, 1 bf16 g, 2 one fp32 decay per (b, t, h) (bf16 inputs at
+// D <= 64 only)
+hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_kind, int nchunks, hipStream_t st) {
+    if (g_kind == 2) {
+        if (!in_bf16) return hipErrorInvalidValue;
+        if (D == 32) return launch_prep_t<32, uint16_t, GHead>(a, nchunks, st);
+        if (D == 64) return launch_prep_t<64, uint16_t, GHead>(a, nchunks, st);
+        return hipErrorInvalidValue;
+    }
+    const int g_bf16 = g_kind == 1;
 #define KDA_PREP_CASE(DD)                                                                          \
     if (D == DD) {                                                                                 \
         if (in_bf16) return g_bf16 ? launch_prep_t<DD, uint16_t, uint16_t>(a, nchunks, st)         \

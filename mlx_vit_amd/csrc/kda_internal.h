@@ -104,13 +104,15 @@ hipError_t launch_seg_fwd(const SegArgs& a, hipStream_t st);
 // once per device under std::call_once, so concurrent callers are safe.
 int device_cu_count(int dev);
 
-hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
+// g_kind: 0 fp32 g [B, T, H, D], 1 bf16 g, 2 one fp32 decay per (b, t, h),
+// g and dg [B, T, H] (GHead; bf16 inputs at D <= 64 only)
+hipError_t launch_prep(const PrepArgs& a, int D, int in_bf16, int g_kind, int nchunks, hipStream_t st);
 // mode 0: O and the final state (and y when a.y is set); 1: the chunk-start states h
 hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStream_t st);
 // whether launch_recur can fuse the gated RMSNorm for this head size and dtype
 bool recur_epilogue_supported(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
-hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);
+hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_kind, int nchunks, hipStream_t st);
 // the local adjoints at D = 128 (kda_bwdw.hip): reads A_kk, the diagonal-block
 // inverses and V' from the workspace
 hipError_t launch_local_wide(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st);

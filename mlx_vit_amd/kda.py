@@ -45,17 +45,37 @@ def _stream(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
+def head_decay_supported(D: int, dtype: torch.dtype) -> bool:
+    """Whether the kernels take one decay per (b, t, h) -- g of shape (B, T, H),
+    the scalar-alpha GDN's -- for this head size and operand dtype (otherwise
+    broadcast g over the channels)."""
+    return dtype == torch.bfloat16 and D in (32, 64)
+
+
+def _g_code(g: torch.Tensor) -> int:
+    """g_dtype code of a prepared g: per channel by dtype, or one fp32 decay per head."""
+    return _lib.KDA_G_HEAD_F32 if g.dim() == 3 else _DTYPE_CODE[g.dtype]
+
+
 def _prepare(q, k, v, g, beta, initial_state):
-    """Validate and normalise inputs (contiguous, consistent dtypes)."""
+    """Validate and normalise inputs (contiguous, consistent dtypes).  g is
+    (B, T, H, D), or (B, T, H) -- one decay per head, shared by its channels --
+    where ``head_decay_supported``."""
     for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor")
     if q.dim() != 4:
         raise ValueError(f"q must be (B, T, H, D); got shape {tuple(q.shape)}")
     B, T, H, D = q.shape
-    for name, t in (("k", k), ("v", v), ("g", g)):
+    for name, t in (("k", k), ("v", v)):
         if tuple(t.shape) != (B, T, H, D):
             raise ValueError(f"{name} shape {tuple(t.shape)} != q shape {(B, T, H, D)}")
+    if tuple(g.shape) == (B, T, H):
+        if not head_decay_supported(D, q.dtype):
+            raise ValueError(f"g of shape (B, T, H) (one decay per head) needs bf16 operands and head_dim in "
+                             f"(32, 64); got {q.dtype}, head_dim={D}: broadcast g to (B, T, H, D)")
+    elif tuple(g.shape) != (B, T, H, D):
+        raise ValueError(f"g shape {tuple(g.shape)} != q shape {(B, T, H, D)} (or {(B, T, H)}, one per head)")
     if tuple(beta.shape) != (B, T, H):
         raise ValueError(f"beta shape {tuple(beta.shape)} != {(B, T, H)}")
     if initial_state is not None and tuple(initial_state.shape) != (B, H, D, D):
@@ -70,7 +90,7 @@ def _prepare(q, k, v, g, beta, initial_state):
             raise ValueError(f"{name} is on {t.device}, q on {dev}")
     dt = q.dtype
     k, v, beta = (t if t.dtype == dt else t.to(dt) for t in (k, v, beta))
-    if g.dtype not in _DTYPE_CODE:
+    if g.dtype not in _DTYPE_CODE or (g.dim() == 3 and g.dtype != torch.float32):
         g = g.to(torch.float32)
     q, k, v, g, beta = (t.contiguous() for t in (q, k, v, g, beta))
     if initial_state is not None:
@@ -140,7 +160,7 @@ def kda_forward(q, k, v, g, beta, initial_state=None, chunk_size: int = CHUNK,
     s_final = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
     ws = _workspace(_lib.KDA_PASS_FWD, B, T, H, D, dev, q.dtype, workspace)
     rc = lib.kda_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
-                     B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                     B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _g_code(g),
                      _ptr(ws), ws.numel(), _stream(dev))
     _lib.check(rc, "kda_fwd")
     return o, s_final
@@ -166,7 +186,7 @@ def kda_forward_train(q, k, v, g, beta, initial_state=None, chunk_size: int = CH
     ws = _workspace(_lib.KDA_PASS_TRAIN, B, T, H, D, dev, q.dtype, workspace,
                     nbytes=train_kept_bytes(B, T, H, D, q.dtype))
     rc = lib.kda_fwd_train(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(o), _ptr(s_final),
-                           B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                           B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _g_code(g),
                            _ptr(ws), ws.numel(), _stream(dev))
     _lib.check(rc, "kda_fwd_train")
     return o, s_final, ws
@@ -210,7 +230,7 @@ def kda_backward(q, k, v, g, beta, initial_state, do, ds_final=None, chunk_size:
     ws = _workspace(_lib.KDA_PASS_BWD, B, T, H, D, dev, q.dtype, workspace)
     args = (_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(do), _ptr(ds_final),
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ds0),
-            B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype])
+            B, T, H, D, chunk_size, _DTYPE_CODE[q.dtype], _g_code(g))
     if not _train:
         _lib.check(lib.kda_bwd(*args, _ptr(ws), ws.numel(), _stream(dev)), "kda_bwd")
         return dq, dk, dv, dg, dbeta, ds0
@@ -267,7 +287,7 @@ def kda_forward_gated(q, k, v, g, beta, initial_state, gate: torch.Tensor, norm_
                     nbytes=train_kept_bytes(B, T, H, D, q.dtype) if train else None)
     rc = lib.kda_fwd_gated(pass_, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(s0), _ptr(gate), ld_z,
                            _ptr(w), float(eps), _ptr(o), _ptr(y), H * D, _ptr(s_final),
-                           B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _DTYPE_CODE[g.dtype],
+                           B, T, H, D, CHUNK, _DTYPE_CODE[q.dtype], _g_code(g),
                            _ptr(ws), ws.numel(), _stream(dev))
     _lib.check(rc, "kda_fwd_gated")
     return y, o, s_final, ws
@@ -330,13 +350,16 @@ def chunk_gdn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, alpha: torch.Te
     q, k, v (B, T, H, D); alpha, beta (B, T, H) with alpha in (0, 1].  The step
     ``S (alpha (I - beta k k^T)) + beta v k^T`` is the KDA step with every
     channel's decay e^{g} equal to alpha, so this runs the KDA kernels on
-    g = log(alpha) broadcast over D (clamped at -80: e^-80 is below fp32's
-    resolution of any state term).  Autograd through the log and the broadcast
-    gives d alpha = sum_d dg / alpha."""
+    g = log(alpha) (clamped at -80: e^-80 is below fp32's resolution of any
+    state term).  With bf16 operands at head_dim 32 or 64 the kernels take g as
+    one fp32 decay per (b, t, h) and return its gradient summed over the
+    channels (``head_decay_supported``); otherwise g is broadcast over D.
+    Autograd through the log (and the broadcast) gives d alpha = sum_d dg / alpha."""
     if alpha.dim() != 3 or tuple(alpha.shape) != tuple(q.shape[:3]):
         raise ValueError(f"alpha must be (B, T, H) = {tuple(q.shape[:3])}; got {tuple(alpha.shape)}")
     g = torch.clamp(torch.log(alpha.float()), min=GDN_LOG_ALPHA_MIN)
-    g = g.unsqueeze(-1).expand(q.shape).contiguous()
+    if not (q.dim() == 4 and head_decay_supported(q.shape[-1], q.dtype)):
+        g = g.unsqueeze(-1).expand(q.shape).contiguous()
     return chunk_kda(q, k, v, g, beta, initial_state, chunk_size)
 
 

@@ -197,6 +197,9 @@ def test_segment_plan_regions(B, T, H, D, dtype, nseg):
     (1, 64, 1, 48, 64, 1, 1, _lib.KDA_E_UNSUPPORTED),    # head dim
     (1, 64, 1, 64, 64, 2, 1, _lib.KDA_E_UNSUPPORTED),    # dtype
     (1, 64, 1, 64, 64, 1, 5, _lib.KDA_E_UNSUPPORTED),    # g dtype
+    (1, 64, 1, 64, 64, 0, 2, _lib.KDA_E_UNSUPPORTED),    # one decay per head: bf16 operands only
+    (1, 64, 1, 128, 64, 1, 2, _lib.KDA_E_UNSUPPORTED),   # ... and D in {32, 64}
+    (1, 64, 1, 96, 64, 1, 2, _lib.KDA_E_UNSUPPORTED),
     (-1, 64, 1, 64, 64, 1, 1, _lib.KDA_E_INVALID),       # negative size
 ])
 def test_fwd_argument_errors(B, T, H, D, chunk, dtype, gdt, code):

@@ -350,21 +350,23 @@ def _layer_case(dtype, with_state, D, fused, B, L, H, hidden):
     _check(errs, TOL[dtype], case)
 
 
-@pytest.mark.parametrize("B,T,H,D,dtype,with_state", [
-    (2, 100, 3, 64, torch.float32, True),
-    (1, 130, 2, 32, torch.float32, False),
-    (2, 77, 4, 64, torch.bfloat16, True),
+@pytest.mark.parametrize("B,T,H,D,dtype,with_state,shift", [
+    (2, 100, 3, 64, torch.float32, True, 1.5),
+    (1, 130, 2, 32, torch.float32, False, 1.5),
+    (2, 77, 4, 64, torch.bfloat16, True, 1.5),       # bf16 D <= 64: one decay per (b, t, h) in the kernels
+    (1, 150, 2, 32, torch.bfloat16, False, 1.5),
+    (1, 130, 2, 64, torch.bfloat16, True, -4.0),     # alpha down to ~0.002: beyond the span guard
 ])
-def test_chunk_gdn_parity(B, T, H, D, dtype, with_state):
+def test_chunk_gdn_parity(B, T, H, D, dtype, with_state, shift):
     """Scalar-alpha GDN (the reference's original gated delta rule) through the
     KDA kernels against the fp64 step loop (nope_gdn_mlx.py:641-650, 919-947):
     outputs and the gradients of q, k, v, alpha, beta and the initial state."""
     from mlx_vit_amd import chunk_gdn
-    case = f"chunk_gdn B={B} T={T} H={H} D={D} {dtype} state={with_state}"
+    case = f"chunk_gdn B={B} T={T} H={H} D={D} {dtype} state={with_state} shift={shift}"
     print(case, flush=True)
     g = torch.Generator().manual_seed(T + D)
     x = R.make_inputs(B, T, H, D, dtype=dtype, seed=T, with_state=with_state, with_grad=True)
-    alpha = torch.sigmoid(torch.randn(B, T, H, generator=g) + 1.5)   # 0.2 .. 0.98
+    alpha = torch.sigmoid(torch.randn(B, T, H, generator=g) + shift)   # shift 1.5: 0.2 .. 0.98
     cot_s = torch.randn(B, H, D, D, generator=g)
     dev = {n: x[n].to(DEV).requires_grad_() for n in ("q", "k", "v", "beta")}
     a_d = alpha.to(DEV).requires_grad_()
