@@ -1302,8 +1302,13 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                 if constexpr (GH) {
                     const float rsum = sum16(lsum[mm][e] + add);
                     if (r16 == 0) gpart[ct * C + t] = rsum;
-                } else {
+                } else if constexpr (std::is_same<TG, ST>::value) {
                     st1<ST>(&sm.ra.out[3][t][d], lsum[mm][e] + add);
+                } else if (t < valid) {
+                    // fp32 g with bf16 operands: dg in fp32 straight from the
+                    // registers (16 lanes write 64 contiguous bytes), not
+                    // through the bf16 staging tile
+                    st1<TG>(static_cast<TG*>(a.dg) + base + (size_t)t * rs + d, lsum[mm][e] + add);
                 }
             }
     }
@@ -1321,11 +1326,6 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
         }
     } else if constexpr (std::is_same<TG, ST>::value) {
         tile_out<ST, C, D, NTH>(&sm.ra.out[3][0][0], LDK, static_cast<ST*>(a.dg) + base, rs, valid);
-    } else {
-        for (int idx = tid; idx < C * D; idx += NTH) {
-            const int t = idx / D, dd = idx - t * D;
-            if (t < valid) st1<TG>(static_cast<TG*>(a.dg) + base + (size_t)t * rs + dd, ld1<ST>(&sm.ra.out[3][t][dd]));
-        }
     }
     if (tid < valid) st1<ST>(static_cast<ST*>(a.dbeta) + bbase + (size_t)tid * a.H, sm.dbeta[tid]);
 }

@@ -531,10 +531,9 @@ def test_head_decay_equals_broadcast(B, T, H, D, with_state, g_scale):
     """g of shape (B, T, H) -- one fp32 decay per head, the scalar-alpha GDN's --
     gives what the same g broadcast over the channels gives: o, S_T and dq, dk,
     dv, dbeta, dS0 bit for bit (standalone calls and the training pair).  dg is
-    the channel sum, formed in fp32 in the kernel; against the fp64 oracle's
-    channel sum it is within the bf16 bar and at least as close as the
-    broadcast path's dg summed afterwards (whose per-channel values pass
-    through the kernel's bf16 output staging)."""
+    the channel sum, formed in fp32 in the kernel: the broadcast path's fp32
+    per-channel dg summed afterwards (another summation order), and within the
+    bf16 bar of the fp64 oracle's channel sum."""
     kda = _kda()
     x = _inputs(B, T, H, D, torch.bfloat16, seed=41, with_state=with_state, grad=True, g_scale=g_scale)
     gen = torch.Generator().manual_seed(42)
@@ -561,9 +560,10 @@ def test_head_decay_equals_broadcast(B, T, H, D, with_state, g_scale):
     for n, a, b, t in zip(names, gr_h, gr_b, gr_t):
         assert torch.equal(a, t), n
         if n == "dg":
-            err_h, err_b = R.rel_l2(a.double().cpu(), ref), R.rel_l2(b.double().sum(-1).cpu(), ref)
-            print("dg channel sum vs fp64 oracle: head", f"{err_h:.2e}", "broadcast", f"{err_b:.2e}")
-            assert err_h <= TOL[torch.bfloat16] and err_h <= 1.05 * err_b, (err_h, err_b)
+            err_hb = R.rel_l2(a.double().cpu(), b.double().sum(-1).cpu())
+            err_h = R.rel_l2(a.double().cpu(), ref)
+            print("dg channel sum: head vs broadcast", f"{err_hb:.2e}", "head vs fp64 oracle", f"{err_h:.2e}")
+            assert err_hb <= 1e-5 and err_h <= TOL[torch.bfloat16], (err_hb, err_h)
         else:
             assert torch.equal(a, b), n
 
