@@ -51,6 +51,9 @@ WORKLOADS = {
     "cfg2-layerdecay": (8, 1568, 12, 64, True, False,
                         "KDA fwd+VJP (training pair), B8 H12 T1568 D64 bf16, layer-init decay "
                         "g = -A_h softplus(N(0, 0.5^2)), A_h ~ U[1, 16]"),
+    "ssv2-d96-layerdecay": (8, 1568, 8, 96, True, False,
+                            "KDA fwd+VJP (training pair), B8 H8 T1568 D96 bf16 (SSv2 layer), layer-init decay "
+                            "g = -A_h softplus(N(0, 0.5^2)), A_h ~ U[1, 16]"),
     # the scalar-alpha sibling (chunk_gdn, nope_gdn_mlx.py:641-650): one decay per
     # (b, t, h), alpha = e^{-softplus(N(0, 1)) * 0.1}, run as the KDA pair on
     # g = log(alpha) given once per head (bf16, D = 64), with chunk_gdn's host
@@ -59,7 +62,7 @@ WORKLOADS = {
                  "scalar-alpha GDN fwd+VJP (chunk_gdn: the KDA pair on g = log alpha, one decay per head), "
                  "B8 H12 T1568 D64 bf16"),
 }
-LAYER_DECAY = {"cfg2-layerdecay"}
+LAYER_DECAY = {"cfg2-layerdecay", "ssv2-d96-layerdecay"}
 SCALAR_DECAY = {"gdn-cfg2"}
 
 

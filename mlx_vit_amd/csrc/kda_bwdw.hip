@@ -62,6 +62,53 @@ __device__ __forceinline__ float sum4gw(float x) {
     return x;
 }
 
+// The diagonal tile of block m, pair by pair, for the lane's rows t = 16 m +
+// 4 g4 + e of channel d: everything from LDS -- gamma g (row stride ldg), the
+// staged raw k / q rows sk / sq (row stride ldq), dP sp and dA sda (row stride
+// lda) -- and the sums (dk, dq, dgamma terms) to res[3][16][D].  Not inlined:
+// its loops stay out of the register allocation of the kernel's common path.
+template <int D, typename TI, int PREC>
+__device__ __noinline__ void wide_pair_block(const float* __restrict__ g, int ldg, const TI* __restrict__ sk,
+                                             const TI* __restrict__ sq, int ldq, const float* __restrict__ sp,
+                                             const float* __restrict__ sda, int lda, float* __restrict__ res, int m,
+                                             int g4, int d) {
+    // the lane's four rows advance together: four independent sums per step
+    float gt[4], kt[4], qt[4], ak[4], aq[4], ag[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int t = BS * m + 4 * g4 + e;
+        gt[e] = g[t * ldg + d];
+        kt[e] = ld1<TI>(sk + t * ldq + d);
+        qt[e] = ld1<TI>(sq + t * ldq + d);
+        ak[e] = aq[e] = ag[e] = 0.f;
+    }
+#pragma unroll 1
+    for (int r = 0; r < BS; ++r) {
+        const int sx = BS * m + r;
+        const float gs = g[sx * ldg + d], ks_raw = ld1<TI>(sk + sx * ldq + d), qs_raw = ld1<TI>(sq + sx * ldq + d);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int rt = 4 * g4 + e, t = BS * m + rt;
+            // row side: pair (t, s), s < t; column side: pair (s, t), s > t
+            const bool row = r < rt, col = r > rt;
+            const float ex = kexp<PREC>(row ? gt[e] - gs : gs - gt[e]);
+            const float pp = sp[row ? t * lda + sx : sx * lda + t], pa = sda[row ? t * lda + sx : sx * lda + t];
+            const float ks = ks_raw * ex;
+            const float c = (pp * ks_raw + pa * qs_raw) * ex;
+            ak[e] += row ? pp * ks : col ? c : 0.f;
+            aq[e] += row ? pa * ks : 0.f;
+            ag[e] += row ? (pp * kt[e] + pa * qt[e]) * ks : col ? -c * kt[e] : 0.f;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int rt = 4 * g4 + e;
+        res[(0 * BS + rt) * D + d] = ak[e];
+        res[(1 * BS + rt) * D + d] = aq[e];
+        res[(2 * BS + rt) * D + d] = ag[e];
+    }
+}
+
 }  // namespace
 
 template <int D, typename TI, typename TG, int PREC>
@@ -168,7 +215,10 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     }
     // thread (channel cd, block cb): inclusive cumsum of g over the block's 16
     // rows (rows past T are g = 0: no decay), then the totals of earlier blocks
-    int flag = 0;
+    // flag: g > 0 or a NaN somewhere (every pair of the chunk pair by pair);
+    // sflag: a 16-row block's decay span beyond the anchored guard (its
+    // diagonal tile pair by pair, the other tiles on exact per-lane factors)
+    int flag = 0, sflag = 0;
     {
         float run = 0.f;
 #pragma unroll
@@ -192,7 +242,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     // NaN, is evaluated pair by pair)
     for (int idx = tid; idx < NB * D; idx += NTH) {
         const int j = idx / D, d = idx % D;
-        if (!(s.g[BS * j][d] - s.g[BS * j + BS - 1][d] <= SPAN_MAX)) flag = 1;
+        if (!(s.g[BS * j][d] - s.g[BS * j + BS - 1][d] <= SPAN_MAX)) sflag = 1;
         s.er[j][d] = kexp<PREC>(s.g[BS * j][d]);
     }
     for (int idx = tid; idx < 6 * D; idx += NTH) {
@@ -201,6 +251,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
         s.f[p][d] = kexp<PREC>(s.g[BS * i][d] - s.g[BS * j][d]);
     }
     const int unsafe = __syncthreads_or(flag);
+    const int strong = __syncthreads_or(sflag);
 
     // wave w owns channel tile w: rows t = 16 m + 4 g4 + e, channel d
     const int nt = w, d = nt * BS + r16;
@@ -464,27 +515,42 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     __syncthreads();
 
     // ---------------- phase 4: decay-masked K K^T / Q K^T adjoints ----------------
-    if (!unsafe) {
+    // Anchored adjoints (g <= 0 everywhere).  STRONG: some 16-row block spans
+    // more than SPAN_MAX, so the block-start anchor's factor e^{gamma_16j -
+    // gamma_s} could overflow: the off-diagonal tiles take the exact per-lane
+    // factor e^{gamma_16i - gamma_s} (<= 1) instead of er * F_ij, and the
+    // diagonal tiles are evaluated pair by pair within their block.
+    auto anchored = [&](auto strong_c) __attribute__((always_inline)) {
+        constexpr bool STRONG = decltype(strong_c)::value;
         // row and column sides of a pair must agree to fp32: exact split products
         constexpr int PX = PREC >= 3 ? 4 : PREC;
         // er = e^{gamma_r - gamma_t} (r = 16 m), formed here rather than with the
         // other per-lane values so that it is not live across phases 1-3
         float er[NB][4];
+        if constexpr (!STRONG) {
 #pragma unroll
-        for (int m = 0; m < NB; ++m) {
-            const float gr = s.g[BS * m][d];
+            for (int m = 0; m < NB; ++m) {
+                const float gr = s.g[BS * m][d];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) er[m][e] = kexp<PREC>(gr - s.g[BS * m + 4 * g4 + e][d]);
+                for (int e = 0; e < 4; ++e) er[m][e] = kexp<PREC>(gr - s.g[BS * m + 4 * g4 + e][d]);
+            }
         }
+        // STRONG: the exact factor e^{gamma_16i - gamma_s}, s = 16 j + 4 g4 + e,
+        // j < i, formed where it is used (the same expression on both sides of
+        // a pair, so both use the same value)
+        auto wf = [&](int i, int j, int e) __attribute__((always_inline)) {
+            return kexp<PREC>(s.g[BS * i][d] - s.g[BS * j + 4 * g4 + e][d]);
+        };
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             f32x4 dKl = zero4(), dQl = zero4();
 #pragma unroll
             for (int j = 0; j <= i; ++j) {
+                if (STRONG && j == i) continue;
                 const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
-                Fr4 B;   // K_r of the lane's rows of block j (channel d), times F_ij
+                Fr4 B;   // K_r of the lane's rows of block j (channel d), times the pair's factor
 #pragma unroll
-                for (int e = 0; e < 4; ++e) B.v[e] = kx[j][e] * er[j][e] * fs;
+                for (int e = 0; e < 4; ++e) B.v[e] = STRONG ? kx[j][e] * wf(i, j, e) : kx[j][e] * er[j][e] * fs;
                 dKl = mma4<PX>(frag4(&sp[0][0], C + 4, BS * i, BS * j), B, dKl);
                 Fr4 Aq = frag4(&sda[0][0], C + 4, BS * i, BS * j);
                 if (j == i) {   // the diagonal pairs (t, t) are added apart, below
@@ -511,6 +577,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
             }
 #pragma unroll
             for (int j = 0; j <= i; ++j) {
+                if (STRONG && j == i) continue;
                 f32x4 dKr = mma4<PX>(frag4T(&sp[0][0], C + 4, BS * j, BS * i), Bk, zero4());
                 Fr4 Aq = frag4T(&sda[0][0], C + 4, BS * j, BS * i);
                 if (j == i) {
@@ -522,12 +589,55 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
                 const float fs = (j < i) ? s.f[pair_idx(i, j)][d] : 1.f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    dka[j][e] += dKr[e] * fs * er[j][e];
+                    const float ws = STRONG ? wf(i, j, e) : fs * er[j][e];
+                    dka[j][e] += dKr[e] * ws;
                     // the row side's B operand for this s and block pair
-                    dga[j][e] -= dKr[e] * mfma_operand<PREC>(kx[j][e] * er[j][e] * fs);
+                    dga[j][e] -= dKr[e] * mfma_operand<PREC>(STRONG ? kx[j][e] * ws : kx[j][e] * er[j][e] * fs);
                 }
             }
         }
+        if constexpr (STRONG) {
+            // The diagonal tiles pair by pair within each block, with the exact
+            // weight e^{gamma_t - gamma_s} (s < t) from LDS gamma.  Everything the
+            // pair loops read comes from LDS -- the raw k and q rows (exact in
+            // bf16) staged in the free staging area -- and their sums go back
+            // there (per block: 16 rows x 3 planes, fp32), so the loops hold no
+            // per-lane arrays; each lane then adds its own rows' sums.
+            TI* const sk = st0;
+            TI* const sq = st1p;
+            float* const res = reinterpret_cast<float*>(stg + 2 * T_BYTES);   // [3][BS][D]
+            static_assert(2 * T_BYTES + 3 * BS * D * 4 <= STG_BYTES, "pair sums fit the staging area");
+#pragma unroll
+            for (int m = 0; m < NB; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = BS * m + 4 * g4 + e;
+                    st1<TI>(sk + t * LDQ + d, kx[m][e]);
+                    st1<TI>(sq + t * LDQ + d, qx[m][e]);
+                }
+#pragma unroll
+            for (int m = 0; m < NB; ++m) {
+                __syncthreads();   // staged rows visible; the previous block's sums read
+                wide_pair_block<D, TI, PREC>(&s.g[0][0], D + 4, sk, sq, LDQ, &sp[0][0], &sda[0][0], C + 4, res, m, g4,
+                                             d);
+                // the lane's own rows: written by itself above, no barrier needed
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int rt = 4 * g4 + e;
+                    dka[m][e] += res[(0 * BS + rt) * D + d];
+                    dqa[m][e] += res[(1 * BS + rt) * D + d];
+                    dga[m][e] += res[(2 * BS + rt) * D + d];
+                }
+            }
+        }
+    };
+    // (fp32 operands: no room to stage k and q, so a chunk past the span guard
+    // takes the pair-by-pair path below)
+    if (!unsafe && !(strong && !STG)) {
+        if (STG && strong)
+            anchored(std::integral_constant<bool, STG>{});
+        else
+            anchored(std::false_type{});
     } else {
         // pair by pair with the exact weight e^{gamma_t - gamma_s}: raw k and q of
         // the other rows from global memory, gamma from LDS

@@ -279,6 +279,42 @@ def test_mixed_span_blocks(dtype, scales):
     _assert_all(_bwd_errors(x, dtype), TOL[dtype], f"bwd mixed spans {dtype} {scales}")
 
 
+@pytest.mark.parametrize("scales", [(12.0, 0.1, 12.0, 0.1), (0.1, 0.1, 0.1, 14.0), (16.0, 16.0, 0.3, 6.0)])
+def test_mixed_span_blocks_d128(scales):
+    """bf16 at D = 128 (the wide local-adjoint kernel): 16-row blocks beyond the
+    span guard next to weakly decaying ones.  Their diagonal tiles go pair by
+    pair within the block and the other tiles take exact per-lane factors;
+    forward and backward against the fp64 oracle."""
+    x = _inputs(1, 200, 2, 128, torch.bfloat16, seed=33, with_state=True, grad=True, g_scale=1.0)
+    x = _block_scaled(x, scales)
+    x["g"] = x["g"].float()
+    _assert_all(_fwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], f"fwd mixed spans D128 {scales}")
+    _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], f"bwd mixed spans D128 {scales}")
+
+
+def test_layer_init_decay_d96():
+    """The SSv2 layer's decay at initialisation, g = -A_h softplus(N(0, 0.5^2))
+    with A_h ~ U[1, 16] per head (nope_gdn_mlx.py:749): nearly every 16-row
+    block beyond the span guard, at D = 96, bf16, through the training pair."""
+    kda = _kda()
+    B, T, H, D = 1, 300, 4, 96
+    x = _inputs(B, T, H, D, torch.bfloat16, seed=34, with_state=True, grad=True)
+    gen = torch.Generator().manual_seed(35)
+    A = torch.linspace(1.0, 16.0, H)
+    x["g"] = (-A[None, None, :, None] * torch.nn.functional.softplus(0.5 * torch.randn(B, T, H, D, generator=gen))
+              ).to(torch.bfloat16)
+    q, k, v, g, beta = _dev(x)
+    s0, do = x["s0"].to(DEV), x["do"].to(DEV)
+    o, sf, ws = kda.kda_forward_train(q, k, v, g, beta, s0)
+    grads = kda.kda_backward_train(q, k, v, g, beta, s0, do, None, ws)
+    torch.cuda.synchronize()
+    ref = cref.forward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"])
+    refb = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"])
+    errs = {"o": R.rel_l2(o.cpu(), ref["o"]), "s_final": R.rel_l2(sf.cpu(), ref["s_final"])}
+    errs.update({n: R.rel_l2(gr.cpu(), refb[n]) for n, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads)})
+    _assert_all(errs, TOL[torch.bfloat16], "layer-init decay D96")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_positive_decay_chunks(dtype):
     """g > 0 in some chunks (outside the layer's domain, but the op and the
