@@ -10,7 +10,7 @@
 //   kda_segchain_kernel<D, 1>  pass A: X and M of every segment but the last,
 //                              one workgroup per (b, h, segment);
 //   kda_segscan_kernel<D>      pass B: Sigma_in of segments 1 .. nseg-1 in
-//                              order, per (b, h) and 64-column block;
+//                              order, per (b, h) and 16-column block;
 //   kda_segchain_kernel<D, 0>  pass C: every segment's forward from its
 //                              Sigma_in -- O, and the final state from the
 //                              last segment.
@@ -385,23 +385,35 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
     }
 }
 
-// Pass B: Sigma_in of segments 1 .. nseg - 1 of one (b, h), 64 dv columns per
-// workgroup (wave w: 16 columns), Sigma_in[s + 1] = M_s Sigma_in[s] + X_s with
-// fp32-accurate split-bf16 products (Sigma and M as bf16 hi + lo).  M_s^T (hi
-// and lo planes) reaches LDS by DMA one step ahead; X_s is loaded one step
-// ahead into registers.  Natural row order; written in the reference
-// orientation [dv][dk], as s0 is.
+// Pass B: Sigma_in of segments 1 .. nseg - 1 of one (b, h), 16 dv columns per
+// workgroup, Sigma_in[s + 1] = M_s Sigma_in[s] + X_s with fp32-accurate
+// split-bf16 products (Sigma and M as bf16 hi + lo).  Wave w owns the row
+// tiles 2 w and 2 w + 1 (dk_out rows 32 w .. 32 w + 31) of the columns: four
+// waves share a step's products instead of each forming all 128 rows of its
+// own columns.  Those two tiles are the B operand of k-step w of the next
+// step, so each wave passes its split fragments lane for lane to the others
+// through a double-buffered LDS exchange, one barrier per step.  M_s^T (hi
+// and lo planes) reaches LDS by DMA one step ahead and is read once per
+// workgroup; X_s is loaded one step ahead into registers; a step's result is
+// stored during the next step, so that no wait at a step's start covers a
+// store just issued.  Natural row order; written in the reference orientation
+// [dv][dk], as s0 is.  Same products in the same order as one wave forming
+// all rows: the results do not depend on the split.
 template <int D>
 __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
     using ST = uint16_t;
-    constexpr int NI = D / BS, KS = D / 32, NCB = D / 64, RB = 2 * D, PLANE = D * RB;
+    constexpr int NI = D / BS, KS = D / 32, RB = 2 * D, PLANE = D * RB;
+    static_assert(NI == 2 * KS && KS == 4, "four waves, wave w owning row tiles 2 w and 2 w + 1 (k-step w)");
     using TM = DmaTile<D, RB, 4>;
     __shared__ __align__(1024) char smem[2 * 2 * PLANE];
+    __shared__ __align__(16) uint4 xch[2][KS][2][64];   // [buffer][k-step][hi, lo][lane]: B fragments of Sigma
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
               g4 = l >> 4;
     __builtin_assume(w >= 0 && w < 4);
-    const int bh = blockIdx.x / NCB, cbk = blockIdx.x - bh * NCB;
-    const int col = 64 * cbk + BS * w + r16;
+    // workgroups go to the XCDs round robin: with BH a multiple of 8, the
+    // column blocks of one (b, h) share an XCD (and its L2 copy of M)
+    const int bh = blockIdx.x % a.BH, cbk = blockIdx.x / a.BH;
+    const int col = BS * cbk + r16;
     const int nsteps = a.nseg - 1;
     uint32_t oM[TM::COUNT];
     TM::offsets(oM, RB, w, l);
@@ -410,41 +422,61 @@ __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
         TM::issue_s(src, oM, buf, w);
         TM::issue_s(src + PLANE, oM, buf + PLANE, w);
     };
-    auto load_x = [&](int s, f32x4 (&X)[NI]) __attribute__((always_inline)) {
+    // rows BS i + 4 g4 .. + 3, i = 2 w + u, of the lane's column
+    auto load_x = [&](int s, f32x4 (&X)[2]) __attribute__((always_inline)) {
         const float* xp = a.segX + ((size_t)bh * a.nseg + s) * D * D + (size_t)col * D;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const float4 x = *reinterpret_cast<const float4*>(xp + BS * i + 4 * g4);
-            X[i] = f32x4{x.x, x.y, x.z, x.w};
+        for (int u = 0; u < 2; ++u) {
+            const float4 x = *reinterpret_cast<const float4*>(xp + BS * (2 * w + u) + 4 * g4);
+            X[u] = f32x4{x.x, x.y, x.z, x.w};
         }
     };
-    f32x4 S[NI], Xn[NI];
+    auto store_s = [&](int s, const f32x4 (&S)[2]) __attribute__((always_inline)) {
+        float* out = a.segS + ((size_t)bh * a.nseg + s) * D * D + (size_t)col * D;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        S[i] = zero4();
+        for (int u = 0; u < 2; ++u)
+            *reinterpret_cast<float4*>(out + BS * (2 * w + u) + 4 * g4) = make_float4(S[u][0], S[u][1], S[u][2], S[u][3]);
+    };
+    // the wave's two tiles as the split B fragment of k-step w
+    auto put_b = [&](int buf, const f32x4 (&S)[2]) __attribute__((always_inline)) {
+        const Frag8 f = accfrag<3>(S[0], S[1]);
+        xch[buf][w][0][l] = __builtin_bit_cast(uint4, f.h);
+        xch[buf][w][1][l] = __builtin_bit_cast(uint4, f.l);
+    };
+    f32x4 S[2], Xn[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        S[u] = zero4();
         if (a.s0) {
-            const float4 x = *reinterpret_cast<const float4*>(a.s0 + ((size_t)bh * D + col) * D + BS * i + 4 * g4);
-            S[i] = f32x4{x.x, x.y, x.z, x.w};
+            const float4 x =
+                *reinterpret_cast<const float4*>(a.s0 + ((size_t)bh * D + col) * D + BS * (2 * w + u) + 4 * g4);
+            S[u] = f32x4{x.x, x.y, x.z, x.w};
         }
     }
+    put_b(0, S);
     dma_m(0, smem);
     load_x(0, Xn);
     for (int s = 0; s < nsteps; ++s) {
         dma_wait<0>();
-        lds_barrier();   // M_s landed for every wave; the other buffer is free
+        lds_barrier();   // M_s landed for every wave, the exchange buffer s & 1 written; the other M buffer is free
+        if (s > 0) store_s(s, S);   // Sigma_in of segment s, formed in the previous step
         if (s + 1 < nsteps) dma_m(s + 1, smem + ((s + 1) & 1) * 2 * PLANE);
-        f32x4 Xc[NI];
+        f32x4 Xc[2];
 #pragma unroll
-        for (int i = 0; i < NI; ++i) Xc[i] = Xn[i];
+        for (int u = 0; u < 2; ++u) Xc[u] = Xn[u];
         if (s + 1 < nsteps) load_x(s + 1, Xn);
         const ST* Mh = reinterpret_cast<const ST*>(smem + (s & 1) * 2 * PLANE);
         const ST* Ml = reinterpret_cast<const ST*>(smem + (s & 1) * 2 * PLANE + PLANE);
         Frag8 B[KS];
 #pragma unroll
-        for (int k = 0; k < KS; ++k) B[k] = accfrag<3>(S[2 * k], S[2 * k + 1]);
+        for (int k = 0; k < KS; ++k) {
+            B[k].h = __builtin_bit_cast(bf16x8, xch[s & 1][k][0][l]);
+            B[k].l = __builtin_bit_cast(bf16x8, xch[s & 1][k][1][l]);
+        }
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            f32x4 acc = Xc[i];
+        for (int u = 0; u < 2; ++u) {
+            const int i = 2 * w + u;
+            f32x4 acc = Xc[u];
 #pragma unroll
             for (int k = 0; k < KS; ++k) {
                 Frag8 A;
@@ -452,13 +484,12 @@ __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
                 A.l = ldfragT_sw<RB>(Ml, BS * i, 32 * k).h;
                 acc = mma<3>(A, B[k], acc);
             }
-            S[i] = acc;
+            S[u] = acc;
         }
-        float* out = a.segS + ((size_t)bh * a.nseg + s + 1) * D * D + (size_t)col * D;
-#pragma unroll
-        for (int i = 0; i < NI; ++i)
-            *reinterpret_cast<float4*>(out + BS * i + 4 * g4) = make_float4(S[i][0], S[i][1], S[i][2], S[i][3]);
+        // buffer (s + 1) & 1 was last read in step s - 1, before this step's barrier
+        put_b((s + 1) & 1, S);
     }
+    if (nsteps > 0) store_s(nsteps, S);
 }
 
 // waves per workgroup of the segment maps and the segment forwards (eight: two
@@ -489,7 +520,7 @@ hipError_t launch_seg_map(const SegArgs& a, hipStream_t st) {
 
 hipError_t launch_seg_scan(const SegArgs& a, hipStream_t st) {
     if (a.nseg < 2) return hipSuccess;
-    hipLaunchKernelGGL((kda_segscan_kernel<128>), dim3(a.BH * (128 / 64)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((kda_segscan_kernel<128>), dim3(a.BH * (128 / BS)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
