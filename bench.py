@@ -43,6 +43,10 @@ WORKLOADS = {
              "KDA fwd+VJP (training pair), B8 H12 T1568 D64 bf16 (config 2)"),
     "cfg1": (8, 1568, 12, 64, False, False, "KDA fwd, B8 H12 T1568 D64 bf16 (config 1)"),
     "cfg3": (1, 32768, 16, 128, False, True, "KDA fwd, B1 H16 T32768 D128 bf16, fp32 S0 (config 3)"),
+    # config 3's shape trained: 16 long sequences at D = 128 (the backward's
+    # state recompute over segments)
+    "cfg3-train": (1, 32768, 16, 128, True, True,
+                   "KDA fwd+VJP (training pair), B1 H16 T32768 D128 bf16, fp32 S0 (config 3's shape)"),
     # the reference's SSv2 layer (train_mlx_ssv2.py:71-80): 8 heads of 96, 1568 tokens
     "ssv2-d96": (8, 1568, 8, 96, True, False, "KDA fwd+VJP (training pair), B8 H8 T1568 D96 bf16 (SSv2 layer)"),
     # config 2's shape with the decay of the reference layer at initialisation:

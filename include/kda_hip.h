@@ -53,8 +53,10 @@ extern "C" {
 #define KDA_PASS_TRAIN 2   /* kda_fwd_train + kda_bwd_train share one workspace */
 
 /* Workspace regions (see kda_workspace_offsets).  SEGX, SEGM and SEGS exist
- * only for the bf16 forward at D = 128 when it splits the sequence into
- * segments: per (b, h, segment) the segment's state map and start state.
+ * only at bf16 D = 128 when the sequence is split into segments: per (b, h,
+ * segment) the segment's state map and start state, for the forward (pass 0,
+ * more than one segment) and for the backward's state recompute (passes 1 and
+ * 2, at least 8 segments; in pass 2 among the backward's own regions).
  * PAD and PADB exist only at D = 96, which runs the D = 128 kernels with
  * channels 96..127 zero: the other regions are then those of D = 128; PAD
  * holds the padded s0 (and, for the forward passes, o and s_final), PADB the
@@ -62,8 +64,8 @@ extern "C" {
  * Order: passes 0 and 1 lay the regions out in this order.  Pass 2 puts first
  * the regions kda_fwd_train writes and kda_bwd_train reads (the kept part,
  * kda_train_kept_size bytes: W .. EG and PAD) and after them those only the
- * backward uses (H, DH, VP, DVP, PADB), so that the backward's part can be a
- * buffer of its own (kda_bwd_train_split). */
+ * backward uses (H, DH, VP, DVP, SEGX, SEGM, SEGS, PADB), so that the
+ * backward's part can be a buffer of its own (kda_bwd_train_split). */
 enum kda_ws_region {
     KDA_WS_W = 0, KDA_WS_U, KDA_WS_QP, KDA_WS_QPT, KDA_WS_KB, KDA_WS_KBT, KDA_WS_WT,
     KDA_WS_AQK, KDA_WS_AQKT, KDA_WS_AKK, KDA_WS_TII, KDA_WS_EG, KDA_WS_H, KDA_WS_DH,

@@ -42,7 +42,8 @@ struct Layout {
 
 // regions only the backward writes and reads (the training pair's scratch)
 bool backward_region(int r) {
-    return r == KDA_WS_H || r == KDA_WS_DH || r == KDA_WS_VP || r == KDA_WS_DVP || r == KDA_WS_PADB;
+    return r == KDA_WS_H || r == KDA_WS_DH || r == KDA_WS_VP || r == KDA_WS_DVP || r == KDA_WS_PADB ||
+           r == KDA_WS_SEGX || r == KDA_WS_SEGM || r == KDA_WS_SEGS;
 }
 
 int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, bool bwd) {
@@ -75,6 +76,26 @@ bool seg_forward(int pass, int B, int T, int H, int D, int dtype, int* nseg, int
     if (pass != KDA_PASS_FWD || dtype != KDA_DTYPE_BF16 || D != 128 || (size_t)B * T * H == 0) return false;
     kda::seg_plan(B * H, (T + kda::C - 1) / kda::C, nseg, seg_len);
     return *nseg > 1;
+}
+
+// Whether the backward's state recompute runs segmented (the same plan and
+// passes A and B, then the chunk-start states per segment): bf16 at the
+// kernels' D = 128 when the plan has at least SEG_STATES_MIN segments.  The
+// segment passes read the chunk slabs twice (maps, then states), about 1.4x
+// the bytes of one chain per (b, h), and take about 3.4 times as long per
+// chunk of a segment as that chain per chunk at D = 128 (SSv2's shape, 64
+// (b, h) x 25 chunks, 4 segments: 95 against 87 us); with 8 or more segments
+// (at most 32 (b, h)) the segments' length, not the sequence's, sets the time.
+constexpr int SEG_STATES_MIN = 8;
+bool seg_states(int pass, int B, int T, int H, int D, int dtype, int* nseg, int* seg_len) {
+    *nseg = 1;
+    *seg_len = 0;
+    if (pass == KDA_PASS_FWD || dtype != KDA_DTYPE_BF16 || D != 128 || (size_t)B * T * H == 0) return false;
+    kda::seg_plan(B * H, (T + kda::C - 1) / kda::C, nseg, seg_len);
+    if (*nseg >= SEG_STATES_MIN) return true;
+    *nseg = 1;
+    *seg_len = 0;
+    return false;
 }
 
 // D = 96 runs the D = 128 kernels.  The prep and the local-adjoint kernel read
@@ -157,7 +178,8 @@ void region_sizes(int pass, int B, int T, int H, int D, int dtype, size_t* sz) {
         }
     }
     int nseg, seg_len;
-    if (seg_forward(pass, B, T, H, D, dtype, &nseg, &seg_len)) {
+    if (seg_forward(pass, B, T, H, D, dtype, &nseg, &seg_len) ||
+        seg_states(pass, B, T, H, D, dtype, &nseg, &seg_len)) {
         const size_t per = (size_t)B * H * nseg * D * D * 4;
         sz[KDA_WS_SEGX] = per;
         sz[KDA_WS_SEGM] = per;
@@ -667,13 +689,32 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
     void* Vp = region(ws, KDA_WS_VP);
     void* dVp = region(ws, KDA_WS_DVP);
 
-    // chunk-boundary states, recomputed from the per-chunk factors
-    kda::RecurArgs ra = {};
-    ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
-    ra.Kb = region(ws, KDA_WS_KB);
-    ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-    e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
-    if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
+    // chunk-boundary states, recomputed from the per-chunk factors: bf16 D = 128
+    // over segments (maps, start states, the segments' chunk-start states),
+    // otherwise one chain per (b, h)
+    int nseg, seg_len;
+    if (seg_states(pass, B, T, H, D, dtype, &nseg, &seg_len)) {
+        kda::SegArgs sa = {};
+        sa.W = W; sa.U = U; sa.KbT = KbT; sa.eG = eG; sa.s0 = s0; sa.h = hS; sa.Vp = Vp;
+        sa.segX = fregion(ws, KDA_WS_SEGX);
+        sa.segM = static_cast<uint16_t*>(region(ws, KDA_WS_SEGM));
+        sa.segS = fregion(ws, KDA_WS_SEGS);
+        sa.T = T; sa.H = H; sa.nc = nc; sa.BH = BH; sa.nseg = nseg; sa.seg_len = seg_len;
+        e = timed(PROF_RECUR_H, st, [&] {
+            hipError_t r = kda::launch_seg_map(sa, st);
+            if (r == hipSuccess) r = kda::launch_seg_scan(sa, st);
+            if (r == hipSuccess) r = kda::launch_seg_states(sa, st);
+            return r;
+        });
+        if (e != hipSuccess) return hip_fail(e, "kda_segchain_kernel(states)");
+    } else {
+        kda::RecurArgs ra = {};
+        ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
+        ra.Kb = region(ws, KDA_WS_KB);
+        ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
+        e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
+        if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
+    }
 
     kda::DhArgs da = {};
     da.AqkT = region(ws, KDA_WS_AQKT);

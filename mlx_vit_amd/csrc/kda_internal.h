@@ -81,8 +81,10 @@ struct LocalArgs {
 // The bf16 forward at D = 128 split over segments of the sequence (kda_seg.hip):
 // pass A (launch_seg_map) writes each segment's map X, M; pass B
 // (launch_seg_scan) the start state of segments 1 .. nseg - 1; pass C
-// (launch_seg_fwd) O and the final state.  segX, segS: [BH][nseg][D][D] fp32 in
-// the reference orientation [dv][dk]; segM: [BH][nseg][2][D][D] bf16, M^T
+// (launch_seg_fwd) O and the final state, or, for the backward's state
+// recompute, (launch_seg_states) the chunk-start states h and V'.  segX, segS:
+// [BH][nseg][D][D] fp32 in the reference orientation [dv][dk]; segM:
+// [BH][nseg][2][D][D] bf16, M^T
 // ([dk_in][dk_out]) split into hi and lo planes (the same bytes as fp32).
 struct SegArgs {
     const void *W, *U, *Qp, *KbT, *Aqk;
@@ -90,6 +92,7 @@ struct SegArgs {
     const float* s0;
     float* s_final;
     void* o;
+    void *h, *Vp;   // launch_seg_states: chunk-start states [BH nc][D][D], V' [BH nc][C][D] (bf16)
     float *segX, *segS;
     uint16_t* segM;
     int T, H, nc, BH, nseg, seg_len;
@@ -99,6 +102,7 @@ void seg_plan(int BH, int nc, int* nseg, int* seg_len);
 hipError_t launch_seg_map(const SegArgs& a, hipStream_t st);
 hipError_t launch_seg_scan(const SegArgs& a, hipStream_t st);
 hipError_t launch_seg_fwd(const SegArgs& a, hipStream_t st);
+hipError_t launch_seg_states(const SegArgs& a, hipStream_t st);
 
 // Compute-unit count of device `dev` (0 if it cannot be queried), looked up
 // once per device under std::call_once, so concurrent callers are safe.

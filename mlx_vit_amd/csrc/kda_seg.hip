@@ -13,7 +13,10 @@
 //                              order, per (b, h) and 16-column block;
 //   kda_segchain_kernel<D, 0>  pass C: every segment's forward from its
 //                              Sigma_in -- O, and the final state from the
-//                              last segment.
+//                              last segment;
+//   kda_segchain_kernel<D, 2>  pass C of the backward's state recompute: the
+//                              chunk-start states h and V' = U - W h of every
+//                              chunk instead of O (after passes A and B).
 // This is the chunk loop of nope_gdn_mlx.py:2408-2451 (V' = U - W Sigma, O =
 // Qp Sigma + Aqk V', Sigma <- diag(e^G) Sigma + Kb^T V') regrouped: the loop is
 // linear in Sigma, so its segments compose.
@@ -138,7 +141,7 @@ __device__ __forceinline__ f32x4 quad_transpose(const f32x4& x) {
 
 template <int D, int PASS, int NW>
 struct SegLayout {
-    static constexpr int NS = PASS == 0 ? 2 : 3;                   // LDS sets
+    static constexpr int NS = PASS == 0 ? 2 : 3;                   // LDS sets (PASS 2: no Qp, Aqk)
     static constexpr int RB_W = 2 * D, RB_C = 2 * C;              // swizzled row bytes
     static constexpr int W_OFF = 0;                               // W   [C][D]
     static constexpr int U_OFF = W_OFF + C * RB_W;                // U   [C][D]
@@ -160,8 +163,11 @@ struct SegLayout {
 }  // namespace
 
 // Pass C (PASS 0): the forward of one segment from its start state.  Pass A
-// (PASS 1): the segment's map (X, M).  One 512-thread workgroup per (b, h,
-// segment); layout, roles and row order in the file comment.
+// (PASS 1): the segment's map (X, M).  PASS 2: the segment's chunk-start
+// states h and V' = U - W h (bf16, natural indices: h[chunk][dk][dv],
+// V'[chunk][t][dv]) from its start state, for the backward.  One 512-thread
+// workgroup per (b, h, segment); layout, roles and row order in the file
+// comment.
 template <int D, int PASS, int NW>
 __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) {
     using ST = uint16_t;
@@ -169,7 +175,7 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
     using TW = typename Lay::TW;
     using TK = typename Lay::TK;
     using TA = typename Lay::TA;
-    constexpr int NS = Lay::NS, NI = D / BS, KS = D / 32, NJ = (PASS == 0) ? D / (16 * NW) : 2 * D / (16 * NW);
+    constexpr int NS = Lay::NS, NI = D / BS, KS = D / 32, NJ = (PASS == 1) ? 2 * D / (16 * NW) : D / (16 * NW);
     constexpr int RB_W = Lay::RB_W, RB_C = Lay::RB_C, LI = Lay::LI;
     static_assert(NJ >= 1 && NS >= 2 && Lay::EG_LANES >= 1, "whole column tiles per wave");
     __shared__ __align__(1024) char smem[Lay::BYTES];
@@ -177,13 +183,13 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
               g4 = l >> 4;
     __builtin_assume(w >= 0 && w < NW);
-    const int nsegw = (PASS == 0) ? a.nseg : a.nseg - 1;   // segments this pass covers
+    const int nsegw = (PASS == 1) ? a.nseg - 1 : a.nseg;   // segments this pass covers
     const int bh = blockIdx.x / nsegw, seg = blockIdx.x - bh * nsegw;
     const int b = bh / a.H, h = bh - b * a.H;
     const int n0 = seg * a.seg_len, L = min(a.nc, n0 + a.seg_len) - n0;
     constexpr int CPW = BS * NJ;                                        // columns per wave
     const bool ident = PASS == 1 && w >= NW / 2;                        // identity columns (M)
-    const int cb = (PASS == 0) ? CPW * w : CPW * (w % (NW / 2));        // first owned column
+    const int cb = (PASS == 1) ? CPW * (w % (NW / 2)) : CPW * w;        // first owned column
     const size_t seg_ix = (size_t)bh * a.nseg + seg;
 
     // ---- the start state of the owned columns (rows in perm_row order) ----
@@ -191,14 +197,14 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
     {
         // this (b, h)'s start state: s0 for the first segment, pass B's result after
         const float* src = nullptr;
-        if constexpr (PASS == 0)
+        if constexpr (PASS != 1)
             src = (seg == 0) ? (a.s0 ? a.s0 + (size_t)bh * D * D : nullptr) : a.segS + seg_ix * D * D;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const int col = cb + BS * j + r16, row0 = perm_row(BS * i + 4 * g4);
-                if constexpr (PASS == 0) {
+                if constexpr (PASS != 1) {
                     S[i][j] = zero4();
                     if (src) {
                         const float4 x = *reinterpret_cast<const float4*>(src + (size_t)col * D + row0);
@@ -253,6 +259,25 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
             }
     };
 
+    // PASS 2: h and V' of the previous chunk, packed the way O is (four
+    // consecutive columns of one row per lane)
+    uint2 Hpk[NI][NJ], Vpk[NB][NJ];
+    auto store_hv = [&](int c) __attribute__((always_inline)) {
+        const size_t ch = (size_t)bh * a.nc + c;
+        ST* hp = static_cast<ST*>(a.h) + ch * D * D;
+        ST* vp = static_cast<ST*>(a.Vp) + ch * C * D;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int col = cb + BS * j + 4 * (r16 >> 2);
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                *reinterpret_cast<uint2*>(hp + (size_t)(perm_row(BS * i + 4 * g4) + (r16 & 3)) * D + col) = Hpk[i][j];
+#pragma unroll
+            for (int m = 0; m < NB; ++m)
+                *reinterpret_cast<uint2*>(vp + (size_t)(perm_row(BS * m + 4 * g4) + (r16 & 3)) * D + col) = Vpk[m][j];
+        }
+    };
+
 #pragma unroll
     for (int c = 0; c < NS - 1; ++c)
         if (c < L) dma_chunk(n0 + c, smem + c * Lay::SET_BYTES);
@@ -263,6 +288,8 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
         lds_barrier();   // every wave's share landed; set (n - 1) % NS is free
         if constexpr (PASS == 0)
             if (n > 0) store_o(n0 + n - 1);
+        if constexpr (PASS == 2)
+            if (n > 0) store_hv(n0 + n - 1);
         if (n + NS - 1 < L) dma_chunk(n0 + n + NS - 1, smem + ((n + NS - 1) % NS) * Lay::SET_BYTES);
         const char* sb = smem + (n % NS) * Lay::SET_BYTES;
         const ST* sW = reinterpret_cast<const ST*>(sb + Lay::W_OFF);
@@ -270,6 +297,15 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
         const ST* sKbT = reinterpret_cast<const ST*>(sb + Lay::KBT_OFF);
         const float* sEg = reinterpret_cast<const float*>(sb + Lay::EG_OFF);
 
+        if constexpr (PASS == 2) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const f32x4 y = quad_transpose(S[i][j]);
+                    Hpk[i][j] = make_uint2(pack2bf(y[0], y[1]), pack2bf(y[2], y[3]));
+                }
+        }
         // B operands of the chunk-start state
         bf16x8 Bs[NJ][KS];
 #pragma unroll
@@ -302,6 +338,15 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int s = 0; s < 2; ++s) Bv[j][s] = bfrag(Vp[2 * s][j], Vp[2 * s + 1][j]);
+        if constexpr (PASS == 2) {
+#pragma unroll
+            for (int m = 0; m < NB; ++m)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const f32x4 y = quad_transpose(Vp[m][j]);
+                    Vpk[m][j] = make_uint2(pack2bf(y[0], y[1]), pack2bf(y[2], y[3]));
+                }
+        }
         if constexpr (PASS == 0) {
             // O = Qp Sigma + Aqk V' (row block m holds tokens 32 (m >> 1) ..
             // + 31, and Aqk is zero above the diagonal: k-steps s <= m >> 1)
@@ -347,7 +392,9 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
         }
     }
 
-    if constexpr (PASS == 0) {
+    if constexpr (PASS == 2) {
+        store_hv(n0 + L - 1);
+    } else if constexpr (PASS == 0) {
         store_o(n0 + L - 1);
         if (seg == a.nseg - 1 && a.s_final) {
 #pragma unroll
@@ -521,6 +568,12 @@ hipError_t launch_seg_map(const SegArgs& a, hipStream_t st) {
 hipError_t launch_seg_scan(const SegArgs& a, hipStream_t st) {
     if (a.nseg < 2) return hipSuccess;
     hipLaunchKernelGGL((kda_segscan_kernel<128>), dim3(a.BH * (128 / BS)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_seg_states(const SegArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((kda_segchain_kernel<128, 2, SEG_NW>), dim3(a.BH * a.nseg), dim3(64 * SEG_NW), 0, st,
+                       a);
     return hipGetLastError();
 }
 

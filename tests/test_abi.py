@@ -108,7 +108,7 @@ def _offsets(lib, pass_, B, T, H, D, dtype):
     return dict(zip(_lib.WS_REGIONS, arr))
 
 
-BACKWARD_REGIONS = ("h", "dh", "Vp", "dVp", "PadB")
+BACKWARD_REGIONS = ("h", "dh", "Vp", "dVp", "SegX", "SegM", "SegS", "PadB")
 
 
 @pytest.mark.parametrize("pass_,dtype", [(0, 0), (0, 1), (1, 0), (1, 1), (2, 0), (2, 1)])
@@ -168,7 +168,8 @@ def test_train_workspace_kept_part_first(B, T, H, D, dtype):
 @pytest.mark.parametrize("B,T,H,D,dtype,nseg", [
     (1, 32768, 16, 128, 1, 16),   # config 3: 16 (b, h) x 16 segments of 32 chunks
     (1, 2000, 2, 128, 1, 8),      # 32 chunks: segments of at least 4 chunks
-    (2, 600, 3, 128, 1, 2),
+    (2, 600, 3, 128, 1, 2),       # the backward's state recompute: one chain per (b, h)
+    (2, 2500, 3, 128, 1, 10),
     (1, 129, 2, 128, 1, 1),       # 3 chunks: one segment, the unsegmented kernel
     (16, 1024, 16, 128, 1, 1),    # 256 (b, h) fill the GPU by themselves
     (1, 32768, 16, 128, 0, 1),    # fp32 inputs: not segmented
@@ -177,19 +178,24 @@ def test_train_workspace_kept_part_first(B, T, H, D, dtype):
 def test_segment_plan_regions(B, T, H, D, dtype, nseg):
     """The bf16 forward at D = 128 is split into segments exactly when the plan
     (about 256 workgroups, >= 4 chunks per segment) gives more than one; the
-    three segment regions are then B*H*nseg*D*D fp32 each."""
+    three segment regions are then B*H*nseg*D*D fp32 each.  The backward's state
+    recompute follows the same plan where it gives at least 8 segments: passes
+    1 and 2 then hold the same three regions (in pass 2 among the backward's
+    own, after the kept part)."""
     lib = _lib.load()
-    arr = (ctypes.c_int64 * len(_lib.WS_REGIONS))()
-    assert lib.kda_workspace_offsets(0, B, T, H, D, 64, dtype, arr) == 0
-    off = dict(zip(_lib.WS_REGIONS, arr))
     seg = ("SegX", "SegM", "SegS")
-    if nseg == 1:
-        assert all(off[r] == -1 for r in seg)
-        return
     per = B * H * nseg * D * D * 4
-    for a, b in zip(seg, seg[1:]):
-        assert off[b] - off[a] == per
-    assert lib.kda_workspace_size(0, B, T, H, D, 64, dtype) - off["SegS"] == per
+    for pass_ in (0, 1, 2):
+        off = _offsets(lib, pass_, B, T, H, D, dtype)
+        if nseg == 1 or (pass_ != 0 and nseg < 8):
+            assert all(off[r] == -1 for r in seg), pass_
+            continue
+        for a, b in zip(seg, seg[1:]):
+            assert off[b] - off[a] == per, pass_
+        if pass_ == 0:
+            assert lib.kda_workspace_size(0, B, T, H, D, 64, dtype) - off["SegS"] == per
+        if pass_ == 2:
+            assert off["SegX"] >= lib.kda_train_kept_size(B, T, H, D, 64, dtype)
 
 
 @pytest.mark.parametrize("B,T,H,D,chunk,dtype,gdt,code", [

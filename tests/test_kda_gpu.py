@@ -367,6 +367,25 @@ def test_bwd_parity_bf16_d128(B, T, H, D, with_state, with_dsf, g_scale):
 
 
 @pytest.mark.parametrize("B,T,H,D,with_state,with_dsf,g_scale", [
+    (1, 2000, 2, 128, True, True, 0.1),    # 8 segments of 4 chunks, ragged last chunk
+    (2, 2500, 3, 128, True, False, 0.1),   # 10 segments for each of six (b, h)
+    (1, 2340, 2, 128, False, True, 1.0),   # 8 segments, the last of 2 chunks; strong decay
+    (1, 2560, 2, 96, True, True, 0.1),     # D = 96: 10 segments of the padded state
+])
+def test_bwd_parity_bf16_segmented_states(B, T, H, D, with_state, with_dsf, g_scale):
+    """The bf16 backward at D = 128 (and 96) with its state recompute split
+    over segments of the sequence (few long sequences: at least 8 segments):
+    the segment maps and start states of the segmented forward, then each
+    segment's chunk-start states h and V'."""
+    kda = _kda()
+    assert kda.workspace_offsets(1, B, T, H, D, torch.bfloat16)["SegX"] >= 0, "segmented recompute not taken"
+    x = _inputs(B, T, H, D, torch.bfloat16, seed=29, with_state=with_state, grad=True, g_scale=g_scale)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9)) if with_dsf else None
+    _assert_all(_bwd_errors(x, torch.bfloat16, dsf), TOL[torch.bfloat16],
+                f"bwd bf16 segmented states {B},{T},{H},{D},{with_state},{with_dsf},{g_scale}")
+
+
+@pytest.mark.parametrize("B,T,H,D,with_state,with_dsf,g_scale", [
     (1, 200, 2, 128, True, True, 0.1),     # ragged last chunk, state + final-state cotangent
     (2, 64, 3, 128, False, False, 0.1),    # one full chunk
     (1, 130, 2, 128, True, False, 6.0),    # strong decay: every pair pair by pair
@@ -522,6 +541,8 @@ def test_training_pair_equals_standalone_calls(B, T, H, D, dtype, g_scale):
     (1, 150, 2, 128, torch.bfloat16),
     (1, 100, 2, 128, torch.float32),
     (1, 150, 2, 96, torch.bfloat16),          # PAD kept, PADB the backward's
+    (1, 2560, 2, 128, torch.bfloat16),        # segmented state recompute: the segment regions
+    (1, 2560, 2, 96, torch.bfloat16),         # are the backward's
 ])
 def test_training_pair_kept_part_and_split_scratch(B, T, H, D, dtype):
     """kda_fwd_train writes nothing past the kept part of the pair's workspace
