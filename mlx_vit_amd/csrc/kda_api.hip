@@ -78,8 +78,9 @@ bool seg_forward(int pass, int B, int T, int H, int D, int dtype, int* nseg, int
     return *nseg > 1;
 }
 
-// Whether the backward's state recompute runs segmented (the same plan and
-// passes A and B, then the chunk-start states per segment): bf16 at the
+// Whether the backward's state recompute and reverse carry run segmented (the
+// same plan; passes A and B, then the chunk-start states per segment; the
+// segments' reverse maps, a reverse scan and the segments' dh): bf16 at the
 // kernels' D = 128 when the plan has at least SEG_STATES_MIN segments.  The
 // segment passes read the chunk slabs twice (maps, then states), about 1.4x
 // the bytes of one chain per (b, h), and take about 3.4 times as long per
@@ -700,6 +701,7 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
         sa.segM = static_cast<uint16_t*>(region(ws, KDA_WS_SEGM));
         sa.segS = fregion(ws, KDA_WS_SEGS);
         sa.T = T; sa.H = H; sa.nc = nc; sa.BH = BH; sa.nseg = nseg; sa.seg_len = seg_len;
+        sa.all_maps = 1;   // the reverse carry's scan below uses the last segment's map too
         e = timed(PROF_RECUR_H, st, [&] {
             hipError_t r = kda::launch_seg_map(sa, st);
             if (r == hipSuccess) r = kda::launch_seg_scan(sa, st);
@@ -726,7 +728,30 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
     da.WT = region(ws, KDA_WS_WT);
     da.eG = eG; da.dout = dout_rec; da.dsf = ds_final; da.ds0 = ds0; da.dh = dhS; da.dVp = dVp;
     da.T = T; da.H = H; da.nc = nc; da.BH = BH;
-    e = timed(PROF_DH, st, [&] { return kda::launch_dh(da, D, in_bf16, st); });
+    if (nseg > 1) {
+        // the reverse carry over the recompute's segments: each segment's reverse
+        // map (into segX, free after the recompute), the reverse scan from
+        // ds_final through the forward maps' transposes (into segS), then every
+        // segment's dh, dV' and dS0
+        da.segX = fregion(ws, KDA_WS_SEGX);
+        da.segS = fregion(ws, KDA_WS_SEGS);
+        da.nseg = nseg;
+        da.seg_len = seg_len;
+        kda::SegArgs sr = {};
+        sr.dsf = ds_final;
+        sr.segX = da.segX;
+        sr.segS = da.segS;
+        sr.segM = static_cast<uint16_t*>(region(ws, KDA_WS_SEGM));
+        sr.T = T; sr.H = H; sr.nc = nc; sr.BH = BH; sr.nseg = nseg; sr.seg_len = seg_len;
+        e = timed(PROF_DH, st, [&] {
+            hipError_t r = kda::launch_dh_seg_maps(da, st);
+            if (r == hipSuccess) r = kda::launch_seg_rscan(sr, st);
+            if (r == hipSuccess) r = kda::launch_dh_seg(da, st);
+            return r;
+        });
+    } else {
+        e = timed(PROF_DH, st, [&] { return kda::launch_dh(da, D, in_bf16, st); });
+    }
     if (e != hipSuccess) return hip_fail(e, "kda_dh_kernel");
 
     kda::LocalArgs la = {};

@@ -63,6 +63,10 @@ struct DhArgs {
     float* ds0;
     void *dh, *dVp;
     int T, H, nc, BH;
+    // launch_dh_seg_maps / launch_dh_seg (bf16 D = 128): the segment plan, the
+    // segments' reverse maps X_rev and incoming dSigma ([BH][nseg][D][D] fp32)
+    float *segX, *segS;
+    int nseg, seg_len;
 };
 
 struct LocalArgs {
@@ -93,6 +97,8 @@ struct SegArgs {
     float* s_final;
     void* o;
     void *h, *Vp;   // launch_seg_states: chunk-start states [BH nc][D][D], V' [BH nc][C][D] (bf16)
+    const float* dsf;   // launch_seg_rscan: ds_final (null: zero)
+    int all_maps;       // launch_seg_map: the last segment's map too (the reverse scan's)
     float *segX, *segS;
     uint16_t* segM;
     int T, H, nc, BH, nseg, seg_len;
@@ -103,6 +109,11 @@ hipError_t launch_seg_map(const SegArgs& a, hipStream_t st);
 hipError_t launch_seg_scan(const SegArgs& a, hipStream_t st);
 hipError_t launch_seg_fwd(const SegArgs& a, hipStream_t st);
 hipError_t launch_seg_states(const SegArgs& a, hipStream_t st);
+// The reverse scan of the backward's reverse carry over segments: from
+// ds_final, dSigma entering segment s from its end, for s = nseg - 2 .. 0, as
+// M_{s+1}^T dSigma_{s+1} + X_rev_{s+1} (segM from launch_seg_map with
+// all_maps, segX the reverse maps), written to segS[s].
+hipError_t launch_seg_rscan(const SegArgs& a, hipStream_t st);
 
 // Compute-unit count of device `dev` (0 if it cannot be queried), looked up
 // once per device under std::call_once, so concurrent callers are safe.
@@ -116,6 +127,8 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
 // whether launch_recur can fuse the gated RMSNorm for this head size and dtype
 bool recur_epilogue_supported(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
+hipError_t launch_dh_seg_maps(const DhArgs& a, hipStream_t st);
+hipError_t launch_dh_seg(const DhArgs& a, hipStream_t st);
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_kind, int nchunks, hipStream_t st);
 // the local adjoints at D = 128 (kda_bwdw.hip): reads A_kk, the diagonal-block
 // inverses and V' from the workspace

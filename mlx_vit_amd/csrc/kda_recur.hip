@@ -354,7 +354,14 @@ __global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
 // fragment is then used by one column tile of a wave, so fragments are read
 // from LDS where they are used instead of being held for the whole chunk (at
 // D = 128 in fp32 the whole set would take about 430 VGPRs).
-template <int D, typename ST, int PREC, int CS = 1>
+// SEGM: the chunks of one segment of a.seg_len chunks per workgroup (the loop
+// is linear in dSigma, so segments compose; the segment's map on dSigma is the
+// transpose of the forward segment map M).  SEGM 1: segments 1 .. nseg - 1
+// from dSigma = 0, writing only the segment's end value X_rev (to a.segX, the
+// reference orientation [dv][dk]); SEGM 2: every segment from its incoming
+// dSigma (ds_final for the last segment, a.segS, the reverse scan's result,
+// for the others), writing dh and dV' and, for segment 0, dS0.
+template <int D, typename ST, int PREC, int CS = 1, int SEGM = 0>
 __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
     using Lay = DhLayout<D, ST, CS>;
     constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, TPW = (NTW + 3) / 4;
@@ -364,7 +371,17 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
     __shared__ __align__(16) unsigned char smem[Lay::BYTES];
 
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
-    const int bh = blockIdx.x / CS, c0 = (blockIdx.x - bh * CS) * DC, b = bh / a.H, h = bh - b * a.H;
+    // the workgroup's segment: chunks n0 .. n0 + L - 1 (the whole sequence without SEGM)
+    int wg = blockIdx.x, sgi = 0, n0 = 0, L = a.nc;
+    if constexpr (SEGM != 0) {
+        const int nsegw = (SEGM == 1) ? a.nseg - 1 : a.nseg;
+        const int si = wg % nsegw;
+        wg /= nsegw;
+        sgi = (SEGM == 1) ? si + 1 : si;
+        n0 = sgi * a.seg_len;
+        L = min(a.nc, n0 + a.seg_len) - n0;
+    }
+    const int bh = wg / CS, c0 = (wg - bh * CS) * DC, b = bh / a.H, h = bh - b * a.H;
     const ST* gAqkT = static_cast<const ST*>(a.AqkT);
     const ST* gKb = static_cast<const ST*>(a.Kb);
     const ST* gQpT = static_cast<const ST*>(a.QpT);
@@ -384,15 +401,20 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
         col[j] = (w + 4 * j) * BS + r16;
     }
 
+    // the incoming dSigma ([dv][dk] like ds_final): ds_final, or for SEGM 2 the
+    // reverse scan's value at a segment's end; zero for SEGM 1
+    const float* dsin = a.dsf ? a.dsf + (size_t)bh * D * D : nullptr;
+    if constexpr (SEGM == 1) dsin = nullptr;
+    if constexpr (SEGM == 2)
+        if (sgi < a.nseg - 1) dsin = a.segS + ((size_t)bh * a.nseg + sgi) * D * D;
     f32x4 dS[TPW][NT];
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) {
             dS[j][mt] = zero4();
-            if (has[j] && a.dsf) {
-                const float4 x =
-                    *reinterpret_cast<const float4*>(a.dsf + ((size_t)bh * D + c0 + col[j]) * D + BS * mt + 4 * g4);
+            if (has[j] && dsin) {
+                const float4 x = *reinterpret_cast<const float4*>(dsin + (size_t)(c0 + col[j]) * D + BS * mt + 4 * g4);
                 dS[j][mt] = f32x4{x.x, x.y, x.z, x.w};
             }
         }
@@ -422,20 +444,21 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
         pEg.store(seg(buf), D);
     };
     auto flush = [&](int it, int n) __attribute__((always_inline)) {   // stores of chunk n (loop step it)
+        if constexpr (SEGM == 1) return;   // the segment map writes only its end value
         const ST* sst = stg((Lay::NBUF == 2) ? (it & 1) : 0);
         const size_t ch = (size_t)bh * a.nc + n;
         tile_out<ST, D, DC>(sst, LDU, static_cast<ST*>(a.dh) + ch * D * D + c0, D, D);
         tile_out<ST, C, DC>(sst + D * LDU, LDU, static_cast<ST*>(a.dVp) + ch * C * D + c0, D, C);
     };
 
-    issue(a.nc - 1);
+    issue(n0 + L - 1);
     commit(0);
     __syncthreads();
 
-    for (int it = 0; it < a.nc; ++it) {
-        const int n = a.nc - 1 - it;
+    for (int it = 0; it < L; ++it) {
+        const int n = n0 + L - 1 - it;
         const int buf = (Lay::NBUF == 2) ? (it & 1) : 0;
-        if (n > 0) issue(n - 1);
+        if (n > n0) issue(n - 1);
         if (Lay::NBUF == 2 && it > 0) flush(it - 1, n + 1);
 
         const ST* sAqkT = set(buf) + Lay::AQKT_OFF;
@@ -544,18 +567,29 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
 
         order_after_compute();
         if constexpr (Lay::NBUF == 2) {
-            if (n > 0) commit(buf ^ 1);
+            if (n > n0) commit(buf ^ 1);
             __syncthreads();
         } else {
             __syncthreads();
             flush(it, n);
-            if (n > 0) commit(0);
+            if (n > n0) commit(0);
             __syncthreads();
         }
     }
-    if (Lay::NBUF == 2) flush(a.nc - 1, 0);
+    if (Lay::NBUF == 2) flush(L - 1, n0);
 
-    if (a.ds0) {
+    if constexpr (SEGM == 1) {
+        float* xo = a.segX + ((size_t)bh * a.nseg + sgi) * D * D;
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+            if (has[j])
+#pragma unroll
+                for (int mt = 0; mt < NT; ++mt)
+                    *reinterpret_cast<float4*>(xo + (size_t)(c0 + col[j]) * D + BS * mt + 4 * g4) =
+                        make_float4(dS[j][mt][0], dS[j][mt][1], dS[j][mt][2], dS[j][mt][3]);
+        return;
+    }
+    if (a.ds0 && sgi == 0) {
 #pragma unroll
         for (int j = 0; j < TPW; ++j)
             if (has[j])
@@ -2350,6 +2384,21 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
 }
 
 bool recur_epilogue_supported(int D, int in_bf16) { return in_bf16 ? D == 64 : (D == 32 || D == 64); }
+
+// The reverse carry over segments (bf16, D = 128): the segments' reverse maps
+// X_rev (a.segX), the reverse scan (a.segS, launched by the caller between the
+// two), then every segment's dh, dV' and dS0.
+hipError_t launch_dh_seg_maps(const DhArgs& a, hipStream_t st) {
+    if (a.nseg < 2) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1, 2, 1>), dim3(a.BH * 2 * (a.nseg - 1)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_dh_seg(const DhArgs& a, hipStream_t st) {
+    if (a.nseg < 2) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1, 2, 2>), dim3(a.BH * 2 * a.nseg), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st) {
     if (D == 32) return in_bf16 ? launch_dh_t<32, uint16_t>(a, st) : launch_dh_t<32, float>(a, st);

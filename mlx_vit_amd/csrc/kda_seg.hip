@@ -183,7 +183,8 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15,
               g4 = l >> 4;
     __builtin_assume(w >= 0 && w < NW);
-    const int nsegw = (PASS == 1) ? a.nseg - 1 : a.nseg;   // segments this pass covers
+    // segments this pass covers (pass A: the last one only for the reverse scan)
+    const int nsegw = (PASS == 1 && !a.all_maps) ? a.nseg - 1 : a.nseg;
     const int bh = blockIdx.x / nsegw, seg = blockIdx.x - bh * nsegw;
     const int b = bh / a.H, h = bh - b * a.H;
     const int n0 = seg * a.seg_len, L = min(a.nc, n0 + a.seg_len) - n0;
@@ -432,8 +433,8 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
     }
 }
 
-// Pass B: Sigma_in of segments 1 .. nseg - 1 of one (b, h), 16 dv columns per
-// workgroup, Sigma_in[s + 1] = M_s Sigma_in[s] + X_s with fp32-accurate
+// Pass B (REV = false): Sigma_in of segments 1 .. nseg - 1 of one (b, h), 16 dv
+// columns per workgroup, Sigma_in[s + 1] = M_s Sigma_in[s] + X_s with fp32-accurate
 // split-bf16 products (Sigma and M as bf16 hi + lo).  Wave w owns the row
 // tiles 2 w and 2 w + 1 (dk_out rows 32 w .. 32 w + 31) of the columns: four
 // waves share a step's products instead of each forming all 128 rows of its
@@ -446,7 +447,11 @@ __global__ __launch_bounds__(64 * NW) void kda_segchain_kernel(const SegArgs a) 
 // store just issued.  Natural row order; written in the reference orientation
 // [dv][dk], as s0 is.  Same products in the same order as one wave forming
 // all rows: the results do not depend on the split.
-template <int D>
+// REV = true: the backward's reverse scan, from ds_final through segments
+// nseg - 1 .. 1: dSigma_{s-1} = M_s^T dSigma_s + X_rev_s, written to segS[s - 1]
+// (the segment's reverse map on dSigma is the transpose of its forward map, so
+// the A operand reads the stored M^T planes by rows instead of transposed).
+template <int D, bool REV = false>
 __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
     using ST = uint16_t;
     constexpr int NI = D / BS, KS = D / 32, RB = 2 * D, PLANE = D * RB;
@@ -469,6 +474,9 @@ __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
         TM::issue_s(src, oM, buf, w);
         TM::issue_s(src + PLANE, oM, buf + PLANE, w);
     };
+    // the segment whose map step q applies, and where its result goes
+    auto seg_of = [&](int q) __attribute__((always_inline)) { return REV ? a.nseg - 1 - q : q; };
+    auto out_of = [&](int q) __attribute__((always_inline)) { return REV ? a.nseg - 2 - q : q + 1; };
     // rows BS i + 4 g4 .. + 3, i = 2 w + u, of the lane's column
     auto load_x = [&](int s, f32x4 (&X)[2]) __attribute__((always_inline)) {
         const float* xp = a.segX + ((size_t)bh * a.nseg + s) * D * D + (size_t)col * D;
@@ -491,27 +499,28 @@ __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
         xch[buf][w][1][l] = __builtin_bit_cast(uint4, f.l);
     };
     f32x4 S[2], Xn[2];
+    const float* sin = REV ? a.dsf : a.s0;   // [BH][dv][dk]
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         S[u] = zero4();
-        if (a.s0) {
+        if (sin) {
             const float4 x =
-                *reinterpret_cast<const float4*>(a.s0 + ((size_t)bh * D + col) * D + BS * (2 * w + u) + 4 * g4);
+                *reinterpret_cast<const float4*>(sin + ((size_t)bh * D + col) * D + BS * (2 * w + u) + 4 * g4);
             S[u] = f32x4{x.x, x.y, x.z, x.w};
         }
     }
     put_b(0, S);
-    dma_m(0, smem);
-    load_x(0, Xn);
+    dma_m(seg_of(0), smem);
+    load_x(seg_of(0), Xn);
     for (int s = 0; s < nsteps; ++s) {
         dma_wait<0>();
-        lds_barrier();   // M_s landed for every wave, the exchange buffer s & 1 written; the other M buffer is free
-        if (s > 0) store_s(s, S);   // Sigma_in of segment s, formed in the previous step
-        if (s + 1 < nsteps) dma_m(s + 1, smem + ((s + 1) & 1) * 2 * PLANE);
+        lds_barrier();   // M of step s landed for every wave, the exchange buffer s & 1 written; the other M buffer is free
+        if (s > 0) store_s(out_of(s - 1), S);   // the previous step's result
+        if (s + 1 < nsteps) dma_m(seg_of(s + 1), smem + ((s + 1) & 1) * 2 * PLANE);
         f32x4 Xc[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) Xc[u] = Xn[u];
-        if (s + 1 < nsteps) load_x(s + 1, Xn);
+        if (s + 1 < nsteps) load_x(seg_of(s + 1), Xn);
         const ST* Mh = reinterpret_cast<const ST*>(smem + (s & 1) * 2 * PLANE);
         const ST* Ml = reinterpret_cast<const ST*>(smem + (s & 1) * 2 * PLANE + PLANE);
         Frag8 B[KS];
@@ -527,8 +536,13 @@ __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
 #pragma unroll
             for (int k = 0; k < KS; ++k) {
                 Frag8 A;
-                A.h = ldfragT_sw<RB>(Mh, BS * i, 32 * k).h;   // A[dk_out][dk_in] = M^T[dk_in][dk_out]
-                A.l = ldfragT_sw<RB>(Ml, BS * i, 32 * k).h;
+                if constexpr (REV) {
+                    A.h = ldfrag_sw<RB>(Mh, BS * i, 32 * k).h;    // A[i][k] = M^T[i][k]
+                    A.l = ldfrag_sw<RB>(Ml, BS * i, 32 * k).h;
+                } else {
+                    A.h = ldfragT_sw<RB>(Mh, BS * i, 32 * k).h;   // A[dk_out][dk_in] = M^T[dk_in][dk_out]
+                    A.l = ldfragT_sw<RB>(Ml, BS * i, 32 * k).h;
+                }
                 acc = mma<3>(A, B[k], acc);
             }
             S[u] = acc;
@@ -536,7 +550,7 @@ __global__ __launch_bounds__(256) void kda_segscan_kernel(const SegArgs a) {
         // buffer (s + 1) & 1 was last read in step s - 1, before this step's barrier
         put_b((s + 1) & 1, S);
     }
-    if (nsteps > 0) store_s(nsteps, S);
+    if (nsteps > 0) store_s(out_of(nsteps - 1), S);
 }
 
 // waves per workgroup of the segment maps and the segment forwards (eight: two
@@ -560,14 +574,20 @@ void seg_plan(int BH, int nc, int* nseg, int* seg_len) {
 
 hipError_t launch_seg_map(const SegArgs& a, hipStream_t st) {
     if (a.nseg < 2) return hipSuccess;
-    hipLaunchKernelGGL((kda_segchain_kernel<128, 1, SEG_NW>), dim3(a.BH * (a.nseg - 1)), dim3(64 * SEG_NW), 0,
-                       st, a);
+    hipLaunchKernelGGL((kda_segchain_kernel<128, 1, SEG_NW>), dim3(a.BH * (a.all_maps ? a.nseg : a.nseg - 1)),
+                       dim3(64 * SEG_NW), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_seg_scan(const SegArgs& a, hipStream_t st) {
     if (a.nseg < 2) return hipSuccess;
     hipLaunchKernelGGL((kda_segscan_kernel<128>), dim3(a.BH * (128 / BS)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_seg_rscan(const SegArgs& a, hipStream_t st) {
+    if (a.nseg < 2) return hipSuccess;
+    hipLaunchKernelGGL((kda_segscan_kernel<128, true>), dim3(a.BH * (128 / BS)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

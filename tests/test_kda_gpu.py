@@ -373,10 +373,12 @@ def test_bwd_parity_bf16_d128(B, T, H, D, with_state, with_dsf, g_scale):
     (1, 2560, 2, 96, True, True, 0.1),     # D = 96: 10 segments of the padded state
 ])
 def test_bwd_parity_bf16_segmented_states(B, T, H, D, with_state, with_dsf, g_scale):
-    """The bf16 backward at D = 128 (and 96) with its state recompute split
-    over segments of the sequence (few long sequences: at least 8 segments):
-    the segment maps and start states of the segmented forward, then each
-    segment's chunk-start states h and V'."""
+    """The bf16 backward at D = 128 (and 96) with its recurrences split over
+    segments of the sequence (few long sequences: at least 8 segments): the
+    state recompute (segment maps, start states, then each segment's
+    chunk-start states h and V') and the reverse carry (each segment's reverse
+    map, a reverse scan through the maps' transposes from ds_final, then each
+    segment's dh, dV' and dS0)."""
     kda = _kda()
     assert kda.workspace_offsets(1, B, T, H, D, torch.bfloat16)["SegX"] >= 0, "segmented recompute not taken"
     x = _inputs(B, T, H, D, torch.bfloat16, seed=29, with_state=with_state, grad=True, g_scale=g_scale)
