@@ -68,14 +68,22 @@ int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, b
     return KDA_OK;
 }
 
-// Whether the forward runs segmented (kda_seg.hip): bf16 at D = 128 whenever
-// the plan has more than one segment.  *nseg / *seg_len: the plan.
+// Whether the forward runs segmented (kda_seg.hip): bf16 at D = 128 when the
+// plan has at least 8 segments or segments of at least 32 chunks.  A chunk of
+// a segment costs the two segment passes about 3.5 times a chunk of the
+// one-chain-per-(b, h) forward, so short segments lose: at B8 H8 T1568 (4
+// segments of 7 chunks) the forward took 181 us segmented against 153 us
+// unsegmented; with 4 segments of 16 chunks or 2 of 13 the two were level.
+// *nseg / *seg_len: the plan.
 bool seg_forward(int pass, int B, int T, int H, int D, int dtype, int* nseg, int* seg_len) {
     *nseg = 1;
     *seg_len = 0;
     if (pass != KDA_PASS_FWD || dtype != KDA_DTYPE_BF16 || D != 128 || (size_t)B * T * H == 0) return false;
     kda::seg_plan(B * H, (T + kda::C - 1) / kda::C, nseg, seg_len);
-    return *nseg > 1;
+    if (*nseg > 1 && (*nseg >= 8 || *seg_len >= 32)) return true;
+    *nseg = 1;
+    *seg_len = 0;
+    return false;
 }
 
 // Whether the backward's state recompute and reverse carry run segmented (the

@@ -168,17 +168,19 @@ def test_train_workspace_kept_part_first(B, T, H, D, dtype):
 @pytest.mark.parametrize("B,T,H,D,dtype,nseg", [
     (1, 32768, 16, 128, 1, 16),   # config 3: 16 (b, h) x 16 segments of 32 chunks
     (1, 2000, 2, 128, 1, 8),      # 32 chunks: segments of at least 4 chunks
-    (2, 600, 3, 128, 1, 2),       # the backward's state recompute: one chain per (b, h)
+    (2, 600, 3, 128, 1, 1),       # 2 segments of 5 chunks: one chain per (b, h)
     (2, 2500, 3, 128, 1, 10),
+    (5, 12288, 8, 128, 1, 6),     # 6 segments of 32 chunks: the forward only
     (1, 129, 2, 128, 1, 1),       # 3 chunks: one segment, the unsegmented kernel
     (16, 1024, 16, 128, 1, 1),    # 256 (b, h) fill the GPU by themselves
     (1, 32768, 16, 128, 0, 1),    # fp32 inputs: not segmented
     (1, 32768, 16, 64, 1, 1),     # D = 64: not segmented
 ])
 def test_segment_plan_regions(B, T, H, D, dtype, nseg):
-    """The bf16 forward at D = 128 is split into segments exactly when the plan
-    (about 256 workgroups, >= 4 chunks per segment) gives more than one; the
-    three segment regions are then B*H*nseg*D*D fp32 each.  The backward's state
+    """The bf16 forward at D = 128 is split into segments when the plan (about
+    256 workgroups, >= 4 chunks per segment) gives at least 8 segments or
+    segments of at least 32 chunks; the three segment regions are then
+    B*H*nseg*D*D fp32 each.  The backward's state
     recompute follows the same plan where it gives at least 8 segments: passes
     1 and 2 then hold the same three regions (in pass 2 among the backward's
     own, after the kept part)."""
@@ -187,7 +189,7 @@ def test_segment_plan_regions(B, T, H, D, dtype, nseg):
     per = B * H * nseg * D * D * 4
     for pass_ in (0, 1, 2):
         off = _offsets(lib, pass_, B, T, H, D, dtype)
-        if nseg == 1 or (pass_ != 0 and nseg < 8):
+        if nseg == 1 or (pass_ != 0 and nseg < 8):   # the backward: from 8 segments
             assert all(off[r] == -1 for r in seg), pass_
             continue
         for a, b in zip(seg, seg[1:]):

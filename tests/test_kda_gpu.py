@@ -159,8 +159,9 @@ def test_fwd_parity_bf16(B, T, H, D, with_state):
 
 @pytest.mark.parametrize("B,T,H,D,with_state", [
     (1, 2000, 2, 128, True),     # 8 segments of 4 chunks, ragged last chunk
-    (1, 1700, 2, 128, False),    # 6 segments, the last of 2 chunks
-    (2, 600, 3, 128, True),      # 2 segments for each of six (b, h)
+    (1, 2340, 2, 128, False),    # 8 segments, the last of 2 chunks
+    (2, 2500, 3, 128, True),     # 10 segments for each of six (b, h)
+    (5, 12288, 8, 128, True),    # 40 (b, h): 6 segments of 32 chunks
 ])
 def test_fwd_parity_bf16_segmented(B, T, H, D, with_state):
     """The bf16 forward at D = 128 split over segments of the sequence: segment
