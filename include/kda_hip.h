@@ -55,9 +55,9 @@ extern "C" {
 /* Workspace regions (see kda_workspace_offsets).  SEGX, SEGM and SEGS exist
  * only at bf16 D = 128 when the sequence is split into segments: per (b, h,
  * segment) the segment's state map and start state, for the forward (pass 0,
- * more than one segment) and for the backward's state recompute and reverse
- * carry (passes 1 and 2, at least 8 segments; in pass 2 among the backward's
- * own regions).
+ * at least 8 segments or segments of 32 or more chunks) and for the
+ * backward's state recompute and reverse carry (passes 1 and 2, at least 8
+ * segments; in pass 2 among the backward's own regions).
  * PAD and PADB exist only at D = 96, which runs the D = 128 kernels with
  * channels 96..127 zero: the other regions are then those of D = 128; PAD
  * holds the padded s0 (and, for the forward passes, o and s_final), PADB the
