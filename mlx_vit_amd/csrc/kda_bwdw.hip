@@ -120,6 +120,7 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     __shared__ float sda[C][C + 4];         // dAqk (lower, with the diagonal)
     __shared__ __align__(16) float tii[NB][BS][BS + 4];
     __shared__ float sdb[NB + NT][C];       // dbeta partials: [j] from dL tiles of column block j, [NB + nt] channel tile nt
+    __shared__ __align__(16) char pfbuf[256];   // landing bytes of the L2 prefetch
     // Staging area.  bf16 (STG): the chunk's raw k and q rows (phase 0 to the
     // per-lane values), then dO, V', dV' and v (phase 1 and the dA tiles), then one
     // half of dR (fp32) beside W or U (phases 2-3), each brought in with
@@ -462,6 +463,31 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
     if constexpr (STG) tw.store(swu, LDQ);
     __syncthreads();
 
+    // L2 prefetch of the chunk this XCD starts next (chunk ids a CU count apart
+    // go to one XCD and start about when this one ends): its phase-0 inputs --
+    // the rows of q, k and g (two 128-byte lines a row) and A_kk and the
+    // inverses -- one 4-byte DMA per line, the landing bytes scratch.  Issued
+    // after this chunk's last global load, so that no wait of this chunk covers
+    // it, and waited for at the end.  Waves 0-1 take q, 2-3 k, 4-5 g, 6-7 A_kk,
+    // and 32 lanes of wave 0 the inverses (the pointer is picked per wave).
+    if (a.pf_ahead > 0 && ch + a.pf_ahead < (int)gridDim.x) {
+        const int pc = ch + a.pf_ahead, pbh = pc / a.nc, pn = pc - pbh * a.nc;
+        const int pb = pbh / a.H, ph = pbh - pb * a.H, pvalid = min(C, a.T - pn * C);
+        const size_t pbase = ((size_t)pb * a.T + (size_t)pn * C) * rs + (size_t)ph * dio;
+        const uint32_t m = lds_addr(pfbuf);
+        const int grp = w >> 1, li = tid & 127, r = li >> 1;
+        const char* p = nullptr;
+        if (grp == 3) {
+            p = reinterpret_cast<const char*>(a.Akk + (size_t)pc * C * C) + 128 * li;
+        } else if (r < pvalid) {
+            const char* tp = static_cast<const char*>(grp == 0 ? a.q : grp == 1 ? a.k : a.g);
+            const size_t es = (grp == 2) ? sizeof(TG) : sizeof(TI);
+            p = tp + (pbase + (size_t)r * rs) * es + 128 * (li & 1);
+        }
+        if (p) dma4(p, m);
+        if (w == 0 && l < 32) dma4(reinterpret_cast<const char*>(a.Tii + (size_t)pc * NB * BS * BS) + 128 * l, m);
+    }
+
     // ---------------- phase 3: dL = -tril(dR [W | U]^T, -1), one half of dR at a time ----------------
     // bf16: W and U are exact in bf16, so splitting only dR (PREC 2) keeps the
     // product fp32-accurate; fp32: both split (PREC 3)
@@ -726,12 +752,17 @@ __global__ __launch_bounds__(4 * D) void kda_bwd_localw_kernel(const LocalArgs a
         for (int j = 0; j < NB + NT; ++j) db += sdb[j][tid];
         st1<TI>(static_cast<TI*>(a.dbeta) + bbase + (size_t)tid * a.H, db);
     }
+    dma_wait<0>();   // the prefetch has landed before the workgroup's LDS is released
 }
 
 // bf16 operands: bf16 MFMA products (PREC 1); fp32: split-bf16 products
 // accurate to fp32 (PREC 3)
-hipError_t launch_local_wide(const LocalArgs& a, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st) {
+hipError_t launch_local_wide(const LocalArgs& args, int D, int in_bf16, int g_bf16, int nchunks, hipStream_t st) {
     if (D != 128) return hipErrorInvalidValue;
+    // prefetch distance: one chunk per CU (one workgroup fills a CU)
+    int dev = 0;
+    LocalArgs a = args;
+    a.pf_ahead = (hipGetDevice(&dev) == hipSuccess) ? device_cu_count(dev) : 0;
     if (in_bf16) {
         if (g_bf16)
             hipLaunchKernelGGL((kda_bwd_localw_kernel<128, uint16_t, uint16_t, 1>), dim3(nchunks), dim3(512), 0, st, a);
