@@ -93,7 +93,10 @@ int kda_workspace_offsets(int pass, int B, int T, int H, int D, int chunk, int d
 /* Bytes at the start of the training pair's (pass 2) workspace that
  * kda_fwd_train writes and kda_bwd_train reads -- the per-chunk factors (and,
  * at D = 96, the padded s0) -- all a caller must keep between the two
- * calls; 0 on invalid arguments.  The rest of kda_workspace_size(2, ...) is
+ * calls; 0 on invalid arguments.  Where the training forward runs over
+ * segments (bf16, D = 128 or 96; the plan of kda_fwd) the kept part ends with
+ * that forward's segment temporaries, which kda_workspace_offsets does not
+ * name and the backward does not read.  The rest of kda_workspace_size(2, ...) is
  * the backward's own scratch (the chunk-boundary states and their adjoints,
  * V' and dV'), which kda_bwd_train_split takes as a separate buffer.  No
  * counterpart in the reference, whose forward keeps U_traj and S_traj

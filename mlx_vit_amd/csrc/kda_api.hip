@@ -38,6 +38,11 @@ struct Layout {
     // backward reads (placed first); the backward's own regions follow.
     // Passes 0 and 1: total.
     size_t kept;
+    // pass 2, a forward over segments: its segment temporaries (X, M, S, segf_per
+    // bytes each from segf), unnamed bytes at the end of the kept part that only
+    // the training forward writes; -1: none
+    int64_t segf = -1;
+    size_t segf_per = 0;
 };
 
 // regions only the backward writes and reads (the training pair's scratch)
@@ -74,11 +79,11 @@ int check_shape(int B, int T, int H, int D, int chunk, int dtype, int g_dtype, b
 // one-chain-per-(b, h) forward, so short segments lose: at B8 H8 T1568 (4
 // segments of 7 chunks) the forward took 181 us segmented against 153 us
 // unsegmented; with 4 segments of 16 chunks or 2 of 13 the two were level.
-// *nseg / *seg_len: the plan.
+// Passes 0 and 2 (the training forward).  *nseg / *seg_len: the plan.
 bool seg_forward(int pass, int B, int T, int H, int D, int dtype, int* nseg, int* seg_len) {
     *nseg = 1;
     *seg_len = 0;
-    if (pass != KDA_PASS_FWD || dtype != KDA_DTYPE_BF16 || D != 128 || (size_t)B * T * H == 0) return false;
+    if (pass == KDA_PASS_BWD || dtype != KDA_DTYPE_BF16 || D != 128 || (size_t)B * T * H == 0) return false;
     kda::seg_plan(B * H, (T + kda::C - 1) / kda::C, nseg, seg_len);
     if (*nseg > 1 && (*nseg >= 8 || *seg_len >= 32)) return true;
     *nseg = 1;
@@ -186,8 +191,10 @@ void region_sizes(int pass, int B, int T, int H, int D, int dtype, size_t* sz) {
             sz[KDA_WS_VP] = CD;
         }
     }
+    // the named segment regions: the forward's (pass 0) and the backward's;
+    // the training forward's temporaries are unnamed (make_layout)
     int nseg, seg_len;
-    if (seg_forward(pass, B, T, H, D, dtype, &nseg, &seg_len) ||
+    if ((pass == KDA_PASS_FWD && seg_forward(pass, B, T, H, D, dtype, &nseg, &seg_len)) ||
         seg_states(pass, B, T, H, D, dtype, &nseg, &seg_len)) {
         const size_t per = (size_t)B * H * nseg * D * D * 4;
         sz[KDA_WS_SEGX] = per;
@@ -220,6 +227,15 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
     if (pass == KDA_PASS_TRAIN) {
         for (int r = 0; r < KDA_WS_NREGIONS; ++r)
             if (!backward_region(r)) place(r);
+        // the training forward over segments: its temporaries, in the kept part
+        // (the forward is given only that part; the backward does not touch them)
+        int nseg, seg_len;
+        const int Dk = padded_head(D) ? PAD_D : D;
+        if (seg_forward(pass, B, T, H, Dk, dtype, &nseg, &seg_len)) {
+            L.segf_per = ((size_t)B * H * nseg * Dk * Dk * 4 + 255) & ~(size_t)255;
+            L.segf = (int64_t)cur;
+            cur += 3 * L.segf_per;
+        }
         L.kept = cur;
         for (int r = 0; r < KDA_WS_NREGIONS; ++r)
             if (backward_region(r)) place(r);
@@ -234,10 +250,14 @@ void make_layout(int pass, int B, int T, int H, int D, int dtype, Layout& L) {
 // `scratch` (null: the caller touches none of them).
 struct Ws {
     void* r[KDA_WS_NREGIONS];
+    char* segf;        // the training forward's segment temporaries (X, M, S), or null
+    size_t segf_per;
 };
 
 Ws resolve(const Layout& L, void* kept, void* scratch) {
     Ws w;
+    w.segf = L.segf >= 0 ? static_cast<char*>(kept) + L.segf : nullptr;
+    w.segf_per = L.segf_per;
     for (int r = 0; r < KDA_WS_NREGIONS; ++r) {
         const int64_t o = L.off[r];
         if (o < 0)
@@ -598,9 +618,17 @@ int fwd_launch(int pass, const void* q, const void* k, const void* v, const void
         sa.Aqk = region(ws, KDA_WS_AQK);
         sa.eG = fregion(ws, KDA_WS_EG);
         sa.s0 = s0; sa.s_final = s_final; sa.o = o;
-        sa.segX = fregion(ws, KDA_WS_SEGX);
-        sa.segM = static_cast<uint16_t*>(region(ws, KDA_WS_SEGM));
-        sa.segS = fregion(ws, KDA_WS_SEGS);
+        if (pass == KDA_PASS_TRAIN) {
+            // the training forward's own temporaries in the kept part
+            if (!ws.segf) return fail(KDA_E_INVALID, "training forward over segments without its temporaries");
+            sa.segX = reinterpret_cast<float*>(ws.segf);
+            sa.segM = reinterpret_cast<uint16_t*>(ws.segf + ws.segf_per);
+            sa.segS = reinterpret_cast<float*>(ws.segf + 2 * ws.segf_per);
+        } else {
+            sa.segX = fregion(ws, KDA_WS_SEGX);
+            sa.segM = static_cast<uint16_t*>(region(ws, KDA_WS_SEGM));
+            sa.segS = fregion(ws, KDA_WS_SEGS);
+        }
         sa.T = T; sa.H = H; sa.nc = nc; sa.BH = BH; sa.nseg = nseg; sa.seg_len = seg_len;
         e = timed(PROF_SEG_MAP, st, [&] { return kda::launch_seg_map(sa, st); }, prof);
         if (e != hipSuccess) return hip_fail(e, "kda_segchain_kernel(map)");

@@ -520,6 +520,8 @@ def test_bwd_parity_config2_full():
     (1, 100, 2, 128, torch.float32, 0.1),
     (1, 150, 2, 96, torch.bfloat16, 0.1),     # D = 96: padded inputs in the pair's workspace
     (2, 70, 2, 96, torch.float32, 0.1),
+    (1, 2560, 2, 128, torch.bfloat16, 0.1),   # forward and backward over 10 segments
+    (1, 2560, 2, 96, torch.bfloat16, 0.1),
 ])
 def test_training_pair_equals_standalone_calls(B, T, H, D, dtype, g_scale):
     """kda_fwd_train / kda_bwd_train reproduce kda_fwd / kda_bwd bit for bit."""
