@@ -49,7 +49,7 @@ template <int D, typename ST, typename TG, int PREC, int NTH>
 __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
     using G = PrepGeom<D, ST>;
     constexpr int NW = NTH / 64;   // waves
-    static_assert(NW == 4 || NW == 8, "four or eight waves");
+    static_assert(NW == 4 || NW == 8 || NW == 16, "four, eight or sixteen waves");
     constexpr int LDK = G::LDK, LDA = G::LDA, LDT = G::LDT, NT = D / BS, NCT = 2 * NT;
     constexpr int TPW = (NCT + NW - 1) / NW;
     constexpr int EPV = 16 / (int)sizeof(ST);
@@ -616,8 +616,10 @@ __global__ __launch_bounds__(NTH) void kda_prep_kernel(const PrepArgs a) {
 template <int D, typename ST, typename TG>
 static hipError_t launch_prep_t(const PrepArgs& a, int nchunks, hipStream_t st) {
     constexpr int PREC = std::is_same<ST, float>::value ? 3 : 1;
-    // eight waves per chunk where the registers allow four waves per SIMD
-    constexpr int NTH = (D >= 64) ? KDA_PREP_NTH : 256;
+    // eight waves per chunk where the registers allow four waves per SIMD;
+    // bf16 at D = 128 (133 KB of LDS: one workgroup per CU, 123 VGPRs) sixteen,
+    // four per SIMD on one chunk: config 3's prep 396 -> 368 us, bit-identical
+    constexpr int NTH = (D >= 128 && std::is_same<ST, uint16_t>::value) ? 1024 : (D >= 64) ? KDA_PREP_NTH : 256;
     hipLaunchKernelGGL((kda_prep_kernel<D, ST, TG, PREC, NTH>), dim3(nchunks), dim3(NTH), 0, st, a);
     return hipGetLastError();
 }
