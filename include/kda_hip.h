@@ -293,9 +293,11 @@ size_t kda_layer_workspace_size(int which, int B, int T, int H, int D);
  * producer (forward), 8 layer producer (backward, with its parameter-gradient
  * reduction), 9 gated RMSNorm (forward), 10 gated RMSNorm (backward, with its
  * reduction), 11-13 the segmented forward at D = 128 (bf16): 11 segment maps,
- * 12 segment start states, 13 the forward of every segment.
+ * 12 segment start states, 13 the forward of every segment; 14 the backward's
+ * state recompute and reverse carry in one launch (bf16 D = 128 without
+ * segments: then ids 3 and 4 record nothing).
  * kda_profile_read must be called after the streams have completed. */
-#define KDA_PROF_NKERNELS 14
+#define KDA_PROF_NKERNELS 15
 int kda_profile_enable(int on);              /* 1: clear records and start; 0: stop */
 const char* kda_profile_name(int id);
 int kda_profile_read(int id, double* total_ms, int* launches);

@@ -60,7 +60,7 @@ SIGNATURES = {
     "kda_profile_name": ([_I], ctypes.c_char_p),
     "kda_profile_read": ([_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)], _I),
 }
-PROF_NKERNELS = 14
+PROF_NKERNELS = 15
 
 _lib = None
 _lock = threading.Lock()

@@ -292,14 +292,15 @@ int hip_fail(hipError_t e, const char* where) {
 // ---- optional launch timing: an event pair around each launch, on its stream ----
 enum { PROF_PREP_FWD = 0, PROF_RECUR_FWD, PROF_PREP_BWD, PROF_RECUR_H, PROF_DH, PROF_LOCAL, PROF_PREP_TRAIN,
        PROF_PRODUCER_FWD, PROF_PRODUCER_BWD, PROF_RMSNORM_FWD, PROF_RMSNORM_BWD, PROF_SEG_MAP, PROF_SEG_SCAN,
-       PROF_SEG_FWD };
+       PROF_SEG_FWD, PROF_STATES_DH };
 const char* const kProfNames[KDA_PROF_NKERNELS] = {"kda_prep_kernel(fwd)", "kda_recur_kernel(fwd)",
                                                    "kda_prep_kernel(bwd)", "kda_recur_kernel(states)",
                                                    "kda_dh_kernel", "kda_bwd_local_kernel",
                                                    "kda_prep_kernel(train)", "producer_fwd_kernel",
                                                    "producer_bwd_kernel(+reduce)", "rmsnorm_fwd_kernel",
                                                    "rmsnorm_bwd_kernel(+reduce)", "kda_segchain_kernel(map)",
-                                                   "kda_segscan_kernel", "kda_segchain_kernel(fwd)"};
+                                                   "kda_segscan_kernel", "kda_segchain_kernel(fwd)",
+                                                   "kda_states_dh_kernel(states + dh)"};
 struct Profiler {
     std::mutex mu;
     bool on = false;
@@ -745,13 +746,19 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
             return r;
         });
         if (e != hipSuccess) return hip_fail(e, "kda_segchain_kernel(states)");
-    } else {
-        kda::RecurArgs ra = {};
+    }
+    // bf16 D = 128 without segments: the state recompute shares one launch with
+    // the reverse carry below (kda_states_dh_kernel)
+    const bool merged = nseg == 1 && in_bf16 && D == 128;
+    kda::RecurArgs ra = {};
+    if (nseg == 1) {
         ra.W = W; ra.U = U; ra.KbT = KbT; ra.eG = eG; ra.s0 = s0; ra.h = hS; ra.Vp = Vp;
         ra.Kb = region(ws, KDA_WS_KB);
         ra.T = T; ra.H = H; ra.nc = nc; ra.BH = BH;
-        e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
-        if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
+        if (!merged) {
+            e = timed(PROF_RECUR_H, st, [&] { return kda::launch_recur(ra, D, in_bf16, 1, st); });
+            if (e != hipSuccess) return hip_fail(e, "kda_recur_kernel");
+        }
     }
 
     kda::DhArgs da = {};
@@ -785,6 +792,8 @@ int bwd_launch(int pass, const void* q, const void* k, const void* v, const void
             if (r == hipSuccess) r = kda::launch_dh_seg(da, st);
             return r;
         });
+    } else if (merged) {
+        e = timed(PROF_STATES_DH, st, [&] { return kda::launch_states_dh(ra, da, st); });
     } else {
         e = timed(PROF_DH, st, [&] { return kda::launch_dh(da, D, in_bf16, st); });
     }

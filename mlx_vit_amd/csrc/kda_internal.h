@@ -128,6 +128,8 @@ hipError_t launch_recur(const RecurArgs& a, int D, int in_bf16, int mode, hipStr
 bool recur_epilogue_supported(int D, int in_bf16);
 hipError_t launch_dh(const DhArgs& a, int D, int in_bf16, hipStream_t st);
 hipError_t launch_dh_seg_maps(const DhArgs& a, hipStream_t st);
+// bf16 D = 128: the state recompute (MODE 1) and the reverse carry in one launch
+hipError_t launch_states_dh(const RecurArgs& ra, const DhArgs& da, hipStream_t st);
 hipError_t launch_dh_seg(const DhArgs& a, hipStream_t st);
 hipError_t launch_local(const LocalArgs& a, int D, int in_bf16, int g_kind, int nchunks, hipStream_t st);
 // the local adjoints at D = 128 (kda_bwdw.hip): reads A_kk, the diagonal-block

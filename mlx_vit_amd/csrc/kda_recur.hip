@@ -105,15 +105,16 @@ struct DhLayout {
 //   wait for the loads, write them to LDS set (n+1)&1; barrier.
 // With NBUF = 1 an extra barrier separates the compute from the overwrite.
 // ----------------------------------------------------------------------------
+// The kernel body (kda_recur_kernel, kda_states_dh_kernel): workgroup wgi of
+// the launch's recurrence workgroups, Lay::BYTES of LDS at smem.
 template <int D, typename ST, int PREC, int MODE, int CS, bool EPI = false>
-__global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
+__device__ __forceinline__ void recur_body(const RecurArgs& a, unsigned char* smem, const int wgi) {
     using Lay = RecurLayout<D, ST, MODE, CS>;
     constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, TPW = (NTW + 3) / 4;
     constexpr int LDR = Lay::LDR, LDU = Lay::LDU, LDC = Lay::LDC;
-    __shared__ __align__(16) unsigned char smem[Lay::BYTES];
 
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
-    const int bh = blockIdx.x / CS, c0 = (blockIdx.x - bh * CS) * DC;
+    const int bh = wgi / CS, c0 = (wgi - bh * CS) * DC;
     const int b = bh / a.H, h = bh - b * a.H;
     const ST* gW = static_cast<const ST*>(a.W);
     const ST* gU = static_cast<const ST*>(a.U);
@@ -350,6 +351,12 @@ __global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
 // ----------------------------------------------------------------------------
 // reverse state recurrence (same pipeline, chunks in reverse order)
 // ----------------------------------------------------------------------------
+template <int D, typename ST, int PREC, int MODE, int CS, bool EPI = false>
+__global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
+    __shared__ __align__(16) unsigned char smem[RecurLayout<D, ST, MODE, CS>::BYTES];
+    recur_body<D, ST, PREC, MODE, CS, EPI>(a, smem, blockIdx.x);
+}
+
 // CS > 1: CS workgroups per (batch, head), DC = D / CS columns each; every A
 // fragment is then used by one column tile of a wave, so fragments are read
 // from LDS where they are used instead of being held for the whole chunk (at
@@ -361,18 +368,19 @@ __global__ __launch_bounds__(256) void kda_recur_kernel(const RecurArgs a) {
 // reference orientation [dv][dk]); SEGM 2: every segment from its incoming
 // dSigma (ds_final for the last segment, a.segS, the reverse scan's result,
 // for the others), writing dh and dV' and, for segment 0, dS0.
+// The kernel body (kda_dh_kernel, kda_states_dh_kernel): workgroup wgi of the
+// launch's reverse-carry workgroups, Lay::BYTES of LDS at smem.
 template <int D, typename ST, int PREC, int CS = 1, int SEGM = 0>
-__global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
+__device__ __forceinline__ void dh_body(const DhArgs& a, unsigned char* smem, const int wgi) {
     using Lay = DhLayout<D, ST, CS>;
     constexpr int NT = D / BS, DC = Lay::DC, NTW = DC / BS, TPW = (NTW + 3) / 4;
     constexpr int LDR = Lay::LDR, LDC = Lay::LDC, LDU = Lay::LDU;
     constexpr bool HOLD = CS == 1;   // A fragments held in registers for the chunk
     static_assert(Lay::BYTES <= 160 * 1024, "reverse recurrence LDS");
-    __shared__ __align__(16) unsigned char smem[Lay::BYTES];
 
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g4 = l >> 4;
     // the workgroup's segment: chunks n0 .. n0 + L - 1 (the whole sequence without SEGM)
-    int wg = blockIdx.x, sgi = 0, n0 = 0, L = a.nc;
+    int wg = wgi, sgi = 0, n0 = 0, L = a.nc;
     if constexpr (SEGM != 0) {
         const int nsegw = (SEGM == 1) ? a.nseg - 1 : a.nseg;
         const int si = wg % nsegw;
@@ -598,6 +606,28 @@ __global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
                     *reinterpret_cast<float4*>(a.ds0 + ((size_t)bh * D + c0 + col[j]) * D + BS * mt + 4 * g4) =
                         make_float4(dS[j][mt][0], dS[j][mt][1], dS[j][mt][2], dS[j][mt][3]);
     }
+}
+
+template <int D, typename ST, int PREC, int CS = 1, int SEGM = 0>
+__global__ __launch_bounds__(256) void kda_dh_kernel(const DhArgs a) {
+    __shared__ __align__(16) unsigned char smem[DhLayout<D, ST, CS>::BYTES];
+    dh_body<D, ST, PREC, CS, SEGM>(a, smem, blockIdx.x);
+}
+
+// The backward's state recompute and reverse carry at bf16 D = 128 in one
+// launch.  They are independent (the reverse carry does not read the states)
+// and one workgroup of either fills a CU's LDS, so workgroups 0 .. 2 BH - 1
+// recompute the states (two per (b, h), as kda_recur_kernel) and the next 2 BH
+// run the reverse carry (two per (b, h), as kda_dh_kernel), side by side on
+// 4 BH CUs instead of one kernel after the other.
+__global__ __launch_bounds__(256) void kda_states_dh_kernel(const RecurArgs ra, const DhArgs da) {
+    constexpr int B1 = RecurLayout<128, uint16_t, 1, 2>::BYTES, B2 = DhLayout<128, uint16_t, 2>::BYTES;
+    __shared__ __align__(16) unsigned char smem[B1 > B2 ? B1 : B2];
+    const int n1 = 2 * ra.BH;
+    if ((int)blockIdx.x < n1)
+        recur_body<128, uint16_t, 1, 1, 2>(ra, smem, blockIdx.x);
+    else
+        dh_body<128, uint16_t, 1, 2, 0>(da, smem, (int)blockIdx.x - n1);
 }
 
 // ----------------------------------------------------------------------------
@@ -2397,6 +2427,12 @@ hipError_t launch_dh_seg_maps(const DhArgs& a, hipStream_t st) {
 hipError_t launch_dh_seg(const DhArgs& a, hipStream_t st) {
     if (a.nseg < 2) return hipErrorInvalidValue;
     hipLaunchKernelGGL((kda_dh_kernel<128, uint16_t, 1, 2, 2>), dim3(a.BH * 2 * a.nseg), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_states_dh(const RecurArgs& ra, const DhArgs& da, hipStream_t st) {
+    if (ra.BH != da.BH || !ra.Vp || !ra.KbT || !da.AqkT || !da.QpT || !da.WT || !da.Kb) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(kda_states_dh_kernel, dim3(4 * ra.BH), dim3(256), 0, st, ra, da);
     return hipGetLastError();
 }
 
