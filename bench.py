@@ -184,6 +184,8 @@ def kernel_counts_at(B, T, H, D, es=2):
         6: io_in + (N * (4 * CD * es + CC * es + D * f4) if tr else                      # -> both sets
                     N * (7 * CD * es + 2 * CC * es + x * (CC + TII) * f4 + D * f4)),
     }
+    # the state recompute and the reverse carry in one launch (bf16 D = 128)
+    fl[14], alg[14], ws[14] = fl[3] + fl[4], alg[3] + alg[4], ws[3] + ws[4]
     return fl, alg, ws
 
 
