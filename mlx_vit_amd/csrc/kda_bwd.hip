@@ -1109,14 +1109,29 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
 #pragma unroll
                 for (int p = 1; p < NB; ++p) arp[p] = __shfl(at[mm][3], 16 * (p - 1) + r16, 64);
                 const float arg = (g4 == 0) ? arp[0] : (g4 == 1) ? arp[1] : (g4 == 2) ? arp[2] : arp[3];
-                float eo[4], av[4], aqv[4];
+                // Pass factors e^{a_{r_p} - a_t} (p >= g, 0 before) as W_p V_t, with
+                // a_l the lane's last row l = 16 m + 4 g + 3: W_p = e^{a_{r_p} - a_l}
+                // (<= e^{4-row span} for p = g, <= 1 after), V_t = e^{a_l - a_t} in
+                // [e^{-4-row span}, 1].  Neither factor overflows; where W_p underflows
+                // the product is below it.  (A large negative exponent gives W_p = 0
+                // for p < g: no per-element select.)
+                float eo[4], vt[4], wp[NB];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     eo[e] = kexp<PREC>(at[mm][e] - arg);
-                    av[e] = bf2f(f2bf(kx[mm][e] * eo[e]));
-                    aqv[e] = bf2f(f2bf(qx[mm][e] * eo[e]));
+                    vt[e] = (e == 3) ? 1.f : kexp<PREC>(at[mm][3] - at[mm][e]);
                 }
-                const Frag4 Ak = frag4_from_f32<1>(av), Aq = frag4_from_f32<1>(aqv);
+#pragma unroll
+                for (int p = 0; p < NB; ++p) wp[p] = kexp<PREC>(((p >= g4) ? arp[p] : -1e30f) - at[mm][3]);
+                // A_t, Aq_t as packed bf16 pairs, and the same values back as floats
+                const uint32_t ak0 = pack2bf(kx[mm][0] * eo[0], kx[mm][1] * eo[1]);
+                const uint32_t ak1 = pack2bf(kx[mm][2] * eo[2], kx[mm][3] * eo[3]);
+                const uint32_t aq0 = pack2bf(qx[mm][0] * eo[0], qx[mm][1] * eo[1]);
+                const uint32_t aq1 = pack2bf(qx[mm][2] * eo[2], qx[mm][3] * eo[3]);
+                const float av[4] = {bf_lo(ak0), bf_hi(ak0), bf_lo(ak1), bf_hi(ak1)};
+                const float aqv[4] = {bf_lo(aq0), bf_hi(aq0), bf_lo(aq1), bf_hi(aq1)};
+                const Frag4 Ak{__builtin_bit_cast(short4v, make_uint2(ak0, ak1)), short4v{0, 0, 0, 0}};
+                const Frag4 Aq{__builtin_bit_cast(short4v, make_uint2(aq0, aq1)), short4v{0, 0, 0, 0}};
                 // row-side A operands (rows t = 16 m + r16) and column-side A
                 // operands (rows s = 16 m + r16, k = t = 16 m + 4 g + e)
                 const float bi = s.beta[BS * m + r16];
@@ -1125,25 +1140,32 @@ __device__ __forceinline__ void local3_tail(const LocalArgs& a, LocalSmem<D, ST>
                 // (dA is strictly lower: the diagonal pairs are added apart, below)
                 Frag4 Ar = frag4_from_f32<1>(pr), Aqr = ldfrag4<1, ST>(&sm.dA[0][0], LDT, BS * m, BS * m);
                 float pc[4], ac[4];
+                short4v acr;   // bf16 dA: its raw halves are the fragment
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int t = BS * m + 4 * g4 + e;
                     pc[e] = s.beta[t] * sdL[t * LDL + BS * m + r16];
-                    ac[e] = ld1<ST>(&sm.dA[t][BS * m + r16]);
+                    if constexpr (std::is_same<ST, uint16_t>::value)
+                        acr[e] = (short)sm.dA[t][BS * m + r16];
+                    else
+                        ac[e] = ld1<ST>(&sm.dA[t][BS * m + r16]);
                 }
-                const Frag4 Ac = frag4_from_f32<1>(pc), Aqc = frag4_from_f32<1>(ac);
+                const Frag4 Ac = frag4_from_f32<1>(pc);
+                Frag4 Aqc;
+                if constexpr (std::is_same<ST, uint16_t>::value) Aqc = Frag4{acr, short4v{0, 0, 0, 0}};
+                else Aqc = frag4_from_f32<1>(ac);
                 const Frag4 z4{short4v{0, 0, 0, 0}, short4v{0, 0, 0, 0}};
                 f32x4 rk = zero4(), rq = zero4();
                 float ck[4] = {0.f, 0.f, 0.f, 0.f}, cg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int p = 0; p < NB; ++p) {
-                    float f[4], bv[4];
+                    float f[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        f[e] = (p >= g4) ? kexp<PREC>(arp[p] - at[mm][e]) : 0.f;
-                        bv[e] = bf2f(f2bf(kx[mm][e] * f[e]));
-                    }
-                    const Frag4 Bp = frag4_from_f32<1>(bv);
+                    for (int e = 0; e < 4; ++e) f[e] = wp[p] * vt[e];
+                    const uint32_t b0 = pack2bf(kx[mm][0] * f[0], kx[mm][1] * f[1]);
+                    const uint32_t b1 = pack2bf(kx[mm][2] * f[2], kx[mm][3] * f[3]);
+                    const float bv[4] = {bf_lo(b0), bf_hi(b0), bf_lo(b1), bf_hi(b1)};
+                    const Frag4 Bp{__builtin_bit_cast(short4v, make_uint2(b0, b1)), short4v{0, 0, 0, 0}};
                     const bool rowp = (r16 >> 2) == p, colp = g4 == p;
                     rk = mma4f<1>(rowp ? Ar : z4, Bp, rk);
                     rq = mma4f<1>(rowp ? Aqr : z4, Bp, rq);

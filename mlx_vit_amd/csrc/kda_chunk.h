@@ -433,18 +433,28 @@ __device__ __forceinline__ void subanchor_tile(const ChunkSmem<D, ST>& s, int i,
             const float arq = (q == 0) ? ar[0][e] : (q == 1) ? ar[1][e] : (q == 2) ? ar[2][e] : ar[3][e];
             ea[e] = kexp<PREC>(av[e] - arq);
         }
+        // the lane's A operands, packed once; pass p keeps them on sub-block p's
+        // rows only, and B on the rows of sub-blocks <= p (zeros picked after the
+        // packing, a register at a time: past p the exponent is positive and may
+        // overflow, and the pick drops that value)
+        float ka[8], qa[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            ka[e] = kv[e] * ea[e];
+            qa[e] = qv[e] * ea[e];
+        }
+        const Frag8 FA = frag_from_f32<PREC>(ka);
+        Frag8 FQ{};
+        if constexpr (WITH_Q) FQ = frag_from_f32<PREC>(qa);
+        const Frag8 Z{};
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
-            float aa[8], aq[8], bb[8];
+            float bb[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                aa[e] = (q == p) ? kv[e] * ea[e] : 0.f;
-                aq[e] = (q == p) ? qv[e] * ea[e] : 0.f;
-                bb[e] = (q <= p) ? kv[e] * kexp<PREC>(ar[p][e] - av[e]) : 0.f;
-            }
-            const Frag8 B = frag_from_f32<PREC>(bb);
-            P = mma<PREC>(frag_from_f32<PREC>(aa), B, P);
-            if constexpr (WITH_Q) Q = mma<PREC>(frag_from_f32<PREC>(aq), B, Q);
+            for (int e = 0; e < 8; ++e) bb[e] = kv[e] * kexp<PREC>(ar[p][e] - av[e]);
+            const Frag8 B = (q <= p) ? frag_from_f32<PREC>(bb) : Z;
+            P = mma<PREC>((q == p) ? FA : Z, B, P);
+            if constexpr (WITH_Q) Q = mma<PREC>((q == p) ? FQ : Z, B, Q);
         }
     }
 }

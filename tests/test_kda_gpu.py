@@ -293,12 +293,15 @@ def test_mixed_span_blocks_d128(scales):
     _assert_all(_bwd_errors(x, torch.bfloat16), TOL[torch.bfloat16], f"bwd mixed spans D128 {scales}")
 
 
-def test_layer_init_decay_d96():
+@pytest.mark.parametrize("D", [96, 64])
+def test_layer_init_decay(D):
     """The SSv2 layer's decay at initialisation, g = -A_h softplus(N(0, 0.5^2))
     with A_h ~ U[1, 16] per head (nope_gdn_mlx.py:749): nearly every 16-row
-    block beyond the span guard, at D = 96, bf16, through the training pair."""
+    block beyond the span guard, bf16, through the training pair -- at D = 96
+    (the SSv2 heads, wide local-adjoint kernel) and D = 64 (config 2's heads,
+    the sub-anchored diagonal tiles of the D <= 64 kernel)."""
     kda = _kda()
-    B, T, H, D = 1, 300, 4, 96
+    B, T, H = 1, 300, 4
     x = _inputs(B, T, H, D, torch.bfloat16, seed=34, with_state=True, grad=True)
     gen = torch.Generator().manual_seed(35)
     A = torch.linspace(1.0, 16.0, H)
@@ -313,7 +316,7 @@ def test_layer_init_decay_d96():
     refb = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"])
     errs = {"o": R.rel_l2(o.cpu(), ref["o"]), "s_final": R.rel_l2(sf.cpu(), ref["s_final"])}
     errs.update({n: R.rel_l2(gr.cpu(), refb[n]) for n, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads)})
-    _assert_all(errs, TOL[torch.bfloat16], "layer-init decay D96")
+    _assert_all(errs, TOL[torch.bfloat16], f"layer-init decay D{D}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
