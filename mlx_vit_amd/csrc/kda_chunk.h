@@ -411,7 +411,7 @@ __device__ __forceinline__ void subanchor_tile(const ChunkSmem<D, ST>& s, int i,
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
         if (ksel >= 0 && ks != ksel) continue;
-        float kv[8], qv[8], av[8], ar[NB][8];
+        float kv[8], qv[8], av[8], ar[NB][8], arq[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int c = 32 * ks + 16 * h + 4 * g4;
@@ -426,13 +426,16 @@ __device__ __forceinline__ void subanchor_tile(const ChunkSmem<D, ST>& s, int i,
                                     : make_float4(0.f, 0.f, 0.f, 0.f);
                 ar[p][4 * h] = r4.x; ar[p][4 * h + 1] = r4.y; ar[p][4 * h + 2] = r4.z; ar[p][4 * h + 3] = r4.w;
             }
+            // the anchor of the lane's own sub-block, read by row (a pick among the
+            // four loaded above compiles to branches per element); q = 0 reads a row
+            // of the block and takes 0
+            const float4 o4 = *reinterpret_cast<const float4*>(&s.g[BS * i + 4 * q - (q ? 1 : 0)][c]);
+            arq[4 * h] = q ? o4.x : 0.f; arq[4 * h + 1] = q ? o4.y : 0.f;
+            arq[4 * h + 2] = q ? o4.z : 0.f; arq[4 * h + 3] = q ? o4.w : 0.f;
         }
         float ea[8];   // e^{a_t - a_{r_q}}, the lane's row in its own sub-block q
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float arq = (q == 0) ? ar[0][e] : (q == 1) ? ar[1][e] : (q == 2) ? ar[2][e] : ar[3][e];
-            ea[e] = kexp<PREC>(av[e] - arq);
-        }
+        for (int e = 0; e < 8; ++e) ea[e] = kexp<PREC>(av[e] - arq[e]);
         // the lane's A operands, packed once; pass p keeps them on sub-block p's
         // rows only, and B on the rows of sub-blocks <= p (zeros picked after the
         // packing, a register at a time: past p the exponent is positive and may
