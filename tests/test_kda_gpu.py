@@ -793,3 +793,59 @@ def test_solve_triangular_kat(upper):
         y = kda.solve_unit_triangular(torch.from_numpy(Mm).to(DEV), torch.from_numpy(b).to(DEV), upper=upper)
         rel = float(np.max(np.abs(y.cpu().numpy() - y_np))) / (float(np.max(np.abs(y_np))) + 1e-9)
         assert rel < 1e-4, (C, rel)
+
+
+# ---------------------------------------------------------------- randomized sweep
+
+def _sweep_cases(n=44, seed=20261202):
+    """Seeded random shapes: D in {32, 64, 96, 128}, fp32 (D <= 64) or bf16,
+    T from 1 to 2600 (ragged and chunk-aligned, single- and multi-segment),
+    with or without S0 and dS_T, and three decays: the default, a scaled one
+    (g_scale up to 2.5) and the layer's initial decay per head."""
+    import random
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        D = rng.choice([32, 64, 64, 96, 128, 128])
+        dt = "bf16" if (D > 64 or rng.random() < 0.7) else "fp32"
+        T = rng.choice([1, 63, 64, 65, 130, 777, 1568, 2100, 2600])
+        H = rng.randint(1, 5)
+        B = rng.randint(1, 3)
+        st = rng.random() < 0.5
+        dsf_on = rng.random() < 0.4
+        mode = rng.choice(["default", "scaled", "layer"])
+        gs = rng.choice([0.1, 0.5, 1.0, 2.5]) if mode == "scaled" else 0.1
+        out.append((i, B, T, H, D, dt, st, dsf_on, mode, gs))
+    return out
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: f"{c[0]}-B{c[1]}T{c[2]}H{c[3]}D{c[4]}-{c[5]}-{c[8]}")
+def test_random_sweep(case):
+    """Forward, standalone backward and the training pair on one seeded random
+    case, every output and gradient against the fp64 oracle."""
+    i, B, T, H, D, dt, st, dsf_on, mode, gs = case
+    dtype = torch.bfloat16 if dt == "bf16" else torch.float32
+    kda = _kda()
+    x = _inputs(B, T, H, D, dtype, seed=100 + i, with_state=st, grad=True, g_scale=gs)
+    if mode == "layer":
+        gen = torch.Generator().manual_seed(200 + i)
+        A = torch.empty(H).uniform_(1.0, 16.0, generator=gen)
+        x["g"] = (-A[None, None, :, None] * torch.nn.functional.softplus(
+            0.5 * torch.randn(B, T, H, D, generator=gen))).to(x["g"].dtype)
+    dsf = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(5)) if dsf_on else None
+    errs = {"f_" + k: v for k, v in _fwd_errors(x, dtype).items()}
+    errs.update({"b_" + k: v for k, v in _bwd_errors(x, dtype, dsf).items()})
+    q, k, v, g, beta = _dev(x)
+    s0 = x["s0"].to(DEV) if x["s0"] is not None else None
+    o, sf, ws = kda.kda_forward_train(q, k, v, g, beta, s0)
+    grads = kda.kda_backward_train(q, k, v, g, beta, s0, x["do"].to(DEV),
+                                   None if dsf is None else dsf.to(DEV), ws)
+    torch.cuda.synchronize()
+    ref = cref.forward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"])
+    refb = cref.backward(x["q"], x["k"], x["v"], x["g"], x["beta"], x["s0"], x["do"], dsf)
+    errs["t_o"] = R.rel_l2(o.cpu(), ref["o"])
+    errs["t_s_final"] = R.rel_l2(sf.cpu(), ref["s_final"])
+    for n, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), grads):
+        if gr is not None and refb.get(n) is not None:
+            errs["t_" + n] = R.rel_l2(gr.cpu(), refb[n])
+    _assert_all(errs, TOL[dtype], f"random sweep {case}")
